@@ -1,0 +1,67 @@
+"""ctypes binding of ``libbioemu2_mi355x.so`` (the C ABI in ``include/bioemu2_mi355x.h``).
+
+The library is loaded lazily on first use.  There is no fallback: if the
+library is missing or fails to load, every op raises ``RuntimeError``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libbioemu2_mi355x.so"
+
+_c_void_p = ctypes.c_void_p
+_c_size_t = ctypes.c_size_t
+_c_int64 = ctypes.c_int64
+_c_int = ctypes.c_int
+
+# name -> (restype, argtypes).  Keep in the order of include/bioemu2_mi355x.h.
+SIGNATURES: dict[str, tuple[object, list[object]]] = {
+    "bioemu_version": (ctypes.c_char_p, []),
+    "bioemu_last_error": (ctypes.c_char_p, []),
+    "bioemu_trimul_workspace_bytes": (_c_size_t, [_c_int64, _c_int64, _c_int64]),
+    "bioemu_trimul_fwd": (
+        _c_int,
+        [_c_void_p] * 11 + [_c_void_p, _c_size_t, _c_int64, _c_int64, _c_int64, _c_int, _c_int, _c_void_p],
+    ),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+class NativeLibraryError(RuntimeError):
+    pass
+
+
+def lib() -> ctypes.CDLL:
+    """Returns the loaded native library, loading it on first use."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise NativeLibraryError(
+                    f"bioemu2_amd native library not found at {LIB_PATH}; "
+                    "build it with `python -m bioemu2_amd.build` (hipcc, gfx950)"
+                )
+            handle = ctypes.CDLL(str(LIB_PATH))
+            for name, (restype, argtypes) in SIGNATURES.items():
+                fn = getattr(handle, name)
+                fn.restype = restype
+                fn.argtypes = argtypes
+            _lib = handle
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    """Raises on a non-zero C-ABI return code, mapping codes to Python exceptions."""
+    if rc == 0:
+        return
+    msg = lib().bioemu_last_error().decode(errors="replace")
+    if rc in (-1, -2):
+        raise ValueError(f"{what}: {msg} (code {rc})")
+    raise RuntimeError(f"{what}: {msg} (code {rc})")

@@ -1,0 +1,65 @@
+/*
+ * bioemu2_mi355x — C ABI of the MI355X (gfx950) Pairformer hot-path kernels.
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t, runs
+ * asynchronously on that stream, allocates nothing, and returns 0 or a
+ * negative BIOEMU_ERR_* code (bioemu_last_error() gives the message).
+ *
+ * Data types:
+ *   activations  bf16, channel-last ([B, N, N, C] pair tensors, [B, N, C] singles)
+ *   masks        uint8 0/1
+ *   LayerNorm    gamma/beta fp32
+ *   Linear       weights bf16, row-major [out, in] (torch nn.Linear layout)
+ * Arithmetic: bf16 MFMA operands with fp32 accumulation; LayerNorm statistics,
+ * softmax and gates in fp32.
+ *
+ * Scratch memory is caller-owned: each op with intermediates has a
+ * *_workspace_bytes() query and takes (workspace, workspace_bytes).
+ */
+#ifndef BIOEMU2_MI355X_H
+#define BIOEMU2_MI355X_H
+
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BIOEMU_OK 0
+#define BIOEMU_ERR_INVALID_ARG (-1)
+#define BIOEMU_ERR_UNSUPPORTED (-2)
+#define BIOEMU_ERR_WORKSPACE (-3)
+#define BIOEMU_ERR_LAUNCH (-4)
+
+/* Library version string and the message of the last failing call (per thread). */
+const char* bioemu_version(void);
+const char* bioemu_last_error(void);
+
+/*
+ * Triangle multiplicative update, outgoing (outgoing=1) or incoming (0).
+ *
+ * Replaces TriangleMultiplicationFull.forward / TriangleMultiplicationCueq.forward
+ * (src/bioemu2/biomoa/ops/triangle_multiplication.py:89-99 and :137-151):
+ *   xn  = LN_in(x);  p = p_in(xn) * sigmoid(g_in(xn));  p[~mask] = 0
+ *   a, b = p[..., :D], p[..., D:]
+ *   o[i,j] = sum_k a[i,k] * b[j,k]       (outgoing)
+ *   o[i,j] = sum_k a[k,i] * b[k,j]       (incoming)
+ *   out = p_out(LN_out(o)) * sigmoid(g_out(xn))   (+ x when residual != 0)
+ * x, out: [B,N,N,D] bf16 (out may equal x when residual != 0); mask [B,N,N].
+ * p_in_w, g_in_w: [2D, D]; p_out_w, g_out_w: [D, D].  D must be 128.
+ */
+size_t bioemu_trimul_workspace_bytes(int64_t B, int64_t N, int64_t D);
+int bioemu_trimul_fwd(const void* x, const uint8_t* mask, const float* norm_in_w,
+                      const float* norm_in_b, const void* p_in_w, const void* g_in_w,
+                      const float* norm_out_w, const float* norm_out_b, const void* p_out_w,
+                      const void* g_out_w, void* out, void* workspace, size_t workspace_bytes,
+                      int64_t B, int64_t N, int64_t D, int outgoing, int residual,
+                      hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BIOEMU2_MI355X_H */

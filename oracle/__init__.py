@@ -1,0 +1,47 @@
+"""CPU oracle for the Pairformer hot path — TEST INFRASTRUCTURE ONLY.
+
+This package is the checker, never the product.  Only ``tests/``,
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
+import it.  The product path (``bioemu2_amd``) never routes through it and
+fails loudly when its HIP library is missing.
+
+Every function is a float32 PyTorch-on-CPU restatement of the reference's
+algorithm (itsawesomeabhishek/bioemu2) and cites the reference file:line it
+follows.  Parameters are passed as dicts whose keys are the reference modules'
+``state_dict`` keys, so ``oracle.trimul(x, mask, module.state_dict(), ...)``
+works for both the reference classes and the drop-in HIP classes.
+
+How each function is pinned (see ``tests/test_oracle.py``):
+
+* ``trimul``      — brute-force Python loops (tiny N), the
+                    incoming(x) == outgoing(x^T, a<->b swapped)^T identity, the
+                    bit-exact masking and padding invariances of the reference
+                    tests (test_triangle_multiplication.py:303-399).
+* ``triangle_attention`` — NOT in the reference (AF3 suppl. Alg. 14/15).
+                    Pinned by brute-force loops, ending(z) == starting(z^T)^T,
+                    reduction to per-row SDPA with a zero bias, and the
+                    fully-masked-row closed form (uniform weights).
+* ``attention_pair_bias`` — brute-force loops, reduction to torch SDPA with an
+                    additive mask, tiled == untiled, multiplicity == separate runs,
+                    bitwise padding invariance (test_attention_pair_bias.py:805-867).
+* ``outer_product_mean`` — brute-force loops over S, masked rows contribute
+                    exact zeros (test_outer_product_mean.py:286-310), the
+                    divisor is the per-batch valid-row count (duplicating the
+                    MSA leaves the mean unchanged).
+* ``transition``  — brute-force loops and the SwiGLU closed form.
+* ``pairformer_block`` — composition only (AF3 suppl. Alg. 17); each term is
+                    pinned above, the order is pinned by a hand-built
+                    composition test.
+
+No function here is "parity unpinned".
+"""
+
+from .pairformer_ref import (  # noqa: F401
+    attention_pair_bias,
+    outer_product_mean,
+    pair_mask_from_token_mask,
+    pairformer_block,
+    transition,
+    triangle_attention,
+    trimul,
+)

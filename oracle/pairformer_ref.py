@@ -1,0 +1,302 @@
+"""float32 CPU restatement of the Pairformer hot-path ops (test infrastructure only).
+
+All citations are ``path:line`` inside the reference repository
+itsawesomeabhishek/bioemu2 (``src/bioemu2/biomoa/...``).  The arithmetic is
+plain float32 PyTorch on the CPU; nothing here runs on, or is shipped to, the
+GPU product path.
+
+Parameter dicts use the reference modules' ``state_dict`` keys.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor
+
+__all__ = [
+    "trimul",
+    "triangle_attention",
+    "attention_pair_bias",
+    "outer_product_mean",
+    "transition",
+    "pairformer_block",
+    "pair_mask_from_token_mask",
+]
+
+
+def _f32(t: Tensor) -> Tensor:
+    return t.detach().to(device="cpu", dtype=torch.float32)
+
+
+def _p(params: dict, key: str) -> Tensor:
+    return _f32(params[key])
+
+
+def _ln(x: Tensor, params: dict, prefix: str, eps: float = 1e-5) -> Tensor:
+    w = _p(params, prefix + ".weight")
+    b = _p(params, prefix + ".bias") if (prefix + ".bias") in params else None
+    return F.layer_norm(x, (x.shape[-1],), w, b, eps)
+
+
+def pair_mask_from_token_mask(token_mask: Tensor) -> Tensor:
+    """``pair_mask = mask_i & mask_j`` (biomoa/modules/pairmixer.py:263-264)."""
+    m = token_mask.bool()
+    return m.unsqueeze(-1) & m.unsqueeze(-2)
+
+
+# ----------------------------------------------------------------------------
+# Triangle multiplicative update
+# ----------------------------------------------------------------------------
+def trimul(x: Tensor, mask: Tensor, params: dict, mode: str = "outgoing") -> Tensor:
+    """TriangleMultiplicationFull.forward (biomoa/ops/triangle_multiplication.py:89-99).
+
+    Parameters: ``_TriMulBase.__init__`` (triangle_multiplication.py:62-76) —
+    norm_in (LN, eps 1e-5), p_in/g_in Linear(D->2D, no bias), norm_out (LN),
+    p_out/g_out Linear(D->D, no bias).
+
+    x [B,N,N,D], mask [B,N,N] -> [B,N,N,D] (float32).  The output is not masked.
+    """
+    if mode not in ("outgoing", "incoming"):
+        raise AssertionError(mode)
+    x = _f32(x)
+    xn = _ln(x, params, "norm_in")  # :90
+    proj = (xn @ _p(params, "p_in.weight").T) * torch.sigmoid(
+        xn @ _p(params, "g_in.weight").T
+    )  # :92
+    proj = proj.masked_fill(~mask.bool().unsqueeze(-1), 0.0)  # :93
+    a, b = proj.chunk(2, dim=-1)  # :94 (a = channels 0..D-1)
+    if mode == "outgoing":
+        out = torch.einsum("bikd,bjkd->bijd", a, b)  # :96
+    else:
+        out = torch.einsum("bkid,bkjd->bijd", a, b)  # :98
+    on = _ln(out, params, "norm_out")
+    return (on @ _p(params, "p_out.weight").T) * torch.sigmoid(
+        xn @ _p(params, "g_out.weight").T
+    )  # :99
+
+
+# ----------------------------------------------------------------------------
+# Triangle attention (NOT in the reference: AF3 supplement Alg. 14/15)
+# ----------------------------------------------------------------------------
+TRIATT_INF = 1e6
+
+
+def triangle_attention(
+    z: Tensor,
+    mask: Tensor,
+    params: dict,
+    num_heads: int = 4,
+    starting: bool = True,
+    inf: float = TRIATT_INF,
+    row_chunk: int | None = None,
+) -> Tensor:
+    """Triangle attention around the starting (Alg. 14) or ending (Alg. 15) node.
+
+    The reference has no triangle attention (biomoa/modules/pairmixer.py:459-462
+    removes it); this restates AlphaFold3 supplement Alg. 14/15 with
+    LinearNoBias projections and the reference's masking convention for
+    attention: masked keys are *replaced* by ``-inf`` (``masked_fill``), as in
+    AttentionPairBias.forward (biomoa/ops/attention_pair_bias.py:184-190).
+
+    Starting node, per batch b, row i, head h:
+        zn = LN(z);  q,k,v,g = LinearNoBias(zn) (g through a sigmoid)
+        bias[h,j,k] = LinearNoBias(zn)[j,k,h]
+        logit[j,k] = q[i,j]·k[i,k]/sqrt(d) + bias[h,j,k];  masked_fill(~mask[i,k], -inf)
+        o[i,j] = sum_k softmax_k(logit[j,k]) v[i,k]
+        out = LinearNoBias(g ⊙ o)
+    Ending node = starting node applied to z^T (mask^T), output transposed back.
+
+    Keys: norm.{weight,bias}, proj_q/k/v/g.weight [H*d, c], proj_b.weight [H, c],
+    proj_o.weight [c, H*d].
+    """
+    z = _f32(z)
+    m = mask.bool()
+    if not starting:
+        z = z.transpose(1, 2)
+        m = m.transpose(1, 2)
+    B, N, _, _ = z.shape
+    H = num_heads
+    zn = _ln(z, params, "norm")
+    wq, wk, wv = (_p(params, f"proj_{n}.weight") for n in "qkv")
+    hd = wq.shape[0]
+    d = hd // H
+    q = (zn @ wq.T).view(B, N, N, H, d)
+    k = (zn @ wk.T).view(B, N, N, H, d)
+    v = (zn @ wv.T).view(B, N, N, H, d)
+    g = torch.sigmoid(zn @ _p(params, "proj_g.weight").T)
+    bias = (zn @ _p(params, "proj_b.weight").T).permute(0, 3, 1, 2)  # [B,H,N(j),N(k)]
+    o = torch.empty(B, N, N, H, d)
+    chunk = row_chunk or N
+    for r0 in range(0, N, chunk):
+        r1 = min(N, r0 + chunk)
+        # logits [B, rows, H, j, k]
+        logit = torch.einsum("brjhd,brkhd->brhjk", q[:, r0:r1], k[:, r0:r1])
+        logit = logit / math.sqrt(d) + bias.unsqueeze(1)
+        key_mask = m[:, r0:r1][:, :, None, None, :]  # [B, rows, 1, 1, k]
+        logit = logit.masked_fill(~key_mask, -inf)
+        attn = logit.softmax(dim=-1)
+        o[:, r0:r1] = torch.einsum("brhjk,brkhd->brjhd", attn, v[:, r0:r1])
+    out = (g * o.reshape(B, N, N, hd)) @ _p(params, "proj_o.weight").T
+    if not starting:
+        out = out.transpose(1, 2)
+    return out.contiguous()
+
+
+# ----------------------------------------------------------------------------
+# Attention with pair bias
+# ----------------------------------------------------------------------------
+def attention_pair_bias(
+    s: Tensor,
+    z: Tensor,
+    mask: Tensor,
+    params: dict,
+    num_heads: int,
+    multiplicity: int = 1,
+    initial_norm: bool = True,
+    tile_size: int | None = 512,
+    inf: float = 1e6,
+) -> Tensor:
+    """AttentionPairBias.forward (biomoa/ops/attention_pair_bias.py:128-225).
+
+    s [B*M,N,c_s], z [B,N,N,c_z], mask [B,N] bool -> [B*M,N,c_s] (float32).
+    Bias = permute(proj_z(norm_z(z))) (``_proj_z_fused`` non-fused branch,
+    :114-117); ``norm_z`` has a bias only when its key is present
+    (``use_bias_in_layer_norm``, :90).  The core runs query-tiled when
+    ``tile_size < N`` (:193-222) exactly as the reference does.
+    """
+    s = _f32(s)
+    z = _f32(z)
+    mask = mask.bool().cpu()
+    assert s.ndim == 3 and z.ndim == 4 and mask.ndim == 2  # :146
+    assert s.shape[0] == z.shape[0] * multiplicity  # :147
+    BM, N, c_s = s.shape
+    H = num_heads
+    d = c_s // H
+    if initial_norm:
+        s = _ln(s, params, "norm_s")  # :152-153
+    qkv = s @ _p(params, "proj_qkv.weight").T  # :156
+    q, k, v = qkv.chunk(3, dim=-1)  # :157
+    q = (q + _p(params, "proj_q_bias")).view(BM, N, H, d)  # :158
+    k = k.view(BM, N, H, d)
+    v = v.view(BM, N, H, d)
+    g = torch.sigmoid(s @ _p(params, "proj_g.weight").T)  # :161
+    zb = _ln(z, params, "norm_z") @ _p(params, "proj_z.weight").T  # :115-116
+    z_f = zb.permute(0, 3, 1, 2)  # [B,H,N,N] (:117)
+    B_real = z_f.shape[0]
+    mask_view = mask.unsqueeze(1).unsqueeze(1)  # [B,1,1,N] (:184)
+    chunk = tile_size
+    if chunk is None or chunk >= N:
+        chunk = N
+    o = torch.zeros(BM, N, H, d)
+    for qs in range(0, N, chunk):
+        qe = min(qs + chunk, N)
+        attn = torch.einsum("bchd,bnhd->bhcn", q[:, qs:qe], k)  # :206
+        attn = attn / (d**0.5)  # :207
+        z_chunk = z_f[..., qs:qe, :]
+        attn = (
+            attn.view(B_real, multiplicity, *z_chunk.shape[1:]) + z_chunk.unsqueeze(1)
+        ).view(attn.shape)  # :209-214
+        attn = (
+            attn.view(B_real, multiplicity, *attn.shape[1:]).masked_fill(
+                ~mask_view.unsqueeze(1), -inf
+            )
+        ).view(attn.shape)  # :215-220
+        attn = attn.softmax(dim=-1)  # :221
+        o[:, qs:qe] = torch.einsum("bhcn,bnhd->bchd", attn, v)  # :222
+    o = o.reshape(BM, N, c_s)  # :224
+    return (g * o) @ _p(params, "proj_o.weight").T  # :225
+
+
+# ----------------------------------------------------------------------------
+# Outer product mean
+# ----------------------------------------------------------------------------
+def outer_product_mean(m: Tensor, mask: Tensor, params: dict, i_chunk: int | None = None) -> Tensor:
+    """OuterProductMeanVanilla.forward (biomoa/ops/outer_product_mean.py:45-75).
+
+    m [B,S,N,C_in], mask [B,S,N] or [B,N] -> [B,N,N,C_out] (float32).
+    ``num_valid = mask.any(-1).sum(1).clamp(min=1)`` per batch for a [B,S,N]
+    mask, 1 for a [B,N] mask (:67-70); flatten order c*C_H + d (:72-73); the
+    mean is taken before the output projection (:74-75 and the memory-saving
+    kernel's "normalize before the cast", ops/triton/opm.py:114-116).
+    """
+    m = _f32(m)
+    mask = mask.bool().cpu()
+    mp = _ln(m, params, "norm") @ _p(params, "proj_ab.weight").T  # :61
+    mp = mp.masked_fill(~mask.unsqueeze(-1), 0.0)  # :62
+    a, b = mp.chunk(2, dim=-1)  # :63
+    if mask.ndim == 3:
+        num_valid = mask.any(dim=-1).sum(dim=1).clamp(min=1).float()  # :68
+    else:
+        num_valid = torch.ones(m.shape[0])  # :70
+    B, S, N, C = a.shape
+    wo = _p(params, "proj_o.weight")
+    bo = _p(params, "proj_o.bias")
+    out = torch.empty(B, N, N, wo.shape[0])
+    step = i_chunk or N
+    for i0 in range(0, N, step):
+        i1 = min(N, i0 + step)
+        zc = torch.einsum("bsic,bsjd->bijcd", a[:, :, i0:i1], b)  # :72
+        zc = zc.reshape(B, i1 - i0, N, C * C)  # :73
+        zc = zc / num_valid[:, None, None, None]  # :74
+        out[:, i0:i1] = zc @ wo.T + bo  # :75
+    return out
+
+
+# ----------------------------------------------------------------------------
+# Transition (SwiGLU MLP)
+# ----------------------------------------------------------------------------
+def transition(x: Tensor, params: dict, use_norm: bool = True) -> Tensor:
+    """Transition.forward (biomoa/ops/transition.py:52-76): fc3(silu(fc1(xn)) * fc2(xn))."""
+    x = _f32(x)
+    if use_norm:
+        x = _ln(x, params, "norm")  # :68-69
+    a = F.silu(x @ _p(params, "fc1.weight").T)  # :71-72
+    b = x @ _p(params, "fc2.weight").T  # :73
+    return (a * b) @ _p(params, "fc3.weight").T  # :74-75
+
+
+# ----------------------------------------------------------------------------
+# Pairformer block (NOT in the reference: AF3 supplement Alg. 17 ordering)
+# ----------------------------------------------------------------------------
+def _sub(params: dict, prefix: str) -> dict:
+    n = len(prefix) + 1
+    return {k[n:]: v for k, v in params.items() if k.startswith(prefix + ".")}
+
+
+def pairformer_block(
+    s: Tensor,
+    z: Tensor,
+    token_mask: Tensor,
+    params: dict,
+    triatt_heads: int = 4,
+    apb_heads: int = 16,
+    triatt_row_chunk: int | None = None,
+) -> tuple[Tensor, Tensor]:
+    """One Pairformer block (AF3 suppl. Alg. 17) built from the reference ops.
+
+    z += TriMulOut; z += TriMulIn; z += TriAttStart; z += TriAttEnd; z += Transition_z;
+    s += APB(s, z, mask) (initial_norm=True); s += Transition_s.
+    Residual form and dropout-at-eval identity follow PairMixerLayer.forward
+    (biomoa/modules/pairmixer.py:446-456) and apply_axiswise_dropout
+    (biomoa/ops/dropout.py:68-69).  pair_mask = mask_i & mask_j (pairmixer.py:263-264).
+    """
+    s = _f32(s)
+    z = _f32(z)
+    pm = pair_mask_from_token_mask(token_mask.cpu())
+    z = z + trimul(z, pm, _sub(params, "tri_mul_out"), "outgoing")
+    z = z + trimul(z, pm, _sub(params, "tri_mul_in"), "incoming")
+    z = z + triangle_attention(
+        z, pm, _sub(params, "tri_att_start"), triatt_heads, True, row_chunk=triatt_row_chunk
+    )
+    z = z + triangle_attention(
+        z, pm, _sub(params, "tri_att_end"), triatt_heads, False, row_chunk=triatt_row_chunk
+    )
+    z = z + transition(z, _sub(params, "transition_z"))
+    s = s + attention_pair_bias(
+        s, z, token_mask.bool(), _sub(params, "attention_pair_bias"), apb_heads, tile_size=None
+    )
+    s = s + transition(s, _sub(params, "transition_s"))
+    return s, z

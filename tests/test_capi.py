@@ -1,0 +1,58 @@
+"""CPU checks of the C ABI: the library loads and exports every declared symbol."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from bioemu2_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+_DECL = re.compile(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b(bioemu_\w+)\s*\(", re.M)
+
+
+def _declared() -> list[str]:
+    names: list[str] = []
+    for h in sorted((ROOT / "include").glob("*.h")):
+        names += _DECL.findall(h.read_text())
+    return sorted(set(names))
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    assert "bioemu_trimul_fwd" in names
+    assert len(names) >= 4
+
+
+def test_library_exports_every_declared_symbol():
+    if not _lib.LIB_PATH.exists():
+        pytest.fail(f"native library not built: {_lib.LIB_PATH}")
+    handle = ctypes.CDLL(str(_lib.LIB_PATH))
+    missing = [n for n in _declared() if not hasattr(handle, n)]
+    assert not missing, missing
+
+
+def test_python_binding_covers_every_declared_symbol():
+    assert sorted(_lib.SIGNATURES) == _declared()
+
+
+def test_host_only_queries():
+    lib = _lib.lib()
+    assert b"gfx950" in lib.bioemu_version()
+    n = 768
+    np_ = 768  # already a multiple of 128
+    assert lib.bioemu_trimul_workspace_bytes(1, n, 128) == 3 * 128 * np_ * np_ * 2
+    assert lib.bioemu_trimul_workspace_bytes(0, n, 128) == 0
+
+
+def test_invalid_arguments_rejected_without_gpu():
+    """Argument validation runs on the host before any launch."""
+    lib = _lib.lib()
+    rc = lib.bioemu_trimul_fwd(*([None] * 11), None, 0, 1, 16, 128, 1, 0, None)
+    assert rc == -1
+    assert b"null" in lib.bioemu_last_error()
+    rc = lib.bioemu_trimul_fwd(*([None] * 11), None, 0, 1, 16, 64, 1, 0, None)
+    assert rc == -2

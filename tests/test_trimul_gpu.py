@@ -1,0 +1,141 @@
+"""HIP TriMul vs the fp32 CPU oracle, plus bit-exact mask/padding invariance on the GPU."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import oracle
+from bioemu2_amd import _ops
+from bioemu2_amd.strategy import make
+from bioemu2_amd.triangle_multiplication import REGISTRY, TriangleMultiplicationHip
+from tests._helpers import max_abs, redraw_zero_params, rel_l2, state
+
+pytestmark = pytest.mark.gpu
+
+D = 128
+# north_star tolerance for bf16 vs the fp32 reference
+ATOL = 2e-2
+RTOL_L2 = 1e-2
+
+
+def _module(mode: str, device) -> TriangleMultiplicationHip:
+    torch.manual_seed(42)
+    m = make(REGISTRY, "cueq", dim=D, mode=mode, tile_size=None, matmul_precision="ieee")
+    return redraw_zero_params(m).to(device).eval()
+
+
+def _inputs(n: int, device, seed: int = 0, p_valid: float = 0.75):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(1, n, n, D, generator=g).to(torch.bfloat16)
+    mask = torch.rand(1, n, n, generator=g) < p_valid
+    return x.to(device), mask.to(device)
+
+
+@pytest.mark.parametrize("mode", ["outgoing", "incoming"])
+@pytest.mark.parametrize("n", [16, 37, 130, 256])
+def test_matches_oracle(gpu_device, mode, n):
+    m = _module(mode, gpu_device)
+    x, mask = _inputs(n, gpu_device)
+    with torch.no_grad():
+        got = m(x, mask).float().cpu()
+    want = oracle.trimul(x.float().cpu(), mask.cpu(), state(m), mode)
+    assert want.abs().max() > 0
+    err, rl2 = max_abs(got, want), rel_l2(got, want)
+    print(f"trimul {mode} n={n}: max_abs={err:.3e} rel_l2={rl2:.3e}")
+    assert err <= ATOL and rl2 <= RTOL_L2
+
+
+def test_matches_oracle_n768_token_padding(gpu_device):
+    """Config 4 shape: N=768, last 76 tokens padded, pair mask = outer AND."""
+    n = 768
+    m = _module("outgoing", gpu_device)
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(1, n, n, D, generator=g).to(torch.bfloat16)
+    tok = torch.ones(1, n, dtype=torch.bool)
+    tok[:, n - 76:] = False
+    pm = oracle.pair_mask_from_token_mask(tok)
+    with torch.no_grad():
+        got = m(x.to(gpu_device), pm.to(gpu_device)).float().cpu()
+    want = oracle.trimul(x.float(), pm, state(m), "outgoing")
+    err, rl2 = max_abs(got, want), rel_l2(got, want)
+    print(f"trimul outgoing n=768: max_abs={err:.3e} rel_l2={rl2:.3e}")
+    assert err <= ATOL and rl2 <= RTOL_L2
+
+
+@pytest.mark.parametrize("mode", ["outgoing", "incoming"])
+def test_masking_bit_exact(gpu_device, mode):
+    m = _module(mode, gpu_device)
+    x, mask = _inputs(70, gpu_device)
+    changed = x.clone()
+    changed[~mask] = 1000.0
+    with torch.no_grad():
+        a = m(x, mask)
+        b = m(changed, mask)
+    assert torch.equal(a[mask], b[mask])
+
+
+@pytest.mark.parametrize("mode", ["outgoing", "incoming"])
+def test_padding_bit_exact(gpu_device, mode):
+    n, pad = 100, 29  # crosses the 128 padding boundary of the contraction
+    m = _module(mode, gpu_device)
+    x, mask = _inputs(n, gpu_device)
+    px = torch.full((1, n + pad, n + pad, D), 1000.0, dtype=x.dtype, device=gpu_device)
+    px[:, :n, :n] = x
+    pmask = torch.zeros(1, n + pad, n + pad, dtype=torch.bool, device=gpu_device)
+    pmask[:, :n, :n] = mask
+    with torch.no_grad():
+        a = m(x, mask)
+        b = m(px, pmask)[:, :n, :n]
+    assert torch.equal(a, b)
+
+
+def test_batch_equals_separate(gpu_device):
+    m = _module("incoming", gpu_device)
+    x0, m0 = _inputs(48, gpu_device, seed=1)
+    x1, m1 = _inputs(48, gpu_device, seed=2)
+    with torch.no_grad():
+        both = m(torch.cat([x0, x1]), torch.cat([m0, m1]))
+        assert torch.equal(both[0:1], m(x0, m0))
+        assert torch.equal(both[1:2], m(x1, m1))
+
+
+def test_deterministic(gpu_device):
+    m = _module("outgoing", gpu_device)
+    x, mask = _inputs(130, gpu_device)
+    with torch.no_grad():
+        assert torch.equal(m(x, mask), m(x, mask))
+
+
+@pytest.mark.parametrize("mode", ["outgoing", "incoming"])
+def test_fused_residual_in_place(gpu_device, mode):
+    m = _module(mode, gpu_device)
+    x, mask = _inputs(64, gpu_device)
+    with torch.no_grad():
+        upd = m(x, mask)
+        z = x.clone()
+        _ops.launch_trimul(z, _ops.mask_u8(mask), *m.prepared_params(), z, mode == "outgoing", residual=True)
+    ref = (x.float() + upd.float())
+    assert max_abs(z.float(), ref) <= 2 ** -7 * ref.abs().max().item()
+
+
+def test_fp32_input_roundtrip(gpu_device):
+    m = _module("outgoing", gpu_device)
+    x, mask = _inputs(40, gpu_device)
+    with torch.no_grad():
+        a = m(x.float(), mask)
+        b = m(x, mask)
+    assert a.dtype == torch.float32
+    assert torch.equal(a, b.float())
+
+
+def test_rejects_cpu_tensors():
+    m = TriangleMultiplicationHip(dim=D)
+    with pytest.raises(RuntimeError):
+        m(torch.zeros(1, 4, 4, D), torch.ones(1, 4, 4, dtype=torch.bool))
+
+
+def test_rejects_unsupported_dim(gpu_device):
+    m = TriangleMultiplicationHip(dim=64).to(gpu_device)
+    with pytest.raises(ValueError):
+        m(torch.zeros(1, 8, 8, 64, device=gpu_device), torch.ones(1, 8, 8, dtype=torch.bool, device=gpu_device))
