@@ -1,0 +1,182 @@
+"""Benchmark of the MI355X Pairformer hot path (one GPU).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--op block] [--n 768]
+
+A "step" is one forward pass of the selected op over one batch of synthetic,
+HBM-resident input.  The default op is one full bf16 Pairformer block at N=768,
+c_z=128, c_s=384 (the BASELINE metric); ``--op`` selects a single op at its
+config shape instead (those are diagnostic lines).
+
+Printed on one line as JSON: ms per step, the roofline of the dominant kernel
+(its average duration measured live with the library's hipEvent kernel timer
+on the kernel's own launch stream, over the timed region) and a CPU baseline
+(the fp32 oracle timed on a bounded sample, rank 0 only).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
+
+
+def _parse() -> argparse.Namespace:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--op", default="block")
+    ap.add_argument("--n", type=int, default=None, help="override N (tokens)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kernels", action="store_true", help="also print the per-kernel table to stderr")
+    return ap.parse_args()
+
+
+def cpu_baseline(wl) -> dict:
+    """The fp32 CPU oracle on a bounded sample of the same workload (rank 0, N=1 only).
+
+    1 warm-up then the median of up to 3 timed calls, stopping early once
+    ~30 s of CPU time is spent; ``value`` is scaled to ms per full step.
+    """
+    import torch
+
+    import oracle  # the checker, timed here as the CPU baseline only
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    fn, fraction, sample = wl.cpu_sample(oracle)
+    fn()  # warm-up
+    times = []
+    budget = time.perf_counter() + 30.0
+    while len(times) < 3:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() > budget:
+            break
+    times.sort()
+    med = times[len(times) // 2]
+    return {
+        "value": round(med * 1e3 / fraction, 1),
+        "unit": "ms",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{sample}; {len(times)} timed call(s) after 1 warm-up, median",
+    }
+
+
+def main() -> int:
+    args = _parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(
+            "bench.py measures one MI355X only: this build has no multi-GPU path "
+            "(how the ops would shard is described in DESIGN.md). Run with --gpus 1.",
+            file=sys.stderr,
+        )
+        return 2
+
+    import torch
+
+    from bioemu2_amd import workloads
+    from bioemu2_amd.timing import KernelTimer
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    wl = workloads.make(args.op, dev, n=args.n)
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            wl.step()
+        torch.cuda.synchronize()
+
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        with KernelTimer() as kt:
+            torch.cuda.synchronize()
+            start.record()
+            for _ in range(args.steps):
+                wl.step()
+            stop.record()
+            torch.cuda.synchronize()
+        ms_per_step = start.elapsed_time(stop) / args.steps
+        kernels = kt.results()
+
+    # Dominant kernel = largest total time in the timed region.
+    dom_name, (dom_launches, dom_ms) = max(kernels.items(), key=lambda kv: kv[1][1])
+    dom_avg_ms = dom_ms / dom_launches
+    work = wl.kernel_work(dom_name)  # (bound, algorithmic amount per launch)
+    bound, amount = work
+    if bound == "mfma":
+        achieved = amount / (dom_avg_ms * 1e-3) / 1e12
+        peak, unit = PEAK_BF16_TFLOPS, "TFLOP/s"
+    else:
+        achieved = amount / (dom_avg_ms * 1e-3) / 1e9
+        peak, unit = PEAK_HBM_GBS, "GB/s"
+    roofline = {
+        "kernel": dom_name,
+        "bound": bound,
+        "achieved": round(achieved, 2),
+        "peak": peak,
+        "unit": unit,
+        "frac": round(achieved / peak, 4),
+        "traffic": workloads.measured_traffic(dom_name, wl.name),
+        "avg_ms": round(dom_avg_ms, 5),
+        "algorithmic_per_launch": amount,
+    }
+    per_kernel = {}
+    for name, (n, ms) in sorted(kernels.items(), key=lambda kv: -kv[1][1]):
+        b, a = wl.kernel_work(name)
+        avg = ms / n
+        rate = a / (avg * 1e-3) / (1e12 if b == "mfma" else 1e9)
+        per_kernel[name] = {
+            "launches_per_step": n / args.steps,
+            "avg_ms": round(avg, 5),
+            "bound": b,
+            "rate": round(rate, 1),
+            "frac": round(rate / (PEAK_BF16_TFLOPS if b == "mfma" else PEAK_HBM_GBS), 4),
+        }
+    if args.kernels:
+        for k, v in per_kernel.items():
+            print(f"[kernel] {k}: {v}", file=sys.stderr)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(wl)
+
+    line = {
+        "metric": wl.metric,
+        "value": round(ms_per_step, 4),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded randn inputs, seeded random-init weights)",
+        "config": wl.config,
+        "tflops": round(wl.flops / (ms_per_step * 1e-3) / 1e12, 1),
+        "roofline": roofline,
+        "kernels": per_kernel,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -21,6 +21,13 @@ _c_int = ctypes.c_int
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "bioemu_version": (ctypes.c_char_p, []),
     "bioemu_last_error": (ctypes.c_char_p, []),
+    "bioemu_timer_enable": (_c_int, [_c_int]),
+    "bioemu_timer_reset": (_c_int, []),
+    "bioemu_timer_count": (_c_int, []),
+    "bioemu_timer_query": (
+        _c_int,
+        [_c_int, ctypes.c_char_p, _c_size_t, ctypes.POINTER(_c_int64), ctypes.POINTER(ctypes.c_double)],
+    ),
     "bioemu_trimul_workspace_bytes": (_c_size_t, [_c_int64, _c_int64, _c_int64]),
     "bioemu_trimul_fwd": (
         _c_int,

@@ -127,6 +127,7 @@ int launch_bgemm_nt(const void* A, const void* B, void* C, int64_t batch, int64_
                      (long long)batch, (long long)n);
   }
   dim3 grid((unsigned)(n / BN), (unsigned)(n / BM), (unsigned)batch);
+  KernelTimerScope timed("bgemm_nt", stream);
   hipLaunchKernelGGL(bgemm_nt_kernel, grid, dim3(kThreads), 0, stream,
                      static_cast<const bf16*>(A), static_cast<const bf16*>(B), static_cast<bf16*>(C),
                      (int)n);

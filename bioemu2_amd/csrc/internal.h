@@ -15,6 +15,21 @@ int set_error(int code, const char* fmt, ...);
 // Checks the launch status of the most recent kernel launch.
 int check_launch(const char* what);
 
+// Brackets one kernel launch with hipEvents on `stream` while the kernel
+// timer is enabled (bioemu_timer_enable); a no-op otherwise.
+class KernelTimerScope {
+ public:
+  KernelTimerScope(const char* name, hipStream_t stream);
+  ~KernelTimerScope();
+  KernelTimerScope(const KernelTimerScope&) = delete;
+  KernelTimerScope& operator=(const KernelTimerScope&) = delete;
+
+ private:
+  hipStream_t stream_;
+  int name_idx_ = -1;
+  hipEvent_t start_ = nullptr, stop_ = nullptr;
+};
+
 inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }

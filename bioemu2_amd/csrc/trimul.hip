@@ -253,6 +253,8 @@ extern "C" int bioemu_trimul_fwd(const void* x, const uint8_t* mask, const float
   bf16* ob = ab + 2 * plane_elems;
 
   dim3 g1((unsigned)(Np / 64), (unsigned)(Np / 4), (unsigned)B);
+  {
+  KernelTimerScope timed("trimul_proj_in", stream);
   if (outgoing) {
     hipLaunchKernelGGL(trimul_proj_in_kernel<true>, g1, dim3(kThreads), 0, stream,
                        static_cast<const bf16*>(x), mask, norm_in_w, norm_in_b,
@@ -264,18 +266,17 @@ extern "C" int bioemu_trimul_fwd(const void* x, const uint8_t* mask, const float
                        static_cast<const bf16*>(p_in_w), static_cast<const bf16*>(g_in_w), ab, (int)B,
                        (int)N, (int)Np);
   }
+  }
   int rc = check_launch("trimul_proj_in");
   if (rc) return rc;
   rc = launch_bgemm_nt(ab, ab + plane_elems, ob, B * D, Np, stream);
   if (rc) return rc;
 
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipFuncSetAttribute(reinterpret_cast<const void*>(trimul_out_kernel),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, kOutSmem);
-    attr_set = true;
-  }
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(trimul_out_kernel),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, kOutSmem) != hipSuccess)
+    return set_error(BIOEMU_ERR_LAUNCH, "trimul_out: cannot set dynamic LDS size");
   dim3 g3((unsigned)((N + 63) / 64), (unsigned)((N + 3) / 4), (unsigned)B);
+  KernelTimerScope timed("trimul_out", stream);
   hipLaunchKernelGGL(trimul_out_kernel, g3, dim3(kThreads), kOutSmem, stream, ob,
                      static_cast<const bf16*>(x), norm_in_w, norm_in_b, norm_out_w, norm_out_b,
                      static_cast<const bf16*>(p_out_w), static_cast<const bf16*>(g_out_w),

@@ -1,0 +1,139 @@
+"""Synthetic, HBM-resident workloads for the benchmark configs.
+
+Each workload owns its seeded inputs, random-init weights, preallocated
+outputs and workspaces, so ``step()`` launches kernels and allocates nothing.
+``kernel_work(name)`` gives the algorithmic work of one launch of a named
+kernel at the workload's shape: ``("mfma", flops)`` or ``("hbm", bytes)``,
+chosen by comparing the kernel's flops per minimum HBM byte with the MI355X
+ridge point (2.5 PFLOP/s / 8 TB/s ~ 312 flop/B).
+"""
+
+from __future__ import annotations
+
+import json
+import math
+from pathlib import Path
+
+import torch
+from torch import Tensor
+
+from . import _ops
+
+RIDGE = 2500e12 / 8000e9
+_PROFILES = Path(__file__).resolve().parents[1] / "profiles" / "traffic.json"
+
+
+def measured_traffic(kernel: str, workload: str):
+    """HBM bytes per launch measured with rocprofv3 PMC counters, if recorded."""
+    try:
+        table = json.loads(_PROFILES.read_text())
+    except (OSError, ValueError):
+        return None
+    return table.get(workload, {}).get(kernel)
+
+
+def token_mask(n: int, n_pad: int, device, batch: int = 1) -> Tensor:
+    """Valid tokens first, the last ``n_pad`` padded (deterministic trailing padding)."""
+    m = torch.ones(batch, n, dtype=torch.bool)
+    if n_pad:
+        m[:, n - n_pad:] = False
+    return m.to(device)
+
+
+def init_module(module: torch.nn.Module, seed: int = 0) -> torch.nn.Module:
+    """Module default init under ``manual_seed(seed)``, then zero params re-drawn N(0, 0.02)."""
+    with torch.no_grad():
+        g = torch.Generator().manual_seed(seed + 1)
+        for p in module.parameters():
+            if torch.count_nonzero(p) == 0:
+                p.copy_(torch.randn(p.shape, generator=g) * 0.02)
+    return module
+
+
+def _bound(flops: float, nbytes: float) -> tuple[str, float]:
+    if nbytes <= 0 or flops / nbytes > RIDGE:
+        return ("mfma", float(flops))
+    return ("hbm", float(nbytes))
+
+
+# ----------------------------------------------------------------------------
+# Per-kernel algorithmic work.  P = B*N*N pairs, c = 128 channels, bf16 = 2 B.
+# ----------------------------------------------------------------------------
+def trimul_kernel_work(name: str, B: int, N: int, c: int = 128) -> tuple[str, float] | None:
+    P = B * N * N
+    if name == "trimul_proj_in":
+        # LN + [p_in | g_in] (c -> 4c) ; reads x, writes a and b planes
+        return _bound(2.0 * P * c * 4 * c, P * (c * 2 + 2 * c * 2))
+    if name == "bgemm_nt":
+        # o[d,i,j] = sum_k a[d,i,k] b[d,j,k] over the valid N
+        return _bound(2.0 * B * c * N * N * N, 3 * P * c * 2)
+    if name == "trimul_out":
+        # LN_out(o) -> p_out, LN_in(x) -> g_out ; reads o and x, writes out
+        return _bound(2.0 * P * c * 2 * c, 3 * P * c * 2)
+    return None
+
+
+class Workload:
+    name: str
+    metric: str
+    config: dict
+    flops: float
+
+    def step(self) -> None:
+        raise NotImplementedError
+
+    def kernel_work(self, kernel: str) -> tuple[str, float]:
+        raise NotImplementedError
+
+    def cpu_sample(self, oracle):
+        raise NotImplementedError
+
+
+class TriMulWorkload(Workload):
+    """Config 4: one triangle multiplication (outgoing or incoming) at N=768, bf16."""
+
+    def __init__(self, device, mode: str, n: int = 768, seed: int = 0):
+        from .triangle_multiplication import TriangleMultiplicationHip
+
+        self.mode = mode
+        self.n = n
+        self.n_pad = n // 10
+        self.name = f"trimul_{'out' if mode == 'outgoing' else 'in'}_n{n}"
+        self.metric = f"ms per triangle multiplication ({mode}) at N={n} bf16"
+        self.config = {"workload": self.name, "N": n, "c_z": 128, "batch": 1, "padded_tokens": self.n_pad}
+        torch.manual_seed(seed)
+        self.module = init_module(TriangleMultiplicationHip(dim=128, mode=mode), seed).to(device).eval()
+        g = torch.Generator().manual_seed(seed)
+        self.x_cpu = torch.randn(1, n, n, 128, generator=g).to(torch.bfloat16)
+        self.x = self.x_cpu.to(device)
+        self.tok = token_mask(n, self.n_pad, device)
+        self.pair_mask = _ops.mask_u8(self.tok[:, :, None] & self.tok[:, None, :])
+        self.out = torch.empty_like(self.x)
+        self.ws = _ops.workspace(_ops.trimul_workspace_bytes(1, n, 128), device)
+        self.params = self.module.prepared_params()
+        self.flops = 2.0 * n * n * 128 * (4 * 128 + 2 * 128) + 2.0 * 128 * n ** 3
+
+    def step(self) -> None:
+        _ops.launch_trimul(self.x, self.pair_mask, *self.params, self.out, self.mode == "outgoing", ws=self.ws)
+
+    def cpu_sample(self, oracle):
+        """(callable, fraction of one step it computes, description) for the CPU baseline."""
+        x = self.x_cpu.float()
+        pm = (self.tok[:, :, None] & self.tok[:, None, :]).cpu()
+        params = {k: v.detach().cpu() for k, v in self.module.state_dict().items()}
+        return (lambda: oracle.trimul(x, pm, params, self.mode)), 1.0, f"oracle.trimul fp32, full N={self.n}"
+
+    def kernel_work(self, kernel: str) -> tuple[str, float]:
+        w = trimul_kernel_work(kernel, 1, self.n)
+        if w is None:
+            raise KeyError(kernel)
+        return w
+
+
+def make(op: str, device, n: int | None = None) -> Workload:
+    if op in ("trimul_out", "trimul_in"):
+        return TriMulWorkload(device, "outgoing" if op == "trimul_out" else "incoming", n or 768)
+    raise ValueError(f"unknown bench op {op!r}")
+
+
+__all__ = ["make", "measured_traffic", "Workload", "token_mask", "init_module", "math"]

@@ -38,6 +38,19 @@ const char* bioemu_version(void);
 const char* bioemu_last_error(void);
 
 /*
+ * Kernel timer (instrumentation; no counterpart in the reference, which times
+ * whole calls with CUDA events, examples/search_batch_size.py:28-46).
+ * While enabled, every kernel this library launches is bracketed by two
+ * hipEvents on its launch stream.  bioemu_timer_query() synchronises on the
+ * pending events and returns, per kernel name, the launch count and the summed
+ * event-to-event duration in milliseconds.
+ */
+int bioemu_timer_enable(int on);
+int bioemu_timer_reset(void);
+int bioemu_timer_count(void);
+int bioemu_timer_query(int idx, char* name, size_t name_len, int64_t* launches, double* total_ms);
+
+/*
  * Triangle multiplicative update, outgoing (outgoing=1) or incoming (0).
  *
  * Replaces TriangleMultiplicationFull.forward / TriangleMultiplicationCueq.forward
