@@ -33,6 +33,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _c_int,
         [_c_void_p] * 11 + [_c_void_p, _c_size_t, _c_int64, _c_int64, _c_int64, _c_int, _c_int, _c_void_p],
     ),
+    "bioemu_triatt_workspace_bytes": (_c_size_t, [_c_int64] * 4),
+    "bioemu_triatt_fwd": (
+        _c_int,
+        [_c_void_p] * 7 + [_c_void_p, _c_size_t] + [_c_int64] * 4 + [_c_int, _c_int, _c_void_p],
+    ),
 }
 
 _lock = threading.Lock()

@@ -146,3 +146,73 @@ def trimul(
 @trimul.register_fake
 def _(x, mask, norm_in_w, norm_in_b, p_in_w, g_in_w, norm_out_w, norm_out_b, p_out_w, g_out_w, outgoing):
     return torch.empty_like(x)
+
+
+# ----------------------------------------------------------------------------
+# Triangle attention
+# ----------------------------------------------------------------------------
+def triatt_workspace_bytes(B: int, N: int, D: int = 128, H: int = 4) -> int:
+    return int(lib().bioemu_triatt_workspace_bytes(B, N, D, H))
+
+
+def launch_triatt(
+    z: Tensor,
+    mask: Tensor,
+    norm_w: Tensor,
+    norm_b: Tensor,
+    w_proj: Tensor,
+    w_o: Tensor,
+    out: Tensor,
+    starting: bool,
+    num_heads: int = 4,
+    residual: bool = False,
+    ws: Tensor | None = None,
+) -> Tensor:
+    require_gpu(z, "triatt")
+    if z.ndim != 4 or z.shape[1] != z.shape[2]:
+        raise ValueError(f"triatt: z must be [B,N,N,D], got {tuple(z.shape)}")
+    B, N, _, D = z.shape
+    dev = z.device
+    _check_tensor(z, "triatt z", BF16, (B, N, N, D), dev)
+    _check_tensor(out, "triatt out", BF16, (B, N, N, D), dev)
+    _check_tensor(mask, "triatt mask", torch.uint8, (B, N, N), dev)
+    _check_tensor(norm_w, "triatt norm.weight", torch.float32, (D,), dev)
+    _check_tensor(norm_b, "triatt norm.bias", torch.float32, (D,), dev)
+    _check_tensor(w_proj, "triatt packed projection", BF16, (4 * D + num_heads, D), dev)
+    _check_tensor(w_o, "triatt proj_o.weight", BF16, (D, D), dev)
+    need = triatt_workspace_bytes(B, N, D, num_heads)
+    if ws is None or ws.numel() < need:
+        ws = workspace(need, dev)
+    rc = lib().bioemu_triatt_fwd(
+        _ptr(z), _ptr(mask), _ptr(norm_w), _ptr(norm_b), _ptr(w_proj), _ptr(w_o), _ptr(out),
+        _ptr(ws), ctypes.c_size_t(ws.numel()), B, N, D, num_heads, int(bool(starting)),
+        int(bool(residual)), _stream(z),
+    )
+    check(rc, "bioemu_triatt_fwd")
+    return out
+
+
+@torch.library.custom_op("bioemu_mi355x::triangle_attention", mutates_args=(), device_types="cuda")
+def triangle_attention(
+    z: Tensor,
+    mask: Tensor,
+    norm_w: Tensor,
+    norm_b: Tensor,
+    w_proj: Tensor,
+    w_o: Tensor,
+    starting: bool,
+    num_heads: int,
+) -> Tensor:
+    zb = z.to(BF16).contiguous()
+    out = torch.empty_like(zb)
+    f32 = torch.float32
+    launch_triatt(
+        zb, mask_u8(mask), norm_w.to(f32).contiguous(), norm_b.to(f32).contiguous(),
+        w_proj.to(BF16).contiguous(), w_o.to(BF16).contiguous(), out, starting, num_heads,
+    )
+    return out.to(z.dtype)
+
+
+@triangle_attention.register_fake
+def _(z, mask, norm_w, norm_b, w_proj, w_o, starting, num_heads):
+    return torch.empty_like(z)

@@ -1,0 +1,132 @@
+// Register-resident pair tiles for the 32x32x16 bf16 MFMA.
+//
+// A wave holds a tile of 32 pairs x 128 channels as MFMA operands: lane l
+// (rho = l & 31, h = l >> 5) owns pair slot rho and channel half h, i.e.
+// channels [64h, 64h + 64).  For the 8 MFMA k-steps s the lane supplies
+// channels 64h + 8s .. 64h + 8s + 7 (a k-permutation of the 128 channels;
+// the weight operand reads the same channels, so the product is unchanged).
+//
+// Pair slots are filled in the order perm32(rho), which makes the
+// accumulator of an MFMA whose rows are pair slots come out with every lane
+// holding 16 *consecutive* pairs:  D lane (n, h) register u  <->  pair 16h + u.
+// The same permutation applied to weight rows makes a lane hold 16
+// consecutive output channels.  Both give 32-byte contiguous stores.
+#pragma once
+
+#include "common.h"
+
+namespace bioemu {
+
+constexpr int kPairC = 128;          // channels of a pair tile
+constexpr int kLdw = kPairC + 8;     // LDS row stride (bf16) of 128-wide weight rows
+
+// rho = 8r + 4h + c  ->  16h + 4r + c
+__device__ __forceinline__ int perm32(int rho) {
+  return ((rho >> 2) & 1) * 16 + (rho >> 3) * 4 + (rho & 3);
+}
+
+// Loads this lane's channel half of a 128-channel bf16 row (or zeros).
+__device__ __forceinline__ void load_half_row(const bf16* row, int h, bool valid, bf16x8 raw[8]) {
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    if (valid) {
+      raw[s] = load8(row + 64 * h + 8 * s);
+    } else {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) raw[s][t] = f2bf(0.f);
+    }
+  }
+}
+
+// LayerNorm over the 128 channels held by lanes l and l^32 (biased variance,
+// two-pass, fp32), gamma/beta fp32 (beta may be null); bf16 result in the
+// MFMA operand layout.
+__device__ __forceinline__ void layernorm_half_row(const bf16x8 raw[8], const float* __restrict__ gamma,
+                                                   const float* __restrict__ beta, int h, float eps,
+                                                   bf16x8 out[8]) {
+  float v[64];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) unpack8(raw[s], v + 8 * s);
+  float sum = 0.f;
+#pragma unroll
+  for (int t = 0; t < 64; ++t) sum += v[t];
+  sum += __shfl_xor(sum, 32);
+  const float mean = sum * (1.0f / kPairC);
+  float ss = 0.f;
+#pragma unroll
+  for (int t = 0; t < 64; ++t) {
+    const float d = v[t] - mean;
+    ss += d * d;
+  }
+  ss += __shfl_xor(ss, 32);
+  const float rstd = rsqrtf(ss * (1.0f / kPairC) + eps);
+  const float4* g4 = reinterpret_cast<const float4*>(gamma + 64 * h);
+  const float4* b4 = beta ? reinterpret_cast<const float4*>(beta + 64 * h) : nullptr;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const float4 g = g4[q];
+    float4 b = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (b4) b = b4[q];
+    const int t = 4 * q;
+    out[t >> 3][(t & 7) + 0] = f2bf((v[t + 0] - mean) * rstd * g.x + b.x);
+    out[t >> 3][(t & 7) + 1] = f2bf((v[t + 1] - mean) * rstd * g.y + b.y);
+    out[t >> 3][(t & 7) + 2] = f2bf((v[t + 2] - mean) * rstd * g.z + b.z);
+    out[t >> 3][(t & 7) + 3] = f2bf((v[t + 3] - mean) * rstd * g.w + b.w);
+  }
+}
+
+// Channel-major projection block: 32 pair slots x 32 output channels.
+//   acc = X(32 x 128) * W[row0 .. row0+31, :]^T       (W in LDS, stride kLdw)
+// D lane (n, h): output channel row0 + n, register u <-> pair slot 16h + u.
+__device__ __forceinline__ f32x16 proj_block_cm(const bf16x8 x[8], const bf16* wl, int row0, int n,
+                                                int h) {
+  f32x16 acc = zero16();
+  const bf16* w = wl + (row0 + n) * kLdw + 64 * h;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) acc = mfma32(x[s], load8(w + 8 * s), acc);
+  return acc;
+}
+
+// Pair-major projection block: 32 output channels x 32 pair slots.
+//   acc = W[row0 + perm32(.), :] * X^T
+// D lane (n, h): pair slot perm32(n), register u <-> output channel row0 + 16h + u.
+__device__ __forceinline__ f32x16 proj_block_pm(const bf16x8 x[8], const bf16* wl, int row0, int n,
+                                                int h) {
+  f32x16 acc = zero16();
+  const bf16* w = wl + (row0 + perm32(n)) * kLdw + 64 * h;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) acc = mfma32(load8(w + 8 * s), x[s], acc);
+  return acc;
+}
+
+// 16 fp32 accumulator values -> two 16-byte bf16 chunks.
+__device__ __forceinline__ void store16(bf16* dst, const float* v) {
+  bf16x8 a, b;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    a[t] = f2bf(v[t]);
+    b[t] = f2bf(v[8 + t]);
+  }
+  store8(dst, a);
+  store8(dst + 8, b);
+}
+
+// Copies `rows` x 128 bf16 weight rows from global memory into LDS (stride
+// kLdw) and zero-fills rows [rows, rows_padded).  Whole workgroup; no barrier.
+__device__ __forceinline__ void stage_weights(bf16* wl, const bf16* __restrict__ w, int rows,
+                                              int rows_padded) {
+  const int chunks = rows_padded * (kPairC / 8);
+  for (int q = threadIdx.x; q < chunks; q += blockDim.x) {
+    const int r = q >> 4, part = q & 15;
+    bf16x8 v;
+    if (r < rows) {
+      v = load8(w + (size_t)r * kPairC + part * 8);
+    } else {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) v[t] = f2bf(0.f);
+    }
+    store8(wl + r * kLdw + part * 8, v);
+  }
+}
+
+}  // namespace bioemu

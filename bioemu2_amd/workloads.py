@@ -73,6 +73,17 @@ def trimul_kernel_work(name: str, B: int, N: int, c: int = 128) -> tuple[str, fl
     return None
 
 
+def triatt_kernel_work(name: str, B: int, N: int, c: int = 128, H: int = 4) -> tuple[str, float] | None:
+    P = B * N * N
+    if name == "triatt_proj":
+        # LN + q,k,v,g (c -> 4c) + bias (c -> H); reads z, writes q,k,v,g (+ bias)
+        return ("hbm", float(P * (c * 2 + 4 * c * 2 + H * 2)))
+    if name == "triatt_flash":
+        # QK^T and PV over all keys for every (row, query, head) + output projection
+        return ("mfma", 2.0 * B * N * N * N * c * 2 + 2.0 * P * c * c)
+    return None
+
+
 class Workload:
     name: str
     metric: str
@@ -130,7 +141,52 @@ class TriMulWorkload(Workload):
         return w
 
 
+class TriAttWorkload(Workload):
+    """Config 4: one triangle attention (starting or ending node) at N=768, bf16."""
+
+    def __init__(self, device, starting: bool, n: int = 768, seed: int = 0):
+        from .triangle_attention import TriangleAttentionHip
+
+        self.starting = starting
+        self.n = n
+        self.n_pad = n // 10
+        node = "start" if starting else "end"
+        self.name = f"triatt_{node}_n{n}"
+        self.metric = f"ms per triangle attention ({node}ing node) at N={n} bf16"
+        self.config = {"workload": self.name, "N": n, "c_z": 128, "heads": 4, "head_dim": 32,
+                       "batch": 1, "padded_tokens": self.n_pad}
+        torch.manual_seed(seed)
+        self.module = init_module(TriangleAttentionHip(128, 4, starting=starting), seed).to(device).eval()
+        g = torch.Generator().manual_seed(seed)
+        self.x_cpu = torch.randn(1, n, n, 128, generator=g).to(torch.bfloat16)
+        self.x = self.x_cpu.to(device)
+        self.tok = token_mask(n, self.n_pad, device)
+        self.pair_mask = _ops.mask_u8(self.tok[:, :, None] & self.tok[:, None, :])
+        self.out = torch.empty_like(self.x)
+        self.ws = _ops.workspace(_ops.triatt_workspace_bytes(1, n), device)
+        self.params = self.module.prepared_params()
+        self.flops = 2.0 * n * n * 128 * (4 * 128 + 4 + 128) + 2.0 * 2 * n ** 3 * 128
+
+    def step(self) -> None:
+        _ops.launch_triatt(self.x, self.pair_mask, *self.params, self.out, self.starting, ws=self.ws)
+
+    def cpu_sample(self, oracle):
+        x = self.x_cpu.float()
+        pm = (self.tok[:, :, None] & self.tok[:, None, :]).cpu()
+        params = {k: v.detach().cpu() for k, v in self.module.state_dict().items()}
+        fn = lambda: oracle.triangle_attention(x, pm, params, 4, self.starting, row_chunk=64)  # noqa: E731
+        return fn, 1.0, f"oracle.triangle_attention fp32, full N={self.n} (64-row chunks)"
+
+    def kernel_work(self, kernel: str) -> tuple[str, float]:
+        w = triatt_kernel_work(kernel, 1, self.n)
+        if w is None:
+            raise KeyError(kernel)
+        return w
+
+
 def make(op: str, device, n: int | None = None) -> Workload:
+    if op in ("triatt_start", "triatt_end"):
+        return TriAttWorkload(device, op == "triatt_start", n or 768)
     if op in ("trimul_out", "trimul_in"):
         return TriMulWorkload(device, "outgoing" if op == "trimul_out" else "incoming", n or 768)
     raise ValueError(f"unknown bench op {op!r}")

@@ -71,6 +71,28 @@ int bioemu_trimul_fwd(const void* x, const uint8_t* mask, const float* norm_in_w
                       int64_t B, int64_t N, int64_t D, int outgoing, int residual,
                       hipStream_t stream);
 
+/*
+ * Triangle attention around the starting node (starting=1) or ending node (0).
+ *
+ * No counterpart in the reference (biomoa/modules/pairmixer.py:459-462 removed
+ * it); AlphaFold3 suppl. Alg. 14/15 with the reference's attention masking
+ * convention (masked keys replaced by -1e6, attention_pair_bias.py:184-190).
+ * It would bind through the make() 3-tuple registry form
+ * (src/bioemu2/biomoa/utils/strategy.py:33-36).  Per batch, frame row i, head h
+ * (frame = z for starting, z^T for ending):
+ *   zn = LN(z); q,k,v,g,bias = zn W^T (g through a sigmoid; bias has H columns)
+ *   o[i,j] = sum_k softmax_k(q[i,j].k[i,k]/sqrt(d) + bias[j,k,h]; mask[i,k]) v[i,k]
+ *   update[i,j] = (g[i,j] * o[i,j]) Wo^T    (+ z when residual != 0)
+ * z, out: [B,N,N,D] bf16 (out may equal z when residual != 0); mask [B,N,N].
+ * w_proj: [4*D + H, D] = rows of Wq, Wk, Wv, Wg, Wbias; w_o: [D, D].
+ * D must be 128 and H 4 (head dim 32).
+ */
+size_t bioemu_triatt_workspace_bytes(int64_t B, int64_t N, int64_t D, int64_t H);
+int bioemu_triatt_fwd(const void* z, const uint8_t* mask, const float* norm_w, const float* norm_b,
+                      const void* w_proj, const void* w_o, void* out, void* workspace,
+                      size_t workspace_bytes, int64_t B, int64_t N, int64_t D, int64_t H,
+                      int starting, int residual, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
