@@ -44,8 +44,9 @@ def _parse() -> argparse.Namespace:
 def cpu_baseline(wl) -> dict:
     """The fp32 CPU oracle on a bounded sample of the same workload (rank 0, N=1 only).
 
-    1 warm-up then the median of up to 3 timed calls, stopping early once
-    ~30 s of CPU time is spent; ``value`` is scaled to ms per full step.
+    By default 1 warm-up then the median of up to 3 timed calls, stopping
+    early once ~30 s of CPU time is spent (the full block is one cold call);
+    ``value`` is scaled to ms per full step.
     """
     import torch
 
@@ -54,10 +55,13 @@ def cpu_baseline(wl) -> dict:
     threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
     fn, fraction, sample = wl.cpu_sample(oracle)
-    fn()  # warm-up
+    warm = getattr(wl, "cpu_warmup", 1)
+    calls = getattr(wl, "cpu_calls", 3)
+    for _ in range(warm):
+        fn()
     times = []
     budget = time.perf_counter() + 30.0
-    while len(times) < 3:
+    while len(times) < calls:
         t0 = time.perf_counter()
         fn()
         times.append(time.perf_counter() - t0)
@@ -70,7 +74,7 @@ def cpu_baseline(wl) -> dict:
         "unit": "ms",
         "cores": threads,
         "kind": "port",
-        "sample": f"{sample}; {len(times)} timed call(s) after 1 warm-up, median",
+        "sample": f"{sample}; {len(times)} timed call(s) after {warm} warm-up(s), median",
     }
 
 

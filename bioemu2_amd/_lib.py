@@ -38,6 +38,20 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _c_int,
         [_c_void_p] * 7 + [_c_void_p, _c_size_t] + [_c_int64] * 4 + [_c_int, _c_int, _c_void_p],
     ),
+    "bioemu_transition_pair_fwd": (
+        _c_int,
+        [_c_void_p] * 7 + [_c_int64] * 3 + [_c_int, _c_int, _c_void_p],
+    ),
+    "bioemu_transition_token_workspace_bytes": (_c_size_t, [_c_int64] * 3),
+    "bioemu_transition_token_fwd": (
+        _c_int,
+        [_c_void_p] * 7 + [_c_void_p, _c_size_t] + [_c_int64] * 3 + [_c_int, _c_int, _c_void_p],
+    ),
+    "bioemu_apb_workspace_bytes": (_c_size_t, [_c_int64] * 5),
+    "bioemu_apb_fwd": (
+        _c_int,
+        [_c_void_p] * 13 + [_c_void_p, _c_size_t] + [_c_int64] * 6 + [_c_int, _c_void_p],
+    ),
 }
 
 _lock = threading.Lock()

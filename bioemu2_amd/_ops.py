@@ -216,3 +216,204 @@ def triangle_attention(
 @triangle_attention.register_fake
 def _(z, mask, norm_w, norm_b, w_proj, w_o, starting, num_heads):
     return torch.empty_like(z)
+
+
+# ----------------------------------------------------------------------------
+# Transition (SwiGLU MLP)
+# ----------------------------------------------------------------------------
+def launch_transition_pair(
+    x: Tensor,
+    norm_w: Tensor | None,
+    norm_b: Tensor | None,
+    fc1_w: Tensor,
+    fc2_w: Tensor,
+    fc3_w: Tensor,
+    out: Tensor,
+    residual: bool = False,
+) -> Tensor:
+    require_gpu(x, "transition")
+    D = x.shape[-1]
+    P = x.numel() // D
+    dev = x.device
+    hidden = fc1_w.shape[0]
+    _check_tensor(x, "transition x", BF16, tuple(x.shape), dev)
+    _check_tensor(out, "transition out", BF16, tuple(x.shape), dev)
+    _check_tensor(fc1_w, "transition fc1.weight", BF16, (hidden, D), dev)
+    _check_tensor(fc2_w, "transition fc2.weight", BF16, (hidden, D), dev)
+    _check_tensor(fc3_w, "transition fc3.weight", BF16, (D, hidden), dev)
+    use_norm = norm_w is not None
+    if use_norm:
+        _check_tensor(norm_w, "transition norm.weight", torch.float32, (D,), dev)
+        _check_tensor(norm_b, "transition norm.bias", torch.float32, (D,), dev)
+    rc = lib().bioemu_transition_pair_fwd(
+        _ptr(x), _ptr(norm_w), _ptr(norm_b), _ptr(fc1_w), _ptr(fc2_w), _ptr(fc3_w), _ptr(out),
+        P, D, hidden, int(use_norm), int(bool(residual)), _stream(x),
+    )
+    check(rc, "bioemu_transition_pair_fwd")
+    return out
+
+
+def transition_token_workspace_bytes(M: int, D: int, hidden: int) -> int:
+    return int(lib().bioemu_transition_token_workspace_bytes(M, D, hidden))
+
+
+def launch_transition_token(
+    x: Tensor,
+    norm_w: Tensor | None,
+    norm_b: Tensor | None,
+    fc1_w: Tensor,
+    fc2_w: Tensor,
+    fc3_w: Tensor,
+    out: Tensor,
+    residual: bool = False,
+    ws: Tensor | None = None,
+) -> Tensor:
+    require_gpu(x, "transition")
+    D = x.shape[-1]
+    M = x.numel() // D
+    dev = x.device
+    hidden = fc1_w.shape[0]
+    _check_tensor(x, "transition x", BF16, tuple(x.shape), dev)
+    _check_tensor(out, "transition out", BF16, tuple(x.shape), dev)
+    _check_tensor(fc1_w, "transition fc1.weight", BF16, (hidden, D), dev)
+    _check_tensor(fc2_w, "transition fc2.weight", BF16, (hidden, D), dev)
+    _check_tensor(fc3_w, "transition fc3.weight", BF16, (D, hidden), dev)
+    use_norm = norm_w is not None
+    if use_norm:
+        _check_tensor(norm_w, "transition norm.weight", torch.float32, (D,), dev)
+        _check_tensor(norm_b, "transition norm.bias", torch.float32, (D,), dev)
+    need = transition_token_workspace_bytes(M, D, hidden)
+    if ws is None or ws.numel() < need:
+        ws = workspace(need, dev)
+    rc = lib().bioemu_transition_token_fwd(
+        _ptr(x), _ptr(norm_w), _ptr(norm_b), _ptr(fc1_w), _ptr(fc2_w), _ptr(fc3_w), _ptr(out),
+        _ptr(ws), ctypes.c_size_t(ws.numel()), M, D, hidden, int(use_norm), int(bool(residual)), _stream(x),
+    )
+    check(rc, "bioemu_transition_token_fwd")
+    return out
+
+
+def _is_pair_transition(x: Tensor, hidden: int) -> bool:
+    return x.ndim == 4 and x.shape[-1] == 128 and hidden == 512
+
+
+@torch.library.custom_op("bioemu_mi355x::transition", mutates_args=(), device_types="cuda")
+def transition(
+    x: Tensor, norm_w: Tensor | None, norm_b: Tensor | None, fc1_w: Tensor, fc2_w: Tensor, fc3_w: Tensor
+) -> Tensor:
+    xb = x.to(BF16).contiguous()
+    out = torch.empty_like(xb)
+    f32 = torch.float32
+    nw = None if norm_w is None else norm_w.to(f32).contiguous()
+    nb = None if norm_b is None else norm_b.to(f32).contiguous()
+    w1, w2, w3 = (w.to(BF16).contiguous() for w in (fc1_w, fc2_w, fc3_w))
+    if _is_pair_transition(xb, w1.shape[0]):
+        launch_transition_pair(xb, nw, nb, w1, w2, w3, out)
+    else:
+        launch_transition_token(xb, nw, nb, w1, w2, w3, out)
+    return out.to(x.dtype)
+
+
+@transition.register_fake
+def _(x, norm_w, norm_b, fc1_w, fc2_w, fc3_w):
+    return torch.empty_like(x)
+
+
+# ----------------------------------------------------------------------------
+# Attention with pair bias
+# ----------------------------------------------------------------------------
+def apb_workspace_bytes(B: int, mult: int, N: int, c_s: int, H: int) -> int:
+    return int(lib().bioemu_apb_workspace_bytes(B, mult, N, c_s, H))
+
+
+def launch_apb(
+    s: Tensor,
+    z: Tensor,
+    mask: Tensor,
+    norm_s_w: Tensor | None,
+    norm_s_b: Tensor | None,
+    w_qkv: Tensor,
+    q_bias: Tensor,
+    w_g: Tensor,
+    norm_z_w: Tensor,
+    norm_z_b: Tensor | None,
+    w_z: Tensor,
+    w_o: Tensor,
+    out: Tensor,
+    num_heads: int,
+    multiplicity: int = 1,
+    residual: bool = False,
+    ws: Tensor | None = None,
+) -> Tensor:
+    require_gpu(s, "attention_pair_bias")
+    if s.ndim != 3 or z.ndim != 4 or mask.ndim != 2:
+        raise AssertionError(f"{tuple(s.shape)}, {tuple(z.shape)}, {tuple(mask.shape)}")
+    if s.shape[0] != z.shape[0] * multiplicity:
+        raise AssertionError(f"{tuple(s.shape)}, {tuple(z.shape)}, multiplicity={multiplicity}")
+    BM, N, c_s = s.shape
+    B, _, _, c_z = z.shape
+    dev = s.device
+    _check_tensor(s, "apb s", BF16, (BM, N, c_s), dev)
+    _check_tensor(out, "apb out", BF16, (BM, N, c_s), dev)
+    _check_tensor(z, "apb z", BF16, (B, N, N, c_z), dev)
+    _check_tensor(mask, "apb mask", torch.uint8, (B, N), dev)
+    if norm_s_w is not None:
+        _check_tensor(norm_s_w, "apb norm_s.weight", torch.float32, (c_s,), dev)
+        _check_tensor(norm_s_b, "apb norm_s.bias", torch.float32, (c_s,), dev)
+    _check_tensor(w_qkv, "apb proj_qkv.weight", BF16, (3 * c_s, c_s), dev)
+    _check_tensor(q_bias, "apb proj_q_bias", torch.float32, (c_s,), dev)
+    _check_tensor(w_g, "apb proj_g.weight", BF16, (c_s, c_s), dev)
+    _check_tensor(norm_z_w, "apb norm_z.weight", torch.float32, (c_z,), dev)
+    if norm_z_b is not None:
+        _check_tensor(norm_z_b, "apb norm_z.bias", torch.float32, (c_z,), dev)
+    _check_tensor(w_z, "apb proj_z.weight", BF16, (num_heads, c_z), dev)
+    _check_tensor(w_o, "apb proj_o.weight", BF16, (c_s, c_s), dev)
+    need = apb_workspace_bytes(B, multiplicity, N, c_s, num_heads)
+    if ws is None or ws.numel() < need:
+        ws = workspace(need, dev)
+    rc = lib().bioemu_apb_fwd(
+        _ptr(s), _ptr(z), _ptr(mask), _ptr(norm_s_w), _ptr(norm_s_b), _ptr(w_qkv), _ptr(q_bias), _ptr(w_g),
+        _ptr(norm_z_w), _ptr(norm_z_b), _ptr(w_z), _ptr(w_o), _ptr(out), _ptr(ws), ctypes.c_size_t(ws.numel()),
+        B, multiplicity, N, c_s, c_z, num_heads, int(bool(residual)), _stream(s),
+    )
+    check(rc, "bioemu_apb_fwd")
+    return out
+
+
+@torch.library.custom_op("bioemu_mi355x::attention_pair_bias", mutates_args=(), device_types="cuda")
+def attention_pair_bias(
+    s: Tensor,
+    z: Tensor,
+    mask: Tensor,
+    norm_s_w: Tensor | None,
+    norm_s_b: Tensor | None,
+    w_qkv: Tensor,
+    q_bias: Tensor,
+    w_g: Tensor,
+    norm_z_w: Tensor,
+    norm_z_b: Tensor | None,
+    w_z: Tensor,
+    w_o: Tensor,
+    num_heads: int,
+    multiplicity: int,
+) -> Tensor:
+    sb = s.to(BF16).contiguous()
+    out = torch.empty_like(sb)
+    f32 = torch.float32
+
+    def f(t):
+        return None if t is None else t.to(f32).contiguous()
+
+    def h(t):
+        return t.to(BF16).contiguous()
+
+    launch_apb(
+        sb, h(z), mask_u8(mask), f(norm_s_w), f(norm_s_b), h(w_qkv), f(q_bias), h(w_g), f(norm_z_w), f(norm_z_b),
+        h(w_z), h(w_o), out, num_heads, multiplicity,
+    )
+    return out.to(s.dtype)
+
+
+@attention_pair_bias.register_fake
+def _(s, z, mask, norm_s_w, norm_s_b, w_qkv, q_bias, w_g, norm_z_w, norm_z_b, w_z, w_o, num_heads, multiplicity):
+    return torch.empty_like(s)

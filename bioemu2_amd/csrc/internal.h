@@ -40,4 +40,13 @@ constexpr int kGemmTile = 128;
 int launch_bgemm_nt(const void* A, const void* B, void* C, int64_t batch, int64_t n,
                     hipStream_t stream);
 
+// Token-side helpers (token.hip).  Rows are B batches of N tokens stored
+// padded to Np rows each; see token.hip for the row conventions.
+int token_layernorm(const void* x, const float* gamma, const float* beta, void* y, int64_t B, int64_t N,
+                    int64_t Np, int64_t K, hipStream_t stream);
+int token_gemm(int epi, bool trans, const void* A, const void* W, const void* W2, const float* col_bias,
+               const void* res, void* out, int64_t M, int64_t K, int64_t Nout, int64_t N, int64_t Np,
+               int64_t out_rows, hipStream_t stream, const char* name);
+constexpr int kEpiStoreId = 0, kEpiSigmoidId = 1, kEpiSwiGLUId = 2, kEpiResidualId = 3;
+
 }  // namespace bioemu

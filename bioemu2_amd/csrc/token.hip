@@ -1,0 +1,256 @@
+// Token-side (single representation) kernels for gfx950: row LayerNorm and a
+// small MFMA GEMM with fused epilogues.  These carry the per-token parts of
+// AttentionPairBias (src/bioemu2/biomoa/ops/attention_pair_bias.py:150-161,
+// :224-225) and the single-representation Transition
+// (src/bioemu2/biomoa/ops/transition.py:52-91).  The token dimension is small
+// (B * N rows of c_s = 384), so one wave computes one 32x32 output block with
+// operands read straight from L2.
+//
+// Row spaces.  A GEMM runs over M = B * Np "padded" rows (Np = N rounded up to
+// 32, rows t >= N of each batch are zero).  Row-major outputs/residuals use
+// either the same padded layout or, with out_rows = N, the caller's compact
+// [B][N] layout (padded rows are then dropped).  Transposed outputs are laid
+// out [B][Nout][Np].
+#include "common.h"
+#include "internal.h"
+#include "pairtile.h"
+
+namespace bioemu {
+namespace {
+
+enum Epilogue : int {
+  kEpiStore = 0,     // out = acc (+ col_bias)
+  kEpiSigmoid = 1,   // out = sigmoid(acc)
+  kEpiSwiGLU = 2,    // out = silu(A W^T) * (A W2^T)
+  kEpiResidual = 3,  // out = res + acc
+};
+
+// ---------------------------------------------------------------------------
+// y[b][t] = LN(x[b][t]) for t < N, 0 for N <= t < Np.  One wave per row,
+// K <= 512 and K % 64 == 0 (each lane holds K/64 values).  gamma == null
+// copies the rows unnormalised (same padding).
+// ---------------------------------------------------------------------------
+template <int K>
+__global__ __launch_bounds__(256) void token_ln_kernel(const bf16* __restrict__ x, const float* __restrict__ gamma,
+                                                       const float* __restrict__ beta, bf16* __restrict__ y, int B,
+                                                       int N, int Np, float eps) {
+  const int lane = threadIdx.x & 63;
+  const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= (long long)B * Np) return;
+  const int b = (int)(row / Np), t = (int)(row % Np);
+  constexpr int PER = K / 64;
+  bf16* yr = y + (size_t)row * K;
+  if (t >= N) {
+#pragma unroll
+    for (int e = 0; e < PER; ++e) yr[lane + 64 * e] = f2bf(0.f);
+    return;
+  }
+  const bf16* xr = x + ((size_t)b * N + t) * K;
+  float v[PER];
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < PER; ++e) {
+    v[e] = bf2f(xr[lane + 64 * e]);
+    s += v[e];
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
+  const float mean = s * (1.0f / K);
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < PER; ++e) {
+    const float d = v[e] - mean;
+    ss += d * d;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+  const float rstd = rsqrtf(ss * (1.0f / K) + eps);
+#pragma unroll
+  for (int e = 0; e < PER; ++e) {
+    const int c = lane + 64 * e;
+    float o = v[e];
+    if (gamma) {
+      o = (v[e] - mean) * rstd * gamma[c];
+      if (beta) o += beta[c];
+    }
+    yr[c] = f2bf(o);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// out = epilogue(A[M][K] * W[Nout][K]^T).  One wave per 32x32 block.
+// Row-major (kTrans = false): D = W A^T, lane (n, hh) holds row n and columns
+// 16hh..16hh+15 of the block.  Transposed (kTrans = true): D = A W^T with A
+// rows permuted, lane (n, hh) holds column n and rows 16hh..16hh+15.
+// ---------------------------------------------------------------------------
+template <int kEpi, bool kTrans>
+__global__ __launch_bounds__(256) void token_gemm_kernel(const bf16* __restrict__ A, const bf16* __restrict__ W,
+                                                         const bf16* __restrict__ W2,
+                                                         const float* __restrict__ col_bias, const bf16* res,
+                                                         bf16* out, int M, int K, int Nout, int N, int Np,
+                                                         int out_rows) {
+  const int lane = threadIdx.x & 63;
+  const int wid = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int nb = Nout / 32;
+  const int mb = (M + 31) / 32;
+  if (wid >= mb * nb) return;
+  const int row0 = (wid / nb) * 32, col0 = (wid % nb) * 32;
+  const int n = lane & 31, hh = lane >> 5;
+
+  f32x16 acc = zero16(), acc2 = zero16();
+  if (!kTrans) {
+    const bf16* wr = W + (size_t)(col0 + perm32(n)) * K + 8 * hh;
+    const bf16* wr2 = (kEpi == kEpiSwiGLU) ? W2 + (size_t)(col0 + perm32(n)) * K + 8 * hh : nullptr;
+    const int ra = min(row0 + n, M - 1);
+    const bf16* ar = A + (size_t)ra * K + 8 * hh;
+    for (int k = 0; k < K; k += 16) {
+      const bf16x8 af = load8(ar + k);
+      acc = mfma32(load8(wr + k), af, acc);
+      if (kEpi == kEpiSwiGLU) acc2 = mfma32(load8(wr2 + k), af, acc2);
+    }
+  } else {
+    const int ra = min(row0 + perm32(n), M - 1);
+    const bf16* ar = A + (size_t)ra * K + 8 * hh;
+    const bf16* wr = W + (size_t)(col0 + n) * K + 8 * hh;
+    for (int k = 0; k < K; k += 16) acc = mfma32(load8(ar + k), load8(wr + k), acc);
+  }
+
+  float v[16];
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {
+    float a = acc[u];
+    if (kEpi == kEpiSigmoid) a = sigmoidf_fast(a);
+    if (kEpi == kEpiSwiGLU) a = siluf_fast(a) * acc2[u];
+    v[u] = a;
+  }
+
+  if (!kTrans) {
+    const int r = row0 + n;
+    if (r >= M) return;
+    const int b = r / Np, t = r % Np;
+    if (out_rows != Np && t >= out_rows) return;
+    const size_t orow = (out_rows == Np) ? (size_t)r : (size_t)b * out_rows + t;
+    const int c0 = col0 + 16 * hh;
+    if (kEpi == kEpiStore && col_bias) {
+#pragma unroll
+      for (int u = 0; u < 16; ++u) v[u] += col_bias[c0 + u];
+    }
+    if (kEpi == kEpiResidual) {
+      const bf16x8 r0 = load8(res + orow * Nout + c0), r1 = load8(res + orow * Nout + c0 + 8);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        v[u] += bf2f(r0[u]);
+        v[8 + u] += bf2f(r1[u]);
+      }
+    }
+    store16(out + orow * Nout + c0, v);
+  } else {
+    // rows row0 + 16hh .. +15 of column col0 + n; a 16-row run never crosses a batch (Np % 32 == 0)
+    const int r = row0 + 16 * hh;
+    if (r >= M) return;
+    const int b = r / Np, t = r % Np;
+    store16(out + ((size_t)b * Nout + col0 + n) * Np + t, v);
+  }
+}
+
+template <int kEpi, bool kTrans>
+int launch_gemm(const void* A, const void* W, const void* W2, const float* col_bias, const void* res, void* out,
+                int64_t M, int64_t K, int64_t Nout, int64_t N, int64_t Np, int64_t out_rows, hipStream_t stream,
+                const char* name) {
+  const int64_t waves = ((M + 31) / 32) * (Nout / 32);
+  KernelTimerScope timed(name, stream);
+  hipLaunchKernelGGL((token_gemm_kernel<kEpi, kTrans>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream,
+                     static_cast<const bf16*>(A), static_cast<const bf16*>(W), static_cast<const bf16*>(W2),
+                     col_bias, static_cast<const bf16*>(res), static_cast<bf16*>(out), (int)M, (int)K, (int)Nout,
+                     (int)N, (int)Np, (int)out_rows);
+  return check_launch(name);
+}
+
+}  // namespace
+
+int token_layernorm(const void* x, const float* gamma, const float* beta, void* y, int64_t B, int64_t N,
+                    int64_t Np, int64_t K, hipStream_t stream) {
+  const int64_t rows = B * Np;
+  dim3 grid((unsigned)((rows + 3) / 4));
+  KernelTimerScope timed("token_layernorm", stream);
+  switch (K) {
+    case 128:
+      hipLaunchKernelGGL(token_ln_kernel<128>, grid, dim3(256), 0, stream, static_cast<const bf16*>(x), gamma, beta,
+                         static_cast<bf16*>(y), (int)B, (int)N, (int)Np, 1e-5f);
+      break;
+    case 384:
+      hipLaunchKernelGGL(token_ln_kernel<384>, grid, dim3(256), 0, stream, static_cast<const bf16*>(x), gamma, beta,
+                         static_cast<bf16*>(y), (int)B, (int)N, (int)Np, 1e-5f);
+      break;
+    default:
+      return set_error(BIOEMU_ERR_UNSUPPORTED, "token_layernorm: width %lld unsupported (128 or 384)", (long long)K);
+  }
+  return check_launch("token_layernorm");
+}
+
+int token_gemm(int epi, bool trans, const void* A, const void* W, const void* W2, const float* col_bias,
+               const void* res, void* out, int64_t M, int64_t K, int64_t Nout, int64_t N, int64_t Np,
+               int64_t out_rows, hipStream_t stream, const char* name) {
+  if (M <= 0 || K <= 0 || K % 16 || Nout <= 0 || Nout % 32 || Np % 32 || M % Np)
+    return set_error(BIOEMU_ERR_INVALID_ARG, "%s: bad GEMM shape M=%lld K=%lld Nout=%lld Np=%lld", name,
+                     (long long)M, (long long)K, (long long)Nout, (long long)Np);
+  if (trans) {
+    if (epi != kEpiStore) return set_error(BIOEMU_ERR_INVALID_ARG, "%s: transposed GEMM stores plainly", name);
+    return launch_gemm<kEpiStore, true>(A, W, W2, col_bias, res, out, M, K, Nout, N, Np, out_rows, stream, name);
+  }
+  switch (epi) {
+    case kEpiStore:
+      return launch_gemm<kEpiStore, false>(A, W, W2, col_bias, res, out, M, K, Nout, N, Np, out_rows, stream, name);
+    case kEpiSigmoid:
+      return launch_gemm<kEpiSigmoid, false>(A, W, W2, col_bias, res, out, M, K, Nout, N, Np, out_rows, stream, name);
+    case kEpiSwiGLU:
+      return launch_gemm<kEpiSwiGLU, false>(A, W, W2, col_bias, res, out, M, K, Nout, N, Np, out_rows, stream, name);
+    case kEpiResidual:
+      return launch_gemm<kEpiResidual, false>(A, W, W2, col_bias, res, out, M, K, Nout, N, Np, out_rows, stream, name);
+    default:
+      return set_error(BIOEMU_ERR_INVALID_ARG, "%s: unknown epilogue %d", name, epi);
+  }
+}
+
+}  // namespace bioemu
+
+using namespace bioemu;
+
+// ---------------------------------------------------------------------------
+// Single-representation Transition: s (+)= fc3(silu(fc1(LN s)) * fc2(LN s)).
+// ---------------------------------------------------------------------------
+extern "C" size_t bioemu_transition_token_workspace_bytes(int64_t M, int64_t Dc, int64_t hidden) {
+  if (M <= 0 || Dc <= 0 || hidden <= 0) return 0;
+  const size_t Mp = (size_t)round_up(M, 32);
+  return round_up(Mp * Dc * 2, 256) + round_up(Mp * hidden * 2, 256);
+}
+
+extern "C" int bioemu_transition_token_fwd(const void* x, const float* norm_w, const float* norm_b,
+                                           const void* fc1_w, const void* fc2_w, const void* fc3_w, void* out,
+                                           void* workspace, size_t workspace_bytes, int64_t M, int64_t Dc,
+                                           int64_t hidden, int use_norm, int residual, hipStream_t stream) {
+  if (M <= 0 || (Dc != 128 && Dc != 384) || hidden <= 0 || hidden % 32)
+    return set_error(BIOEMU_ERR_UNSUPPORTED, "transition_token: dim %lld / hidden %lld unsupported", (long long)Dc,
+                     (long long)hidden);
+  if (!x || !fc1_w || !fc2_w || !fc3_w || !out || !workspace || (use_norm && !norm_w))
+    return set_error(BIOEMU_ERR_INVALID_ARG, "transition_token: null pointer argument");
+  if (!aligned16(x) || !aligned16(out) || !aligned16(fc1_w) || !aligned16(fc2_w) || !aligned16(fc3_w) ||
+      !aligned16(workspace))
+    return set_error(BIOEMU_ERR_INVALID_ARG, "transition_token: tensors must be 16-byte aligned");
+  if (out == x && !residual)
+    return set_error(BIOEMU_ERR_INVALID_ARG, "transition_token: out may alias x only with residual=1");
+  if (workspace_bytes < bioemu_transition_token_workspace_bytes(M, Dc, hidden))
+    return set_error(BIOEMU_ERR_WORKSPACE, "transition_token: workspace too small");
+  // Rows are treated as one batch of M tokens padded to Mp.
+  const int64_t Mp = round_up(M, 32);
+  char* p = static_cast<char*>(workspace);
+  bf16* xn = reinterpret_cast<bf16*>(p);
+  bf16* hbuf = reinterpret_cast<bf16*>(p + round_up(Mp * Dc * 2, 256));
+  int rc = token_layernorm(x, use_norm ? norm_w : nullptr, use_norm ? norm_b : nullptr, xn, 1, M, Mp, Dc, stream);
+  if (rc) return rc;
+  rc = token_gemm(kEpiSwiGLU, false, xn, fc1_w, fc2_w, nullptr, nullptr, hbuf, Mp, Dc, hidden, M, Mp, Mp, stream,
+                  "transition_token_swiglu");
+  if (rc) return rc;
+  return token_gemm(residual ? kEpiResidual : kEpiStore, false, hbuf, fc3_w, nullptr, nullptr, x, out, Mp, hidden,
+                    Dc, M, Mp, M, stream, "transition_token_out");
+}

@@ -184,7 +184,81 @@ class TriAttWorkload(Workload):
         return w
 
 
+class BlockWorkload(Workload):
+    """The BASELINE metric: one full bf16 Pairformer block at N=768 (config 4 + s [1,768,384])."""
+
+    cpu_warmup = 0
+    cpu_calls = 1
+
+    def __init__(self, device, n: int = 768, seed: int = 0):
+        from .pairformer import PairformerBlockHip
+
+        self.n = n
+        self.n_pad = n // 10
+        self.name = f"pairformer_block_n{n}"
+        self.metric = f"ms per Pairformer block at N={n} bf16"
+        self.config = {"workload": self.name, "N": n, "c_z": 128, "c_s": 384, "batch": 1,
+                       "triatt_heads": 4, "apb_heads": 16, "padded_tokens": self.n_pad}
+        torch.manual_seed(seed)
+        self.module = init_module(PairformerBlockHip(), seed).to(device).eval()
+        g = torch.Generator().manual_seed(seed)
+        self.z_cpu = torch.randn(1, n, n, 128, generator=g).to(torch.bfloat16)
+        self.s_cpu = torch.randn(1, n, 384, generator=g).to(torch.bfloat16)
+        self.z = self.z_cpu.to(device)
+        self.s = self.s_cpu.to(device)
+        self.tok = token_mask(n, self.n_pad, device)
+        self.module.forward_(self.s.clone(), self.z.clone(), self.tok)  # sizes the shared workspace
+        c, cs = 128, 384
+        P = n * n
+        trimul = 2.0 * P * c * 6 * c + 2.0 * c * n ** 3
+        triatt = 2.0 * P * c * (5 * c + 4) + 4.0 * n ** 3 * c
+        trans_z = 2.0 * P * c * 12 * c
+        apb = 2.0 * P * c * 16 + 2.0 * n * cs * 5 * cs + 4.0 * n * n * cs
+        trans_s = 2.0 * n * cs * 12 * cs
+        self.flops = 2 * trimul + 2 * triatt + trans_z + apb + trans_s
+
+    def step(self) -> None:
+        self.module.forward_(self.s, self.z, self.tok)
+
+    def cpu_sample(self, oracle):
+        s = self.s_cpu.float()
+        z = self.z_cpu.float()
+        tok = self.tok.cpu()
+        params = {k: v.detach().cpu() for k, v in self.module.state_dict().items()}
+        fn = lambda: oracle.pairformer_block(s, z, tok, params, triatt_row_chunk=64)  # noqa: E731
+        return fn, 1.0, f"oracle.pairformer_block fp32, full N={self.n}"
+
+    def kernel_work(self, kernel: str) -> tuple[str, float]:
+        n, c, cs = self.n, 128, 384
+        for fn in (trimul_kernel_work, triatt_kernel_work):
+            w = fn(kernel, 1, n)
+            if w is not None:
+                return w
+        if kernel == "transition_pair":
+            return ("mfma", 2.0 * n * n * c * 12 * c)
+        if kernel == "apb_pair_bias":
+            return ("hbm", float(n * n * (c * 2 + 16 * 2)))
+        if kernel == "apb_flash":
+            return ("mfma", 4.0 * n * n * cs)
+        # token-side kernels: tiny; report against HBM with their operand bytes
+        token_bytes = {
+            "token_layernorm": 2 * n * cs * 2,
+            "apb_proj_q": n * cs * 2 * 2 + cs * cs * 2,
+            "apb_proj_k": n * cs * 2 * 2 + cs * cs * 2,
+            "apb_proj_v": n * cs * 2 * 2 + cs * cs * 2,
+            "apb_proj_g": n * cs * 2 * 2 + cs * cs * 2,
+            "apb_proj_o": n * cs * 2 * 3 + cs * cs * 2,
+            "transition_token_swiglu": n * cs * 2 + n * 4 * cs * 2 + 2 * 4 * cs * cs * 2,
+            "transition_token_out": n * 4 * cs * 2 + 2 * n * cs * 2 + 4 * cs * cs * 2,
+        }
+        if kernel in token_bytes:
+            return ("hbm", float(token_bytes[kernel]))
+        raise KeyError(kernel)
+
+
 def make(op: str, device, n: int | None = None) -> Workload:
+    if op == "block":
+        return BlockWorkload(device, n or 768)
     if op in ("triatt_start", "triatt_end"):
         return TriAttWorkload(device, op == "triatt_start", n or 768)
     if op in ("trimul_out", "trimul_in"):

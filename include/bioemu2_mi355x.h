@@ -93,6 +93,48 @@ int bioemu_triatt_fwd(const void* z, const uint8_t* mask, const float* norm_w, c
                       size_t workspace_bytes, int64_t B, int64_t N, int64_t D, int64_t H,
                       int starting, int residual, hipStream_t stream);
 
+/*
+ * Pair Transition (SwiGLU MLP), fused: LN -> fc1/fc2 -> silu(a)*b -> fc3 (+ x).
+ * Replaces Transition.forward (src/bioemu2/biomoa/ops/transition.py:52-91) for
+ * the pair representation.  x, out: [P, D] bf16 rows (P = B*N*N), out may equal
+ * x when residual != 0.  fc1_w, fc2_w: [hidden, D]; fc3_w: [D, hidden].
+ * D must be 128 and hidden 512.  use_norm=0 skips the LayerNorm (norm_* unused).
+ */
+int bioemu_transition_pair_fwd(const void* x, const float* norm_w, const float* norm_b,
+                               const void* fc1_w, const void* fc2_w, const void* fc3_w, void* out,
+                               int64_t P, int64_t D, int64_t hidden, int use_norm, int residual,
+                               hipStream_t stream);
+
+/*
+ * Token Transition (same op over [M, D] rows of the single representation,
+ * D in {128, 384}, hidden a multiple of 32): LN kernel + two MFMA GEMMs.
+ * Replaces Transition.forward (transition.py:52-91) for s.
+ */
+size_t bioemu_transition_token_workspace_bytes(int64_t M, int64_t D, int64_t hidden);
+int bioemu_transition_token_fwd(const void* x, const float* norm_w, const float* norm_b,
+                                const void* fc1_w, const void* fc2_w, const void* fc3_w, void* out,
+                                void* workspace, size_t workspace_bytes, int64_t M, int64_t D,
+                                int64_t hidden, int use_norm, int residual, hipStream_t stream);
+
+/*
+ * Attention with pair bias over the single representation.
+ * Replaces AttentionPairBias.forward (src/bioemu2/biomoa/ops/attention_pair_bias.py:128-225)
+ * with the non-fused bias branch (_proj_z_fused, :114-117):
+ *   s' = LN_s(s) (norm_s_w/b null: initial_norm=False);  q,k,v = chunk(s' Wqkv^T); q += q_bias
+ *   g = sigmoid(s' Wg^T);  bias = LN_z(z) Wz^T  (norm_z_b may be null)
+ *   o = softmax(q k^T / sqrt(d) + bias; keys with mask 0 replaced by -1e6) v
+ *   out = (g * o) Wo^T   (+ s when residual != 0)
+ * s, out: [B*mult, N, c_s] bf16; z: [B, N, N, c_z] bf16; mask [B, N] uint8.
+ * The bias is shared by the `mult` copies of each batch element (multiplicity).
+ * Supported: c_z = 128, head dim 24 (c_s = 24*H, c_s in {128, 384}).
+ */
+size_t bioemu_apb_workspace_bytes(int64_t B, int64_t mult, int64_t N, int64_t c_s, int64_t H);
+int bioemu_apb_fwd(const void* s, const void* z, const uint8_t* mask, const float* norm_s_w,
+                   const float* norm_s_b, const void* w_qkv, const float* q_bias, const void* w_g,
+                   const float* norm_z_w, const float* norm_z_b, const void* w_z, const void* w_o,
+                   void* out, void* workspace, size_t workspace_bytes, int64_t B, int64_t mult,
+                   int64_t N, int64_t c_s, int64_t c_z, int64_t H, int residual, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
