@@ -417,3 +417,93 @@ def attention_pair_bias(
 @attention_pair_bias.register_fake
 def _(s, z, mask, norm_s_w, norm_s_b, w_qkv, q_bias, w_g, norm_z_w, norm_z_b, w_z, w_o, num_heads, multiplicity):
     return torch.empty_like(s)
+
+
+# ----------------------------------------------------------------------------
+# Outer product mean
+# ----------------------------------------------------------------------------
+def opm_workspace_bytes(B: int, S: int, N: int, c_in: int = 64, c_hidden: int = 32) -> int:
+    return int(lib().bioemu_opm_workspace_bytes(B, S, N, c_in, c_hidden))
+
+
+def opm_mask3(mask: Tensor, B: int, S: int, N: int) -> tuple[Tensor, bool]:
+    """Reference mask -> ([B,S,N] uint8, mean over rows?).
+
+    A [B,S,N] mask is used as is (divisor = count of rows with any valid
+    entry).  A 2-D mask is broadcast exactly as ``masked_fill_(~mask.unsqueeze(-1))``
+    broadcasts it against ``[B,S,N,2C]`` (its first dim lines up with S) and
+    the divisor is 1 (outer_product_mean.py:62, :69-70).
+    """
+    if mask.ndim == 3:
+        if tuple(mask.shape) != (B, S, N):
+            raise ValueError(f"opm: mask shape {tuple(mask.shape)} != {(B, S, N)}")
+        return mask_u8(mask), True
+    if mask.ndim == 2:
+        m3 = torch.broadcast_to(mask.bool(), (S, N)).unsqueeze(0).expand(B, S, N)
+        return mask_u8(m3.contiguous()), False
+    raise ValueError(f"opm: mask must be [B,S,N] or [B,N], got {tuple(mask.shape)}")
+
+
+def launch_opm(
+    m: Tensor,
+    mask3: Tensor,
+    mean_rows: bool,
+    norm_w: Tensor,
+    norm_b: Tensor,
+    w_ab: Tensor,
+    w_o: Tensor,
+    b_o: Tensor,
+    out: Tensor,
+    z_res: Tensor | None = None,
+    ws: Tensor | None = None,
+) -> Tensor:
+    require_gpu(m, "outer_product_mean")
+    if m.ndim != 4:
+        raise ValueError(f"opm: m must be [B,S,N,C], got {tuple(m.shape)}")
+    B, S, N, c_in = m.shape
+    c_h = w_ab.shape[0] // 2
+    c_out = w_o.shape[0]
+    dev = m.device
+    _check_tensor(m, "opm m", BF16, (B, S, N, c_in), dev)
+    _check_tensor(mask3, "opm mask", torch.uint8, (B, S, N), dev)
+    _check_tensor(norm_w, "opm norm.weight", torch.float32, (c_in,), dev)
+    _check_tensor(norm_b, "opm norm.bias", torch.float32, (c_in,), dev)
+    _check_tensor(w_ab, "opm proj_ab.weight", BF16, (2 * c_h, c_in), dev)
+    _check_tensor(w_o, "opm proj_o.weight", BF16, (c_out, c_h * c_h), dev)
+    _check_tensor(b_o, "opm proj_o.bias", torch.float32, (c_out,), dev)
+    _check_tensor(out, "opm out", BF16, (B, N, N, c_out), dev)
+    if z_res is not None:
+        _check_tensor(z_res, "opm z", BF16, (B, N, N, c_out), dev)
+    need = opm_workspace_bytes(B, S, N, c_in, c_h)
+    if need == 0:
+        raise ValueError(f"opm: unsupported widths c_in={c_in} c_hidden={c_h}")
+    if ws is None or ws.numel() < need:
+        ws = workspace(need, dev)
+    rc = lib().bioemu_opm_fwd(
+        _ptr(m), _ptr(mask3), int(bool(mean_rows)), _ptr(norm_w), _ptr(norm_b), _ptr(w_ab), _ptr(w_o), _ptr(b_o),
+        _ptr(z_res), _ptr(out), _ptr(ws), ctypes.c_size_t(ws.numel()), B, S, N, c_in, c_h, c_out, _stream(m),
+    )
+    check(rc, "bioemu_opm_fwd")
+    return out
+
+
+@torch.library.custom_op("bioemu_mi355x::outer_product_mean", mutates_args=(), device_types="cuda")
+def outer_product_mean(
+    m: Tensor, mask: Tensor, norm_w: Tensor, norm_b: Tensor, w_ab: Tensor, w_o: Tensor, b_o: Tensor
+) -> Tensor:
+    mb = m.to(BF16).contiguous()
+    B, S, N, _ = mb.shape
+    mask3, mean_rows = opm_mask3(mask, B, S, N)
+    out = torch.empty(B, N, N, w_o.shape[0], dtype=BF16, device=m.device)
+    f32 = torch.float32
+    launch_opm(
+        mb, mask3, mean_rows, norm_w.to(f32).contiguous(), norm_b.to(f32).contiguous(), w_ab.to(BF16).contiguous(),
+        w_o.to(BF16).contiguous(), b_o.to(f32).contiguous(), out,
+    )
+    return out.to(m.dtype)
+
+
+@outer_product_mean.register_fake
+def _(m, mask, norm_w, norm_b, w_ab, w_o, b_o):
+    B, S, N, _ = m.shape
+    return m.new_empty(B, N, N, w_o.shape[0])

@@ -25,7 +25,6 @@ namespace {
 
 constexpr int CZ = 128;
 constexpr int kBiasThreads = 256;
-constexpr int kBiasSmem = 32 * kLdw * 2;
 
 // bias[b][h][i][j] = LN(z[b][i][j]) . Wz[h] for i, j < Np (zero pair rows outside [0, N)).
 __global__ __launch_bounds__(kBiasThreads) void pair_bias_kernel(const bf16* __restrict__ z,
@@ -245,7 +244,7 @@ extern "C" int bioemu_apb_fwd(const void* s, const void* z, const uint8_t* mask,
   if (rc) return rc;
 
   int dev = 0, cus = 0;
-  hipGetDevice(&dev);
+  (void)hipGetDevice(&dev);
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
   const long long ntiles = B * Np * (Np / 32);
   const unsigned grid1 = (unsigned)std::min<long long>(4LL * cus, (ntiles + 3) / 4);

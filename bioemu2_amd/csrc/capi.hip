@@ -104,14 +104,14 @@ KernelTimerScope::KernelTimerScope(const char* name, hipStream_t stream) : strea
     name_idx_ = -1;
     return;
   }
-  hipEventRecord(start_, stream_);
+  (void)hipEventRecord(start_, stream_);
 }
 
 KernelTimerScope::~KernelTimerScope() {
   if (name_idx_ < 0) return;
   TimerState& t = timer();
   std::lock_guard<std::mutex> lock(t.mu);
-  hipEventRecord(stop_, stream_);
+  (void)hipEventRecord(stop_, stream_);
   t.records.push_back({name_idx_, start_, stop_});
 }
 

@@ -1,0 +1,380 @@
+// Fused OuterProductMean for gfx950.
+//
+// Reference: OuterProductMeanVanilla.forward
+// (src/bioemu2/biomoa/ops/outer_product_mean.py:45-75):
+//   p = proj_ab(LN(m)); p[~mask] = 0; a, b = chunk(p, 2)            [B,S,N,C_H] each
+//   num_valid = mask.any(-1).sum(1).clamp(min=1)   ([B,S,N] mask; 1 for a [B,N] mask)
+//   o[b,i,j,c*C_H+d] = sum_s a[b,s,i,c] b[b,s,j,d] / num_valid[b]   (fp32)
+//   out = proj_o(o.to(m.dtype)) (+ bias)
+// The mean is applied before the cast to the operand dtype, as the reference's
+// memory-saving kernel does (src/bioemu2/biomoa/ops/triton/opm.py:114-116).
+//
+// Kernels:
+//   opm_rows  : per batch, the ordered list of MSA rows with any valid entry
+//               and its length (= the reference's num_valid before clamping).
+//               Rows outside the list are all-zero after the mask, so
+//               contracting over the list only is exact.
+//   opm_proj  : LN + proj_ab on MFMA; masked entries are zeroed *before* the
+//               bias-free projection (0 * W = 0 exactly, the same as
+//               masked_fill after it).  Writes aT[b][n][c][r], bT[b][n][d][r]
+//               with the compacted row r contiguous (zero for r >= count).
+//   opm_fused : one workgroup per (b, 8 i, 8 j) pair tile.  X^T[(j,d),(i,c)] =
+//               sum_r bT[(j,d)][r] aT[(i,c)][r] (256 x 256 MFMA tile over the
+//               valid rows, operands double-buffered through LDS), times
+//               1/num_valid, cast to bf16 into LDS as [pair][c*32+d], then
+//               out^T = Wo * X^T + bias (+ z) from LDS on MFMA.
+#include <algorithm>
+
+#include "common.h"
+#include "internal.h"
+#include "pairtile.h"
+
+namespace bioemu {
+namespace {
+
+constexpr int CIN = 64;
+constexpr int CH = 32;
+constexpr int COUT = 128;
+constexpr int CH2 = CH * CH;  // 1024
+
+// ---------------------------------------------------------------------------
+// Row compaction.  One workgroup per batch.
+// ---------------------------------------------------------------------------
+constexpr int kRowsThreads = 256;
+
+__global__ __launch_bounds__(kRowsThreads) void opm_rows_kernel(const uint8_t* __restrict__ mask, int* __restrict__ idx,
+                                                                int* __restrict__ count, int S, int N) {
+  __shared__ int part[kRowsThreads];
+  const int b = blockIdx.x;
+  const int per = (S + kRowsThreads - 1) / kRowsThreads;
+  const int s0 = min(S, (int)threadIdx.x * per), s1 = min(S, s0 + per);
+  const uint8_t* mb = mask + (size_t)b * S * N;
+  const bool vec = (N % 16 == 0) && ((reinterpret_cast<uintptr_t>(mask) & 15) == 0);
+  uint64_t bits = 0;  // per <= 64 rows per thread (S <= 16384)
+  int cnt = 0;
+  for (int s = s0; s < s1; ++s) {
+    const uint8_t* row = mb + (size_t)s * N;
+    bool any = false;
+    if (vec) {
+      for (int t = 0; t < N && !any; t += 16) {
+        const uint4 v = *reinterpret_cast<const uint4*>(row + t);
+        any = (v.x | v.y | v.z | v.w) != 0;
+      }
+    } else {
+      for (int t = 0; t < N && !any; ++t) any = row[t] != 0;
+    }
+    if (any) {
+      bits |= 1ull << (s - s0);
+      ++cnt;
+    }
+  }
+  part[threadIdx.x] = cnt;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int run = 0;
+    for (int t = 0; t < kRowsThreads; ++t) {
+      const int c = part[t];
+      part[t] = run;
+      run += c;
+    }
+    count[b] = run;
+  }
+  __syncthreads();
+  int out = part[threadIdx.x];
+  for (int s = s0; s < s1; ++s)
+    if (bits >> (s - s0) & 1ull) idx[(size_t)b * S + out++] = s;
+}
+
+// ---------------------------------------------------------------------------
+// Projection.  Tile = (b, token n, 32 compacted rows).  A 64-channel row is
+// held by lanes l and l^32 (channels 32h .. 32h+31, 4 MFMA k-steps).
+// ---------------------------------------------------------------------------
+constexpr int kProjThreads = 256;
+
+__global__ __launch_bounds__(kProjThreads) void opm_proj_kernel(
+    const bf16* __restrict__ m, const uint8_t* __restrict__ mask, const int* __restrict__ idx,
+    const int* __restrict__ count, const float* __restrict__ ln_w, const float* __restrict__ ln_b,
+    const bf16* __restrict__ w_ab, bf16* __restrict__ aT, bf16* __restrict__ bT, int B, int S, int N, int Nt,
+    int Sp) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rho = lane & 31, h = lane >> 5;
+  const int waves = blockDim.x >> 6;
+  const int rtiles = Sp / 32;
+  const long long ntiles = (long long)B * Nt * rtiles;
+  for (long long t = (long long)blockIdx.x * waves + wave; t < ntiles; t += (long long)gridDim.x * waves) {
+    const int rt = (int)(t % rtiles);
+    const int n = (int)((t / rtiles) % Nt);
+    const int b = (int)(t / ((long long)rtiles * Nt));
+    const int r0 = rt * 32;
+    const int nv = count[b];
+    const int r = r0 + perm32(rho);
+    int s = -1;
+    if (r < nv && n < N) s = idx[(size_t)b * S + r];
+    bool valid = s >= 0;
+    if (valid) valid = mask[((size_t)b * S + s) * N + n] != 0;
+    float v[32];
+    bf16x8 raw[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (s >= 0) {
+        raw[q] = load8(m + (((size_t)b * S + s) * N + n) * CIN + 32 * h + 8 * q);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) raw[q][e] = f2bf(0.f);
+      }
+      unpack8(raw[q], v + 8 * q);
+    }
+    float sum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 32; ++e) sum += v[e];
+    sum += __shfl_xor(sum, 32);
+    const float mean = sum * (1.0f / CIN);
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 32; ++e) {
+      const float d = v[e] - mean;
+      ss += d * d;
+    }
+    ss += __shfl_xor(ss, 32);
+    const float rstd = rsqrtf(ss * (1.0f / CIN) + 1e-5f);
+    bf16x8 xf[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int c = 32 * h + 8 * q + e;
+        const float y = (v[8 * q + e] - mean) * rstd * ln_w[c] + ln_b[c];
+        xf[q][e] = f2bf(valid ? y : 0.f);  // masked_fill before the bias-free projection
+      }
+#pragma unroll
+    for (int which = 0; which < 2; ++which) {
+      f32x16 acc = zero16();
+      const bf16* wr = w_ab + (size_t)(which * CH + rho) * CIN + 32 * h;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc = mfma32(xf[q], load8(wr + 8 * q), acc);
+      float o[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) o[u] = acc[u];
+      bf16* dst = (which ? bT : aT) + (((size_t)b * Nt + n) * CH + rho) * Sp + r0 + 16 * h;
+      store16(dst, o);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Fused contraction + mean + output projection.
+// ---------------------------------------------------------------------------
+constexpr int kFusedThreads = 512;
+constexpr int TI = 8, TJ = 8;            // pair tile
+constexpr int TR = 32;                   // rows per K stage
+constexpr int LDK = TR + 8;              // LDS row stride of the operand stages
+constexpr int LDX = CH2 + 8;             // LDS row stride of the mean tile
+constexpr int kStageElems = 2 * 256 * LDK;
+constexpr int kFusedSmemA = 2 * kStageElems * 2;
+constexpr int kFusedSmemB = TI * TJ * LDX * 2;
+constexpr int kFusedSmem = kFusedSmemA > kFusedSmemB ? kFusedSmemA : kFusedSmemB;
+
+__global__ __launch_bounds__(kFusedThreads) void opm_fused_kernel(
+    const bf16* __restrict__ aT, const bf16* __restrict__ bT, const int* __restrict__ count, int mean_rows,
+    const bf16* __restrict__ w_o, const float* __restrict__ b_o, const bf16* zres, bf16* out, int N, int Nt, int Sp) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  bf16* stage = reinterpret_cast<bf16*>(smem);
+  bf16* xb = reinterpret_cast<bf16*>(smem);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int n = lane & 31, h = lane >> 5;
+  const int b = blockIdx.z;
+  const int i0 = blockIdx.y * TI, j0 = blockIdx.x * TJ;
+  const int nv = count[b];
+  const int kend = (nv + TR - 1) / TR * TR;
+
+  // A rows = (j, d) from bT, B rows = (i, c) from aT: 256 contiguous rows each.
+  const bf16* Ag = bT + ((size_t)b * Nt + j0) * CH * Sp;
+  const bf16* Bg = aT + ((size_t)b * Nt + i0) * CH * Sp;
+
+  // Staging: 256 rows x 32 r (64 B) per operand = 1024 16-byte chunks each.
+  bf16x8 ra[2], rb[2];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      const int q = it * kFusedThreads + tid;
+      const int row = q >> 2, part = q & 3;
+      ra[it] = load8(Ag + (size_t)row * Sp + k0 + part * 8);
+      rb[it] = load8(Bg + (size_t)row * Sp + k0 + part * 8);
+    }
+  };
+  auto lstore = [&](int buf) {
+    bf16* sa = stage + buf * kStageElems;
+    bf16* sb = sa + 256 * LDK;
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      const int q = it * kFusedThreads + tid;
+      const int row = q >> 2, part = q & 3;
+      store8(sa + row * LDK + part * 8, ra[it]);
+      store8(sb + row * LDK + part * 8, rb[it]);
+    }
+  };
+
+  // Wave tile: rows [128*wr, +128) (4 blocks), cols [64*wc, +64) (2 blocks).
+  const int wr = wave >> 2, wc = wave & 3;
+  f32x16 acc[4][2];
+#pragma unroll
+  for (int x = 0; x < 4; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y) acc[x][y] = zero16();
+
+  if (kend > 0) {
+    gload(0);
+    lstore(0);
+  }
+  __syncthreads();
+  for (int k0 = 0; k0 < kend; k0 += TR) {
+    const int cur = (k0 / TR) & 1;
+    const bool more = k0 + TR < kend;
+    if (more) gload(k0 + TR);
+    const bf16* sa = stage + cur * kStageElems;
+    const bf16* sb = sa + 256 * LDK;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      bf16x8 af[4], bfr[2];
+#pragma unroll
+      for (int x = 0; x < 4; ++x) af[x] = load8(sa + (wr * 128 + x * 32 + perm32(n)) * LDK + ks * 16 + 8 * h);
+#pragma unroll
+      for (int y = 0; y < 2; ++y) bfr[y] = load8(sb + (wc * 64 + y * 32 + n) * LDK + ks * 16 + 8 * h);
+#pragma unroll
+      for (int x = 0; x < 4; ++x)
+#pragma unroll
+        for (int y = 0; y < 2; ++y) acc[x][y] = mfma32(af[x], bfr[y], acc[x][y]);
+    }
+    if (more) lstore(cur ^ 1);
+    __syncthreads();
+  }
+
+  // Mean before the cast: xb[pair (ii, jj)][c*32 + d] = X[(i,c),(j,d)] / num_valid.
+  const float inv = mean_rows ? 1.0f / (float)max(nv, 1) : 1.0f;
+#pragma unroll
+  for (int x = 0; x < 4; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y) {
+      const int jj = wr * 4 + x;          // row block = one j, d = 16h + u
+      const int col = wc * 64 + y * 32 + n;
+      const int ii = col >> 5, c = col & 31;
+      float v[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) v[u] = acc[x][y][u] * inv;
+      store16(xb + (ii * TJ + jj) * LDX + c * CH + 16 * h, v);
+    }
+  __syncthreads();
+
+  // out^T[e][pair] = Wo[e][:] . xb[pair][:] ; wave -> (e block, pair block)
+  const int eb = wave & 3, pb = wave >> 2;
+  f32x16 y = zero16();
+  const bf16* wrow = w_o + (size_t)(eb * 32 + perm32(n)) * CH2 + 8 * h;
+  const bf16* xrow = xb + (pb * 32 + n) * LDX + 8 * h;
+#pragma unroll 8
+  for (int k = 0; k < CH2; k += 16) y = mfma32(load8(wrow + k), load8(xrow + k), y);
+  const int p = pb * 32 + n, ii = p / TJ, jj = p % TJ;
+  const int i = i0 + ii, j = j0 + jj;
+  if (i >= N || j >= N) return;
+  const size_t off = (((size_t)b * N + i) * N + j) * COUT + eb * 32 + 16 * h;
+  float v[16];
+#pragma unroll
+  for (int u = 0; u < 16; ++u) v[u] = y[u] + b_o[eb * 32 + 16 * h + u];
+  if (zres) {
+    const bf16x8 r0 = load8(zres + off), r1 = load8(zres + off + 8);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      v[u] += bf2f(r0[u]);
+      v[8 + u] += bf2f(r1[u]);
+    }
+  }
+  store16(out + off, v);
+}
+
+struct OpmLayout {
+  int* idx;
+  int* count;
+  bf16* aT;
+  bf16* bT;
+};
+
+size_t opm_layout(int64_t B, int64_t S, int64_t N, OpmLayout* L, char* base) {
+  const size_t Nt = (size_t)round_up(N, 8), Sp = (size_t)round_up(S, 32);
+  const size_t idx_b = round_up((size_t)B * S * 4, 256), cnt_b = round_up((size_t)B * 4, 256);
+  const size_t ab_b = round_up((size_t)B * Nt * CH * Sp * 2, 256);
+  if (L) {
+    L->idx = reinterpret_cast<int*>(base);
+    L->count = reinterpret_cast<int*>(base + idx_b);
+    L->aT = reinterpret_cast<bf16*>(base + idx_b + cnt_b);
+    L->bT = reinterpret_cast<bf16*>(base + idx_b + cnt_b + ab_b);
+  }
+  return idx_b + cnt_b + 2 * ab_b;
+}
+
+}  // namespace
+}  // namespace bioemu
+
+using namespace bioemu;
+
+extern "C" size_t bioemu_opm_workspace_bytes(int64_t B, int64_t S, int64_t N, int64_t c_in, int64_t c_hidden) {
+  if (B <= 0 || S <= 0 || N <= 0 || c_in != CIN || c_hidden != CH) return 0;
+  return opm_layout(B, S, N, nullptr, nullptr);
+}
+
+extern "C" int bioemu_opm_fwd(const void* m, const uint8_t* mask, int mean_rows, const float* norm_w,
+                              const float* norm_b, const void* w_ab, const void* w_o, const float* b_o,
+                              const void* z_res, void* out, void* workspace, size_t workspace_bytes, int64_t B,
+                              int64_t S, int64_t N, int64_t c_in, int64_t c_hidden, int64_t c_out,
+                              hipStream_t stream) {
+  if (c_in != CIN || c_hidden != CH || c_out != COUT)
+    return set_error(BIOEMU_ERR_UNSUPPORTED, "opm: only c_in=64, c_hidden=32, c_out=128 supported (got %lld/%lld/%lld)",
+                     (long long)c_in, (long long)c_hidden, (long long)c_out);
+  if (B <= 0 || S <= 0 || N <= 0 || S > 16384 || N > 16384 || B > 65535)
+    return set_error(BIOEMU_ERR_INVALID_ARG, "opm: bad shape B=%lld S=%lld N=%lld", (long long)B, (long long)S,
+                     (long long)N);
+  if (!m || !mask || !norm_w || !norm_b || !w_ab || !w_o || !b_o || !out || !workspace)
+    return set_error(BIOEMU_ERR_INVALID_ARG, "opm: null pointer argument");
+  if (!aligned16(m) || !aligned16(w_ab) || !aligned16(w_o) || !aligned16(out) || !aligned16(workspace) ||
+      (z_res && !aligned16(z_res)))
+    return set_error(BIOEMU_ERR_INVALID_ARG, "opm: tensors must be 16-byte aligned");
+  if (workspace_bytes < opm_layout(B, S, N, nullptr, nullptr))
+    return set_error(BIOEMU_ERR_WORKSPACE, "opm: workspace too small");
+  OpmLayout L;
+  opm_layout(B, S, N, &L, static_cast<char*>(workspace));
+  const int64_t Nt = round_up(N, 8), Sp = round_up(S, 32);
+
+  {
+    KernelTimerScope timed("opm_rows", stream);
+    hipLaunchKernelGGL(opm_rows_kernel, dim3((unsigned)B), dim3(kRowsThreads), 0, stream, mask, L.idx, L.count,
+                       (int)S, (int)N);
+  }
+  int rc = check_launch("opm_rows");
+  if (rc) return rc;
+
+  int dev = 0, cus = 0;
+  (void)hipGetDevice(&dev);
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+  const long long ntiles = B * Nt * (Sp / 32);
+  const unsigned grid2 = (unsigned)std::min<long long>(8LL * cus, (ntiles + 3) / 4);
+  {
+    KernelTimerScope timed("opm_proj", stream);
+    hipLaunchKernelGGL(opm_proj_kernel, dim3(grid2), dim3(kProjThreads), 0, stream, static_cast<const bf16*>(m), mask,
+                       L.idx, L.count, norm_w, norm_b, static_cast<const bf16*>(w_ab), L.aT, L.bT, (int)B, (int)S,
+                       (int)N, (int)Nt, (int)Sp);
+  }
+  rc = check_launch("opm_proj");
+  if (rc) return rc;
+
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(opm_fused_kernel),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, kFusedSmem) != hipSuccess)
+    return set_error(BIOEMU_ERR_LAUNCH, "opm_fused: cannot set dynamic LDS size");
+  dim3 g3((unsigned)(Nt / TJ), (unsigned)(Nt / TI), (unsigned)B);
+  {
+    KernelTimerScope timed("opm_fused", stream);
+    hipLaunchKernelGGL(opm_fused_kernel, g3, dim3(kFusedThreads), kFusedSmem, stream, L.aT, L.bT, L.count, mean_rows,
+                       static_cast<const bf16*>(w_o), b_o, static_cast<const bf16*>(z_res), static_cast<bf16*>(out),
+                       (int)N, (int)Nt, (int)Sp);
+  }
+  return check_launch("opm_fused");
+}

@@ -327,7 +327,7 @@ extern "C" int bioemu_triatt_fwd(const void* z, const uint8_t* mask, const float
   buf.mask = reinterpret_cast<uint8_t*>(p);
 
   int dev = 0, cus = 0;
-  hipGetDevice(&dev);
+  (void)hipGetDevice(&dev);
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
   const void* kproj = starting ? reinterpret_cast<const void*>(triatt_proj_kernel<true>)
                                : reinterpret_cast<const void*>(triatt_proj_kernel<false>);

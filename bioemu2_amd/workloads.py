@@ -256,7 +256,62 @@ class BlockWorkload(Workload):
         raise KeyError(kernel)
 
 
+class OpmWorkload(Workload):
+    """Config 3: fused OuterProductMean, m [1,1024,512,64] bf16, seeded 20% of rows masked, added into z."""
+
+    def __init__(self, device, n: int = 512, S: int = 1024, seed: int = 0):
+        from .outer_product_mean import OuterProductMeanHip
+
+        self.n, self.S = n, S
+        self.name = f"opm_s{S}_n{n}"
+        self.metric = f"ms per fused OuterProductMean at S={S}, N={n} bf16"
+        torch.manual_seed(seed)
+        self.module = init_module(OuterProductMeanHip(64, 32, 128), seed).to(device).eval()
+        g = torch.Generator().manual_seed(seed)
+        self.m_cpu = torch.randn(1, S, n, 64, generator=g).to(torch.bfloat16)
+        rows = torch.rand(S, generator=torch.Generator().manual_seed(seed)) >= 0.2
+        self.s_valid = int(rows.sum())
+        self.mask_cpu = rows[None, :, None].expand(1, S, n).contiguous()
+        self.z_cpu = torch.randn(1, n, n, 128, generator=g).to(torch.bfloat16)
+        self.m = self.m_cpu.to(device)
+        self.mask3, self.mean_rows = _ops.opm_mask3(self.mask_cpu.to(device), 1, S, n)
+        self.z = self.z_cpu.to(device)
+        self.ws = _ops.workspace(_ops.opm_workspace_bytes(1, S, n), device)
+        self.params = self.module.prepared_params()
+        self.config = {"workload": self.name, "S": S, "N": n, "c_m": 64, "c_hidden": 32, "c_out": 128,
+                       "valid_rows": self.s_valid, "residual": True}
+        self.flops = (2.0 * n * n * 1024 * self.s_valid + 2.0 * n * n * 1024 * 128
+                      + 2.0 * self.s_valid * n * 64 * 64)
+
+    def step(self) -> None:
+        _ops.launch_opm(self.m, self.mask3, self.mean_rows, *self.params, out=self.z, z_res=self.z, ws=self.ws)
+
+    def cpu_sample(self, oracle):
+        rows = 64
+        m = self.m_cpu.float()
+        mask = self.mask_cpu
+        params = {k: v.detach().cpu() for k, v in self.module.state_dict().items()}
+
+        def fn():
+            # the oracle's i-chunked loop, stopped after the first `rows` output rows
+            return oracle.outer_product_mean(m, mask, params, i_chunk=rows, i_stop=rows)
+
+        return fn, rows / self.n, f"oracle.outer_product_mean fp32 on {rows} of {self.n} output rows"
+
+    def kernel_work(self, kernel: str) -> tuple[str, float]:
+        n, S = self.n, self.S
+        if kernel == "opm_fused":
+            return ("mfma", 2.0 * n * n * 1024 * self.s_valid + 2.0 * n * n * 1024 * 128)
+        if kernel == "opm_proj":
+            return ("hbm", float(self.s_valid * n * 64 * 2 + 2 * S * n * 32 * 2))
+        if kernel == "opm_rows":
+            return ("hbm", float(S * n))
+        raise KeyError(kernel)
+
+
 def make(op: str, device, n: int | None = None) -> Workload:
+    if op == "opm":
+        return OpmWorkload(device, n or 512)
     if op == "block":
         return BlockWorkload(device, n or 768)
     if op in ("triatt_start", "triatt_end"):

@@ -135,6 +135,26 @@ int bioemu_apb_fwd(const void* s, const void* z, const uint8_t* mask, const floa
                    void* out, void* workspace, size_t workspace_bytes, int64_t B, int64_t mult,
                    int64_t N, int64_t c_s, int64_t c_z, int64_t H, int residual, hipStream_t stream);
 
+/*
+ * Fused OuterProductMean.
+ * Replaces OuterProductMeanVanilla.forward / OuterProductMeanTritonMemorySaving.forward
+ * (src/bioemu2/biomoa/ops/outer_product_mean.py:45-75, :129-152):
+ *   p = proj_ab(LN(m)); p[mask == 0] = 0; a, b = chunk(p, 2)
+ *   o[b,i,j,c*C_H+d] = sum_s a[b,s,i,c] b[b,s,j,d] / num_valid[b]   (fp32, mean before the bf16 cast)
+ *   out = o Wo^T + b_o   (+ z_res when z_res != NULL; out may equal z_res)
+ * m: [B,S,N,c_in] bf16; mask: [B,S,N] uint8.  mean_rows=1 divides by
+ * num_valid = max(1, #rows with any valid entry) (a [B,S,N] reference mask);
+ * mean_rows=0 divides by 1 (a [B,N] reference mask, expanded over S by the caller).
+ * w_ab: [2*C_H, c_in]; w_o: [c_out, C_H*C_H]; b_o: [c_out] fp32; out: [B,N,N,c_out] bf16.
+ * Supported: c_in = 64, C_H = 32, c_out = 128.
+ */
+size_t bioemu_opm_workspace_bytes(int64_t B, int64_t S, int64_t N, int64_t c_in, int64_t c_hidden);
+int bioemu_opm_fwd(const void* m, const uint8_t* mask, int mean_rows, const float* norm_w,
+                   const float* norm_b, const void* w_ab, const void* w_o, const float* b_o,
+                   const void* z_res, void* out, void* workspace, size_t workspace_bytes, int64_t B,
+                   int64_t S, int64_t N, int64_t c_in, int64_t c_hidden, int64_t c_out,
+                   hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -213,7 +213,9 @@ def attention_pair_bias(
 # ----------------------------------------------------------------------------
 # Outer product mean
 # ----------------------------------------------------------------------------
-def outer_product_mean(m: Tensor, mask: Tensor, params: dict, i_chunk: int | None = None) -> Tensor:
+def outer_product_mean(
+    m: Tensor, mask: Tensor, params: dict, i_chunk: int | None = None, i_stop: int | None = None
+) -> Tensor:
     """OuterProductMeanVanilla.forward (biomoa/ops/outer_product_mean.py:45-75).
 
     m [B,S,N,C_in], mask [B,S,N] or [B,N] -> [B,N,N,C_out] (float32).
@@ -221,6 +223,8 @@ def outer_product_mean(m: Tensor, mask: Tensor, params: dict, i_chunk: int | Non
     mask, 1 for a [B,N] mask (:67-70); flatten order c*C_H + d (:72-73); the
     mean is taken before the output projection (:74-75 and the memory-saving
     kernel's "normalize before the cast", ops/triton/opm.py:114-116).
+    ``i_stop`` computes only output rows [0, i_stop) (rows beyond stay
+    uninitialised; used to time a bounded sample).
     """
     m = _f32(m)
     mask = mask.bool().cpu()
@@ -236,7 +240,7 @@ def outer_product_mean(m: Tensor, mask: Tensor, params: dict, i_chunk: int | Non
     bo = _p(params, "proj_o.bias")
     out = torch.empty(B, N, N, wo.shape[0])
     step = i_chunk or N
-    for i0 in range(0, N, step):
+    for i0 in range(0, min(N, i_stop or N), step):
         i1 = min(N, i0 + step)
         zc = torch.einsum("bsic,bsjd->bijcd", a[:, :, i0:i1], b)  # :72
         zc = zc.reshape(B, i1 - i0, N, C * C)  # :73

@@ -39,6 +39,24 @@ def test_python_binding_covers_every_declared_symbol():
     assert sorted(_lib.SIGNATURES) == _declared()
 
 
+def _declared_arity() -> dict[str, int]:
+    """Parameter count of every declared entry point, parsed from include/*.h."""
+    text = "\n".join(h.read_text() for h in sorted((ROOT / "include").glob("*.h")))
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(bioemu_\w+)\s*\(([^;{]*?)\)\s*;", text, re.S):
+        params = m.group(2).strip()
+        out[m.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+def test_binding_arity_matches_header():
+    arity = _declared_arity()
+    assert set(arity) == set(_lib.SIGNATURES)
+    for name, (_, argtypes) in _lib.SIGNATURES.items():
+        assert len(argtypes) == arity[name], (name, len(argtypes), arity[name])
+
+
 def test_host_only_queries():
     lib = _lib.lib()
     assert b"gfx950" in lib.bioemu_version()
