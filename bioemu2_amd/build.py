@@ -23,6 +23,11 @@ ARCH = os.environ.get("BIOEMU_OFFLOAD_ARCH", "gfx950")
 
 # Packed-fp32 VALU ops are disabled for device code; the host pass warns that
 # it does not know the feature, which is harmless.
+# -fno-honor-nans: no kernel relies on NaN propagation (infinities are still
+# honoured: the softmax masks use -inf), and it lets fmaxf lower to a single
+# v_max_f32 instead of canonicalise + max.
+# -amdgpu-mfma-vgpr-form: MFMA accumulators live in VGPRs, which removes the
+# AGPR<->VGPR copies around every softmax / epilogue touch of an accumulator.
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
@@ -34,6 +39,9 @@ HIPCC_FLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    "-fno-honor-nans",
+    "-mllvm",
+    "-amdgpu-mfma-vgpr-form",
     f"-I{INCLUDE}",
 ]
 

@@ -40,12 +40,16 @@ constexpr int kProjThreads = 512;
 constexpr int kProjSmem = kProjRowsPad * kLdw * 2;
 constexpr int kFlashThreads = 256;         // 4 waves x 32 queries = 128 queries per workgroup
 
+// Softmax in base 2: q is stored pre-scaled by log2(e)/sqrt(d) and the bias by
+// log2(e), so QK^T + bias comes out of the MFMA directly in log2 units.
+constexpr float kQScale = 0.17677669529663687f * kLog2e;
+
 struct TriAttBuffers {
-  bf16* q;       // [B][Np][Np][C]  frame-ordered, pair-major
+  bf16* q;       // [B][Np][Np][C]  frame-ordered, pair-major, times kQScale
   bf16* k;       // [B][Np][Np][C]
   bf16* g;       // [B][Np][Np][C]  sigmoid already applied
   bf16* vt;      // [B][Np][C][Np]  channel-major per frame row
-  bf16* bias;    // [B][H][Np][Np]
+  bf16* bias;    // [B][H][Np][Np]  times log2(e)
   uint8_t* mask; // [B][Np][Np]     frame-ordered 0/1 (0 outside [0, N))
 };
 
@@ -91,7 +95,7 @@ __global__ __launch_bounds__(kProjThreads) void triatt_proj_kernel(
       f32x16 aq = proj_block_pm(x, wl, 0 * C + cb * 32, rho, h);
       float vq[16];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) vq[u] = aq[u];
+      for (int u = 0; u < 16; ++u) vq[u] = aq[u] * kQScale;
       store16(buf.q + pm_off + cb * 32 + 16 * h, vq);
       f32x16 ak = proj_block_pm(x, wl, 1 * C + cb * 32, rho, h);
 #pragma unroll
@@ -116,7 +120,7 @@ __global__ __launch_bounds__(kProjThreads) void triatt_proj_kernel(
       if (rho < H) {
         float vb[16];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) vb[u] = ab[u];
+        for (int u = 0; u < 16; ++u) vb[u] = ab[u] * kLog2e;
         store16(buf.bias + ((size_t)b * H + rho) * plane + (size_t)i * Np + k0 + 16 * h, vb);
       }
     }
@@ -134,120 +138,217 @@ __global__ __launch_bounds__(kProjThreads) void triatt_proj_kernel(
 
 // ---------------------------------------------------------------------------
 // Flash attention kernel.  Workgroup = (b, frame row i, 128 queries);
-// wave w owns queries q0 = 128*blockIdx.x + 32w, all 4 heads.
+// wave w owns queries q0 = 128*blockIdx.x + 32w.
 //
-// S^T = K Q^T per head: A = K (pair slot rho <-> key k0 + perm32(rho)),
-// B = Q^T (lane n <-> query q0 + n).  D lane (n, hh) register u <-> key
-// k0 + 16hh + u, so a lane holds 16 consecutive keys of one query; the row
-// max / sum need one cross-half shuffle.  O^T = V^T P^T: A = V^T (slot rho <->
-// d = perm32(rho)), B = P^T straight from the softmax registers (k-step s,
-// half hh, t <-> key k0 + 16hh + 8s + t).  D lane (n, hh) register u <->
-// d = 16hh + u.  The epilogue feeds g*o back as the B operand of
-// update^T = Wo (g*o)^T, again without leaving registers.
+// At head dim 32 the attention is bound by vector-ALU and issue work, not by
+// the matrix cores, so everything that can ride on an MFMA does:
+//   S^T = K Q^T               2 MFMAs (k-steps over d)
+//       + bias               2 MFMAs: A = one-hot "identity" fragments,
+//                             B = the bias tile in B-operand layout
+//       + key mask           1 MFMA:  rank-1 product of a per-key column
+//                             (0 valid, -1e30 masked, -inf beyond N) with e_0
+// A masked key's logit is -1e30 + (q.k + bias) = -1e30 exactly in fp32, so a
+// fully masked row gets equal logits (uniform weights, the reference's
+// masked_fill(-1e6) result) and a partially masked row gets exact zeros.
+// The running max is only moved (and o, l rescaled) when some row's block
+// max exceeds it by more than 2^8, so most blocks skip the rescale.
+//
+// Loops: heads outermost (one head's accumulator live; a finished head leaves
+// o/l as 8 packed-bf16 registers), then 64-key blocks.  A block is two
+// independent 32-key halves whose MFMA chains and softmax interleave.  The 4
+// waves share frame row i, so each (head, 64-key) tile of K and V^T is staged
+// once per workgroup in LDS, double-buffered; the next tile and the next
+// bias slice are fetched while the current block is consumed.
+//
+// Layouts: S^T D lane (n, hh) register u <-> key k0 + 16hh + u of query q0+n
+// (A rows = keys k0 + perm32(rho)); O^T = V^T P^T with P^T taken straight
+// from the softmax registers (k-step s, half hh, t <-> key k0 + 16hh + 8s + t),
+// D lane (n, hh) register u <-> d = 16hh + u; the epilogue feeds g*o back as
+// the B operand of update^T = Wo (g*o)^T.  LDS tiles are [32][32] bf16 with a
+// 96-byte row stride and an XOR swizzle of the 16-byte chunk index (bank
+// conflict free for the perm32 row pattern).
 // ---------------------------------------------------------------------------
+constexpr int TLD = 48;                 // LDS row stride (bf16) of a [32][32] tile
+constexpr int kTile = 32 * TLD;
+constexpr int kStage = 4 * kTile;       // K (2 halves) + V^T (2 halves)
+constexpr int kMaxN = 16384;
+constexpr float kRescaleSlack = 8.0f;   // log2 units
+
+__device__ __forceinline__ int t_off(int r, int chunk) { return r * TLD + ((chunk ^ (((r >> 2) ^ (r >> 4)) & 1)) << 3); }
+
 template <bool kStarting>
 __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
     TriAttBuffers buf, const bf16* __restrict__ wo, const bf16* zres, bf16* out, int N, int Np,
     int residual) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __shared__ __attribute__((aligned(16))) bf16 smem[2 * kStage];
+  __shared__ __attribute__((aligned(16))) bf16 kadd[kMaxN];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
   const int n = lane & 31, hh = lane >> 5;
   const int b = blockIdx.z, i = blockIdx.y;
   const int q0 = blockIdx.x * 128 + wave * 32;
-  if (q0 >= Np) return;  // no barriers in this kernel
+  const bool active = q0 < Np;          // idle waves still stage tiles and meet every barrier
+  const int qrow = active ? q0 + n : 0;
 
   const size_t frow = ((size_t)b * Np + i) * Np;
-  const size_t plane = (size_t)Np * Np;
-  const float qk_scale = 0.17677669529663687f * kLog2e;  // log2(e) / sqrt(32)
-  const float masked_logit = -1e6f * kLog2e;
+  const unsigned plane = (unsigned)Np * (unsigned)Np;
 
-  // Q^T fragments (B operand): lane (n, hh), step s: d = 16s + 8hh + t.
-  bf16x8 qf[H][2];
-  {
-    const bf16* qrow = buf.q + (frow + q0 + n) * C;
+  const bf16* __restrict__ kg = buf.k + frow * C;                           // [Np keys][C]
+  const bf16* __restrict__ vg = buf.vt + ((size_t)b * Np + i) * C * Np;     // [C][Np keys]
+  const bf16* __restrict__ bg = buf.bias + (size_t)b * H * plane;           // [H][Np][Np]
+  const bf16* __restrict__ qg = buf.q + frow * C;                           // [Np][C]
+  for (int t = tid; t < Np; t += kFlashThreads)
+    kadd[t] = f2bf(t >= N ? -INFINITY : (buf.mask[frow + t] ? 0.f : -1e30f));
+
+  // Staging of one (head, 64-key) tile: K is 64 rows x 4 chunks, V^T 32 rows x
+  // 8 chunks; thread tid moves K chunk tid and V^T chunk tid.
+  const int k_row = tid >> 2, k_chunk = tid & 3;
+  const int v_row = tid >> 3, v_chunk = tid & 7;
+  const unsigned k_off0 = (unsigned)k_row * C + k_chunk * 8;
+  const unsigned v_off0 = (unsigned)v_row * Np + v_chunk * 8;
+  const int k_lds = (k_row >> 5) * kTile + t_off(k_row & 31, k_chunk);
+  const int v_lds = 2 * kTile + (v_chunk >> 2) * kTile + t_off(v_row, v_chunk & 3);
+  bf16x8 rk, rv;
+  auto gload = [&](int hn, int kn) {
+    rk = load8(kg + k_off0 + (unsigned)kn * C + hn * DH);
+    rv = load8(vg + v_off0 + (unsigned)(hn * DH) * Np + kn);
+  };
+  auto lstore = [&](int st) {
+    store8(smem + st * kStage + k_lds, rk);
+    store8(smem + st * kStage + v_lds, rv);
+  };
+  // Bias slices in B-operand layout: lane (n, hh), half a, k-step s <-> keys
+  // k0 + 32a + 16s + 8hh + t.
+  const unsigned bias_lane = (unsigned)qrow * Np + 8 * hh;
+  auto bload = [&](int hn, int kn, bf16x8 (&bb)[4]) {
+    const bf16* p = bg + hn * plane + bias_lane + kn;
 #pragma unroll
-    for (int hd = 0; hd < H; ++hd)
+    for (int x = 0; x < 4; ++x) bb[x] = load8(p + 16 * x);
+  };
+
+  const int krow = perm32(n);
+  // One-hot fragments: A[rho][(s, hh, t)] = 1 iff perm32(rho) == 16s + 8hh + t.
+  bf16x8 ident[2], qone, zero8;
 #pragma unroll
-      for (int s = 0; s < 2; ++s) qf[hd][s] = load8(qrow + hd * DH + 16 * s + 8 * hh);
+  for (int t = 0; t < 8; ++t) {
+    ident[0][t] = f2bf(krow == 8 * hh + t ? 1.f : 0.f);
+    ident[1][t] = f2bf(krow == 16 + 8 * hh + t ? 1.f : 0.f);
+    qone[t] = f2bf(hh == 0 && t == 0 ? 1.f : 0.f);
+    zero8[t] = f2bf(0.f);
   }
 
-  f32x16 o[H];
-  float m[H], l[H];
-#pragma unroll
+  const int nk = Np / 64;
+  bf16x8 gob[2 * H];   // finished heads: o / l (bf16), gated in the epilogue
+  bf16x8 bcur[4], bnext[4];
+
+  gload(0, 0);
+  bload(0, 0, bcur);
+  lstore(0);
+  __syncthreads();
+  int st = 0;
+#pragma unroll 1
   for (int hd = 0; hd < H; ++hd) {
-    o[hd] = zero16();
-    m[hd] = -INFINITY;
-    l[hd] = 0.f;
-  }
-
-  const bf16* krow = buf.k + frow * C;
-  const bf16* vrow = buf.vt + ((size_t)b * Np + i) * C * Np;
-  const uint8_t* mrow = buf.mask + frow;
-
-  for (int k0 = 0; k0 < Np; k0 += 32) {
-    // Key mask of this lane's 16 keys k0 + 16hh + u.
-    const uint4 mk = *reinterpret_cast<const uint4*>(mrow + k0 + 16 * hh);
-    const uint32_t mw[4] = {mk.x, mk.y, mk.z, mk.w};
-    const int kslot = k0 + perm32(n);  // key row of this lane as an A operand
-#pragma unroll
-    for (int hd = 0; hd < H; ++hd) {
-      const bf16* kp = krow + (size_t)kslot * C + hd * DH + 8 * hh;
-      f32x16 s = zero16();
-      s = mfma32(load8(kp), qf[hd][0], s);
-      s = mfma32(load8(kp + 16), qf[hd][1], s);
-
-      const bf16* bp = buf.bias + ((size_t)b * H + hd) * plane + (size_t)(q0 + n) * Np + k0 + 16 * hh;
-      const bf16x8 b0 = load8(bp), b1 = load8(bp + 8);
-      float t[16];
-      float bmax = -INFINITY;
-#pragma unroll
-      for (int u = 0; u < 16; ++u) {
-        const float bv = bf2f(u < 8 ? b0[u] : b1[u - 8]);
-        float x = s[u] * qk_scale + bv * kLog2e;
-        const bool valid_key = ((mw[u >> 2] >> (8 * (u & 3))) & 0xff) != 0;
-        if (!valid_key) x = masked_logit;
-        if (k0 + 16 * hh + u >= N) x = -INFINITY;
-        t[u] = x;
-        bmax = fmaxf(bmax, x);
+    const bf16x8 qf0 = load8(qg + (unsigned)qrow * C + hd * DH + 8 * hh);
+    const bf16x8 qf1 = load8(qg + (unsigned)qrow * C + hd * DH + 16 + 8 * hh);
+    f32x16 o = zero16();
+    float m = -INFINITY, l = 0.f;
+#pragma unroll 1
+    for (int kb = 0; kb < nk; ++kb) {
+      const int k0 = kb * 64;
+      // next tile: (hd, kb + 1) or (hd + 1, 0); the very last iteration refetches itself
+      int hn = hd, kn = k0 + 64;
+      if (kn == Np) {
+        kn = 0;
+        hn = hd + 1 < H ? hd + 1 : hd;
+        if (hd + 1 == H) kn = k0;
       }
-      bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
-      const float m_new = fmaxf(m[hd], bmax);
-      const float alpha = fast_exp2(m[hd] - m_new);
-      m[hd] = m_new;
-      float psum = 0.f;
-      bf16x8 pb[2];
+      gload(hn, kn);
+      bload(hn, kn, bnext);
+      if (active) {
+        const bf16* ks = smem + st * kStage;
+        const bf16* vs = ks + 2 * kTile;
+        bf16x8 km0 = zero8, km1 = zero8;
+        if (hh == 0) {
+          km0[0] = kadd[k0 + krow];
+          km1[0] = kadd[k0 + 32 + krow];
+        }
+        f32x16 s0 = zero16(), s1 = zero16();
+        s0 = mfma32(load8(ks + t_off(krow, hh)), qf0, s0);
+        s1 = mfma32(load8(ks + kTile + t_off(krow, hh)), qf0, s1);
+        s0 = mfma32(load8(ks + t_off(krow, 2 + hh)), qf1, s0);
+        s1 = mfma32(load8(ks + kTile + t_off(krow, 2 + hh)), qf1, s1);
+        s0 = mfma32(ident[0], bcur[0], s0);
+        s1 = mfma32(ident[0], bcur[2], s1);
+        s0 = mfma32(ident[1], bcur[1], s0);
+        s1 = mfma32(ident[1], bcur[3], s1);
+        s0 = mfma32(km0, qone, s0);
+        s1 = mfma32(km1, qone, s1);
+        float bmax = fmaxf(s0[0], s1[0]);
 #pragma unroll
-      for (int u = 0; u < 16; ++u) {
-        const float p = fast_exp2(t[u] - m_new);
-        psum += p;
-        pb[u >> 3][u & 7] = f2bf(p);
+        for (int u = 1; u < 16; ++u) bmax = fmaxf(bmax, fmaxf(s0[u], s1[u]));
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+        if (__any(bmax > m + kRescaleSlack)) {
+          const float m_new = fmaxf(m, bmax);
+          const float alpha = fast_exp2(m - m_new);
+          m = m_new;
+          l *= alpha;
+#pragma unroll
+          for (int u = 0; u < 16; ++u) o[u] *= alpha;
+        }
+        float psum = 0.f;
+        bf16x8 pa[2], pb[2];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          const float p0 = fast_exp2(s0[u] - m);
+          const float p1 = fast_exp2(s1[u] - m);
+          psum += p0 + p1;
+          pa[u >> 3][u & 7] = f2bf(p0);
+          pb[u >> 3][u & 7] = f2bf(p1);
+        }
+        l += psum;
+        o = mfma32(load8(vs + t_off(krow, 2 * hh)), pa[0], o);
+        o = mfma32(load8(vs + t_off(krow, 2 * hh + 1)), pa[1], o);
+        o = mfma32(load8(vs + kTile + t_off(krow, 2 * hh)), pb[0], o);
+        o = mfma32(load8(vs + kTile + t_off(krow, 2 * hh + 1)), pb[1], o);
       }
-      l[hd] = l[hd] * alpha + psum;
+      lstore(st ^ 1);
 #pragma unroll
-      for (int u = 0; u < 16; ++u) o[hd][u] *= alpha;
-
-      const bf16* vp = vrow + (size_t)(hd * DH + perm32(n)) * Np + k0 + 16 * hh;
-      o[hd] = mfma32(load8(vp), pb[0], o[hd]);
-      o[hd] = mfma32(load8(vp + 8), pb[1], o[hd]);
+      for (int x = 0; x < 4; ++x) bcur[x] = bnext[x];
+      st ^= 1;
+      __syncthreads();
     }
+    // head finished: normalise and pack
+    const float inv = 1.0f / (l + __shfl_xor(l, 32));
+    bf16x8 r0, r1;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      r0[u] = f2bf(o[u] * inv);
+      r1[u] = f2bf(o[8 + u] * inv);
+    }
+#pragma unroll
+    for (int h2 = 0; h2 < H; ++h2)
+      if (h2 == hd) {
+        gob[2 * h2] = r0;
+        gob[2 * h2 + 1] = r1;
+      }
   }
+  if (!active) return;
 
-  // Epilogue: normalise, gate, output projection, residual.
-  bf16x8 gob[8];
+  // Gate: g * (o / l) per head, as the out-projection's B operand.
   {
-    const bf16* grow = buf.g + (frow + q0 + n) * C;
+    const bf16* grow = buf.g + (frow + q0 + n) * C + 16 * hh;
 #pragma unroll
     for (int hd = 0; hd < H; ++hd) {
-      const float lt = l[hd] + __shfl_xor(l[hd], 32);
-      const float inv = 1.0f / lt;
-      const bf16x8 g0 = load8(grow + hd * DH + 16 * hh);
-      const bf16x8 g1 = load8(grow + hd * DH + 16 * hh + 8);
+      const bf16x8 g0 = load8(grow + hd * DH), g1 = load8(grow + hd * DH + 8);
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        gob[2 * hd][u] = f2bf(bf2f(g0[u]) * (o[hd][u] * inv));
-        gob[2 * hd + 1][u] = f2bf(bf2f(g1[u]) * (o[hd][8 + u] * inv));
+        gob[2 * hd][u] = f2bf(bf2f(g0[u]) * bf2f(gob[2 * hd][u]));
+        gob[2 * hd + 1][u] = f2bf(bf2f(g1[u]) * bf2f(gob[2 * hd + 1][u]));
       }
     }
   }
+
+  // update^T = Wo (g*o)^T, residual add, store in z's frame.
   const int q = q0 + n;
   const bool store = q < N;
   const size_t zpair = kStarting ? ((size_t)b * N + i) * N + q : ((size_t)b * N + q) * N + i;
@@ -280,7 +381,7 @@ __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
 
 using namespace bioemu;
 
-static size_t triatt_np(int64_t N) { return (size_t)round_up(N, 32); }
+static size_t triatt_np(int64_t N) { return (size_t)round_up(N, 64); }
 
 extern "C" size_t bioemu_triatt_workspace_bytes(int64_t B, int64_t N, int64_t Dc, int64_t Hc) {
   if (B <= 0 || N <= 0 || Dc != C || Hc != H) return 0;
