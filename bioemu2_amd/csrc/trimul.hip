@@ -12,208 +12,183 @@
 // Padded planes (Np = N rounded up to 128) are zero in every padded row and
 // column, so the contraction needs no edge handling and padding never changes
 // a valid output bit.
+#include <algorithm>
+
 #include "common.h"
 #include "internal.h"
+#include "pairtile.h"
 
 namespace bioemu {
 namespace {
 
-constexpr int D = 128;           // pair channels (c_z)
-constexpr int LDX = D + 8;       // LDS row stride (bf16) of a pair tile
-constexpr int kThreads = 256;    // 4 waves
-constexpr int kTilePairs = 256;  // pairs per workgroup: 4 frame rows x 64 frame columns
+constexpr int D = 128;               // pair channels (c_z)
 
 // ---------------------------------------------------------------------------
 // Stage 1: LN_in + gated input projection + mask, channel-major output.
-// Frame tile: rows i0..i0+3 (one per wave) x columns k0..k0+63.
-// Outgoing reads x[i][k]; incoming reads x[k][i] (frame = transpose).
+//
+// Tile = (b, frame row i, 32 frame columns); frame (i, k) is x[i][k]
+// (outgoing) or x[k][i] (incoming).  The LayerNorm'd tile stays in registers
+// as MFMA operands (pairtile.h); p_in and g_in (512 x 128) sit in LDS for the
+// whole persistent workgroup.  A masked pair's LayerNorm row is zeroed before
+// the bias-free projections, so its p is exactly 0 and so is p * sigmoid(g):
+// the masked_fill of the reference (triangle_multiplication.py:93).  Rows and
+// columns in [N, Np) come out zero, which the padded contraction relies on.
+// Output: a and b as channel-major planes [B][D][Np][Np] (k contiguous).
 // ---------------------------------------------------------------------------
+constexpr int kInThreads = 512;
+constexpr int kInRows = 4 * D;                 // p_in (2D rows) then g_in (2D rows)
+constexpr int kInSmem = kInRows * kLdw * 2;
+
 template <bool kOutgoing>
-__global__ __launch_bounds__(kThreads) void trimul_proj_in_kernel(
+__global__ __launch_bounds__(kInThreads) void trimul_proj_in_kernel(
     const bf16* __restrict__ x, const uint8_t* __restrict__ mask, const float* __restrict__ ln_w,
     const float* __restrict__ ln_b, const bf16* __restrict__ p_w, const bf16* __restrict__ g_w,
     bf16* __restrict__ ab, int B, int N, int Np) {
-  __shared__ __attribute__((aligned(16))) bf16 xt[kTilePairs * LDX];
-  __shared__ uint8_t mk[kTilePairs];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int ln = lane & 31, lh = lane >> 5;
-  const int b = blockIdx.z;
-  const int i0 = blockIdx.y * 4;
-  const int k0 = blockIdx.x * 64;
-  const size_t pair_base = (size_t)b * N * N;
-
-  // Coalesced tile load: 16 threads per pair (16 B each).  Outgoing walks the
-  // 64 frame columns of one x row (16 KB contiguous); incoming walks the 4
-  // frame rows, which are 4 consecutive pairs of one x row (1 KB contiguous).
-#pragma unroll 4
-  for (int it = 0; it < 16; ++it) {
-    const int q = it * kThreads + tid;
-    const int part = q & 15;
-    int w, kk;
-    if (kOutgoing) {
-      kk = (q >> 4) & 63;
-      w = q >> 10;
-    } else {
-      w = (q >> 4) & 3;
-      kk = q >> 6;
-    }
-    const int i = i0 + w, k = k0 + kk;
-    bf16x8 v;
-#pragma unroll
-    for (int t = 0; t < 8; ++t) v[t] = f2bf(0.f);
-    if (i < N && k < N) {
-      const int r = kOutgoing ? i : k, c = kOutgoing ? k : i;
-      v = load8(x + (pair_base + (size_t)r * N + c) * D + part * 8);
-    }
-    store8(xt + (w * 64 + kk) * LDX + part * 8, v);
-  }
-  {
-    const int w = tid >> 6, kk = tid & 63;
-    const int i = i0 + w, k = k0 + kk;
-    uint8_t valid = 0;
-    if (i < N && k < N) {
-      const int r = kOutgoing ? i : k, c = kOutgoing ? k : i;
-      valid = mask[pair_base + (size_t)r * N + c] != 0;
-    }
-    mk[tid] = valid;
-  }
-  __syncthreads();
-  layernorm_row_lds<D>(xt + tid * LDX, ln_w, ln_b, 1e-5f);
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  bf16* wl = reinterpret_cast<bf16*>(smem);
+  stage_weights(wl, p_w, 2 * D, 2 * D);
+  stage_weights(wl + 2 * D * kLdw, g_w, 2 * D, 2 * D);
   __syncthreads();
 
-  // MFMA: rows = this wave's 64 pairs (2 blocks of 32), cols = 32 channels.
-  bf16x8 afr[2][D / 16];
-#pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-    for (int s = 0; s < D / 16; ++s)
-      afr[rb][s] = load8(xt + (wave * 64 + rb * 32 + ln) * LDX + s * 16 + lh * 8);
-
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rho = lane & 31, h = lane >> 5;
+  const int waves = blockDim.x >> 6;
+  const int tiles_per_row = Np / 32;
+  const long long ntiles = (long long)B * Np * tiles_per_row;
   const size_t plane = (size_t)Np * Np;
-  for (int which = 0; which < 2; ++which) {
-    for (int cc = 0; cc < D / 32; ++cc) {
-      const int wrow = which * D + cc * 32 + ln;
-      bf16x8 bp[D / 16], bg[D / 16];
+
+  for (long long t = (long long)blockIdx.x * waves + wave; t < ntiles; t += (long long)gridDim.x * waves) {
+    const int kt = (int)(t % tiles_per_row);
+    const int i = (int)((t / tiles_per_row) % Np);
+    const int b = (int)(t / ((long long)tiles_per_row * Np));
+    const int k0 = kt * 32;
+    const int kk = k0 + perm32(rho);
+    const bool inb = i < N && kk < N;
+    const size_t pair = kOutgoing ? ((size_t)b * N + i) * N + kk : ((size_t)b * N + kk) * N + i;
+    const bool keep = inb && mask[inb ? pair : 0] != 0;
+    bf16x8 raw[8], xf[8];
+    load_half_row(x + (inb ? pair : 0) * D, h, inb, raw);
+    layernorm_half_row(raw, ln_w, ln_b, h, 1e-5f, xf);
+    if (!keep) {
 #pragma unroll
-      for (int s = 0; s < D / 16; ++s) {
-        bp[s] = load8(p_w + (size_t)wrow * D + s * 16 + lh * 8);
-        bg[s] = load8(g_w + (size_t)wrow * D + s * 16 + lh * 8);
-      }
-      const int ch = cc * 32 + ln;
-      bf16* dst_plane = ab + ((size_t)(which * B + b) * D + ch) * plane + (size_t)(i0 + wave) * Np + k0;
+      for (int s = 0; s < 8; ++s) xf[s] = bf16x8{};
+    }
+#pragma unroll 1
+    for (int blk = 0; blk < 8; ++blk) {   // a: blk 0..3, b: blk 4..7 (32 channels each)
+      const f32x16 pa = proj_block_cm(xf, wl, blk * 32, rho, h);
+      const f32x16 ga = proj_block_cm(xf, wl, 2 * D + blk * 32, rho, h);
+      float v[16];
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb) {
-        f32x16 accp = zero16(), accg = zero16();
-#pragma unroll
-        for (int s = 0; s < D / 16; ++s) {
-          accp = mfma32(afr[rb][s], bp[s], accp);
-          accg = mfma32(afr[rb][s], bg[s], accg);
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float o[4];
-#pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            const int kk = rb * 32 + 8 * r + 4 * lh + c;
-            const float v = accp[4 * r + c] * sigmoidf_fast(accg[4 * r + c]);
-            o[c] = mk[wave * 64 + kk] ? v : 0.f;  // masked_fill semantics (select, not multiply)
-          }
-          *reinterpret_cast<bf16x4*>(dst_plane + rb * 32 + 8 * r + 4 * lh) = pack4(o[0], o[1], o[2], o[3]);
-        }
-      }
+      for (int u = 0; u < 16; ++u) v[u] = pa[u] * sigmoidf_fast(ga[u]);
+      const int which = blk >> 2, ch = (blk & 3) * 32 + rho;
+      store16(ab + ((size_t)(which * B + b) * D + ch) * plane + (size_t)i * Np + k0 + 16 * h, v);
     }
   }
 }
 
 // ---------------------------------------------------------------------------
-// Stage 3: LN_out(o) -> p_out, LN_in(x) -> g_out, out = p * sigmoid(g) (+ x).
-// Output tile: rows i0..i0+3 (one per wave) x columns j0..j0+63, channel-last.
+// Stage 3: out = p_out(LN_out(o)) * sigmoid(g_out(LN_in(x)))  (+ x).
+//
+// Tile = (b, row i, 32 columns j).  o is channel-major (the contraction's
+// output planes), so each lane gathers its pair's 64-channel half with 2-byte
+// loads (the 32 lanes of a half read 64 contiguous bytes per channel); x is
+// pair-major.  Both LayerNorms run in registers; p_out / g_out (2 x 128 x 128)
+// sit in LDS.  The result comes out pair-major (16 consecutive channels per
+// lane) and is stored with the residual add fused.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kThreads) void trimul_out_kernel(
+constexpr int kOutThreads = 512;
+constexpr int kOutSmem = 2 * D * kLdw * 2;
+
+__global__ __launch_bounds__(kOutThreads) void trimul_out_kernel(
     const bf16* __restrict__ o, const bf16* x, const float* __restrict__ ln_in_w,
     const float* __restrict__ ln_in_b, const float* __restrict__ ln_out_w,
     const float* __restrict__ ln_out_b, const bf16* __restrict__ p_w, const bf16* __restrict__ g_w,
-    bf16* out, int N, int Np, int residual) {
+    bf16* out, int B, int N, int Np, int residual) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  bf16* ot = reinterpret_cast<bf16*>(smem);  // [256][LDX] contraction result, pair-major
-  bf16* xt = ot + kTilePairs * LDX;          // [256][LDX] x tile
+  bf16* wl = reinterpret_cast<bf16*>(smem);
+  stage_weights(wl, p_w, D, D);
+  stage_weights(wl + D * kLdw, g_w, D, D);
+  __syncthreads();
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int ln = lane & 31, lh = lane >> 5;
-  const int b = blockIdx.z;
-  const int i0 = blockIdx.y * 4;
-  const int j0 = blockIdx.x * 64;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rho = lane & 31, h = lane >> 5;
+  const int waves = blockDim.x >> 6;
+  const int tiles_per_row = (N + 31) / 32;
+  const long long ntiles = (long long)B * N * tiles_per_row;
   const size_t plane = (size_t)Np * Np;
-  const size_t pair_base = (size_t)b * N * N;
 
-  // o planes are channel-major: read 128-byte row pieces, transpose into LDS.
-#pragma unroll 4
-  for (int it = 0; it < 16; ++it) {
-    const int q = it * kThreads + tid;
-    const int part = q & 7, w = (q >> 3) & 3, d = q >> 5;
-    const bf16x8 v = load8(o + ((size_t)b * D + d) * plane + (size_t)(i0 + w) * Np + j0 + part * 8);
-#pragma unroll
-    for (int t = 0; t < 8; ++t) ot[(w * 64 + part * 8 + t) * LDX + d] = v[t];
-  }
-#pragma unroll 4
-  for (int it = 0; it < 16; ++it) {
-    const int q = it * kThreads + tid;
-    const int part = q & 15, jj = (q >> 4) & 63, w = q >> 10;
-    const int i = i0 + w, j = j0 + jj;
-    bf16x8 v;
-#pragma unroll
-    for (int t = 0; t < 8; ++t) v[t] = f2bf(0.f);
-    if (i < N && j < N) v = load8(x + (pair_base + (size_t)i * N + j) * D + part * 8);
-    store8(xt + (w * 64 + jj) * LDX + part * 8, v);
-  }
-  __syncthreads();
-  layernorm_row_lds<D>(ot + tid * LDX, ln_out_w, ln_out_b, 1e-5f);
-  layernorm_row_lds<D>(xt + tid * LDX, ln_in_w, ln_in_b, 1e-5f);
-  __syncthreads();
+  for (long long t = (long long)blockIdx.x * waves + wave; t < ntiles; t += (long long)gridDim.x * waves) {
+    const int jt = (int)(t % tiles_per_row);
+    const int i = (int)((t / tiles_per_row) % N);
+    const int b = (int)(t / ((long long)tiles_per_row * N));
+    const int jj = jt * 32 + perm32(rho);
+    const bool valid = jj < N;
 
-  const int i = i0 + wave;
-  for (int cc = 0; cc < D / 32; ++cc) {
-    bf16x8 ap[D / 16], ag[D / 16];
+    // LN_in(x) first (its 32 packed registers stay live), then o.
+    const size_t pair = ((size_t)b * N + i) * N + (valid ? jj : 0);
+    bf16x8 xraw[8], xf[8];
+    load_half_row(x + pair * D, h, valid, xraw);
+    layernorm_half_row(xraw, ln_in_w, ln_in_b, h, 1e-5f, xf);
+    asm volatile("" ::: "memory");  // finish LN_in before the o gather is scheduled
+
+    // o gather: channels 64h + 8s + e of pair (i, jj), jj < Np always.  One
+    // buffer resource per batch, the lane's plane offset in a VGPR and the
+    // channel's plane offset in an SGPR, so the 64 loads share one address;
+    // each 16-bit result is widened to fp32 in place for the LayerNorm.
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<bf16*>(o + (size_t)b * D * plane), (short)0, (int)(D * plane * 2), 0x00020000);
+    const unsigned voff = (unsigned)((64 * h * plane + (size_t)i * Np + jj) * 2);
+    float v[64];
 #pragma unroll
-    for (int s = 0; s < D / 16; ++s) {
-      ap[s] = load8(p_w + (size_t)(cc * 32 + ln) * D + s * 16 + lh * 8);
-      ag[s] = load8(g_w + (size_t)(cc * 32 + ln) * D + s * 16 + lh * 8);
+    for (int c = 0; c < 64; ++c) {
+      const unsigned short r =
+          (unsigned short)__builtin_amdgcn_raw_buffer_load_b16(rsrc, voff, (unsigned)(c * plane * 2), 0);
+      v[c] = __uint_as_float((unsigned)r << 16);
     }
+    bf16x8 of[8];
+    {
+      float sum = 0.f;
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
-      const int prow = wave * 64 + cb * 32 + ln;
-      f32x16 accp = zero16(), accg = zero16();
+      for (int c = 0; c < 64; ++c) sum += v[c];
+      sum += __shfl_xor(sum, 32);
+      const float mean = sum * (1.0f / D);
+      float ss = 0.f;
 #pragma unroll
-      for (int s = 0; s < D / 16; ++s) {
-        accp = mfma32(ap[s], load8(ot + prow * LDX + s * 16 + lh * 8), accp);
-        accg = mfma32(ag[s], load8(xt + prow * LDX + s * 16 + lh * 8), accg);
+      for (int c = 0; c < 64; ++c) {
+        const float d = v[c] - mean;
+        ss += d * d;
       }
-      const int j = j0 + cb * 32 + ln;
-      if (i < N && j < N) {
-        bf16* dst = out + (pair_base + (size_t)i * N + j) * D + cc * 32;
-        const bf16* res = x + (pair_base + (size_t)i * N + j) * D + cc * 32;
+      ss += __shfl_xor(ss, 32);
+      const float rstd = rsqrtf(ss * (1.0f / D) + 1e-5f);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float v[4];
+      for (int c = 0; c < 64; ++c) {
+        const int ch = 64 * h + c;
+        of[c >> 3][c & 7] = f2bf((v[c] - mean) * rstd * ln_out_w[ch] + ln_out_b[ch]);
+      }
+    }
+
+#pragma unroll 1
+    for (int cb = 0; cb < 4; ++cb) {
+      const f32x16 pa = proj_block_pm(of, wl, cb * 32, rho, h);
+      const f32x16 ga = proj_block_pm(xf, wl, D + cb * 32, rho, h);
+      if (valid) {
+        const size_t off = pair * D + cb * 32 + 16 * h;
+        float v[16];
 #pragma unroll
-          for (int c = 0; c < 4; ++c) v[c] = accp[4 * r + c] * sigmoidf_fast(accg[4 * r + c]);
-          const int ch = 8 * r + 4 * lh;
-          if (residual) {
-            const bf16x4 xr = *reinterpret_cast<const bf16x4*>(res + ch);
+        for (int u = 0; u < 16; ++u) v[u] = pa[u] * sigmoidf_fast(ga[u]);
+        if (residual) {
+          const bf16x8 r0 = load8(x + off), r1 = load8(x + off + 8);
 #pragma unroll
-            for (int c = 0; c < 4; ++c) v[c] += bf2f(xr[c]);
+          for (int u = 0; u < 8; ++u) {
+            v[u] += bf2f(r0[u]);
+            v[8 + u] += bf2f(r1[u]);
           }
-          *reinterpret_cast<bf16x4*>(dst + ch) = pack4(v[0], v[1], v[2], v[3]);
         }
+        store16(out + off, v);
       }
     }
   }
 }
-
-constexpr int kOutSmem = 2 * kTilePairs * LDX * 2;
 
 }  // namespace
 }  // namespace bioemu
@@ -238,6 +213,9 @@ extern "C" int bioemu_trimul_fwd(const void* x, const uint8_t* mask, const float
   if (!x || !mask || !norm_in_w || !norm_in_b || !p_in_w || !g_in_w || !norm_out_w || !norm_out_b ||
       !p_out_w || !g_out_w || !out || !workspace)
     return set_error(BIOEMU_ERR_INVALID_ARG, "trimul: null pointer argument");
+  if (round_up(N, kGemmTile) * round_up(N, kGemmTile) * Dc * 2 >= (int64_t)1 << 31)
+    return set_error(BIOEMU_ERR_UNSUPPORTED, "trimul: N=%lld too large (contraction planes must stay below 2 GiB per batch)",
+                     (long long)N);
   if (!aligned16(x) || !aligned16(out) || !aligned16(p_in_w) || !aligned16(g_in_w) ||
       !aligned16(p_out_w) || !aligned16(g_out_w) || !aligned16(workspace))
     return set_error(BIOEMU_ERR_INVALID_ARG, "trimul: x/out/weights/workspace must be 16-byte aligned");
@@ -252,34 +230,39 @@ extern "C" int bioemu_trimul_fwd(const void* x, const uint8_t* mask, const float
   bf16* ab = static_cast<bf16*>(workspace);
   bf16* ob = ab + 2 * plane_elems;
 
-  dim3 g1((unsigned)(Np / 64), (unsigned)(Np / 4), (unsigned)B);
+  int dev = 0, cus = 0;
+  (void)hipGetDevice(&dev);
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+  const void* kin = outgoing ? reinterpret_cast<const void*>(trimul_proj_in_kernel<true>)
+                             : reinterpret_cast<const void*>(trimul_proj_in_kernel<false>);
+  if (hipFuncSetAttribute(kin, hipFuncAttributeMaxDynamicSharedMemorySize, kInSmem) != hipSuccess ||
+      hipFuncSetAttribute(reinterpret_cast<const void*>(trimul_out_kernel),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, kOutSmem) != hipSuccess)
+    return set_error(BIOEMU_ERR_LAUNCH, "trimul: cannot set dynamic LDS size");
+  const long long waves_in = (long long)B * Np * (Np / 32);
+  const unsigned grid1 = (unsigned)std::min<long long>(cus, (waves_in + 7) / 8);
   {
-  KernelTimerScope timed("trimul_proj_in", stream);
-  if (outgoing) {
-    hipLaunchKernelGGL(trimul_proj_in_kernel<true>, g1, dim3(kThreads), 0, stream,
-                       static_cast<const bf16*>(x), mask, norm_in_w, norm_in_b,
-                       static_cast<const bf16*>(p_in_w), static_cast<const bf16*>(g_in_w), ab, (int)B,
-                       (int)N, (int)Np);
-  } else {
-    hipLaunchKernelGGL(trimul_proj_in_kernel<false>, g1, dim3(kThreads), 0, stream,
-                       static_cast<const bf16*>(x), mask, norm_in_w, norm_in_b,
-                       static_cast<const bf16*>(p_in_w), static_cast<const bf16*>(g_in_w), ab, (int)B,
-                       (int)N, (int)Np);
-  }
+    KernelTimerScope timed("trimul_proj_in", stream);
+    if (outgoing)
+      hipLaunchKernelGGL(trimul_proj_in_kernel<true>, dim3(grid1), dim3(kInThreads), kInSmem, stream,
+                         static_cast<const bf16*>(x), mask, norm_in_w, norm_in_b, static_cast<const bf16*>(p_in_w),
+                         static_cast<const bf16*>(g_in_w), ab, (int)B, (int)N, (int)Np);
+    else
+      hipLaunchKernelGGL(trimul_proj_in_kernel<false>, dim3(grid1), dim3(kInThreads), kInSmem, stream,
+                         static_cast<const bf16*>(x), mask, norm_in_w, norm_in_b, static_cast<const bf16*>(p_in_w),
+                         static_cast<const bf16*>(g_in_w), ab, (int)B, (int)N, (int)Np);
   }
   int rc = check_launch("trimul_proj_in");
   if (rc) return rc;
   rc = launch_bgemm_nt(ab, ab + plane_elems, ob, B * D, Np, stream);
   if (rc) return rc;
 
-  if (hipFuncSetAttribute(reinterpret_cast<const void*>(trimul_out_kernel),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, kOutSmem) != hipSuccess)
-    return set_error(BIOEMU_ERR_LAUNCH, "trimul_out: cannot set dynamic LDS size");
-  dim3 g3((unsigned)((N + 63) / 64), (unsigned)((N + 3) / 4), (unsigned)B);
+  const long long waves_out = (long long)B * N * ((N + 31) / 32);
+  const unsigned grid3 = (unsigned)std::min<long long>(2LL * cus, (waves_out + 7) / 8);
   KernelTimerScope timed("trimul_out", stream);
-  hipLaunchKernelGGL(trimul_out_kernel, g3, dim3(kThreads), kOutSmem, stream, ob,
+  hipLaunchKernelGGL(trimul_out_kernel, dim3(grid3), dim3(kOutThreads), kOutSmem, stream, ob,
                      static_cast<const bf16*>(x), norm_in_w, norm_in_b, norm_out_w, norm_out_b,
                      static_cast<const bf16*>(p_out_w), static_cast<const bf16*>(g_out_w),
-                     static_cast<bf16*>(out), (int)N, (int)Np, residual);
+                     static_cast<bf16*>(out), (int)B, (int)N, (int)Np, residual);
   return check_launch("trimul_out");
 }
