@@ -36,7 +36,7 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 // Batched bf16 "NT" GEMM: C[z][i][j] = sum_k A[z][i][k] * B[z][j][k] for
 // z < batch, with M = N = K = n (a multiple of kGemmTile) and bf16 output.
-constexpr int kGemmTile = 128;
+constexpr int kGemmTile = 256;
 int launch_bgemm_nt(const void* A, const void* B, void* C, int64_t batch, int64_t n,
                     hipStream_t stream);
 
