@@ -179,14 +179,25 @@ __device__ __forceinline__ int t_off(int r, int chunk) { return r * TLD + ((chun
 template <bool kStarting>
 __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
     TriAttBuffers buf, const bf16* __restrict__ wo, const bf16* zres, bf16* out, int N, int Np,
-    int residual) {
+    int residual, int nitems) {
   __shared__ __attribute__((aligned(16))) bf16 smem[2 * kStage];
   __shared__ __attribute__((aligned(16))) bf16 kadd[kMaxN];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int n = lane & 31, hh = lane >> 5;
-  const int b = blockIdx.z, i = blockIdx.y;
-  const int q0 = blockIdx.x * 128 + wave * 32;
+  // XCD-aware mapping: workgroup w runs on XCD w % 8.  Work items are
+  // (b, row i, query block) with the query block fastest; each XCD gets a
+  // contiguous range, so the query blocks of one row (which read the same K
+  // and V) share an L2.
+  const int nq = (Np + 127) / 128;
+  const int total = gridDim.x;  // = padded item count, a multiple of 8
+  const int per_xcd = total / 8;
+  const int item = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (item >= nitems) return;   // before any barrier: the whole workgroup leaves
+  const int qb = item % nq;
+  const int i = (item / nq) % N;
+  const int b = item / (nq * N);
+  const int q0 = qb * 128 + wave * 32;
   const bool active = q0 < Np;          // idle waves still stage tiles and meet every barrier
   const int qrow = active ? q0 + n : 0;
 
@@ -451,17 +462,19 @@ extern "C" int bioemu_triatt_fwd(const void* z, const uint8_t* mask, const float
   int rc = check_launch("triatt_proj");
   if (rc) return rc;
 
-  dim3 g2((unsigned)((Np + 127) / 128), (unsigned)N, (unsigned)B);
+  const long long nitems = (long long)B * N * ((Np + 127) / 128);
+  const long long grid2 = (nitems + 7) / 8 * 8;
+  if (grid2 > 0x7fffffffLL) return set_error(BIOEMU_ERR_INVALID_ARG, "triatt: too many work items");
   {
     KernelTimerScope timed("triatt_flash", stream);
     if (starting)
-      hipLaunchKernelGGL(triatt_flash_kernel<true>, g2, dim3(kFlashThreads), 0, stream, buf,
+      hipLaunchKernelGGL(triatt_flash_kernel<true>, dim3((unsigned)grid2), dim3(kFlashThreads), 0, stream, buf,
                          static_cast<const bf16*>(w_o), static_cast<const bf16*>(z), static_cast<bf16*>(out),
-                         (int)N, (int)Np, residual);
+                         (int)N, (int)Np, residual, (int)nitems);
     else
-      hipLaunchKernelGGL(triatt_flash_kernel<false>, g2, dim3(kFlashThreads), 0, stream, buf,
+      hipLaunchKernelGGL(triatt_flash_kernel<false>, dim3((unsigned)grid2), dim3(kFlashThreads), 0, stream, buf,
                          static_cast<const bf16*>(w_o), static_cast<const bf16*>(z), static_cast<bf16*>(out),
-                         (int)N, (int)Np, residual);
+                         (int)N, (int)Np, residual, (int)nitems);
   }
   return check_launch("triatt_flash");
 }
