@@ -171,7 +171,6 @@ __global__ __launch_bounds__(kProjThreads) void triatt_proj_kernel(
 constexpr int TLD = 48;                 // LDS row stride (bf16) of a [32][32] tile
 constexpr int kTile = 32 * TLD;
 constexpr int kStage = 4 * kTile;       // K (2 halves) + V^T (2 halves)
-constexpr int kMaxN = 16384;
 constexpr float kRescaleSlack = 8.0f;   // log2 units
 
 __device__ __forceinline__ int t_off(int r, int chunk) { return r * TLD + ((chunk ^ (((r >> 2) ^ (r >> 4)) & 1)) << 3); }
@@ -181,7 +180,7 @@ __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
     TriAttBuffers buf, const bf16* __restrict__ wo, const bf16* zres, bf16* out, int N, int Np,
     int residual, int nitems) {
   __shared__ __attribute__((aligned(16))) bf16 smem[2 * kStage];
-  __shared__ __attribute__((aligned(16))) bf16 kadd[kMaxN];
+  extern __shared__ __attribute__((aligned(16))) bf16 kadd[];   // [Np] additive key mask
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int n = lane & 31, hh = lane >> 5;
@@ -263,8 +262,8 @@ __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
     const bf16x8 qf1 = load8(qg + (unsigned)qrow * C + hd * DH + 16 + 8 * hh);
     f32x16 o = zero16();
     float m = -INFINITY, l = 0.f;
-#pragma unroll 1
-    for (int kb = 0; kb < nk; ++kb) {
+    // One 64-key block: fetch the next tile, consume the current one.
+    auto block = [&](int kb, const bf16x8 (&bc)[4], bf16x8 (&bn)[4]) {
       const int k0 = kb * 64;
       // next tile: (hd, kb + 1) or (hd + 1, 0); the very last iteration refetches itself
       int hn = hd, kn = k0 + 64;
@@ -274,7 +273,7 @@ __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
         if (hd + 1 == H) kn = k0;
       }
       gload(hn, kn);
-      bload(hn, kn, bnext);
+      bload(hn, kn, bn);
       if (active) {
         const bf16* ks = smem + st * kStage;
         const bf16* vs = ks + 2 * kTile;
@@ -288,15 +287,15 @@ __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
         s1 = mfma32(load8(ks + kTile + t_off(krow, hh)), qf0, s1);
         s0 = mfma32(load8(ks + t_off(krow, 2 + hh)), qf1, s0);
         s1 = mfma32(load8(ks + kTile + t_off(krow, 2 + hh)), qf1, s1);
-        s0 = mfma32(ident[0], bcur[0], s0);
-        s1 = mfma32(ident[0], bcur[2], s1);
-        s0 = mfma32(ident[1], bcur[1], s0);
-        s1 = mfma32(ident[1], bcur[3], s1);
+        s0 = mfma32(ident[0], bc[0], s0);
+        s1 = mfma32(ident[0], bc[2], s1);
+        s0 = mfma32(ident[1], bc[1], s0);
+        s1 = mfma32(ident[1], bc[3], s1);
         s0 = mfma32(km0, qone, s0);
         s1 = mfma32(km1, qone, s1);
         float bmax = fmaxf(s0[0], s1[0]);
 #pragma unroll
-        for (int u = 1; u < 16; ++u) bmax = fmaxf(bmax, fmaxf(s0[u], s1[u]));
+        for (int u = 1; u < 16; ++u) bmax = __builtin_fmaxf(bmax, __builtin_fmaxf(s0[u], s1[u]));
         bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
         if (__any(bmax > m + kRescaleSlack)) {
           const float m_new = fmaxf(m, bmax);
@@ -323,10 +322,21 @@ __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
         o = mfma32(load8(vs + kTile + t_off(krow, 2 * hh + 1)), pb[1], o);
       }
       lstore(st ^ 1);
-#pragma unroll
-      for (int x = 0; x < 4; ++x) bcur[x] = bnext[x];
       st ^= 1;
       __syncthreads();
+    };
+    // Two blocks per trip with the bias registers ping-ponged (no copies).
+    // nk is even for every head but the fetch chain crosses heads, so the
+    // roles of bcur / bnext alternate on a global parity.
+    int kb = 0;
+    for (; kb + 1 < nk; kb += 2) {
+      block(kb, bcur, bnext);
+      block(kb + 1, bnext, bcur);
+    }
+    if (kb < nk) {
+      block(kb, bcur, bnext);
+#pragma unroll
+      for (int x = 0; x < 4; ++x) bcur[x] = bnext[x];
     }
     // head finished: normalise and pack
     const float inv = 1.0f / (l + __shfl_xor(l, 32));
@@ -463,16 +473,21 @@ extern "C" int bioemu_triatt_fwd(const void* z, const uint8_t* mask, const float
   if (rc) return rc;
 
   const long long nitems = (long long)B * N * ((Np + 127) / 128);
+  const size_t flash_smem = (size_t)Np * 2;   // additive key mask row
+  const void* kflash = starting ? reinterpret_cast<const void*>(triatt_flash_kernel<true>)
+                                : reinterpret_cast<const void*>(triatt_flash_kernel<false>);
+  if (hipFuncSetAttribute(kflash, hipFuncAttributeMaxDynamicSharedMemorySize, (int)flash_smem) != hipSuccess)
+    return set_error(BIOEMU_ERR_LAUNCH, "triatt_flash: cannot set dynamic LDS size");
   const long long grid2 = (nitems + 7) / 8 * 8;
   if (grid2 > 0x7fffffffLL) return set_error(BIOEMU_ERR_INVALID_ARG, "triatt: too many work items");
   {
     KernelTimerScope timed("triatt_flash", stream);
     if (starting)
-      hipLaunchKernelGGL(triatt_flash_kernel<true>, dim3((unsigned)grid2), dim3(kFlashThreads), 0, stream, buf,
+      hipLaunchKernelGGL(triatt_flash_kernel<true>, dim3((unsigned)grid2), dim3(kFlashThreads), flash_smem, stream, buf,
                          static_cast<const bf16*>(w_o), static_cast<const bf16*>(z), static_cast<bf16*>(out),
                          (int)N, (int)Np, residual, (int)nitems);
     else
-      hipLaunchKernelGGL(triatt_flash_kernel<false>, dim3((unsigned)grid2), dim3(kFlashThreads), 0, stream, buf,
+      hipLaunchKernelGGL(triatt_flash_kernel<false>, dim3((unsigned)grid2), dim3(kFlashThreads), flash_smem, stream, buf,
                          static_cast<const bf16*>(w_o), static_cast<const bf16*>(z), static_cast<bf16*>(out),
                          (int)N, (int)Np, residual, (int)nitems);
   }
