@@ -26,14 +26,16 @@ namespace {
 constexpr int CZ = 128;
 constexpr int kBiasThreads = 256;
 
-// bias[b][h][i][j] = LN(z[b][i][j]) . Wz[h] for i, j < Np (zero pair rows outside [0, N)).
+// bias[b][h][i][j] = LN(z[b][i][j]) . Wz[h] for i, j < Np (zero pair rows outside [0, N)),
+// with the LayerNorm folded into Wz (wf, cf from launch_fold_ln).
 __global__ __launch_bounds__(kBiasThreads) void pair_bias_kernel(const bf16* __restrict__ z,
-                                                                 const float* __restrict__ ln_w,
-                                                                 const float* __restrict__ ln_b,
-                                                                 const bf16* __restrict__ wz, bf16* __restrict__ bias,
+                                                                 const bf16* __restrict__ wf,
+                                                                 const bf16* __restrict__ cf, bf16* __restrict__ bias,
                                                                  int B, int N, int Np, int H) {
   __shared__ __attribute__((aligned(16))) bf16 wl[32 * kLdw];
-  stage_weights(wl, wz, H, 32);
+  __shared__ bf16 cl[64];
+  stage_weights(wl, wf, H, 32);
+  stage_bias(cl, cf, H, 32);
   __syncthreads();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rho = lane & 31, h = lane >> 5;
@@ -48,15 +50,16 @@ __global__ __launch_bounds__(kBiasThreads) void pair_bias_kernel(const bf16* __r
     const int k0 = kt * 32;
     const int kk = k0 + perm32(rho);
     const bool valid = i < N && kk < N;
-    bf16x8 raw[8], x[8];
-    load_half_row(z + (((size_t)b * N + i) * N + kk) * CZ, h, valid, raw);
-    layernorm_half_row(raw, ln_w, ln_b, h, 1e-5f, x);
-    const f32x16 acc = proj_block_cm(x, wl, 0, rho, h);
+    float v[64];
+    bf16x8 x[8];
+    load_half_row_f32(z + (((size_t)b * N + (valid ? i : 0)) * N + (valid ? kk : 0)) * CZ, h, valid, v);
+    normalize_half_row(v, valid, x);
+    const f32x16 acc = proj_block_cm_f(x, bias_step_x(valid, h), wl, cl, 0, rho, h);
     if (rho < H) {
-      float v[16];
+      float o[16];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) v[u] = acc[u];
-      store16(bias + ((size_t)b * H + rho) * plane + (size_t)i * Np + k0 + 16 * h, v);
+      for (int u = 0; u < 16; ++u) o[u] = acc[u];
+      store16(bias + ((size_t)b * H + rho) * plane + (size_t)i * Np + k0 + 16 * h, o);
     }
   }
 }
@@ -167,7 +170,7 @@ __global__ __launch_bounds__(256) void apb_flash_kernel(const bf16* __restrict__
 }
 
 struct ApbBuffers {
-  bf16 *sn, *q, *k, *vt, *g, *go, *bias;
+  bf16 *sn, *q, *k, *vt, *g, *go, *bias, *wf, *cf;
 };
 
 size_t apb_layout(int64_t B, int64_t BM, int64_t N, int64_t CS, int64_t H, ApbBuffers* buf, char* base) {
@@ -189,8 +192,11 @@ size_t apb_layout(int64_t B, int64_t BM, int64_t N, int64_t CS, int64_t H, ApbBu
     buf->go = reinterpret_cast<bf16*>(p);
     p += tok;
     buf->bias = reinterpret_cast<bf16*>(p);
+    p += bias_bytes;
+    buf->wf = reinterpret_cast<bf16*>(p);
+    buf->cf = reinterpret_cast<bf16*>(p + round_up((size_t)32 * 128 * 2, 256));
   }
-  return 6 * tok + bias_bytes;
+  return 6 * tok + bias_bytes + fold_bytes(32);
 }
 
 }  // namespace
@@ -248,10 +254,12 @@ extern "C" int bioemu_apb_fwd(const void* s, const void* z, const uint8_t* mask,
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
   const long long ntiles = B * Np * (Np / 32);
   const unsigned grid1 = (unsigned)std::min<long long>(4LL * cus, (ntiles + 3) / 4);
+  rc = launch_fold_ln(w_z, norm_z_w, norm_z_b, buf.wf, buf.cf, H, stream);
+  if (rc) return rc;
   {
     KernelTimerScope timed("apb_pair_bias", stream);
     hipLaunchKernelGGL(pair_bias_kernel, dim3(grid1), dim3(kBiasThreads), 0, stream, static_cast<const bf16*>(z),
-                       norm_z_w, norm_z_b, static_cast<const bf16*>(w_z), buf.bias, (int)B, (int)N, (int)Np, (int)H);
+                       buf.wf, buf.cf, buf.bias, (int)B, (int)N, (int)Np, (int)H);
   }
   rc = check_launch("apb_pair_bias");
   if (rc) return rc;

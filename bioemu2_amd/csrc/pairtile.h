@@ -99,6 +99,105 @@ __device__ __forceinline__ f32x16 proj_block_pm(const bf16x8 x[8], const bf16* w
   return acc;
 }
 
+// ---------------------------------------------------------------------------
+// LayerNorm folded into the projection that follows it.
+//
+//   LN(x) W^T = xhat (W diag(gamma))^T + W beta,   xhat = (x - mean) * rstd
+//
+// launch_fold_ln (fold.hip) writes W' = W diag(gamma) (bf16, [rows][128]) and the bias
+// W beta split into two bf16 parts (hi + lo, ~16 mantissa bits together,
+// [rows][2]).  Kernels normalise affine-free (no gamma/beta registers) and
+// add the bias with one extra MFMA k-step: x-side operand [keep, keep, 0..]
+// against weight-side [hi, lo, 0..].  keep = 0 zeroes a pair's whole output
+// (its xhat row is zeroed too), which is the masked_fill of the reference
+// for bias-free projections.
+// ---------------------------------------------------------------------------
+// Affine-free LayerNorm of the 128 channels held by lanes l and l^32 (this
+// lane's 64 in v, fp32), bf16 result in the MFMA operand layout; a row with
+// keep == false comes out zero.
+__device__ __forceinline__ void normalize_half_row(const float* v, bool keep, bf16x8 out[8]) {
+  float sum = 0.f;
+#pragma unroll
+  for (int c = 0; c < 64; ++c) sum += v[c];
+  sum += __shfl_xor(sum, 32);
+  const float mean = sum * (1.0f / kPairC);
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < 64; ++c) {
+    const float d = v[c] - mean;
+    ss += d * d;
+  }
+  ss += __shfl_xor(ss, 32);
+  const float rstd = keep ? rsqrtf(ss * (1.0f / kPairC) + 1e-5f) : 0.f;
+#pragma unroll
+  for (int c = 0; c < 64; ++c) out[c >> 3][c & 7] = f2bf((v[c] - mean) * rstd);
+}
+
+// Loads this lane's channel half of a pair row as fp32 (zeros when !valid).
+__device__ __forceinline__ void load_half_row_f32(const bf16* row, int h, bool valid, float* v) {
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    bf16x8 raw;
+    if (valid) {
+      raw = load8(row + 64 * h + 8 * s);
+    } else {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) raw[t] = f2bf(0.f);
+    }
+    unpack8(raw, v + 8 * s);
+  }
+}
+
+// x-side operand of the bias k-step: [keep, keep, 0, ...] in channel half 0.
+__device__ __forceinline__ bf16x8 bias_step_x(bool keep, int h) {
+  bf16x8 r;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) r[t] = f2bf(0.f);
+  if (h == 0 && keep) {
+    r[0] = f2bf(1.f);
+    r[1] = f2bf(1.f);
+  }
+  return r;
+}
+
+// weight-side operand of the bias k-step for weight row `row`: [hi, lo, 0, ...].
+__device__ __forceinline__ bf16x8 bias_step_w(const bf16* cl, int row, int h) {
+  bf16x8 r;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) r[t] = f2bf(0.f);
+  if (h == 0) {
+    r[0] = cl[2 * row];
+    r[1] = cl[2 * row + 1];
+  }
+  return r;
+}
+
+// Channel-major folded projection block: X(32 x 128) W'[row0..+31]^T + keep * c.
+__device__ __forceinline__ f32x16 proj_block_cm_f(const bf16x8 x[8], bf16x8 xb, const bf16* wl, const bf16* cl,
+                                                  int row0, int n, int h) {
+  f32x16 acc = zero16();
+  const bf16* w = wl + (row0 + n) * kLdw + 64 * h;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) acc = mfma32(x[s], load8(w + 8 * s), acc);
+  return mfma32(xb, bias_step_w(cl, row0 + n, h), acc);
+}
+
+// Pair-major folded projection block: W'[row0 + perm32(.)] X^T + c * keep.
+__device__ __forceinline__ f32x16 proj_block_pm_f(const bf16x8 x[8], bf16x8 xb, const bf16* wl, const bf16* cl,
+                                                  int row0, int n, int h) {
+  f32x16 acc = zero16();
+  const int r = row0 + perm32(n);
+  const bf16* w = wl + r * kLdw + 64 * h;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) acc = mfma32(load8(w + 8 * s), x[s], acc);
+  return mfma32(bias_step_w(cl, r, h), xb, acc);
+}
+
+// Copies `rows` bias pairs (hi, lo) into LDS, zero-filling up to rows_padded.
+__device__ __forceinline__ void stage_bias(bf16* cl, const bf16* __restrict__ cf, int rows, int rows_padded) {
+  for (int q = threadIdx.x; q < 2 * rows_padded; q += blockDim.x) cl[q] = q < 2 * rows ? cf[q] : f2bf(0.f);
+}
+
 // 16 fp32 accumulator values -> two 16-byte bf16 chunks.
 __device__ __forceinline__ void store16(bf16* dst, const float* v) {
   bf16x8 a, b;

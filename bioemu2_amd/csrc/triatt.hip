@@ -36,8 +36,8 @@ constexpr int H = 4;
 constexpr int DH = 32;
 constexpr int kProjRows = 4 * C + H;       // q, k, v, g, bias rows of the packed weight
 constexpr int kProjRowsPad = 4 * C + 32;   // bias block padded to one 32-row MFMA block
-constexpr int kProjThreads = 512;
-constexpr int kProjSmem = kProjRowsPad * kLdw * 2;
+constexpr int kProjThreads = 1024;
+constexpr int kProjSmem = kProjRowsPad * kLdw * 2 + kProjRowsPad * 2 * 2;
 constexpr int kFlashThreads = 256;         // 4 waves x 32 queries = 128 queries per workgroup
 
 // Softmax in base 2: q is stored pre-scaled by log2(e)/sqrt(d) and the bias by
@@ -58,12 +58,13 @@ struct TriAttBuffers {
 // ---------------------------------------------------------------------------
 template <bool kStarting>
 __global__ __launch_bounds__(kProjThreads) void triatt_proj_kernel(
-    const bf16* __restrict__ z, const uint8_t* __restrict__ mask, const float* __restrict__ ln_w,
-    const float* __restrict__ ln_b, const bf16* __restrict__ w, TriAttBuffers buf, int B, int N,
-    int Np) {
+    const bf16* __restrict__ z, const uint8_t* __restrict__ mask, const bf16* __restrict__ wf,
+    const bf16* __restrict__ cf, TriAttBuffers buf, int B, int N, int Np) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   bf16* wl = reinterpret_cast<bf16*>(smem);
-  stage_weights(wl, w, kProjRows, kProjRowsPad);
+  bf16* cl = wl + kProjRowsPad * kLdw;
+  stage_weights(wl, wf, kProjRows, kProjRowsPad);
+  stage_bias(cl, cf, kProjRows, kProjRowsPad);
   __syncthreads();
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -82,41 +83,39 @@ __global__ __launch_bounds__(kProjThreads) void triatt_proj_kernel(
     // This lane's pair slot: frame (i, k0 + perm32(rho)).
     const int kk = k0 + perm32(rho);
     const bool valid = i < N && kk < N;
-    const size_t zpair = kStarting ? ((size_t)b * N + i) * N + kk : ((size_t)b * N + kk) * N + i;
-    bf16x8 raw[8], x[8];
-    load_half_row(z + zpair * C, h, valid, raw);
-    layernorm_half_row(raw, ln_w, ln_b, h, 1e-5f, x);
+    const size_t zpair = !valid ? 0 : kStarting ? ((size_t)b * N + i) * N + kk : ((size_t)b * N + kk) * N + i;
+    float v[64];
+    bf16x8 x[8];
+    load_half_row_f32(z + zpair * C, h, valid, v);
+    normalize_half_row(v, valid, x);
+    const bf16x8 xb = bias_step_x(valid, h);
 
     const size_t frow = ((size_t)b * Np + i) * Np;  // frame row base (pairs)
-    // q, k, g: pair-major.  Lane (n, h) holds pair slot perm32(rho), channels cb*32+16h..+15.
+    // q (times the softmax scale), k, g: pair-major; lane holds pair slot
+    // perm32(rho), channels blk*32 + 16h .. +15.
     const size_t pm_off = (frow + kk) * C;
 #pragma unroll 1
-    for (int cb = 0; cb < 4; ++cb) {
-      f32x16 aq = proj_block_pm(x, wl, 0 * C + cb * 32, rho, h);
+    for (int blk = 0; blk < 12; ++blk) {
+      const int which = blk >> 2, cb = blk & 3;   // 0: q, 1: k, 2: g
+      const int row0 = (which == 2 ? 3 * C : which * C) + cb * 32;
+      const f32x16 a = proj_block_pm_f(x, xb, wl, cl, row0, rho, h);
       float vq[16];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) vq[u] = aq[u] * kQScale;
-      store16(buf.q + pm_off + cb * 32 + 16 * h, vq);
-      f32x16 ak = proj_block_pm(x, wl, 1 * C + cb * 32, rho, h);
-#pragma unroll
-      for (int u = 0; u < 16; ++u) vq[u] = ak[u];
-      store16(buf.k + pm_off + cb * 32 + 16 * h, vq);
-      f32x16 ag = proj_block_pm(x, wl, 3 * C + cb * 32, rho, h);
-#pragma unroll
-      for (int u = 0; u < 16; ++u) vq[u] = sigmoidf_fast(ag[u]);
-      store16(buf.g + pm_off + cb * 32 + 16 * h, vq);
+      for (int u = 0; u < 16; ++u) vq[u] = which == 0 ? a[u] * kQScale : which == 1 ? a[u] : sigmoidf_fast(a[u]);
+      bf16* dst = which == 0 ? buf.q : which == 1 ? buf.k : buf.g;
+      store16(dst + pm_off + cb * 32 + 16 * h, vq);
     }
     // v^T: channel-major.  Lane (n, h) holds channel cb*32+n, pairs k0+16h..+15.
 #pragma unroll 1
     for (int cb = 0; cb < 4; ++cb) {
-      f32x16 av = proj_block_cm(x, wl, 2 * C + cb * 32, rho, h);
+      const f32x16 av = proj_block_cm_f(x, xb, wl, cl, 2 * C + cb * 32, rho, h);
       float vv[16];
 #pragma unroll
       for (int u = 0; u < 16; ++u) vv[u] = av[u];
       store16(buf.vt + (((size_t)b * Np + i) * C + cb * 32 + rho) * Np + k0 + 16 * h, vv);
     }
     {
-      f32x16 ab = proj_block_cm(x, wl, 4 * C, rho, h);
+      const f32x16 ab = proj_block_cm_f(x, xb, wl, cl, 4 * C, rho, h);
       if (rho < H) {
         float vb[16];
 #pragma unroll
@@ -409,7 +408,8 @@ extern "C" size_t bioemu_triatt_workspace_bytes(int64_t B, int64_t N, int64_t Dc
   const size_t Np = triatt_np(N);
   const size_t pairs = (size_t)B * Np * Np;
   // q, k, g, v^T (bf16 x C each) + bias (bf16 x H) + mask (u8), each 256-byte aligned
-  return round_up(pairs * C * 2, 256) * 4 + round_up(pairs * H * 2, 256) + round_up(pairs, 256);
+  return round_up(pairs * C * 2, 256) * 4 + round_up(pairs * H * 2, 256) + round_up(pairs, 256) +
+         fold_bytes(kProjRows);
 }
 
 extern "C" int bioemu_triatt_fwd(const void* z, const uint8_t* mask, const float* norm_w,
@@ -447,6 +447,11 @@ extern "C" int bioemu_triatt_fwd(const void* z, const uint8_t* mask, const float
   buf.bias = reinterpret_cast<bf16*>(p);
   p += round_up(pairs * H * 2, 256);
   buf.mask = reinterpret_cast<uint8_t*>(p);
+  p += round_up(pairs, 256);
+  bf16* wf = reinterpret_cast<bf16*>(p);
+  bf16* cf = reinterpret_cast<bf16*>(p + round_up((size_t)kProjRows * C * 2, 256));
+  int rc = launch_fold_ln(w_proj, norm_w, norm_b, wf, cf, kProjRows, stream);
+  if (rc) return rc;
 
   int dev = 0, cus = 0;
   (void)hipGetDevice(&dev);
@@ -462,14 +467,12 @@ extern "C" int bioemu_triatt_fwd(const void* z, const uint8_t* mask, const float
     KernelTimerScope timed("triatt_proj", stream);
     if (starting)
       hipLaunchKernelGGL(triatt_proj_kernel<true>, dim3(grid1), dim3(kProjThreads), kProjSmem, stream,
-                         static_cast<const bf16*>(z), mask, norm_w, norm_b, static_cast<const bf16*>(w_proj),
-                         buf, (int)B, (int)N, (int)Np);
+                         static_cast<const bf16*>(z), mask, wf, cf, buf, (int)B, (int)N, (int)Np);
     else
       hipLaunchKernelGGL(triatt_proj_kernel<false>, dim3(grid1), dim3(kProjThreads), kProjSmem, stream,
-                         static_cast<const bf16*>(z), mask, norm_w, norm_b, static_cast<const bf16*>(w_proj),
-                         buf, (int)B, (int)N, (int)Np);
+                         static_cast<const bf16*>(z), mask, wf, cf, buf, (int)B, (int)N, (int)Np);
   }
-  int rc = check_launch("triatt_proj");
+  rc = check_launch("triatt_proj");
   if (rc) return rc;
 
   const long long nitems = (long long)B * N * ((Np + 127) / 128);

@@ -87,27 +87,81 @@ __global__ __launch_bounds__(kInThreads) void trimul_proj_in_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Stage 3 prep: fold the two LayerNorm affines into the output projections.
+//   p_out(LN_out(o)) = xhat_o (Wp diag(g_out))^T + Wp b_out
+//   g_out(LN_in(x))  = xhat_x (Wg diag(g_in))^T  + Wg b_in
+// with xhat the normalised (affine-free) rows.  One workgroup per output row.
+// fold layout: [Wp' (D x D) | Wg' (D x D)] bf16, then [cp (D) | cg (D)] fp32.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(D) void trimul_fold_kernel(const bf16* __restrict__ p_w, const bf16* __restrict__ g_w,
+                                                      const float* __restrict__ ln_out_w,
+                                                      const float* __restrict__ ln_out_b,
+                                                      const float* __restrict__ ln_in_w,
+                                                      const float* __restrict__ ln_in_b, bf16* __restrict__ wfold,
+                                                      float* __restrict__ cfold) {
+  __shared__ float red[2][D];
+  const int e = blockIdx.x, c = threadIdx.x;
+  const float wp = bf2f(p_w[e * D + c]), wg = bf2f(g_w[e * D + c]);
+  wfold[e * D + c] = f2bf(wp * ln_out_w[c]);
+  wfold[D * D + e * D + c] = f2bf(wg * ln_in_w[c]);
+  red[0][c] = wp * ln_out_b[c];
+  red[1][c] = wg * ln_in_b[c];
+  __syncthreads();
+  for (int st = D / 2; st > 0; st >>= 1) {
+    if (c < st) {
+      red[0][c] += red[0][c + st];
+      red[1][c] += red[1][c + st];
+    }
+    __syncthreads();
+  }
+  if (c == 0) {
+    cfold[e] = red[0][0];
+    cfold[D + e] = red[1][0];
+  }
+}
+
+// Affine-free LayerNorm of the 128 channels held by lanes l and l^32, bf16
+// result in the MFMA operand layout (pairtile.h); v holds this lane's 64.
+__device__ __forceinline__ void normalize_half_row(const float* v, bf16x8 out[8]) {
+  float sum = 0.f;
+#pragma unroll
+  for (int c = 0; c < 64; ++c) sum += v[c];
+  sum += __shfl_xor(sum, 32);
+  const float mean = sum * (1.0f / D);
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < 64; ++c) {
+    const float d = v[c] - mean;
+    ss += d * d;
+  }
+  ss += __shfl_xor(ss, 32);
+  const float rstd = rsqrtf(ss * (1.0f / D) + 1e-5f);
+#pragma unroll
+  for (int c = 0; c < 64; ++c) out[c >> 3][c & 7] = f2bf((v[c] - mean) * rstd);
+}
+
+// ---------------------------------------------------------------------------
 // Stage 3: out = p_out(LN_out(o)) * sigmoid(g_out(LN_in(x)))  (+ x).
 //
 // Tile = (b, row i, 32 columns j).  o is channel-major (the contraction's
 // output planes), so each lane gathers its pair's 64-channel half with 2-byte
-// loads (the 32 lanes of a half read 64 contiguous bytes per channel); x is
-// pair-major.  Both LayerNorms run in registers; p_out / g_out (2 x 128 x 128)
-// sit in LDS.  The result comes out pair-major (16 consecutive channels per
-// lane) and is stored with the residual add fused.
+// buffer loads (the 32 lanes of a half read 64 contiguous bytes per channel;
+// one VGPR address, the channel offset in an SGPR); x is pair-major.  Both
+// LayerNorms run affine-free in registers against the folded weights, which
+// sit in LDS with the folded biases.  The result comes out pair-major (16
+// consecutive channels per lane) and is stored with the residual add fused.
 // ---------------------------------------------------------------------------
 constexpr int kOutThreads = 512;
-constexpr int kOutSmem = 2 * D * kLdw * 2;
+constexpr int kOutSmem = 2 * D * kLdw * 2 + 2 * D * 4;
 
-__global__ __launch_bounds__(kOutThreads) void trimul_out_kernel(
-    const bf16* __restrict__ o, const bf16* x, const float* __restrict__ ln_in_w,
-    const float* __restrict__ ln_in_b, const float* __restrict__ ln_out_w,
-    const float* __restrict__ ln_out_b, const bf16* __restrict__ p_w, const bf16* __restrict__ g_w,
+__global__ __launch_bounds__(kOutThreads) __attribute__((amdgpu_waves_per_eu(4, 8))) void trimul_out_kernel(
+    const bf16* __restrict__ o, const bf16* x, const bf16* __restrict__ wfold, const float* __restrict__ cfold,
     bf16* out, int B, int N, int Np, int residual) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   bf16* wl = reinterpret_cast<bf16*>(smem);
-  stage_weights(wl, p_w, D, D);
-  stage_weights(wl + D * kLdw, g_w, D, D);
+  float* cl = reinterpret_cast<float*>(smem + 2 * D * kLdw * 2);
+  stage_weights(wl, wfold, 2 * D, 2 * D);
+  for (int t = threadIdx.x; t < 2 * D; t += blockDim.x) cl[t] = cfold[t];
   __syncthreads();
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -123,68 +177,49 @@ __global__ __launch_bounds__(kOutThreads) void trimul_out_kernel(
     const int b = (int)(t / ((long long)tiles_per_row * N));
     const int jj = jt * 32 + perm32(rho);
     const bool valid = jj < N;
-
-    // LN_in(x) first (its 32 packed registers stay live), then o.
     const size_t pair = ((size_t)b * N + i) * N + (valid ? jj : 0);
-    bf16x8 xraw[8], xf[8];
-    load_half_row(x + pair * D, h, valid, xraw);
-    layernorm_half_row(xraw, ln_in_w, ln_in_b, h, 1e-5f, xf);
-    asm volatile("" ::: "memory");  // finish LN_in before the o gather is scheduled
 
-    // o gather: channels 64h + 8s + e of pair (i, jj), jj < Np always.  One
-    // buffer resource per batch, the lane's plane offset in a VGPR and the
-    // channel's plane offset in an SGPR, so the 64 loads share one address;
-    // each 16-bit result is widened to fp32 in place for the LayerNorm.
-    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<bf16*>(o + (size_t)b * D * plane), (short)0, (int)(D * plane * 2), 0x00020000);
-    const unsigned voff = (unsigned)((64 * h * plane + (size_t)i * Np + jj) * 2);
     float v[64];
-#pragma unroll
-    for (int c = 0; c < 64; ++c) {
-      const unsigned short r =
-          (unsigned short)__builtin_amdgcn_raw_buffer_load_b16(rsrc, voff, (unsigned)(c * plane * 2), 0);
-      v[c] = __uint_as_float((unsigned)r << 16);
-    }
-    bf16x8 of[8];
+    bf16x8 xf[8], of[8];
     {
-      float sum = 0.f;
+      bf16x8 xraw[8];
+      load_half_row(x + pair * D, h, valid, xraw);
 #pragma unroll
-      for (int c = 0; c < 64; ++c) sum += v[c];
-      sum += __shfl_xor(sum, 32);
-      const float mean = sum * (1.0f / D);
-      float ss = 0.f;
-#pragma unroll
-      for (int c = 0; c < 64; ++c) {
-        const float d = v[c] - mean;
-        ss += d * d;
-      }
-      ss += __shfl_xor(ss, 32);
-      const float rstd = rsqrtf(ss * (1.0f / D) + 1e-5f);
+      for (int s = 0; s < 8; ++s) unpack8(xraw[s], v + 8 * s);
+    }
+    normalize_half_row(v, xf);
+    {
+      const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<bf16*>(o + (size_t)b * D * plane), (short)0, (int)(D * plane * 2), 0x00020000);
+      const unsigned voff = (unsigned)((64 * h * plane + (size_t)i * Np + jj) * 2);
 #pragma unroll
       for (int c = 0; c < 64; ++c) {
-        const int ch = 64 * h + c;
-        of[c >> 3][c & 7] = f2bf((v[c] - mean) * rstd * ln_out_w[ch] + ln_out_b[ch]);
+        const unsigned short r =
+            (unsigned short)__builtin_amdgcn_raw_buffer_load_b16(rsrc, voff, (unsigned)(c * plane * 2), 0);
+        v[c] = __uint_as_float((unsigned)r << 16);
       }
     }
+    normalize_half_row(v, of);
 
 #pragma unroll 1
     for (int cb = 0; cb < 4; ++cb) {
       const f32x16 pa = proj_block_pm(of, wl, cb * 32, rho, h);
       const f32x16 ga = proj_block_pm(xf, wl, D + cb * 32, rho, h);
       if (valid) {
-        const size_t off = pair * D + cb * 32 + 16 * h;
-        float v[16];
+        const int e0 = cb * 32 + 16 * h;
+        const size_t off = pair * D + e0;
+        float r[16];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) v[u] = pa[u] * sigmoidf_fast(ga[u]);
+        for (int u = 0; u < 16; ++u) r[u] = (pa[u] + cl[e0 + u]) * sigmoidf_fast(ga[u] + cl[D + e0 + u]);
         if (residual) {
           const bf16x8 r0 = load8(x + off), r1 = load8(x + off + 8);
 #pragma unroll
           for (int u = 0; u < 8; ++u) {
-            v[u] += bf2f(r0[u]);
-            v[8 + u] += bf2f(r1[u]);
+            r[u] += bf2f(r0[u]);
+            r[8 + u] += bf2f(r1[u]);
           }
         }
-        store16(out + off, v);
+        store16(out + off, r);
       }
     }
   }
@@ -198,7 +233,9 @@ using namespace bioemu;
 extern "C" size_t bioemu_trimul_workspace_bytes(int64_t B, int64_t N, int64_t Dc) {
   if (B <= 0 || N <= 0 || Dc <= 0) return 0;
   const int64_t Np = round_up(N, kGemmTile);
-  return (size_t)(3 * B * Dc * Np * Np) * sizeof(bf16);
+  // a, b, o planes + the folded output weights and biases
+  return (size_t)(3 * B * Dc * Np * Np) * sizeof(bf16) + (size_t)(2 * Dc * Dc) * sizeof(bf16) +
+         (size_t)(2 * Dc) * sizeof(float);
 }
 
 extern "C" int bioemu_trimul_fwd(const void* x, const uint8_t* mask, const float* norm_in_w,
@@ -229,6 +266,8 @@ extern "C" int bioemu_trimul_fwd(const void* x, const uint8_t* mask, const float
   const size_t plane_elems = (size_t)(B * D * Np * Np);
   bf16* ab = static_cast<bf16*>(workspace);
   bf16* ob = ab + 2 * plane_elems;
+  bf16* wfold = ob + plane_elems;                                  // [2][D][D]
+  float* cfold = reinterpret_cast<float*>(wfold + 2 * D * D);      // [2][D]
 
   int dev = 0, cus = 0;
   (void)hipGetDevice(&dev);
@@ -256,13 +295,19 @@ extern "C" int bioemu_trimul_fwd(const void* x, const uint8_t* mask, const float
   if (rc) return rc;
   rc = launch_bgemm_nt(ab, ab + plane_elems, ob, B * D, Np, stream);
   if (rc) return rc;
+  {
+    KernelTimerScope timed("trimul_fold", stream);
+    hipLaunchKernelGGL(trimul_fold_kernel, dim3(D), dim3(D), 0, stream, static_cast<const bf16*>(p_out_w),
+                       static_cast<const bf16*>(g_out_w), norm_out_w, norm_out_b, norm_in_w, norm_in_b, wfold, cfold);
+  }
+  rc = check_launch("trimul_fold");
+  if (rc) return rc;
 
   const long long waves_out = (long long)B * N * ((N + 31) / 32);
   const unsigned grid3 = (unsigned)std::min<long long>(2LL * cus, (waves_out + 7) / 8);
   KernelTimerScope timed("trimul_out", stream);
   hipLaunchKernelGGL(trimul_out_kernel, dim3(grid3), dim3(kOutThreads), kOutSmem, stream, ob,
-                     static_cast<const bf16*>(x), norm_in_w, norm_in_b, norm_out_w, norm_out_b,
-                     static_cast<const bf16*>(p_out_w), static_cast<const bf16*>(g_out_w),
-                     static_cast<bf16*>(out), (int)B, (int)N, (int)Np, residual);
+                     static_cast<const bf16*>(x), wfold, cfold, static_cast<bf16*>(out), (int)B, (int)N, (int)Np,
+                     residual);
   return check_launch("trimul_out");
 }

@@ -63,13 +63,23 @@ def trimul_kernel_work(name: str, B: int, N: int, c: int = 128) -> tuple[str, fl
     P = B * N * N
     if name == "trimul_proj_in":
         # LN + [p_in | g_in] (c -> 4c) ; reads x, writes a and b planes
-        return _bound(2.0 * P * c * 4 * c, P * (c * 2 + 2 * c * 2))
+        return ("hbm", float(P * (c * 2 + 2 * c * 2)))
     if name == "bgemm_nt":
-        # o[d,i,j] = sum_k a[d,i,k] b[d,j,k] over the valid N
-        return _bound(2.0 * B * c * N * N * N, 3 * P * c * 2)
+        # o[d,i,j] = sum_k a[d,i,k] b[d,j,k] over the valid N: the contraction, reported on MFMA
+        return ("mfma", 2.0 * B * c * N * N * N)
     if name == "trimul_out":
         # LN_out(o) -> p_out, LN_in(x) -> g_out ; reads o and x, writes out
-        return _bound(2.0 * P * c * 2 * c, 3 * P * c * 2)
+        return ("hbm", float(3 * P * c * 2))
+    if name == "trimul_fold":
+        # folds the LayerNorm affines into the output weights: reads 2 c x c bf16, writes them back
+        return ("hbm", float(4 * c * c * 2))
+    return None
+
+
+def fold_kernel_work(name: str, rows: int) -> tuple[str, float] | None:
+    if name == "fold_ln":
+        # W diag(gamma) and W beta for a [rows, 128] weight: reads and writes it once
+        return ("hbm", float(2 * rows * 128 * 2))
     return None
 
 
@@ -178,7 +188,7 @@ class TriAttWorkload(Workload):
         return fn, 1.0, f"oracle.triangle_attention fp32, full N={self.n} (64-row chunks)"
 
     def kernel_work(self, kernel: str) -> tuple[str, float]:
-        w = triatt_kernel_work(kernel, 1, self.n)
+        w = triatt_kernel_work(kernel, 1, self.n) or fold_kernel_work(kernel, 4 * 128 + 4)
         if w is None:
             raise KeyError(kernel)
         return w
@@ -234,6 +244,8 @@ class BlockWorkload(Workload):
             w = fn(kernel, 1, n)
             if w is not None:
                 return w
+        if kernel == "fold_ln":  # triatt (516 rows) x2, APB bias (16 rows), transition (1024 rows)
+            return fold_kernel_work(kernel, (2 * 516 + 16 + 1024) // 4)
         if kernel == "transition_pair":
             return ("mfma", 2.0 * n * n * c * 12 * c)
         if kernel == "apb_pair_bias":

@@ -61,8 +61,9 @@ def test_host_only_queries():
     lib = _lib.lib()
     assert b"gfx950" in lib.bioemu_version()
     n = 768
-    np_ = 768  # already a multiple of 128
-    assert lib.bioemu_trimul_workspace_bytes(1, n, 128) == 3 * 128 * np_ * np_ * 2
+    np_ = 768  # already a multiple of the 256 contraction tile
+    folded = 2 * 128 * 128 * 2 + 2 * 128 * 4  # folded output weights and biases
+    assert lib.bioemu_trimul_workspace_bytes(1, n, 128) == 3 * 128 * np_ * np_ * 2 + folded
     assert lib.bioemu_trimul_workspace_bytes(0, n, 128) == 0
 
 
