@@ -7,10 +7,12 @@ HBM-resident input.  The default op is one full bf16 Pairformer block at N=768,
 c_z=128, c_s=384 (the BASELINE metric); ``--op`` selects a single op at its
 config shape instead (those are diagnostic lines).
 
-Printed on one line as JSON: ms per step, the roofline of the dominant kernel
-(its average duration measured live with the library's hipEvent kernel timer
-on the kernel's own launch stream, over the timed region) and a CPU baseline
-(the fp32 oracle timed on a bounded sample, rank 0 only).
+Printed on one line as JSON: ms per step (K steps between two hipEvents on the
+launch stream, synchronised on both sides), the roofline of the dominant
+kernel and a CPU baseline (the fp32 oracle timed on a bounded sample, rank 0
+only).  The dominant kernel's average duration comes from a second timed
+region of the same K steps in which the library's kernel timer brackets every
+launch with hipEvents on the kernel's own stream.
 """
 
 from __future__ import annotations
@@ -38,6 +40,11 @@ def _parse() -> argparse.Namespace:
     ap.add_argument("--n", type=int, default=None, help="override N (tokens)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernels", action="store_true", help="also print the per-kernel table to stderr")
+    ap.add_argument("--no-kernel-timer", action="store_true",
+                    help="time the steps without per-kernel events (no roofline; diagnostic)")
+    ap.add_argument("--calibrate-bytes", type=int, default=0,
+                    help="first run torch's negation of a tensor of this many bf16 bytes (a PMC calibration "
+                         "dispatch that reads and writes exactly that much)")
     return ap.parse_args()
 
 
@@ -91,6 +98,7 @@ def main() -> int:
     import torch
 
     from bioemu2_amd import workloads
+    from bioemu2_amd.profiling import TIMER_TO_KERNEL
     from bioemu2_amd.timing import KernelTimer
 
     if not torch.cuda.is_available():
@@ -98,6 +106,12 @@ def main() -> int:
         return 2
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+
+    if args.calibrate_bytes:
+        src = torch.ones(args.calibrate_bytes // 2, dtype=torch.bfloat16, device=dev)
+        torch.neg(src, out=torch.empty_like(src))
+        torch.cuda.synchronize()
+        del src
 
     wl = workloads.make(args.op, dev, n=args.n)
     with torch.no_grad():
@@ -107,14 +121,27 @@ def main() -> int:
 
         start = torch.cuda.Event(enable_timing=True)
         stop = torch.cuda.Event(enable_timing=True)
-        with KernelTimer() as kt:
+
+        def timed(steps: int) -> float:
             torch.cuda.synchronize()
             start.record()
-            for _ in range(args.steps):
+            for _ in range(steps):
                 wl.step()
             stop.record()
             torch.cuda.synchronize()
-        ms_per_step = start.elapsed_time(stop) / args.steps
+            return start.elapsed_time(stop) / steps
+
+        # Timed region 1: the K steps alone -> value.
+        ms_per_step = timed(args.steps)
+        if args.no_kernel_timer:
+            print(json.dumps({"metric": wl.metric, "ms_per_step": round(ms_per_step, 4), "kernel_timer": False}),
+                  flush=True)
+            return 0
+        # Timed region 2: the same K steps with a hipEvent pair around every
+        # kernel launch (on the launch stream) -> per-kernel average durations.
+        # The events serialise kernel tails, so this region runs a few % slower.
+        with KernelTimer() as kt:
+            ms_per_step_events = timed(args.steps)
         kernels = kt.results()
 
     # Dominant kernel = largest total time in the timed region.
@@ -135,7 +162,7 @@ def main() -> int:
         "peak": peak,
         "unit": unit,
         "frac": round(achieved / peak, 4),
-        "traffic": workloads.measured_traffic(dom_name, wl.name),
+        "traffic": workloads.measured_traffic(TIMER_TO_KERNEL.get(dom_name, dom_name), wl.name),
         "avg_ms": round(dom_avg_ms, 5),
         "algorithmic_per_launch": amount,
     }
@@ -179,6 +206,7 @@ def main() -> int:
         "data": "synthetic (seeded randn inputs, seeded random-init weights)",
         "config": wl.config,
         "tflops": round(wl.flops / (ms_per_step * 1e-3) / 1e12, 1),
+        "ms_per_step_with_kernel_events": round(ms_per_step_events, 4),
         "roofline": roofline,
         "kernels": per_kernel,
         "cpu_baseline": cpu,

@@ -70,6 +70,28 @@ __device__ __forceinline__ bf16x4 pack4(float a, float b, float c, float d) {
 __device__ __forceinline__ bf16x8 load8(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
 __device__ __forceinline__ void store8(bf16* p, bf16x8 v) { *reinterpret_cast<bf16x8*>(p) = v; }
 
+// Buffer resource over [base, base + bytes) (raw buffer, 32-bit offsets).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// 16-byte load at byte offset voff (per lane) + soff (wave-uniform).
+__device__ __forceinline__ bf16x8 buffer_load8(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+// acc + sum of the eight bf16 values of v (four bf16 dot2 steps against ones).
+__device__ __forceinline__ float sum8_bf16(bf16x8 v, float acc) {
+  const bf16x2 one = {(bf16)1.0f, (bf16)1.0f};
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const bf16x2 pair = {v[2 * t], v[2 * t + 1]};
+    acc = __builtin_amdgcn_fdot2_f32_bf16(pair, one, acc, false);
+  }
+  return acc;
+}
+
 // A 16-byte chunk as eight bf16 -> fp32 values.
 __device__ __forceinline__ void unpack8(bf16x8 v, float* out) {
 #pragma unroll

@@ -46,12 +46,24 @@ constexpr float kQScale = 0.17677669529663687f * kLog2e;
 
 struct TriAttBuffers {
   bf16* q;       // [B][Np][Np][C]  frame-ordered, pair-major, times kQScale
-  bf16* k;       // [B][Np][Np][C]
+  bf16* k;       // [B][Np][H][Np][DH]  per frame row and head: keys x head channels
   bf16* g;       // [B][Np][Np][C]  sigmoid already applied
   bf16* vt;      // [B][Np][C][Np]  channel-major per frame row
-  bf16* bias;    // [B][H][Np][Np]  times log2(e)
+  bf16* bias;    // [B][H][Np/32][Np/64][4][64][8]  times log2(e), in MFMA B-operand tiles
+                 //   (see bias_tile_index)
   uint8_t* mask; // [B][Np][Np]     frame-ordered 0/1 (0 outside [0, N))
 };
+
+// Bias storage: for head h, query q and key k the value sits in the 4 KB tile
+// (h, q / 32, k / 64) at chunk x = (k % 64) / 16, lane (q % 32) + 32 ((k % 16) / 8),
+// element k % 8 -- the B-operand layout in which the attention kernel adds the
+// bias, so that each of its bias loads is 1 KB contiguous.  For k a multiple of
+// 8 this returns the start of the 8-key chunk.
+__device__ __forceinline__ size_t bias_tile_index(int h, int q, int k, int Np) {
+  const size_t tile = ((size_t)h * (Np / 32) + q / 32) * (Np / 64) + k / 64;
+  const int x = (k & 63) >> 4, lane = (q & 31) + 32 * ((k & 15) >> 3);
+  return tile * 2048 + (x * 64 + lane) * 8 + (k & 7);
+}
 
 // ---------------------------------------------------------------------------
 // Projection kernel.  Tile = (b, frame row i, 32 frame columns).
@@ -102,8 +114,10 @@ __global__ __launch_bounds__(kProjThreads) void triatt_proj_kernel(
       float vq[16];
 #pragma unroll
       for (int u = 0; u < 16; ++u) vq[u] = which == 0 ? a[u] * kQScale : which == 1 ? a[u] : sigmoidf_fast(a[u]);
-      bf16* dst = which == 0 ? buf.q : which == 1 ? buf.k : buf.g;
-      store16(dst + pm_off + cb * 32 + 16 * h, vq);
+      // k is head-major per frame row: [H][Np][DH]
+      bf16* base = which == 0 ? buf.q : which == 1 ? buf.k : buf.g;
+      const size_t dst = which == 1 ? (frow * H + (size_t)cb * Np + kk) * DH + 16 * h : pm_off + cb * 32 + 16 * h;
+      store16(base + dst, vq);
     }
     // v^T: channel-major.  Lane (n, h) holds channel cb*32+n, pairs k0+16h..+15.
 #pragma unroll 1
@@ -120,7 +134,16 @@ __global__ __launch_bounds__(kProjThreads) void triatt_proj_kernel(
         float vb[16];
 #pragma unroll
         for (int u = 0; u < 16; ++u) vb[u] = ab[u] * kLog2e;
-        store16(buf.bias + ((size_t)b * H + rho) * plane + (size_t)i * Np + k0 + 16 * h, vb);
+        // keys k0 + 16h + u: u < 8 and u >= 8 go to the chunks of lanes hh = 0 / 1
+        bf16* dst = buf.bias + (size_t)b * H * plane + bias_tile_index(rho, i, k0 + 16 * h, Np);
+        bf16x8 lo, hi;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          lo[u] = f2bf(vb[u]);
+          hi[u] = f2bf(vb[8 + u]);
+        }
+        store8(dst, lo);
+        store8(dst + 32 * 8, hi);
       }
     }
     if (h == 0) {
@@ -170,7 +193,7 @@ __global__ __launch_bounds__(kProjThreads) void triatt_proj_kernel(
 constexpr int TLD = 48;                 // LDS row stride (bf16) of a [32][32] tile
 constexpr int kTile = 32 * TLD;
 constexpr int kStage = 4 * kTile;       // K (2 halves) + V^T (2 halves)
-constexpr float kRescaleSlack = 8.0f;   // log2 units
+constexpr float kSlackSum = 65536.0f;   // 2^16: a block sum above this may hold p > 2^16
 
 __device__ __forceinline__ int t_off(int r, int chunk) { return r * TLD + ((chunk ^ (((r >> 2) ^ (r >> 4)) & 1)) << 3); }
 
@@ -181,7 +204,7 @@ __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
   __shared__ __attribute__((aligned(16))) bf16 smem[2 * kStage];
   extern __shared__ __attribute__((aligned(16))) bf16 kadd[];   // [Np] additive key mask
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 31, hh = lane >> 5;
   // XCD-aware mapping: workgroup w runs on XCD w % 8.  Work items are
   // (b, row i, query block) with the query block fastest; each XCD gets a
@@ -202,25 +225,40 @@ __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
   const size_t frow = ((size_t)b * Np + i) * Np;
   const unsigned plane = (unsigned)Np * (unsigned)Np;
 
-  const bf16* __restrict__ kg = buf.k + frow * C;                           // [Np keys][C]
+  const bf16* __restrict__ kg = buf.k + frow * C;                           // [H][Np keys][DH]
   const bf16* __restrict__ vg = buf.vt + ((size_t)b * Np + i) * C * Np;     // [C][Np keys]
   const bf16* __restrict__ bg = buf.bias + (size_t)b * H * plane;           // [H][Np][Np]
-  const bf16* __restrict__ qg = buf.q + frow * C;                           // [Np][C]
+  // q row of this workgroup's frame row; once a head's q has been read, its
+  // 32-channel slot holds that head's normalised output o / l (bf16) until
+  // the epilogue (each lane rewrites only the slot it read itself).
+  bf16* qio = buf.q + frow * C;                                             // [Np][C]
+  // Key-mask row.  A row whose keys are all masked attends uniformly to its
+  // N keys (every logit replaced by the same value); it runs with zero q and
+  // zero bias so that all its logits are exactly 0 instead.
+  int any_valid = 0;
+  for (int t = tid; t < N; t += kFlashThreads) any_valid |= buf.mask[frow + t];
+  const bool dead = __syncthreads_or(any_valid) == 0;
   for (int t = tid; t < Np; t += kFlashThreads)
-    kadd[t] = f2bf(t >= N ? -INFINITY : (buf.mask[frow + t] ? 0.f : -1e30f));
+    kadd[t] = f2bf(t >= N ? -INFINITY : (dead || buf.mask[frow + t]) ? 0.f : -1e30f);
+
+  // Operand fetches through buffer resources: per-lane byte offsets are fixed,
+  // the (head, key block) part is a wave-uniform scalar offset.
+  const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(kg, (unsigned)Np * C * 2);
+  const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(vg, (unsigned)Np * C * 2);
+  const __amdgpu_buffer_rsrc_t brs = buffer_rsrc(bg, (unsigned)H * plane * 2);
 
   // Staging of one (head, 64-key) tile: K is 64 rows x 4 chunks, V^T 32 rows x
   // 8 chunks; thread tid moves K chunk tid and V^T chunk tid.
   const int k_row = tid >> 2, k_chunk = tid & 3;
   const int v_row = tid >> 3, v_chunk = tid & 7;
-  const unsigned k_off0 = (unsigned)k_row * C + k_chunk * 8;
-  const unsigned v_off0 = (unsigned)v_row * Np + v_chunk * 8;
+  const unsigned k_voff = (unsigned)tid * 16;   // = (k_row * DH + k_chunk * 8) * 2
+  const unsigned v_voff = ((unsigned)v_row * Np + v_chunk * 8) * 2;
   const int k_lds = (k_row >> 5) * kTile + t_off(k_row & 31, k_chunk);
   const int v_lds = 2 * kTile + (v_chunk >> 2) * kTile + t_off(v_row, v_chunk & 3);
   bf16x8 rk, rv;
   auto gload = [&](int hn, int kn) {
-    rk = load8(kg + k_off0 + (unsigned)kn * C + hn * DH);
-    rv = load8(vg + v_off0 + (unsigned)(hn * DH) * Np + kn);
+    rk = buffer_load8(krs, k_voff, (unsigned)(hn * Np + kn) * DH * 2);
+    rv = buffer_load8(vrs, v_voff, (unsigned)(hn * DH * Np + kn) * 2);
   };
   auto lstore = [&](int st) {
     store8(smem + st * kStage + k_lds, rk);
@@ -228,41 +266,49 @@ __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
   };
   // Bias slices in B-operand layout: lane (n, hh), half a, k-step s <-> keys
   // k0 + 32a + 16s + 8hh + t.
-  const unsigned bias_lane = (unsigned)qrow * Np + 8 * hh;
+  // One wave's bias slice for a (head, 64-key) block is one contiguous 4 KB
+  // tile: instruction x reads 1 KB, lane l at byte 16 l.
+  const unsigned bias_voff = (unsigned)lane * 16;
   auto bload = [&](int hn, int kn, bf16x8 (&bb)[4]) {
-    const bf16* p = bg + hn * plane + bias_lane + kn;
+    const unsigned soff = (unsigned)bias_tile_index(hn, active ? q0 : 0, kn, Np) * 2;
 #pragma unroll
-    for (int x = 0; x < 4; ++x) bb[x] = load8(p + 16 * x);
+    for (int x = 0; x < 4; ++x) bb[x] = buffer_load8(brs, bias_voff + 1024 * x, soff);
   };
 
   const int krow = perm32(n);
   // One-hot fragments: A[rho][(s, hh, t)] = 1 iff perm32(rho) == 16s + 8hh + t.
-  bf16x8 ident[2], qone, zero8;
+  bf16x8 ident[2], zero8;
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
-    ident[0][t] = f2bf(krow == 8 * hh + t ? 1.f : 0.f);
-    ident[1][t] = f2bf(krow == 16 + 8 * hh + t ? 1.f : 0.f);
-    qone[t] = f2bf(hh == 0 && t == 0 ? 1.f : 0.f);
+    ident[0][t] = f2bf(!dead && krow == 8 * hh + t ? 1.f : 0.f);
+    ident[1][t] = f2bf(!dead && krow == 16 + 8 * hh + t ? 1.f : 0.f);
     zero8[t] = f2bf(0.f);
   }
 
   const int nk = Np / 64;
-  bf16x8 gob[2 * H];   // finished heads: o / l (bf16), gated in the epilogue
-  bf16x8 bcur[4], bnext[4];
+  bf16x8 bias[4];   // bias slice of the block being consumed, then of the next one
 
   gload(0, 0);
-  bload(0, 0, bcur);
+  bload(0, 0, bias);
   lstore(0);
   __syncthreads();
   int st = 0;
 #pragma unroll 1
   for (int hd = 0; hd < H; ++hd) {
-    const bf16x8 qf0 = load8(qg + (unsigned)qrow * C + hd * DH + 8 * hh);
-    const bf16x8 qf1 = load8(qg + (unsigned)qrow * C + hd * DH + 16 + 8 * hh);
+    bf16x8 qf0 = zero8, qf1 = zero8;
+    if (!dead) {
+      qf0 = load8(qio + (unsigned)qrow * C + hd * DH + 8 * hh);
+      qf1 = load8(qio + (unsigned)qrow * C + hd * DH + 16 + 8 * hh);
+    }
     f32x16 o = zero16();
     float m = -INFINITY, l = 0.f;
-    // One 64-key block: fetch the next tile, consume the current one.
-    auto block = [&](int kb, const bf16x8 (&bc)[4], bf16x8 (&bn)[4]) {
+    bool m_set = false;   // m is the (bf16-rounded) max of some unmasked logit
+    // B operand of the rank-2 mask / shift product: k = 0 -> 1 (picks the key
+    // column kadd), k = 1 -> -m (against a key column of ones).
+    bf16x8 qm = zero8;
+    if (hh == 0) qm[0] = f2bf(1.f);
+    // One 64-key block: fetch the next K/V tile, consume the current one.
+    auto block = [&](int kb) {
       const int k0 = kb * 64;
       // next tile: (hd, kb + 1) or (hd + 1, 0); the very last iteration refetches itself
       int hn = hd, kn = k0 + 64;
@@ -272,7 +318,6 @@ __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
         if (hd + 1 == H) kn = k0;
       }
       gload(hn, kn);
-      bload(hn, kn, bn);
       if (active) {
         const bf16* ks = smem + st * kStage;
         const bf16* vs = ks + 2 * kTile;
@@ -280,39 +325,67 @@ __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
         if (hh == 0) {
           km0[0] = kadd[k0 + krow];
           km1[0] = kadd[k0 + 32 + krow];
+          km0[1] = f2bf(1.f);
+          km1[1] = f2bf(1.f);
         }
-        f32x16 s0 = zero16(), s1 = zero16();
-        s0 = mfma32(load8(ks + t_off(krow, hh)), qf0, s0);
-        s1 = mfma32(load8(ks + kTile + t_off(krow, hh)), qf0, s1);
+        // Logits minus the running max m, all on MFMA (no shift while m is
+        // not yet set).  The bias registers are refilled with the next
+        // block's slice as soon as the bias products have been issued.
+        bf16x8 qs = qm;
+        if (!m_set) qs[1] = f2bf(0.f);
+        f32x16 s0 = mfma32(load8(ks + t_off(krow, hh)), qf0, zero16());
+        f32x16 s1 = mfma32(load8(ks + kTile + t_off(krow, hh)), qf0, zero16());
         s0 = mfma32(load8(ks + t_off(krow, 2 + hh)), qf1, s0);
         s1 = mfma32(load8(ks + kTile + t_off(krow, 2 + hh)), qf1, s1);
-        s0 = mfma32(ident[0], bc[0], s0);
-        s1 = mfma32(ident[0], bc[2], s1);
-        s0 = mfma32(ident[1], bc[1], s0);
-        s1 = mfma32(ident[1], bc[3], s1);
-        s0 = mfma32(km0, qone, s0);
-        s1 = mfma32(km1, qone, s1);
-        float bmax = fmaxf(s0[0], s1[0]);
+        s0 = mfma32(ident[0], bias[0], s0);
+        s1 = mfma32(ident[0], bias[2], s1);
+        s0 = mfma32(ident[1], bias[1], s0);
+        s1 = mfma32(ident[1], bias[3], s1);
+        s0 = mfma32(km0, qs, s0);
+        s1 = mfma32(km1, qs, s1);
+        bload(hn, kn, bias);
+        bf16x8 pa[2], pb[2];
+        float psum;
+        bool slow = !m_set;
+        if (!slow) {
 #pragma unroll
-        for (int u = 1; u < 16; ++u) bmax = __builtin_fmaxf(bmax, __builtin_fmaxf(s0[u], s1[u]));
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
-        if (__any(bmax > m + kRescaleSlack)) {
-          const float m_new = fmaxf(m, bmax);
+          for (int u = 0; u < 16; ++u) {
+            pa[u >> 3][u & 7] = f2bf(fast_exp2(s0[u]));
+            pb[u >> 3][u & 7] = f2bf(fast_exp2(s1[u]));
+          }
+          psum = sum8_bf16(pa[1], sum8_bf16(pa[0], 0.f)) + sum8_bf16(pb[1], sum8_bf16(pb[0], 0.f));
+          // a sum above 2^16 may hold a weight above 2^16: move m (rare)
+          slow = __any(psum > kSlackSum);
+          if (slow) {
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+              s0[u] += m;
+              s1[u] += m;
+            }
+          }
+        }
+        if (slow) {
+          // s0, s1 hold the unshifted logits here
+          float bmax = fmaxf(s0[0], s1[0]);
+#pragma unroll
+          for (int u = 1; u < 16; ++u) bmax = __builtin_fmaxf(bmax, __builtin_fmaxf(s0[u], s1[u]));
+          bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+          // the shift is kept bf16-representable: it enters the MFMA as -m
+          const float m_new = bf2f(f2bf(fmaxf(m, bmax)));
           const float alpha = fast_exp2(m - m_new);
           m = m_new;
           l *= alpha;
 #pragma unroll
           for (int u = 0; u < 16; ++u) o[u] *= alpha;
-        }
-        float psum = 0.f;
-        bf16x8 pa[2], pb[2];
+          // a block of masked keys only (logits ~ -1e30) does not set m
+          m_set = m_set || __all(m > -1e29f);
+          if (hh == 0) qm[1] = f2bf(-m);
 #pragma unroll
-        for (int u = 0; u < 16; ++u) {
-          const float p0 = fast_exp2(s0[u] - m);
-          const float p1 = fast_exp2(s1[u] - m);
-          psum += p0 + p1;
-          pa[u >> 3][u & 7] = f2bf(p0);
-          pb[u >> 3][u & 7] = f2bf(p1);
+          for (int u = 0; u < 16; ++u) {
+            pa[u >> 3][u & 7] = f2bf(fast_exp2(s0[u] - m));
+            pb[u >> 3][u & 7] = f2bf(fast_exp2(s1[u] - m));
+          }
+          psum = sum8_bf16(pa[1], sum8_bf16(pa[0], 0.f)) + sum8_bf16(pb[1], sum8_bf16(pb[0], 0.f));
         }
         l += psum;
         o = mfma32(load8(vs + t_off(krow, 2 * hh)), pa[0], o);
@@ -324,46 +397,30 @@ __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
       st ^= 1;
       __syncthreads();
     };
-    // Two blocks per trip with the bias registers ping-ponged (no copies).
-    // nk is even for every head but the fetch chain crosses heads, so the
-    // roles of bcur / bnext alternate on a global parity.
-    int kb = 0;
-    for (; kb + 1 < nk; kb += 2) {
-      block(kb, bcur, bnext);
-      block(kb + 1, bnext, bcur);
-    }
-    if (kb < nk) {
-      block(kb, bcur, bnext);
-#pragma unroll
-      for (int x = 0; x < 4; ++x) bcur[x] = bnext[x];
-    }
-    // head finished: normalise and pack
+#pragma unroll 1
+    for (int kb = 0; kb < nk; ++kb) block(kb);
+    // head finished: o / l (bf16) parked in this head's q slot
     const float inv = 1.0f / (l + __shfl_xor(l, 32));
-    bf16x8 r0, r1;
+    float r[16];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      r0[u] = f2bf(o[u] * inv);
-      r1[u] = f2bf(o[8 + u] * inv);
-    }
-#pragma unroll
-    for (int h2 = 0; h2 < H; ++h2)
-      if (h2 == hd) {
-        gob[2 * h2] = r0;
-        gob[2 * h2 + 1] = r1;
-      }
+    for (int u = 0; u < 16; ++u) r[u] = o[u] * inv;
+    if (active) store16(qio + (unsigned)qrow * C + hd * DH + 16 * hh, r);
   }
   if (!active) return;
 
   // Gate: g * (o / l) per head, as the out-projection's B operand.
+  bf16x8 gob[2 * H];
   {
     const bf16* grow = buf.g + (frow + q0 + n) * C + 16 * hh;
+    const bf16* orow = qio + (unsigned)qrow * C + 16 * hh;
 #pragma unroll
     for (int hd = 0; hd < H; ++hd) {
       const bf16x8 g0 = load8(grow + hd * DH), g1 = load8(grow + hd * DH + 8);
+      const bf16x8 o0 = load8(orow + hd * DH), o1 = load8(orow + hd * DH + 8);
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        gob[2 * hd][u] = f2bf(bf2f(g0[u]) * bf2f(gob[2 * hd][u]));
-        gob[2 * hd + 1][u] = f2bf(bf2f(g1[u]) * bf2f(gob[2 * hd + 1][u]));
+        gob[2 * hd][u] = f2bf(bf2f(g0[u]) * bf2f(o0[u]));
+        gob[2 * hd + 1][u] = f2bf(bf2f(g1[u]) * bf2f(o1[u]));
       }
     }
   }

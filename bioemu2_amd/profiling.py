@@ -1,0 +1,165 @@
+"""Summaries of rocprofv3 output for the kernels of this library.
+
+    python -m bioemu2_amd.profiling stats  <kernel_stats.csv> --title T --cmd C [--out F]
+    python -m bioemu2_amd.profiling traffic --fetch <counter_collection.csv> --write <counter_collection.csv>
+                                            --workload block --calib-bytes B --cmd C [--out F] [--json J]
+
+``stats`` turns a ``--kernel-trace --stats -f csv`` kernel table into a short
+markdown table.  ``traffic`` turns two ``--pmc FETCH_SIZE`` / ``--pmc
+WRITE_SIZE`` runs of ``bench.py --calibrate-bytes B`` into HBM bytes per launch
+for every kernel: each counter (KiB per dispatch) is scaled by what the same
+counter reads for torch's elementwise negation of a B-byte bf16 tensor, which
+moves exactly B bytes in and B bytes out.  The per-kernel figures are merged
+into ``profiles/traffic.json`` under the workload name, which ``bench.py``
+reports as ``roofline.traffic``.
+"""
+
+from __future__ import annotations
+
+import argparse
+import csv
+import json
+import re
+from collections import defaultdict
+from pathlib import Path
+
+TRAFFIC_JSON = Path(__file__).resolve().parents[1] / "profiles" / "traffic.json"
+
+# Kernel-timer names whose kernel function is named differently.
+TIMER_TO_KERNEL = {"apb_pair_bias": "pair_bias", "token_layernorm": "token_ln"}
+
+
+def short_name(mangled: str) -> str:
+    """`_ZN6bioemu12_GLOBAL__N_1<len><name>...` -> name (with a bool/int template tag)."""
+    m = re.match(r"_ZN6bioemu12_GLOBAL__N_1(\d+)", mangled)
+    if m:
+        k = int(m.group(1))
+        name = mangled[m.end():m.end() + k]
+        rest = mangled[m.end() + k:]
+        if rest.startswith("ILb1"):
+            return name + "<true>"
+        if rest.startswith("ILb0"):
+            return name + "<false>"
+        mm = re.match(r"ILi(\d+)ELb(\d)", rest)
+        if mm:
+            return f"{name}<epi={mm.group(1)},trans={mm.group(2)}>"
+        mm = re.match(r"ILi(\d+)E", rest)
+        if mm:
+            return f"{name}<{mm.group(1)}>"
+        return name
+    m = re.search(r"bioemu::\(anonymous namespace\)::(\w+)(<[^>(]*>)?", mangled)
+    if m:
+        return m.group(1) + (m.group(2) or "")
+    return mangled[:60]
+
+
+def is_library_kernel(name: str) -> bool:
+    return name.startswith("_ZN6bioemu") or re.match(r"(void )?bioemu::", name) is not None
+
+
+def base_name(short: str) -> str:
+    """Kernel function name without template tag and `_kernel` suffix."""
+    return re.sub(r"<.*>$", "", short).removesuffix("_kernel")
+
+
+def stats_markdown(path: str, title: str, cmd: str) -> str:
+    rows = list(csv.DictReader(open(path)))
+    out = [f"# {title}", "", "Command (from the repo root on the MI355X box):", "", "```", cmd, "```", "",
+           "| kernel | calls | avg µs | min µs | max µs | % of GPU time |", "|---|---|---|---|---|---|"]
+    for r in rows:
+        out.append(f"| `{short_name(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
+                   f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | {float(r['Percentage']):.2f} |")
+    return "\n".join(out) + "\n"
+
+
+def _per_dispatch(path: str, counter: str) -> list[tuple[str, float]]:
+    """(kernel name, counter value in KiB) per dispatch, summed over dimensions."""
+    acc: dict[int, list] = {}
+    for r in csv.DictReader(open(path)):
+        if r["Counter_Name"] != counter:
+            continue
+        d = int(r["Dispatch_Id"])
+        e = acc.setdefault(d, [r["Kernel_Name"], 0.0])
+        e[1] += float(r["Counter_Value"])
+    return [tuple(acc[d]) for d in sorted(acc)]
+
+
+def _calibration(dispatches: list[tuple[str, float]]) -> float:
+    cal = [v for n, v in dispatches if "neg_kernel" in n]
+    if not cal:
+        raise SystemExit("no calibration dispatch (torch neg kernel) in the counter file")
+    return max(cal)
+
+
+def traffic(fetch_csv: str, write_csv: str, calib_bytes: int) -> tuple[dict, float, float]:
+    """Per kernel base name: average HBM read/write bytes per launch after calibration."""
+    fetch = _per_dispatch(fetch_csv, "FETCH_SIZE")
+    write = _per_dispatch(write_csv, "WRITE_SIZE")
+    f_scale = calib_bytes / _calibration(fetch)
+    w_scale = calib_bytes / _calibration(write)
+    table: dict[str, dict] = {}
+    for counter, disp, scale in (("read", fetch, f_scale), ("write", write, w_scale)):
+        sums: dict[str, list] = defaultdict(lambda: [0.0, 0])
+        for name, v in disp:
+            if not is_library_kernel(name):
+                continue
+            s = sums[base_name(short_name(name))]
+            s[0] += v * scale
+            s[1] += 1
+        for k, (tot, n) in sums.items():
+            table.setdefault(k, {})[counter] = tot / n
+    for k, v in table.items():
+        v["total"] = v.get("read", 0.0) + v.get("write", 0.0)
+    # KiB of counter per real KiB moved: 1 / scale
+    return table, 1024.0 / f_scale, 1024.0 / w_scale
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser()
+    sub = ap.add_subparsers(dest="cmd_name", required=True)
+    s = sub.add_parser("stats")
+    s.add_argument("csv")
+    s.add_argument("--title", required=True)
+    s.add_argument("--cmd", required=True)
+    s.add_argument("--out")
+    t = sub.add_parser("traffic")
+    t.add_argument("--fetch", required=True)
+    t.add_argument("--write", required=True)
+    t.add_argument("--workload", required=True)
+    t.add_argument("--calib-bytes", type=int, required=True)
+    t.add_argument("--cmd", required=True, help="the two rocprofv3 commands, as run")
+    t.add_argument("--out")
+    t.add_argument("--json", default=str(TRAFFIC_JSON))
+    a = ap.parse_args(argv)
+    if a.cmd_name == "stats":
+        text = stats_markdown(a.csv, a.title, a.cmd)
+    else:
+        table, f_per_kib, w_per_kib = traffic(a.fetch, a.write, a.calib_bytes)
+        lines = [f"# HBM traffic per launch — workload `{a.workload}`", "",
+                 "Commands (from the repo root on the MI355X box):", "", "```", a.cmd, "```", "",
+                 f"Calibration: torch's negation of a {a.calib_bytes} B bf16 tensor (reads and writes exactly that many "
+                 f"bytes) read FETCH_SIZE {f_per_kib:.4f} KiB and WRITE_SIZE {w_per_kib:.4f} KiB per real KiB; "
+                 "kernel counters below are divided by those factors.", "",
+                 "| kernel | read MB | write MB | total MB |", "|---|---|---|---|"]
+        for k, v in sorted(table.items(), key=lambda kv: -kv[1]["total"]):
+            lines.append(f"| `{k}` | {v.get('read', 0) / 1e6:.1f} | {v.get('write', 0) / 1e6:.1f} | "
+                         f"{v['total'] / 1e6:.1f} |")
+        text = "\n".join(lines) + "\n"
+        path = Path(a.json)
+        try:
+            data = json.loads(path.read_text())
+        except (OSError, ValueError):
+            data = {}
+        data[a.workload] = {k: round(v["total"]) for k, v in table.items()}
+        data.setdefault("_calibration", {})[a.workload] = {"fetch_kib_per_kib": round(f_per_kib, 5),
+                                                           "write_kib_per_kib": round(w_per_kib, 5)}
+        path.write_text(json.dumps(data, indent=1, sort_keys=True) + "\n")
+    if a.out:
+        Path(a.out).write_text(text)
+    else:
+        print(text, end="")
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())
