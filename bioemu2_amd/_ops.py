@@ -221,6 +221,10 @@ def _(z, mask, norm_w, norm_b, w_proj, w_o, starting, num_heads):
 # ----------------------------------------------------------------------------
 # Transition (SwiGLU MLP)
 # ----------------------------------------------------------------------------
+def transition_pair_workspace_bytes(D: int, hidden: int) -> int:
+    return int(lib().bioemu_transition_pair_workspace_bytes(D, hidden))
+
+
 def launch_transition_pair(
     x: Tensor,
     norm_w: Tensor | None,
@@ -230,6 +234,7 @@ def launch_transition_pair(
     fc3_w: Tensor,
     out: Tensor,
     residual: bool = False,
+    ws: Tensor | None = None,
 ) -> Tensor:
     require_gpu(x, "transition")
     D = x.shape[-1]
@@ -245,9 +250,12 @@ def launch_transition_pair(
     if use_norm:
         _check_tensor(norm_w, "transition norm.weight", torch.float32, (D,), dev)
         _check_tensor(norm_b, "transition norm.bias", torch.float32, (D,), dev)
+    need = transition_pair_workspace_bytes(D, hidden)
+    if ws is None or ws.numel() < need:
+        ws = workspace(need, dev)
     rc = lib().bioemu_transition_pair_fwd(
         _ptr(x), _ptr(norm_w), _ptr(norm_b), _ptr(fc1_w), _ptr(fc2_w), _ptr(fc3_w), _ptr(out),
-        P, D, hidden, int(use_norm), int(bool(residual)), _stream(x),
+        _ptr(ws), ctypes.c_size_t(ws.numel()), P, D, hidden, int(use_norm), int(bool(residual)), _stream(x),
     )
     check(rc, "bioemu_transition_pair_fwd")
     return out

@@ -59,6 +59,7 @@ class PairformerBlockHip(nn.Module):
             _ops.triatt_workspace_bytes(B, N, self.c_z, self.tri_att_start.num_heads),
             _ops.apb_workspace_bytes(B, 1, N, self.c_s, self.apb_heads),
             _ops.transition_token_workspace_bytes(B * N, self.c_s, self.transition_s.hidden),
+            _ops.transition_pair_workspace_bytes(self.c_z, self.transition_z.hidden),
         )
 
     def _workspace(self, B: int, N: int, device) -> Tensor:
@@ -87,7 +88,7 @@ class PairformerBlockHip(nn.Module):
         _ops.launch_trimul(z, pm, *self.tri_mul_in.prepared_params(), z, False, residual=True, ws=ws)
         _ops.launch_triatt(z, pm, *self.tri_att_start.prepared_params(), z, True, residual=True, ws=ws)
         _ops.launch_triatt(z, pm, *self.tri_att_end.prepared_params(), z, False, residual=True, ws=ws)
-        _ops.launch_transition_pair(z, *self.transition_z.prepared_params(), z, residual=True)
+        _ops.launch_transition_pair(z, *self.transition_z.prepared_params(), z, residual=True, ws=ws)
         _ops.launch_apb(s, z, tok, *self.attention_pair_bias.prepared_params(), s, self.apb_heads,
                         residual=True, ws=ws)
         _ops.launch_transition_token(s, *self.transition_s.prepared_params(), s, residual=True, ws=ws)

@@ -99,11 +99,14 @@ int bioemu_triatt_fwd(const void* z, const uint8_t* mask, const float* norm_w, c
  * the pair representation.  x, out: [P, D] bf16 rows (P = B*N*N), out may equal
  * x when residual != 0.  fc1_w, fc2_w: [hidden, D]; fc3_w: [D, hidden].
  * D must be 128 and hidden 512.  use_norm=0 skips the LayerNorm (norm_* unused).
+ * The workspace holds fc1/fc2 with the LayerNorm affine folded in (size from
+ * bioemu_transition_pair_workspace_bytes, independent of P).
  */
+size_t bioemu_transition_pair_workspace_bytes(int64_t D, int64_t hidden);
 int bioemu_transition_pair_fwd(const void* x, const float* norm_w, const float* norm_b,
                                const void* fc1_w, const void* fc2_w, const void* fc3_w, void* out,
-                               int64_t P, int64_t D, int64_t hidden, int use_norm, int residual,
-                               hipStream_t stream);
+                               void* workspace, size_t workspace_bytes, int64_t P, int64_t D,
+                               int64_t hidden, int use_norm, int residual, hipStream_t stream);
 
 /*
  * Token Transition (same op over [M, D] rows of the single representation,

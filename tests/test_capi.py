@@ -65,6 +65,9 @@ def test_host_only_queries():
     folded = 2 * 128 * 128 * 2 + 2 * 128 * 4  # folded output weights and biases
     assert lib.bioemu_trimul_workspace_bytes(1, n, 128) == 3 * 128 * np_ * np_ * 2 + folded
     assert lib.bioemu_trimul_workspace_bytes(0, n, 128) == 0
+    # folded fc1 | fc2 ([1024][128] bf16) and their bias pairs ([1024][2] bf16)
+    assert lib.bioemu_transition_pair_workspace_bytes(128, 512) == 1024 * 128 * 2 + 1024 * 4
+    assert lib.bioemu_transition_pair_workspace_bytes(64, 256) == 0
 
 
 def test_invalid_arguments_rejected_without_gpu():
