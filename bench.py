@@ -89,8 +89,7 @@ def main() -> int:
     args = _parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(
-            "bench.py measures one MI355X only: this build has no multi-GPU path "
-            "(how the ops would shard is described in DESIGN.md). Run with --gpus 1.",
+            "bench.py measures one MI355X only: this build has no multi-GPU path. Run with --gpus 1.",
             file=sys.stderr,
         )
         return 2
