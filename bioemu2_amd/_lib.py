@@ -48,6 +48,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _c_int,
         [_c_void_p] * 7 + [_c_void_p, _c_size_t] + [_c_int64] * 3 + [_c_int, _c_int, _c_void_p],
     ),
+    "bioemu_pwa_workspace_bytes": (_c_size_t, [_c_int64] * 6),
+    "bioemu_pwa_fwd": (
+        _c_int,
+        [_c_void_p] * 12 + [_c_void_p, _c_size_t] + [_c_int64] * 7 + [_c_int, _c_void_p],
+    ),
     "bioemu_apb_workspace_bytes": (_c_size_t, [_c_int64] * 5),
     "bioemu_apb_fwd": (
         _c_int,

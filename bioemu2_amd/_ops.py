@@ -495,6 +495,97 @@ def launch_opm(
     return out
 
 
+# ----------------------------------------------------------------------------
+# Pair-weighted averaging (MSA module)
+# ----------------------------------------------------------------------------
+def pwa_workspace_bytes(B: int, S: int, N: int, c_m: int, c_h: int, H: int) -> int:
+    return int(lib().bioemu_pwa_workspace_bytes(B, S, N, c_m, c_h, H))
+
+
+def launch_pwa(
+    m: Tensor,
+    z: Tensor,
+    mask_u8: Tensor,
+    norm_m_w: Tensor,
+    norm_m_b: Tensor,
+    w_m: Tensor,
+    w_g: Tensor,
+    norm_z_w: Tensor,
+    norm_z_b: Tensor | None,
+    w_z: Tensor,
+    w_o: Tensor,
+    out: Tensor,
+    num_heads: int,
+    residual: bool = False,
+    ws: Tensor | None = None,
+) -> Tensor:
+    require_gpu(m, "pair_weighted_averaging")
+    if m.ndim != 4 or z.ndim != 4:
+        raise ValueError(f"pwa: m must be [B,S,N,c_m] and z [B,N,N,c_z], got {tuple(m.shape)}, {tuple(z.shape)}")
+    B, S, N, c_m = m.shape
+    c_z = z.shape[-1]
+    H = num_heads
+    c_h = w_m.shape[0] // H
+    dev = m.device
+    _check_tensor(m, "pwa m", BF16, (B, S, N, c_m), dev)
+    _check_tensor(z, "pwa z", BF16, (B, N, N, c_z), dev)
+    _check_tensor(mask_u8, "pwa mask", torch.uint8, (B, N, N), dev)
+    _check_tensor(norm_m_w, "pwa norm_m.weight", torch.float32, (c_m,), dev)
+    _check_tensor(norm_m_b, "pwa norm_m.bias", torch.float32, (c_m,), dev)
+    _check_tensor(w_m, "pwa proj_m.weight", BF16, (H * c_h, c_m), dev)
+    _check_tensor(w_g, "pwa proj_g.weight", BF16, (H * c_h, c_m), dev)
+    _check_tensor(norm_z_w, "pwa norm_z.weight", torch.float32, (c_z,), dev)
+    if norm_z_b is not None:
+        _check_tensor(norm_z_b, "pwa norm_z.bias", torch.float32, (c_z,), dev)
+    _check_tensor(w_z, "pwa proj_z.weight", BF16, (H, c_z), dev)
+    _check_tensor(w_o, "pwa proj_o.weight", BF16, (c_m, H * c_h), dev)
+    _check_tensor(out, "pwa out", BF16, (B, S, N, c_m), dev)
+    need = pwa_workspace_bytes(B, S, N, c_m, c_h, H)
+    if need == 0:
+        raise ValueError(f"pwa: unsupported widths c_m={c_m} c_h={c_h} heads={H} (supported: 64, 32, 8)")
+    if ws is None or ws.numel() < need:
+        ws = workspace(need, dev)
+    rc = lib().bioemu_pwa_fwd(
+        _ptr(m), _ptr(z), _ptr(mask_u8), _ptr(norm_m_w), _ptr(norm_m_b), _ptr(w_m), _ptr(w_g), _ptr(norm_z_w),
+        _ptr(norm_z_b), _ptr(w_z), _ptr(w_o), _ptr(out), _ptr(ws), ctypes.c_size_t(ws.numel()),
+        B, S, N, c_m, c_z, c_h, H, int(bool(residual)), _stream(m),
+    )
+    check(rc, "bioemu_pwa_fwd")
+    return out
+
+
+@torch.library.custom_op("bioemu_mi355x::pair_weighted_averaging", mutates_args=(), device_types="cuda")
+def pair_weighted_averaging(
+    m: Tensor,
+    z: Tensor,
+    mask: Tensor,
+    norm_m_w: Tensor,
+    norm_m_b: Tensor,
+    w_m: Tensor,
+    w_g: Tensor,
+    norm_z_w: Tensor,
+    norm_z_b: Tensor | None,
+    w_z: Tensor,
+    w_o: Tensor,
+    num_heads: int,
+) -> Tensor:
+    mb = m.to(BF16).contiguous()
+    out = torch.empty_like(mb)
+    f32 = torch.float32
+    launch_pwa(
+        mb, z.to(BF16).contiguous(), mask_u8(mask), norm_m_w.to(f32).contiguous(), norm_m_b.to(f32).contiguous(),
+        w_m.to(BF16).contiguous(), w_g.to(BF16).contiguous(), norm_z_w.to(f32).contiguous(),
+        None if norm_z_b is None else norm_z_b.to(f32).contiguous(), w_z.to(BF16).contiguous(),
+        w_o.to(BF16).contiguous(), out, num_heads,
+    )
+    return out.to(m.dtype)
+
+
+@pair_weighted_averaging.register_fake
+def _(m, z, mask, norm_m_w, norm_m_b, w_m, w_g, norm_z_w, norm_z_b, w_z, w_o, num_heads):
+    return torch.empty_like(m)
+
+
 @torch.library.custom_op("bioemu_mi355x::outer_product_mean", mutates_args=(), device_types="cuda")
 def outer_product_mean(
     m: Tensor, mask: Tensor, norm_w: Tensor, norm_b: Tensor, w_ab: Tensor, w_o: Tensor, b_o: Tensor

@@ -6,8 +6,7 @@
 namespace bioemu {
 namespace {
 
-constexpr int kC = 128;
-
+template <int kC>
 __global__ __launch_bounds__(kC) void fold_ln_kernel(const bf16* __restrict__ w, const float* __restrict__ gamma,
                                                      const float* __restrict__ beta, bf16* __restrict__ wf,
                                                      bf16* __restrict__ cf) {
@@ -32,11 +31,16 @@ __global__ __launch_bounds__(kC) void fold_ln_kernel(const bf16* __restrict__ w,
 }  // namespace
 
 int launch_fold_ln(const void* w, const float* gamma, const float* beta, void* wf, void* cf, int64_t rows,
-                   hipStream_t stream) {
+                   hipStream_t stream, int width) {
   if (rows <= 0 || rows > 65535) return set_error(BIOEMU_ERR_INVALID_ARG, "fold_ln: bad row count %lld", (long long)rows);
+  if (width != 64 && width != 128) return set_error(BIOEMU_ERR_INVALID_ARG, "fold_ln: width %d unsupported", width);
   KernelTimerScope timed("fold_ln", stream);
-  hipLaunchKernelGGL(fold_ln_kernel, dim3((unsigned)rows), dim3(kC), 0, stream, static_cast<const bf16*>(w), gamma,
-                     beta, static_cast<bf16*>(wf), static_cast<bf16*>(cf));
+  if (width == 128)
+    hipLaunchKernelGGL(fold_ln_kernel<128>, dim3((unsigned)rows), dim3(128), 0, stream, static_cast<const bf16*>(w),
+                       gamma, beta, static_cast<bf16*>(wf), static_cast<bf16*>(cf));
+  else
+    hipLaunchKernelGGL(fold_ln_kernel<64>, dim3((unsigned)rows), dim3(64), 0, stream, static_cast<const bf16*>(w),
+                       gamma, beta, static_cast<bf16*>(wf), static_cast<bf16*>(cf));
   return check_launch("fold_ln");
 }
 

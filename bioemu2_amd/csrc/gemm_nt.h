@@ -1,0 +1,113 @@
+// One 256 x 256 output tile of C = A B^T on MFMA, A and B row-major with k
+// contiguous (an "NT" GEMM), for gfx950.  Shared by the triangle contraction
+// (bgemm.hip) and the pair-weighted-averaging contraction (pwa.hip), which
+// differ only in their epilogues.
+//
+// Tiling: BK = 64, 512 threads = 8 waves in a 4 (i) x 2 (j) grid, each wave
+// 64 (i) x 128 (j) = 2 x 4 MFMA 32x32x16 blocks.  Per 16-deep k-step a wave
+// reads 6 operand fragments for 8 MFMAs.  The MFMA A operand is the B tile
+// (rows j, permuted with perm32) and the B operand is the A tile (rows i), so
+// accumulator acc[jb][ib], lane (ln, lh), register u holds
+//   C[i = wi*64 + ib*32 + ln][j = wj*128 + jb*32 + 16 lh + u]
+// (16 consecutive j of one i: epilogues write 32-byte runs).
+// Global -> LDS staging uses buffer loads with an LDS destination (1 KB per
+// instruction, no registers), double-buffered: k-tile kt + 1 is in flight
+// while kt is multiplied.  LDS rows are 128 bytes, unpadded, with the 16-byte
+// chunk index XOR-swizzled per row.  The k reduction order is fixed (k = 0,
+// 1, ... in 16-wide MFMA steps), so appending zero-valued k columns never
+// changes a result bit.
+#pragma once
+
+#include "common.h"
+#include "pairtile.h"
+
+namespace bioemu {
+
+constexpr int kNtTile = 256;                   // BM = BN
+constexpr int kNtBK = 64;
+constexpr int kNtThreads = 512;
+constexpr int kNtTileElems = kNtTile * kNtBK;  // one operand tile: [256 rows][8 chunks of 8]
+constexpr int kNtStage = 2 * kNtTileElems;     // A tile | B tile
+constexpr int kNtSmem = 2 * kNtStage * 2;      // bytes: double-buffered, 128 KB
+constexpr int kNtXcds = 8;
+
+// 16-byte chunk swizzle of a 128-byte tile row: conflict-free both for rows
+// read in natural order and in perm32 order (16 lanes -> 16 bank groups).
+__device__ __forceinline__ int nt_swz(int r) { return ((r >> 1) & 7) ^ (((r >> 4) & 1) << 2); }
+__device__ __forceinline__ int nt_off(int r, int c) { return (r * 8 + (c ^ nt_swz(r))) * 8; }
+
+__device__ __forceinline__ void nt_copy16_to_lds(__amdgpu_buffer_rsrc_t r, const bf16* lds, unsigned voff,
+                                                 unsigned soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(lds), 16, voff, soff, 0, 0);
+}
+
+// A points at the tile's first row of A (256 rows of K), B at the tile's first
+// row of B; K % 64 == 0 and 256 * K * 2 < 2^32.  Whole workgroup; smem holds
+// kNtSmem bytes.  Ends with a barrier-free epilogue-ready acc.
+__device__ __forceinline__ void gemm_nt_tile(const bf16* A, const bf16* B, int K, bf16* smem, f32x16 (&acc)[4][2]) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ln = lane & 31, lh = lane >> 5;
+  const int wi = wave & 3, wj = wave >> 2;
+  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(A, (unsigned)kNtTile * K * 2);
+  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(B, (unsigned)kNtTile * K * 2);
+  // Each operand tile (256 rows x 128 B) is 32 copies of 1 KB; wave w moves
+  // copies w, w + 8, w + 16, w + 24 of A and of B.  Copy j writes LDS chunk
+  // 64 j + lane = (row, swizzled chunk) of the tile.
+  unsigned voff[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int p = (wave + 8 * q) * 64 + lane, r = p >> 3, c = (p & 7) ^ nt_swz(p >> 3);
+    voff[q] = (unsigned)(r * K + c * 8) * 2;
+  }
+  auto stage = [&](int kt) {
+    bf16* st = smem + (kt & 1) * kNtStage;
+    const unsigned soff = (unsigned)(kt * kNtBK) * 2;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      nt_copy16_to_lds(ra, st + (wave + 8 * q) * 512, voff[q], soff);
+      nt_copy16_to_lds(rb, st + kNtTileElems + (wave + 8 * q) * 512, voff[q], soff);
+    }
+  };
+
+#pragma unroll
+  for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+    for (int ib = 0; ib < 2; ++ib) acc[jb][ib] = zero16();
+
+  const int nk = K / kNtBK;
+  stage(0);
+  const int jrow = perm32(ln);
+#pragma unroll 1
+  for (int kt = 0; kt < nk; ++kt) {
+    __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's copies of k-tile kt landed
+    __syncthreads();                       // ... and everyone's; the other stage is free again
+    if (kt + 1 < nk) stage(kt + 1);
+    const bf16* sa = smem + (kt & 1) * kNtStage;
+    const bf16* sb = sa + kNtTileElems;
+#pragma unroll
+    for (int ks = 0; ks < kNtBK / 16; ++ks) {
+      bf16x8 fj[4], fi[2];
+#pragma unroll
+      for (int jb = 0; jb < 4; ++jb) fj[jb] = load8(sb + nt_off(wj * 128 + jb * 32 + jrow, 2 * ks + lh));
+#pragma unroll
+      for (int ib = 0; ib < 2; ++ib) fi[ib] = load8(sa + nt_off(wi * 64 + ib * 32 + ln, 2 * ks + lh));
+#pragma unroll
+      for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+        for (int ib = 0; ib < 2; ++ib) acc[jb][ib] = mfma32(fj[jb], fi[ib], acc[jb][ib]);
+    }
+  }
+}
+
+// XCD-aware work-item order: workgroup w runs on XCD w % 8; each XCD gets a
+// contiguous range of items (so the tiles of one plane share its L2).
+// grid = items rounded up to a multiple of 8; returns -1 for padding groups.
+__device__ __forceinline__ int nt_item(int total) {
+  const int w = blockIdx.x;
+  const int per_xcd = (total + kNtXcds - 1) / kNtXcds;
+  const int item = (w % kNtXcds) * per_xcd + w / kNtXcds;
+  return item < total ? item : -1;
+}
+
+}  // namespace bioemu

@@ -40,11 +40,14 @@ constexpr int kGemmTile = 256;
 int launch_bgemm_nt(const void* A, const void* B, void* C, int64_t batch, int64_t n,
                     hipStream_t stream);
 
-// LayerNorm folding (fold.hip): wf = W diag(gamma) [rows][128] bf16, cf = W beta
-// as bf16 (hi, lo) pairs [rows][2]; beta may be null.  W is [rows][128] bf16.
+// LayerNorm folding (fold.hip): wf = W diag(gamma) [rows][width] bf16, cf = W beta
+// as bf16 (hi, lo) pairs [rows][2]; beta may be null.  W is [rows][width] bf16,
+// width 128 (default) or 64.
 int launch_fold_ln(const void* w, const float* gamma, const float* beta, void* wf, void* cf, int64_t rows,
-                   hipStream_t stream);
-inline size_t fold_bytes(int64_t rows) { return (size_t)round_up(rows * 128 * 2, 256) + (size_t)round_up(rows * 4, 256); }
+                   hipStream_t stream, int width = 128);
+inline size_t fold_bytes(int64_t rows, int64_t width = 128) {
+  return (size_t)round_up(rows * width * 2, 256) + (size_t)round_up(rows * 4, 256);
+}
 
 // Token-side helpers (token.hip).  Rows are B batches of N tokens stored
 // padded to Np rows each; see token.hip for the row conventions.

@@ -120,6 +120,23 @@ int bioemu_transition_token_fwd(const void* x, const float* norm_w, const float*
                                 int64_t hidden, int use_norm, int residual, hipStream_t stream);
 
 /*
+ * Pair-weighted averaging (MSA module), fused: LN_m -> v = Wm m', g = sigmoid(Wg m');
+ * w = softmax_j(LN_z(z) Wz^T, keys with mask 0 replaced by -1e6);
+ * o[s,i,h] = sum_j w[h,i,j] v[s,j,h];  out = (g * o) Wo^T (+ m when residual).
+ * Replaces PairWeightedAveraging.forward
+ * (src/bioemu2/biomoa/ops/pair_weighted_averaging.py:59-154; both of its
+ * chunk_heads paths compute these values).  m, out: [B, S, N, c_m] bf16 (out
+ * may equal m when residual != 0); z: [B, N, N, c_z] bf16; mask: [B, N, N]
+ * uint8.  norm_z_b may be null (use_bias_in_layer_norm=False).  Supported:
+ * c_m = 64, c_z = 128, c_h = 32, H = 8, N <= 4096.
+ */
+size_t bioemu_pwa_workspace_bytes(int64_t B, int64_t S, int64_t N, int64_t c_m, int64_t c_h, int64_t H);
+int bioemu_pwa_fwd(const void* m, const void* z, const uint8_t* mask, const float* norm_m_w, const float* norm_m_b,
+                   const void* w_m, const void* w_g, const float* norm_z_w, const float* norm_z_b, const void* w_z,
+                   const void* w_o, void* out, void* workspace, size_t workspace_bytes, int64_t B, int64_t S,
+                   int64_t N, int64_t c_m, int64_t c_z, int64_t c_h, int64_t H, int residual, hipStream_t stream);
+
+/*
  * Attention with pair bias over the single representation.
  * Replaces AttentionPairBias.forward (src/bioemu2/biomoa/ops/attention_pair_bias.py:128-225)
  * with the non-fused bias branch (_proj_z_fused, :114-117):

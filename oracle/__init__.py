@@ -11,7 +11,7 @@ follows.  Parameters are passed as dicts whose keys are the reference modules'
 ``state_dict`` keys, so ``oracle.trimul(x, mask, module.state_dict(), ...)``
 works for both the reference classes and the drop-in HIP classes.
 
-How each function is pinned (see ``tests/test_oracle.py``):
+How each function is pinned (see ``tests/test_oracle_*.py``):
 
 * ``trimul``      — brute-force Python loops (tiny N), the
                     incoming(x) == outgoing(x^T, a<->b swapped)^T identity, the
@@ -28,6 +28,9 @@ How each function is pinned (see ``tests/test_oracle.py``):
                     exact zeros (test_outer_product_mean.py:286-310), the
                     divisor is the per-batch valid-row count (duplicating the
                     MSA leaves the mean unchanged).
+* ``pair_weighted_averaging`` — brute-force loops, the all-masked row (uniform
+                    average over the N keys), a single valid key (o = v of that
+                    key exactly), MSA-row independence of the weights.
 * ``transition``  — brute-force loops and the SwiGLU closed form.
 * ``pairformer_block`` — composition only (AF3 suppl. Alg. 17); each term is
                     pinned above, the order is pinned by a hand-built
@@ -40,6 +43,7 @@ from .pairformer_ref import (  # noqa: F401
     attention_pair_bias,
     outer_product_mean,
     pair_mask_from_token_mask,
+    pair_weighted_averaging,
     pairformer_block,
     transition,
     triangle_attention,

@@ -21,6 +21,7 @@ __all__ = [
     "triangle_attention",
     "attention_pair_bias",
     "outer_product_mean",
+    "pair_weighted_averaging",
     "transition",
     "pairformer_block",
     "pair_mask_from_token_mask",
@@ -247,6 +248,37 @@ def outer_product_mean(
         zc = zc / num_valid[:, None, None, None]  # :74
         out[:, i0:i1] = zc @ wo.T + bo  # :75
     return out
+
+
+# ----------------------------------------------------------------------------
+# Pair-weighted averaging (MSA module)
+# ----------------------------------------------------------------------------
+def pair_weighted_averaging(
+    m: Tensor, z: Tensor, mask: Tensor, params: dict, num_heads: int = 8, c_h: int = 32, inf: float = 1e6
+) -> Tensor:
+    """PairWeightedAveraging.forward, unchunked path (biomoa/ops/pair_weighted_averaging.py:125-153).
+
+    m [B,S,N,c_m], z [B,N,N,c_z], mask [B,N,N] -> [B,S,N,c_m] (float32).
+    m' = LN_m(m) (:84); v = proj_m(m') split into heads (:127-129);
+    b = proj_z(LN_z(z)) per head, masked_fill(~mask, -inf) (:131-143);
+    w = softmax over j (:144); g = sigmoid(proj_g(m')) (:147-148);
+    o[s,i,h] = sum_j w[h,i,j] v[s,j,h] with heads flattened h*c_h + d (:151-153);
+    out = proj_o(g * o) (:154).  LN_z has a bias unless ``norm_z.bias`` is absent
+    (use_bias_in_layer_norm=False, :134-141 -- the same values, computed fused).
+    """
+    m = _f32(m)
+    z = _f32(z)
+    mask = mask.bool().cpu()
+    B, S, N, _ = m.shape
+    mn = _ln(m, params, "norm_m")
+    v = (mn @ _p(params, "proj_m.weight").T).reshape(B, S, N, num_heads, c_h).permute(0, 3, 1, 2, 4)
+    b = (_ln(z, params, "norm_z") @ _p(params, "proj_z.weight").T).permute(0, 3, 1, 2)
+    b = b.masked_fill(~mask[:, None], -inf)
+    w = torch.softmax(b, dim=-1)
+    g = torch.sigmoid(mn @ _p(params, "proj_g.weight").T)
+    o = torch.einsum("bhij,bhsjd->bhsid", w, v)
+    o = o.permute(0, 2, 3, 1, 4).reshape(B, S, N, num_heads * c_h)
+    return (g * o) @ _p(params, "proj_o.weight").T
 
 
 # ----------------------------------------------------------------------------
