@@ -321,9 +321,74 @@ class OpmWorkload(Workload):
         raise KeyError(kernel)
 
 
+class PwaWorkload(Workload):
+    """MSA module shape: PairWeightedAveraging, m [1,1024,512,64] bf16, z [1,512,512,128], trailing
+    10% of tokens padded, residual into m (m += PWA(m, z, pair mask))."""
+
+    def __init__(self, device, n: int = 512, S: int = 1024, seed: int = 0):
+        from .pair_weighted_averaging import PairWeightedAveraging
+
+        self.n, self.S = n, S
+        self.name = f"pwa_s{S}_n{n}"
+        self.metric = f"ms per PairWeightedAveraging at S={S}, N={n} bf16"
+        torch.manual_seed(seed)
+        self.module = init_module(PairWeightedAveraging(64, 128, 32, 8), seed).to(device).eval()
+        g = torch.Generator().manual_seed(seed)
+        self.m_cpu = torch.randn(1, S, n, 64, generator=g).to(torch.bfloat16)
+        self.z_cpu = torch.randn(1, n, n, 128, generator=g).to(torch.bfloat16)
+        self.n_pad = n // 10
+        tok = token_mask(n, self.n_pad, "cpu")
+        self.mask_cpu = tok[:, :, None] & tok[:, None, :]
+        self.m = self.m_cpu.to(device)
+        self.z = self.z_cpu.to(device)
+        self.mask = _ops.mask_u8(self.mask_cpu.to(device))
+        self.ws = _ops.workspace(_ops.pwa_workspace_bytes(1, S, n, 64, 32, 8), device)
+        self.params = self.module.prepared_params()
+        self.config = {"workload": self.name, "S": S, "N": n, "c_m": 64, "c_z": 128, "c_h": 32, "heads": 8,
+                       "padded_tokens": self.n_pad, "residual": True}
+        # v, g projections + per-head averaging + output projection + bias
+        self.flops = (2.0 * S * n * 64 * 512 + 2.0 * 8 * n * n * S * 32 + 2.0 * S * n * 256 * 64
+                      + 2.0 * n * n * 128 * 8)
+
+    def step(self) -> None:
+        _ops.launch_pwa(self.m, self.z, self.mask, *self.params, self.m, 8, residual=True, ws=self.ws)
+
+    def cpu_sample(self, oracle):
+        rows = 16
+        m = self.m_cpu[:, :rows].float()
+        z = self.z_cpu.float()
+        params = {k: v.detach().cpu() for k, v in self.module.state_dict().items()}
+
+        def fn():
+            return oracle.pair_weighted_averaging(m, z, self.mask_cpu, params, num_heads=8, c_h=32)
+
+        return fn, rows / self.S, f"oracle.pair_weighted_averaging fp32 on {rows} of {self.S} MSA rows"
+
+    def kernel_work(self, kernel: str) -> tuple[str, float]:
+        n, S = self.n, self.S
+        npad = -(-n // 256) * 256
+        if kernel == "pwa_contract":
+            # sum_j w[h,i,j] v[s,j,h,:] over the valid keys, every head and MSA row
+            return ("mfma", 2.0 * 8 * n * n * S * 32)
+        if kernel == "pwa_weights":
+            # reads z, writes the 8 weight rows (bf16)
+            return ("hbm", float(n * n * 128 * 2 + 8 * n * npad * 2))
+        if kernel == "pwa_proj":
+            # reads m, writes v^T and g (256 channels each)
+            return ("hbm", float(S * n * 64 * 2 + 2 * S * npad * 256 * 2))
+        if kernel == "pwa_out":
+            # reads g*o (256) and m, writes m
+            return ("hbm", float(S * n * (256 * 2 + 64 * 2 * 2)))
+        if kernel == "fold_ln":
+            return ("hbm", float(2 * (8 * 128 + 512 * 64) * 2))
+        raise KeyError(kernel)
+
+
 def make(op: str, device, n: int | None = None) -> Workload:
     if op == "opm":
         return OpmWorkload(device, n or 512)
+    if op == "pwa":
+        return PwaWorkload(device, n or 512)
     if op == "block":
         return BlockWorkload(device, n or 768)
     if op in ("triatt_start", "triatt_end"):
