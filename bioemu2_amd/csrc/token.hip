@@ -174,6 +174,10 @@ int token_layernorm(const void* x, const float* gamma, const float* beta, void* 
   dim3 grid((unsigned)((rows + 3) / 4));
   KernelTimerScope timed("token_layernorm", stream);
   switch (K) {
+    case 64:
+      hipLaunchKernelGGL(token_ln_kernel<64>, grid, dim3(256), 0, stream, static_cast<const bf16*>(x), gamma, beta,
+                         static_cast<bf16*>(y), (int)B, (int)N, (int)Np, 1e-5f);
+      break;
     case 128:
       hipLaunchKernelGGL(token_ln_kernel<128>, grid, dim3(256), 0, stream, static_cast<const bf16*>(x), gamma, beta,
                          static_cast<bf16*>(y), (int)B, (int)N, (int)Np, 1e-5f);
@@ -183,7 +187,7 @@ int token_layernorm(const void* x, const float* gamma, const float* beta, void* 
                          static_cast<bf16*>(y), (int)B, (int)N, (int)Np, 1e-5f);
       break;
     default:
-      return set_error(BIOEMU_ERR_UNSUPPORTED, "token_layernorm: width %lld unsupported (128 or 384)", (long long)K);
+      return set_error(BIOEMU_ERR_UNSUPPORTED, "token_layernorm: width %lld unsupported (64, 128 or 384)", (long long)K);
   }
   return check_launch("token_layernorm");
 }
@@ -229,7 +233,7 @@ extern "C" int bioemu_transition_token_fwd(const void* x, const float* norm_w, c
                                            const void* fc1_w, const void* fc2_w, const void* fc3_w, void* out,
                                            void* workspace, size_t workspace_bytes, int64_t M, int64_t Dc,
                                            int64_t hidden, int use_norm, int residual, hipStream_t stream) {
-  if (M <= 0 || (Dc != 128 && Dc != 384) || hidden <= 0 || hidden % 32)
+  if (M <= 0 || (Dc != 64 && Dc != 128 && Dc != 384) || hidden <= 0 || hidden % 32)
     return set_error(BIOEMU_ERR_UNSUPPORTED, "transition_token: dim %lld / hidden %lld unsupported", (long long)Dc,
                      (long long)hidden);
   if (!x || !fc1_w || !fc2_w || !fc3_w || !out || !workspace || (use_norm && !norm_w))

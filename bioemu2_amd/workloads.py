@@ -12,6 +12,7 @@ from __future__ import annotations
 
 import json
 import math
+import time
 from pathlib import Path
 
 import torch
@@ -76,10 +77,12 @@ def trimul_kernel_work(name: str, B: int, N: int, c: int = 128) -> tuple[str, fl
     return None
 
 
-def fold_kernel_work(name: str, rows: int) -> tuple[str, float] | None:
+def fold_kernel_work(name: str, launches: int, rows128: int, rows64: int = 0) -> tuple[str, float] | None:
+    """LayerNorm folds: W diag(gamma) and W beta, reading and writing each weight once; the amount
+    per launch averaged over the step's `launches` folds of `rows128` rows of width 128 and
+    `rows64` of width 64."""
     if name == "fold_ln":
-        # W diag(gamma) and W beta for a [rows, 128] weight: reads and writes it once
-        return ("hbm", float(2 * rows * 128 * 2))
+        return ("hbm", float(2 * (rows128 * 128 + rows64 * 64) * 2) / launches)
     return None
 
 
@@ -188,7 +191,7 @@ class TriAttWorkload(Workload):
         return fn, 1.0, f"oracle.triangle_attention fp32, full N={self.n} (64-row chunks)"
 
     def kernel_work(self, kernel: str) -> tuple[str, float]:
-        w = triatt_kernel_work(kernel, 1, self.n) or fold_kernel_work(kernel, 4 * 128 + 4)
+        w = triatt_kernel_work(kernel, 1, self.n) or fold_kernel_work(kernel, 1, 4 * 128 + 4)
         if w is None:
             raise KeyError(kernel)
         return w
@@ -244,8 +247,8 @@ class BlockWorkload(Workload):
             w = fn(kernel, 1, n)
             if w is not None:
                 return w
-        if kernel == "fold_ln":  # triatt (516 rows) x2, APB bias (16 rows), transition (1024 rows)
-            return fold_kernel_work(kernel, (2 * 516 + 16 + 1024) // 4)
+        if kernel == "fold_ln":  # triatt (516 rows) x2, APB bias (16 rows), transition fc1 and fc2 (512 rows each)
+            return fold_kernel_work(kernel, 5, 2 * 516 + 16 + 1024)
         if kernel == "transition_pair":
             return ("mfma", 2.0 * n * n * c * 12 * c)
         if kernel == "apb_pair_bias":
@@ -379,8 +382,158 @@ class PwaWorkload(Workload):
         if kernel == "pwa_out":
             # reads g*o (256) and m, writes m
             return ("hbm", float(S * n * (256 * 2 + 64 * 2 * 2)))
-        if kernel == "fold_ln":
-            return ("hbm", float(2 * (8 * 128 + 512 * 64) * 2))
+        if kernel == "fold_ln":  # w_z (8 rows), w_m and w_g (256 rows of width 64 each)
+            return fold_kernel_work(kernel, 3, 8, 512)
+        raise KeyError(kernel)
+
+
+class PairMixerWorkload(Workload):
+    """The reference trunk's layer (PairMixerLayer: TriMulOut, TriMulIn, Transition_z) at N=768 bf16,
+    trailing 10% of tokens padded, in place."""
+
+    cpu_warmup = 0
+    cpu_calls = 1
+
+    def __init__(self, device, n: int = 768, seed: int = 0):
+        from .pairmixer import PairMixerLayerHip
+
+        self.n = n
+        self.name = f"pairmixer_layer_n{n}"
+        self.metric = f"ms per PairMixer layer at N={n} bf16"
+        torch.manual_seed(seed)
+        self.layer = init_module(PairMixerLayerHip(384, 128), seed).to(device).eval()
+        g = torch.Generator().manual_seed(seed)
+        self.z_cpu = torch.randn(1, n, n, 128, generator=g).to(torch.bfloat16)
+        self.n_pad = n // 10
+        self.tok_cpu = token_mask(n, self.n_pad, "cpu")
+        self.pm_cpu = self.tok_cpu[:, :, None] & self.tok_cpu[:, None, :]
+        self.z = self.z_cpu.to(device)
+        self.pm = self.pm_cpu.to(device)
+        self.config = {"workload": self.name, "N": n, "c_z": 128, "batch": 1, "padded_tokens": self.n_pad}
+        trimul = 2.0 * n * n * 128 * 6 * 128 + 2.0 * 128 * n ** 3
+        self.flops = 2 * trimul + 2.0 * n * n * 128 * 12 * 128
+
+    def step(self) -> None:
+        self.layer.forward_(None, self.z, self.pm)
+
+    def cpu_sample(self, oracle):
+        params = {k: v.detach().cpu() for k, v in self.layer.state_dict().items()}
+        z = self.z_cpu.float()
+        s = torch.zeros(1, self.n, 384)  # passes through the layer
+
+        def fn():
+            return oracle.pairmixer_layer(s, z, self.pm_cpu, params)
+
+        return fn, 1.0, f"oracle.pairmixer_layer fp32, full N={self.n}"
+
+    def kernel_work(self, kernel: str) -> tuple[str, float]:
+        w = trimul_kernel_work(kernel, 1, self.n)
+        if w is not None:
+            return w
+        if kernel == "transition_pair":
+            return ("mfma", 2.0 * self.n * self.n * 128 * 12 * 128)
+        if kernel == "fold_ln":  # transition fc1 and fc2 (512 rows each)
+            return fold_kernel_work(kernel, 2, 1024)
+        raise KeyError(kernel)
+
+
+class PairMixerMsaWorkload(Workload):
+    """The reference MSA-module layer (PairMixerMSALayer) at S=1024, N=512 bf16: PWA, MSA transition,
+    OPM (20% of MSA rows masked), TriMulOut, TriMulIn, Transition_z, in place."""
+
+    cpu_warmup = 0
+    cpu_calls = 1
+
+    def __init__(self, device, n: int = 512, S: int = 1024, seed: int = 0):
+        from .pairmixer import PairMixerMSALayerHip
+
+        self.n, self.S = n, S
+        self.name = f"pairmixer_msa_layer_s{S}_n{n}"
+        self.metric = f"ms per PairMixer MSA layer at S={S}, N={n} bf16"
+        torch.manual_seed(seed)
+        self.layer = init_module(PairMixerMSALayerHip(384, 64, 128, 0.15, 0.25), seed).to(device).eval()
+        g = torch.Generator().manual_seed(seed)
+        self.m_cpu = torch.randn(1, S, n, 64, generator=g).to(torch.bfloat16)
+        self.z_cpu = torch.randn(1, n, n, 128, generator=g).to(torch.bfloat16)
+        self.n_pad = n // 10
+        tok = token_mask(n, self.n_pad, "cpu")
+        self.pm_cpu = tok[:, :, None] & tok[:, None, :]
+        rows = torch.rand(S, generator=torch.Generator().manual_seed(seed)) >= 0.2
+        self.msa_mask_cpu = rows[None, :, None] & tok[:, None, :]
+        self.m = self.m_cpu.to(device)
+        self.z = self.z_cpu.to(device)
+        self.pm = self.pm_cpu.to(device)
+        self.msa_mask = self.msa_mask_cpu.to(device)
+        self.s_valid = int(rows.sum())
+        self.config = {"workload": self.name, "S": S, "N": n, "c_m": 64, "c_z": 128, "batch": 1,
+                       "padded_tokens": self.n_pad, "valid_msa_rows": self.s_valid}
+        pwa = 2.0 * S * n * 64 * 512 + 2.0 * 8 * n * n * S * 32 + 2.0 * S * n * 256 * 64
+        msa_tr = 2.0 * S * n * 64 * 12 * 64
+        opm = 2.0 * n * n * 1024 * self.s_valid + 2.0 * n * n * 1024 * 128
+        trimul = 2.0 * n * n * 128 * 6 * 128 + 2.0 * 128 * n ** 3
+        self.flops = pwa + msa_tr + opm + 2 * trimul + 2.0 * n * n * 128 * 12 * 128
+
+    def step(self) -> None:
+        self.layer.forward_(None, self.z, self.m, self.pm, self.msa_mask)
+
+    def cpu_sample(self, oracle):
+        """Every op of the layer, each on a bounded slice scaled to the full layer: PWA and the MSA
+        transition on 16 of S MSA rows (both are independent per MSA row), the OPM on 64 of N output
+        rows, the two triangle multiplications and the pair transition at full size.  The callable
+        returns that extrapolated time in seconds (fraction None)."""
+        rows, opm_rows = 16, 64
+        params = {k: v.detach().cpu() for k, v in self.layer.state_dict().items()}
+
+        def sub(prefix):
+            return {k[len(prefix) + 1:]: v for k, v in params.items() if k.startswith(prefix + ".")}
+
+        m = self.m_cpu.float()
+        z = self.z_cpu.float()
+        msa_mask = self.msa_mask_cpu
+
+        def fn():
+            t0 = time.perf_counter()
+            mm = m[:, :rows] + oracle.pair_weighted_averaging(m[:, :rows], z, self.pm_cpu,
+                                                               sub("pair_weighted_averaging"))
+            mm = mm + oracle.transition(mm, sub("msa_transition"))
+            t1 = time.perf_counter()
+            oracle.outer_product_mean(m, msa_mask, sub("outer_product_mean"), i_chunk=opm_rows, i_stop=opm_rows)
+            t2 = time.perf_counter()
+            zz = z + oracle.trimul(z, self.pm_cpu, sub("tri_mul_out"), "outgoing")
+            zz = zz + oracle.trimul(zz, self.pm_cpu, sub("tri_mul_in"), "incoming")
+            zz = zz + oracle.transition(zz, sub("z_transition"))
+            t3 = time.perf_counter()
+            return (t1 - t0) * self.S / rows + (t2 - t1) * self.n / opm_rows + (t3 - t2)
+
+        return fn, None, (f"fp32 oracle ops: PWA + MSA transition on {rows} of {self.S} MSA rows, "
+                          f"OPM on {opm_rows} of {self.n} output rows, TriMulOut + TriMulIn + Transition_z "
+                          f"at full N; each part scaled to the full layer")
+
+    def kernel_work(self, kernel: str) -> tuple[str, float]:
+        n, S = self.n, self.S
+        w = trimul_kernel_work(kernel, 1, n)
+        if w is not None:
+            return w
+        if kernel == "transition_pair":
+            return ("mfma", 2.0 * n * n * 128 * 12 * 128)
+        if kernel == "opm_fused":
+            return ("mfma", 2.0 * n * n * 1024 * self.s_valid + 2.0 * n * n * 1024 * 128)
+        if kernel == "opm_proj":
+            return ("hbm", float(self.s_valid * n * 64 * 2 + 2 * S * n * 32 * 2))
+        if kernel == "opm_rows":
+            return ("hbm", float(S * n))
+        if kernel == "pwa_contract":
+            return ("mfma", 2.0 * 8 * n * n * S * 32)
+        if kernel in ("pwa_weights", "pwa_proj", "pwa_out"):
+            return PwaWorkload.kernel_work(self, kernel)
+        if kernel == "token_layernorm":
+            return ("hbm", float(S * n * 64 * 2 * 2))
+        if kernel == "transition_token_swiglu":
+            return ("hbm", float(S * n * (64 + 256) * 2))
+        if kernel == "transition_token_out":
+            return ("hbm", float(S * n * (256 + 2 * 64) * 2))
+        if kernel == "fold_ln":  # PWA (3 folds) and transition fc1, fc2
+            return fold_kernel_work(kernel, 5, 8 + 1024, 512)
         raise KeyError(kernel)
 
 
@@ -389,6 +542,10 @@ def make(op: str, device, n: int | None = None) -> Workload:
         return OpmWorkload(device, n or 512)
     if op == "pwa":
         return PwaWorkload(device, n or 512)
+    if op == "pairmixer":
+        return PairMixerWorkload(device, n or 768)
+    if op == "pairmixer_msa":
+        return PairMixerMsaWorkload(device, n or 512)
     if op == "block":
         return BlockWorkload(device, n or 768)
     if op in ("triatt_start", "triatt_end"):

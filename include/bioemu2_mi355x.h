@@ -109,9 +109,9 @@ int bioemu_transition_pair_fwd(const void* x, const float* norm_w, const float* 
                                int64_t hidden, int use_norm, int residual, hipStream_t stream);
 
 /*
- * Token Transition (same op over [M, D] rows of the single representation,
- * D in {128, 384}, hidden a multiple of 32): LN kernel + two MFMA GEMMs.
- * Replaces Transition.forward (transition.py:52-91) for s.
+ * Token Transition (same op over [M, D] rows of the single or MSA
+ * representation, D in {64, 128, 384}, hidden a multiple of 32): LN kernel +
+ * two MFMA GEMMs.  Replaces Transition.forward (transition.py:52-91) for s and m.
  */
 size_t bioemu_transition_token_workspace_bytes(int64_t M, int64_t D, int64_t hidden);
 int bioemu_transition_token_fwd(const void* x, const float* norm_w, const float* norm_b,

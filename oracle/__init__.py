@@ -35,6 +35,9 @@ How each function is pinned (see ``tests/test_oracle_*.py``):
 * ``pairformer_block`` — composition only (AF3 suppl. Alg. 17); each term is
                     pinned above, the order is pinned by a hand-built
                     composition test.
+* ``pairmixer_layer``, ``pairmixer_msa_layer`` — the reference trunk's layers
+                    (pairmixer.py:430-456, :711-757), compositions of the pinned
+                    terms; zeroed output projections reduce them to the identity.
 
 No function here is "parity unpinned".
 """
@@ -45,6 +48,8 @@ from .pairformer_ref import (  # noqa: F401
     pair_mask_from_token_mask,
     pair_weighted_averaging,
     pairformer_block,
+    pairmixer_layer,
+    pairmixer_msa_layer,
     transition,
     triangle_attention,
     trimul,

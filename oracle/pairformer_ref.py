@@ -24,6 +24,8 @@ __all__ = [
     "pair_weighted_averaging",
     "transition",
     "pairformer_block",
+    "pairmixer_layer",
+    "pairmixer_msa_layer",
     "pair_mask_from_token_mask",
 ]
 
@@ -336,3 +338,43 @@ def pairformer_block(
     )
     s = s + transition(s, _sub(params, "transition_s"))
     return s, z
+
+
+# ----------------------------------------------------------------------------
+# The reference trunk's layers (PairMixer)
+# ----------------------------------------------------------------------------
+def pairmixer_layer(s: Tensor, z: Tensor, pair_mask: Tensor, params: dict) -> tuple[Tensor, Tensor]:
+    """PairMixerLayer.forward (biomoa/modules/pairmixer.py:430-456), eval mode.
+
+    z += TriMulOut(z, pm); z += TriMulIn(z, pm); z += Transition_z(z); s passes
+    through.  Dropout is the identity at eval (biomoa/ops/dropout.py:68-69).
+    """
+    s = _f32(s)
+    z = _f32(z)
+    pm = pair_mask.bool().cpu()
+    z = z + trimul(z, pm, _sub(params, "tri_mul_out"), "outgoing")  # :447-449
+    z = z + trimul(z, pm, _sub(params, "tri_mul_in"), "incoming")  # :450-452
+    z = z + transition(z, _sub(params, "transition_z"))  # :454
+    return s, z
+
+
+def pairmixer_msa_layer(
+    s: Tensor, z: Tensor, m: Tensor, token_mask: Tensor, msa_mask: Tensor, params: dict
+) -> tuple[Tensor, Tensor, Tensor]:
+    """PairMixerMSALayer.forward (biomoa/modules/pairmixer.py:711-757), eval mode.
+
+    ``token_mask`` is the pair mask [B,T,T] (built as mask_i & mask_j,
+    pairmixer.py:589).  m += PWA(m, z, token_mask); m += Transition_m(m);
+    z += OPM(m, msa_mask); z += TriMulOut; z += TriMulIn; z += Transition_z.
+    """
+    s = _f32(s)
+    z = _f32(z)
+    m = _f32(m)
+    pm = token_mask.bool().cpu()
+    m = m + pair_weighted_averaging(m, z, pm, _sub(params, "pair_weighted_averaging"))  # :737-741
+    m = m + transition(m, _sub(params, "msa_transition"))  # :742
+    z = z + outer_product_mean(m, msa_mask, _sub(params, "outer_product_mean"))  # :745
+    z = z + trimul(z, pm, _sub(params, "tri_mul_out"), "outgoing")  # :748-750
+    z = z + trimul(z, pm, _sub(params, "tri_mul_in"), "incoming")  # :751-753
+    z = z + transition(z, _sub(params, "z_transition"))  # :755
+    return s, z, m

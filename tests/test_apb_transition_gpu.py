@@ -161,6 +161,16 @@ def test_token_transition_matches_oracle(gpu_device, rows):
     _check(got, want, f"token transition rows={rows}")
 
 
+def test_msa_transition_matches_oracle(gpu_device):
+    """The MSA representation's transition (dim 64, hidden 256) over [B,S,N,64] rows."""
+    m = _transition(gpu_device, 64, 256)
+    x = torch.randn(1, 7, 33, 64).to(torch.bfloat16).to(gpu_device)
+    with torch.no_grad():
+        got = m(x).float().cpu()
+    want = oracle.transition(x.cpu(), state(m))
+    _check(got, want, "msa transition")
+
+
 def test_pair_transition_residual_and_rowwise(gpu_device):
     m = _transition(gpu_device, 128, 512)
     x = torch.randn(2, 30, 30, 128).to(torch.bfloat16).to(gpu_device)

@@ -1,0 +1,80 @@
+"""The reference trunk's PairMixer layers on the GPU vs the fp32 CPU oracle compositions."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import oracle
+from bioemu2_amd.pairmixer import PairMixerLayerHip, PairMixerMSALayerHip
+from bioemu2_amd.workloads import init_module
+from tests._helpers import max_abs, rel_l2, state
+
+pytestmark = pytest.mark.gpu
+
+
+def _tok(B, n, n_pad, device):
+    tok = torch.ones(B, n, dtype=torch.bool)
+    if n_pad:
+        tok[:, n - n_pad:] = False
+    return tok.to(device)
+
+
+def _check(name, got, want, sel, adds):
+    g, w = got.float().cpu()[sel], want[sel]
+    err, rl2 = max_abs(g, w), rel_l2(g, w)
+    # The north_star bf16 bound (max-abs 2e-2, rel-L2 1e-2) per element, plus one bf16
+    # rounding of the residual stream per residual add (2^-9 |x|): the layers keep z and m in
+    # bf16 between ops, as the reference's bf16-mixed trunk does.
+    excess = ((g - w).abs() - (2e-2 + adds * 2.0 ** -9 * w.abs())).max().item()
+    print(f"{name}: max_abs={err:.3e} rel_l2={rl2:.3e} |want|max={w.abs().max():.2f} excess={excess:.3e}")
+    assert rl2 <= 1e-2 and excess <= 0.0
+
+
+@pytest.mark.parametrize("n,n_pad", [(64, 0), (96, 9)])
+def test_pairmixer_layer_matches_oracle(gpu_device, n, n_pad):
+    torch.manual_seed(0)
+    layer = init_module(PairMixerLayerHip(384, 128), 0).to(gpu_device).eval()
+    g = torch.Generator().manual_seed(1)
+    s = torch.randn(1, n, 384, generator=g).to(torch.bfloat16).to(gpu_device)
+    z = torch.randn(1, n, n, 128, generator=g).to(torch.bfloat16).to(gpu_device)
+    tok = _tok(1, n, n_pad, gpu_device)
+    pm = tok[:, :, None] & tok[:, None, :]
+    s_got, z_got = layer(s, z, pm)
+    assert s_got is s
+    _, z_want = oracle.pairmixer_layer(s.cpu(), z.cpu(), pm.cpu(), state(layer))
+    _check(f"pairmixer n={n}", z_got, z_want, pm.cpu(), 3)
+
+
+@pytest.mark.parametrize("S,n,n_pad", [(16, 64, 0), (24, 80, 8)])
+def test_pairmixer_msa_layer_matches_oracle(gpu_device, S, n, n_pad):
+    torch.manual_seed(0)
+    layer = init_module(PairMixerMSALayerHip(384, 64, 128, 0.15, 0.25), 0).to(gpu_device).eval()
+    g = torch.Generator().manual_seed(2)
+    s = torch.randn(1, n, 384, generator=g).to(torch.bfloat16).to(gpu_device)
+    z = torch.randn(1, n, n, 128, generator=g).to(torch.bfloat16).to(gpu_device)
+    m = torch.randn(1, S, n, 64, generator=g).to(torch.bfloat16).to(gpu_device)
+    tok = _tok(1, n, n_pad, gpu_device)
+    pm = tok[:, :, None] & tok[:, None, :]
+    msa_mask = tok[:, None, :].expand(1, S, n).clone()
+    msa_mask[:, -3:] = False  # a few padded MSA rows
+    _, z_got, m_got = layer(s, z, m, pm, msa_mask)
+    _, z_want, m_want = oracle.pairmixer_msa_layer(s.cpu(), z.cpu(), m.cpu(), pm.cpu(), msa_mask.cpu(), state(layer))
+    _check(f"pairmixer-msa S={S} n={n} m", m_got, m_want, tok.cpu()[:, None, :].expand(1, S, n), 2)
+    _check(f"pairmixer-msa S={S} n={n} z", z_got, z_want, pm.cpu(), 4)
+
+
+def test_pairmixer_inplace_matches_out_of_place(gpu_device):
+    torch.manual_seed(0)
+    layer = init_module(PairMixerMSALayerHip(384, 64, 128, 0.15, 0.25), 0).to(gpu_device).eval()
+    g = torch.Generator().manual_seed(3)
+    s = torch.randn(1, 48, 384, generator=g).to(torch.bfloat16).to(gpu_device)
+    z = torch.randn(1, 48, 48, 128, generator=g).to(torch.bfloat16).to(gpu_device)
+    m = torch.randn(1, 8, 48, 64, generator=g).to(torch.bfloat16).to(gpu_device)
+    tok = _tok(1, 48, 4, gpu_device)
+    pm = tok[:, :, None] & tok[:, None, :]
+    msa_mask = tok[:, None, :].expand(1, 8, 48).clone()
+    _, z_new, m_new = layer(s, z, m, pm, msa_mask)
+    z2, m2 = z.clone(), m.clone()
+    layer.forward_(s, z2, m2, pm, msa_mask)
+    assert torch.equal(z2, z_new) and torch.equal(m2, m_new)
