@@ -301,8 +301,9 @@ def launch_transition_token(
     return out
 
 
-def _is_pair_transition(x: Tensor, hidden: int) -> bool:
-    return x.ndim == 4 and x.shape[-1] == 128 and hidden == 512
+def _is_row_transition(x: Tensor, hidden: int) -> bool:
+    """Widths the fused row kernel takes: pair (128, hidden 512) and MSA (64, hidden 256) rows."""
+    return x.shape[-1] in (64, 128) and hidden == 4 * x.shape[-1]
 
 
 @torch.library.custom_op("bioemu_mi355x::transition", mutates_args=(), device_types="cuda")
@@ -315,7 +316,7 @@ def transition(
     nw = None if norm_w is None else norm_w.to(f32).contiguous()
     nb = None if norm_b is None else norm_b.to(f32).contiguous()
     w1, w2, w3 = (w.to(BF16).contiguous() for w in (fc1_w, fc2_w, fc3_w))
-    if _is_pair_transition(xb, w1.shape[0]):
+    if _is_row_transition(xb, w1.shape[0]):
         launch_transition_pair(xb, nw, nb, w1, w2, w3, out)
     else:
         launch_transition_token(xb, nw, nb, w1, w2, w3, out)

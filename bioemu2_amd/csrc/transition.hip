@@ -1,22 +1,26 @@
-// Pair Transition (SwiGLU MLP) for gfx950.
+// Row-wise Transition (SwiGLU MLP) for gfx950: the pair representation
+// (c = 128) and the MSA representation (c = 64), hidden = 4c.
 //
 // Reference: Transition.forward (src/bioemu2/biomoa/ops/transition.py:52-91):
 //   xn = LN(x) (eps 1e-5, with bias) when use_norm;  out = fc3(silu(fc1(xn)) * fc2(xn))
-// with c = 128 and hidden = 4c = 512 for the pair representation, no biases.
+// with no biases; PairMixerLayer / Pairformer use it on z (c = 128) and
+// PairMixerMSALayer on m (c = 64) (biomoa/modules/pairmixer.py:631-634).
 //
 // The LayerNorm affine is folded into fc1 / fc2 once per call (fold.hip):
 //   LN(x) W^T = xhat (W diag(gamma))^T + W beta
-// so a wave normalises its pair tile affine-free and adds W beta with one
+// so a wave normalises its row tile affine-free and adds W beta with one
 // extra MFMA k-step (pairtile.h).
 //
-// One workgroup = 4 waves x 32 pairs.  Each wave keeps its normalised pair
-// tile in registers as MFMA operands and its 32x128 output accumulator in
+// One workgroup = 4 waves x 32 rows.  Each wave keeps its normalised row
+// tile in registers as MFMA operands (lane (n, hh) holds channels
+// [hh c/2, (hh + 1) c/2) of row slot n) and its 32 x c output accumulator in
 // registers; the hidden dimension is walked in chunks of 32.  A chunk's weight
-// slices (fc1 and fc2 rows, the fc3 columns and the two bias columns, 24.25 KB)
-// are copied by buffer loads straight into LDS (no registers), double-buffered:
-// chunk h + 1 is in flight while chunk h is multiplied.  The hidden
-// activations never leave registers: silu(a) * b comes out of the fc1 / fc2
-// MFMAs in exactly the layout fc3 consumes as its B operand.
+// slices (fc1 and fc2 rows, the fc3 columns and the two bias columns; 24.25 KB
+// at c = 128, 12.25 KB at c = 64) are copied by buffer loads straight into LDS
+// (no registers), double-buffered: chunk h + 1 is in flight while chunk h is
+// multiplied.  The hidden activations never leave registers: silu(a) * b comes
+// out of the fc1 / fc2 MFMAs in exactly the layout fc3 consumes as its B
+// operand.
 //
 // LDS tiles are unpadded (the copies write 1 KB runs); the 16-byte chunk index
 // of each row is XOR-swizzled so that the perm32 row pattern of the operand
@@ -28,22 +32,36 @@
 namespace bioemu {
 namespace {
 
-constexpr int C = 128;
-constexpr int HID = 512;
 constexpr int HC = 32;                      // hidden chunk
-constexpr int NCH = HID / HC;               // 16 chunks
 constexpr int kThreads = 256;               // 4 waves
-constexpr int kPairsPerWg = 128;
-constexpr int kW12Tile = HC * C;            // bf16: [32 rows][16 chunks]
-constexpr int kW3Tile = C * HC;             // bf16: [128 rows][4 chunks]
-constexpr int kBiasElems = 2 * HC * 2;      // bf16: [fc1 | fc2][32 rows][hi, lo]
-constexpr int kStage = 2 * kW12Tile + kW3Tile + kBiasElems;
-constexpr int kSmem = 2 * kStage * 2;       // bytes
-constexpr int kCopies = 3 * 8 + 1;          // 1 KB copies per stage (+ the 256-byte bias copy)
+constexpr int kRowsPerWg = 128;
 
+template <int C>
+struct Geo {
+  static constexpr int HID = 4 * C;
+  static constexpr int NCH = HID / HC;                       // hidden chunks
+  static constexpr int KS = C / 16;                          // 8-channel groups per lane (k-steps)
+  static constexpr int RowChunks = C / 8;                    // 16-byte chunks per fc1 / fc2 row
+  static constexpr int W12Tile = HC * C;                     // bf16: [32 rows][C / 8 chunks]
+  static constexpr int W3Tile = C * HC;                      // bf16: [C rows][4 chunks]
+  static constexpr int BiasElems = 2 * HC * 2;               // bf16: [fc1 | fc2][32 rows][hi, lo]
+  static constexpr int Stage = 2 * W12Tile + W3Tile + BiasElems;
+  static constexpr int Smem = 2 * Stage * 2;                 // bytes
+  static constexpr int W12Copies = W12Tile * 2 / 1024;       // 1 KB copies per fc1 / fc2 tile
+  static constexpr int W3Copies = W3Tile * 2 / 1024;
+  static constexpr int Copies = 2 * W12Copies + W3Copies + 1;  // + the 256-byte bias copy
+};
+
+// Row swizzles of the 16-byte chunk index: 16-chunk (256 B) rows, 8-chunk
+// (128 B) rows and 4-chunk (64 B) rows, each making the rows perm32(0..15)
+// (and perm32(16..31)) land on distinct bank groups.
 __device__ __forceinline__ int swz16(int r) { return (r & 7) | ((r & 16) >> 1); }
+__device__ __forceinline__ int swz8(int r) { return ((r >> 1) & 7) ^ (((r >> 4) & 1) << 2); }
 __device__ __forceinline__ int swz4(int r) { return ((r >> 2) & 1) | (((r >> 4) & 1) << 1); }
-__device__ __forceinline__ int w12_off(int r, int c) { return (r * 16 + (c ^ swz16(r))) * 8; }
+template <int C>
+__device__ __forceinline__ int w12_swz(int r) { return C == 128 ? swz16(r) : swz8(r); }
+template <int C>
+__device__ __forceinline__ int w12_off(int r, int c) { return (r * (C / 8) + (c ^ w12_swz<C>(r))) * 8; }
 __device__ __forceinline__ int w3_off(int r, int c) { return (r * 4 + (c ^ swz4(r))) * 8; }
 
 // 16 (or 4) bytes per lane from a buffer straight into LDS at lds + 16 (4) * lane.
@@ -54,9 +72,12 @@ __device__ __forceinline__ void copy4_to_lds(__amdgpu_buffer_rsrc_t r, const bf1
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(lds), 4, voff, soff, 0, 0);
 }
 
-__global__ __launch_bounds__(kThreads) void transition_pair_kernel(
+template <int C>
+__global__ __launch_bounds__(kThreads) void transition_rows_kernel(
     const bf16* x, const bf16* __restrict__ w1, const bf16* __restrict__ w2, const bf16* __restrict__ w3,
     const bf16* __restrict__ cf, bf16* out, long long P, int use_norm, int residual) {
+  using G = Geo<C>;
+  constexpr int HID = G::HID, KS = G::KS;
   extern __shared__ __attribute__((aligned(16))) char smem_raw[];
   bf16* smem = reinterpret_cast<bf16*>(smem_raw);
   const int tid = threadIdx.x;
@@ -67,68 +88,96 @@ __global__ __launch_bounds__(kThreads) void transition_pair_kernel(
   const __amdgpu_buffer_rsrc_t r2 = buffer_rsrc(w2, HID * C * 2);
   const __amdgpu_buffer_rsrc_t r3 = buffer_rsrc(w3, C * HID * 2);
   const __amdgpu_buffer_rsrc_t rc = buffer_rsrc(cf, 2 * HID * 2 * 2);
-  // Copy k of a stage (k = wave, wave + 4, ...): 0-7 fc1 rows, 8-15 fc2 rows,
-  // 16-23 fc3 columns (1 KB each, LDS chunk 64 j + lane of the tile), 24 the
-  // bias pairs of both (4 bytes per lane).
+  // Copy k of a stage (k = wave, wave + 4, ...): fc1 rows, fc2 rows, fc3
+  // columns (1 KB each, LDS chunk 64 j + lane of the tile), last the bias
+  // pairs of both (4 bytes per lane).
   auto stage_chunk = [&](int hc) {
-    bf16* st = smem + (hc & 1) * kStage;
+    bf16* st = smem + (hc & 1) * G::Stage;
 #pragma unroll
-    for (int k = wave; k < kCopies; k += 4) {
-      if (k < 16) {
-        const int j = k & 7, p = j * 64 + lane, r = p >> 4, c = (p & 15) ^ swz16(r);
-        copy16_to_lds(k < 8 ? r1 : r2, st + (k < 8 ? 0 : kW12Tile) + j * 512, (unsigned)(r * C + c * 8) * 2,
-                        (unsigned)(hc * HC * C) * 2);
-      } else if (k < 24) {
-        const int j = k - 16, p = j * 64 + lane, r = p >> 2, c = (p & 3) ^ swz4(r);
-        copy16_to_lds(r3, st + 2 * kW12Tile + j * 512, (unsigned)(r * HID + c * 8) * 2, (unsigned)(hc * HC) * 2);
+    for (int k = wave; k < G::Copies; k += 4) {
+      if (k < 2 * G::W12Copies) {
+        const bool second = k >= G::W12Copies;
+        const int j = second ? k - G::W12Copies : k;
+        const int p = j * 64 + lane, r = p / G::RowChunks, c = (p % G::RowChunks) ^ w12_swz<C>(r);
+        copy16_to_lds(second ? r2 : r1, st + (second ? G::W12Tile : 0) + j * 512, (unsigned)(r * C + c * 8) * 2,
+                      (unsigned)(hc * HC * C) * 2);
+      } else if (k < 2 * G::W12Copies + G::W3Copies) {
+        const int j = k - 2 * G::W12Copies, p = j * 64 + lane, r = p >> 2, c = (p & 3) ^ swz4(r);
+        copy16_to_lds(r3, st + 2 * G::W12Tile + j * 512, (unsigned)(r * HID + c * 8) * 2, (unsigned)(hc * HC) * 2);
       } else if (use_norm) {
         const int which = lane >> 5, row = lane & 31;
-        copy4_to_lds(rc, st + 2 * kW12Tile + kW3Tile, (unsigned)((which * HID + row) * 2) * 2,
-                       (unsigned)(hc * HC * 2) * 2);
+        copy4_to_lds(rc, st + 2 * G::W12Tile + G::W3Tile, (unsigned)((which * HID + row) * 2) * 2,
+                     (unsigned)(hc * HC * 2) * 2);
       }
     }
   };
 
   stage_chunk(0);
 
-  // This wave's 32 pairs: lane (n, hh) holds channel half hh of pair p0 + n.
-  const long long p0 = (long long)blockIdx.x * kPairsPerWg + wave * 32;
+  // This wave's 32 rows: lane (n, hh) holds channel half hh of row p0 + n.
+  const long long p0 = (long long)blockIdx.x * kRowsPerWg + wave * 32;
   const long long pair = p0 + n;
   const bool valid = pair < P;
-  bf16x8 xf[8];
+  bf16x8 xf[KS];
   {
-    float v[64];
-    load_half_row_f32(x + (size_t)(valid ? pair : 0) * C, hh, valid, v);
+    float v[C / 2];
+    const bf16* row = x + (size_t)(valid ? pair : 0) * C + hh * (C / 2);
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      bf16x8 raw;
+      if (valid) {
+        raw = load8(row + 8 * s);
+      } else {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) raw[t] = f2bf(0.f);
+      }
+      unpack8(raw, v + 8 * s);
+    }
     if (use_norm) {
-      normalize_half_row(v, valid, xf);
+      // affine-free LayerNorm over the C channels of lanes l and l ^ 32 (two-pass, fp32)
+      float sum = 0.f;
+#pragma unroll
+      for (int c = 0; c < C / 2; ++c) sum += v[c];
+      sum += __shfl_xor(sum, 32);
+      const float mean = sum * (1.0f / C);
+      float ss = 0.f;
+#pragma unroll
+      for (int c = 0; c < C / 2; ++c) {
+        const float d = v[c] - mean;
+        ss += d * d;
+      }
+      ss += __shfl_xor(ss, 32);
+      const float rstd = valid ? rsqrtf(ss * (1.0f / C) + 1e-5f) : 0.f;
+#pragma unroll
+      for (int c = 0; c < C / 2; ++c) xf[c >> 3][c & 7] = f2bf((v[c] - mean) * rstd);
     } else {
 #pragma unroll
-      for (int c = 0; c < 64; ++c) xf[c >> 3][c & 7] = f2bf(v[c]);
+      for (int c = 0; c < C / 2; ++c) xf[c >> 3][c & 7] = f2bf(v[c]);
     }
   }
   const bf16x8 xb = bias_step_x(valid, hh);
   const int rw = perm32(n);   // weight row read by this lane in the fc1 / fc2 blocks
 
-  f32x16 acc[4];
+  f32x16 acc[C / 32];
 #pragma unroll
-  for (int cb = 0; cb < 4; ++cb) acc[cb] = zero16();
+  for (int cb = 0; cb < C / 32; ++cb) acc[cb] = zero16();
 
 #pragma unroll 1
-  for (int hc = 0; hc < NCH; ++hc) {
+  for (int hc = 0; hc < G::NCH; ++hc) {
     __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's copies of chunk hc landed
     __syncthreads();                       // ... and everyone's; the other stage is free again
-    if (hc + 1 < NCH) stage_chunk(hc + 1);
-    const bf16* st = smem + (hc & 1) * kStage;
+    if (hc + 1 < G::NCH) stage_chunk(hc + 1);
+    const bf16* st = smem + (hc & 1) * G::Stage;
     const bf16* s1 = st;
-    const bf16* s2 = st + kW12Tile;
-    const bf16* s3 = st + 2 * kW12Tile;
-    const bf16* cl = st + 2 * kW12Tile + kW3Tile;
-    // h^T blocks: lane (n = pair slot, hh) holds hidden hc*32 + 16hh + u.
+    const bf16* s2 = st + G::W12Tile;
+    const bf16* s3 = st + 2 * G::W12Tile;
+    const bf16* cl = st + 2 * G::W12Tile + G::W3Tile;
+    // h^T blocks: lane (n = row slot, hh) holds hidden hc*32 + 16hh + u.
     f32x16 a = zero16(), g = zero16();
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      a = mfma32(load8(s1 + w12_off(rw, 8 * hh + s)), xf[s], a);
-      g = mfma32(load8(s2 + w12_off(rw, 8 * hh + s)), xf[s], g);
+    for (int s = 0; s < KS; ++s) {
+      a = mfma32(load8(s1 + w12_off<C>(rw, KS * hh + s)), xf[s], a);
+      g = mfma32(load8(s2 + w12_off<C>(rw, KS * hh + s)), xf[s], g);
     }
     if (use_norm) {
       a = mfma32(bias_step_w(cl, rw, hh), xb, a);
@@ -138,17 +187,17 @@ __global__ __launch_bounds__(kThreads) void transition_pair_kernel(
 #pragma unroll
     for (int u = 0; u < 16; ++u) hb[u >> 3][u & 7] = f2bf(siluf_fast(a[u]) * g[u]);
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb) {
+    for (int cb = 0; cb < C / 32; ++cb) {
       const int r = cb * 32 + perm32(n);
       acc[cb] = mfma32(load8(s3 + w3_off(r, 2 * hh)), hb[0], acc[cb]);
       acc[cb] = mfma32(load8(s3 + w3_off(r, 2 * hh + 1)), hb[1], acc[cb]);
     }
   }
 
-  // D lane (n, hh) of block cb: output channel cb*32 + 16hh + u of pair p0 + n
+  // D lane (n, hh) of block cb: output channel cb*32 + 16hh + u of row p0 + n
   if (!valid) return;
 #pragma unroll
-  for (int cb = 0; cb < 4; ++cb) {
+  for (int cb = 0; cb < C / 32; ++cb) {
     const size_t off = (size_t)pair * C + cb * 32 + 16 * hh;
     float v[16];
 #pragma unroll
@@ -165,14 +214,29 @@ __global__ __launch_bounds__(kThreads) void transition_pair_kernel(
   }
 }
 
+template <int C>
+int launch_rows(const bf16* x, const bf16* w1, const bf16* w2, const bf16* w3, const bf16* cf, bf16* out,
+                long long P, int use_norm, int residual, hipStream_t stream) {
+  auto* kern = transition_rows_kernel<C>;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          Geo<C>::Smem) != hipSuccess)
+    return set_error(BIOEMU_ERR_LAUNCH, "transition_pair: cannot set dynamic LDS size");
+  const long long nwg = (P + kRowsPerWg - 1) / kRowsPerWg;
+  if (nwg > 0x7fffffffLL) return set_error(BIOEMU_ERR_INVALID_ARG, "transition_pair: too many rows");
+  KernelTimerScope timed(C == 128 ? "transition_pair" : "transition_msa", stream);
+  hipLaunchKernelGGL(kern, dim3((unsigned)nwg), dim3(kThreads), Geo<C>::Smem, stream, x, w1, w2, w3, cf, out, P,
+                     use_norm, residual);
+  return check_launch("transition_pair");
+}
+
 }  // namespace
 }  // namespace bioemu
 
 using namespace bioemu;
 
 extern "C" size_t bioemu_transition_pair_workspace_bytes(int64_t Dc, int64_t hidden) {
-  if (Dc != C || hidden != HID) return 0;
-  return fold_bytes(2 * HID);
+  if ((Dc != 64 && Dc != 128) || hidden != 4 * Dc) return 0;
+  return fold_bytes(2 * hidden, Dc);
 }
 
 extern "C" int bioemu_transition_pair_fwd(const void* x, const float* norm_w, const float* norm_b,
@@ -180,8 +244,9 @@ extern "C" int bioemu_transition_pair_fwd(const void* x, const float* norm_w, co
                                           void* out, void* workspace, size_t workspace_bytes, int64_t P,
                                           int64_t Dc, int64_t hidden, int use_norm, int residual,
                                           hipStream_t stream) {
-  if (Dc != C || hidden != HID)
-    return set_error(BIOEMU_ERR_UNSUPPORTED, "transition_pair: only dim=128, hidden=512 supported (got %lld, %lld)",
+  if ((Dc != 64 && Dc != 128) || hidden != 4 * Dc)
+    return set_error(BIOEMU_ERR_UNSUPPORTED,
+                     "transition_pair: only dim 128 / hidden 512 and dim 64 / hidden 256 supported (got %lld, %lld)",
                      (long long)Dc, (long long)hidden);
   if (P <= 0) return set_error(BIOEMU_ERR_INVALID_ARG, "transition_pair: bad row count %lld", (long long)P);
   if (!x || !fc1_w || !fc2_w || !fc3_w || !out || !workspace || (use_norm && (!norm_w || !norm_b)))
@@ -195,27 +260,22 @@ extern "C" int bioemu_transition_pair_fwd(const void* x, const float* norm_w, co
   if (workspace_bytes < need)
     return set_error(BIOEMU_ERR_WORKSPACE, "transition_pair: workspace %zu < required %zu", workspace_bytes, need);
 
-  // Folded fc1 | fc2 (one [1024][128] matrix) and their bias pairs ([1024][2]).
+  // Folded fc1 | fc2 (one [2 hidden][Dc] matrix) and their bias pairs ([2 hidden][2]).
   char* p = static_cast<char*>(workspace);
   bf16* wf = reinterpret_cast<bf16*>(p);
-  bf16* cf = reinterpret_cast<bf16*>(p + round_up((int64_t)2 * HID * C * 2, 256));
+  bf16* cf = reinterpret_cast<bf16*>(p + round_up(2 * hidden * Dc * 2, 256));
   const bf16* w1 = static_cast<const bf16*>(fc1_w);
   const bf16* w2 = static_cast<const bf16*>(fc2_w);
   if (use_norm) {
-    int rc = launch_fold_ln(fc1_w, norm_w, norm_b, wf, cf, HID, stream);
-    if (!rc) rc = launch_fold_ln(fc2_w, norm_w, norm_b, wf + HID * C, cf + HID * 2, HID, stream);
+    int rc = launch_fold_ln(fc1_w, norm_w, norm_b, wf, cf, hidden, stream, (int)Dc);
+    if (!rc) rc = launch_fold_ln(fc2_w, norm_w, norm_b, wf + hidden * Dc, cf + hidden * 2, hidden, stream, (int)Dc);
     if (rc) return rc;
     w1 = wf;
-    w2 = wf + HID * C;
+    w2 = wf + hidden * Dc;
   }
-  if (hipFuncSetAttribute(reinterpret_cast<const void*>(transition_pair_kernel),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, kSmem) != hipSuccess)
-    return set_error(BIOEMU_ERR_LAUNCH, "transition_pair: cannot set dynamic LDS size");
-  const long long nwg = (P + kPairsPerWg - 1) / kPairsPerWg;
-  if (nwg > 0x7fffffffLL) return set_error(BIOEMU_ERR_INVALID_ARG, "transition_pair: too many rows");
-  KernelTimerScope timed("transition_pair", stream);
-  hipLaunchKernelGGL(transition_pair_kernel, dim3((unsigned)nwg), dim3(kThreads), kSmem, stream,
-                     static_cast<const bf16*>(x), w1, w2, static_cast<const bf16*>(fc3_w), cf,
-                     static_cast<bf16*>(out), (long long)P, use_norm, residual);
-  return check_launch("transition_pair");
+  const bf16* xb = static_cast<const bf16*>(x);
+  const bf16* w3 = static_cast<const bf16*>(fc3_w);
+  bf16* ob = static_cast<bf16*>(out);
+  return Dc == 128 ? launch_rows<128>(xb, w1, w2, w3, cf, ob, (long long)P, use_norm, residual, stream)
+                   : launch_rows<64>(xb, w1, w2, w3, cf, ob, (long long)P, use_norm, residual, stream);
 }

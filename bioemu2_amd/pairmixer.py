@@ -123,7 +123,7 @@ class PairMixerMSALayerHip(nn.Module, _WorkspaceMixin):
     def workspace_bytes(self, B: int, S: int, N: int) -> int:
         return max(
             _ops.pwa_workspace_bytes(B, S, N, self.msa_s, 32, 8),
-            _ops.transition_token_workspace_bytes(B * S * N, self.msa_s, self.msa_transition.hidden),
+            _ops.transition_pair_workspace_bytes(self.msa_s, self.msa_transition.hidden),
             _ops.opm_workspace_bytes(B, S, N, self.msa_s, 32),
             _ops.trimul_workspace_bytes(B, N, self.token_z),
             _ops.transition_pair_workspace_bytes(self.token_z, self.z_transition.hidden),
@@ -139,7 +139,7 @@ class PairMixerMSALayerHip(nn.Module, _WorkspaceMixin):
         ws = self._workspace(self.workspace_bytes(B, S, N), z.device)
         pm = _ops.mask_u8(token_mask)
         _ops.launch_pwa(m, z, pm, *self.pair_weighted_averaging.prepared_params(), m, 8, residual=True, ws=ws)
-        _ops.launch_transition_token(m, *self.msa_transition.prepared_params(), m, residual=True, ws=ws)
+        _ops.launch_transition_pair(m, *self.msa_transition.prepared_params(), m, residual=True, ws=ws)
         mask3, mean_rows = _ops.opm_mask3(msa_mask, B, S, N)
         _ops.launch_opm(m, mask3, mean_rows, *self.outer_product_mean.prepared_params(), out=z, z_res=z, ws=ws)
         _ops.launch_trimul(z, pm, *self.tri_mul_out.prepared_params(), z, True, residual=True, ws=ws)

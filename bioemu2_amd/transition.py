@@ -3,9 +3,10 @@
 Same constructor (``dim, hidden, out_dim, use_norm, chunk_size``), parameters
 and ``state_dict`` keys (``norm.{weight,bias}`` when ``use_norm``,
 ``fc1.weight``, ``fc2.weight``, ``fc3.weight``; transition.py:34-50) and the
-same result ``fc3(silu(fc1(LN x)) * fc2(LN x))`` (:52-76).  Pair inputs
-(``[B,N,N,128]``, hidden 512) run one fused HIP kernel; other row counts and
-widths (the single representation) run the token LN + GEMM kernels.
+same result ``fc3(silu(fc1(LN x)) * fc2(LN x))`` (:52-76).  Rows of width 128
+(hidden 512: the pair representation) or 64 (hidden 256: the MSA
+representation) run one fused HIP kernel; other widths (the single
+representation, 384) run the token LN + GEMM kernels.
 ``chunk_size`` only tiled the hidden dimension for memory in the reference
 (:76-91): the fused kernel never materialises the hidden activations, so it
 is accepted and has no effect on the result.

@@ -526,14 +526,10 @@ class PairMixerMsaWorkload(Workload):
             return ("mfma", 2.0 * 8 * n * n * S * 32)
         if kernel in ("pwa_weights", "pwa_proj", "pwa_out"):
             return PwaWorkload.kernel_work(self, kernel)
-        if kernel == "token_layernorm":
-            return ("hbm", float(S * n * 64 * 2 * 2))
-        if kernel == "transition_token_swiglu":
-            return ("hbm", float(S * n * (64 + 256) * 2))
-        if kernel == "transition_token_out":
-            return ("hbm", float(S * n * (256 + 2 * 64) * 2))
-        if kernel == "fold_ln":  # PWA (3 folds) and transition fc1, fc2
-            return fold_kernel_work(kernel, 5, 8 + 1024, 512)
+        if kernel == "transition_msa":
+            return ("mfma", 2.0 * S * n * 64 * 12 * 64)
+        if kernel == "fold_ln":  # PWA (3 folds), MSA transition and pair transition fc1, fc2
+            return fold_kernel_work(kernel, 7, 8 + 1024, 512 + 512)
         raise KeyError(kernel)
 
 

@@ -94,11 +94,13 @@ int bioemu_triatt_fwd(const void* z, const uint8_t* mask, const float* norm_w, c
                       int starting, int residual, hipStream_t stream);
 
 /*
- * Pair Transition (SwiGLU MLP), fused: LN -> fc1/fc2 -> silu(a)*b -> fc3 (+ x).
+ * Row Transition (SwiGLU MLP), fused: LN -> fc1/fc2 -> silu(a)*b -> fc3 (+ x).
  * Replaces Transition.forward (src/bioemu2/biomoa/ops/transition.py:52-91) for
- * the pair representation.  x, out: [P, D] bf16 rows (P = B*N*N), out may equal
- * x when residual != 0.  fc1_w, fc2_w: [hidden, D]; fc3_w: [D, hidden].
- * D must be 128 and hidden 512.  use_norm=0 skips the LayerNorm (norm_* unused).
+ * the pair representation (D 128, hidden 512) and the MSA representation
+ * (D 64, hidden 256; biomoa/modules/pairmixer.py:631-634).  x, out: [P, D] bf16
+ * rows (P = B*N*N pairs or B*S*N MSA entries), out may equal x when
+ * residual != 0.  fc1_w, fc2_w: [hidden, D]; fc3_w: [D, hidden].  D must be 128
+ * or 64 and hidden 4*D.  use_norm=0 skips the LayerNorm (norm_* unused).
  * The workspace holds fc1/fc2 with the LayerNorm affine folded in (size from
  * bioemu_transition_pair_workspace_bytes, independent of P).
  */
@@ -109,9 +111,10 @@ int bioemu_transition_pair_fwd(const void* x, const float* norm_w, const float* 
                                int64_t hidden, int use_norm, int residual, hipStream_t stream);
 
 /*
- * Token Transition (same op over [M, D] rows of the single or MSA
- * representation, D in {64, 128, 384}, hidden a multiple of 32): LN kernel +
- * two MFMA GEMMs.  Replaces Transition.forward (transition.py:52-91) for s and m.
+ * Token Transition (same op over [M, D] rows, D in {64, 128, 384}, hidden a
+ * multiple of 32): LN kernel + two MFMA GEMMs.  Replaces Transition.forward
+ * (transition.py:52-91) for the single representation s and any width /
+ * hidden pair the fused row kernel does not take.
  */
 size_t bioemu_transition_token_workspace_bytes(int64_t M, int64_t D, int64_t hidden);
 int bioemu_transition_token_fwd(const void* x, const float* norm_w, const float* norm_b,

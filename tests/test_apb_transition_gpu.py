@@ -161,14 +161,32 @@ def test_token_transition_matches_oracle(gpu_device, rows):
     _check(got, want, f"token transition rows={rows}")
 
 
-def test_msa_transition_matches_oracle(gpu_device):
-    """The MSA representation's transition (dim 64, hidden 256) over [B,S,N,64] rows."""
-    m = _transition(gpu_device, 64, 256)
-    x = torch.randn(1, 7, 33, 64).to(torch.bfloat16).to(gpu_device)
+@pytest.mark.parametrize("use_norm", [True, False])
+@pytest.mark.parametrize("shape", [(1, 7, 33), (2, 16, 64), (1, 1, 1)])
+def test_msa_transition_matches_oracle(gpu_device, use_norm, shape):
+    """The MSA representation's transition (dim 64, hidden 256) over [B,S,N,64] rows: the fused
+    row kernel (ragged row counts, a single row) and, on the same input, the token LN + GEMM path."""
+    m = _transition(gpu_device, 64, 256, use_norm)
+    x = torch.randn(*shape, 64).to(torch.bfloat16).to(gpu_device)
     with torch.no_grad():
         got = m(x).float().cpu()
-    want = oracle.transition(x.cpu(), state(m))
-    _check(got, want, "msa transition")
+        tok = torch.empty_like(x)
+        _ops.launch_transition_token(x, *m.prepared_params(), tok)
+    want = oracle.transition(x.cpu(), state(m), use_norm=use_norm)
+    _check(got, want, f"msa transition {shape} use_norm={use_norm}")
+    _check(tok.float().cpu(), want, f"msa transition (token path) {shape} use_norm={use_norm}")
+
+
+def test_msa_transition_residual_and_rowwise(gpu_device):
+    m = _transition(gpu_device, 64, 256)
+    x = torch.randn(1, 40, 70, 64).to(torch.bfloat16).to(gpu_device)
+    with torch.no_grad():
+        upd = m(x)
+        assert torch.equal(m(x[:, 13:14]), upd[:, 13:14])
+        xx = x.clone()
+        _ops.launch_transition_pair(xx, *m.prepared_params(), xx, residual=True)
+    ref = x.float() + upd.float()
+    assert max_abs(xx.float(), ref) <= 2 ** -7 * ref.abs().max().item()
 
 
 def test_pair_transition_residual_and_rowwise(gpu_device):

@@ -67,7 +67,9 @@ def test_host_only_queries():
     assert lib.bioemu_trimul_workspace_bytes(0, n, 128) == 0
     # folded fc1 | fc2 ([1024][128] bf16) and their bias pairs ([1024][2] bf16)
     assert lib.bioemu_transition_pair_workspace_bytes(128, 512) == 1024 * 128 * 2 + 1024 * 4
-    assert lib.bioemu_transition_pair_workspace_bytes(64, 256) == 0
+    assert lib.bioemu_transition_pair_workspace_bytes(64, 256) == 512 * 64 * 2 + 512 * 4
+    assert lib.bioemu_transition_pair_workspace_bytes(64, 128) == 0
+    assert lib.bioemu_transition_pair_workspace_bytes(384, 1536) == 0
 
 
 def test_invalid_arguments_rejected_without_gpu():
