@@ -78,3 +78,56 @@ def test_pairmixer_inplace_matches_out_of_place(gpu_device):
     z2, m2 = z.clone(), m.clone()
     layer.forward_(s, z2, m2, pm, msa_mask)
     assert torch.equal(z2, z_new) and torch.equal(m2, m_new)
+
+
+def test_msa_mask_controls_pair_update(gpu_device):
+    """As the reference's test_msa_mask_controls_pair_update (tests/biomoa/modules/test_pairmixer.py):
+    changing a masked MSA row leaves z bit-identical; changing a valid row changes it."""
+    torch.manual_seed(0)
+    layer = init_module(PairMixerMSALayerHip(384, 64, 128, 0.0, 0.0), 0).to(gpu_device).eval()
+    g = torch.Generator().manual_seed(4)
+    B, S, n = 1, 6, 40
+    z = torch.randn(B, n, n, 128, generator=g).to(torch.bfloat16).to(gpu_device)
+    m = torch.randn(B, S, n, 64, generator=g).to(torch.bfloat16).to(gpu_device)
+    pm = torch.ones(B, n, n, dtype=torch.bool, device=gpu_device)
+    msa_mask = torch.ones(B, S, n, dtype=torch.bool, device=gpu_device)
+    msa_mask[:, 4:] = False
+    _, z_base, _ = layer(None, z, m, pm, msa_mask)
+    m_masked = m.clone()
+    m_masked[:, 5] += 10.0
+    _, z_masked, _ = layer(None, z, m_masked, pm, msa_mask)
+    m_valid = m.clone()
+    m_valid[:, 0] += 10.0
+    _, z_valid, _ = layer(None, z, m_valid, pm, msa_mask)
+    assert torch.equal(z_masked, z_base)
+    assert not torch.equal(z_valid, z_base)
+
+
+def test_ragged_batch_equals_systems_alone(gpu_device):
+    """As the reference's test_pairmixer_padding_integration: a ragged batch (short system padded to the
+    long one's token and MSA-row counts) gives each system's valid outputs bit-identical to running it alone."""
+    torch.manual_seed(0)
+    layer = init_module(PairMixerMSALayerHip(384, 64, 128, 0.15, 0.25), 0).to(gpu_device).eval()
+    g = torch.Generator().manual_seed(6)
+    sizes = [(37, 9), (70, 12)]  # (tokens, MSA rows)
+    n_max, s_max = 70, 12
+    z = torch.randn(2, n_max, n_max, 128, generator=g).to(torch.bfloat16)
+    m = torch.randn(2, s_max, n_max, 64, generator=g).to(torch.bfloat16)
+    tok = torch.zeros(2, n_max, dtype=torch.bool)
+    msa_mask = torch.zeros(2, s_max, n_max, dtype=torch.bool)
+    for b, (n, s) in enumerate(sizes):
+        tok[b, :n] = True
+        msa_mask[b, :s, :n] = True
+    pm = tok[:, :, None] & tok[:, None, :]
+    dev = gpu_device
+    _, z_rag, m_rag = layer(None, z.to(dev), m.to(dev), pm.to(dev), msa_mask.to(dev))
+    for b, (n, s) in enumerate(sizes):
+        zb = z[b:b + 1, :n, :n].contiguous().to(dev)
+        mb = m[b:b + 1, :s, :n].contiguous().to(dev)
+        pmb = torch.ones(1, n, n, dtype=torch.bool, device=dev)
+        mmb = torch.ones(1, s, n, dtype=torch.bool, device=dev)
+        _, z_one, m_one = layer(None, zb, mb, pmb, mmb)
+        dz = (z_rag[b, :n, :n].float() - z_one[0].float()).abs().max().item()
+        dm = (m_rag[b, :s, :n].float() - m_one[0].float()).abs().max().item()
+        print(f"system {b} (n={n}, S={s}): max |ragged - alone| z={dz:.3e} m={dm:.3e}")
+        assert dz == 0.0 and dm == 0.0
