@@ -58,6 +58,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _c_int,
         [_c_void_p] * 13 + [_c_void_p, _c_size_t] + [_c_int64] * 6 + [_c_int, _c_void_p],
     ),
+    "bioemu_swa_workspace_bytes": (_c_size_t, [_c_int64] * 7),
+    "bioemu_swa_fwd": (
+        _c_int,
+        [_c_void_p] * 13 + [_c_void_p, _c_size_t] + [_c_int64] * 8 + [_c_int, _c_void_p],
+    ),
     "bioemu_opm_workspace_bytes": (_c_size_t, [_c_int64] * 5),
     "bioemu_opm_fwd": (
         _c_int,

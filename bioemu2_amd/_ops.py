@@ -429,6 +429,107 @@ def _(s, z, mask, norm_s_w, norm_s_b, w_qkv, q_bias, w_g, norm_z_w, norm_z_b, w_
 
 
 # ----------------------------------------------------------------------------
+# Sliding-window attention with pair bias
+# ----------------------------------------------------------------------------
+def swa_workspace_bytes(B: int, mult: int, NW: int, W: int, H: int, c_s: int, heads: int) -> int:
+    return int(lib().bioemu_swa_workspace_bytes(B, mult, NW, W, H, c_s, heads))
+
+
+def launch_swa(
+    s: Tensor,
+    z: Tensor,
+    mask: Tensor,
+    norm_s_w: Tensor | None,
+    norm_s_b: Tensor | None,
+    w_qkv: Tensor,
+    q_bias: Tensor,
+    w_g: Tensor,
+    norm_z_w: Tensor,
+    norm_z_b: Tensor | None,
+    w_z: Tensor,
+    w_o: Tensor,
+    out: Tensor,
+    num_heads: int,
+    multiplicity: int = 1,
+    residual: bool = False,
+    ws: Tensor | None = None,
+) -> Tensor:
+    """s [B*M*NW, W, c_s], z [B, NW, W, H, c_z], mask [B*NW, W] uint8 (attention_pair_bias.py:277-340)."""
+    require_gpu(s, "attention_pair_bias_sliding_window")
+    if s.ndim != 3 or z.ndim != 5 or mask.ndim != 2:
+        raise AssertionError(f"{tuple(s.shape)}, {tuple(z.shape)}, {tuple(mask.shape)}")
+    B, NW, W, H, c_z = z.shape
+    folded, _, c_s = s.shape
+    if folded != B * multiplicity * NW:
+        raise AssertionError(f"{tuple(s.shape)}, {tuple(z.shape)}, multiplicity={multiplicity}")
+    dev = s.device
+    _check_tensor(s, "swa s", BF16, (folded, W, c_s), dev)
+    _check_tensor(out, "swa out", BF16, (folded, W, c_s), dev)
+    _check_tensor(z, "swa z", BF16, (B, NW, W, H, c_z), dev)
+    _check_tensor(mask, "swa mask", torch.uint8, (B * NW, W), dev)
+    if norm_s_w is not None:
+        _check_tensor(norm_s_w, "swa norm_s.weight", torch.float32, (c_s,), dev)
+        _check_tensor(norm_s_b, "swa norm_s.bias", torch.float32, (c_s,), dev)
+    _check_tensor(w_qkv, "swa proj_qkv.weight", BF16, (3 * c_s, c_s), dev)
+    _check_tensor(q_bias, "swa proj_q_bias", torch.float32, (c_s,), dev)
+    _check_tensor(w_g, "swa proj_g.weight", BF16, (c_s, c_s), dev)
+    _check_tensor(norm_z_w, "swa norm_z.weight", torch.float32, (c_z,), dev)
+    if norm_z_b is not None:
+        _check_tensor(norm_z_b, "swa norm_z.bias", torch.float32, (c_z,), dev)
+    _check_tensor(w_z, "swa proj_z.weight", BF16, (num_heads, c_z), dev)
+    _check_tensor(w_o, "swa proj_o.weight", BF16, (c_s, c_s), dev)
+    need = swa_workspace_bytes(B, multiplicity, NW, W, H, c_s, num_heads)
+    if ws is None or ws.numel() < need:
+        ws = workspace(need, dev)
+    rc = lib().bioemu_swa_fwd(
+        _ptr(s), _ptr(z), _ptr(mask), _ptr(norm_s_w), _ptr(norm_s_b), _ptr(w_qkv), _ptr(q_bias), _ptr(w_g),
+        _ptr(norm_z_w), _ptr(norm_z_b), _ptr(w_z), _ptr(w_o), _ptr(out), _ptr(ws), ctypes.c_size_t(ws.numel()),
+        B, multiplicity, NW, W, H, c_s, c_z, num_heads, int(bool(residual)), _stream(s),
+    )
+    check(rc, "bioemu_swa_fwd")
+    return out
+
+
+@torch.library.custom_op("bioemu_mi355x::attention_pair_bias_sliding_window", mutates_args=(), device_types="cuda")
+def attention_pair_bias_sliding_window(
+    s: Tensor,
+    z: Tensor,
+    mask: Tensor,
+    norm_s_w: Tensor | None,
+    norm_s_b: Tensor | None,
+    w_qkv: Tensor,
+    q_bias: Tensor,
+    w_g: Tensor,
+    norm_z_w: Tensor,
+    norm_z_b: Tensor | None,
+    w_z: Tensor,
+    w_o: Tensor,
+    num_heads: int,
+    multiplicity: int,
+) -> Tensor:
+    sb = s.to(BF16).contiguous()
+    out = torch.empty_like(sb)
+    f32 = torch.float32
+
+    def f(t):
+        return None if t is None else t.to(f32).contiguous()
+
+    def h(t):
+        return t.to(BF16).contiguous()
+
+    launch_swa(
+        sb, h(z), mask_u8(mask), f(norm_s_w), f(norm_s_b), h(w_qkv), f(q_bias), h(w_g), f(norm_z_w), f(norm_z_b),
+        h(w_z), h(w_o), out, num_heads, multiplicity,
+    )
+    return out.to(s.dtype)
+
+
+@attention_pair_bias_sliding_window.register_fake
+def _(s, z, mask, norm_s_w, norm_s_b, w_qkv, q_bias, w_g, norm_z_w, norm_z_b, w_z, w_o, num_heads, multiplicity):
+    return torch.empty_like(s)
+
+
+# ----------------------------------------------------------------------------
 # Outer product mean
 # ----------------------------------------------------------------------------
 def opm_workspace_bytes(B: int, S: int, N: int, c_in: int = 64, c_hidden: int = 32) -> int:

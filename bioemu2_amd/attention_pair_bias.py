@@ -1,4 +1,5 @@
-"""Attention with pair bias on MI355X — drop-in for ``AttentionPairBias``.
+"""Attention with pair bias on MI355X — drop-ins for ``AttentionPairBias`` and
+``AttentionPairBiasSlidingWindow``.
 
 Mirrors ``src/bioemu2/biomoa/ops/attention_pair_bias.py:42-225``: the same
 constructor arguments, parameters and ``state_dict`` keys (``norm_s.*`` when
@@ -11,6 +12,12 @@ materialised logits (:193-222); the flash kernel never materialises them, so
 it is accepted and does not change the result.  ``use_efficient_fusion``
 folds the LayerNorm gain into the projection in the reference (:118-126);
 mathematically the same bias, so both settings run the same kernel.
+
+``AttentionPairBiasSlidingWindow`` mirrors :228-340 (the denoiser's atom
+transformer): constructor ``(c_s, c_z, num_heads, window_queries=32,
+window_keys=128, inf, initial_norm, tile_size, zero_init_output,
+use_bias_in_layer_norm)``, the same parameters, and
+``forward(s [B*M*NW, W, c_s], z [B, NW, W, H, c_z], mask [B*NW, W], multiplicity)``.
 """
 
 from __future__ import annotations
@@ -88,5 +95,36 @@ class AttentionPairBias(nn.Module):
         if self.inf != 1e6:
             raise ValueError("AttentionPairBias (HIP): only inf=1e6, the reference default, is supported")
         return torch.ops.bioemu_mi355x.attention_pair_bias(
+            s, z, _ops.mask_u8(mask), *self.prepared_params(), self.num_heads, multiplicity
+        )
+
+
+class AttentionPairBiasSlidingWindow(AttentionPairBias):
+    def __init__(
+        self,
+        c_s: int,
+        c_z: int,
+        num_heads: int,
+        window_queries: int = 32,
+        window_keys: int = 128,
+        inf: float = 1e6,
+        initial_norm: bool = True,
+        tile_size: int | None = 512,
+        zero_init_output: bool = False,
+        use_bias_in_layer_norm: bool = False,
+    ) -> None:
+        super().__init__(
+            c_s, c_z, num_heads, inf=inf, initial_norm=initial_norm, tile_size=tile_size,
+            zero_init_output=zero_init_output, use_bias_in_layer_norm=use_bias_in_layer_norm,
+        )
+        self.window_queries = window_queries
+        self.window_keys = window_keys
+
+    def forward(self, s: Tensor, z: Tensor, mask: Tensor, multiplicity: int = 1) -> Tensor:
+        assert s.ndim == 3 and z.ndim == 5 and mask.ndim == 2, f"{s.shape}, {z.shape}, {mask.shape}"
+        _ops.require_gpu(s, type(self).__name__)
+        if self.inf != 1e6:
+            raise ValueError("AttentionPairBiasSlidingWindow (HIP): only inf=1e6, the reference default, is supported")
+        return torch.ops.bioemu_mi355x.attention_pair_bias_sliding_window(
             s, z, _ops.mask_u8(mask), *self.prepared_params(), self.num_heads, multiplicity
         )

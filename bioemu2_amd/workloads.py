@@ -533,11 +533,75 @@ class PairMixerMsaWorkload(Workload):
         raise KeyError(kernel)
 
 
+class SwaWorkload(Workload):
+    """The denoiser's atom transformer attention (AttentionPairBiasSlidingWindow as AttentionLayer builds it,
+    transformer.py:96-105: initial_norm=False): NA = 6144 atoms (NW = 192 windows of W = 32, H = 128 keys),
+    c_s = 128, 4 heads, c_z = 16, multiplicity M = 8, trailing 40 atoms padded."""
+
+    def __init__(self, device, nw: int = 192, mult: int = 8, seed: int = 0):
+        from .attention_pair_bias import AttentionPairBiasSlidingWindow
+
+        self.nw, self.mult = nw, mult
+        self.na = nw * 32
+        self.name = f"swa_na{self.na}_m{mult}"
+        self.metric = f"ms per sliding-window pair-bias attention at {self.na} atoms, M={mult} bf16"
+        torch.manual_seed(seed)
+        self.module = init_module(AttentionPairBiasSlidingWindow(128, 16, 4, initial_norm=False), seed)
+        self.module = self.module.to(device).eval()
+        g = torch.Generator().manual_seed(seed)
+        self.s_cpu = torch.randn(mult * nw, 32, 128, generator=g).to(torch.bfloat16)
+        self.z_cpu = torch.randn(1, nw, 32, 128, 16, generator=g).to(torch.bfloat16)
+        mask = torch.ones(1, self.na, dtype=torch.bool)
+        mask[:, -40:] = False
+        self.mask_cpu = mask.view(nw, 32)
+        self.s = self.s_cpu.to(device)
+        self.z = self.z_cpu.to(device)
+        self.mask = _ops.mask_u8(self.mask_cpu.to(device))
+        self.out = torch.empty_like(self.s)
+        self.ws = _ops.workspace(_ops.swa_workspace_bytes(1, mult, nw, 32, 128, 128, 4), device)
+        self.params = self.module.prepared_params()
+        self.config = {"workload": self.name, "atoms": self.na, "windows": nw, "window_queries": 32,
+                       "window_keys": 128, "c_s": 128, "c_z": 16, "heads": 4, "multiplicity": mult,
+                       "initial_norm": False, "padded_atoms": 40}
+        rows = mult * self.na
+        self.flops = 2.0 * rows * 128 * 128 * 5 + 2.0 * mult * nw * 4 * 32 * 128 * 32 * 2 + 2.0 * nw * 32 * 128 * 16 * 4
+
+    def step(self) -> None:
+        _ops.launch_swa(self.s, self.z, self.mask, *self.params, self.out, 4, multiplicity=self.mult, ws=self.ws)
+
+    def cpu_sample(self, oracle):
+        s = self.s_cpu[: self.nw].float()   # copy 0 of M (copies are independent)
+        z = self.z_cpu.float()
+        params = {k: v.detach().cpu() for k, v in self.module.state_dict().items()}
+
+        def fn():
+            return oracle.attention_pair_bias_sliding_window(s, z, self.mask_cpu, params, 4, initial_norm=False)
+
+        return fn, 1.0 / self.mult, f"oracle.attention_pair_bias_sliding_window fp32 on 1 of {self.mult} copies"
+
+    def kernel_work(self, kernel: str) -> tuple[str, float]:
+        rows = self.mult * self.na
+        tok = rows * 128 * 2
+        bias = self.nw * 4 * 32 * 128 * 2
+        if kernel == "swa_attn":
+            # reads q, k, v, g and the bias once, writes g*o
+            return ("hbm", float(5 * tok + bias))
+        if kernel == "swa_pair_bias":
+            return ("hbm", float(self.nw * 32 * 128 * 16 * 2 + bias))
+        if kernel in ("swa_proj_q", "swa_proj_k", "swa_proj_v", "swa_proj_g"):
+            return ("hbm", float(2 * tok + 128 * 128 * 2))
+        if kernel == "swa_proj_o":
+            return ("hbm", float(2 * tok + 128 * 128 * 2))
+        raise KeyError(kernel)
+
+
 def make(op: str, device, n: int | None = None) -> Workload:
     if op == "opm":
         return OpmWorkload(device, n or 512)
     if op == "pwa":
         return PwaWorkload(device, n or 512)
+    if op == "swa":
+        return SwaWorkload(device)
     if op == "pairmixer":
         return PairMixerWorkload(device, n or 768)
     if op == "pairmixer_msa":

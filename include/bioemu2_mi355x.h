@@ -159,6 +159,29 @@ int bioemu_apb_fwd(const void* s, const void* z, const uint8_t* mask, const floa
                    int64_t N, int64_t c_s, int64_t c_z, int64_t H, int residual, hipStream_t stream);
 
 /*
+ * Sliding-window attention with pair bias (the denoiser's atom transformer).
+ * Replaces AttentionPairBiasSlidingWindow.forward
+ * (src/bioemu2/biomoa/ops/attention_pair_bias.py:277-340): the projections of
+ * bioemu_apb_fwd per atom; window w of W queries attends to the H keys at atom
+ * positions [w*W - (H-W)/2, w*W - (H-W)/2 + H) of the same copy (zero k / v,
+ * mask 0 outside [0, NW*W)); bias = LN_z(z) Wz^T per (batch, window), shared
+ * by the `mult` copies; masked keys replaced by -1e6.
+ * s, out: [B*mult*NW, W, c_s] bf16 (rows ordered batch, copy, window; out may
+ * equal s when residual != 0); z: [B, NW, W, H, c_z] bf16; mask: [B*NW, W]
+ * uint8.  norm_s_w/b null: initial_norm=False; norm_z_b may be null.
+ * Supported: W = 32, H a multiple of 32 with H - W a multiple of 32, head dim
+ * 32 (c_s = 32*heads, c_s in {64, 128, 384}), c_z in {16, 32}.
+ */
+size_t bioemu_swa_workspace_bytes(int64_t B, int64_t mult, int64_t NW, int64_t W, int64_t H, int64_t c_s,
+                                  int64_t heads);
+int bioemu_swa_fwd(const void* s, const void* z, const uint8_t* mask, const float* norm_s_w,
+                   const float* norm_s_b, const void* w_qkv, const float* q_bias, const void* w_g,
+                   const float* norm_z_w, const float* norm_z_b, const void* w_z, const void* w_o,
+                   void* out, void* workspace, size_t workspace_bytes, int64_t B, int64_t mult,
+                   int64_t NW, int64_t W, int64_t H, int64_t c_s, int64_t c_z, int64_t heads, int residual,
+                   hipStream_t stream);
+
+/*
  * Fused OuterProductMean.
  * Replaces OuterProductMeanVanilla.forward / OuterProductMeanTritonMemorySaving.forward
  * (src/bioemu2/biomoa/ops/outer_product_mean.py:45-75, :129-152):

@@ -24,6 +24,12 @@ How each function is pinned (see ``tests/test_oracle_*.py``):
 * ``attention_pair_bias`` — brute-force loops, reduction to torch SDPA with an
                     additive mask, tiled == untiled, multiplicity == separate runs,
                     bitwise padding invariance (test_attention_pair_bias.py:805-867).
+* ``attention_pair_bias_sliding_window`` — brute-force loops over absolute
+                    atom positions, a planted one-hot bias that must select the
+                    key the centred window puts at that offset (the window's
+                    own queries sit at offsets ctx..ctx+W-1), reduction to
+                    ``attention_pair_bias`` per window when H == W, sequence-edge
+                    keys masked, multiplicity == separate runs.
 * ``outer_product_mean`` — brute-force loops over S, masked rows contribute
                     exact zeros (test_outer_product_mean.py:286-310), the
                     divisor is the per-batch valid-row count (duplicating the
@@ -44,12 +50,14 @@ No function here is "parity unpinned".
 
 from .pairformer_ref import (  # noqa: F401
     attention_pair_bias,
+    attention_pair_bias_sliding_window,
     outer_product_mean,
     pair_mask_from_token_mask,
     pair_weighted_averaging,
     pairformer_block,
     pairmixer_layer,
     pairmixer_msa_layer,
+    sliding_window_keys,
     transition,
     triangle_attention,
     trimul,

@@ -213,6 +213,75 @@ def attention_pair_bias(
     return (g * o) @ _p(params, "proj_o.weight").T  # :225
 
 
+def sliding_window_keys(num_windows: int, window_queries: int, window_keys: int) -> tuple[Tensor, Tensor]:
+    """Absolute key positions of every window and whether they lie in the sequence.
+
+    The key window of size H is centred on the W-query window: it starts
+    (H - W) / 2 positions before the window's first query; positions outside
+    [0, NW*W) are the reference's zero padding (attention_pair_bias.py:302-309,
+    :311-317).  Returns ``pos [NW, H]`` (clamped into range) and ``inside [NW, H]``.
+    """
+    ctx = (window_keys - window_queries) // 2
+    start = torch.arange(num_windows) * window_queries - ctx
+    pos = start[:, None] + torch.arange(window_keys)[None, :]
+    inside = (pos >= 0) & (pos < num_windows * window_queries)
+    return pos.clamp(0, num_windows * window_queries - 1), inside
+
+
+def attention_pair_bias_sliding_window(
+    s: Tensor,
+    z: Tensor,
+    mask: Tensor,
+    params: dict,
+    num_heads: int,
+    multiplicity: int = 1,
+    initial_norm: bool = True,
+    inf: float = 1e6,
+) -> Tensor:
+    """AttentionPairBiasSlidingWindow.forward (biomoa/ops/attention_pair_bias.py:277-340).
+
+    s [B*M*NW, W, c_s], z [B, NW, W, H, c_z], mask [B*NW, W] bool -> [B*M*NW, W, c_s]
+    (float32).  Rows of s are ordered (b, m, window); the keys of window w are
+    the k/v rows of the same (b, m) sequence at ``sliding_window_keys`` (zero
+    outside the sequence, :302-309), their mask is gathered the same way (False
+    outside, :311-317); the pair bias ``proj_z(norm_z(z))`` is per (b, window)
+    and shared by the M copies (:319, :328-330); masked keys are replaced by
+    -inf (:332-334); out = proj_o(g * o) (:339-340).
+    """
+    s = _f32(s)
+    z = _f32(z)
+    mask = mask.bool().cpu()
+    assert s.ndim == 3 and z.ndim == 5 and mask.ndim == 2  # :288
+    M = multiplicity
+    B, NW, W, H = z.shape[:4]
+    folded, _, c_s = s.shape
+    BM = folded // NW
+    assert BM == B * M and s.shape[1] == W and mask.shape == (B * NW, W)
+    nh = num_heads
+    d = c_s // nh
+    if initial_norm:
+        s = _ln(s, params, "norm_s")  # :294-295
+    wqkv = _p(params, "proj_qkv.weight")
+    q = (s @ wqkv[:c_s].T + _p(params, "proj_q_bias")).view(BM, NW, W, nh, d)  # :297-299
+    kvals = (s @ wqkv[c_s:2 * c_s].T).reshape(BM, NW * W, nh, d)
+    vvals = (s @ wqkv[2 * c_s:].T).reshape(BM, NW * W, nh, d)
+    g = torch.sigmoid(s @ _p(params, "proj_g.weight").T).view(BM, NW, W, c_s)  # :300
+    pos, inside = sliding_window_keys(NW, W, H)
+    kw = kvals[:, pos] * inside[None, :, :, None, None]  # [BM, NW, H, nh, d]
+    vw = vvals[:, pos] * inside[None, :, :, None, None]
+    key_ok = mask.view(B, NW * W)[:, pos] & inside[None]  # [B, NW, H]
+    bias = (_ln(z, params, "norm_z") @ _p(params, "proj_z.weight").T).permute(0, 1, 4, 2, 3)  # [B,NW,nh,W,H] (:319)
+    out = torch.empty(BM, NW, W, c_s)
+    for bm in range(BM):
+        b = bm // M
+        logits = torch.einsum("wihd,wjhd->whij", q[bm], kw[bm]) / (d**0.5)  # :325-326
+        logits = logits + bias[b]  # :328-330
+        logits = logits.masked_fill(~key_ok[b][:, None, None, :], -inf)  # :332-334
+        o = torch.einsum("whij,wjhd->wihd", logits.softmax(dim=-1), vw[bm])  # :336-337
+        out[bm] = (g[bm] * o.reshape(NW, W, c_s)) @ _p(params, "proj_o.weight").T  # :339-340
+    return out.view(folded, W, c_s)
+
+
 # ----------------------------------------------------------------------------
 # Outer product mean
 # ----------------------------------------------------------------------------
