@@ -63,6 +63,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _c_int,
         [_c_void_p] * 13 + [_c_void_p, _c_size_t] + [_c_int64] * 8 + [_c_int, _c_void_p],
     ),
+    "bioemu_distogram_fwd": (_c_int, [_c_void_p] * 4 + [_c_int64] * 4 + [_c_void_p]),
+    "bioemu_pair_cond_workspace_bytes": (_c_size_t, [_c_int64] * 3),
+    "bioemu_pair_cond_proj_fwd": (
+        _c_int,
+        [_c_void_p] * 7 + [_c_size_t] + [_c_int64] * 4 + [_c_void_p],
+    ),
     "bioemu_opm_workspace_bytes": (_c_size_t, [_c_int64] * 5),
     "bioemu_opm_fwd": (
         _c_int,

@@ -302,8 +302,9 @@ def launch_transition_token(
 
 
 def _is_row_transition(x: Tensor, hidden: int) -> bool:
-    """Widths the fused row kernel takes: pair (128, hidden 512) and MSA (64, hidden 256) rows."""
-    return x.shape[-1] in (64, 128) and hidden == 4 * x.shape[-1]
+    """Widths the fused row kernel takes: rows of 64 or 128 channels with hidden 4x (the trunk's pair and MSA
+    transitions) or 2x (the denoiser's pairwise conditioning)."""
+    return x.shape[-1] in (64, 128) and hidden in (2 * x.shape[-1], 4 * x.shape[-1])
 
 
 @torch.library.custom_op("bioemu_mi355x::transition", mutates_args=(), device_types="cuda")
@@ -527,6 +528,53 @@ def attention_pair_bias_sliding_window(
 @attention_pair_bias_sliding_window.register_fake
 def _(s, z, mask, norm_s_w, norm_s_b, w_qkv, q_bias, w_g, norm_z_w, norm_z_b, w_z, w_o, num_heads, multiplicity):
     return torch.empty_like(s)
+
+
+# ----------------------------------------------------------------------------
+# Pair glue: distogram head, pairwise-conditioning projection
+# ----------------------------------------------------------------------------
+def launch_distogram(z: Tensor, w: Tensor, b: Tensor, out: Tensor) -> Tensor:
+    require_gpu(z, "distogram")
+    if z.ndim != 4 or z.shape[1] != z.shape[2]:
+        raise ValueError(f"distogram: z must be [B,N,N,c_z], got {tuple(z.shape)}")
+    B, N, _, c_z = z.shape
+    nb = w.shape[0]
+    dev = z.device
+    _check_tensor(z, "distogram z", BF16, (B, N, N, c_z), dev)
+    _check_tensor(w, "distogram.weight", BF16, (nb, c_z), dev)
+    _check_tensor(b, "distogram.bias", torch.float32, (nb,), dev)
+    _check_tensor(out, "distogram out", BF16, (B, N, N, nb), dev)
+    rc = lib().bioemu_distogram_fwd(_ptr(z), _ptr(w), _ptr(b), _ptr(out), B, N, c_z, nb, _stream(z))
+    check(rc, "bioemu_distogram_fwd")
+    return out
+
+
+def pair_cond_workspace_bytes(token_z: int, c_rel: int, a_z: int) -> int:
+    return int(lib().bioemu_pair_cond_workspace_bytes(token_z, c_rel, a_z))
+
+
+def launch_pair_cond_proj(
+    z: Tensor, rel: Tensor, ln_w: Tensor, ln_b: Tensor, w: Tensor, out: Tensor, ws: Tensor | None = None
+) -> Tensor:
+    require_gpu(z, "pairwise_conditioning")
+    token_z, c_rel, a_z = z.shape[-1], rel.shape[-1], w.shape[0]
+    P = z.numel() // token_z
+    dev = z.device
+    _check_tensor(z, "pair_cond z_trunk", BF16, tuple(z.shape), dev)
+    _check_tensor(rel, "pair_cond rel_pos", BF16, tuple(z.shape[:-1]) + (c_rel,), dev)
+    _check_tensor(ln_w, "pair_cond norm.weight", torch.float32, (token_z + c_rel,), dev)
+    _check_tensor(ln_b, "pair_cond norm.bias", torch.float32, (token_z + c_rel,), dev)
+    _check_tensor(w, "pair_cond proj.weight", BF16, (a_z, token_z + c_rel), dev)
+    _check_tensor(out, "pair_cond out", BF16, tuple(z.shape[:-1]) + (a_z,), dev)
+    need = pair_cond_workspace_bytes(token_z, c_rel, a_z)
+    if ws is None or ws.numel() < need:
+        ws = workspace(max(need, 1), dev)
+    rc = lib().bioemu_pair_cond_proj_fwd(
+        _ptr(z), _ptr(rel), _ptr(ln_w), _ptr(ln_b), _ptr(w), _ptr(out), _ptr(ws), ctypes.c_size_t(ws.numel()),
+        P, token_z, c_rel, a_z, _stream(z),
+    )
+    check(rc, "bioemu_pair_cond_proj_fwd")
+    return out
 
 
 # ----------------------------------------------------------------------------

@@ -33,9 +33,13 @@ __global__ __launch_bounds__(kC) void fold_ln_kernel(const bf16* __restrict__ w,
 int launch_fold_ln(const void* w, const float* gamma, const float* beta, void* wf, void* cf, int64_t rows,
                    hipStream_t stream, int width) {
   if (rows <= 0 || rows > 65535) return set_error(BIOEMU_ERR_INVALID_ARG, "fold_ln: bad row count %lld", (long long)rows);
-  if (width != 64 && width != 128) return set_error(BIOEMU_ERR_INVALID_ARG, "fold_ln: width %d unsupported", width);
+  if (width != 64 && width != 128 && width != 256)
+    return set_error(BIOEMU_ERR_INVALID_ARG, "fold_ln: width %d unsupported", width);
   KernelTimerScope timed("fold_ln", stream);
-  if (width == 128)
+  if (width == 256)
+    hipLaunchKernelGGL(fold_ln_kernel<256>, dim3((unsigned)rows), dim3(256), 0, stream, static_cast<const bf16*>(w),
+                       gamma, beta, static_cast<bf16*>(wf), static_cast<bf16*>(cf));
+  else if (width == 128)
     hipLaunchKernelGGL(fold_ln_kernel<128>, dim3((unsigned)rows), dim3(128), 0, stream, static_cast<const bf16*>(w),
                        gamma, beta, static_cast<bf16*>(wf), static_cast<bf16*>(cf));
   else

@@ -42,7 +42,7 @@ int launch_bgemm_nt(const void* A, const void* B, void* C, int64_t batch, int64_
 
 // LayerNorm folding (fold.hip): wf = W diag(gamma) [rows][width] bf16, cf = W beta
 // as bf16 (hi, lo) pairs [rows][2]; beta may be null.  W is [rows][width] bf16,
-// width 128 (default) or 64.
+// width 128 (default), 64 or 256.
 int launch_fold_ln(const void* w, const float* gamma, const float* beta, void* wf, void* cf, int64_t rows,
                    hipStream_t stream, int width = 128);
 inline size_t fold_bytes(int64_t rows, int64_t width = 128) {

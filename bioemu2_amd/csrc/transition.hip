@@ -1,5 +1,6 @@
 // Row-wise Transition (SwiGLU MLP) for gfx950: the pair representation
-// (c = 128) and the MSA representation (c = 64), hidden = 4c.
+// (c = 128) and the MSA representation (c = 64), hidden = 4c (the trunk) or
+// 2c (the denoiser's pairwise conditioning, diffusion.py:498-507).
 //
 // Reference: Transition.forward (src/bioemu2/biomoa/ops/transition.py:52-91):
 //   xn = LN(x) (eps 1e-5, with bias) when use_norm;  out = fc3(silu(fc1(xn)) * fc2(xn))
@@ -36,9 +37,9 @@ constexpr int HC = 32;                      // hidden chunk
 constexpr int kThreads = 256;               // 4 waves
 constexpr int kRowsPerWg = 128;
 
-template <int C>
+template <int C, int HIDDEN>
 struct Geo {
-  static constexpr int HID = 4 * C;
+  static constexpr int HID = HIDDEN;
   static constexpr int NCH = HID / HC;                       // hidden chunks
   static constexpr int KS = C / 16;                          // 8-channel groups per lane (k-steps)
   static constexpr int RowChunks = C / 8;                    // 16-byte chunks per fc1 / fc2 row
@@ -72,11 +73,11 @@ __device__ __forceinline__ void copy4_to_lds(__amdgpu_buffer_rsrc_t r, const bf1
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(lds), 4, voff, soff, 0, 0);
 }
 
-template <int C>
+template <int C, int HIDDEN>
 __global__ __launch_bounds__(kThreads) void transition_rows_kernel(
     const bf16* x, const bf16* __restrict__ w1, const bf16* __restrict__ w2, const bf16* __restrict__ w3,
     const bf16* __restrict__ cf, bf16* out, long long P, int use_norm, int residual) {
-  using G = Geo<C>;
+  using G = Geo<C, HIDDEN>;
   constexpr int HID = G::HID, KS = G::KS;
   extern __shared__ __attribute__((aligned(16))) char smem_raw[];
   bf16* smem = reinterpret_cast<bf16*>(smem_raw);
@@ -214,18 +215,19 @@ __global__ __launch_bounds__(kThreads) void transition_rows_kernel(
   }
 }
 
-template <int C>
+template <int C, int HIDDEN>
 int launch_rows(const bf16* x, const bf16* w1, const bf16* w2, const bf16* w3, const bf16* cf, bf16* out,
                 long long P, int use_norm, int residual, hipStream_t stream) {
-  auto* kern = transition_rows_kernel<C>;
-  if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                          Geo<C>::Smem) != hipSuccess)
+  auto* kern = transition_rows_kernel<C, HIDDEN>;
+  constexpr int smem = Geo<C, HIDDEN>::Smem;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, smem) !=
+      hipSuccess)
     return set_error(BIOEMU_ERR_LAUNCH, "transition_pair: cannot set dynamic LDS size");
   const long long nwg = (P + kRowsPerWg - 1) / kRowsPerWg;
   if (nwg > 0x7fffffffLL) return set_error(BIOEMU_ERR_INVALID_ARG, "transition_pair: too many rows");
   KernelTimerScope timed(C == 128 ? "transition_pair" : "transition_msa", stream);
-  hipLaunchKernelGGL(kern, dim3((unsigned)nwg), dim3(kThreads), Geo<C>::Smem, stream, x, w1, w2, w3, cf, out, P,
-                     use_norm, residual);
+  hipLaunchKernelGGL(kern, dim3((unsigned)nwg), dim3(kThreads), smem, stream, x, w1, w2, w3, cf, out, P, use_norm,
+                     residual);
   return check_launch("transition_pair");
 }
 
@@ -234,8 +236,12 @@ int launch_rows(const bf16* x, const bf16* w1, const bf16* w2, const bf16* w3, c
 
 using namespace bioemu;
 
+static bool supported(int64_t Dc, int64_t hidden) {
+  return (Dc == 64 || Dc == 128) && (hidden == 4 * Dc || hidden == 2 * Dc);
+}
+
 extern "C" size_t bioemu_transition_pair_workspace_bytes(int64_t Dc, int64_t hidden) {
-  if ((Dc != 64 && Dc != 128) || hidden != 4 * Dc) return 0;
+  if (!supported(Dc, hidden)) return 0;
   return fold_bytes(2 * hidden, Dc);
 }
 
@@ -244,9 +250,9 @@ extern "C" int bioemu_transition_pair_fwd(const void* x, const float* norm_w, co
                                           void* out, void* workspace, size_t workspace_bytes, int64_t P,
                                           int64_t Dc, int64_t hidden, int use_norm, int residual,
                                           hipStream_t stream) {
-  if ((Dc != 64 && Dc != 128) || hidden != 4 * Dc)
+  if (!supported(Dc, hidden))
     return set_error(BIOEMU_ERR_UNSUPPORTED,
-                     "transition_pair: only dim 128 / hidden 512 and dim 64 / hidden 256 supported (got %lld, %lld)",
+                     "transition_pair: dim must be 64 or 128 with hidden 4*dim or 2*dim (got %lld, %lld)",
                      (long long)Dc, (long long)hidden);
   if (P <= 0) return set_error(BIOEMU_ERR_INVALID_ARG, "transition_pair: bad row count %lld", (long long)P);
   if (!x || !fc1_w || !fc2_w || !fc3_w || !out || !workspace || (use_norm && (!norm_w || !norm_b)))
@@ -276,6 +282,10 @@ extern "C" int bioemu_transition_pair_fwd(const void* x, const float* norm_w, co
   const bf16* xb = static_cast<const bf16*>(x);
   const bf16* w3 = static_cast<const bf16*>(fc3_w);
   bf16* ob = static_cast<bf16*>(out);
-  return Dc == 128 ? launch_rows<128>(xb, w1, w2, w3, cf, ob, (long long)P, use_norm, residual, stream)
-                   : launch_rows<64>(xb, w1, w2, w3, cf, ob, (long long)P, use_norm, residual, stream);
+  const long long rows = (long long)P;
+  if (Dc == 128)
+    return hidden == 512 ? launch_rows<128, 512>(xb, w1, w2, w3, cf, ob, rows, use_norm, residual, stream)
+                         : launch_rows<128, 256>(xb, w1, w2, w3, cf, ob, rows, use_norm, residual, stream);
+  return hidden == 256 ? launch_rows<64, 256>(xb, w1, w2, w3, cf, ob, rows, use_norm, residual, stream)
+                       : launch_rows<64, 128>(xb, w1, w2, w3, cf, ob, rows, use_norm, residual, stream);
 }

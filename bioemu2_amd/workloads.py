@@ -77,12 +77,13 @@ def trimul_kernel_work(name: str, B: int, N: int, c: int = 128) -> tuple[str, fl
     return None
 
 
-def fold_kernel_work(name: str, launches: int, rows128: int, rows64: int = 0) -> tuple[str, float] | None:
+def fold_kernel_work(name: str, launches: int, rows128: int, rows64: int = 0,
+                     rows256: int = 0) -> tuple[str, float] | None:
     """LayerNorm folds: W diag(gamma) and W beta, reading and writing each weight once; the amount
-    per launch averaged over the step's `launches` folds of `rows128` rows of width 128 and
-    `rows64` of width 64."""
+    per launch averaged over the step's `launches` folds of `rows128` rows of width 128, `rows64`
+    of width 64 and `rows256` of width 256."""
     if name == "fold_ln":
-        return ("hbm", float(2 * (rows128 * 128 + rows64 * 64) * 2) / launches)
+        return ("hbm", float(2 * (rows128 * 128 + rows64 * 64 + rows256 * 256) * 2) / launches)
     return None
 
 
@@ -595,6 +596,143 @@ class SwaWorkload(Workload):
         raise KeyError(kernel)
 
 
+class ApbWorkload(Workload):
+    """Config 2: pair-bias attention, s [8,512,384] bf16, z [8,512,512,128], 16 heads of 24, last 51 keys
+    masked (initial_norm=True); with ``mult`` > 1 the denoiser form: B=1, M copies sharing one z."""
+
+    def __init__(self, device, n: int = 512, B: int = 8, mult: int = 1, initial_norm: bool = True, seed: int = 0):
+        from .attention_pair_bias import AttentionPairBias
+
+        self.n, self.B, self.mult = n, B, mult
+        self.name = f"apb_b{B}_m{mult}_n{n}"
+        self.metric = f"ms per pair-bias attention at B={B}, M={mult}, N={n} bf16"
+        torch.manual_seed(seed)
+        self.module = init_module(AttentionPairBias(384, 128, 16, initial_norm=initial_norm), seed).to(device)
+        self.module = self.module.eval()
+        g = torch.Generator().manual_seed(seed)
+        self.s_cpu = torch.randn(B * mult, n, 384, generator=g).to(torch.bfloat16)
+        self.z_cpu = torch.randn(B, n, n, 128, generator=g).to(torch.bfloat16)
+        self.mask_cpu = torch.ones(B, n, dtype=torch.bool)
+        self.mask_cpu[:, n - n // 10:] = False
+        self.initial_norm = initial_norm
+        self.s = self.s_cpu.to(device)
+        self.z = self.z_cpu.to(device)
+        self.mask = _ops.mask_u8(self.mask_cpu.to(device))
+        self.out = torch.empty_like(self.s)
+        self.ws = _ops.workspace(_ops.apb_workspace_bytes(B, mult, n, 384, 16), device)
+        self.params = self.module.prepared_params()
+        self.config = {"workload": self.name, "batch": B, "multiplicity": mult, "N": n, "c_s": 384, "c_z": 128,
+                       "heads": 16, "head_dim": 24, "masked_keys": n // 10, "initial_norm": initial_norm}
+        rows = B * mult * n
+        self.flops = (2.0 * rows * 384 * 384 * 5 + 2.0 * B * n * n * 128 * 16
+                      + 2.0 * 2 * B * mult * n * n * 384)
+
+    def step(self) -> None:
+        _ops.launch_apb(self.s, self.z, self.mask, *self.params, self.out, 16, self.mult, ws=self.ws)
+
+    def cpu_sample(self, oracle):
+        s = self.s_cpu[: self.mult].float()   # batch element 0 with its M copies
+        z = self.z_cpu[:1].float()
+        params = {k: v.detach().cpu() for k, v in self.module.state_dict().items()}
+
+        def fn():
+            return oracle.attention_pair_bias(s, z, self.mask_cpu[:1], params, 16, multiplicity=self.mult,
+                                              initial_norm=self.initial_norm)
+
+        return fn, 1.0 / self.B, f"oracle.attention_pair_bias fp32 on batch element 1 of {self.B}"
+
+    def kernel_work(self, kernel: str) -> tuple[str, float]:
+        n, B, M = self.n, self.B, self.mult
+        np_ = -(-n // 32) * 32
+        tok = B * M * np_ * 384 * 2
+        if kernel == "apb_pair_bias":
+            return ("hbm", float(B * n * n * 128 * 2 + B * 16 * np_ * np_ * 2))
+        if kernel == "apb_flash":
+            # reads q, k, v, g and the bias, writes g*o; the QK^T / PV products are 4 N^2 c_s flops per copy
+            return ("hbm", float(5 * tok + B * 16 * np_ * np_ * 2))
+        if kernel in ("apb_proj_q", "apb_proj_k", "apb_proj_v", "apb_proj_g", "apb_proj_o", "token_layernorm"):
+            return ("hbm", float(2 * tok + 384 * 384 * 2))
+        if kernel == "fold_ln":
+            return fold_kernel_work(kernel, 1, 16)
+        raise KeyError(kernel)
+
+
+class DistogramWorkload(Workload):
+    """The trunk's distogram head (DistogramModule, token_z 128, 64 bins) on z [1,768,768,128] bf16."""
+
+    def __init__(self, device, n: int = 768, bins: int = 64, seed: int = 0):
+        from .glue import DistogramModule
+
+        self.n, self.bins = n, bins
+        self.name = f"distogram_n{n}_bins{bins}"
+        self.metric = f"ms per distogram head at N={n}, {bins} bins bf16"
+        torch.manual_seed(seed)
+        self.module = init_module(DistogramModule(128, bins), seed).to(device)
+        g = torch.Generator().manual_seed(seed)
+        self.z_cpu = torch.randn(1, n, n, 128, generator=g).to(torch.bfloat16)
+        self.z = self.z_cpu.to(device)
+        self.out = torch.empty(1, n, n, bins, dtype=torch.bfloat16, device=device)
+        self.params = self.module.prepared_params()
+        self.config = {"workload": self.name, "N": n, "c_z": 128, "num_bins": bins}
+        self.flops = 2.0 * n * n * 128 * bins
+
+    def step(self) -> None:
+        _ops.launch_distogram(self.z, *self.params, self.out)
+
+    def cpu_sample(self, oracle):
+        z = self.z_cpu.float()
+        params = {k: v.detach().cpu() for k, v in self.module.state_dict().items()}
+        return (lambda: oracle.distogram(z, params)), 1.0, f"oracle.distogram fp32, full N={self.n}"
+
+    def kernel_work(self, kernel: str) -> tuple[str, float]:
+        if kernel == "distogram":
+            # reads z once (each unordered pair's two rows), writes both orders of the output
+            return ("hbm", float(self.n * self.n * (128 + self.bins) * 2))
+        raise KeyError(kernel)
+
+
+class PairCondWorkload(Workload):
+    """The denoiser's PairwiseConditioning (token_z = rel = a_z = 128, 2 transitions of hidden 256) at N=768."""
+
+    def __init__(self, device, n: int = 768, seed: int = 0):
+        from .glue import PairwiseConditioning
+
+        self.n = n
+        self.name = f"pair_cond_n{n}"
+        self.metric = f"ms per pairwise conditioning at N={n} bf16"
+        torch.manual_seed(seed)
+        self.module = init_module(PairwiseConditioning(128, 128), seed).to(device)
+        g = torch.Generator().manual_seed(seed)
+        self.z_cpu = torch.randn(1, n, n, 128, generator=g).to(torch.bfloat16)
+        self.rel_cpu = torch.randn(1, n, n, 128, generator=g).to(torch.bfloat16)
+        self.z = self.z_cpu.to(device)
+        self.rel = self.rel_cpu.to(device)
+        self.config = {"workload": self.name, "N": n, "token_z": 128, "rel_pos": 128, "a_z": 128,
+                       "transitions": 2, "transition_hidden": 256}
+        self.flops = 2.0 * n * n * 256 * 128 + 2 * 2.0 * n * n * 128 * 768
+
+    def step(self) -> None:
+        self.module(self.z, self.rel)
+
+    def cpu_sample(self, oracle):
+        rows = 64
+        z = self.z_cpu[:, :rows].float()
+        rel = self.rel_cpu[:, :rows].float()
+        params = {k: v.detach().cpu() for k, v in self.module.state_dict().items()}
+        return ((lambda: oracle.pairwise_conditioning(z, rel, params)), rows / self.n,
+                f"oracle.pairwise_conditioning fp32 on {rows} of {self.n} rows")
+
+    def kernel_work(self, kernel: str) -> tuple[str, float]:
+        P = self.n * self.n
+        if kernel == "pair_cond_proj":
+            return ("hbm", float(P * (256 + 128) * 2))
+        if kernel == "transition_pair":
+            return ("mfma", 2.0 * P * 128 * 768)
+        if kernel == "fold_ln":  # the projection (128 rows of width 256) and fc1, fc2 of both transitions
+            return fold_kernel_work(kernel, 5, 4 * 256, rows256=128)
+        raise KeyError(kernel)
+
+
 def make(op: str, device, n: int | None = None) -> Workload:
     if op == "opm":
         return OpmWorkload(device, n or 512)
@@ -602,6 +740,14 @@ def make(op: str, device, n: int | None = None) -> Workload:
         return PwaWorkload(device, n or 512)
     if op == "swa":
         return SwaWorkload(device)
+    if op == "apb":
+        return ApbWorkload(device, n or 512)
+    if op == "apb_denoiser":
+        return ApbWorkload(device, n or 768, B=1, mult=8, initial_norm=False)
+    if op == "distogram":
+        return DistogramWorkload(device, n or 768)
+    if op == "pair_cond":
+        return PairCondWorkload(device, n or 768)
     if op == "pairmixer":
         return PairMixerWorkload(device, n or 768)
     if op == "pairmixer_msa":

@@ -100,7 +100,8 @@ int bioemu_triatt_fwd(const void* z, const uint8_t* mask, const float* norm_w, c
  * (D 64, hidden 256; biomoa/modules/pairmixer.py:631-634).  x, out: [P, D] bf16
  * rows (P = B*N*N pairs or B*S*N MSA entries), out may equal x when
  * residual != 0.  fc1_w, fc2_w: [hidden, D]; fc3_w: [D, hidden].  D must be 128
- * or 64 and hidden 4*D.  use_norm=0 skips the LayerNorm (norm_* unused).
+ * or 64 and hidden 4*D or 2*D (the denoiser's PairwiseConditioning transitions,
+ * diffusion.py:498-507).  use_norm=0 skips the LayerNorm (norm_* unused).
  * The workspace holds fc1/fc2 with the LayerNorm affine folded in (size from
  * bioemu_transition_pair_workspace_bytes, independent of P).
  */
@@ -180,6 +181,31 @@ int bioemu_swa_fwd(const void* s, const void* z, const uint8_t* mask, const floa
                    void* out, void* workspace, size_t workspace_bytes, int64_t B, int64_t mult,
                    int64_t NW, int64_t W, int64_t H, int64_t c_s, int64_t c_z, int64_t heads, int residual,
                    hipStream_t stream);
+
+/*
+ * Distogram head: out[b,i,j,:] = (z[b,i,j] + z[b,j,i]) w^T + b.
+ * Replaces DistogramModule.forward (src/bioemu2/biomoa/modules/embedders.py:191-206).
+ * z: [B, N, N, c_z] bf16; w: [num_bins, c_z] bf16; b: [num_bins] fp32;
+ * out: [B, N, N, num_bins] bf16 (exactly symmetric in i, j).
+ * Supported: c_z = 128, 1 <= num_bins <= 128.
+ */
+int bioemu_distogram_fwd(const void* z, const void* w, const float* b, void* out, int64_t B, int64_t N,
+                         int64_t c_z, int64_t num_bins, hipStream_t stream);
+
+/*
+ * PairwiseConditioning input projection: out = LN([z_trunk, rel]) w^T (LayerNorm
+ * over the token_z + c_rel concatenated channels, eps 1e-5, no Linear bias).
+ * Replaces the dim_pairwise_init_proj step of PairwiseConditioning.forward
+ * (src/bioemu2/biomoa/modules/diffusion.py:509-525); its transitions run
+ * bioemu_transition_pair_fwd (hidden = 2*a_z) with residual=1.
+ * z_trunk, rel: [P, 128] bf16 rows; ln_w, ln_b: [256] fp32; w: [a_z, 256] bf16;
+ * out: [P, a_z] bf16.  The workspace holds w with the LayerNorm folded in.
+ * Supported: token_z = c_rel = a_z = 128.
+ */
+size_t bioemu_pair_cond_workspace_bytes(int64_t token_z, int64_t c_rel, int64_t a_z);
+int bioemu_pair_cond_proj_fwd(const void* z_trunk, const void* rel, const float* ln_w, const float* ln_b,
+                              const void* w, void* out, void* workspace, size_t workspace_bytes, int64_t P,
+                              int64_t token_z, int64_t c_rel, int64_t a_z, hipStream_t stream);
 
 /*
  * Fused OuterProductMean.

@@ -30,6 +30,11 @@ How each function is pinned (see ``tests/test_oracle_*.py``):
                     own queries sit at offsets ctx..ctx+W-1), reduction to
                     ``attention_pair_bias`` per window when H == W, sequence-edge
                     keys masked, multiplicity == separate runs.
+* ``distogram``   — brute-force loops; the output is exactly symmetric in
+                    (i, j); a planted variant without the transpose fails it.
+* ``pairwise_conditioning`` — brute-force loops; the concatenation order
+                    (z_trunk first) is pinned by an asymmetric LayerNorm; zero
+                    transitions reduce it to LN + projection.
 * ``outer_product_mean`` — brute-force loops over S, masked rows contribute
                     exact zeros (test_outer_product_mean.py:286-310), the
                     divisor is the per-batch valid-row count (duplicating the
@@ -51,12 +56,14 @@ No function here is "parity unpinned".
 from .pairformer_ref import (  # noqa: F401
     attention_pair_bias,
     attention_pair_bias_sliding_window,
+    distogram,
     outer_product_mean,
     pair_mask_from_token_mask,
     pair_weighted_averaging,
     pairformer_block,
     pairmixer_layer,
     pairmixer_msa_layer,
+    pairwise_conditioning,
     sliding_window_keys,
     transition,
     triangle_attention,

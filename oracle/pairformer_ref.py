@@ -283,6 +283,32 @@ def attention_pair_bias_sliding_window(
 
 
 # ----------------------------------------------------------------------------
+# Pair glue either side of the trunk
+# ----------------------------------------------------------------------------
+def distogram(z: Tensor, params: dict) -> Tensor:
+    """DistogramModule.forward (biomoa/modules/embedders.py:191-206): Linear(z + z^T), with bias.
+
+    z [B,N,N,c_z] -> [B,N,N,num_bins] (float32); params ``distogram.{weight,bias}``.
+    """
+    z = _f32(z)
+    sym = z + z.transpose(1, 2)  # :205
+    return sym @ _p(params, "distogram.weight").T + _p(params, "distogram.bias")  # :206
+
+
+def pairwise_conditioning(z_trunk: Tensor, rel_pos: Tensor, params: dict, num_transitions: int = 2) -> Tensor:
+    """PairwiseConditioning.forward (biomoa/modules/diffusion.py:509-535).
+
+    cat([z_trunk, rel_pos], -1) -> LayerNorm -> LinearNoBias (``dim_pairwise_init_proj``,
+    :521-524), then ``z = transition(z) + z`` for each of ``transitions`` (:526-527).
+    """
+    x = torch.cat([_f32(z_trunk), _f32(rel_pos)], dim=-1)  # :521-523
+    x = _ln(x, params, "dim_pairwise_init_proj.0") @ _p(params, "dim_pairwise_init_proj.1.weight").T  # :524
+    for k in range(num_transitions):
+        x = transition(x, _sub(params, f"transitions.{k}")) + x  # :526-527
+    return x
+
+
+# ----------------------------------------------------------------------------
 # Outer product mean
 # ----------------------------------------------------------------------------
 def outer_product_mean(

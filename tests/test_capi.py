@@ -68,7 +68,8 @@ def test_host_only_queries():
     # folded fc1 | fc2 ([1024][128] bf16) and their bias pairs ([1024][2] bf16)
     assert lib.bioemu_transition_pair_workspace_bytes(128, 512) == 1024 * 128 * 2 + 1024 * 4
     assert lib.bioemu_transition_pair_workspace_bytes(64, 256) == 512 * 64 * 2 + 512 * 4
-    assert lib.bioemu_transition_pair_workspace_bytes(64, 128) == 0
+    assert lib.bioemu_transition_pair_workspace_bytes(64, 128) == 256 * 64 * 2 + 256 * 4
+    assert lib.bioemu_transition_pair_workspace_bytes(128, 384) == 0
     assert lib.bioemu_transition_pair_workspace_bytes(384, 1536) == 0
 
 

@@ -12,7 +12,8 @@ from __future__ import annotations
 import pytest
 import torch
 
-from bioemu2_amd.attention_pair_bias import AttentionPairBias
+from bioemu2_amd.attention_pair_bias import AttentionPairBias, AttentionPairBiasSlidingWindow
+from bioemu2_amd.glue import DistogramModule, PairwiseConditioning
 from bioemu2_amd.outer_product_mean import REGISTRY as OPM_REGISTRY
 from bioemu2_amd.outer_product_mean import OuterProductMeanHip
 from bioemu2_amd.pair_weighted_averaging import PairWeightedAveraging
@@ -68,6 +69,21 @@ def test_opm_transition_pwa_state_dicts():
     assert set(_shapes(Transition(C, 4 * C, use_norm=False))) == {"fc1.weight", "fc2.weight", "fc3.weight"}
     assert _shapes(PairWeightedAveraging(64, C, 32, 8)) == PWA
     assert "norm_z.bias" not in _shapes(PairWeightedAveraging(64, C, 32, 8, use_bias_in_layer_norm=False))
+
+
+def test_sliding_window_and_glue_state_dicts():
+    swa = _shapes(AttentionPairBiasSlidingWindow(128, 16, 4))
+    assert swa == {"norm_s.weight": (128,), "norm_s.bias": (128,), "proj_qkv.weight": (384, 128),
+                   "proj_q_bias": (128,), "proj_g.weight": (128, 128), "norm_z.weight": (16,),
+                   "proj_z.weight": (4, 16), "proj_o.weight": (128, 128)}
+    assert "norm_s.weight" not in _shapes(AttentionPairBiasSlidingWindow(128, 16, 4, initial_norm=False))
+    assert _shapes(DistogramModule(C, 64)) == {"distogram.weight": (64, C), "distogram.bias": (64,)}
+    tz = {k: v for k, v in TRANSITION_Z.items()}
+    tz.update({"fc1.weight": (2 * C, C), "fc2.weight": (2 * C, C), "fc3.weight": (C, 2 * C)})
+    want = {"dim_pairwise_init_proj.0.weight": (2 * C,), "dim_pairwise_init_proj.0.bias": (2 * C,),
+            "dim_pairwise_init_proj.1.weight": (C, 2 * C), **_prefixed("transitions.0", tz),
+            **_prefixed("transitions.1", tz)}
+    assert _shapes(PairwiseConditioning(C, C)) == want
 
 
 def test_pairmixer_layer_state_dict_and_variants():
