@@ -31,9 +31,12 @@ constexpr int kNtStage = 2 * kNtTileElems;     // A tile | B tile
 constexpr int kNtSmem = 2 * kNtStage * 2;      // bytes: double-buffered, 128 KB
 constexpr int kNtXcds = 8;
 
-// 16-byte chunk swizzle of a 128-byte tile row: conflict-free both for rows
-// read in natural order and in perm32 order (16 lanes -> 16 bank groups).
-__device__ __forceinline__ int nt_swz(int r) { return ((r >> 1) & 7) ^ (((r >> 4) & 1) << 2); }
+// 16-byte chunk swizzle of a 128-byte tile row: XOR with row bits 1..3.  On
+// gfx950 a ds_read_b128 whose 32 lanes read 32 rows of one 32-row block (in
+// natural or perm32 order, chunk c or c + 1 per half-wave) is free of bank
+// conflicts exactly when the swizzle takes row bit 1 and two of bits 2..4 and
+// not row bit 0 (measured with the SQ_LDS_BANK_CONFLICT counter).
+__device__ __forceinline__ int nt_swz(int r) { return (r >> 1) & 7; }
 __device__ __forceinline__ int nt_off(int r, int c) { return (r * 8 + (c ^ nt_swz(r))) * 8; }
 
 __device__ __forceinline__ void nt_copy16_to_lds(__amdgpu_buffer_rsrc_t r, const bf16* lds, unsigned voff,
@@ -77,7 +80,11 @@ __device__ __forceinline__ void gemm_nt_tile(const bf16* A, const bf16* B, int K
 
   const int nk = K / kNtBK;
   stage(0);
-  const int jrow = perm32(ln);
+  int offj[4], offi[2];
+#pragma unroll
+  for (int jb = 0; jb < 4; ++jb) offj[jb] = wj * 128 + jb * 32 + perm32(ln);
+#pragma unroll
+  for (int ib = 0; ib < 2; ++ib) offi[ib] = wi * 64 + ib * 32 + ln;
 #pragma unroll 1
   for (int kt = 0; kt < nk; ++kt) {
     __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's copies of k-tile kt landed
@@ -85,18 +92,25 @@ __device__ __forceinline__ void gemm_nt_tile(const bf16* A, const bf16* B, int K
     if (kt + 1 < nk) stage(kt + 1);
     const bf16* sa = smem + (kt & 1) * kNtStage;
     const bf16* sb = sa + kNtTileElems;
+    // All 24 operand fragments of the k-tile are requested before the first
+    // MFMA (the scheduler otherwise recycles a few registers and waits on
+    // every read); the 32 MFMAs then consume them as they land.
+    bf16x8 fj[4][4], fi[4][2];
 #pragma unroll
     for (int ks = 0; ks < kNtBK / 16; ++ks) {
-      bf16x8 fj[4], fi[2];
 #pragma unroll
-      for (int jb = 0; jb < 4; ++jb) fj[jb] = load8(sb + nt_off(wj * 128 + jb * 32 + jrow, 2 * ks + lh));
+      for (int jb = 0; jb < 4; ++jb) fj[ks][jb] = load8(sb + nt_off(offj[jb], 2 * ks + lh));
 #pragma unroll
-      for (int ib = 0; ib < 2; ++ib) fi[ib] = load8(sa + nt_off(wi * 64 + ib * 32 + ln, 2 * ks + lh));
+      for (int ib = 0; ib < 2; ++ib) fi[ks][ib] = load8(sa + nt_off(offi[ib], 2 * ks + lh));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int ks = 0; ks < kNtBK / 16; ++ks)
 #pragma unroll
       for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
-        for (int ib = 0; ib < 2; ++ib) acc[jb][ib] = mfma32(fj[jb], fi[ib], acc[jb][ib]);
-    }
+        for (int ib = 0; ib < 2; ++ib) acc[jb][ib] = mfma32(fj[ks][jb], fi[ks][ib], acc[jb][ib]);
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
