@@ -38,7 +38,8 @@ constexpr int kProjRows = 4 * C + H;       // q, k, v, g, bias rows of the packe
 constexpr int kProjRowsPad = 4 * C + 32;   // bias block padded to one 32-row MFMA block
 constexpr int kProjThreads = 1024;
 constexpr int kProjSmem = kProjRowsPad * kLdw * 2 + kProjRowsPad * 2 * 2;
-constexpr int kFlashThreads = 256;         // 4 waves x 32 queries = 128 queries per workgroup
+constexpr int kFlashThreads = 256;         // 4 waves x 64 queries (two 32-query tiles each)
+constexpr int kFlashQueries = 256;         // queries per workgroup
 
 // Softmax in base 2: q is stored pre-scaled by log2(e)/sqrt(d) and the bias by
 // log2(e), so QK^T + bias comes out of the MFMA directly in log2 units.
@@ -212,7 +213,7 @@ __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
   // (b, row i, query block) with the query block fastest; each XCD gets a
   // contiguous range, so the query blocks of one row (which read the same K
   // and V) share an L2.
-  const int nq = (Np + 127) / 128;
+  const int nq = (Np + kFlashQueries - 1) / kFlashQueries;
   const int total = gridDim.x;  // = padded item count, a multiple of 8
   const int per_xcd = total / 8;
   const int item = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
@@ -220,9 +221,13 @@ __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
   const int qb = item % nq;
   const int i = (item / nq) % N;
   const int b = item / (nq * N);
-  const int q0 = qb * 128 + wave * 32;
+  // This wave's two 32-query tiles: q0 + 32t (Np is a multiple of 64, so both
+  // exist or neither does).
+  const int q0 = qb * kFlashQueries + wave * 64;
   const bool active = q0 < Np;          // idle waves still stage tiles and meet every barrier
-  const int qrow = active ? q0 + n : 0;
+  int qrow[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) qrow[t] = active ? q0 + 32 * t + n : 0;
 
   const size_t frow = ((size_t)b * Np + i) * Np;
   const unsigned plane = (unsigned)Np * (unsigned)Np;
@@ -269,12 +274,11 @@ __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
     store8(smem + st * kStage + v_lds, rv);
   };
   // Bias slices in B-operand layout: lane (n, hh), half a, k-step s <-> keys
-  // k0 + 32a + 16s + 8hh + t.
-  // One wave's bias slice for a (head, 64-key) block is one contiguous 4 KB
-  // tile: instruction x reads 1 KB, lane l at byte 16 l.
+  // k0 + 32a + 16s + 8hh + t.  One tile's bias slice for a (head, 64-key)
+  // block is one contiguous 4 KB: instruction x reads 1 KB, lane l at byte 16 l.
   const unsigned bias_voff = (unsigned)lane * 16;
-  auto bload = [&](int hn, int kn, bf16x8 (&bb)[4]) {
-    const unsigned soff = (unsigned)bias_tile_index(hn, active ? q0 : 0, kn, Np) * 2;
+  auto bload = [&](int hn, int kn, int t, bf16x8 (&bb)[4]) {
+    const unsigned soff = (unsigned)bias_tile_index(hn, active ? q0 + 32 * t : 0, kn, Np) * 2;
 #pragma unroll
     for (int x = 0; x < 4; ++x) bb[x] = buffer_load8(brs, bias_voff + 1024 * x, soff);
   };
@@ -290,27 +294,36 @@ __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
   }
 
   const int nk = Np / 64;
-  bf16x8 bias[4];   // bias slice of the block being consumed, then of the next one
+  bf16x8 bias[2][4];   // per query tile: bias slice of the block being consumed, then of the next one
 
   gload(0, 0);
-  bload(0, 0, bias);
+  bload(0, 0, 0, bias[0]);
+  bload(0, 0, 1, bias[1]);
   lstore(0);
   __syncthreads();
   int st = 0;
 #pragma unroll 1
   for (int hd = 0; hd < H; ++hd) {
-    bf16x8 qf0 = zero8, qf1 = zero8;
-    if (!dead) {
-      qf0 = load8(qio + (unsigned)qrow * C + hd * DH + 8 * hh);
-      qf1 = load8(qio + (unsigned)qrow * C + hd * DH + 16 + 8 * hh);
+    bf16x8 qf[2][2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      qf[t][0] = zero8;
+      qf[t][1] = zero8;
+      if (!dead) {
+        qf[t][0] = load8(qio + (unsigned)qrow[t] * C + hd * DH + 8 * hh);
+        qf[t][1] = load8(qio + (unsigned)qrow[t] * C + hd * DH + 16 + 8 * hh);
+      }
     }
-    f32x16 o = zero16();
-    float m = -INFINITY, l = 0.f;
-    bool m_set = false;   // m is the (bf16-rounded) max of some unmasked logit
+    f32x16 o[2] = {zero16(), zero16()};
+    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
+    bool m_set[2] = {false, false};   // m is the (bf16-rounded) max of some unmasked logit
     // B operand of the rank-2 mask / shift product: k = 0 -> 1 (picks the key
     // column kadd), k = 1 -> -m (against a key column of ones).
-    bf16x8 qm = zero8;
-    if (hh == 0) qm[0] = f2bf(1.f);
+    bf16x8 qm[2] = {zero8, zero8};
+    if (hh == 0) {
+      qm[0][0] = f2bf(1.f);
+      qm[1][0] = f2bf(1.f);
+    }
     // One 64-key block: fetch the next K/V tile, consume the current one.
     auto block = [&](int kb) {
       const int k0 = kb * 64;
@@ -332,70 +345,81 @@ __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
           km0[1] = f2bf(1.f);
           km1[1] = f2bf(1.f);
         }
+        const bf16x8 ka0 = load8(ks + t_off(krow, hh)), ka1 = load8(ks + kTile + t_off(krow, hh));
+        const bf16x8 kb0 = load8(ks + t_off(krow, 2 + hh)), kb1 = load8(ks + kTile + t_off(krow, 2 + hh));
         // Logits minus the running max m, all on MFMA (no shift while m is
-        // not yet set).  The bias registers are refilled with the next
-        // block's slice as soon as the bias products have been issued.
-        bf16x8 qs = qm;
-        if (!m_set) qs[1] = f2bf(0.f);
-        f32x16 s0 = mfma32(load8(ks + t_off(krow, hh)), qf0, zero16());
-        f32x16 s1 = mfma32(load8(ks + kTile + t_off(krow, hh)), qf0, zero16());
-        s0 = mfma32(load8(ks + t_off(krow, 2 + hh)), qf1, s0);
-        s1 = mfma32(load8(ks + kTile + t_off(krow, 2 + hh)), qf1, s1);
-        s0 = mfma32(ident[0], bias[0], s0);
-        s1 = mfma32(ident[0], bias[2], s1);
-        s0 = mfma32(ident[1], bias[1], s0);
-        s1 = mfma32(ident[1], bias[3], s1);
-        s0 = mfma32(km0, qs, s0);
-        s1 = mfma32(km1, qs, s1);
-        bload(hn, kn, bias);
-        bf16x8 pa[2], pb[2];
-        float psum;
-        bool slow = !m_set;
-        if (!slow) {
+        // not yet set), for both query tiles before any softmax work so that
+        // one tile's exponentials overlap the other tile's matrix products.
+        f32x16 s[2][2];
 #pragma unroll
-          for (int u = 0; u < 16; ++u) {
-            pa[u >> 3][u & 7] = f2bf(fast_exp2(s0[u]));
-            pb[u >> 3][u & 7] = f2bf(fast_exp2(s1[u]));
-          }
-          psum = sum8_bf16(pa[1], sum8_bf16(pa[0], 0.f)) + sum8_bf16(pb[1], sum8_bf16(pb[0], 0.f));
-          // a sum above 2^16 may hold a weight above 2^16: move m (rare)
-          slow = __any(psum > kSlackSum);
-          if (slow) {
+        for (int t = 0; t < 2; ++t) {
+          bf16x8 qs = qm[t];
+          if (!m_set[t]) qs[1] = f2bf(0.f);
+          s[t][0] = mfma32(ka0, qf[t][0], zero16());
+          s[t][1] = mfma32(ka1, qf[t][0], zero16());
+          s[t][0] = mfma32(kb0, qf[t][1], s[t][0]);
+          s[t][1] = mfma32(kb1, qf[t][1], s[t][1]);
+          s[t][0] = mfma32(ident[0], bias[t][0], s[t][0]);
+          s[t][1] = mfma32(ident[0], bias[t][2], s[t][1]);
+          s[t][0] = mfma32(ident[1], bias[t][1], s[t][0]);
+          s[t][1] = mfma32(ident[1], bias[t][3], s[t][1]);
+          s[t][0] = mfma32(km0, qs, s[t][0]);
+          s[t][1] = mfma32(km1, qs, s[t][1]);
+          bload(hn, kn, t, bias[t]);
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          f32x16& s0 = s[t][0];
+          f32x16& s1 = s[t][1];
+          bf16x8 pa[2], pb[2];
+          float psum;
+          bool slow = !m_set[t];
+          if (!slow) {
 #pragma unroll
             for (int u = 0; u < 16; ++u) {
-              s0[u] += m;
-              s1[u] += m;
+              pa[u >> 3][u & 7] = f2bf(fast_exp2(s0[u]));
+              pb[u >> 3][u & 7] = f2bf(fast_exp2(s1[u]));
+            }
+            psum = sum8_bf16(pa[1], sum8_bf16(pa[0], 0.f)) + sum8_bf16(pb[1], sum8_bf16(pb[0], 0.f));
+            // a sum above 2^16 may hold a weight above 2^16: move m (rare)
+            slow = __any(psum > kSlackSum);
+            if (slow) {
+#pragma unroll
+              for (int u = 0; u < 16; ++u) {
+                s0[u] += m[t];
+                s1[u] += m[t];
+              }
             }
           }
-        }
-        if (slow) {
-          // s0, s1 hold the unshifted logits here
-          float bmax = fmaxf(s0[0], s1[0]);
+          if (slow) {
+            // s0, s1 hold the unshifted logits here
+            float bmax = fmaxf(s0[0], s1[0]);
 #pragma unroll
-          for (int u = 1; u < 16; ++u) bmax = __builtin_fmaxf(bmax, __builtin_fmaxf(s0[u], s1[u]));
-          bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
-          // the shift is kept bf16-representable: it enters the MFMA as -m
-          const float m_new = bf2f(f2bf(fmaxf(m, bmax)));
-          const float alpha = fast_exp2(m - m_new);
-          m = m_new;
-          l *= alpha;
+            for (int u = 1; u < 16; ++u) bmax = __builtin_fmaxf(bmax, __builtin_fmaxf(s0[u], s1[u]));
+            bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+            // the shift is kept bf16-representable: it enters the MFMA as -m
+            const float m_new = bf2f(f2bf(fmaxf(m[t], bmax)));
+            const float alpha = fast_exp2(m[t] - m_new);
+            m[t] = m_new;
+            l[t] *= alpha;
 #pragma unroll
-          for (int u = 0; u < 16; ++u) o[u] *= alpha;
-          // a block of masked keys only (logits ~ -1e30) does not set m
-          m_set = m_set || __all(m > -1e29f);
-          if (hh == 0) qm[1] = f2bf(-m);
+            for (int u = 0; u < 16; ++u) o[t][u] *= alpha;
+            // a block of masked keys only (logits ~ -1e30) does not set m
+            m_set[t] = m_set[t] || __all(m[t] > -1e29f);
+            if (hh == 0) qm[t][1] = f2bf(-m[t]);
 #pragma unroll
-          for (int u = 0; u < 16; ++u) {
-            pa[u >> 3][u & 7] = f2bf(fast_exp2(s0[u] - m));
-            pb[u >> 3][u & 7] = f2bf(fast_exp2(s1[u] - m));
+            for (int u = 0; u < 16; ++u) {
+              pa[u >> 3][u & 7] = f2bf(fast_exp2(s0[u] - m[t]));
+              pb[u >> 3][u & 7] = f2bf(fast_exp2(s1[u] - m[t]));
+            }
+            psum = sum8_bf16(pa[1], sum8_bf16(pa[0], 0.f)) + sum8_bf16(pb[1], sum8_bf16(pb[0], 0.f));
           }
-          psum = sum8_bf16(pa[1], sum8_bf16(pa[0], 0.f)) + sum8_bf16(pb[1], sum8_bf16(pb[0], 0.f));
+          l[t] += psum;
+          o[t] = mfma32(load8(vs + t_off(krow, 2 * hh)), pa[0], o[t]);
+          o[t] = mfma32(load8(vs + t_off(krow, 2 * hh + 1)), pa[1], o[t]);
+          o[t] = mfma32(load8(vs + kTile + t_off(krow, 2 * hh)), pb[0], o[t]);
+          o[t] = mfma32(load8(vs + kTile + t_off(krow, 2 * hh + 1)), pb[1], o[t]);
         }
-        l += psum;
-        o = mfma32(load8(vs + t_off(krow, 2 * hh)), pa[0], o);
-        o = mfma32(load8(vs + t_off(krow, 2 * hh + 1)), pa[1], o);
-        o = mfma32(load8(vs + kTile + t_off(krow, 2 * hh)), pb[0], o);
-        o = mfma32(load8(vs + kTile + t_off(krow, 2 * hh + 1)), pb[1], o);
       }
       lstore(st ^ 1);
       st ^= 1;
@@ -404,55 +428,61 @@ __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
 #pragma unroll 1
     for (int kb = 0; kb < nk; ++kb) block(kb);
     // head finished: o / l (bf16) parked in this head's q slot
-    const float inv = 1.0f / (l + __shfl_xor(l, 32));
-    float r[16];
 #pragma unroll
-    for (int u = 0; u < 16; ++u) r[u] = o[u] * inv;
-    if (active) store16(qio + (unsigned)qrow * C + hd * DH + 16 * hh, r);
+    for (int t = 0; t < 2; ++t) {
+      const float inv = 1.0f / (l[t] + __shfl_xor(l[t], 32));
+      float r[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) r[u] = o[t][u] * inv;
+      if (active) store16(qio + (unsigned)qrow[t] * C + hd * DH + 16 * hh, r);
+    }
   }
   if (!active) return;
 
-  // Gate: g * (o / l) per head, as the out-projection's B operand.
-  bf16x8 gob[2 * H];
-  {
-    const bf16* grow = buf.g + (frow + q0 + n) * C + 16 * hh;
-    const bf16* orow = qio + (unsigned)qrow * C + 16 * hh;
-#pragma unroll
-    for (int hd = 0; hd < H; ++hd) {
-      const bf16x8 g0 = load8(grow + hd * DH), g1 = load8(grow + hd * DH + 8);
-      const bf16x8 o0 = load8(orow + hd * DH), o1 = load8(orow + hd * DH + 8);
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        gob[2 * hd][u] = f2bf(bf2f(g0[u]) * bf2f(o0[u]));
-        gob[2 * hd + 1][u] = f2bf(bf2f(g1[u]) * bf2f(o1[u]));
-      }
-    }
-  }
-
-  // update^T = Wo (g*o)^T, residual add, store in z's frame.
-  const int q = q0 + n;
-  const bool store = q < N;
-  const size_t zpair = kStarting ? ((size_t)b * N + i) * N + q : ((size_t)b * N + q) * N + i;
 #pragma unroll 1
-  for (int cb = 0; cb < 4; ++cb) {
-    f32x16 acc = zero16();
-    const bf16* wrow = wo + (size_t)(cb * 32 + perm32(n)) * C + 16 * hh;
+  for (int t = 0; t < 2; ++t) {
+    // Gate: g * (o / l) per head, as the out-projection's B operand.
+    bf16x8 gob[2 * H];
+    {
+      const bf16* grow = buf.g + (frow + q0 + 32 * t + n) * C + 16 * hh;
+      const bf16* orow = qio + (unsigned)qrow[t] * C + 16 * hh;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) acc = mfma32(load8(wrow + 32 * (s >> 1) + 8 * (s & 1)), gob[s], acc);
-    if (store) {
-      const size_t off = zpair * C + cb * 32 + 16 * hh;
-      float v[16];
-#pragma unroll
-      for (int u = 0; u < 16; ++u) v[u] = acc[u];
-      if (residual) {
-        const bf16x8 r0 = load8(zres + off), r1 = load8(zres + off + 8);
+      for (int hd = 0; hd < H; ++hd) {
+        const bf16x8 g0 = load8(grow + hd * DH), g1 = load8(grow + hd * DH + 8);
+        const bf16x8 o0 = load8(orow + hd * DH), o1 = load8(orow + hd * DH + 8);
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-          v[u] += bf2f(r0[u]);
-          v[8 + u] += bf2f(r1[u]);
+          gob[2 * hd][u] = f2bf(bf2f(g0[u]) * bf2f(o0[u]));
+          gob[2 * hd + 1][u] = f2bf(bf2f(g1[u]) * bf2f(o1[u]));
         }
       }
-      store16(out + off, v);
+    }
+
+    // update^T = Wo (g*o)^T, residual add, store in z's frame.
+    const int q = q0 + 32 * t + n;
+    const bool store = q < N;
+    const size_t zpair = kStarting ? ((size_t)b * N + i) * N + q : ((size_t)b * N + q) * N + i;
+#pragma unroll 1
+    for (int cb = 0; cb < 4; ++cb) {
+      f32x16 acc = zero16();
+      const bf16* wrow = wo + (size_t)(cb * 32 + perm32(n)) * C + 16 * hh;
+#pragma unroll
+      for (int s2 = 0; s2 < 8; ++s2) acc = mfma32(load8(wrow + 32 * (s2 >> 1) + 8 * (s2 & 1)), gob[s2], acc);
+      if (store) {
+        const size_t off = zpair * C + cb * 32 + 16 * hh;
+        float v[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) v[u] = acc[u];
+        if (residual) {
+          const bf16x8 r0 = load8(zres + off), r1 = load8(zres + off + 8);
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            v[u] += bf2f(r0[u]);
+            v[8 + u] += bf2f(r1[u]);
+          }
+        }
+        store16(out + off, v);
+      }
     }
   }
 }
@@ -536,7 +566,7 @@ extern "C" int bioemu_triatt_fwd(const void* z, const uint8_t* mask, const float
   rc = check_launch("triatt_proj");
   if (rc) return rc;
 
-  const long long nitems = (long long)B * N * ((Np + 127) / 128);
+  const long long nitems = (long long)B * N * ((Np + kFlashQueries - 1) / kFlashQueries);
   const size_t flash_smem = (size_t)Np * 2;   // additive key mask row
   const void* kflash = starting ? reinterpret_cast<const void*>(triatt_flash_kernel<true>)
                                 : reinterpret_cast<const void*>(triatt_flash_kernel<false>);
