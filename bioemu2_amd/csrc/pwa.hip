@@ -16,9 +16,9 @@
 //   pwa_proj     : LN_m folded into Wm | Wg; per 32 tokens of one MSA row the
 //                  v block comes out channel-major (V^T, j contiguous: the
 //                  GEMM's B operand) and g pair-major.
-//   pwa_contract : the per-head GEMM (gemm_nt.h main loop); the epilogue
-//                  multiplies by g and writes g * o over g, pair-major.
-//   out          : token GEMM (token.hip) (g * o) Wo^T + m.
+//   pwa_fused    : per head the averaging GEMM on MFMA, then the gate and
+//                  the output projection from the accumulator registers;
+//                  writes (g * o) Wo^T (+ m) once, after the last head.
 // Padding: tokens are padded to Np = N rounded up to 256 (GEMM tiles), MSA rows
 // to S8 = S rounded up to 8; padded keys have weight exactly 0 and padded v
 // rows are exactly 0, so padding never changes a valid output bit.
@@ -217,46 +217,164 @@ __global__ __launch_bounds__(kPThreads) void pwa_proj_kernel(const bf16* __restr
 }
 
 // ---------------------------------------------------------------------------
-// Contraction: item = (b, head, 256 rows i, 256 columns n = (s, d)).
-//   O[i][n] = sum_j W[b][hd][i][j] V^T[b][hd][n][j]
-// Epilogue: g[b][s][i][hd*32 + d] *= O[i][s*32 + d]  (in place).
+// Contraction fused with the gate and the output projection.
+// Workgroup = (b, 4 MSA rows s0.., 128 query rows i0..); 8 waves, wave
+// (wi = wave & 1, ws = wave >> 1) owns rows i0 + 64 wi .. +63 of MSA row s0 + ws.
+// For each head h:
+//   O_h[i][(s, d)] = sum_j W[b][h][i][j] V^T[b][h][(s, d)][j]    (MFMA, K = Np,
+//     64-deep k-tiles copied straight into LDS, double-buffered across heads)
+//   out^T[o][i] += sum_d Wo[o][h*32 + d] (g[b][s][i][h*32 + d] O_h[i][(s, d)])
+// with the gated O_h taken from the accumulator registers as the B operand of
+// the projection (Wo in LDS).  After the 8 heads the 64 output channels (+ m)
+// are written once: neither g * o nor o ever goes to HBM.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kNtThreads) void pwa_contract_kernel(const bf16* __restrict__ w,
-                                                                  const bf16* __restrict__ vt, bf16* g, int B, int S8,
-                                                                  int Np) {
+constexpr int kFuThreads = 512;
+constexpr int kFuI = 128;                       // query rows per workgroup
+constexpr int kFuS = 4;                         // MSA rows per workgroup
+constexpr int kFuBK = 64;
+constexpr int kFuTile = kFuI * kFuBK;           // one operand tile: [128 rows][8 chunks of 8]
+constexpr int kFuStage = 2 * kFuTile;           // W tile | V^T tile
+constexpr int kLdwO = HC + 8;                   // Wo row stride in LDS
+constexpr int kFuSmem = 2 * kFuStage * 2 + CM * kLdwO * 2;
+
+__global__ __launch_bounds__(kFuThreads) void pwa_fused_kernel(const bf16* __restrict__ w,
+                                                               const bf16* __restrict__ vt,
+                                                               const bf16* __restrict__ g,
+                                                               const bf16* __restrict__ wo, const bf16* mres,
+                                                               bf16* out, int S, int S8, int N, int Np, int residual,
+                                                               int nitems) {
   extern __shared__ __attribute__((aligned(16))) char smem_raw[];
   bf16* smem = reinterpret_cast<bf16*>(smem_raw);
-  const int ncol = S8 * CH;
-  const int ti_n = Np / kNtTile, tj_n = ncol / kNtTile;
-  const int tiles = ti_n * tj_n;
-  const int item = nt_item(B * NH * tiles);
-  if (item < 0) return;
-  const int z = item / tiles, t = item % tiles;   // z = b * NH + hd
-  const int ti = t / tj_n, tj = t % tj_n;
-  const int b = z / NH, hd = z % NH;
+  bf16* wol = smem + 2 * kFuStage;
+  // XCD-aware: consecutive items (the i-tiles of one s-tile, which read the
+  // same V^T rows) land on one XCD.
+  const int per_xcd = gridDim.x / kNtXcds;
+  const int item = (blockIdx.x % kNtXcds) * per_xcd + blockIdx.x / kNtXcds;
+  if (item >= nitems) return;   // before any barrier: the whole workgroup leaves
+  const int nit = Np / kFuI, nst = S8 / kFuS;
+  const int it = item % nit, st = (item / nit) % nst, b = item / (nit * nst);
+  const int i0 = it * kFuI, s0 = st * kFuS;
 
-  f32x16 acc[4][2];
-  gemm_nt_tile(w + ((size_t)z * Np + (size_t)ti * kNtTile) * Np, vt + ((size_t)z * ncol + (size_t)tj * kNtTile) * Np,
-               Np, smem, acc);
-
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ln = lane & 31, lh = lane >> 5;
-  const int wi = wave & 3, wj = wave >> 2;
+  const int wi = wave & 1, ws = wave >> 1;
+
+  for (int q = tid; q < CM * (HC / 8); q += kFuThreads) {
+    const int r = q / (HC / 8), part = q % (HC / 8);
+    store8(wol + r * kLdwO + part * 8, load8(wo + (size_t)r * HC + part * 8));
+  }
+
+  // Each operand tile (128 rows x 128 B) is 16 copies of 1 KB; wave w moves
+  // copies w and w + 8 of both.  Copy j writes LDS chunk 64 j + lane.
+  unsigned voff[2];
 #pragma unroll
-  for (int ib = 0; ib < 2; ++ib) {
-    const int i = ti * kNtTile + wi * 64 + ib * 32 + ln;
+  for (int q = 0; q < 2; ++q) {
+    const int p = (wave + 8 * q) * 64 + lane, r = p >> 3, c = (p & 7) ^ nt_swz(p >> 3);
+    voff[q] = (unsigned)(r * Np + c * 8) * 2;
+  }
+  const unsigned tile_bytes = (unsigned)kFuI * Np * 2;
+  auto rsrcs = [&](int h, __amdgpu_buffer_rsrc_t& rw, __amdgpu_buffer_rsrc_t& rv) {
+    rw = buffer_rsrc(w + ((size_t)(b * NH + h) * Np + i0) * Np, tile_bytes);
+    rv = buffer_rsrc(vt + (((size_t)(b * NH + h) * S8 + s0) * CH) * Np, tile_bytes);
+  };
+  auto stage = [&](__amdgpu_buffer_rsrc_t rw, __amdgpu_buffer_rsrc_t rv, int kt, int buf) {
+    bf16* stg = smem + buf * kFuStage;
+    const unsigned soff = (unsigned)(kt * kFuBK) * 2;
 #pragma unroll
-    for (int jb = 0; jb < 4; ++jb) {
-      const int s = (tj * kNtTile + wj * 128 + jb * 32) / CH;
-      bf16* gp = g + (((size_t)b * S8 + s) * Np + i) * HC + hd * CH + 16 * lh;
+    for (int q = 0; q < 2; ++q) {
+      nt_copy16_to_lds(rw, stg + (wave + 8 * q) * 512, voff[q], soff);
+      nt_copy16_to_lds(rv, stg + kFuTile + (wave + 8 * q) * 512, voff[q], soff);
+    }
+  };
+
+  const int nk = Np / kFuBK;
+  const int jrow = ws * 32 + perm32(ln);
+  int offi[2];
+#pragma unroll
+  for (int ib = 0; ib < 2; ++ib) offi[ib] = wi * 64 + ib * 32 + ln;
+  const int s = s0 + ws;
+
+  f32x16 oacc[2][2];   // [ob][ib]: out^T rows ob*32.., columns i
+#pragma unroll
+  for (int ob = 0; ob < 2; ++ob)
+#pragma unroll
+    for (int ib = 0; ib < 2; ++ib) oacc[ob][ib] = zero16();
+
+  __amdgpu_buffer_rsrc_t rw, rv;
+  rsrcs(0, rw, rv);
+  stage(rw, rv, 0, 0);
+  int gk = 0;   // running k-tile index: LDS buffer gk & 1
+#pragma unroll 1
+  for (int h = 0; h < NH; ++h) {
+    f32x16 acc[2] = {zero16(), zero16()};
+#pragma unroll 1
+    for (int kt = 0; kt < nk; ++kt, ++gk) {
+      __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's copies of the k-tile landed
+      __syncthreads();                       // ... and everyone's; the other buffer is free again
+      if (kt + 1 < nk) {
+        stage(rw, rv, kt + 1, (gk + 1) & 1);
+      } else if (h + 1 < NH) {
+        rsrcs(h + 1, rw, rv);
+        stage(rw, rv, 0, (gk + 1) & 1);
+      }
+      const bf16* sa = smem + (gk & 1) * kFuStage;
+      const bf16* sb = sa + kFuTile;
+      bf16x8 fj[4], fi[4][2];
+#pragma unroll
+      for (int ks = 0; ks < kFuBK / 16; ++ks) {
+        fj[ks] = load8(sb + nt_off(jrow, 2 * ks + lh));
+#pragma unroll
+        for (int ib = 0; ib < 2; ++ib) fi[ks][ib] = load8(sa + nt_off(offi[ib], 2 * ks + lh));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int ks = 0; ks < kFuBK / 16; ++ks)
+#pragma unroll
+        for (int ib = 0; ib < 2; ++ib) acc[ib] = mfma32(fj[ks], fi[ks][ib], acc[ib]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // acc[ib] lane (ln, lh) register u <-> O_h[i = i0 + wi*64 + ib*32 + ln][(s, d = 16 lh + u)]
+#pragma unroll
+    for (int ib = 0; ib < 2; ++ib) {
+      const int i = i0 + offi[ib];
+      const bf16* gp = g + (((size_t)b * S8 + s) * Np + i) * HC + h * CH + 16 * lh;
       const bf16x8 g0 = load8(gp), g1 = load8(gp + 8);
-      float v[16];
+      bf16x8 go0, go1;
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        v[u] = acc[jb][ib][u] * bf2f(g0[u]);
-        v[8 + u] = acc[jb][ib][8 + u] * bf2f(g1[u]);
+        go0[u] = f2bf(acc[ib][u] * bf2f(g0[u]));
+        go1[u] = f2bf(acc[ib][8 + u] * bf2f(g1[u]));
       }
-      store16(gp, v);
+#pragma unroll
+      for (int ob = 0; ob < 2; ++ob) {
+        const bf16* wrow = wol + (ob * 32 + perm32(ln)) * kLdwO + h * CH + 16 * lh;
+        oacc[ob][ib] = mfma32(load8(wrow), go0, oacc[ob][ib]);
+        oacc[ob][ib] = mfma32(load8(wrow + 8), go1, oacc[ob][ib]);
+      }
+    }
+  }
+  // oacc[ob][ib] lane (ln, lh) register u <-> out channel ob*32 + 16 lh + u of (s, i0 + offi[ib])
+  if (s >= S) return;
+#pragma unroll
+  for (int ib = 0; ib < 2; ++ib) {
+    const int i = i0 + offi[ib];
+    if (i >= N) continue;
+#pragma unroll
+    for (int ob = 0; ob < 2; ++ob) {
+      const size_t off = (((size_t)b * S + s) * N + i) * CM + ob * 32 + 16 * lh;
+      float v[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) v[u] = oacc[ob][ib][u];
+      if (residual) {
+        const bf16x8 r0 = load8(mres + off), r1 = load8(mres + off + 8);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          v[u] += bf2f(r0[u]);
+          v[8 + u] += bf2f(r1[u]);
+        }
+      }
+      store16(out + off, v);
     }
   }
 }
@@ -344,8 +462,8 @@ extern "C" int bioemu_pwa_fwd(const void* m, const void* z, const uint8_t* mask,
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)wsmem) != hipSuccess ||
       hipFuncSetAttribute(reinterpret_cast<const void*>(pwa_proj_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                           kPSmem) != hipSuccess ||
-      hipFuncSetAttribute(reinterpret_cast<const void*>(pwa_contract_kernel),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, kNtSmem) != hipSuccess)
+      hipFuncSetAttribute(reinterpret_cast<const void*>(pwa_fused_kernel),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, kFuSmem) != hipSuccess)
     return set_error(BIOEMU_ERR_LAUNCH, "pwa: cannot set dynamic LDS size");
   {
     KernelTimerScope timed("pwa_weights", stream);
@@ -364,25 +482,13 @@ extern "C" int bioemu_pwa_fwd(const void* m, const void* z, const uint8_t* mask,
   rc = check_launch("pwa_proj");
   if (rc) return rc;
   {
-    const long long items = B * NH * (Np / kNtTile) * ((S8 * CH) / kNtTile);
+    const long long items = B * (S8 / kFuS) * (Np / kFuI);
     const long long grid = (items + kNtXcds - 1) / kNtXcds * kNtXcds;
     if (grid > 0x7fffffffLL) return set_error(BIOEMU_ERR_INVALID_ARG, "pwa: too many work items");
-    KernelTimerScope timed("pwa_contract", stream);
-    hipLaunchKernelGGL(pwa_contract_kernel, dim3((unsigned)grid), dim3(kNtThreads), kNtSmem, stream, wbuf, vt, gbuf,
-                       (int)B, S8, Np);
-  }
-  rc = check_launch("pwa_contract");
-  if (rc) return rc;
-  // out = (g * o) Wo^T (+ m): rows (b, s, i) of the padded g buffer, compact output.
-  const int epi = residual ? kEpiResidualId : kEpiStoreId;
-  if (S8 == S)
-    return token_gemm(epi, false, gbuf, w_o, nullptr, nullptr, m, out, B * S8 * Np, HC, CM, N, Np, N, stream,
-                      "pwa_out");
-  for (int64_t b = 0; b < B; ++b) {
-    rc = token_gemm(epi, false, gbuf + (size_t)b * S8 * Np * HC, w_o, nullptr, nullptr,
-                    static_cast<const bf16*>(m) + (size_t)b * S * N * CM, static_cast<bf16*>(out) + (size_t)b * S * N * CM,
-                    S * Np, HC, CM, N, Np, N, stream, "pwa_out");
-    if (rc) return rc;
+    KernelTimerScope timed("pwa_fused", stream);
+    hipLaunchKernelGGL(pwa_fused_kernel, dim3((unsigned)grid), dim3(kFuThreads), kFuSmem, stream, wbuf, vt, gbuf,
+                       static_cast<const bf16*>(w_o), static_cast<const bf16*>(m), static_cast<bf16*>(out), (int)S,
+                       S8, (int)N, Np, residual, (int)items);
   }
   return 0;
 }

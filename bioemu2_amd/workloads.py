@@ -371,18 +371,16 @@ class PwaWorkload(Workload):
     def kernel_work(self, kernel: str) -> tuple[str, float]:
         n, S = self.n, self.S
         npad = -(-n // 256) * 256
-        if kernel == "pwa_contract":
-            # sum_j w[h,i,j] v[s,j,h,:] over the valid keys, every head and MSA row
-            return ("mfma", 2.0 * 8 * n * n * S * 32)
+        if kernel == "pwa_fused":
+            # sum_j w[h,i,j] v[s,j,h,:] over the valid keys (every head and MSA row) and the
+            # output projection (g * o) Wo^T
+            return ("mfma", 2.0 * 8 * n * n * S * 32 + 2.0 * S * n * 256 * 64)
         if kernel == "pwa_weights":
             # reads z, writes the 8 weight rows (bf16)
             return ("hbm", float(n * n * 128 * 2 + 8 * n * npad * 2))
         if kernel == "pwa_proj":
             # reads m, writes v^T and g (256 channels each)
             return ("hbm", float(S * n * 64 * 2 + 2 * S * npad * 256 * 2))
-        if kernel == "pwa_out":
-            # reads g*o (256) and m, writes m
-            return ("hbm", float(S * n * (256 * 2 + 64 * 2 * 2)))
         if kernel == "fold_ln":  # w_z (8 rows), w_m and w_g (256 rows of width 64 each)
             return fold_kernel_work(kernel, 3, 8, 512)
         raise KeyError(kernel)
@@ -523,9 +521,7 @@ class PairMixerMsaWorkload(Workload):
             return ("hbm", float(self.s_valid * n * 64 * 2 + 2 * S * n * 32 * 2))
         if kernel == "opm_rows":
             return ("hbm", float(S * n))
-        if kernel == "pwa_contract":
-            return ("mfma", 2.0 * 8 * n * n * S * 32)
-        if kernel in ("pwa_weights", "pwa_proj", "pwa_out"):
+        if kernel in ("pwa_weights", "pwa_proj", "pwa_fused"):
             return PwaWorkload.kernel_work(self, kernel)
         if kernel == "transition_msa":
             return ("mfma", 2.0 * S * n * 64 * 12 * 64)
