@@ -69,3 +69,22 @@ def test_block_inplace_matches_out_of_place(gpu_device):
     s2, z2 = s.clone(), z.clone()
     blk.forward_(s2, z2, tok)
     assert torch.equal(s2, s_new) and torch.equal(z2, z_new)
+
+
+def test_block_config5_size_padding_invariant(gpu_device):
+    """Config 5 shape (N = 2048, 102 padded tokens): the valid region is bit-identical when every padded
+    token's s and every pair touching a padded token in z change, and all outputs are finite."""
+    blk = _block(gpu_device)
+    n, pad = 2048, 102
+    s, z, tok = _inputs(n, pad, gpu_device, seed=5)
+    s2, z2 = s.clone(), z.clone()
+    s2[:, n - pad:] = 7.0
+    z2[:, n - pad:] = -5.0
+    z2[:, :, n - pad:] = 3.0
+    with torch.no_grad():
+        blk.forward_(s, z, tok)
+        blk.forward_(s2, z2, tok)
+    v = n - pad
+    assert torch.isfinite(z[:, :v, :v].float()).all() and torch.isfinite(s[:, :v].float()).all()
+    assert torch.equal(z[:, :v, :v], z2[:, :v, :v])
+    assert torch.equal(s[:, :v], s2[:, :v])
