@@ -26,7 +26,8 @@ from pathlib import Path
 TRAFFIC_JSON = Path(__file__).resolve().parents[1] / "profiles" / "traffic.json"
 
 # Kernel-timer names whose kernel function is named differently.
-TIMER_TO_KERNEL = {"apb_pair_bias": "pair_bias", "token_layernorm": "token_ln"}
+TIMER_TO_KERNEL = {"apb_pair_bias": "pair_bias", "token_layernorm": "token_ln",
+                   "transition_pair": "transition_rows", "transition_msa": "transition_rows"}
 
 
 def short_name(mangled: str) -> str:
