@@ -37,16 +37,15 @@ __global__ __launch_bounds__(kBiasThreads) void pair_bias_kernel(const bf16* __r
   stage_weights(wl, wf, H, 32);
   stage_bias(cl, cf, H, 32);
   __syncthreads();
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int rho = lane & 31, h = lane >> 5;
   const int waves = blockDim.x >> 6;
-  const int tiles_per_row = Np / 32;
-  const long long ntiles = (long long)B * Np * tiles_per_row;
+  const unsigned tiles_per_row = Np / 32;
+  const unsigned ntiles = (unsigned)B * Np * tiles_per_row;
   const size_t plane = (size_t)Np * Np;
-  for (long long t = (long long)blockIdx.x * waves + wave; t < ntiles; t += (long long)gridDim.x * waves) {
-    const int kt = (int)(t % tiles_per_row);
-    const int i = (int)((t / tiles_per_row) % Np);
-    const int b = (int)(t / ((long long)tiles_per_row * Np));
+  for (unsigned t = blockIdx.x * waves + wave; t < ntiles; t += gridDim.x * waves) {
+    const TileIdx ti = split_tile(t, tiles_per_row, Np);
+    const int kt = ti.col, i = ti.row, b = ti.b;
     const int k0 = kt * 32;
     const int kk = k0 + perm32(rho);
     const bool valid = i < N && kk < N;
@@ -86,7 +85,7 @@ __global__ __launch_bounds__(256) void apb_flash_kernel(const bf16* __restrict__
   for (int t = threadIdx.x; t < Np; t += blockDim.x) mrow[t] = (t < N) ? (mask[(size_t)b * N + t] != 0) : 0;
   __syncthreads();
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int n = lane & 31, hh = lane >> 5;
   const int hd = blockIdx.y * 4 + wave;
   if (hd >= H) return;  // after the only barrier
@@ -253,6 +252,7 @@ extern "C" int bioemu_apb_fwd(const void* s, const void* z, const uint8_t* mask,
   (void)hipGetDevice(&dev);
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
   const long long ntiles = B * Np * (Np / 32);
+  if (ntiles >= kMaxTiles) return set_error(BIOEMU_ERR_INVALID_ARG, "apb: too many pair tiles");
   const unsigned grid1 = (unsigned)std::min<long long>(4LL * cus, (ntiles + 3) / 4);
   rc = launch_fold_ln(w_z, norm_z_w, norm_z_b, buf.wf, buf.cf, H, stream);
   if (rc) return rc;

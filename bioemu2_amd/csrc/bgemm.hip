@@ -29,7 +29,7 @@ __global__ __launch_bounds__(kNtThreads) void bgemm_nt_kernel(const bf16* __rest
   f32x16 acc[4][2];
   gemm_nt_tile(A + z * plane + (size_t)ti * kNtTile * n, B + z * plane + (size_t)tj * kNtTile * n, n, smem, acc);
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int ln = lane & 31, lh = lane >> 5;
   const int wi = wave & 3, wj = wave >> 2;
   bf16* Cb = C + z * plane + (size_t)(ti * kNtTile) * n + tj * kNtTile;

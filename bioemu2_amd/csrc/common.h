@@ -70,6 +70,23 @@ __device__ __forceinline__ bf16x4 pack4(float a, float b, float c, float d) {
 __device__ __forceinline__ bf16x8 load8(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
 __device__ __forceinline__ void store8(bf16* p, bf16x8 v) { *reinterpret_cast<bf16x8*>(p) = v; }
 
+// This thread's wave within the workgroup as a wave-uniform (scalar) value.
+// Everything derived from it (tile indices, base pointers, buffer resources)
+// then stays in scalar registers; derived from plain threadIdx.x the compiler
+// must treat it as per-lane, and every buffer load through a resource built
+// from it becomes a readfirstlane loop.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+
+// Flat tile index t = (b * rows + row) * cols + col -> (b, row, col) in 32-bit
+// arithmetic (launchers keep tile counts below 2^31).
+struct TileIdx {
+  int b, row, col;
+};
+__device__ __forceinline__ TileIdx split_tile(unsigned t, unsigned cols, unsigned rows) {
+  const unsigned r = t / cols, b = r / rows;
+  return {(int)b, (int)(r - b * rows), (int)(t - r * cols)};
+}
+
 // Buffer resource over [base, base + bytes) (raw buffer, 32-bit offsets).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, unsigned bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);

@@ -36,14 +36,13 @@ __global__ __launch_bounds__(kThreads) void distogram_kernel(const bf16* __restr
   bf16* wl = reinterpret_cast<bf16*>(smem);
   stage_weights(wl, wd, NB, NBp);
   __syncthreads();
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int n = lane & 31, hh = lane >> 5;
-  const int tiles = (N + 31) / 32;
-  const long long ntiles = (long long)B * N * tiles;
-  for (long long t = (long long)blockIdx.x * 4 + wave; t < ntiles; t += (long long)gridDim.x * 4) {
-    const int jt = (int)(t % tiles);
-    const int i = (int)((t / tiles) % N);
-    const int b = (int)(t / ((long long)tiles * N));
+  const unsigned tiles = (N + 31) / 32;
+  const unsigned ntiles = (unsigned)B * N * tiles;
+  for (unsigned t = blockIdx.x * 4 + wave; t < ntiles; t += gridDim.x * 4) {
+    const TileIdx ti = split_tile(t, tiles, N);
+    const int jt = ti.col, i = ti.row, b = ti.b;
     if (jt * 32 + 31 < i) continue;   // wave-uniform: every pair of the tile has j < i
     const int j = jt * 32 + n;
     const bool valid = j < N && j >= i;
@@ -104,7 +103,7 @@ __global__ __launch_bounds__(kThreads) void pair_cond_proj_kernel(const bf16* __
   }
   for (int q = threadIdx.x; q < 2 * kOut; q += kThreads) cl[q] = cf[q];
   __syncthreads();
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int n = lane & 31, hh = lane >> 5;
   const long long p = (long long)blockIdx.x * 128 + wave * 32 + n;
   const bool valid = p < P;
@@ -178,6 +177,7 @@ extern "C" int bioemu_distogram_fwd(const void* z, const void* w, const float* b
   (void)hipGetDevice(&dev);
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
   const long long ntiles = B * N * ((N + 31) / 32);
+  if (ntiles >= kMaxTiles) return set_error(BIOEMU_ERR_INVALID_ARG, "distogram: too many pair tiles");
   const unsigned grid = (unsigned)std::max<long long>(1, std::min<long long>(8LL * cus, (ntiles + 3) / 4));
   KernelTimerScope timed("distogram", stream);
   hipLaunchKernelGGL(distogram_kernel, dim3(grid), dim3(kThreads), smem, stream, static_cast<const bf16*>(z),

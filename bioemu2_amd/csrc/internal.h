@@ -32,6 +32,11 @@ class KernelTimerScope {
 
 inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 
+// Grid-stride pair-tile loops index their tiles in 32-bit unsigned arithmetic;
+// launchers reject a tile count of 2^31 or more (far beyond any pair tensor
+// that fits in device memory).
+constexpr int64_t kMaxTiles = int64_t(1) << 31;
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // Batched bf16 "NT" GEMM: C[z][i][j] = sum_k A[z][i][k] * B[z][j][k] for

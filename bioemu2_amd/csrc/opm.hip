@@ -96,15 +96,14 @@ __global__ __launch_bounds__(kProjThreads) void opm_proj_kernel(
     const int* __restrict__ count, const float* __restrict__ ln_w, const float* __restrict__ ln_b,
     const bf16* __restrict__ w_ab, bf16* __restrict__ aT, bf16* __restrict__ bT, int B, int S, int N, int Nt,
     int Sp) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int rho = lane & 31, h = lane >> 5;
   const int waves = blockDim.x >> 6;
-  const int rtiles = Sp / 32;
-  const long long ntiles = (long long)B * Nt * rtiles;
-  for (long long t = (long long)blockIdx.x * waves + wave; t < ntiles; t += (long long)gridDim.x * waves) {
-    const int rt = (int)(t % rtiles);
-    const int n = (int)((t / rtiles) % Nt);
-    const int b = (int)(t / ((long long)rtiles * Nt));
+  const unsigned rtiles = Sp / 32;
+  const unsigned ntiles = (unsigned)B * Nt * rtiles;
+  for (unsigned t = blockIdx.x * waves + wave; t < ntiles; t += gridDim.x * waves) {
+    const TileIdx ti = split_tile(t, rtiles, Nt);
+    const int rt = ti.col, n = ti.row, b = ti.b;
     const int r0 = rt * 32;
     const int nv = count[b];
     const int r = r0 + perm32(rho);
@@ -182,7 +181,7 @@ __global__ __launch_bounds__(kFusedThreads) void opm_fused_kernel(
   bf16* xb = reinterpret_cast<bf16*>(smem);
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63, wave = wave_id();
   const int n = lane & 31, h = lane >> 5;
   const int b = blockIdx.z;
   const int i0 = blockIdx.y * TI, j0 = blockIdx.x * TJ;
@@ -343,6 +342,7 @@ extern "C" int bioemu_opm_fwd(const void* m, const uint8_t* mask, int mean_rows,
   OpmLayout L;
   opm_layout(B, S, N, &L, static_cast<char*>(workspace));
   const int64_t Nt = round_up(N, 8), Sp = round_up(S, 32);
+  if (B * Nt * (Sp / 32) >= kMaxTiles) return set_error(BIOEMU_ERR_INVALID_ARG, "opm: too many row tiles");
 
   {
     KernelTimerScope timed("opm_rows", stream);

@@ -56,7 +56,7 @@ __global__ __launch_bounds__(kWThreads) void pwa_weights_kernel(const bf16* __re
   bf16* cl = wl + 32 * kLdw;
   float* lg = reinterpret_cast<float*>(smem + kWFixedSmem);
   const int b = blockIdx.x / Np, i = blockIdx.x % Np;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   if (i >= N) {   // padded query rows: zero weights (their outputs are dropped)
     for (int q = tid; q < NH * Np; q += kWThreads)
       w[((size_t)(b * NH + q / Np) * Np + i) * Np + q % Np] = f2bf(0.f);
@@ -149,15 +149,14 @@ __global__ __launch_bounds__(kPThreads) void pwa_proj_kernel(const bf16* __restr
   stage_bias(cl, cf, kPRows, kPRows);
   __syncthreads();
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int rho = lane & 31, h = lane >> 5;
   const int waves = kPThreads / 64;
-  const int tpr = Np / 32;
-  const long long ntiles = (long long)B * S8 * tpr;
-  for (long long t = (long long)blockIdx.x * waves + wave; t < ntiles; t += (long long)gridDim.x * waves) {
-    const int it = (int)(t % tpr);
-    const int s = (int)((t / tpr) % S8);
-    const int b = (int)(t / ((long long)tpr * S8));
+  const unsigned tpr = Np / 32;
+  const unsigned ntiles = (unsigned)B * S8 * tpr;
+  for (unsigned t = blockIdx.x * waves + wave; t < ntiles; t += gridDim.x * waves) {
+    const TileIdx ti = split_tile(t, tpr, S8);
+    const int it = ti.col, s = ti.row, b = ti.b;
     const int i0 = it * 32;
     const int ii = i0 + perm32(rho);
     const bool valid = ii < N && s < S;
@@ -447,6 +446,7 @@ extern "C" int bioemu_pwa_fwd(const void* m, const void* z, const uint8_t* mask,
   bf16* wmf = reinterpret_cast<bf16*>(ws + L.wmf);
   bf16* cmf = reinterpret_cast<bf16*>(ws + L.cmf);
 
+  if (B * L.S8 * (L.Np / 32) >= kMaxTiles) return set_error(BIOEMU_ERR_INVALID_ARG, "pwa: too many row tiles");
   int rc = launch_fold_ln(w_z, norm_z_w, norm_z_b, wzf, czf, NH, stream);
   if (!rc) rc = launch_fold_ln(w_m, norm_m_w, norm_m_b, wmf, cmf, HC, stream, CM);
   if (!rc) rc = launch_fold_ln(w_g, norm_m_w, norm_m_b, wmf + HC * CM, cmf + HC * 2, HC, stream, CM);

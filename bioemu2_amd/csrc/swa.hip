@@ -104,7 +104,7 @@ __global__ __launch_bounds__(256) void swa_attn_kernel(const bf16* __restrict__ 
                                                        const bf16* __restrict__ bias,
                                                        const uint8_t* __restrict__ mask, bf16* __restrict__ go,
                                                        int NW, int HK, int heads, int mult) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int n = lane & 31, hh = lane >> 5;
   const int hd = blockIdx.y * 4 + wave;
   if (hd >= heads) return;

@@ -23,6 +23,7 @@
 //                  fused in the epilogue and the residual added in place.
 // H = 4 heads of d = 32 over c = 128 channels.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 #include "internal.h"
@@ -36,7 +37,7 @@ constexpr int H = 4;
 constexpr int DH = 32;
 constexpr int kProjRows = 4 * C + H;       // q, k, v, g, bias rows of the packed weight
 constexpr int kProjRowsPad = 4 * C + 32;   // bias block padded to one 32-row MFMA block
-constexpr int kProjThreads = 1024;
+constexpr int kProjThreads = 512;
 constexpr int kProjSmem = kProjRowsPad * kLdw * 2 + kProjRowsPad * 2 * 2;
 constexpr int kFlashThreads = 256;         // 4 waves x 64 queries (two 32-query tiles each)
 constexpr int kFlashQueries = 256;         // queries per workgroup
@@ -80,46 +81,93 @@ __global__ __launch_bounds__(kProjThreads) void triatt_proj_kernel(
   stage_bias(cl, cf, kProjRows, kProjRowsPad);
   __syncthreads();
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int rho = lane & 31, h = lane >> 5;
   const int waves = blockDim.x >> 6;
-  const int tiles_per_row = Np / 32;
-  const long long ntiles = (long long)B * Np * tiles_per_row;
+  const unsigned tiles_per_row = Np / 32;
+  const unsigned ntiles = (unsigned)B * Np * tiles_per_row;
   const size_t plane = (size_t)Np * Np;
 
-  for (long long t = (long long)blockIdx.x * waves + wave; t < ntiles; t += (long long)gridDim.x * waves) {
-    const int kt = (int)(t % tiles_per_row);
-    const int i = (int)((t / tiles_per_row) % Np);
-    const int b = (int)(t / ((long long)tiles_per_row * Np));
-    const int k0 = kt * 32;
-
-    // This lane's pair slot: frame (i, k0 + perm32(rho)).
-    const int kk = k0 + perm32(rho);
+  // Software pipeline over this wave's tiles: tile t + stride's inputs (this
+  // lane's half of the z row of its pair slot and the mask byte of frame
+  // column k0 + rho) are loaded before tile t's stores are issued and
+  // normalised after them.  Vector-memory counters retire in issue order, so
+  // waiting for those loads then does not wait for the stores to be written,
+  // and, being in straight-line code, the wait the compiler places is exact.
+  const unsigned stride = gridDim.x * waves;
+  bf16x8 raw[8];
+  uint8_t mraw = 0;
+  bool mok = false;
+  auto fetch = [&](unsigned tt) {
+    const TileIdx ti = split_tile(tt, tiles_per_row, Np);
+    const int i = ti.row, b = ti.b, k0 = ti.col * 32;
+    const int kc = k0 + rho, kk = k0 + perm32(rho);
+    mok = i < N && kc < N;
+    const size_t mp = !mok ? 0 : kStarting ? ((size_t)b * N + i) * N + kc : ((size_t)b * N + kc) * N + i;
+    mraw = mask[mp];
+    // Unconditional loads (pair 0 for slots outside the sequence, zeroed in
+    // prepare): a zero-filled destination would be written before the loads,
+    // and overwriting registers that earlier stores read makes the compiler
+    // wait for those stores.
     const bool valid = i < N && kk < N;
     const size_t zpair = !valid ? 0 : kStarting ? ((size_t)b * N + i) * N + kk : ((size_t)b * N + kk) * N + i;
+    const bf16* row = z + zpair * C + 64 * h;
+#pragma unroll
+    for (int s8 = 0; s8 < 8; ++s8) raw[s8] = load8(row + 8 * s8);
+  };
+  // Tile operands: normalised row x, the bias k-step operand xb and the mask byte.
+  bf16x8 x[8], xb;
+  uint8_t mv;
+  auto prepare = [&](unsigned tt) {
+    const TileIdx ti = split_tile(tt, tiles_per_row, Np);
+    const int kk = ti.col * 32 + perm32(rho);
+    const bool valid = ti.row < N && kk < N;
     float v[64];
-    bf16x8 x[8];
-    load_half_row_f32(z + zpair * C, h, valid, v);
+#pragma unroll
+    for (int s8 = 0; s8 < 8; ++s8) unpack8(valid ? raw[s8] : bf16x8{}, v + 8 * s8);
     normalize_half_row(v, valid, x);
-    const bf16x8 xb = bias_step_x(valid, h);
+    xb = bias_step_x(valid, h);
+    mv = mok && mraw != 0;
+  };
+
+  unsigned t = blockIdx.x * waves + wave;
+  if (t < ntiles) {
+    fetch(t);
+    prepare(t);
+  }
+  for (; t < ntiles; t += stride) {
+    const unsigned tn = t + stride;
+    if (tn < ntiles) fetch(tn);
+    const TileIdx ti = split_tile(t, tiles_per_row, Np);
+    const int kt = ti.col, i = ti.row, b = ti.b;
+    const int k0 = kt * 32;
+    // This lane's pair slot: frame (i, k0 + perm32(rho)).
+    const int kk = k0 + perm32(rho);
 
     const size_t frow = ((size_t)b * Np + i) * Np;  // frame row base (pairs)
     // q (times the softmax scale), k, g: pair-major; lane holds pair slot
     // perm32(rho), channels blk*32 + 16h .. +15.
     const size_t pm_off = (frow + kk) * C;
+    // One loop per output (the output kind is a compile-time constant, so the
+    // per-element select and the store address need no branches).
+    auto project = [&](auto which_tag) {
+      constexpr int which = decltype(which_tag)::value;   // 0: q, 1: k, 2: g
 #pragma unroll 1
-    for (int blk = 0; blk < 12; ++blk) {
-      const int which = blk >> 2, cb = blk & 3;   // 0: q, 1: k, 2: g
-      const int row0 = (which == 2 ? 3 * C : which * C) + cb * 32;
-      const f32x16 a = proj_block_pm_f(x, xb, wl, cl, row0, rho, h);
-      float vq[16];
+      for (int cb = 0; cb < 4; ++cb) {
+        const int row0 = (which == 2 ? 3 * C : which * C) + cb * 32;
+        const f32x16 a = proj_block_pm_f(x, xb, wl, cl, row0, rho, h);
+        float vq[16];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) vq[u] = which == 0 ? a[u] * kQScale : which == 1 ? a[u] : sigmoidf_fast(a[u]);
-      // k is head-major per frame row: [H][Np][DH]
-      bf16* base = which == 0 ? buf.q : which == 1 ? buf.k : buf.g;
-      const size_t dst = which == 1 ? (frow * H + (size_t)cb * Np + kk) * DH + 16 * h : pm_off + cb * 32 + 16 * h;
-      store16(base + dst, vq);
-    }
+        for (int u = 0; u < 16; ++u) vq[u] = which == 0 ? a[u] * kQScale : which == 1 ? a[u] : sigmoidf_fast(a[u]);
+        // k is head-major per frame row: [H][Np][DH]
+        bf16* base = which == 0 ? buf.q : which == 1 ? buf.k : buf.g;
+        const size_t dst = which == 1 ? (frow * H + (size_t)cb * Np + kk) * DH + 16 * h : pm_off + cb * 32 + 16 * h;
+        store16(base + dst, vq);
+      }
+    };
+    project(std::integral_constant<int, 0>{});
+    project(std::integral_constant<int, 1>{});
+    project(std::integral_constant<int, 2>{});
     // v^T: channel-major.  Lane (n, h) holds channel cb*32+n, pairs k0+16h..+15.
 #pragma unroll 1
     for (int cb = 0; cb < 4; ++cb) {
@@ -147,15 +195,8 @@ __global__ __launch_bounds__(kProjThreads) void triatt_proj_kernel(
         store8(dst + 32 * 8, hi);
       }
     }
-    if (h == 0) {
-      const int kc = k0 + rho;
-      uint8_t mv = 0;
-      if (i < N && kc < N) {
-        const size_t mp = kStarting ? ((size_t)b * N + i) * N + kc : ((size_t)b * N + kc) * N + i;
-        mv = mask[mp] != 0;
-      }
-      buf.mask[frow + kc] = mv;
-    }
+    if (h == 0) buf.mask[frow + k0 + rho] = mv;
+    if (tn < ntiles) prepare(tn);
   }
 }
 
@@ -541,6 +582,7 @@ extern "C" int bioemu_triatt_fwd(const void* z, const uint8_t* mask, const float
   p += round_up(pairs, 256);
   bf16* wf = reinterpret_cast<bf16*>(p);
   bf16* cf = reinterpret_cast<bf16*>(p + round_up((size_t)kProjRows * C * 2, 256));
+  if (B * Np * (Np / 32) >= kMaxTiles) return set_error(BIOEMU_ERR_INVALID_ARG, "triatt: too many pair tiles");
   int rc = launch_fold_ln(w_proj, norm_w, norm_b, wf, cf, kProjRows, stream);
   if (rc) return rc;
 

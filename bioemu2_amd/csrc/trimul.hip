@@ -37,7 +37,7 @@ constexpr int D = 128;               // pair channels (c_z)
 // ---------------------------------------------------------------------------
 constexpr int kInThreads = 512;
 constexpr int kInRows = 4 * D;                 // p_in (2D rows) then g_in (2D rows)
-constexpr int kInSmem = kInRows * kLdw * 2;
+constexpr int kInSmem = kInRows * kLdw * 2 + 2 * D * 4;   // weights, then LayerNorm gamma | beta (fp32)
 
 template <bool kOutgoing>
 __global__ __launch_bounds__(kInThreads) void trimul_proj_in_kernel(
@@ -46,33 +46,67 @@ __global__ __launch_bounds__(kInThreads) void trimul_proj_in_kernel(
     bf16* __restrict__ ab, int B, int N, int Np) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   bf16* wl = reinterpret_cast<bf16*>(smem);
+  // gamma and beta live in LDS: read from global memory inside the tile loop
+  // they would be vector-memory loads issued after the previous tile's
+  // stores, and waiting for them would wait for those stores.
+  float* lnl = reinterpret_cast<float*>(smem + kInRows * kLdw * 2);
   stage_weights(wl, p_w, 2 * D, 2 * D);
   stage_weights(wl + 2 * D * kLdw, g_w, 2 * D, 2 * D);
+  for (int q = threadIdx.x; q < D; q += blockDim.x) {
+    lnl[q] = ln_w[q];
+    lnl[D + q] = ln_b[q];
+  }
   __syncthreads();
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int rho = lane & 31, h = lane >> 5;
   const int waves = blockDim.x >> 6;
-  const int tiles_per_row = Np / 32;
-  const long long ntiles = (long long)B * Np * tiles_per_row;
+  const unsigned tiles_per_row = Np / 32;
+  const unsigned ntiles = (unsigned)B * Np * tiles_per_row;
   const size_t plane = (size_t)Np * Np;
 
-  for (long long t = (long long)blockIdx.x * waves + wave; t < ntiles; t += (long long)gridDim.x * waves) {
-    const int kt = (int)(t % tiles_per_row);
-    const int i = (int)((t / tiles_per_row) % Np);
-    const int b = (int)(t / ((long long)tiles_per_row * Np));
-    const int k0 = kt * 32;
-    const int kk = k0 + perm32(rho);
-    const bool inb = i < N && kk < N;
-    const size_t pair = kOutgoing ? ((size_t)b * N + i) * N + kk : ((size_t)b * N + kk) * N + i;
-    const bool keep = inb && mask[inb ? pair : 0] != 0;
-    bf16x8 raw[8], xf[8];
-    load_half_row(x + (inb ? pair : 0) * D, h, inb, raw);
-    layernorm_half_row(raw, ln_w, ln_b, h, 1e-5f, xf);
-    if (!keep) {
+  // Software pipeline over this wave's tiles: tile t + stride's inputs (this
+  // lane's half of its pair's x row and the pair's mask byte) are loaded
+  // before tile t's stores are issued and normalised after them.  Vector-
+  // memory counters retire in issue order, so waiting for those loads then
+  // does not wait for the stores to be written.  The loads are unconditional
+  // (pair 0 for slots outside the sequence; such slots are zeroed through
+  // `keep`) so that nothing touches their destination registers, or reads the
+  // mask byte, before the wait.
+  const unsigned stride = gridDim.x * waves;
+  bf16x8 raw[8];
+  uint8_t mraw = 0;
+  bool inb_next = false;
+  auto fetch = [&](unsigned tt) {
+    const TileIdx ti = split_tile(tt, tiles_per_row, Np);
+    const int i = ti.row, b = ti.b, kk = ti.col * 32 + perm32(rho);
+    inb_next = i < N && kk < N;
+    const size_t pair = !inb_next ? 0 : kOutgoing ? ((size_t)b * N + i) * N + kk : ((size_t)b * N + kk) * N + i;
+    mraw = mask[pair];
+    const bf16* row = x + pair * D + 64 * h;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) raw[s] = load8(row + 8 * s);
+  };
+  bf16x8 xf[8];
+  auto prepare = [&]() {
+    layernorm_half_row(raw, lnl, lnl + D, h, 1e-5f, xf);
+    if (!(inb_next && mraw != 0)) {
 #pragma unroll
       for (int s = 0; s < 8; ++s) xf[s] = bf16x8{};
     }
+  };
+
+  unsigned t = blockIdx.x * waves + wave;
+  if (t < ntiles) {
+    fetch(t);
+    prepare();
+  }
+  for (; t < ntiles; t += stride) {
+    const unsigned tn = t + stride;
+    if (tn < ntiles) fetch(tn);
+    const TileIdx ti = split_tile(t, tiles_per_row, Np);
+    const int kt = ti.col, i = ti.row, b = ti.b;
+    const int k0 = kt * 32;
 #pragma unroll 1
     for (int blk = 0; blk < 8; ++blk) {   // a: blk 0..3, b: blk 4..7 (32 channels each)
       const f32x16 pa = proj_block_cm(xf, wl, blk * 32, rho, h);
@@ -83,6 +117,7 @@ __global__ __launch_bounds__(kInThreads) void trimul_proj_in_kernel(
       const int which = blk >> 2, ch = (blk & 3) * 32 + rho;
       store16(ab + ((size_t)(which * B + b) * D + ch) * plane + (size_t)i * Np + k0 + 16 * h, v);
     }
+    if (tn < ntiles) prepare();
   }
 }
 
@@ -143,85 +178,127 @@ __device__ __forceinline__ void normalize_half_row(const float* v, bf16x8 out[8]
 // ---------------------------------------------------------------------------
 // Stage 3: out = p_out(LN_out(o)) * sigmoid(g_out(LN_in(x)))  (+ x).
 //
-// Tile = (b, row i, 32 columns j).  o is channel-major (the contraction's
-// output planes), so each lane gathers its pair's 64-channel half with 2-byte
-// buffer loads (the 32 lanes of a half read 64 contiguous bytes per channel;
-// one VGPR address, the channel offset in an SGPR); x is pair-major.  Both
-// LayerNorms run affine-free in registers against the folded weights, which
-// sit in LDS with the folded biases.  The result comes out pair-major (16
-// consecutive channels per lane) and is stored with the residual add fused.
+// Tile = (b, row i, 32 columns j), one per wave at a time.  o is channel-major
+// (the contraction's output planes): a tile's o block, 128 channels x one
+// 64-byte run, is read with 16-byte loads and turned pair-major through a
+// per-wave LDS buffer; x is pair-major.  Both LayerNorms run affine-free in
+// registers against the folded weights, which sit in LDS with the folded
+// biases.
+//
+// Output lanes: LDS row 32 cb + m of each folded weight half holds weight row
+// 64 (m >> 4) + 16 cb + (m & 15), so that lane (rho, h) of output block cb
+// holds channels 64 h + 16 cb + u (u < 16) of its pair: over the four blocks a
+// lane produces exactly the 64 channels of its own x half-row, and the
+// residual comes from registers.
+//
+// Software pipeline: tile t + stride's x and o loads are issued before tile
+// t's stores and consumed after them; vector-memory counters retire in issue
+// order, so waiting for the loads does not wait for the stores.
 // ---------------------------------------------------------------------------
 constexpr int kOutThreads = 512;
-constexpr int kOutSmem = 2 * D * kLdw * 2 + 2 * D * 4;
+constexpr int kOutWaves = kOutThreads / 64;
+constexpr int kOutTile = D * 32 + 32;   // per-wave o buffer, bf16 elements
+constexpr int kOutSmem = 2 * D * kLdw * 2 + 2 * D * 4 + kOutWaves * kOutTile * 2;
 
-__global__ __launch_bounds__(kOutThreads) __attribute__((amdgpu_waves_per_eu(4, 8))) void trimul_out_kernel(
+// Element offset of (channel c, column j) in a wave's o buffer: 64-byte
+// channel rows, the upper 64 channels 64 bytes further on, so that the two
+// half-waves' reads (channels c and c + 64 of the same 32 columns) use
+// different LDS banks; the 16-byte writes of one instruction cover 1 KB
+// contiguously.
+__device__ __forceinline__ int obuf_off(int c, int j) { return c * 32 + j + ((c >> 6) << 5); }
+
+// Lanes of pair slots past N store into `discard` (a dead workspace region,
+// 16 KB) instead of skipping the store: a conditional store would hide the
+// number of stores from the compiler's wait counting, which would then wait
+// for the stores before the next tile's data.
+__global__ __launch_bounds__(kOutThreads) void trimul_out_kernel(
     const bf16* __restrict__ o, const bf16* x, const bf16* __restrict__ wfold, const float* __restrict__ cfold,
-    bf16* out, int B, int N, int Np, int residual) {
+    bf16* out, bf16* __restrict__ discard, int B, int N, int Np, int residual) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   bf16* wl = reinterpret_cast<bf16*>(smem);
   float* cl = reinterpret_cast<float*>(smem + 2 * D * kLdw * 2);
-  stage_weights(wl, wfold, 2 * D, 2 * D);
+  bf16* obuf = reinterpret_cast<bf16*>(smem + 2 * D * kLdw * 2 + 2 * D * 4);
+  for (int q = threadIdx.x; q < 2 * D * (D / 8); q += blockDim.x) {
+    const int r = q >> 4, part = q & 15;
+    const int half = r / D, cb = (r % D) >> 5, m = r & 31;
+    const int src = half * D + 64 * (m >> 4) + 16 * cb + (m & 15);
+    store8(wl + r * kLdw + part * 8, load8(wfold + (size_t)src * D + part * 8));
+  }
   for (int t = threadIdx.x; t < 2 * D; t += blockDim.x) cl[t] = cfold[t];
   __syncthreads();
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int rho = lane & 31, h = lane >> 5;
-  const int waves = blockDim.x >> 6;
-  const int tiles_per_row = (N + 31) / 32;
-  const long long ntiles = (long long)B * N * tiles_per_row;
+  const unsigned tiles_per_row = (N + 31) / 32;
+  const unsigned ntiles = (unsigned)B * N * tiles_per_row;
+  const unsigned stride = gridDim.x * kOutWaves;
   const size_t plane = (size_t)Np * Np;
+  bf16* ob = obuf + wave * kOutTile;
 
-  for (long long t = (long long)blockIdx.x * waves + wave; t < ntiles; t += (long long)gridDim.x * waves) {
-    const int jt = (int)(t % tiles_per_row);
-    const int i = (int)((t / tiles_per_row) % N);
-    const int b = (int)(t / ((long long)tiles_per_row * N));
-    const int jj = jt * 32 + perm32(rho);
-    const bool valid = jj < N;
-    const size_t pair = ((size_t)b * N + i) * N + (valid ? jj : 0);
-
-    float v[64];
-    bf16x8 xf[8], of[8];
-    {
-      bf16x8 xraw[8];
-      load_half_row(x + pair * D, h, valid, xraw);
+  // Next tile's raw inputs: this lane's x half-row, and o channels
+  // 16 q + (lane >> 2), columns j0 + 8 (lane & 3) .. + 7.  Columns of the last
+  // tile of a row may reach past N but stay below Np (o is Np wide).
+  bf16x8 xraw[8], oraw[8];
+  auto fetch = [&](unsigned tt) {
+    const TileIdx ti = split_tile(tt, tiles_per_row, N);
+    const int i = ti.row, b = ti.b, j0 = ti.col * 32;
+    const int jj = j0 + perm32(rho);
+    const size_t pair = ((size_t)b * N + i) * N + (jj < N ? jj : 0);
+    const bf16* xr = x + pair * D + 64 * h;
 #pragma unroll
-      for (int s = 0; s < 8; ++s) unpack8(xraw[s], v + 8 * s);
+    for (int s = 0; s < 8; ++s) xraw[s] = load8(xr + 8 * s);
+    const bf16* orow = o + ((size_t)b * D + (lane >> 2)) * plane + (size_t)i * Np + j0 + 8 * (lane & 3);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) oraw[q] = load8(orow + (size_t)(16 * q) * plane);
+  };
+  // Current tile's operands: normalised o and x rows and the raw x half-row.
+  bf16x8 of[8], xf[8], xres[8];
+  auto prepare = [&]() {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) store8(ob + obuf_off(16 * q + (lane >> 2), 8 * (lane & 3)), oraw[q]);
+    float v[64];
+    const int p = perm32(rho);
+#pragma unroll
+    for (int c = 0; c < 64; ++c) v[c] = bf2f(ob[obuf_off(64 * h + c, p)]);
+    normalize_half_row(v, of);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      unpack8(xraw[s], v + 8 * s);
+      xres[s] = xraw[s];
     }
     normalize_half_row(v, xf);
-    {
-      const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<bf16*>(o + (size_t)b * D * plane), (short)0, (int)(D * plane * 2), 0x00020000);
-      const unsigned voff = (unsigned)((64 * h * plane + (size_t)i * Np + jj) * 2);
-#pragma unroll
-      for (int c = 0; c < 64; ++c) {
-        const unsigned short r =
-            (unsigned short)__builtin_amdgcn_raw_buffer_load_b16(rsrc, voff, (unsigned)(c * plane * 2), 0);
-        v[c] = __uint_as_float((unsigned)r << 16);
-      }
-    }
-    normalize_half_row(v, of);
+  };
 
-#pragma unroll 1
+  unsigned t = blockIdx.x * kOutWaves + wave;
+  if (t < ntiles) {
+    fetch(t);
+    prepare();
+  }
+  for (; t < ntiles; t += stride) {
+    const unsigned tn = t + stride;
+    if (tn < ntiles) fetch(tn);
+    const TileIdx ti = split_tile(t, tiles_per_row, N);
+    const int jj = ti.col * 32 + perm32(rho);
+    const bool valid = jj < N;
+    const size_t pair = ((size_t)ti.b * N + ti.row) * N + (valid ? jj : 0);
+#pragma unroll
     for (int cb = 0; cb < 4; ++cb) {
       const f32x16 pa = proj_block_pm(of, wl, cb * 32, rho, h);
       const f32x16 ga = proj_block_pm(xf, wl, D + cb * 32, rho, h);
-      if (valid) {
-        const int e0 = cb * 32 + 16 * h;
-        const size_t off = pair * D + e0;
-        float r[16];
+      const int e0 = 64 * h + 16 * cb;
+      float r[16];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) r[u] = (pa[u] + cl[e0 + u]) * sigmoidf_fast(ga[u] + cl[D + e0 + u]);
-        if (residual) {
-          const bf16x8 r0 = load8(x + off), r1 = load8(x + off + 8);
+      for (int u = 0; u < 16; ++u) r[u] = (pa[u] + cl[e0 + u]) * sigmoidf_fast(ga[u] + cl[D + e0 + u]);
+      if (residual) {
 #pragma unroll
-          for (int u = 0; u < 8; ++u) {
-            r[u] += bf2f(r0[u]);
-            r[8 + u] += bf2f(r1[u]);
-          }
+        for (int u = 0; u < 8; ++u) {
+          r[u] += bf2f(xres[2 * cb][u]);
+          r[8 + u] += bf2f(xres[2 * cb + 1][u]);
         }
-        store16(out + off, r);
       }
+      store16(valid ? out + pair * D + e0 : discard + lane * D + e0, r);
     }
+    if (tn < ntiles) prepare();
   }
 }
 
@@ -279,6 +356,7 @@ extern "C" int bioemu_trimul_fwd(const void* x, const uint8_t* mask, const float
                           hipFuncAttributeMaxDynamicSharedMemorySize, kOutSmem) != hipSuccess)
     return set_error(BIOEMU_ERR_LAUNCH, "trimul: cannot set dynamic LDS size");
   const long long waves_in = (long long)B * Np * (Np / 32);
+  if (waves_in >= kMaxTiles) return set_error(BIOEMU_ERR_INVALID_ARG, "trimul: too many pair tiles");
   const unsigned grid1 = (unsigned)std::min<long long>(cus, (waves_in + 7) / 8);
   {
     KernelTimerScope timed("trimul_proj_in", stream);
@@ -304,10 +382,12 @@ extern "C" int bioemu_trimul_fwd(const void* x, const uint8_t* mask, const float
   if (rc) return rc;
 
   const long long waves_out = (long long)B * N * ((N + 31) / 32);
-  const unsigned grid3 = (unsigned)std::min<long long>(2LL * cus, (waves_out + 7) / 8);
+  const unsigned grid3 = (unsigned)std::min<long long>(cus, (waves_out + kOutWaves - 1) / kOutWaves);
   KernelTimerScope timed("trimul_out", stream);
+  // The a/b planes are dead once the contraction has run: their first 16 KB
+  // take the discarded stores of pair slots past N.
   hipLaunchKernelGGL(trimul_out_kernel, dim3(grid3), dim3(kOutThreads), kOutSmem, stream, ob,
-                     static_cast<const bf16*>(x), wfold, cfold, static_cast<bf16*>(out), (int)B, (int)N, (int)Np,
+                     static_cast<const bf16*>(x), wfold, cfold, static_cast<bf16*>(out), ab, (int)B, (int)N, (int)Np,
                      residual);
   return check_launch("trimul_out");
 }
