@@ -154,64 +154,83 @@ __global__ __launch_bounds__(kPThreads) void pwa_proj_kernel(const bf16* __restr
   const int waves = kPThreads / 64;
   const unsigned tpr = Np / 32;
   const unsigned ntiles = (unsigned)B * S8 * tpr;
-  for (unsigned t = blockIdx.x * waves + wave; t < ntiles; t += gridDim.x * waves) {
+  // Software pipeline over this wave's tiles: tile t + stride's m half-rows
+  // are loaded before tile t's stores and normalised after them (vector-
+  // memory counters retire in issue order, so that wait does not wait for
+  // the stores).  The loads are unconditional (row 0 for slots outside the
+  // sequence, zeroed when normalised).
+  const unsigned stride = gridDim.x * waves;
+  bf16x8 raw[4];
+  auto fetch = [&](unsigned tt) {
+    const TileIdx ti = split_tile(tt, tpr, S8);
+    const int ii = ti.col * 32 + perm32(rho);
+    const bool valid = ii < N && ti.row < S;
+    const bf16* row = m + (((size_t)ti.b * S + (valid ? ti.row : 0)) * N + (valid ? ii : 0)) * CM + 32 * h;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) raw[q] = load8(row + 8 * q);
+  };
+  bf16x8 x[4], xb;
+  auto prepare = [&](unsigned tt) {
+    const TileIdx ti = split_tile(tt, tpr, S8);
+    const int ii = ti.col * 32 + perm32(rho);
+    const bool valid = ii < N && ti.row < S;
+    float v[32];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) unpack8(valid ? raw[q] : bf16x8{}, v + 8 * q);
+    float sum = 0.f;
+#pragma unroll
+    for (int c = 0; c < 32; ++c) sum += v[c];
+    sum += __shfl_xor(sum, 32);
+    const float mean = sum * (1.0f / CM);
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < 32; ++c) {
+      const float d = v[c] - mean;
+      ss += d * d;
+    }
+    ss += __shfl_xor(ss, 32);
+    const float rstd = valid ? rsqrtf(ss * (1.0f / CM) + 1e-5f) : 0.f;
+#pragma unroll
+    for (int c = 0; c < 32; ++c) x[c >> 3][c & 7] = f2bf((v[c] - mean) * rstd);
+    xb = bias_step_x(valid, h);
+  };
+
+  unsigned t = blockIdx.x * waves + wave;
+  if (t < ntiles) {
+    fetch(t);
+    prepare(t);
+  }
+  for (; t < ntiles; t += stride) {
+    const unsigned tn = t + stride;
+    if (tn < ntiles) fetch(tn);
     const TileIdx ti = split_tile(t, tpr, S8);
     const int it = ti.col, s = ti.row, b = ti.b;
     const int i0 = it * 32;
     const int ii = i0 + perm32(rho);
-    const bool valid = ii < N && s < S;
-    bf16x8 x[4];
-    float v[32];
-    {
-      const bf16* row = m + (((size_t)b * S + (valid ? s : 0)) * N + (valid ? ii : 0)) * CM + 32 * h;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        bf16x8 raw;
-        if (valid) {
-          raw = load8(row + 8 * q);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) raw[e] = f2bf(0.f);
-        }
-        unpack8(raw, v + 8 * q);
-      }
-    }
-    {
-      float sum = 0.f;
-#pragma unroll
-      for (int c = 0; c < 32; ++c) sum += v[c];
-      sum += __shfl_xor(sum, 32);
-      const float mean = sum * (1.0f / CM);
-      float ss = 0.f;
-#pragma unroll
-      for (int c = 0; c < 32; ++c) {
-        const float d = v[c] - mean;
-        ss += d * d;
-      }
-      ss += __shfl_xor(ss, 32);
-      const float rstd = valid ? rsqrtf(ss * (1.0f / CM) + 1e-5f) : 0.f;
-#pragma unroll
-      for (int c = 0; c < 32; ++c) x[c >> 3][c & 7] = f2bf((v[c] - mean) * rstd);
-    }
-    const bf16x8 xb = bias_step_x(valid, h);
     // v^T: D lane (n = channel within head cb, h) holds tokens i0 + 16h + u.
-#pragma unroll 1
+    // (Both output loops are unrolled, one block per scheduling region, so
+    // that the compiler sees every store when it places the wait for the
+    // next tile's loads.)
+#pragma unroll
     for (int cb = 0; cb < NH; ++cb) {
       const f32x16 a = proj64_cm(x, xb, wl, cl, cb * 32, rho, h);
       float r[16];
 #pragma unroll
       for (int u = 0; u < 16; ++u) r[u] = a[u];
       store16(vt + ((((size_t)b * NH + cb) * S8 + s) * CH + rho) * Np + i0 + 16 * h, r);
+      __builtin_amdgcn_sched_barrier(0);
     }
     // g: D lane (n = token slot perm32(n), h) holds channels cb*32 + 16h + u.
-#pragma unroll 1
+#pragma unroll
     for (int cb = 0; cb < NH; ++cb) {
       const f32x16 a = proj64_pm(x, xb, wl, cl, HC + cb * 32, rho, h);
       float r[16];
 #pragma unroll
       for (int u = 0; u < 16; ++u) r[u] = sigmoidf_fast(a[u]);
       store16(g + (((size_t)b * S8 + s) * Np + ii) * HC + cb * 32 + 16 * h, r);
+      __builtin_amdgcn_sched_barrier(0);
     }
+    if (tn < ntiles) prepare(tn);
   }
 }
 
