@@ -18,7 +18,7 @@
 //   triatt_proj  : LN + all five projections (q, k, v, g, bias) on MFMA with
 //                  weights staged once per workgroup in LDS; writes the frame-
 //                  ordered operands of the attention and a frame-ordered mask.
-//   triatt_flash : per (b, row i, 32 queries) online-softmax attention over
+//   triatt_flash : per (b, row i, 256 queries) online-softmax attention over
 //                  all keys, 4 heads, with the gate and the output projection
 //                  fused in the epilogue and the residual added in place.
 // H = 4 heads of d = 32 over c = 128 channels.
@@ -201,8 +201,9 @@ __global__ __launch_bounds__(kProjThreads) void triatt_proj_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Flash attention kernel.  Workgroup = (b, frame row i, 128 queries);
-// wave w owns queries q0 = 128*blockIdx.x + 32w.
+// Flash attention kernel.  Workgroup = (b, frame row i, 256 queries); wave w
+// owns the two 32-query tiles q0 and q0 + 32, q0 = 256 qb + 64 w, which share
+// every K / V fragment the wave reads from LDS.
 //
 // At head dim 32 the attention is bound by vector-ALU and issue work, not by
 // the matrix cores, so everything that can ride on an MFMA does:
@@ -214,8 +215,9 @@ __global__ __launch_bounds__(kProjThreads) void triatt_proj_kernel(
 // A masked key's logit is -1e30 + (q.k + bias) = -1e30 exactly in fp32, so a
 // fully masked row gets equal logits (uniform weights, the reference's
 // masked_fill(-1e6) result) and a partially masked row gets exact zeros.
-// The running max is only moved (and o, l rescaled) when some row's block
-// max exceeds it by more than 2^8, so most blocks skip the rescale.
+// The running max m is set from the first block with an unmasked key and then
+// only moved (o and l rescaled) when a block's weight sum exceeds 2^16 (a
+// weight above 2^16 may be present), so most blocks skip the max search.
 //
 // Loops: heads outermost (one head's accumulator live; a finished head leaves
 // o/l as 8 packed-bf16 registers), then 64-key blocks.  A block is two
