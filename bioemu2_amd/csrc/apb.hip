@@ -43,22 +43,55 @@ __global__ __launch_bounds__(kBiasThreads) void pair_bias_kernel(const bf16* __r
   const unsigned tiles_per_row = Np / 32;
   const unsigned ntiles = (unsigned)B * Np * tiles_per_row;
   const size_t plane = (size_t)Np * Np;
-  for (unsigned t = blockIdx.x * waves + wave; t < ntiles; t += gridDim.x * waves) {
-    const TileIdx ti = split_tile(t, tiles_per_row, Np);
-    const int kt = ti.col, i = ti.row, b = ti.b;
-    const int k0 = kt * 32;
-    const int kk = k0 + perm32(rho);
-    const bool valid = i < N && kk < N;
-    float v[64];
-    bf16x8 x[8];
-    load_half_row_f32(z + (((size_t)b * N + (valid ? i : 0)) * N + (valid ? kk : 0)) * CZ, h, valid, v);
-    normalize_half_row(v, valid, x);
-    const f32x16 acc = proj_block_cm_f(x, bias_step_x(valid, h), wl, cl, 0, rho, h);
-    if (rho < H) {
-      float o[16];
+  // Software pipeline over this wave's tiles: iteration t issues tile
+  // t + stride's z loads, projects tile t, normalises tile t + stride and only
+  // then stores tile t's bias, so the wait for the loads (vector-memory
+  // counters retire in issue order) covers only stores issued a whole tile
+  // earlier.  The loads are unconditional (pair 0 for slots outside the
+  // sequence, zeroed when normalised).
+  const unsigned stride = gridDim.x * waves;
+  bf16x8 raw[8];
+  auto fetch = [&](unsigned tt) {
+    const TileIdx ti = split_tile(tt, tiles_per_row, Np);
+    const int kk = ti.col * 32 + perm32(rho);
+    const bool valid = ti.row < N && kk < N;
+    const bf16* row = z + (((size_t)ti.b * N + (valid ? ti.row : 0)) * N + (valid ? kk : 0)) * CZ + 64 * h;
 #pragma unroll
-      for (int u = 0; u < 16; ++u) o[u] = acc[u];
-      store16(bias + ((size_t)b * H + rho) * plane + (size_t)i * Np + k0 + 16 * h, o);
+    for (int s8 = 0; s8 < 8; ++s8) raw[s8] = load8(row + 8 * s8);
+  };
+  bf16x8 x[8], xb;
+  auto prepare = [&](unsigned tt) {
+    const TileIdx ti = split_tile(tt, tiles_per_row, Np);
+    const int kk = ti.col * 32 + perm32(rho);
+    const bool valid = ti.row < N && kk < N;
+    float v[64];
+#pragma unroll
+    for (int s8 = 0; s8 < 8; ++s8) unpack8(valid ? raw[s8] : bf16x8{}, v + 8 * s8);
+    normalize_half_row(v, valid, x);
+    xb = bias_step_x(valid, h);
+  };
+
+  unsigned t = blockIdx.x * waves + wave;
+  if (t < ntiles) {
+    fetch(t);
+    prepare(t);
+  }
+  for (; t < ntiles; t += stride) {
+    const unsigned tn = t + stride;
+    if (tn < ntiles) fetch(tn);
+    const TileIdx ti = split_tile(t, tiles_per_row, Np);
+    const f32x16 acc = proj_block_cm_f(x, xb, wl, cl, 0, rho, h);
+    bf16x8 o[2];   // tile t's bias, packed while tile t + stride is normalised
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      o[0][u] = f2bf(acc[u]);
+      o[1][u] = f2bf(acc[8 + u]);
+    }
+    if (tn < ntiles) prepare(tn);
+    if (rho < H) {
+      bf16* dst = bias + ((size_t)ti.b * H + rho) * plane + (size_t)ti.row * Np + ti.col * 32 + 16 * h;
+      store8(dst, o[0]);
+      store8(dst + 8, o[1]);
     }
   }
 }

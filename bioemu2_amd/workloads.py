@@ -600,7 +600,7 @@ class ApbWorkload(Workload):
         from .attention_pair_bias import AttentionPairBias
 
         self.n, self.B, self.mult = n, B, mult
-        self.name = f"apb_b{B}_m{mult}_n{n}"
+        self.name = f"apb_b{B}_m{mult}_n{n}" + ("" if initial_norm else "_nonorm")
         self.metric = f"ms per pair-bias attention at B={B}, M={mult}, N={n} bf16"
         torch.manual_seed(seed)
         self.module = init_module(AttentionPairBias(384, 128, 16, initial_norm=initial_norm), seed).to(device)
@@ -738,6 +738,8 @@ def make(op: str, device, n: int | None = None) -> Workload:
         return SwaWorkload(device)
     if op == "apb":
         return ApbWorkload(device, n or 512)
+    if op == "apb_nonorm":   # config 2 in the denoiser's setting (initial_norm=False)
+        return ApbWorkload(device, n or 512, initial_norm=False)
     if op == "apb_denoiser":
         return ApbWorkload(device, n or 768, B=1, mult=8, initial_norm=False)
     if op == "distogram":
