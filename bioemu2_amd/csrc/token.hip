@@ -78,23 +78,36 @@ __global__ __launch_bounds__(256) void token_ln_kernel(const bf16* __restrict__ 
 }
 
 // ---------------------------------------------------------------------------
-// out = epilogue(A[M][K] * W[Nout][K]^T).  One wave per 32x32 block.
+// out = epilogue(A[M][K] * W[Nout][K]^T) on 32x32 output blocks, 4 waves per
+// workgroup.  The token GEMMs are skinny (a few hundred rows), so for K >= 256
+// the k reduction of a block is split over the workgroup's 4 waves (wave w
+// takes the 16-deep steps k = 16 w, 16 (w + 4), ...): 4x the workgroups in
+// flight and a quarter of each wave's chain of dependent loads; wave 0 adds
+// the other waves' partial sums in a fixed order (deterministic) and runs the
+// epilogue.  For smaller K each wave owns a block of its own.
 // Row-major (kTrans = false): D = W A^T, lane (n, hh) holds row n and columns
 // 16hh..16hh+15 of the block.  Transposed (kTrans = true): D = A W^T with A
 // rows permuted, lane (n, hh) holds column n and rows 16hh..16hh+15.
 // ---------------------------------------------------------------------------
+constexpr int kSplitK = 4;        // most waves per workgroup
+constexpr int kSplitMinK = 256;   // smaller K: one wave, no reduction
+
 template <int kEpi, bool kTrans>
-__global__ __launch_bounds__(256) void token_gemm_kernel(const bf16* __restrict__ A, const bf16* __restrict__ W,
-                                                         const bf16* __restrict__ W2,
-                                                         const float* __restrict__ col_bias, const bf16* res,
-                                                         bf16* out, int M, int K, int Nout, int N, int Np,
-                                                         int out_rows) {
-  const int lane = threadIdx.x & 63;
-  const int wid = blockIdx.x * 4 + (threadIdx.x >> 6);
+__global__ __launch_bounds__(64 * kSplitK) void token_gemm_kernel(const bf16* __restrict__ A,
+                                                                  const bf16* __restrict__ W,
+                                                                  const bf16* __restrict__ W2,
+                                                                  const float* __restrict__ col_bias,
+                                                                  const bf16* res, bf16* out, int M, int K, int Nout,
+                                                                  int N, int Np, int out_rows) {
+  constexpr int kAccs = kEpi == kEpiSwiGLU ? 2 : 1;
+  __shared__ float part[kSplitK - 1][kAccs][16][64];   // partial sums of waves 1..3, lane-contiguous
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int splits = K >= kSplitMinK ? kSplitK : 1;   // waves per block (uniform)
+  const int kw = wave % splits;                        // this wave's share of the k steps
+  const int blk = blockIdx.x * (kSplitK / splits) + wave / splits;
   const int nb = Nout / 32;
-  const int mb = (M + 31) / 32;
-  if (wid >= mb * nb) return;
-  const int row0 = (wid / nb) * 32, col0 = (wid % nb) * 32;
+  if (blk >= ((M + 31) / 32) * nb) return;   // only when splits == 1: no barrier follows
+  const int row0 = (blk / nb) * 32, col0 = (blk % nb) * 32;
   const int n = lane & 31, hh = lane >> 5;
 
   f32x16 acc = zero16(), acc2 = zero16();
@@ -103,7 +116,7 @@ __global__ __launch_bounds__(256) void token_gemm_kernel(const bf16* __restrict_
     const bf16* wr2 = (kEpi == kEpiSwiGLU) ? W2 + (size_t)(col0 + perm32(n)) * K + 8 * hh : nullptr;
     const int ra = min(row0 + n, M - 1);
     const bf16* ar = A + (size_t)ra * K + 8 * hh;
-    for (int k = 0; k < K; k += 16) {
+    for (int k = 16 * kw; k < K; k += 16 * splits) {
       const bf16x8 af = load8(ar + k);
       acc = mfma32(load8(wr + k), af, acc);
       if (kEpi == kEpiSwiGLU) acc2 = mfma32(load8(wr2 + k), af, acc2);
@@ -112,7 +125,24 @@ __global__ __launch_bounds__(256) void token_gemm_kernel(const bf16* __restrict_
     const int ra = min(row0 + perm32(n), M - 1);
     const bf16* ar = A + (size_t)ra * K + 8 * hh;
     const bf16* wr = W + (size_t)(col0 + n) * K + 8 * hh;
-    for (int k = 0; k < K; k += 16) acc = mfma32(load8(ar + k), load8(wr + k), acc);
+    for (int k = 16 * kw; k < K; k += 16 * splits) acc = mfma32(load8(ar + k), load8(wr + k), acc);
+  }
+  if (splits > 1) {   // workgroup-uniform
+    if (wave > 0) {
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        part[wave - 1][0][u][lane] = acc[u];
+        if (kEpi == kEpiSwiGLU) part[wave - 1][kAccs - 1][u][lane] = acc2[u];
+      }
+    }
+    __syncthreads();
+    if (wave > 0) return;   // after the only barrier
+    for (int q = 0; q < splits - 1; ++q)
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        acc[u] += part[q][0][u][lane];
+        if (kEpi == kEpiSwiGLU) acc2[u] += part[q][kAccs - 1][u][lane];
+      }
   }
 
   float v[16];
@@ -157,9 +187,11 @@ template <int kEpi, bool kTrans>
 int launch_gemm(const void* A, const void* W, const void* W2, const float* col_bias, const void* res, void* out,
                 int64_t M, int64_t K, int64_t Nout, int64_t N, int64_t Np, int64_t out_rows, hipStream_t stream,
                 const char* name) {
-  const int64_t waves = ((M + 31) / 32) * (Nout / 32);
+  const int64_t blocks = ((M + 31) / 32) * (Nout / 32);
+  const int64_t per_wg = K >= kSplitMinK ? 1 : kSplitK;   // blocks per workgroup
   KernelTimerScope timed(name, stream);
-  hipLaunchKernelGGL((token_gemm_kernel<kEpi, kTrans>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream,
+  hipLaunchKernelGGL((token_gemm_kernel<kEpi, kTrans>), dim3((unsigned)((blocks + per_wg - 1) / per_wg)),
+                     dim3(64 * kSplitK), 0, stream,
                      static_cast<const bf16*>(A), static_cast<const bf16*>(W), static_cast<const bf16*>(W2),
                      col_bias, static_cast<const bf16*>(res), static_cast<bf16*>(out), (int)M, (int)K, (int)Nout,
                      (int)N, (int)Np, (int)out_rows);
