@@ -208,7 +208,9 @@ class BlockWorkload(Workload):
         from .pairformer import PairformerBlockHip
 
         self.n = n
-        self.n_pad = n // 10
+        # padded (masked) trailing tokens: 10 % at the BASELINE size (config 4,
+        # 76 of 768), 5 % at the 48-block trunk size (config 5, 102 of 2048)
+        self.n_pad = n // 20 if n >= 2048 else n // 10
         self.name = f"pairformer_block_n{n}"
         self.metric = f"ms per Pairformer block at N={n} bf16"
         self.config = {"workload": self.name, "N": n, "c_z": 128, "c_s": 384, "batch": 1,
