@@ -4,7 +4,7 @@
 //   * Activations in HBM are bf16, channel-last ([B, N, N, C] for pair tensors).
 //   * Arithmetic: bf16 MFMA operands with fp32 accumulation; LayerNorm
 //     statistics, softmax and gating in fp32 registers.
-//   * Wavefront = 64 lanes.  A workgroup of 256 threads = 4 waves.
+//   * Wavefront = 64 lanes; workgroups are 4 to 16 waves.
 //
 // MFMA 32x32x16 bf16 (v_mfma_f32_32x32x16_bf16), D[32x32] += A[32x16] * B[16x32].
 // Lane l (0..63), h = l >> 5, n = l & 31:
@@ -58,15 +58,6 @@ __device__ __forceinline__ float sigmoidf_fast(float x) {
 // silu(x) = x * sigmoid(x)
 __device__ __forceinline__ float siluf_fast(float x) { return x * sigmoidf_fast(x); }
 
-__device__ __forceinline__ bf16x4 pack4(float a, float b, float c, float d) {
-  bf16x4 r;
-  r[0] = f2bf(a);
-  r[1] = f2bf(b);
-  r[2] = f2bf(c);
-  r[3] = f2bf(d);
-  return r;
-}
-
 __device__ __forceinline__ bf16x8 load8(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
 __device__ __forceinline__ void store8(bf16* p, bf16x8 v) { *reinterpret_cast<bf16x8*>(p) = v; }
 
@@ -113,48 +104,6 @@ __device__ __forceinline__ float sum8_bf16(bf16x8 v, float acc) {
 __device__ __forceinline__ void unpack8(bf16x8 v, float* out) {
 #pragma unroll
   for (int t = 0; t < 8; ++t) out[t] = bf2f(v[t]);
-}
-
-// ---------------------------------------------------------------------------
-// Pair-tile LayerNorm in LDS.
-//
-// The tile holds P rows of C bf16 channels with a row stride of (C + 8)
-// elements (the 16-byte pad keeps row-per-lane 16-byte reads spread over all
-// LDS banks).  Thread `row` normalises its own row in place:
-//   y = (x - mean) * rsqrt(var + eps) * gamma + beta     (biased variance,
-// two-pass in fp32, exactly the definition torch.nn.LayerNorm uses).
-// gamma/beta are fp32; beta may be null (LayerNorm without bias).
-// ---------------------------------------------------------------------------
-template <int C>
-__device__ __forceinline__ void layernorm_row_lds(bf16* row_ptr, const float* __restrict__ gamma,
-                                                  const float* __restrict__ beta, float eps) {
-  static_assert(C % 8 == 0, "channel count must be a multiple of 8");
-  float v[C];
-#pragma unroll
-  for (int q = 0; q < C / 8; ++q) unpack8(load8(row_ptr + 8 * q), v + 8 * q);
-  float s = 0.f;
-#pragma unroll
-  for (int c = 0; c < C; ++c) s += v[c];
-  const float mean = s * (1.0f / C);
-  float ss = 0.f;
-#pragma unroll
-  for (int c = 0; c < C; ++c) {
-    const float d = v[c] - mean;
-    ss += d * d;
-  }
-  const float rstd = rsqrtf(ss * (1.0f / C) + eps);
-#pragma unroll
-  for (int q = 0; q < C / 8; ++q) {
-    bf16x8 o;
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      const int c = 8 * q + t;
-      float y = (v[c] - mean) * rstd * gamma[c];
-      if (beta) y += beta[c];
-      o[t] = f2bf(y);
-    }
-    store8(row_ptr + 8 * q, o);
-  }
 }
 
 }  // namespace bioemu

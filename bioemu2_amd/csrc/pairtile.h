@@ -25,19 +25,6 @@ __device__ __forceinline__ int perm32(int rho) {
   return ((rho >> 2) & 1) * 16 + (rho >> 3) * 4 + (rho & 3);
 }
 
-// Loads this lane's channel half of a 128-channel bf16 row (or zeros).
-__device__ __forceinline__ void load_half_row(const bf16* row, int h, bool valid, bf16x8 raw[8]) {
-#pragma unroll
-  for (int s = 0; s < 8; ++s) {
-    if (valid) {
-      raw[s] = load8(row + 64 * h + 8 * s);
-    } else {
-#pragma unroll
-      for (int t = 0; t < 8; ++t) raw[s][t] = f2bf(0.f);
-    }
-  }
-}
-
 // LayerNorm over the 128 channels held by lanes l and l^32 (biased variance,
 // two-pass, fp32), gamma/beta fp32 (beta may be null); bf16 result in the
 // MFMA operand layout.
