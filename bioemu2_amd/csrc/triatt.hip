@@ -426,23 +426,20 @@ __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
             psum = sum8_bf16(pa[1], sum8_bf16(pa[0], 0.f)) + sum8_bf16(pb[1], sum8_bf16(pb[0], 0.f));
             // a sum above 2^16 may hold a weight above 2^16: move m (rare)
             slow = __any(psum > kSlackSum);
-            if (slow) {
-#pragma unroll
-              for (int u = 0; u < 16; ++u) {
-                s0[u] += m[t];
-                s1[u] += m[t];
-              }
-            }
           }
           if (slow) {
-            // s0, s1 hold the unshifted logits here
+            // s0, s1 hold the logits minus `shift` (the MFMA subtracts m
+            // once m is set).  Everything here works on those shifted values,
+            // so the fast path above never needs the unshifted logits.
+            const float shift = m_set[t] ? m[t] : 0.f;
             float bmax = fmaxf(s0[0], s1[0]);
 #pragma unroll
             for (int u = 1; u < 16; ++u) bmax = __builtin_fmaxf(bmax, __builtin_fmaxf(s0[u], s1[u]));
-            bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+            bmax = fmaxf(bmax, __shfl_xor(bmax, 32)) + shift;
             // the shift is kept bf16-representable: it enters the MFMA as -m
             const float m_new = bf2f(f2bf(fmaxf(m[t], bmax)));
             const float alpha = fast_exp2(m[t] - m_new);
+            const float delta = m_new - shift;
             m[t] = m_new;
             l[t] *= alpha;
 #pragma unroll
@@ -452,8 +449,8 @@ __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
             if (hh == 0) qm[t][1] = f2bf(-m[t]);
 #pragma unroll
             for (int u = 0; u < 16; ++u) {
-              pa[u >> 3][u & 7] = f2bf(fast_exp2(s0[u] - m[t]));
-              pb[u >> 3][u & 7] = f2bf(fast_exp2(s1[u] - m[t]));
+              pa[u >> 3][u & 7] = f2bf(fast_exp2(s0[u] - delta));
+              pb[u >> 3][u & 7] = f2bf(fast_exp2(s1[u] - delta));
             }
             psum = sum8_bf16(pa[1], sum8_bf16(pa[0], 0.f)) + sum8_bf16(pb[1], sum8_bf16(pb[0], 0.f));
           }
