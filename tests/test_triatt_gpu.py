@@ -97,6 +97,49 @@ def test_padding_bit_exact(gpu_device, starting):
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("starting", [True, False])
+def test_running_max_moves_key_order_invariant(gpu_device, starting):
+    """Logits that rise with the key index by far more than 16 log2 units make the kernel move its running max
+    after it has been set: the ascending order takes the max-moving path in later 64-key blocks, the reversed
+    token order (the same problem, relabelled) meets its max in the first block.  Relabelling every token is
+    an exact symmetry of triangle attention, so the two runs must agree to the north_star bf16 bar.  (Against
+    the fp32 oracle these logits are not a fair case: the ×log2e bias is stored in bf16, whose rounding at
+    |logit| ≈ 20 is worth several percent of an attention weight, in any bf16 implementation.)"""
+    n = 250
+    m = _module(starting, gpu_device)
+    with torch.no_grad():
+        m.proj_b.weight.mul_(2.0)
+    w = m.proj_b.weight[0].detach().float().cpu()
+    g = torch.Generator().manual_seed(11)
+    u = w - w.mean()
+    u = u / u.std()
+    v = torch.randn(C, generator=g)
+    v = v - v.mean()
+    v = v - (v @ u) / (u @ u) * u
+    v = v / v.std()
+    theta = torch.pi * (1.0 - torch.arange(n) / (n - 1))          # key k: bias of head 0 ~ -cos(pi k/(n-1))
+    zk = torch.cos(theta)[:, None] * u + torch.sin(theta)[:, None] * v
+    z = (zk[None, None] + 0.1 * torch.randn(1, n, n, C, generator=g)).to(torch.bfloat16)   # z[., j, k] ~ zk[k]
+    if not starting:
+        z = z.transpose(1, 2).contiguous()   # the ending node's bias reads z[k, j]
+    # The construction does what it claims: head 0's bias (log2 units) rises by > 16 after the first key block.
+    lnz = torch.nn.functional.layer_norm(zk, (C,))
+    b2 = (lnz @ w) * 1.4426950408889634
+    assert b2[64:].max() - b2[:64].max() > 24.0
+    mask = torch.ones(1, n, n, dtype=torch.bool)
+    mask[:, :, 5] = False
+    mask[:, 7, :] = False
+    z, mask = z.to(gpu_device), mask.to(gpu_device)
+    with torch.no_grad():
+        fwd = m(z, mask).float()
+        rev = m(z.flip(1, 2).contiguous(), mask.flip(1, 2).contiguous()).flip(1, 2).float()
+    assert torch.isfinite(fwd).all()
+    err, rl2 = max_abs(fwd, rev), rel_l2(fwd, rev)
+    print(f"triatt rising logits starting={starting}: ascending vs reversed max_abs={err:.3e} rel_l2={rl2:.3e} "
+          f"|out|max={fwd.abs().max():.3f}")
+    assert err <= ATOL and rl2 <= RTOL_L2
+
+
 def test_batch_equals_separate(gpu_device):
     m = _module(False, gpu_device)
     z0, m0 = _inputs(40, gpu_device, seed=1)
