@@ -1,7 +1,7 @@
 // One 256 x 256 output tile of C = A B^T on MFMA, A and B row-major with k
-// contiguous (an "NT" GEMM), for gfx950.  Shared by the triangle contraction
-// (bgemm.hip) and the pair-weighted-averaging contraction (pwa.hip), which
-// differ only in their epilogues.
+// contiguous (an "NT" GEMM), for gfx950.  The tile loop serves the triangle
+// contraction (bgemm.hip); the pair-weighted-averaging kernel (pwa.hip)
+// reuses its LDS swizzle, staging copy and XCD constants.
 //
 // Tiling: BK = 64, 512 threads = 8 waves in a 4 (i) x 2 (j) grid, each wave
 // 64 (i) x 128 (j) = 2 x 4 MFMA 32x32x16 blocks.  Per 16-deep k-step a wave
