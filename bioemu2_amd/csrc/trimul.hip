@@ -35,12 +35,36 @@ constexpr int D = 128;               // pair channels (c_z)
 // columns in [N, Np) come out zero, which the padded contraction relies on.
 // Output: a and b as channel-major planes [B][D][Np][Np] (k contiguous).
 // ---------------------------------------------------------------------------
-constexpr int kInThreads = 512;
+// Workgroup size: 8, 12 or 16 waves, chosen per launch (in_waves_per_wg);
+// the staged weights (140 KB of LDS) allow one workgroup per CU.
+constexpr int kInMaxThreads = 1024;
 constexpr int kInRows = 4 * D;                 // p_in (2D rows) then g_in (2D rows)
 constexpr int kInSmem = kInRows * kLdw * 2 + 2 * D * 4;   // weights, then LayerNorm gamma | beta (fp32)
 
+// Waves per workgroup for `tiles` 32-pair tiles on `cus` CUs (one workgroup
+// each).  More waves hide more of each tile's load -> LayerNorm -> MFMA ->
+// store latency (measured with whole rounds of tiles: 16 waves 1.11x the
+// throughput of 8 at N = 512, 12 waves 1.02x at N = 768), but a grid whose
+// last round of tiles is partial pays for a whole round:
+// cost = rounds x waves / throughput.  N = 512 -> 16, 768 -> 12, 2048 -> 16.
+inline int in_waves_per_wg(long long tiles, int cus) {
+  const int cand[3] = {8, 12, 16};
+  const double gain[3] = {1.0, 1.02, 1.11};
+  int best = 8;
+  double best_cost = 0;
+  for (int c = 0; c < 3; ++c) {
+    const long long per_round = (long long)cus * cand[c];
+    const double cost = (double)((tiles + per_round - 1) / per_round) * cand[c] / gain[c];
+    if (c == 0 || cost < best_cost) {
+      best = cand[c];
+      best_cost = cost;
+    }
+  }
+  return best;
+}
+
 template <bool kOutgoing>
-__global__ __launch_bounds__(kInThreads) void trimul_proj_in_kernel(
+__global__ __launch_bounds__(kInMaxThreads) void trimul_proj_in_kernel(
     const bf16* __restrict__ x, const uint8_t* __restrict__ mask, const float* __restrict__ ln_w,
     const float* __restrict__ ln_b, const bf16* __restrict__ p_w, const bf16* __restrict__ g_w,
     bf16* __restrict__ ab, int B, int N, int Np) {
@@ -357,15 +381,16 @@ extern "C" int bioemu_trimul_fwd(const void* x, const uint8_t* mask, const float
     return set_error(BIOEMU_ERR_LAUNCH, "trimul: cannot set dynamic LDS size");
   const long long waves_in = (long long)B * Np * (Np / 32);
   if (waves_in >= kMaxTiles) return set_error(BIOEMU_ERR_INVALID_ARG, "trimul: too many pair tiles");
-  const unsigned grid1 = (unsigned)std::min<long long>(cus, (waves_in + 7) / 8);
+  const int in_waves = in_waves_per_wg(waves_in, cus);
+  const unsigned grid1 = (unsigned)std::min<long long>(cus, (waves_in + in_waves - 1) / in_waves);
   {
     KernelTimerScope timed("trimul_proj_in", stream);
     if (outgoing)
-      hipLaunchKernelGGL(trimul_proj_in_kernel<true>, dim3(grid1), dim3(kInThreads), kInSmem, stream,
+      hipLaunchKernelGGL(trimul_proj_in_kernel<true>, dim3(grid1), dim3(64 * in_waves), kInSmem, stream,
                          static_cast<const bf16*>(x), mask, norm_in_w, norm_in_b, static_cast<const bf16*>(p_in_w),
                          static_cast<const bf16*>(g_in_w), ab, (int)B, (int)N, (int)Np);
     else
-      hipLaunchKernelGGL(trimul_proj_in_kernel<false>, dim3(grid1), dim3(kInThreads), kInSmem, stream,
+      hipLaunchKernelGGL(trimul_proj_in_kernel<false>, dim3(grid1), dim3(64 * in_waves), kInSmem, stream,
                          static_cast<const bf16*>(x), mask, norm_in_w, norm_in_b, static_cast<const bf16*>(p_in_w),
                          static_cast<const bf16*>(g_in_w), ab, (int)B, (int)N, (int)Np);
   }
