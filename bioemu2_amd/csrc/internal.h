@@ -37,6 +37,25 @@ inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 // that fits in device memory).
 constexpr int64_t kMaxTiles = int64_t(1) << 31;
 
+// Waves per workgroup for a persistent grid of one workgroup per CU that
+// walks `tiles` equal tiles: more waves hide more latency (gain[c] = measured
+// throughput of waves[c] relative to waves[0] when the tiles divide evenly),
+// but a partial last round of tiles costs a whole round, so the pick
+// minimises rounds x waves / gain.
+inline int pick_waves_per_wg(int64_t tiles, int cus, const int* waves, const double* gain, int n) {
+  int best = waves[0];
+  double best_cost = 0;
+  for (int c = 0; c < n; ++c) {
+    const int64_t per_round = (int64_t)cus * waves[c];
+    const double cost = (double)((tiles + per_round - 1) / per_round) * waves[c] / gain[c];
+    if (c == 0 || cost < best_cost) {
+      best = waves[c];
+      best_cost = cost;
+    }
+  }
+  return best;
+}
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // Batched bf16 "NT" GEMM: C[z][i][j] = sum_k A[z][i][k] * B[z][j][k] for

@@ -41,26 +41,13 @@ constexpr int kInMaxThreads = 1024;
 constexpr int kInRows = 4 * D;                 // p_in (2D rows) then g_in (2D rows)
 constexpr int kInSmem = kInRows * kLdw * 2 + 2 * D * 4;   // weights, then LayerNorm gamma | beta (fp32)
 
-// Waves per workgroup for `tiles` 32-pair tiles on `cus` CUs (one workgroup
-// each).  More waves hide more of each tile's load -> LayerNorm -> MFMA ->
-// store latency (measured with whole rounds of tiles: 16 waves 1.11x the
-// throughput of 8 at N = 512, 12 waves 1.02x at N = 768), but a grid whose
-// last round of tiles is partial pays for a whole round:
-// cost = rounds x waves / throughput.  N = 512 -> 16, 768 -> 12, 2048 -> 16.
+// Waves per workgroup (pick_waves_per_wg).  Measured with whole rounds of
+// tiles: 16 waves give 1.11x the throughput of 8 at N = 512, 12 waves 1.02x
+// at N = 768.  Picks: N = 512 -> 16, 768 -> 12, 2048 -> 16.
 inline int in_waves_per_wg(long long tiles, int cus) {
-  const int cand[3] = {8, 12, 16};
-  const double gain[3] = {1.0, 1.02, 1.11};
-  int best = 8;
-  double best_cost = 0;
-  for (int c = 0; c < 3; ++c) {
-    const long long per_round = (long long)cus * cand[c];
-    const double cost = (double)((tiles + per_round - 1) / per_round) * cand[c] / gain[c];
-    if (c == 0 || cost < best_cost) {
-      best = cand[c];
-      best_cost = cost;
-    }
-  }
-  return best;
+  static const int waves[3] = {8, 12, 16};
+  static const double gain[3] = {1.0, 1.02, 1.11};
+  return pick_waves_per_wg(tiles, cus, waves, gain, 3);
 }
 
 template <bool kOutgoing>
