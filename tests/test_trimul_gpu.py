@@ -90,6 +90,25 @@ def test_padding_bit_exact(gpu_device, mode):
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("mode", ["outgoing", "incoming"])
+def test_projection_workgroup_sizes_bit_exact(gpu_device, mode):
+    """The input projection's workgroup size is chosen from the tile count: N = 512 runs 16-wave workgroups,
+    the same problem with 88 masked tokens appended (N = 600, padded to 768) runs 12-wave ones.  A tile's result
+    does not depend on which wave computes it and padded k columns are zeros, so the valid region must agree
+    bit for bit."""
+    n, pad = 512, 88
+    m = _module(mode, gpu_device)
+    x, mask = _inputs(n, gpu_device, seed=6)
+    px = torch.full((1, n + pad, n + pad, D), 7.0, dtype=x.dtype, device=gpu_device)
+    px[:, :n, :n] = x
+    pmask = torch.zeros(1, n + pad, n + pad, dtype=torch.bool, device=gpu_device)
+    pmask[:, :n, :n] = mask
+    with torch.no_grad():
+        a = m(x, mask)
+        b = m(px, pmask)[:, :n, :n]
+    assert torch.equal(a, b)
+
+
 def test_batch_equals_separate(gpu_device):
     m = _module("incoming", gpu_device)
     x0, m0 = _inputs(48, gpu_device, seed=1)
