@@ -52,8 +52,8 @@ def cpu_baseline(wl) -> dict:
     """The fp32 CPU oracle on a bounded sample of the same workload (rank 0, N=1 only).
 
     By default 1 warm-up then the median of up to 3 timed calls, stopping
-    early once ~30 s of CPU time is spent (the full block is one cold call);
-    ``value`` is scaled to ms per full step.
+    early once ~30 s of CPU time is spent (the 48-block trunk times one call
+    of its scaled sample); ``value`` is scaled to ms per full step.
     """
     import torch
 
@@ -83,7 +83,18 @@ def cpu_baseline(wl) -> dict:
         "cores": threads,
         "kind": "port",
         "sample": f"{sample}; {len(times)} timed call(s) after {warm} warm-up(s), median",
+        "cpu_model": _cpu_model(),
     }
+
+
+def _cpu_model() -> str:
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def main() -> int:

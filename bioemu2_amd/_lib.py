@@ -31,32 +31,32 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "bioemu_trimul_workspace_bytes": (_c_size_t, [_c_int64, _c_int64, _c_int64]),
     "bioemu_trimul_fwd": (
         _c_int,
-        [_c_void_p] * 11 + [_c_void_p, _c_size_t, _c_int64, _c_int64, _c_int64, _c_int, _c_int, _c_void_p],
+        [_c_void_p] * 12 + [_c_void_p, _c_size_t, _c_int64, _c_int64, _c_int64, _c_int, _c_int, _c_void_p],
     ),
     "bioemu_triatt_workspace_bytes": (_c_size_t, [_c_int64] * 4),
     "bioemu_triatt_fwd": (
         _c_int,
-        [_c_void_p] * 7 + [_c_void_p, _c_size_t] + [_c_int64] * 4 + [_c_int, _c_int, _c_void_p],
+        [_c_void_p] * 8 + [_c_void_p, _c_size_t] + [_c_int64] * 4 + [_c_int, _c_int, _c_void_p],
     ),
     "bioemu_transition_pair_workspace_bytes": (_c_size_t, [_c_int64] * 2),
     "bioemu_transition_pair_fwd": (
         _c_int,
-        [_c_void_p] * 7 + [_c_void_p, _c_size_t] + [_c_int64] * 3 + [_c_int, _c_int, _c_void_p],
+        [_c_void_p] * 8 + [_c_void_p, _c_size_t] + [_c_int64] * 3 + [_c_int, _c_int, _c_void_p],
     ),
     "bioemu_transition_token_workspace_bytes": (_c_size_t, [_c_int64] * 3),
     "bioemu_transition_token_fwd": (
         _c_int,
-        [_c_void_p] * 7 + [_c_void_p, _c_size_t] + [_c_int64] * 3 + [_c_int, _c_int, _c_void_p],
+        [_c_void_p] * 8 + [_c_void_p, _c_size_t] + [_c_int64] * 3 + [_c_int, _c_int, _c_void_p],
     ),
     "bioemu_pwa_workspace_bytes": (_c_size_t, [_c_int64] * 6),
     "bioemu_pwa_fwd": (
         _c_int,
-        [_c_void_p] * 12 + [_c_void_p, _c_size_t] + [_c_int64] * 7 + [_c_int, _c_void_p],
+        [_c_void_p] * 13 + [_c_void_p, _c_size_t] + [_c_int64] * 7 + [_c_int, _c_void_p],
     ),
     "bioemu_apb_workspace_bytes": (_c_size_t, [_c_int64] * 5),
     "bioemu_apb_fwd": (
         _c_int,
-        [_c_void_p] * 13 + [_c_void_p, _c_size_t] + [_c_int64] * 6 + [_c_int, _c_void_p],
+        [_c_void_p] * 14 + [_c_void_p, _c_size_t] + [_c_int64] * 6 + [_c_int, _c_void_p],
     ),
     "bioemu_swa_workspace_bytes": (_c_size_t, [_c_int64] * 7),
     "bioemu_swa_fwd": (
@@ -72,8 +72,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "bioemu_opm_workspace_bytes": (_c_size_t, [_c_int64] * 5),
     "bioemu_opm_fwd": (
         _c_int,
-        [_c_void_p, _c_void_p, _c_int] + [_c_void_p] * 8 + [_c_size_t] + [_c_int64] * 6 + [_c_void_p],
+        [_c_void_p, _c_void_p, _c_int] + [_c_void_p] * 9 + [_c_size_t] + [_c_int64] * 6 + [_c_void_p],
     ),
+    "bioemu_stream_split": (_c_int, [_c_void_p] * 3 + [_c_int64, _c_void_p]),
+    "bioemu_stream_join": (_c_int, [_c_void_p] * 3 + [_c_int64, _c_void_p]),
 }
 
 _lock = threading.Lock()

@@ -62,6 +62,44 @@ def workspace(nbytes: int, device) -> Tensor:
     return torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=device)
 
 
+def _check_tail(tail: Tensor | None, out: Tensor, residual: bool, what: str) -> None:
+    """A residual tail is the int8 plane of the stream ``out`` is written into (one byte per element)."""
+    if tail is None:
+        return
+    if not residual:
+        raise ValueError(f"{what}: a residual tail needs residual=True")
+    _check_tensor(tail, f"{what} residual tail", torch.int8, tuple(out.shape), out.device)
+
+
+# ----------------------------------------------------------------------------
+# Residual streams: fp32 <-> (bf16 value, int8 tail)
+# ----------------------------------------------------------------------------
+def stream_split(x: Tensor, hi: Tensor | None = None, tail: Tensor | None = None) -> tuple[Tensor, Tensor]:
+    """fp32 ``x`` -> (bf16 ``hi``, int8 ``tail``) with hi + tail carrying ~16 significant bits."""
+    require_gpu(x, "stream_split")
+    if x.dtype != torch.float32 or not x.is_contiguous() or x.numel() % 16:
+        raise ValueError("stream_split: x must be a contiguous fp32 tensor with a multiple of 16 elements")
+    hi = torch.empty(x.shape, dtype=BF16, device=x.device) if hi is None else hi
+    tail = torch.empty(x.shape, dtype=torch.int8, device=x.device) if tail is None else tail
+    _check_tensor(hi, "stream_split hi", BF16, tuple(x.shape), x.device)
+    _check_tensor(tail, "stream_split tail", torch.int8, tuple(x.shape), x.device)
+    check(lib().bioemu_stream_split(_ptr(x), _ptr(hi), _ptr(tail), x.numel(), _stream(x)), "bioemu_stream_split")
+    return hi, tail
+
+
+def stream_join(hi: Tensor, tail: Tensor, out: Tensor | None = None) -> Tensor:
+    """(bf16 ``hi``, int8 ``tail``) -> fp32."""
+    require_gpu(hi, "stream_join")
+    if hi.numel() % 16:
+        raise ValueError("stream_join: element count must be a multiple of 16")
+    _check_tensor(hi, "stream_join hi", BF16, tuple(hi.shape), hi.device)
+    _check_tensor(tail, "stream_join tail", torch.int8, tuple(hi.shape), hi.device)
+    out = torch.empty(hi.shape, dtype=torch.float32, device=hi.device) if out is None else out
+    _check_tensor(out, "stream_join out", torch.float32, tuple(hi.shape), hi.device)
+    check(lib().bioemu_stream_join(_ptr(hi), _ptr(tail), _ptr(out), hi.numel(), _stream(hi)), "bioemu_stream_join")
+    return out
+
+
 # ----------------------------------------------------------------------------
 # Triangle multiplication
 # ----------------------------------------------------------------------------
@@ -84,6 +122,7 @@ def launch_trimul(
     outgoing: bool,
     residual: bool = False,
     ws: Tensor | None = None,
+    tail: Tensor | None = None,
 ) -> Tensor:
     require_gpu(x, "trimul")
     if x.ndim != 4 or x.shape[1] != x.shape[2]:
@@ -104,12 +143,13 @@ def launch_trimul(
         ("g_out.weight", g_out_w, (D, D), BF16),
     ):
         _check_tensor(t, f"trimul {name}", dt, shp, dev)
+    _check_tail(tail, out, residual, "trimul")
     need = trimul_workspace_bytes(B, N, D)
     if ws is None or ws.numel() < need:
         ws = workspace(need, dev)
     rc = lib().bioemu_trimul_fwd(
         _ptr(x), _ptr(mask), _ptr(norm_in_w), _ptr(norm_in_b), _ptr(p_in_w), _ptr(g_in_w),
-        _ptr(norm_out_w), _ptr(norm_out_b), _ptr(p_out_w), _ptr(g_out_w), _ptr(out),
+        _ptr(norm_out_w), _ptr(norm_out_b), _ptr(p_out_w), _ptr(g_out_w), _ptr(out), _ptr(tail),
         _ptr(ws), ctypes.c_size_t(ws.numel()), B, N, D, int(bool(outgoing)), int(bool(residual)),
         _stream(x),
     )
@@ -167,6 +207,7 @@ def launch_triatt(
     num_heads: int = 4,
     residual: bool = False,
     ws: Tensor | None = None,
+    tail: Tensor | None = None,
 ) -> Tensor:
     require_gpu(z, "triatt")
     if z.ndim != 4 or z.shape[1] != z.shape[2]:
@@ -180,11 +221,12 @@ def launch_triatt(
     _check_tensor(norm_b, "triatt norm.bias", torch.float32, (D,), dev)
     _check_tensor(w_proj, "triatt packed projection", BF16, (4 * D + num_heads, D), dev)
     _check_tensor(w_o, "triatt proj_o.weight", BF16, (D, D), dev)
+    _check_tail(tail, out, residual, "triatt")
     need = triatt_workspace_bytes(B, N, D, num_heads)
     if ws is None or ws.numel() < need:
         ws = workspace(need, dev)
     rc = lib().bioemu_triatt_fwd(
-        _ptr(z), _ptr(mask), _ptr(norm_w), _ptr(norm_b), _ptr(w_proj), _ptr(w_o), _ptr(out),
+        _ptr(z), _ptr(mask), _ptr(norm_w), _ptr(norm_b), _ptr(w_proj), _ptr(w_o), _ptr(out), _ptr(tail),
         _ptr(ws), ctypes.c_size_t(ws.numel()), B, N, D, num_heads, int(bool(starting)),
         int(bool(residual)), _stream(z),
     )
@@ -235,6 +277,7 @@ def launch_transition_pair(
     out: Tensor,
     residual: bool = False,
     ws: Tensor | None = None,
+    tail: Tensor | None = None,
 ) -> Tensor:
     require_gpu(x, "transition")
     D = x.shape[-1]
@@ -250,11 +293,12 @@ def launch_transition_pair(
     if use_norm:
         _check_tensor(norm_w, "transition norm.weight", torch.float32, (D,), dev)
         _check_tensor(norm_b, "transition norm.bias", torch.float32, (D,), dev)
+    _check_tail(tail, out, residual, "transition")
     need = transition_pair_workspace_bytes(D, hidden)
     if ws is None or ws.numel() < need:
         ws = workspace(need, dev)
     rc = lib().bioemu_transition_pair_fwd(
-        _ptr(x), _ptr(norm_w), _ptr(norm_b), _ptr(fc1_w), _ptr(fc2_w), _ptr(fc3_w), _ptr(out),
+        _ptr(x), _ptr(norm_w), _ptr(norm_b), _ptr(fc1_w), _ptr(fc2_w), _ptr(fc3_w), _ptr(out), _ptr(tail),
         _ptr(ws), ctypes.c_size_t(ws.numel()), P, D, hidden, int(use_norm), int(bool(residual)), _stream(x),
     )
     check(rc, "bioemu_transition_pair_fwd")
@@ -275,6 +319,7 @@ def launch_transition_token(
     out: Tensor,
     residual: bool = False,
     ws: Tensor | None = None,
+    tail: Tensor | None = None,
 ) -> Tensor:
     require_gpu(x, "transition")
     D = x.shape[-1]
@@ -290,11 +335,12 @@ def launch_transition_token(
     if use_norm:
         _check_tensor(norm_w, "transition norm.weight", torch.float32, (D,), dev)
         _check_tensor(norm_b, "transition norm.bias", torch.float32, (D,), dev)
+    _check_tail(tail, out, residual, "transition")
     need = transition_token_workspace_bytes(M, D, hidden)
     if ws is None or ws.numel() < need:
         ws = workspace(need, dev)
     rc = lib().bioemu_transition_token_fwd(
-        _ptr(x), _ptr(norm_w), _ptr(norm_b), _ptr(fc1_w), _ptr(fc2_w), _ptr(fc3_w), _ptr(out),
+        _ptr(x), _ptr(norm_w), _ptr(norm_b), _ptr(fc1_w), _ptr(fc2_w), _ptr(fc3_w), _ptr(out), _ptr(tail),
         _ptr(ws), ctypes.c_size_t(ws.numel()), M, D, hidden, int(use_norm), int(bool(residual)), _stream(x),
     )
     check(rc, "bioemu_transition_token_fwd")
@@ -354,6 +400,7 @@ def launch_apb(
     multiplicity: int = 1,
     residual: bool = False,
     ws: Tensor | None = None,
+    tail: Tensor | None = None,
 ) -> Tensor:
     require_gpu(s, "attention_pair_bias")
     if s.ndim != 3 or z.ndim != 4 or mask.ndim != 2:
@@ -378,12 +425,14 @@ def launch_apb(
         _check_tensor(norm_z_b, "apb norm_z.bias", torch.float32, (c_z,), dev)
     _check_tensor(w_z, "apb proj_z.weight", BF16, (num_heads, c_z), dev)
     _check_tensor(w_o, "apb proj_o.weight", BF16, (c_s, c_s), dev)
+    _check_tail(tail, out, residual, "apb")
     need = apb_workspace_bytes(B, multiplicity, N, c_s, num_heads)
     if ws is None or ws.numel() < need:
         ws = workspace(need, dev)
     rc = lib().bioemu_apb_fwd(
         _ptr(s), _ptr(z), _ptr(mask), _ptr(norm_s_w), _ptr(norm_s_b), _ptr(w_qkv), _ptr(q_bias), _ptr(w_g),
-        _ptr(norm_z_w), _ptr(norm_z_b), _ptr(w_z), _ptr(w_o), _ptr(out), _ptr(ws), ctypes.c_size_t(ws.numel()),
+        _ptr(norm_z_w), _ptr(norm_z_b), _ptr(w_z), _ptr(w_o), _ptr(out), _ptr(tail), _ptr(ws),
+        ctypes.c_size_t(ws.numel()),
         B, multiplicity, N, c_s, c_z, num_heads, int(bool(residual)), _stream(s),
     )
     check(rc, "bioemu_apb_fwd")
@@ -614,6 +663,7 @@ def launch_opm(
     out: Tensor,
     z_res: Tensor | None = None,
     ws: Tensor | None = None,
+    tail: Tensor | None = None,
 ) -> Tensor:
     require_gpu(m, "outer_product_mean")
     if m.ndim != 4:
@@ -632,6 +682,7 @@ def launch_opm(
     _check_tensor(out, "opm out", BF16, (B, N, N, c_out), dev)
     if z_res is not None:
         _check_tensor(z_res, "opm z", BF16, (B, N, N, c_out), dev)
+    _check_tail(tail, out, z_res is not None, "opm")
     need = opm_workspace_bytes(B, S, N, c_in, c_h)
     if need == 0:
         raise ValueError(f"opm: unsupported widths c_in={c_in} c_hidden={c_h}")
@@ -639,7 +690,8 @@ def launch_opm(
         ws = workspace(need, dev)
     rc = lib().bioemu_opm_fwd(
         _ptr(m), _ptr(mask3), int(bool(mean_rows)), _ptr(norm_w), _ptr(norm_b), _ptr(w_ab), _ptr(w_o), _ptr(b_o),
-        _ptr(z_res), _ptr(out), _ptr(ws), ctypes.c_size_t(ws.numel()), B, S, N, c_in, c_h, c_out, _stream(m),
+        _ptr(z_res), _ptr(out), _ptr(tail), _ptr(ws), ctypes.c_size_t(ws.numel()), B, S, N, c_in, c_h, c_out,
+        _stream(m),
     )
     check(rc, "bioemu_opm_fwd")
     return out
@@ -668,6 +720,7 @@ def launch_pwa(
     num_heads: int,
     residual: bool = False,
     ws: Tensor | None = None,
+    tail: Tensor | None = None,
 ) -> Tensor:
     require_gpu(m, "pair_weighted_averaging")
     if m.ndim != 4 or z.ndim != 4:
@@ -690,6 +743,7 @@ def launch_pwa(
     _check_tensor(w_z, "pwa proj_z.weight", BF16, (H, c_z), dev)
     _check_tensor(w_o, "pwa proj_o.weight", BF16, (c_m, H * c_h), dev)
     _check_tensor(out, "pwa out", BF16, (B, S, N, c_m), dev)
+    _check_tail(tail, out, residual, "pwa")
     need = pwa_workspace_bytes(B, S, N, c_m, c_h, H)
     if need == 0:
         raise ValueError(f"pwa: unsupported widths c_m={c_m} c_h={c_h} heads={H} (supported: 64, 32, 8)")
@@ -697,7 +751,7 @@ def launch_pwa(
         ws = workspace(need, dev)
     rc = lib().bioemu_pwa_fwd(
         _ptr(m), _ptr(z), _ptr(mask_u8), _ptr(norm_m_w), _ptr(norm_m_b), _ptr(w_m), _ptr(w_g), _ptr(norm_z_w),
-        _ptr(norm_z_b), _ptr(w_z), _ptr(w_o), _ptr(out), _ptr(ws), ctypes.c_size_t(ws.numel()),
+        _ptr(norm_z_b), _ptr(w_z), _ptr(w_o), _ptr(out), _ptr(tail), _ptr(ws), ctypes.c_size_t(ws.numel()),
         B, S, N, c_m, c_z, c_h, H, int(bool(residual)), _stream(m),
     )
     check(rc, "bioemu_pwa_fwd")

@@ -244,8 +244,9 @@ extern "C" size_t bioemu_apb_workspace_bytes(int64_t B, int64_t mult, int64_t N,
 extern "C" int bioemu_apb_fwd(const void* s, const void* z, const uint8_t* mask, const float* norm_s_w,
                               const float* norm_s_b, const void* w_qkv, const float* q_bias, const void* w_g,
                               const float* norm_z_w, const float* norm_z_b, const void* w_z, const void* w_o,
-                              void* out, void* workspace, size_t workspace_bytes, int64_t B, int64_t mult,
-                              int64_t N, int64_t c_s, int64_t c_z, int64_t H, int residual, hipStream_t stream) {
+                              void* out, int8_t* res_tail, void* workspace, size_t workspace_bytes, int64_t B,
+                              int64_t mult, int64_t N, int64_t c_s, int64_t c_z, int64_t H, int residual,
+                              hipStream_t stream) {
   if (c_z != CZ || H <= 0 || H > 32 || c_s != H * DH || (c_s != 384 && c_s != 128))
     return set_error(BIOEMU_ERR_UNSUPPORTED,
                      "apb: supported shapes are c_z=128 and head dim 24 with c_s in {128, 384} (got c_s=%lld c_z=%lld H=%lld)",
@@ -261,6 +262,8 @@ extern "C" int bioemu_apb_fwd(const void* s, const void* z, const uint8_t* mask,
     return set_error(BIOEMU_ERR_INVALID_ARG, "apb: tensors must be 16-byte aligned");
   if (out == s && !residual)
     return set_error(BIOEMU_ERR_INVALID_ARG, "apb: out may alias s only with residual=1");
+  if (res_tail && (!residual || !aligned16(res_tail)))
+    return set_error(BIOEMU_ERR_INVALID_ARG, "apb: res_tail needs residual=1 and 16-byte alignment");
   const int64_t BM = B * mult;
   if (workspace_bytes < apb_layout(B, BM, N, c_s, H, nullptr, nullptr))
     return set_error(BIOEMU_ERR_WORKSPACE, "apb: workspace too small");
@@ -305,5 +308,5 @@ extern "C" int bioemu_apb_fwd(const void* s, const void* z, const uint8_t* mask,
   rc = check_launch("apb_flash");
   if (rc) return rc;
   return token_gemm(residual ? kEpiResidualId : kEpiStoreId, false, buf.go, w_o, nullptr, nullptr, s, out, M, c_s,
-                    c_s, N, Np, N, stream, "apb_proj_o");
+                    c_s, N, Np, N, stream, "apb_proj_o", res_tail);
 }

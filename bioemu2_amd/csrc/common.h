@@ -106,4 +106,61 @@ __device__ __forceinline__ void unpack8(bf16x8 v, float* out) {
   for (int t = 0; t < 8; ++t) out[t] = bf2f(v[t]);
 }
 
+// ---------------------------------------------------------------------------
+// Residual tails.  A residual stream (the pair tensor z, the single s, the
+// MSA m) can be carried at ~16 significant bits as its bf16 value hi plus one
+// int8 "tail" t per element:
+//   value = hi + t * 2^(E - 142),   E = biased exponent field of hi,
+// so t counts 1/256ths of hi's unit in the last place (ulp = 2^(E - 134) for
+// a normal hi).  hi is the round-to-nearest bf16 of the value, so the
+// remainder is at most half an ulp (|t| <= 128, clamped to 127).  Kernels that
+// only *read* the stream (LayerNorm inputs) use hi; kernels that add a
+// residual read hi + tail and write the sum back as a new (hi, tail).  Tail
+// planes have the layout of their stream with one byte per element.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int bf16_exp_field(bf16 v) {
+  return (int)((__builtin_bit_cast(uint16_t, v) >> 7) & 0xffu);
+}
+
+// hi + t * 2^(E(hi) - 142)
+__device__ __forceinline__ float tail_decode(bf16 hi, int t) {
+  return bf2f(hi) + __builtin_amdgcn_ldexpf((float)t, bf16_exp_field(hi) - 142);
+}
+
+// Splits v into (hi, t); returns hi, writes t in [-127, 127].
+__device__ __forceinline__ bf16 tail_encode(float v, int& t) {
+  const bf16 hi = f2bf(v);
+  const float r = __builtin_amdgcn_ldexpf(v - bf2f(hi), 142 - bf16_exp_field(hi));
+  t = (int)__builtin_amdgcn_fmed3f(__builtin_rintf(r), -127.f, 127.f);
+  return hi;
+}
+
+// Sixteen consecutive elements: raw bf16 halves r0, r1 and their 16 tail bytes
+// -> fp32 values.
+__device__ __forceinline__ void tail_decode16(bf16x8 r0, bf16x8 r1, u32x4 tb, float* v) {
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {
+    const int t = __builtin_amdgcn_sbfe((int)tb[u >> 2], 8 * (u & 3), 8);
+    v[u] = tail_decode(u < 8 ? r0[u] : r1[u - 8], t);
+  }
+}
+
+// Sixteen fp32 values -> bf16 halves (stored at dst, dst + 8) and tail bytes.
+__device__ __forceinline__ void tail_store16(bf16* dst, int8_t* tdst, const float* v) {
+  bf16x8 a, b;
+  u32x4 tb = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {
+    int t;
+    const bf16 hi = tail_encode(v[u], t);
+    if (u < 8) a[u] = hi; else b[u - 8] = hi;
+    tb[u >> 2] |= ((uint32_t)t & 0xffu) << (8 * (u & 3));
+  }
+  *reinterpret_cast<bf16x8*>(dst) = a;
+  *reinterpret_cast<bf16x8*>(dst + 8) = b;
+  *reinterpret_cast<u32x4*>(tdst) = tb;
+}
+
+__device__ __forceinline__ u32x4 load_tail16(const int8_t* p) { return *reinterpret_cast<const u32x4*>(p); }
+
 }  // namespace bioemu

@@ -79,7 +79,7 @@ int token_layernorm(const void* x, const float* gamma, const float* beta, void* 
                     int64_t Np, int64_t K, hipStream_t stream);
 int token_gemm(int epi, bool trans, const void* A, const void* W, const void* W2, const float* col_bias,
                const void* res, void* out, int64_t M, int64_t K, int64_t Nout, int64_t N, int64_t Np,
-               int64_t out_rows, hipStream_t stream, const char* name);
+               int64_t out_rows, hipStream_t stream, const char* name, int8_t* tail = nullptr);
 constexpr int kEpiStoreId = 0, kEpiSigmoidId = 1, kEpiSwiGLUId = 2, kEpiResidualId = 3;
 
 }  // namespace bioemu

@@ -175,7 +175,7 @@ constexpr int kFusedSmem = kFusedSmemA > kFusedSmemB ? kFusedSmemA : kFusedSmemB
 
 __global__ __launch_bounds__(kFusedThreads) void opm_fused_kernel(
     const bf16* __restrict__ aT, const bf16* __restrict__ bT, const int* __restrict__ count, int mean_rows,
-    const bf16* __restrict__ w_o, const float* __restrict__ b_o, const bf16* zres, bf16* out, int N, int Nt, int Sp) {
+    const bf16* __restrict__ w_o, const float* __restrict__ b_o, const bf16* zres, bf16* out, int8_t* tail, int N, int Nt, int Sp) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   bf16* stage = reinterpret_cast<bf16*>(smem);
   bf16* xb = reinterpret_cast<bf16*>(smem);
@@ -280,6 +280,14 @@ __global__ __launch_bounds__(kFusedThreads) void opm_fused_kernel(
   float v[16];
 #pragma unroll
   for (int u = 0; u < 16; ++u) v[u] = y[u] + b_o[eb * 32 + 16 * h + u];
+  if (zres && tail) {   // residual stream with an int8 tail (common.h), in place
+    float zv[16];
+    tail_decode16(load8(zres + off), load8(zres + off + 8), load_tail16(tail + off), zv);
+#pragma unroll
+    for (int u = 0; u < 16; ++u) v[u] += zv[u];
+    tail_store16(out + off, tail + off, v);
+    return;
+  }
   if (zres) {
     const bf16x8 r0 = load8(zres + off), r1 = load8(zres + off + 8);
 #pragma unroll
@@ -323,9 +331,9 @@ extern "C" size_t bioemu_opm_workspace_bytes(int64_t B, int64_t S, int64_t N, in
 
 extern "C" int bioemu_opm_fwd(const void* m, const uint8_t* mask, int mean_rows, const float* norm_w,
                               const float* norm_b, const void* w_ab, const void* w_o, const float* b_o,
-                              const void* z_res, void* out, void* workspace, size_t workspace_bytes, int64_t B,
-                              int64_t S, int64_t N, int64_t c_in, int64_t c_hidden, int64_t c_out,
-                              hipStream_t stream) {
+                              const void* z_res, void* out, int8_t* res_tail, void* workspace,
+                              size_t workspace_bytes, int64_t B, int64_t S, int64_t N, int64_t c_in,
+                              int64_t c_hidden, int64_t c_out, hipStream_t stream) {
   if (c_in != CIN || c_hidden != CH || c_out != COUT)
     return set_error(BIOEMU_ERR_UNSUPPORTED, "opm: only c_in=64, c_hidden=32, c_out=128 supported (got %lld/%lld/%lld)",
                      (long long)c_in, (long long)c_hidden, (long long)c_out);
@@ -337,6 +345,8 @@ extern "C" int bioemu_opm_fwd(const void* m, const uint8_t* mask, int mean_rows,
   if (!aligned16(m) || !aligned16(w_ab) || !aligned16(w_o) || !aligned16(out) || !aligned16(workspace) ||
       (z_res && !aligned16(z_res)))
     return set_error(BIOEMU_ERR_INVALID_ARG, "opm: tensors must be 16-byte aligned");
+  if (res_tail && (!z_res || !aligned16(res_tail)))
+    return set_error(BIOEMU_ERR_INVALID_ARG, "opm: res_tail needs z_res and 16-byte alignment");
   if (workspace_bytes < opm_layout(B, S, N, nullptr, nullptr))
     return set_error(BIOEMU_ERR_WORKSPACE, "opm: workspace too small");
   OpmLayout L;
@@ -374,7 +384,7 @@ extern "C" int bioemu_opm_fwd(const void* m, const uint8_t* mask, int mean_rows,
     KernelTimerScope timed("opm_fused", stream);
     hipLaunchKernelGGL(opm_fused_kernel, g3, dim3(kFusedThreads), kFusedSmem, stream, L.aT, L.bT, L.count, mean_rows,
                        static_cast<const bf16*>(w_o), b_o, static_cast<const bf16*>(z_res), static_cast<bf16*>(out),
-                       (int)N, (int)Nt, (int)Sp);
+                       res_tail, (int)N, (int)Nt, (int)Sp);
   }
   return check_launch("opm_fused");
 }

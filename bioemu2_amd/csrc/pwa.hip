@@ -259,8 +259,8 @@ __global__ __launch_bounds__(kFuThreads) void pwa_fused_kernel(const bf16* __res
                                                                const bf16* __restrict__ vt,
                                                                const bf16* __restrict__ g,
                                                                const bf16* __restrict__ wo, const bf16* mres,
-                                                               bf16* out, int S, int S8, int N, int Np, int residual,
-                                                               int nitems) {
+                                                               bf16* out, int8_t* tail, int S, int S8, int N, int Np,
+                                                               int residual, int nitems) {
   extern __shared__ __attribute__((aligned(16))) char smem_raw[];
   bf16* smem = reinterpret_cast<bf16*>(smem_raw);
   bf16* wol = smem + 2 * kFuStage;
@@ -384,6 +384,14 @@ __global__ __launch_bounds__(kFuThreads) void pwa_fused_kernel(const bf16* __res
       float v[16];
 #pragma unroll
       for (int u = 0; u < 16; ++u) v[u] = oacc[ob][ib][u];
+      if (residual && tail) {   // residual stream with an int8 tail (common.h), in place
+        float mv[16];
+        tail_decode16(load8(mres + off), load8(mres + off + 8), load_tail16(tail + off), mv);
+#pragma unroll
+        for (int u = 0; u < 16; ++u) v[u] += mv[u];
+        tail_store16(out + off, tail + off, v);
+        continue;
+      }
       if (residual) {
         const bf16x8 r0 = load8(mres + off), r1 = load8(mres + off + 8);
 #pragma unroll
@@ -435,9 +443,9 @@ extern "C" size_t bioemu_pwa_workspace_bytes(int64_t B, int64_t S, int64_t N, in
 
 extern "C" int bioemu_pwa_fwd(const void* m, const void* z, const uint8_t* mask, const float* norm_m_w,
                               const float* norm_m_b, const void* w_m, const void* w_g, const float* norm_z_w,
-                              const float* norm_z_b, const void* w_z, const void* w_o, void* out, void* workspace,
-                              size_t workspace_bytes, int64_t B, int64_t S, int64_t N, int64_t c_m, int64_t c_z,
-                              int64_t c_h, int64_t H, int residual, hipStream_t stream) {
+                              const float* norm_z_b, const void* w_z, const void* w_o, void* out, int8_t* res_tail,
+                              void* workspace, size_t workspace_bytes, int64_t B, int64_t S, int64_t N, int64_t c_m,
+                              int64_t c_z, int64_t c_h, int64_t H, int residual, hipStream_t stream) {
   if (c_m != CM || c_z != CZ || c_h != CH || H != NH)
     return set_error(BIOEMU_ERR_UNSUPPORTED,
                      "pwa: only c_m=64, c_z=128, c_h=32, 8 heads are supported (got %lld, %lld, %lld, %lld)",
@@ -451,6 +459,8 @@ extern "C" int bioemu_pwa_fwd(const void* m, const void* z, const uint8_t* mask,
       !aligned16(w_o) || !aligned16(workspace))
     return set_error(BIOEMU_ERR_INVALID_ARG, "pwa: tensors and workspace must be 16-byte aligned");
   if (out == m && !residual) return set_error(BIOEMU_ERR_INVALID_ARG, "pwa: out may alias m only with residual=1");
+  if (res_tail && (!residual || !aligned16(res_tail)))
+    return set_error(BIOEMU_ERR_INVALID_ARG, "pwa: res_tail needs residual=1 and 16-byte alignment");
   const PwaLayout L = pwa_layout(B, S, N);
   if (workspace_bytes < L.total)
     return set_error(BIOEMU_ERR_WORKSPACE, "pwa: workspace %zu < required %zu", workspace_bytes, L.total);
@@ -506,8 +516,8 @@ extern "C" int bioemu_pwa_fwd(const void* m, const void* z, const uint8_t* mask,
     if (grid > 0x7fffffffLL) return set_error(BIOEMU_ERR_INVALID_ARG, "pwa: too many work items");
     KernelTimerScope timed("pwa_fused", stream);
     hipLaunchKernelGGL(pwa_fused_kernel, dim3((unsigned)grid), dim3(kFuThreads), kFuSmem, stream, wbuf, vt, gbuf,
-                       static_cast<const bf16*>(w_o), static_cast<const bf16*>(m), static_cast<bf16*>(out), (int)S,
-                       S8, (int)N, Np, residual, (int)items);
+                       static_cast<const bf16*>(w_o), static_cast<const bf16*>(m), static_cast<bf16*>(out), res_tail,
+                       (int)S, S8, (int)N, Np, residual, (int)items);
   }
-  return 0;
+  return check_launch("pwa_fused");
 }

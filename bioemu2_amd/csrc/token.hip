@@ -97,8 +97,8 @@ __global__ __launch_bounds__(64 * kSplitK) void token_gemm_kernel(const bf16* __
                                                                   const bf16* __restrict__ W,
                                                                   const bf16* __restrict__ W2,
                                                                   const float* __restrict__ col_bias,
-                                                                  const bf16* res, bf16* out, int M, int K, int Nout,
-                                                                  int N, int Np, int out_rows) {
+                                                                  const bf16* res, bf16* out, int8_t* tail, int M,
+                                                                  int K, int Nout, int N, int Np, int out_rows) {
   constexpr int kAccs = kEpi == kEpiSwiGLU ? 2 : 1;
   __shared__ float part[kSplitK - 1][kAccs][16][64];   // partial sums of waves 1..3, lane-contiguous
   const int lane = threadIdx.x & 63, wave = wave_id();
@@ -165,6 +165,15 @@ __global__ __launch_bounds__(64 * kSplitK) void token_gemm_kernel(const bf16* __
 #pragma unroll
       for (int u = 0; u < 16; ++u) v[u] += col_bias[c0 + u];
     }
+    if (kEpi == kEpiResidual && tail) {   // residual stream with an int8 tail (common.h), in place
+      float rv[16];
+      tail_decode16(load8(res + orow * Nout + c0), load8(res + orow * Nout + c0 + 8),
+                    load_tail16(tail + orow * Nout + c0), rv);
+#pragma unroll
+      for (int u = 0; u < 16; ++u) v[u] += rv[u];
+      tail_store16(out + orow * Nout + c0, tail + orow * Nout + c0, v);
+      return;
+    }
     if (kEpi == kEpiResidual) {
       const bf16x8 r0 = load8(res + orow * Nout + c0), r1 = load8(res + orow * Nout + c0 + 8);
 #pragma unroll
@@ -185,15 +194,15 @@ __global__ __launch_bounds__(64 * kSplitK) void token_gemm_kernel(const bf16* __
 
 template <int kEpi, bool kTrans>
 int launch_gemm(const void* A, const void* W, const void* W2, const float* col_bias, const void* res, void* out,
-                int64_t M, int64_t K, int64_t Nout, int64_t N, int64_t Np, int64_t out_rows, hipStream_t stream,
-                const char* name) {
+                int8_t* tail, int64_t M, int64_t K, int64_t Nout, int64_t N, int64_t Np, int64_t out_rows,
+                hipStream_t stream, const char* name) {
   const int64_t blocks = ((M + 31) / 32) * (Nout / 32);
   const int64_t per_wg = K >= kSplitMinK ? 1 : kSplitK;   // blocks per workgroup
   KernelTimerScope timed(name, stream);
   hipLaunchKernelGGL((token_gemm_kernel<kEpi, kTrans>), dim3((unsigned)((blocks + per_wg - 1) / per_wg)),
                      dim3(64 * kSplitK), 0, stream,
                      static_cast<const bf16*>(A), static_cast<const bf16*>(W), static_cast<const bf16*>(W2),
-                     col_bias, static_cast<const bf16*>(res), static_cast<bf16*>(out), (int)M, (int)K, (int)Nout,
+                     col_bias, static_cast<const bf16*>(res), static_cast<bf16*>(out), tail, (int)M, (int)K, (int)Nout,
                      (int)N, (int)Np, (int)out_rows);
   return check_launch(name);
 }
@@ -226,23 +235,25 @@ int token_layernorm(const void* x, const float* gamma, const float* beta, void* 
 
 int token_gemm(int epi, bool trans, const void* A, const void* W, const void* W2, const float* col_bias,
                const void* res, void* out, int64_t M, int64_t K, int64_t Nout, int64_t N, int64_t Np,
-               int64_t out_rows, hipStream_t stream, const char* name) {
+               int64_t out_rows, hipStream_t stream, const char* name, int8_t* tail) {
   if (M <= 0 || K <= 0 || K % 16 || Nout <= 0 || Nout % 32 || Np % 32 || M % Np)
     return set_error(BIOEMU_ERR_INVALID_ARG, "%s: bad GEMM shape M=%lld K=%lld Nout=%lld Np=%lld", name,
                      (long long)M, (long long)K, (long long)Nout, (long long)Np);
+  if (tail && (epi != kEpiResidual || trans))
+    return set_error(BIOEMU_ERR_INVALID_ARG, "%s: a residual tail needs the residual epilogue", name);
   if (trans) {
     if (epi != kEpiStore) return set_error(BIOEMU_ERR_INVALID_ARG, "%s: transposed GEMM stores plainly", name);
-    return launch_gemm<kEpiStore, true>(A, W, W2, col_bias, res, out, M, K, Nout, N, Np, out_rows, stream, name);
+    return launch_gemm<kEpiStore, true>(A, W, W2, col_bias, res, out, tail, M, K, Nout, N, Np, out_rows, stream, name);
   }
   switch (epi) {
     case kEpiStore:
-      return launch_gemm<kEpiStore, false>(A, W, W2, col_bias, res, out, M, K, Nout, N, Np, out_rows, stream, name);
+      return launch_gemm<kEpiStore, false>(A, W, W2, col_bias, res, out, tail, M, K, Nout, N, Np, out_rows, stream, name);
     case kEpiSigmoid:
-      return launch_gemm<kEpiSigmoid, false>(A, W, W2, col_bias, res, out, M, K, Nout, N, Np, out_rows, stream, name);
+      return launch_gemm<kEpiSigmoid, false>(A, W, W2, col_bias, res, out, tail, M, K, Nout, N, Np, out_rows, stream, name);
     case kEpiSwiGLU:
-      return launch_gemm<kEpiSwiGLU, false>(A, W, W2, col_bias, res, out, M, K, Nout, N, Np, out_rows, stream, name);
+      return launch_gemm<kEpiSwiGLU, false>(A, W, W2, col_bias, res, out, tail, M, K, Nout, N, Np, out_rows, stream, name);
     case kEpiResidual:
-      return launch_gemm<kEpiResidual, false>(A, W, W2, col_bias, res, out, M, K, Nout, N, Np, out_rows, stream, name);
+      return launch_gemm<kEpiResidual, false>(A, W, W2, col_bias, res, out, tail, M, K, Nout, N, Np, out_rows, stream, name);
     default:
       return set_error(BIOEMU_ERR_INVALID_ARG, "%s: unknown epilogue %d", name, epi);
   }
@@ -263,8 +274,9 @@ extern "C" size_t bioemu_transition_token_workspace_bytes(int64_t M, int64_t Dc,
 
 extern "C" int bioemu_transition_token_fwd(const void* x, const float* norm_w, const float* norm_b,
                                            const void* fc1_w, const void* fc2_w, const void* fc3_w, void* out,
-                                           void* workspace, size_t workspace_bytes, int64_t M, int64_t Dc,
-                                           int64_t hidden, int use_norm, int residual, hipStream_t stream) {
+                                           int8_t* res_tail, void* workspace, size_t workspace_bytes, int64_t M,
+                                           int64_t Dc, int64_t hidden, int use_norm, int residual,
+                                           hipStream_t stream) {
   if (M <= 0 || (Dc != 64 && Dc != 128 && Dc != 384) || hidden <= 0 || hidden % 32)
     return set_error(BIOEMU_ERR_UNSUPPORTED, "transition_token: dim %lld / hidden %lld unsupported", (long long)Dc,
                      (long long)hidden);
@@ -275,6 +287,8 @@ extern "C" int bioemu_transition_token_fwd(const void* x, const float* norm_w, c
     return set_error(BIOEMU_ERR_INVALID_ARG, "transition_token: tensors must be 16-byte aligned");
   if (out == x && !residual)
     return set_error(BIOEMU_ERR_INVALID_ARG, "transition_token: out may alias x only with residual=1");
+  if (res_tail && (!residual || !aligned16(res_tail)))
+    return set_error(BIOEMU_ERR_INVALID_ARG, "transition_token: res_tail needs residual=1 and 16-byte alignment");
   if (workspace_bytes < bioemu_transition_token_workspace_bytes(M, Dc, hidden))
     return set_error(BIOEMU_ERR_WORKSPACE, "transition_token: workspace too small");
   // Rows are treated as one batch of M tokens padded to Mp.
@@ -288,5 +302,5 @@ extern "C" int bioemu_transition_token_fwd(const void* x, const float* norm_w, c
                   "transition_token_swiglu");
   if (rc) return rc;
   return token_gemm(residual ? kEpiResidual : kEpiStore, false, hbuf, fc3_w, nullptr, nullptr, x, out, Mp, hidden,
-                    Dc, M, Mp, M, stream, "transition_token_out");
+                    Dc, M, Mp, M, stream, "transition_token_out", res_tail);
 }

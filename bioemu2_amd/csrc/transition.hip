@@ -73,10 +73,12 @@ __device__ __forceinline__ void copy4_to_lds(__amdgpu_buffer_rsrc_t r, const bf1
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(lds), 4, voff, soff, 0, 0);
 }
 
-template <int C, int HIDDEN>
+// With kTail the residual stream x carries an int8 tail plane (common.h),
+// read with x and rewritten with out (in place).
+template <int C, int HIDDEN, bool kTail>
 __global__ __launch_bounds__(kThreads) void transition_rows_kernel(
     const bf16* x, const bf16* __restrict__ w1, const bf16* __restrict__ w2, const bf16* __restrict__ w3,
-    const bf16* __restrict__ cf, bf16* out, long long P, int use_norm, int residual) {
+    const bf16* __restrict__ cf, bf16* out, int8_t* tail, long long P, int use_norm, int residual) {
   using G = Geo<C, HIDDEN>;
   constexpr int HID = G::HID, KS = G::KS;
   extern __shared__ __attribute__((aligned(16))) char smem_raw[];
@@ -203,6 +205,14 @@ __global__ __launch_bounds__(kThreads) void transition_rows_kernel(
     float v[16];
 #pragma unroll
     for (int u = 0; u < 16; ++u) v[u] = acc[cb][u];
+    if (kTail) {
+      float xv[16];
+      tail_decode16(load8(x + off), load8(x + off + 8), load_tail16(tail + off), xv);
+#pragma unroll
+      for (int u = 0; u < 16; ++u) v[u] += xv[u];
+      tail_store16(out + off, tail + off, v);
+      continue;
+    }
     if (residual) {
       const bf16x8 q0 = load8(x + off), q1 = load8(x + off + 8);
 #pragma unroll
@@ -217,8 +227,8 @@ __global__ __launch_bounds__(kThreads) void transition_rows_kernel(
 
 template <int C, int HIDDEN>
 int launch_rows(const bf16* x, const bf16* w1, const bf16* w2, const bf16* w3, const bf16* cf, bf16* out,
-                long long P, int use_norm, int residual, hipStream_t stream) {
-  auto* kern = transition_rows_kernel<C, HIDDEN>;
+                int8_t* tail, long long P, int use_norm, int residual, hipStream_t stream) {
+  auto* kern = tail ? transition_rows_kernel<C, HIDDEN, true> : transition_rows_kernel<C, HIDDEN, false>;
   constexpr int smem = Geo<C, HIDDEN>::Smem;
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, smem) !=
       hipSuccess)
@@ -226,8 +236,8 @@ int launch_rows(const bf16* x, const bf16* w1, const bf16* w2, const bf16* w3, c
   const long long nwg = (P + kRowsPerWg - 1) / kRowsPerWg;
   if (nwg > 0x7fffffffLL) return set_error(BIOEMU_ERR_INVALID_ARG, "transition_pair: too many rows");
   KernelTimerScope timed(C == 128 ? "transition_pair" : "transition_msa", stream);
-  hipLaunchKernelGGL(kern, dim3((unsigned)nwg), dim3(kThreads), smem, stream, x, w1, w2, w3, cf, out, P, use_norm,
-                     residual);
+  hipLaunchKernelGGL(kern, dim3((unsigned)nwg), dim3(kThreads), smem, stream, x, w1, w2, w3, cf, out, tail, P,
+                     use_norm, residual);
   return check_launch("transition_pair");
 }
 
@@ -247,14 +257,16 @@ extern "C" size_t bioemu_transition_pair_workspace_bytes(int64_t Dc, int64_t hid
 
 extern "C" int bioemu_transition_pair_fwd(const void* x, const float* norm_w, const float* norm_b,
                                           const void* fc1_w, const void* fc2_w, const void* fc3_w,
-                                          void* out, void* workspace, size_t workspace_bytes, int64_t P,
-                                          int64_t Dc, int64_t hidden, int use_norm, int residual,
+                                          void* out, int8_t* res_tail, void* workspace, size_t workspace_bytes,
+                                          int64_t P, int64_t Dc, int64_t hidden, int use_norm, int residual,
                                           hipStream_t stream) {
   if (!supported(Dc, hidden))
     return set_error(BIOEMU_ERR_UNSUPPORTED,
                      "transition_pair: dim must be 64 or 128 with hidden 4*dim or 2*dim (got %lld, %lld)",
                      (long long)Dc, (long long)hidden);
   if (P <= 0) return set_error(BIOEMU_ERR_INVALID_ARG, "transition_pair: bad row count %lld", (long long)P);
+  if (res_tail && (!residual || !aligned16(res_tail)))
+    return set_error(BIOEMU_ERR_INVALID_ARG, "transition_pair: res_tail needs residual=1 and 16-byte alignment");
   if (!x || !fc1_w || !fc2_w || !fc3_w || !out || !workspace || (use_norm && (!norm_w || !norm_b)))
     return set_error(BIOEMU_ERR_INVALID_ARG, "transition_pair: null pointer argument");
   if (!aligned16(x) || !aligned16(out) || !aligned16(fc1_w) || !aligned16(fc2_w) || !aligned16(fc3_w) ||
@@ -284,8 +296,8 @@ extern "C" int bioemu_transition_pair_fwd(const void* x, const float* norm_w, co
   bf16* ob = static_cast<bf16*>(out);
   const long long rows = (long long)P;
   if (Dc == 128)
-    return hidden == 512 ? launch_rows<128, 512>(xb, w1, w2, w3, cf, ob, rows, use_norm, residual, stream)
-                         : launch_rows<128, 256>(xb, w1, w2, w3, cf, ob, rows, use_norm, residual, stream);
-  return hidden == 256 ? launch_rows<64, 256>(xb, w1, w2, w3, cf, ob, rows, use_norm, residual, stream)
-                       : launch_rows<64, 128>(xb, w1, w2, w3, cf, ob, rows, use_norm, residual, stream);
+    return hidden == 512 ? launch_rows<128, 512>(xb, w1, w2, w3, cf, ob, res_tail, rows, use_norm, residual, stream)
+                         : launch_rows<128, 256>(xb, w1, w2, w3, cf, ob, res_tail, rows, use_norm, residual, stream);
+  return hidden == 256 ? launch_rows<64, 256>(xb, w1, w2, w3, cf, ob, res_tail, rows, use_norm, residual, stream)
+                       : launch_rows<64, 128>(xb, w1, w2, w3, cf, ob, res_tail, rows, use_norm, residual, stream);
 }

@@ -243,9 +243,11 @@ constexpr float kSlackSum = 65536.0f;   // 2^16: a block sum above this may hold
 
 __device__ __forceinline__ int t_off(int r, int chunk) { return r * TLD + ((chunk ^ ((r >> 2) & 3)) << 3); }
 
-template <bool kStarting>
+// With kTail the residual stream z carries an int8 tail plane (common.h),
+// read with z and rewritten with out (in place).
+template <bool kStarting, bool kTail>
 __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
-    TriAttBuffers buf, const bf16* __restrict__ wo, const bf16* zres, bf16* out, int N, int Np,
+    TriAttBuffers buf, const bf16* __restrict__ wo, const bf16* zres, bf16* out, int8_t* tail, int N, int Np,
     int residual, int nitems) {
   __shared__ __attribute__((aligned(16))) bf16 smem[2 * kStage];
   extern __shared__ __attribute__((aligned(16))) bf16 kadd[];   // [Np] additive key mask
@@ -513,6 +515,14 @@ __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
         float v[16];
 #pragma unroll
         for (int u = 0; u < 16; ++u) v[u] = acc[u];
+        if (kTail) {
+          float zv[16];
+          tail_decode16(load8(zres + off), load8(zres + off + 8), load_tail16(tail + off), zv);
+#pragma unroll
+          for (int u = 0; u < 16; ++u) v[u] += zv[u];
+          tail_store16(out + off, tail + off, v);
+          continue;
+        }
         if (residual) {
           const bf16x8 r0 = load8(zres + off), r1 = load8(zres + off + 8);
 #pragma unroll
@@ -545,12 +555,14 @@ extern "C" size_t bioemu_triatt_workspace_bytes(int64_t B, int64_t N, int64_t Dc
 
 extern "C" int bioemu_triatt_fwd(const void* z, const uint8_t* mask, const float* norm_w,
                                  const float* norm_b, const void* w_proj, const void* w_o, void* out,
-                                 void* workspace, size_t workspace_bytes, int64_t B, int64_t N,
+                                 int8_t* res_tail, void* workspace, size_t workspace_bytes, int64_t B, int64_t N,
                                  int64_t Dc, int64_t Hc, int starting, int residual,
                                  hipStream_t stream) {
   if (Dc != C || Hc != H)
     return set_error(BIOEMU_ERR_UNSUPPORTED, "triatt: only c=128 with 4 heads of 32 is supported (got c=%lld H=%lld)",
                      (long long)Dc, (long long)Hc);
+  if (res_tail && (!residual || !aligned16(res_tail)))
+    return set_error(BIOEMU_ERR_INVALID_ARG, "triatt: res_tail needs residual=1 and 16-byte alignment");
   if (B <= 0 || N <= 0 || B > 65535 || N > 16384)
     return set_error(BIOEMU_ERR_INVALID_ARG, "triatt: bad shape B=%lld N=%lld", (long long)B, (long long)N);
   if (!z || !mask || !norm_w || !norm_b || !w_proj || !w_o || !out || !workspace)
@@ -609,22 +621,18 @@ extern "C" int bioemu_triatt_fwd(const void* z, const uint8_t* mask, const float
 
   const long long nitems = (long long)B * N * ((Np + kFlashQueries - 1) / kFlashQueries);
   const size_t flash_smem = (size_t)Np * 2;   // additive key mask row
-  const void* kflash = starting ? reinterpret_cast<const void*>(triatt_flash_kernel<true>)
-                                : reinterpret_cast<const void*>(triatt_flash_kernel<false>);
-  if (hipFuncSetAttribute(kflash, hipFuncAttributeMaxDynamicSharedMemorySize, (int)flash_smem) != hipSuccess)
+  auto* kflash = starting ? (res_tail ? triatt_flash_kernel<true, true> : triatt_flash_kernel<true, false>)
+                          : (res_tail ? triatt_flash_kernel<false, true> : triatt_flash_kernel<false, false>);
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(kflash), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)flash_smem) != hipSuccess)
     return set_error(BIOEMU_ERR_LAUNCH, "triatt_flash: cannot set dynamic LDS size");
   const long long grid2 = (nitems + 7) / 8 * 8;
   if (grid2 > 0x7fffffffLL) return set_error(BIOEMU_ERR_INVALID_ARG, "triatt: too many work items");
   {
     KernelTimerScope timed("triatt_flash", stream);
-    if (starting)
-      hipLaunchKernelGGL(triatt_flash_kernel<true>, dim3((unsigned)grid2), dim3(kFlashThreads), flash_smem, stream, buf,
-                         static_cast<const bf16*>(w_o), static_cast<const bf16*>(z), static_cast<bf16*>(out),
-                         (int)N, (int)Np, residual, (int)nitems);
-    else
-      hipLaunchKernelGGL(triatt_flash_kernel<false>, dim3((unsigned)grid2), dim3(kFlashThreads), flash_smem, stream, buf,
-                         static_cast<const bf16*>(w_o), static_cast<const bf16*>(z), static_cast<bf16*>(out),
-                         (int)N, (int)Np, residual, (int)nitems);
+    hipLaunchKernelGGL(kflash, dim3((unsigned)grid2), dim3(kFlashThreads), flash_smem, stream, buf,
+                       static_cast<const bf16*>(w_o), static_cast<const bf16*>(z), static_cast<bf16*>(out), res_tail,
+                       (int)N, (int)Np, residual, (int)nitems);
   }
   return check_launch("triatt_flash");
 }

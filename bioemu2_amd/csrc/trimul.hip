@@ -9,7 +9,7 @@
 //                       (the incoming direction writes the transposed frame).
 //   2. bgemm_nt       : o[d][i][j] = sum_k a[d][i][k] * b[d][j][k]   (MFMA, fp32 acc)
 //   3. trimul_out     : LN_out(o) -> p_out, LN_in(x) -> g_out, out = p*sigmoid(g) (+x)
-// Padded planes (Np = N rounded up to 128) are zero in every padded row and
+// Padded planes (Np = N rounded up to the 256 contraction tile) are zero in every padded row and
 // column, so the contraction needs no edge handling and padding never changes
 // a valid output bit.
 #include <algorithm>
@@ -222,9 +222,12 @@ __device__ __forceinline__ int obuf_off(int c, int j) { return c * 32 + j + ((c 
 // 16 KB) instead of skipping the store: a conditional store would hide the
 // number of stores from the compiler's wait counting, which would then wait
 // for the stores before the next tile's data.
+// With kTail the residual stream also has an int8 tail plane (common.h):
+// x + tail is read, and the sum is written back as out + tail (in place).
+template <bool kTail>
 __global__ __launch_bounds__(kOutThreads) void trimul_out_kernel(
     const bf16* __restrict__ o, const bf16* x, const bf16* __restrict__ wfold, const float* __restrict__ cfold,
-    bf16* out, bf16* __restrict__ discard, int B, int N, int Np, int residual) {
+    bf16* out, int8_t* tail, bf16* __restrict__ discard, int B, int N, int Np, int residual) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   bf16* wl = reinterpret_cast<bf16*>(smem);
   float* cl = reinterpret_cast<float*>(smem + 2 * D * kLdw * 2);
@@ -250,6 +253,7 @@ __global__ __launch_bounds__(kOutThreads) void trimul_out_kernel(
   // 16 q + (lane >> 2), columns j0 + 8 (lane & 3) .. + 7.  Columns of the last
   // tile of a row may reach past N but stay below Np (o is Np wide).
   bf16x8 xraw[8], oraw[8];
+  u32x4 traw[4];
   auto fetch = [&](unsigned tt) {
     const TileIdx ti = split_tile(tt, tiles_per_row, N);
     const int i = ti.row, b = ti.b, j0 = ti.col * 32;
@@ -258,12 +262,21 @@ __global__ __launch_bounds__(kOutThreads) void trimul_out_kernel(
     const bf16* xr = x + pair * D + 64 * h;
 #pragma unroll
     for (int s = 0; s < 8; ++s) xraw[s] = load8(xr + 8 * s);
+    if (kTail) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) traw[q] = load_tail16(tail + pair * D + 64 * h + 16 * q);
+    }
     const bf16* orow = o + ((size_t)b * D + (lane >> 2)) * plane + (size_t)i * Np + j0 + 8 * (lane & 3);
 #pragma unroll
     for (int q = 0; q < 8; ++q) oraw[q] = load8(orow + (size_t)(16 * q) * plane);
   };
   // Current tile's operands: normalised o and x rows and the raw x half-row.
+  // With kTail, the current tile's tail bytes wait in the first 4 KB of the
+  // wave's o buffer once o has been read from it (registers are full): chunk
+  // q of lane l at 16-byte slot 64 q + l, so each access instruction covers
+  // 1 KB contiguously.
   bf16x8 of[8], xf[8], xres[8];
+  u32x4* tbuf = reinterpret_cast<u32x4*>(ob);
   auto prepare = [&]() {
 #pragma unroll
     for (int q = 0; q < 8; ++q) store8(ob + obuf_off(16 * q + (lane >> 2), 8 * (lane & 3)), oraw[q]);
@@ -271,6 +284,10 @@ __global__ __launch_bounds__(kOutThreads) void trimul_out_kernel(
     const int p = perm32(rho);
 #pragma unroll
     for (int c = 0; c < 64; ++c) v[c] = bf2f(ob[obuf_off(64 * h + c, p)]);
+    if (kTail) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) tbuf[64 * q + lane] = traw[q];
+    }
     normalize_half_row(v, of);
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
@@ -300,6 +317,16 @@ __global__ __launch_bounds__(kOutThreads) void trimul_out_kernel(
       float r[16];
 #pragma unroll
       for (int u = 0; u < 16; ++u) r[u] = (pa[u] + cl[e0 + u]) * sigmoidf_fast(ga[u] + cl[D + e0 + u]);
+      if (kTail) {
+        float xv[16];
+        tail_decode16(xres[2 * cb], xres[2 * cb + 1], tbuf[64 * cb + lane], xv);
+#pragma unroll
+        for (int u = 0; u < 16; ++u) r[u] += xv[u];
+        int8_t* tdiscard = reinterpret_cast<int8_t*>(discard + 64 * D);
+        tail_store16(valid ? out + pair * D + e0 : discard + lane * D + e0,
+                     valid ? tail + pair * D + e0 : tdiscard + lane * D + e0, r);
+        continue;
+      }
       if (residual) {
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
@@ -329,10 +356,12 @@ extern "C" size_t bioemu_trimul_workspace_bytes(int64_t B, int64_t N, int64_t Dc
 extern "C" int bioemu_trimul_fwd(const void* x, const uint8_t* mask, const float* norm_in_w,
                                  const float* norm_in_b, const void* p_in_w, const void* g_in_w,
                                  const float* norm_out_w, const float* norm_out_b,
-                                 const void* p_out_w, const void* g_out_w, void* out,
+                                 const void* p_out_w, const void* g_out_w, void* out, int8_t* res_tail,
                                  void* workspace, size_t workspace_bytes, int64_t B, int64_t N,
                                  int64_t Dc, int outgoing, int residual, hipStream_t stream) {
   if (Dc != D) return set_error(BIOEMU_ERR_UNSUPPORTED, "trimul: channel dim %lld unsupported (must be 128)", (long long)Dc);
+  if (res_tail && (!residual || !aligned16(res_tail)))
+    return set_error(BIOEMU_ERR_INVALID_ARG, "trimul: res_tail needs residual=1 and 16-byte alignment");
   if (B <= 0 || N <= 0 || B > 65535 || N > 16384)
     return set_error(BIOEMU_ERR_INVALID_ARG, "trimul: bad shape B=%lld N=%lld", (long long)B, (long long)N);
   if (!x || !mask || !norm_in_w || !norm_in_b || !p_in_w || !g_in_w || !norm_out_w || !norm_out_b ||
@@ -362,9 +391,10 @@ extern "C" int bioemu_trimul_fwd(const void* x, const uint8_t* mask, const float
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
   const void* kin = outgoing ? reinterpret_cast<const void*>(trimul_proj_in_kernel<true>)
                              : reinterpret_cast<const void*>(trimul_proj_in_kernel<false>);
+  const void* kout = res_tail ? reinterpret_cast<const void*>(trimul_out_kernel<true>)
+                              : reinterpret_cast<const void*>(trimul_out_kernel<false>);
   if (hipFuncSetAttribute(kin, hipFuncAttributeMaxDynamicSharedMemorySize, kInSmem) != hipSuccess ||
-      hipFuncSetAttribute(reinterpret_cast<const void*>(trimul_out_kernel),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, kOutSmem) != hipSuccess)
+      hipFuncSetAttribute(kout, hipFuncAttributeMaxDynamicSharedMemorySize, kOutSmem) != hipSuccess)
     return set_error(BIOEMU_ERR_LAUNCH, "trimul: cannot set dynamic LDS size");
   const long long waves_in = (long long)B * Np * (Np / 32);
   if (waves_in >= kMaxTiles) return set_error(BIOEMU_ERR_INVALID_ARG, "trimul: too many pair tiles");
@@ -396,10 +426,16 @@ extern "C" int bioemu_trimul_fwd(const void* x, const uint8_t* mask, const float
   const long long waves_out = (long long)B * N * ((N + 31) / 32);
   const unsigned grid3 = (unsigned)std::min<long long>(cus, (waves_out + kOutWaves - 1) / kOutWaves);
   KernelTimerScope timed("trimul_out", stream);
-  // The a/b planes are dead once the contraction has run: their first 16 KB
-  // take the discarded stores of pair slots past N.
-  hipLaunchKernelGGL(trimul_out_kernel, dim3(grid3), dim3(kOutThreads), kOutSmem, stream, ob,
-                     static_cast<const bf16*>(x), wfold, cfold, static_cast<bf16*>(out), ab, (int)B, (int)N, (int)Np,
-                     residual);
+  // The a/b planes are dead once the contraction has run: their first 24 KB
+  // take the discarded stores (bf16 values, then tail bytes) of pair slots
+  // past N.
+  if (res_tail)
+    hipLaunchKernelGGL(trimul_out_kernel<true>, dim3(grid3), dim3(kOutThreads), kOutSmem, stream, ob,
+                       static_cast<const bf16*>(x), wfold, cfold, static_cast<bf16*>(out), res_tail, ab, (int)B,
+                       (int)N, (int)Np, residual);
+  else
+    hipLaunchKernelGGL(trimul_out_kernel<false>, dim3(grid3), dim3(kOutThreads), kOutSmem, stream, ob,
+                       static_cast<const bf16*>(x), wfold, cfold, static_cast<bf16*>(out), nullptr, ab, (int)B,
+                       (int)N, (int)Np, residual);
   return check_launch("trimul_out");
 }

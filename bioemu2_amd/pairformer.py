@@ -11,10 +11,18 @@ reference ops plus triangle attention:
 
 with ``pm = mask_i & mask_j`` (pairmixer.py:263-264) and the residual form of
 ``PairMixerLayer.forward`` (pairmixer.py:446-456; dropout is the identity at
-inference, biomoa/ops/dropout.py:58-70).  ``forward_`` updates ``s`` and ``z``
-in place: every residual add is fused into the producing kernel and all ops
-share one preallocated workspace, so a block allocates nothing after the
-first call at a given shape.
+inference, biomoa/ops/dropout.py:58-70).
+
+Residual streams.  ``forward_`` updates bf16 ``s`` and ``z`` in place, with
+every residual add fused into the producing kernel.  Given int8 tail planes
+(``s_tail``, ``z_tail``; see ``include/bioemu2_mi355x.h``, "Residual tails"),
+the streams are carried at ~16 significant bits: each op adds its update to
+value + tail and writes back a bf16 value and a new tail, so a stack of ops
+rounds once, when the stream is joined, instead of after every add as the
+reference's bf16-autocast trunk does (bf16 z + bf16 update under autocast,
+pairmixer.py:446-456, model.py:216-223).  ``forward`` always carries tails:
+fp32 inputs are split into (bf16, tail) and the result joined back to fp32;
+bf16 inputs start with zero tails and the result is rounded once.
 """
 
 from __future__ import annotations
@@ -25,9 +33,16 @@ from torch import Tensor
 
 from . import _ops
 from .attention_pair_bias import AttentionPairBias
+from .residual import join_stream, split_stream
 from .transition import Transition
 from .triangle_attention import TriangleAttentionHip
 from .triangle_multiplication import TriangleMultiplicationHip
+
+
+def pair_masks(token_mask: Tensor) -> tuple[Tensor, Tensor]:
+    """(token mask, pair mask = mask_i & mask_j) as uint8 (pairmixer.py:263-264)."""
+    m = token_mask.bool()
+    return _ops.mask_u8(m), _ops.mask_u8(m[:, :, None] & m[:, None, :])
 
 
 class PairformerBlockHip(nn.Module):
@@ -50,8 +65,6 @@ class PairformerBlockHip(nn.Module):
         self.attention_pair_bias = AttentionPairBias(c_s, c_z, apb_heads, initial_norm=True)
         self.transition_s = Transition(c_s, transition_factor * c_s)
         self._ws: Tensor | None = None
-        self._mask_key: tuple | None = None
-        self._masks: tuple[Tensor, Tensor] | None = None
 
     def workspace_bytes(self, B: int, N: int) -> int:
         return max(
@@ -68,35 +81,81 @@ class PairformerBlockHip(nn.Module):
             self._ws = _ops.workspace(need, device)
         return self._ws
 
-    def _pair_masks(self, token_mask: Tensor) -> tuple[Tensor, Tensor]:
-        """(token mask, pair mask = mask_i & mask_j) as uint8, cached per mask tensor version."""
-        key = (token_mask.data_ptr(), token_mask._version, tuple(token_mask.shape), token_mask.device)
-        if key != self._mask_key or self._masks is None:
-            m = token_mask.bool()
-            self._masks = (_ops.mask_u8(m), _ops.mask_u8(m[:, :, None] & m[:, None, :]))
-            self._mask_key = key
-        return self._masks
-
     @torch.no_grad()
-    def forward_(self, s: Tensor, z: Tensor, token_mask: Tensor) -> tuple[Tensor, Tensor]:
-        """In-place block on bf16 ``s [B,N,c_s]``, ``z [B,N,N,c_z]``, ``token_mask [B,N]``."""
+    def forward_(
+        self,
+        s: Tensor,
+        z: Tensor,
+        token_mask: Tensor,
+        s_tail: Tensor | None = None,
+        z_tail: Tensor | None = None,
+        ws: Tensor | None = None,
+    ) -> tuple[Tensor, Tensor]:
+        """In-place block on bf16 ``s [B,N,c_s]``, ``z [B,N,N,c_z]``, ``token_mask [B,N]``.
+
+        ``s_tail`` / ``z_tail``: int8 tails of the residual streams (same shapes), updated in place;
+        ``None`` keeps that stream in plain bf16.  ``ws``: a caller-owned workspace of at least
+        ``workspace_bytes(B, N)`` bytes (default: one the block caches per shape).  The masks are
+        built from ``token_mask`` on every call.
+        """
         _ops.require_gpu(z, type(self).__name__)
         B, N = token_mask.shape
-        ws = self._workspace(B, N, z.device)
-        tok, pm = self._pair_masks(token_mask)
-        _ops.launch_trimul(z, pm, *self.tri_mul_out.prepared_params(), z, True, residual=True, ws=ws)
-        _ops.launch_trimul(z, pm, *self.tri_mul_in.prepared_params(), z, False, residual=True, ws=ws)
-        _ops.launch_triatt(z, pm, *self.tri_att_start.prepared_params(), z, True, residual=True, ws=ws)
-        _ops.launch_triatt(z, pm, *self.tri_att_end.prepared_params(), z, False, residual=True, ws=ws)
-        _ops.launch_transition_pair(z, *self.transition_z.prepared_params(), z, residual=True, ws=ws)
+        if ws is None:
+            ws = self._workspace(B, N, z.device)
+        tok, pm = pair_masks(token_mask)
+        _ops.launch_trimul(z, pm, *self.tri_mul_out.prepared_params(), z, True, residual=True, ws=ws, tail=z_tail)
+        _ops.launch_trimul(z, pm, *self.tri_mul_in.prepared_params(), z, False, residual=True, ws=ws, tail=z_tail)
+        _ops.launch_triatt(z, pm, *self.tri_att_start.prepared_params(), z, True, residual=True, ws=ws, tail=z_tail)
+        _ops.launch_triatt(z, pm, *self.tri_att_end.prepared_params(), z, False, residual=True, ws=ws, tail=z_tail)
+        _ops.launch_transition_pair(z, *self.transition_z.prepared_params(), z, residual=True, ws=ws, tail=z_tail)
         _ops.launch_apb(s, z, tok, *self.attention_pair_bias.prepared_params(), s, self.apb_heads,
-                        residual=True, ws=ws)
-        _ops.launch_transition_token(s, *self.transition_s.prepared_params(), s, residual=True, ws=ws)
+                        residual=True, ws=ws, tail=s_tail)
+        _ops.launch_transition_token(s, *self.transition_s.prepared_params(), s, residual=True, ws=ws,
+                                     tail=s_tail)
         return s, z
 
     def forward(self, s: Tensor, z: Tensor, token_mask: Tensor) -> tuple[Tensor, Tensor]:
-        """Out-of-place block: returns new ``(s, z)`` in the input dtypes."""
-        s2 = s.to(torch.bfloat16).contiguous().clone()
-        z2 = z.to(torch.bfloat16).contiguous().clone()
-        self.forward_(s2, z2, token_mask)
-        return s2.to(s.dtype), z2.to(z.dtype)
+        """Out-of-place block: returns new ``(s, z)`` in the input dtypes (streams carried with tails)."""
+        (s_hi, s_tail), (z_hi, z_tail) = split_stream(s), split_stream(z)
+        self.forward_(s_hi, z_hi, token_mask, s_tail, z_tail)
+        return join_stream(s_hi, s_tail, s.dtype), join_stream(z_hi, z_tail, z.dtype)
+
+    @torch.no_grad()
+    def capture(
+        self,
+        s: Tensor,
+        z: Tensor,
+        token_mask: Tensor,
+        s_tail: Tensor | None = None,
+        z_tail: Tensor | None = None,
+    ) -> "BlockGraph":
+        """Captures ``forward_`` on these exact buffers into a HIP graph (see ``BlockGraph``)."""
+        return BlockGraph(self, s, z, token_mask, s_tail, z_tail)
+
+
+class BlockGraph:
+    """A HIP graph of one in-place ``PairformerBlockHip.forward_`` on fixed buffers.
+
+    The graph owns its workspace and holds references to every tensor its
+    kernels read or write: the caller's ``s``, ``z``, tails and token mask, the
+    prepared weights of the moment of capture, and the masks built inside the
+    capture (graph-pool memory).  Eager calls of the block at other shapes or
+    masks therefore cannot free anything a replay touches.  ``replay()``
+    re-runs the block on the current contents of those buffers; later weight
+    updates are not seen (capture again after changing parameters).
+    """
+
+    def __init__(self, block: PairformerBlockHip, s, z, token_mask, s_tail=None, z_tail=None):
+        B, N = token_mask.shape
+        self.tensors = (s, z, token_mask, s_tail, z_tail)
+        self.ws = _ops.workspace(block.workspace_bytes(B, N), z.device)
+        # Prepare the weights outside the capture (their conversions allocate and copy).
+        mods = (block.tri_mul_out, block.tri_mul_in, block.tri_att_start, block.tri_att_end, block.transition_z,
+                block.attention_pair_bias, block.transition_s)
+        self.params = tuple(m.prepared_params() for m in mods)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            block.forward_(s, z, token_mask, s_tail, z_tail, ws=self.ws)
+
+    def replay(self) -> None:
+        self.graph.replay()

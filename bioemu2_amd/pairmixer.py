@@ -16,7 +16,9 @@ Mirrors ``src/bioemu2/biomoa/modules/pairmixer.py``:
 Inference only: dropout is the identity at eval (biomoa/ops/dropout.py:68-69),
 so the dropout rates are accepted and stored.  ``forward_`` updates the
 tensors in place: every residual add is fused into the producing kernel and
-all ops share one preallocated workspace.
+all ops share one preallocated workspace.  Optional int8 tails carry the
+residual streams z and m at ~16 significant bits (pairformer.py explains the
+format); ``forward`` always uses them and rounds each stream once.
 """
 
 from __future__ import annotations
@@ -29,12 +31,9 @@ from . import _ops
 from .outer_product_mean import REGISTRY as OPM_REGISTRY
 from .pair_weighted_averaging import PairWeightedAveraging
 from .strategy import make
+from .residual import join_stream, split_stream
 from .transition import Transition
 from .triangle_multiplication import REGISTRY as TRIMUL_REGISTRY
-
-
-def _bf16_inplace(t: Tensor) -> Tensor:
-    return t.to(torch.bfloat16).contiguous().clone()
 
 
 class _WorkspaceMixin:
@@ -72,21 +71,23 @@ class PairMixerLayerHip(nn.Module, _WorkspaceMixin):
                    _ops.transition_pair_workspace_bytes(self.token_z, self.transition_z.hidden))
 
     @torch.no_grad()
-    def forward_(self, s: Tensor, z: Tensor, pair_mask: Tensor) -> tuple[Tensor, Tensor]:
-        """In place on bf16 ``z [B,T,T,token_z]``; ``s`` passes through."""
+    def forward_(
+        self, s: Tensor, z: Tensor, pair_mask: Tensor, z_tail: Tensor | None = None
+    ) -> tuple[Tensor, Tensor]:
+        """In place on bf16 ``z [B,T,T,token_z]`` (and its int8 tail, if given); ``s`` passes through."""
         _ops.require_gpu(z, type(self).__name__)
         B, N = z.shape[0], z.shape[1]
         ws = self._workspace(self.workspace_bytes(B, N), z.device)
         pm = _ops.mask_u8(pair_mask)
-        _ops.launch_trimul(z, pm, *self.tri_mul_out.prepared_params(), z, True, residual=True, ws=ws)
-        _ops.launch_trimul(z, pm, *self.tri_mul_in.prepared_params(), z, False, residual=True, ws=ws)
-        _ops.launch_transition_pair(z, *self.transition_z.prepared_params(), z, residual=True, ws=ws)
+        _ops.launch_trimul(z, pm, *self.tri_mul_out.prepared_params(), z, True, residual=True, ws=ws, tail=z_tail)
+        _ops.launch_trimul(z, pm, *self.tri_mul_in.prepared_params(), z, False, residual=True, ws=ws, tail=z_tail)
+        _ops.launch_transition_pair(z, *self.transition_z.prepared_params(), z, residual=True, ws=ws, tail=z_tail)
         return s, z
 
     def forward(self, s: Tensor, z: Tensor, pair_mask: Tensor) -> tuple[Tensor, Tensor]:
-        z2 = _bf16_inplace(z)
-        self.forward_(s, z2, pair_mask)
-        return s, z2.to(z.dtype)
+        z_hi, z_tail = split_stream(z)
+        self.forward_(s, z_hi, pair_mask, z_tail)
+        return s, join_stream(z_hi, z_tail, z.dtype)
 
 
 class PairMixerMSALayerHip(nn.Module, _WorkspaceMixin):
@@ -131,25 +132,36 @@ class PairMixerMSALayerHip(nn.Module, _WorkspaceMixin):
 
     @torch.no_grad()
     def forward_(
-        self, s: Tensor, z: Tensor, m: Tensor, token_mask: Tensor, msa_mask: Tensor, chunk_heads_pwa: bool = False
+        self,
+        s: Tensor,
+        z: Tensor,
+        m: Tensor,
+        token_mask: Tensor,
+        msa_mask: Tensor,
+        chunk_heads_pwa: bool = False,
+        z_tail: Tensor | None = None,
+        m_tail: Tensor | None = None,
     ) -> tuple[Tensor, Tensor, Tensor]:
-        """In place on bf16 ``z [B,T,T,token_z]`` and ``m [B,S,T,msa_s]``; ``s`` passes through."""
+        """In place on bf16 ``z [B,T,T,token_z]`` and ``m [B,S,T,msa_s]`` (and their int8 tails, if given);
+        ``s`` passes through."""
         _ops.require_gpu(z, type(self).__name__)
         B, S, N = m.shape[0], m.shape[1], m.shape[2]
         ws = self._workspace(self.workspace_bytes(B, S, N), z.device)
         pm = _ops.mask_u8(token_mask)
-        _ops.launch_pwa(m, z, pm, *self.pair_weighted_averaging.prepared_params(), m, 8, residual=True, ws=ws)
-        _ops.launch_transition_pair(m, *self.msa_transition.prepared_params(), m, residual=True, ws=ws)
+        _ops.launch_pwa(m, z, pm, *self.pair_weighted_averaging.prepared_params(), m, 8, residual=True, ws=ws,
+                        tail=m_tail)
+        _ops.launch_transition_pair(m, *self.msa_transition.prepared_params(), m, residual=True, ws=ws, tail=m_tail)
         mask3, mean_rows = _ops.opm_mask3(msa_mask, B, S, N)
-        _ops.launch_opm(m, mask3, mean_rows, *self.outer_product_mean.prepared_params(), out=z, z_res=z, ws=ws)
-        _ops.launch_trimul(z, pm, *self.tri_mul_out.prepared_params(), z, True, residual=True, ws=ws)
-        _ops.launch_trimul(z, pm, *self.tri_mul_in.prepared_params(), z, False, residual=True, ws=ws)
-        _ops.launch_transition_pair(z, *self.z_transition.prepared_params(), z, residual=True, ws=ws)
+        _ops.launch_opm(m, mask3, mean_rows, *self.outer_product_mean.prepared_params(), out=z, z_res=z, ws=ws,
+                        tail=z_tail)
+        _ops.launch_trimul(z, pm, *self.tri_mul_out.prepared_params(), z, True, residual=True, ws=ws, tail=z_tail)
+        _ops.launch_trimul(z, pm, *self.tri_mul_in.prepared_params(), z, False, residual=True, ws=ws, tail=z_tail)
+        _ops.launch_transition_pair(z, *self.z_transition.prepared_params(), z, residual=True, ws=ws, tail=z_tail)
         return s, z, m
 
     def forward(
         self, s: Tensor, z: Tensor, m: Tensor, token_mask: Tensor, msa_mask: Tensor, chunk_heads_pwa: bool = False
     ) -> tuple[Tensor, Tensor, Tensor]:
-        z2, m2 = _bf16_inplace(z), _bf16_inplace(m)
-        self.forward_(s, z2, m2, token_mask, msa_mask, chunk_heads_pwa)
-        return s, z2.to(z.dtype), m2.to(m.dtype)
+        (z_hi, z_tail), (m_hi, m_tail) = split_stream(z), split_stream(m)
+        self.forward_(s, z_hi, m_hi, token_mask, msa_mask, chunk_heads_pwa, z_tail, m_tail)
+        return s, join_stream(z_hi, z_tail, z.dtype), join_stream(m_hi, m_tail, m.dtype)

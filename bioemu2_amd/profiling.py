@@ -10,20 +10,32 @@ WRITE_SIZE`` runs of ``bench.py --calibrate-bytes B`` into HBM bytes per launch
 for every kernel: each counter (KiB per dispatch) is scaled by what the same
 counter reads for torch's elementwise negation of a B-byte bf16 tensor, which
 moves exactly B bytes in and B bytes out.  The per-kernel figures are merged
-into ``profiles/traffic.json`` under the workload name, which ``bench.py``
-reports as ``roofline.traffic``.
+into ``profiles/traffic.json`` under the workload name, together with a hash
+of the kernel sources they were measured on; ``bench.py`` reports them as
+``roofline.traffic`` only while that hash matches the current sources.
 """
 
 from __future__ import annotations
 
 import argparse
 import csv
+import hashlib
 import json
 import re
 from collections import defaultdict
 from pathlib import Path
 
 TRAFFIC_JSON = Path(__file__).resolve().parents[1] / "profiles" / "traffic.json"
+CSRC = Path(__file__).resolve().parent / "csrc"
+
+
+def csrc_hash() -> str:
+    """First 16 hex digits of the SHA-256 of every kernel source (csrc/*.hip, csrc/*.h), in name order."""
+    h = hashlib.sha256()
+    for f in sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.h"))):
+        h.update(f.name.encode())
+        h.update(f.read_bytes())
+    return h.hexdigest()[:16]
 
 # Kernel-timer names whose kernel function is named differently.
 TIMER_TO_KERNEL = {"apb_pair_bias": "pair_bias", "token_layernorm": "token_ln",
@@ -141,6 +153,7 @@ def main(argv=None) -> int:
                  f"Calibration: torch's negation of a {a.calib_bytes} B bf16 tensor (reads and writes exactly that many "
                  f"bytes) read FETCH_SIZE {f_per_kib:.4f} KiB and WRITE_SIZE {w_per_kib:.4f} KiB per real KiB; "
                  "kernel counters below are divided by those factors.", "",
+                 f"Kernel sources: `csrc` SHA-256 prefix `{csrc_hash()}`.", "",
                  "| kernel | read MB | write MB | total MB |", "|---|---|---|---|"]
         for k, v in sorted(table.items(), key=lambda kv: -kv[1]["total"]):
             lines.append(f"| `{k}` | {v.get('read', 0) / 1e6:.1f} | {v.get('write', 0) / 1e6:.1f} | "
@@ -151,7 +164,7 @@ def main(argv=None) -> int:
             data = json.loads(path.read_text())
         except (OSError, ValueError):
             data = {}
-        data[a.workload] = {k: round(v["total"]) for k, v in table.items()}
+        data[a.workload] = {"csrc_sha16": csrc_hash(), "kernels": {k: round(v["total"]) for k, v in table.items()}}
         data.setdefault("_calibration", {})[a.workload] = {"fetch_kib_per_kib": round(f_per_kib, 5),
                                                            "write_kib_per_kib": round(w_per_kib, 5)}
         path.write_text(json.dumps(data, indent=1, sort_keys=True) + "\n")

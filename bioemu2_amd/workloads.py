@@ -25,12 +25,17 @@ _PROFILES = Path(__file__).resolve().parents[1] / "profiles" / "traffic.json"
 
 
 def measured_traffic(kernel: str, workload: str):
-    """HBM bytes per launch measured with rocprofv3 PMC counters, if recorded."""
+    """HBM bytes per launch measured with rocprofv3 PMC counters, if recorded on the current kernel sources
+    (None when absent or measured on other sources)."""
+    from .profiling import csrc_hash
+
     try:
-        table = json.loads(_PROFILES.read_text())
+        entry = json.loads(_PROFILES.read_text()).get(workload, {})
     except (OSError, ValueError):
         return None
-    return table.get(workload, {}).get(kernel)
+    if entry.get("csrc_sha16") != csrc_hash():
+        return None
+    return entry.get("kernels", {}).get(kernel)
 
 
 def token_mask(n: int, n_pad: int, device, batch: int = 1) -> Tensor:
@@ -198,23 +203,40 @@ class TriAttWorkload(Workload):
         return w
 
 
+def block_flops(n: int, c: int = 128, cs: int = 384) -> float:
+    """Algorithmic flops of one Pairformer block at N = n (B = 1)."""
+    P = n * n
+    trimul = 2.0 * P * c * 6 * c + 2.0 * c * n ** 3
+    triatt = 2.0 * P * c * (5 * c + 4) + 4.0 * n ** 3 * c
+    trans_z = 2.0 * P * c * 12 * c
+    apb = 2.0 * P * c * 16 + 2.0 * n * cs * 5 * cs + 4.0 * n * n * cs
+    trans_s = 2.0 * n * cs * 12 * cs
+    return 2 * trimul + 2 * triatt + trans_z + apb + trans_s
+
+
 class BlockWorkload(Workload):
-    """The BASELINE metric: one full bf16 Pairformer block at N=768 (config 4 + s [1,768,384])."""
+    """The BASELINE metric: one full bf16 Pairformer block at N=768 (config 4 + s [1,768,384]).
 
-    cpu_warmup = 0
-    cpu_calls = 1
+    With ``tails`` (the default) the residual streams z and s carry int8 tails, the path held to the
+    north_star bound against the fp32 oracle; without them they are plain bf16 (rounded after every add,
+    as the reference's bf16-autocast trunk stores them)."""
 
-    def __init__(self, device, n: int = 768, seed: int = 0):
+    cpu_warmup = 1
+    cpu_calls = 3
+
+    def __init__(self, device, n: int = 768, seed: int = 0, tails: bool = True):
         from .pairformer import PairformerBlockHip
 
         self.n = n
+        self.tails = tails
         # padded (masked) trailing tokens: 10 % at the BASELINE size (config 4,
         # 76 of 768), 5 % at the 48-block trunk size (config 5, 102 of 2048)
         self.n_pad = n // 20 if n >= 2048 else n // 10
-        self.name = f"pairformer_block_n{n}"
+        self.name = f"pairformer_block_n{n}" + ("" if tails else "_bf16stream")
         self.metric = f"ms per Pairformer block at N={n} bf16"
         self.config = {"workload": self.name, "N": n, "c_z": 128, "c_s": 384, "batch": 1,
-                       "triatt_heads": 4, "apb_heads": 16, "padded_tokens": self.n_pad}
+                       "triatt_heads": 4, "apb_heads": 16, "padded_tokens": self.n_pad,
+                       "residual_stream": "bf16 + int8 tail" if tails else "bf16"}
         torch.manual_seed(seed)
         self.module = init_module(PairformerBlockHip(), seed).to(device).eval()
         g = torch.Generator().manual_seed(seed)
@@ -222,19 +244,14 @@ class BlockWorkload(Workload):
         self.s_cpu = torch.randn(1, n, 384, generator=g).to(torch.bfloat16)
         self.z = self.z_cpu.to(device)
         self.s = self.s_cpu.to(device)
+        self.z_tail = torch.zeros(self.z.shape, dtype=torch.int8, device=device) if tails else None
+        self.s_tail = torch.zeros(self.s.shape, dtype=torch.int8, device=device) if tails else None
         self.tok = token_mask(n, self.n_pad, device)
-        self.module.forward_(self.s.clone(), self.z.clone(), self.tok)  # sizes the shared workspace
-        c, cs = 128, 384
-        P = n * n
-        trimul = 2.0 * P * c * 6 * c + 2.0 * c * n ** 3
-        triatt = 2.0 * P * c * (5 * c + 4) + 4.0 * n ** 3 * c
-        trans_z = 2.0 * P * c * 12 * c
-        apb = 2.0 * P * c * 16 + 2.0 * n * cs * 5 * cs + 4.0 * n * n * cs
-        trans_s = 2.0 * n * cs * 12 * cs
-        self.flops = 2 * trimul + 2 * triatt + trans_z + apb + trans_s
+        self.ws = _ops.workspace(self.module.workspace_bytes(1, n), device)
+        self.flops = block_flops(n)
 
     def step(self) -> None:
-        self.module.forward_(self.s, self.z, self.tok)
+        self.module.forward_(self.s, self.z, self.tok, self.s_tail, self.z_tail, ws=self.ws)
 
     def cpu_sample(self, oracle):
         s = self.s_cpu.float()
@@ -272,6 +289,44 @@ class BlockWorkload(Workload):
         if kernel in token_bytes:
             return ("hbm", float(token_bytes[kernel]))
         raise KeyError(kernel)
+
+
+class TrunkWorkload(BlockWorkload):
+    """Config 5: the full 48-block Pairformer trunk at N=2048 on one GPU (z [1,2048,2048,128] bf16 with its
+    int8 tail, s [1,2048,384], 5 % padded tokens), every block's weights random-init, the pair tensor and
+    one shared workspace resident in HBM.  A step is one pass through the 48 blocks."""
+
+    cpu_warmup = 0
+    cpu_calls = 1
+
+    def __init__(self, device, n: int = 2048, blocks: int = 48, seed: int = 0):
+        from .pairformer import PairformerBlockHip
+
+        super().__init__(device, n, seed)
+        self.blocks = [self.module] + [init_module(PairformerBlockHip(), seed + 1 + k).to(device).eval()
+                                       for k in range(blocks - 1)]
+        self.name = f"pairformer_trunk{blocks}_n{n}"
+        self.metric = f"ms per {blocks}-block Pairformer trunk pass at N={n} bf16"
+        self.config = dict(self.config, workload=self.name, blocks=blocks)
+        self.flops = blocks * block_flops(n)
+
+    def step(self) -> None:
+        for blk in self.blocks:
+            blk.forward_(self.s, self.z, self.tok, self.s_tail, self.z_tail, ws=self.ws)
+
+    def cpu_sample(self, oracle):
+        """One fp32 oracle block at N=512 (5 % padded), scaled to the trunk by algorithmic flops
+        (48 x block_flops(2048) / block_flops(512)); the full trunk would take ~1 h on the host."""
+        n = 512
+        g = torch.Generator().manual_seed(0)
+        z = torch.randn(1, n, n, 128, generator=g)
+        s = torch.randn(1, n, 384, generator=g)
+        tok = token_mask(n, n // 20, "cpu")
+        params = {k: v.detach().cpu() for k, v in self.module.state_dict().items()}
+        fn = lambda: oracle.pairformer_block(s, z, tok, params, triatt_row_chunk=64)  # noqa: E731
+        frac = block_flops(n) / (len(self.blocks) * block_flops(self.n))
+        return fn, frac, (f"oracle.pairformer_block fp32 at N={n}, scaled to {len(self.blocks)} blocks at "
+                          f"N={self.n} by algorithmic flops")
 
 
 class OpmWorkload(Workload):
@@ -409,13 +464,15 @@ class PairMixerWorkload(Workload):
         self.tok_cpu = token_mask(n, self.n_pad, "cpu")
         self.pm_cpu = self.tok_cpu[:, :, None] & self.tok_cpu[:, None, :]
         self.z = self.z_cpu.to(device)
+        self.z_tail = torch.zeros(self.z.shape, dtype=torch.int8, device=device)
         self.pm = self.pm_cpu.to(device)
-        self.config = {"workload": self.name, "N": n, "c_z": 128, "batch": 1, "padded_tokens": self.n_pad}
+        self.config = {"workload": self.name, "N": n, "c_z": 128, "batch": 1, "padded_tokens": self.n_pad,
+                       "residual_stream": "bf16 + int8 tail"}
         trimul = 2.0 * n * n * 128 * 6 * 128 + 2.0 * 128 * n ** 3
         self.flops = 2 * trimul + 2.0 * n * n * 128 * 12 * 128
 
     def step(self) -> None:
-        self.layer.forward_(None, self.z, self.pm)
+        self.layer.forward_(None, self.z, self.pm, self.z_tail)
 
     def cpu_sample(self, oracle):
         params = {k: v.detach().cpu() for k, v in self.layer.state_dict().items()}
@@ -466,8 +523,11 @@ class PairMixerMsaWorkload(Workload):
         self.pm = self.pm_cpu.to(device)
         self.msa_mask = self.msa_mask_cpu.to(device)
         self.s_valid = int(rows.sum())
+        self.z_tail = torch.zeros(self.z.shape, dtype=torch.int8, device=device)
+        self.m_tail = torch.zeros(self.m.shape, dtype=torch.int8, device=device)
         self.config = {"workload": self.name, "S": S, "N": n, "c_m": 64, "c_z": 128, "batch": 1,
-                       "padded_tokens": self.n_pad, "valid_msa_rows": self.s_valid}
+                       "padded_tokens": self.n_pad, "valid_msa_rows": self.s_valid,
+                       "residual_stream": "bf16 + int8 tail"}
         pwa = 2.0 * S * n * 64 * 512 + 2.0 * 8 * n * n * S * 32 + 2.0 * S * n * 256 * 64
         msa_tr = 2.0 * S * n * 64 * 12 * 64
         opm = 2.0 * n * n * 1024 * self.s_valid + 2.0 * n * n * 1024 * 128
@@ -475,7 +535,7 @@ class PairMixerMsaWorkload(Workload):
         self.flops = pwa + msa_tr + opm + 2 * trimul + 2.0 * n * n * 128 * 12 * 128
 
     def step(self) -> None:
-        self.layer.forward_(None, self.z, self.m, self.pm, self.msa_mask)
+        self.layer.forward_(None, self.z, self.m, self.pm, self.msa_mask, z_tail=self.z_tail, m_tail=self.m_tail)
 
     def cpu_sample(self, oracle):
         """Every op of the layer, each on a bounded slice scaled to the full layer: PWA and the MSA
@@ -754,6 +814,10 @@ def make(op: str, device, n: int | None = None) -> Workload:
         return PairMixerMsaWorkload(device, n or 512)
     if op == "block":
         return BlockWorkload(device, n or 768)
+    if op == "block_bf16stream":   # the same block with plain bf16 residual streams (no tails)
+        return BlockWorkload(device, n or 768, tails=False)
+    if op == "trunk":              # config 5: 48 blocks at N = 2048
+        return TrunkWorkload(device, n or 2048)
     if op in ("triatt_start", "triatt_end"):
         return TriAttWorkload(device, op == "triatt_start", n or 768)
     if op in ("trimul_out", "trimul_in"):

@@ -15,6 +15,18 @@
  *
  * Scratch memory is caller-owned: each op with intermediates has a
  * *_workspace_bytes() query and takes (workspace, workspace_bytes).
+ *
+ * Residual tails.  Every entry point that can add its result into a residual
+ * stream (residual=1, or z_res for the OPM) takes an optional `res_tail`: an
+ * int8 plane with one byte per element of `out`.  The stream's value is then
+ * hi + t * 2^(E(hi) - 142) (hi the bf16 element, E its biased exponent field,
+ * t the tail byte: 1/256ths of hi's unit in the last place), ~16 significant
+ * bits.  The op reads x + tail, adds its update in fp32 and writes the sum
+ * back as a bf16 element plus a new tail byte (the tail is updated in place).
+ * Inputs that an op only normalises are read as bf16 (the tail is not read).
+ * res_tail = NULL keeps the plain bf16 stream, rounded after every add (the
+ * reference's bf16-autocast trunk).  bioemu_stream_split / _join convert
+ * between fp32 tensors and (bf16, tail) pairs.
  */
 #ifndef BIOEMU2_MI355X_H
 #define BIOEMU2_MI355X_H
@@ -62,12 +74,14 @@ int bioemu_timer_query(int idx, char* name, size_t name_len, int64_t* launches, 
  *   out = p_out(LN_out(o)) * sigmoid(g_out(xn))   (+ x when residual != 0)
  * x, out: [B,N,N,D] bf16 (out may equal x when residual != 0); mask [B,N,N].
  * p_in_w, g_in_w: [2D, D]; p_out_w, g_out_w: [D, D].  D must be 128.
+ * res_tail: NULL or the [B,N,N,D] int8 tail of the residual stream (residual=1).
  */
 size_t bioemu_trimul_workspace_bytes(int64_t B, int64_t N, int64_t D);
 int bioemu_trimul_fwd(const void* x, const uint8_t* mask, const float* norm_in_w,
                       const float* norm_in_b, const void* p_in_w, const void* g_in_w,
                       const float* norm_out_w, const float* norm_out_b, const void* p_out_w,
-                      const void* g_out_w, void* out, void* workspace, size_t workspace_bytes,
+                      const void* g_out_w, void* out, int8_t* res_tail, void* workspace,
+                      size_t workspace_bytes,
                       int64_t B, int64_t N, int64_t D, int outgoing, int residual,
                       hipStream_t stream);
 
@@ -86,10 +100,11 @@ int bioemu_trimul_fwd(const void* x, const uint8_t* mask, const float* norm_in_w
  * z, out: [B,N,N,D] bf16 (out may equal z when residual != 0); mask [B,N,N].
  * w_proj: [4*D + H, D] = rows of Wq, Wk, Wv, Wg, Wbias; w_o: [D, D].
  * D must be 128 and H 4 (head dim 32).
+ * res_tail: NULL or the [B,N,N,D] int8 tail of the residual stream (residual=1).
  */
 size_t bioemu_triatt_workspace_bytes(int64_t B, int64_t N, int64_t D, int64_t H);
 int bioemu_triatt_fwd(const void* z, const uint8_t* mask, const float* norm_w, const float* norm_b,
-                      const void* w_proj, const void* w_o, void* out, void* workspace,
+                      const void* w_proj, const void* w_o, void* out, int8_t* res_tail, void* workspace,
                       size_t workspace_bytes, int64_t B, int64_t N, int64_t D, int64_t H,
                       int starting, int residual, hipStream_t stream);
 
@@ -104,11 +119,12 @@ int bioemu_triatt_fwd(const void* z, const uint8_t* mask, const float* norm_w, c
  * diffusion.py:498-507).  use_norm=0 skips the LayerNorm (norm_* unused).
  * The workspace holds fc1/fc2 with the LayerNorm affine folded in (size from
  * bioemu_transition_pair_workspace_bytes, independent of P).
+ * res_tail: NULL or the [P, D] int8 tail of the residual stream (residual=1).
  */
 size_t bioemu_transition_pair_workspace_bytes(int64_t D, int64_t hidden);
 int bioemu_transition_pair_fwd(const void* x, const float* norm_w, const float* norm_b,
                                const void* fc1_w, const void* fc2_w, const void* fc3_w, void* out,
-                               void* workspace, size_t workspace_bytes, int64_t P, int64_t D,
+                               int8_t* res_tail, void* workspace, size_t workspace_bytes, int64_t P, int64_t D,
                                int64_t hidden, int use_norm, int residual, hipStream_t stream);
 
 /*
@@ -116,11 +132,12 @@ int bioemu_transition_pair_fwd(const void* x, const float* norm_w, const float* 
  * multiple of 32): LN kernel + two MFMA GEMMs.  Replaces Transition.forward
  * (transition.py:52-91) for the single representation s and any width /
  * hidden pair the fused row kernel does not take.
+ * res_tail: NULL or the [M, D] int8 tail of the residual stream (residual=1).
  */
 size_t bioemu_transition_token_workspace_bytes(int64_t M, int64_t D, int64_t hidden);
 int bioemu_transition_token_fwd(const void* x, const float* norm_w, const float* norm_b,
                                 const void* fc1_w, const void* fc2_w, const void* fc3_w, void* out,
-                                void* workspace, size_t workspace_bytes, int64_t M, int64_t D,
+                                int8_t* res_tail, void* workspace, size_t workspace_bytes, int64_t M, int64_t D,
                                 int64_t hidden, int use_norm, int residual, hipStream_t stream);
 
 /*
@@ -133,11 +150,12 @@ int bioemu_transition_token_fwd(const void* x, const float* norm_w, const float*
  * may equal m when residual != 0); z: [B, N, N, c_z] bf16; mask: [B, N, N]
  * uint8.  norm_z_b may be null (use_bias_in_layer_norm=False).  Supported:
  * c_m = 64, c_z = 128, c_h = 32, H = 8, N <= 4096.
+ * res_tail: NULL or the [B, S, N, c_m] int8 tail of the residual stream m (residual=1).
  */
 size_t bioemu_pwa_workspace_bytes(int64_t B, int64_t S, int64_t N, int64_t c_m, int64_t c_h, int64_t H);
 int bioemu_pwa_fwd(const void* m, const void* z, const uint8_t* mask, const float* norm_m_w, const float* norm_m_b,
                    const void* w_m, const void* w_g, const float* norm_z_w, const float* norm_z_b, const void* w_z,
-                   const void* w_o, void* out, void* workspace, size_t workspace_bytes, int64_t B, int64_t S,
+                   const void* w_o, void* out, int8_t* res_tail, void* workspace, size_t workspace_bytes, int64_t B, int64_t S,
                    int64_t N, int64_t c_m, int64_t c_z, int64_t c_h, int64_t H, int residual, hipStream_t stream);
 
 /*
@@ -151,12 +169,13 @@ int bioemu_pwa_fwd(const void* m, const void* z, const uint8_t* mask, const floa
  * s, out: [B*mult, N, c_s] bf16; z: [B, N, N, c_z] bf16; mask [B, N] uint8.
  * The bias is shared by the `mult` copies of each batch element (multiplicity).
  * Supported: c_z = 128, head dim 24 (c_s = 24*H, c_s in {128, 384}).
+ * res_tail: NULL or the [B*mult, N, c_s] int8 tail of the residual stream s (residual=1).
  */
 size_t bioemu_apb_workspace_bytes(int64_t B, int64_t mult, int64_t N, int64_t c_s, int64_t H);
 int bioemu_apb_fwd(const void* s, const void* z, const uint8_t* mask, const float* norm_s_w,
                    const float* norm_s_b, const void* w_qkv, const float* q_bias, const void* w_g,
                    const float* norm_z_w, const float* norm_z_b, const void* w_z, const void* w_o,
-                   void* out, void* workspace, size_t workspace_bytes, int64_t B, int64_t mult,
+                   void* out, int8_t* res_tail, void* workspace, size_t workspace_bytes, int64_t B, int64_t mult,
                    int64_t N, int64_t c_s, int64_t c_z, int64_t H, int residual, hipStream_t stream);
 
 /*
@@ -219,13 +238,23 @@ int bioemu_pair_cond_proj_fwd(const void* z_trunk, const void* rel, const float*
  * mean_rows=0 divides by 1 (a [B,N] reference mask, expanded over S by the caller).
  * w_ab: [2*C_H, c_in]; w_o: [c_out, C_H*C_H]; b_o: [c_out] fp32; out: [B,N,N,c_out] bf16.
  * Supported: c_in = 64, C_H = 32, c_out = 128.
+ * res_tail: NULL or the [B,N,N,c_out] int8 tail of the residual stream z_res (needs z_res).
  */
 size_t bioemu_opm_workspace_bytes(int64_t B, int64_t S, int64_t N, int64_t c_in, int64_t c_hidden);
 int bioemu_opm_fwd(const void* m, const uint8_t* mask, int mean_rows, const float* norm_w,
                    const float* norm_b, const void* w_ab, const void* w_o, const float* b_o,
-                   const void* z_res, void* out, void* workspace, size_t workspace_bytes, int64_t B,
+                   const void* z_res, void* out, int8_t* res_tail, void* workspace, size_t workspace_bytes, int64_t B,
                    int64_t S, int64_t N, int64_t c_in, int64_t c_hidden, int64_t c_out,
                    hipStream_t stream);
+
+/*
+ * Residual-stream conversion (no counterpart in the reference, whose bf16
+ * trunk stores z and s as plain bf16; see "Residual tails" above).
+ * split: x (n fp32) -> hi (n bf16, round to nearest) + tail (n int8).
+ * join:  hi + tail -> out (n fp32).  n a multiple of 16; 16-byte aligned buffers.
+ */
+int bioemu_stream_split(const float* x, void* hi, int8_t* tail, int64_t n, hipStream_t stream);
+int bioemu_stream_join(const void* hi, const int8_t* tail, float* out, int64_t n, hipStream_t stream);
 
 #ifdef __cplusplus
 }

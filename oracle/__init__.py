@@ -43,12 +43,16 @@ How each function is pinned (see ``tests/test_oracle_*.py``):
                     average over the N keys), a single valid key (o = v of that
                     key exactly), MSA-row independence of the weights.
 * ``transition``  — brute-force loops and the SwiGLU closed form.
-* ``pairformer_block`` — composition only (AF3 suppl. Alg. 17); each term is
-                    pinned above, the order is pinned by a hand-built
-                    composition test.
-* ``pairmixer_layer``, ``pairmixer_msa_layer`` — the reference trunk's layers
-                    (pairmixer.py:430-456, :711-757), compositions of the pinned
-                    terms; zeroed output projections reduce them to the identity.
+* ``pairformer_block`` (AF3 suppl. Alg. 17), ``pairmixer_layer``
+  (pairmixer.py:430-456) and ``pairmixer_msa_layer`` (pairmixer.py:711-757)
+                  — compositions of the pinned terms above, pinned in
+                    tests/test_oracle_compositions.py: with every output
+                    projection zeroed they return their inputs bit for bit;
+                    with one left non-zero they return input + that op's
+                    update (computed from the op function and a sub-dict the
+                    test builds itself); with two consecutive ops non-zero
+                    the second sees the first one's output, and the reversed
+                    order (a negative control) differs.
 
 No function here is "parity unpinned".
 """

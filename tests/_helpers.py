@@ -61,3 +61,34 @@ def rel_l2(a: torch.Tensor, b: torch.Tensor) -> float:
 
 def max_abs(a: torch.Tensor, b: torch.Tensor) -> float:
     return float((a.double() - b.double()).abs().max())
+
+
+# ----------------------------------------------------------------------------
+# Residual-tail format, restated in numpy (the statement the HIP split/join and
+# every residual epilogue are checked against): value = hi + t * 2^(E(hi) - 142)
+# with hi = round-to-nearest-even bf16 of the value, E its biased exponent
+# field, t = clamp(rint((value - hi) * 2^(142 - E)), -127, 127).
+# ----------------------------------------------------------------------------
+def np_bf16_rne(x: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 bit patterns (uint16), round to nearest even (finite inputs)."""
+    u = np.asarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    return r.astype(np.uint16)
+
+
+def np_bf16_to_f32(b: np.ndarray) -> np.ndarray:
+    return (b.astype(np.uint32) << 16).view(np.float32)
+
+
+def np_tail_encode(v: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    v = np.asarray(v, dtype=np.float32)
+    hi = np_bf16_rne(v)
+    e = ((hi >> 7) & 0xFF).astype(np.int32)
+    r = (v - np_bf16_to_f32(hi)).astype(np.float32)
+    t = np.clip(np.rint(np.ldexp(r.astype(np.float64), 142 - e)), -127, 127).astype(np.int8)
+    return hi, t
+
+
+def np_tail_decode(hi: np.ndarray, t: np.ndarray) -> np.ndarray:
+    e = ((hi >> 7) & 0xFF).astype(np.int32)
+    return (np_bf16_to_f32(hi).astype(np.float64) + np.ldexp(t.astype(np.float64), e - 142)).astype(np.float32)

@@ -76,8 +76,8 @@ def test_host_only_queries():
 def test_invalid_arguments_rejected_without_gpu():
     """Argument validation runs on the host before any launch."""
     lib = _lib.lib()
-    rc = lib.bioemu_trimul_fwd(*([None] * 11), None, 0, 1, 16, 128, 1, 0, None)
+    rc = lib.bioemu_trimul_fwd(*([None] * 12), None, 0, 1, 16, 128, 1, 0, None)
     assert rc == -1
     assert b"null" in lib.bioemu_last_error()
-    rc = lib.bioemu_trimul_fwd(*([None] * 11), None, 0, 1, 16, 64, 1, 0, None)
+    rc = lib.bioemu_trimul_fwd(*([None] * 12), None, 0, 1, 16, 64, 1, 0, None)
     assert rc == -2

@@ -13,7 +13,7 @@ from tests._helpers import max_abs, rel_l2, state
 
 pytestmark = pytest.mark.gpu
 
-ATOL = 2.5e-2  # the reference's own bf16 OPM tolerance (test_outer_product_mean.py:22)
+ATOL = 2e-2  # north_star bf16 bound (the reference's own bf16 OPM bound is 2.5e-2, test_outer_product_mean.py:22)
 RTOL_L2 = 1e-2
 
 
@@ -61,17 +61,16 @@ def test_config3_shape_rows_subset(gpu_device):
 
 
 def test_2d_mask(gpu_device):
+    """A [B,N] mask divides by 1 (outer_product_mean.py:69-70): the result is the sum over S, so S is kept
+    small enough (6 rows) that outputs stay O(1) and the absolute bound is meaningful."""
     m_ = _module(gpu_device)
-    m, _ = _inputs(1, 50, 20, gpu_device)
+    m, _ = _inputs(1, 6, 20, gpu_device)
     tok = torch.ones(1, 20, dtype=torch.bool, device=gpu_device)
     tok[:, 15:] = False
     with torch.no_grad():
         got = m_(m, tok).float().cpu()
     want = oracle.outer_product_mean(m.cpu(), tok.cpu(), state(m_))
-    err, rl2 = max_abs(got, want), rel_l2(got, want)
-    # no averaging over S: magnitudes are ~S times larger; hold rel-L2 and a scaled max-abs
-    print(f"opm 2d mask: max_abs={err:.3e} rel_l2={rl2:.3e} |want|max={want.abs().max():.2f}")
-    assert rl2 <= RTOL_L2 and err <= ATOL * max(1.0, float(want.abs().max()))
+    _check(got, want, "opm 2d mask")
 
 
 def test_all_rows_masked_gives_bias(gpu_device):

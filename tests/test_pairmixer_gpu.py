@@ -1,4 +1,9 @@
-"""The reference trunk's PairMixer layers on the GPU vs the fp32 CPU oracle compositions."""
+"""The reference trunk's PairMixer layers on the GPU vs the fp32 CPU oracle compositions.
+
+The layers carry their residual streams (z, m) with int8 tails and return fp32
+for fp32 inputs, so they are held to the bf16 bound itself (max-abs 2e-2,
+rel-L2 1e-2) on every valid element.
+"""
 
 from __future__ import annotations
 
@@ -20,15 +25,16 @@ def _tok(B, n, n_pad, device):
     return tok.to(device)
 
 
-def _check(name, got, want, sel, adds):
+def _check(name, got, want, sel):
     g, w = got.float().cpu()[sel], want[sel]
     err, rl2 = max_abs(g, w), rel_l2(g, w)
-    # The north_star bf16 bound (max-abs 2e-2, rel-L2 1e-2) per element, plus one bf16
-    # rounding of the residual stream per residual add (2^-9 |x|): the layers keep z and m in
-    # bf16 between ops, as the reference's bf16-mixed trunk does.
-    excess = ((g - w).abs() - (2e-2 + adds * 2.0 ** -9 * w.abs())).max().item()
-    print(f"{name}: max_abs={err:.3e} rel_l2={rl2:.3e} |want|max={w.abs().max():.2f} excess={excess:.3e}")
-    assert rl2 <= 1e-2 and excess <= 0.0
+    print(f"{name}: max_abs={err:.3e} rel_l2={rl2:.3e} |want|max={w.abs().max():.2f}", flush=True)
+    assert err <= 2e-2 and rl2 <= 1e-2, (name, err, rl2)
+
+
+def _randn(shape, g, device):
+    """~N(0, 1), bf16-representable, held in fp32."""
+    return torch.randn(*shape, generator=g).to(torch.bfloat16).float().to(device)
 
 
 @pytest.mark.parametrize("n,n_pad", [(64, 0), (96, 9)])
@@ -36,14 +42,14 @@ def test_pairmixer_layer_matches_oracle(gpu_device, n, n_pad):
     torch.manual_seed(0)
     layer = init_module(PairMixerLayerHip(384, 128), 0).to(gpu_device).eval()
     g = torch.Generator().manual_seed(1)
-    s = torch.randn(1, n, 384, generator=g).to(torch.bfloat16).to(gpu_device)
-    z = torch.randn(1, n, n, 128, generator=g).to(torch.bfloat16).to(gpu_device)
+    s = _randn((1, n, 384), g, gpu_device)
+    z = _randn((1, n, n, 128), g, gpu_device)
     tok = _tok(1, n, n_pad, gpu_device)
     pm = tok[:, :, None] & tok[:, None, :]
     s_got, z_got = layer(s, z, pm)
-    assert s_got is s
+    assert s_got is s and z_got.dtype == torch.float32
     _, z_want = oracle.pairmixer_layer(s.cpu(), z.cpu(), pm.cpu(), state(layer))
-    _check(f"pairmixer n={n}", z_got, z_want, pm.cpu(), 3)
+    _check(f"pairmixer n={n}", z_got, z_want, pm.cpu())
 
 
 @pytest.mark.parametrize("S,n,n_pad", [(16, 64, 0), (24, 80, 8)])
@@ -51,17 +57,17 @@ def test_pairmixer_msa_layer_matches_oracle(gpu_device, S, n, n_pad):
     torch.manual_seed(0)
     layer = init_module(PairMixerMSALayerHip(384, 64, 128, 0.15, 0.25), 0).to(gpu_device).eval()
     g = torch.Generator().manual_seed(2)
-    s = torch.randn(1, n, 384, generator=g).to(torch.bfloat16).to(gpu_device)
-    z = torch.randn(1, n, n, 128, generator=g).to(torch.bfloat16).to(gpu_device)
-    m = torch.randn(1, S, n, 64, generator=g).to(torch.bfloat16).to(gpu_device)
+    s = _randn((1, n, 384), g, gpu_device)
+    z = _randn((1, n, n, 128), g, gpu_device)
+    m = _randn((1, S, n, 64), g, gpu_device)
     tok = _tok(1, n, n_pad, gpu_device)
     pm = tok[:, :, None] & tok[:, None, :]
     msa_mask = tok[:, None, :].expand(1, S, n).clone()
     msa_mask[:, -3:] = False  # a few padded MSA rows
     _, z_got, m_got = layer(s, z, m, pm, msa_mask)
     _, z_want, m_want = oracle.pairmixer_msa_layer(s.cpu(), z.cpu(), m.cpu(), pm.cpu(), msa_mask.cpu(), state(layer))
-    _check(f"pairmixer-msa S={S} n={n} m", m_got, m_want, tok.cpu()[:, None, :].expand(1, S, n), 2)
-    _check(f"pairmixer-msa S={S} n={n} z", z_got, z_want, pm.cpu(), 4)
+    _check(f"pairmixer-msa S={S} n={n} m", m_got, m_want, tok.cpu()[:, None, :].expand(1, S, n))
+    _check(f"pairmixer-msa S={S} n={n} z", z_got, z_want, pm.cpu())
 
 
 def test_pairmixer_inplace_matches_out_of_place(gpu_device):
@@ -74,10 +80,13 @@ def test_pairmixer_inplace_matches_out_of_place(gpu_device):
     tok = _tok(1, 48, 4, gpu_device)
     pm = tok[:, :, None] & tok[:, None, :]
     msa_mask = tok[:, None, :].expand(1, 8, 48).clone()
+    from bioemu2_amd.residual import join_stream, split_stream
+
     _, z_new, m_new = layer(s, z, m, pm, msa_mask)
-    z2, m2 = z.clone(), m.clone()
-    layer.forward_(s, z2, m2, pm, msa_mask)
-    assert torch.equal(z2, z_new) and torch.equal(m2, m_new)
+    (z2, zt), (m2, mt) = split_stream(z), split_stream(m)
+    layer.forward_(s, z2, m2, pm, msa_mask, z_tail=zt, m_tail=mt)
+    assert torch.equal(join_stream(z2, zt, torch.bfloat16), z_new)
+    assert torch.equal(join_stream(m2, mt, torch.bfloat16), m_new)
 
 
 def test_msa_mask_controls_pair_update(gpu_device):
