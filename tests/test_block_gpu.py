@@ -137,3 +137,35 @@ def test_block_config5_size_padding_invariant(gpu_device):
     assert torch.isfinite(z[:, :v, :v].float()).all() and torch.isfinite(s[:, :v].float()).all()
     assert torch.equal(z[:, :v, :v], z2[:, :v, :v])
     assert torch.equal(s[:, :v], s2[:, :v])
+
+
+def test_trunk_48_blocks_config5(gpu_device):
+    """Config 5: all 48 blocks at N = 2048 (102 padded tokens), residual streams with tails, one shared
+    workspace.  The whole trunk's valid outputs are finite and bit-identical when every padded token's s
+    and every pair touching a padded token in z change."""
+    from bioemu2_amd.residual import join_stream, split_stream
+
+    n, pad, nblk = 2048, 102, 48
+    blocks = [_block(gpu_device, seed=k) for k in range(nblk)]
+    ws = torch.empty(blocks[0].workspace_bytes(1, n), dtype=torch.uint8, device=gpu_device)
+    s, z, tok = _inputs(n, pad, gpu_device, seed=5, dtype=torch.bfloat16)
+    s2, z2 = s.clone(), z.clone()
+    s2[:, n - pad:] = 7.0
+    z2[:, n - pad:] = -5.0
+    z2[:, :, n - pad:] = 3.0
+    results = []
+    for s_in, z_in in ((s, z), (s2, z2)):
+        (sh, st), (zh, zt) = split_stream(s_in), split_stream(z_in)
+        del s_in, z_in
+        for k, blk in enumerate(blocks):
+            blk.forward_(sh, zh, tok, st, zt, ws=ws)
+        torch.cuda.synchronize()
+        print(f"trunk pass done ({nblk} blocks)", flush=True)
+        v = n - pad
+        results.append((join_stream(sh[:, :v], st[:, :v]),
+                        join_stream(zh[:, :v, :v].contiguous(), zt[:, :v, :v].contiguous())))
+        del sh, st, zh, zt
+    (sa, za), (sb, zb) = results
+    assert torch.isfinite(za).all() and torch.isfinite(sa).all()
+    print(f"trunk |z|max={za.abs().max().item():.2f} |s|max={sa.abs().max().item():.2f}", flush=True)
+    assert torch.equal(za, zb) and torch.equal(sa, sb)

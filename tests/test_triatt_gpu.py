@@ -63,6 +63,24 @@ def test_token_padding_config_shape(gpu_device, starting):
 
 
 @pytest.mark.parametrize("starting", [True, False])
+def test_config4_shape_n768(gpu_device, starting):
+    """Config 4: N=768, last 76 tokens padded, pair mask = outer AND (oracle row-chunked)."""
+    n, n_pad = 768, 76
+    m = _module(starting, gpu_device)
+    g = torch.Generator().manual_seed(0)
+    z = torch.randn(1, n, n, C, generator=g).to(torch.bfloat16)
+    tok = torch.ones(1, n, dtype=torch.bool)
+    tok[:, n - n_pad:] = False
+    pm = oracle.pair_mask_from_token_mask(tok)
+    with torch.no_grad():
+        got = m(z.to(gpu_device), pm.to(gpu_device)).float().cpu()
+    want = oracle.triangle_attention(z.float(), pm, state(m), H, starting, row_chunk=64)
+    err, rl2 = max_abs(got, want), rel_l2(got, want)
+    print(f"triatt n=768 padded starting={starting}: max_abs={err:.3e} rel_l2={rl2:.3e}", flush=True)
+    assert err <= ATOL and rl2 <= RTOL_L2
+
+
+@pytest.mark.parametrize("starting", [True, False])
 def test_masking_bit_exact(gpu_device, starting):
     """Values under masked pairs never reach valid outputs... except through
     their own row/col: for the starting node a masked pair (i,k) is a masked key

@@ -46,10 +46,11 @@ def test_matches_oracle(gpu_device, mode, n):
     assert err <= ATOL and rl2 <= RTOL_L2
 
 
-def test_matches_oracle_n768_token_padding(gpu_device):
+@pytest.mark.parametrize("mode", ["outgoing", "incoming"])
+def test_matches_oracle_n768_token_padding(gpu_device, mode):
     """Config 4 shape: N=768, last 76 tokens padded, pair mask = outer AND."""
     n = 768
-    m = _module("outgoing", gpu_device)
+    m = _module(mode, gpu_device)
     g = torch.Generator().manual_seed(0)
     x = torch.randn(1, n, n, D, generator=g).to(torch.bfloat16)
     tok = torch.ones(1, n, dtype=torch.bool)
@@ -57,9 +58,9 @@ def test_matches_oracle_n768_token_padding(gpu_device):
     pm = oracle.pair_mask_from_token_mask(tok)
     with torch.no_grad():
         got = m(x.to(gpu_device), pm.to(gpu_device)).float().cpu()
-    want = oracle.trimul(x.float(), pm, state(m), "outgoing")
+    want = oracle.trimul(x.float(), pm, state(m), mode)
     err, rl2 = max_abs(got, want), rel_l2(got, want)
-    print(f"trimul outgoing n=768: max_abs={err:.3e} rel_l2={rl2:.3e}")
+    print(f"trimul {mode} n=768: max_abs={err:.3e} rel_l2={rl2:.3e}")
     assert err <= ATOL and rl2 <= RTOL_L2
 
 
@@ -77,7 +78,7 @@ def test_masking_bit_exact(gpu_device, mode):
 
 @pytest.mark.parametrize("mode", ["outgoing", "incoming"])
 def test_padding_bit_exact(gpu_device, mode):
-    n, pad = 100, 29  # crosses the 128 padding boundary of the contraction
+    n, pad = 200, 100  # the contraction pads N to a multiple of 256: 200 -> 256, 300 -> 512
     m = _module(mode, gpu_device)
     x, mask = _inputs(n, gpu_device)
     px = torch.full((1, n + pad, n + pad, D), 1000.0, dtype=x.dtype, device=gpu_device)
