@@ -43,6 +43,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _c_int,
         [_c_void_p] * 8 + [_c_void_p, _c_size_t] + [_c_int64] * 3 + [_c_int, _c_int, _c_void_p],
     ),
+    "bioemu_transition_pair_fwd_noalloc": (
+        _c_int,
+        [_c_void_p] * 8 + [_c_int64] * 3 + [_c_int, _c_int, _c_void_p],
+    ),
     "bioemu_transition_token_workspace_bytes": (_c_size_t, [_c_int64] * 3),
     "bioemu_transition_token_fwd": (
         _c_int,

@@ -26,6 +26,8 @@
 // LDS tiles are unpadded (the copies write 1 KB runs); the 16-byte chunk index
 // of each row is XOR-swizzled so that the perm32 row pattern of the operand
 // reads hits 16 distinct bank groups per 16 lanes.
+#include <mutex>
+
 #include "common.h"
 #include "internal.h"
 #include "pairtile.h"
@@ -300,4 +302,60 @@ extern "C" int bioemu_transition_pair_fwd(const void* x, const float* norm_w, co
                          : launch_rows<128, 256>(xb, w1, w2, w3, cf, ob, res_tail, rows, use_norm, residual, stream);
   return hidden == 256 ? launch_rows<64, 256>(xb, w1, w2, w3, cf, ob, res_tail, rows, use_norm, residual, stream)
                        : launch_rows<64, 128>(xb, w1, w2, w3, cf, ob, res_tail, rows, use_norm, residual, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free variant: the same kernels, with the folded-weight workspace
+// in a static device array instead of a caller-provided buffer.
+//
+// The workspace of bioemu_transition_pair_fwd does not grow with the row count:
+// it holds fc1 | fc2 with the LayerNorm folded in and their bias pairs, at most
+// fold_bytes(2 * 512, 128) = 266240 bytes (D = 128, hidden = 512).  Every GPU
+// the library runs on holds one copy of `scratch` until the process ends; its
+// device address is looked up once per device (hipGetSymbolAddress) on the
+// first call made with that device current.  Each call rewrites every byte it
+// reads (the fold kernels write all folded rows before the row kernel runs), so
+// nothing needs clearing between calls; calls that overlap on one GPU (other
+// streams, other threads) share the array and race.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr size_t kScratchBytes = 266240;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_for_current_device(void** ptr) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return set_error(BIOEMU_ERR_LAUNCH, "transition_pair_noalloc: no current device (or device id >= %d)",
+                     kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_error(BIOEMU_ERR_LAUNCH, "transition_pair_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s",
+                       dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return BIOEMU_OK;
+}
+}  // namespace
+
+extern "C" int bioemu_transition_pair_fwd_noalloc(const void* x, const float* norm_w, const float* norm_b,
+                                                  const void* fc1_w, const void* fc2_w, const void* fc3_w,
+                                                  void* out, int8_t* res_tail, int64_t P, int64_t Dc,
+                                                  int64_t hidden, int use_norm, int residual, hipStream_t stream) {
+  const size_t need = bioemu_transition_pair_workspace_bytes(Dc, hidden);
+  if (need > kScratchBytes)
+    return set_error(BIOEMU_ERR_UNSUPPORTED, "transition_pair_noalloc: dim %lld / hidden %lld need %zu bytes of scratch, "
+                     "more than the static %zu", (long long)Dc, (long long)hidden, need, kScratchBytes);
+  void* ws = nullptr;
+  const int rc = scratch_for_current_device(&ws);
+  if (rc) return rc;
+  return bioemu_transition_pair_fwd(x, norm_w, norm_b, fc1_w, fc2_w, fc3_w, out, res_tail, ws, kScratchBytes, P, Dc,
+                                    hidden, use_norm, residual, stream);
 }

@@ -128,6 +128,24 @@ int bioemu_transition_pair_fwd(const void* x, const float* norm_w, const float* 
                                int64_t hidden, int use_norm, int residual, hipStream_t stream);
 
 /*
+ * Allocation-free variant of bioemu_transition_pair_fwd (same arguments minus
+ * the workspace, same kernels, bit-identical results).  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory -- code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
+ * The folded-weight scratch (at most 266240 bytes: D = 128, hidden = 512) lives
+ * in a static device array, one per GPU, held until the process ends; its
+ * address is looked up once per device on the first call with that device
+ * current.  Every call on one GPU shares that array: calls that overlap on a
+ * GPU (other streams or threads) race.  Each call rewrites all the scratch it
+ * reads, so nothing needs clearing between calls.  Rejects shapes whose scratch
+ * would exceed the array (BIOEMU_ERR_UNSUPPORTED).
+ */
+int bioemu_transition_pair_fwd_noalloc(const void* x, const float* norm_w, const float* norm_b,
+                                       const void* fc1_w, const void* fc2_w, const void* fc3_w, void* out,
+                                       int8_t* res_tail, int64_t P, int64_t D, int64_t hidden, int use_norm,
+                                       int residual, hipStream_t stream);
+
+/*
  * Token Transition (same op over [M, D] rows, D in {64, 128, 384}, hidden a
  * multiple of 32): LN kernel + two MFMA GEMMs.  Replaces Transition.forward
  * (transition.py:52-91) for the single representation s and any width /
