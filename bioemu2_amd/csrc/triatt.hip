@@ -380,7 +380,12 @@ __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
         if (hd + 1 == H) kn = k0;
       }
       gload(hn, kn);
-      if (active) {
+      // Every wave runs the block, idle ones (q0 >= Np, only when Np is not a
+      // multiple of 256) on row 0 queries whose results they never store: with
+      // a branch here the compiler's wait before the K / V staging store below
+      // would have to cover the inactive path too, where nothing follows the
+      // K / V loads, and would then also wait for the bias prefetch.
+      {
         const bf16* ks = smem + st * kStage;
         const bf16* vs = ks + 2 * kTile;
         bf16x8 km0 = zero8, km1 = zero8;
@@ -483,6 +488,21 @@ __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
 
 #pragma unroll 1
   for (int t = 0; t < 2; ++t) {
+    // The residual (and its tail) of each output block is requested one block
+    // ahead, so that its latency hides behind the gate loads and the previous
+    // block's MFMAs.  Lanes of queries past N read pair 0 and store nothing.
+    const int q = q0 + 32 * t + n;
+    const bool store = q < N;
+    const size_t zpair = !store ? 0 : kStarting ? ((size_t)b * N + i) * N + q : ((size_t)b * N + q) * N + i;
+    bf16x8 zr[2][2];
+    u32x4 zt[2];
+    auto zload = [&](int cb) {
+      const size_t off = zpair * C + cb * 32 + 16 * hh;
+      zr[cb & 1][0] = load8(zres + off);
+      zr[cb & 1][1] = load8(zres + off + 8);
+      if (kTail) zt[cb & 1] = load_tail16(tail + off);
+    };
+    if (residual) zload(0);
     // Gate: g * (o / l) per head, as the out-projection's B operand.
     bf16x8 gob[2 * H];
     {
@@ -500,12 +520,13 @@ __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
       }
     }
 
-    // update^T = Wo (g*o)^T, residual add, store in z's frame.
-    const int q = q0 + 32 * t + n;
-    const bool store = q < N;
-    const size_t zpair = kStarting ? ((size_t)b * N + i) * N + q : ((size_t)b * N + q) * N + i;
-#pragma unroll 1
+    // update^T = Wo (g*o)^T, residual add, store in z's frame.  The scheduling
+    // barrier keeps the four output blocks apart (interleaved, their weight
+    // loads and accumulators would not fit the register budget).
+#pragma unroll
     for (int cb = 0; cb < 4; ++cb) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (residual && cb + 1 < 4) zload(cb + 1);
       f32x16 acc = zero16();
       const bf16* wrow = wo + (size_t)(cb * 32 + perm32(n)) * C + 16 * hh;
 #pragma unroll
@@ -517,18 +538,17 @@ __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
         for (int u = 0; u < 16; ++u) v[u] = acc[u];
         if (kTail) {
           float zv[16];
-          tail_decode16(load8(zres + off), load8(zres + off + 8), load_tail16(tail + off), zv);
+          tail_decode16(zr[cb & 1][0], zr[cb & 1][1], zt[cb & 1], zv);
 #pragma unroll
           for (int u = 0; u < 16; ++u) v[u] += zv[u];
           tail_store16(out + off, tail + off, v);
           continue;
         }
         if (residual) {
-          const bf16x8 r0 = load8(zres + off), r1 = load8(zres + off + 8);
 #pragma unroll
           for (int u = 0; u < 8; ++u) {
-            v[u] += bf2f(r0[u]);
-            v[8 + u] += bf2f(r1[u]);
+            v[u] += bf2f(zr[cb & 1][0][u]);
+            v[8 + u] += bf2f(zr[cb & 1][1][u]);
           }
         }
         store16(out + off, v);

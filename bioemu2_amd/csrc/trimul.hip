@@ -249,14 +249,30 @@ __global__ __launch_bounds__(kOutThreads) void trimul_out_kernel(
   const size_t plane = (size_t)Np * Np;
   bf16* ob = obuf + wave * kOutTile;
 
-  // Next tile's raw inputs: this lane's x half-row, and o channels
-  // 16 q + (lane >> 2), columns j0 + 8 (lane & 3) .. + 7.  Columns of the last
-  // tile of a row may reach past N but stay below Np (o is Np wide).
-  bf16x8 xraw[8], oraw[8];
+  // Next tile's raw inputs.  o channels 16 q + (lane >> 2), columns
+  // j0 + 8 (lane & 3) .. + 7 go straight from global memory into the wave's
+  // o buffer (buffer loads that write LDS: no registers; instruction q writes
+  // 1 KB contiguously, lane l at obuf_off(16 q + (l >> 2), 8 (l & 3))); this
+  // lane's x half-row (and its tail bytes) go to registers.  Columns of the
+  // last tile of a row may reach past N but stay below Np (o is Np wide).
+  // The o copies are issued first, so the wait for them in prepare() counts
+  // the x / tail loads and the current tile's stores issued after them.
+  bf16x8 xraw[8];
   u32x4 traw[4];
   auto fetch = [&](unsigned tt) {
     const TileIdx ti = split_tile(tt, tiles_per_row, N);
     const int i = ti.row, b = ti.b, j0 = ti.col * 32;
+    const __amdgpu_buffer_rsrc_t ors =
+        buffer_rsrc(o + (size_t)b * D * plane + (size_t)i * Np + j0, (unsigned)(((D - 1) * plane + 32) * 2));
+    const unsigned ovoff = ((unsigned)(lane >> 2) * (unsigned)plane + 8u * (lane & 3)) * 2u;
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          ors, (__attribute__((address_space(3))) void*)(ob + 512 * q + (q >= 4 ? 32 : 0)), 16, ovoff,
+          (unsigned)(16 * q) * (unsigned)plane * 2u, 0, 0);
+    // Nothing may be scheduled above the copies: the wait in prepare() counts
+    // every vector-memory operation issued after them.
+    __builtin_amdgcn_sched_barrier(0);
     const int jj = j0 + perm32(rho);
     const size_t pair = ((size_t)b * N + i) * N + (jj < N ? jj : 0);
     const bf16* xr = x + pair * D + 64 * h;
@@ -266,33 +282,36 @@ __global__ __launch_bounds__(kOutThreads) void trimul_out_kernel(
 #pragma unroll
       for (int q = 0; q < 4; ++q) traw[q] = load_tail16(tail + pair * D + 64 * h + 16 * q);
     }
-    const bf16* orow = o + ((size_t)b * D + (lane >> 2)) * plane + (size_t)i * Np + j0 + 8 * (lane & 3);
-#pragma unroll
-    for (int q = 0; q < 8; ++q) oraw[q] = load8(orow + (size_t)(16 * q) * plane);
   };
-  // Current tile's operands: normalised o and x rows and the raw x half-row.
-  // With kTail, the current tile's tail bytes wait in the first 4 KB of the
-  // wave's o buffer once o has been read from it (registers are full): chunk
-  // q of lane l at 16-byte slot 64 q + l, so each access instruction covers
-  // 1 KB contiguously.
+  // Vector-memory operations issued after a tile's o copies and before its
+  // prepare(): the x (and tail) loads, then (except for a wave's first tile)
+  // the previous tile's stores: two bf16 chunks, plus a tail chunk with kTail,
+  // per output block.
+  constexpr int kAfterLoads = 8 + (kTail ? 4 : 0);
+  constexpr int kAfterOCopies = kAfterLoads + 4 * (kTail ? 3 : 2);
+  // Current tile's operands: normalised o and x rows, the raw x half-row and its tail.
   bf16x8 of[8], xf[8], xres[8];
-  u32x4* tbuf = reinterpret_cast<u32x4*>(ob);
-  auto prepare = [&]() {
-#pragma unroll
-    for (int q = 0; q < 8; ++q) store8(ob + obuf_off(16 * q + (lane >> 2), 8 * (lane & 3)), oraw[q]);
+  u32x4 tres[4];
+  auto prepare = [&](bool first) {
+    // vmcnt <= (loads and stores issued after the o copies): this wave's o copies have landed
+    if (first)
+      __builtin_amdgcn_s_waitcnt(0x0f70 | (kAfterLoads & 15) | ((kAfterLoads >> 4) << 14));
+    else
+      __builtin_amdgcn_s_waitcnt(0x0f70 | (kAfterOCopies & 15) | ((kAfterOCopies >> 4) << 14));
+    __builtin_amdgcn_sched_barrier(0);   // the o reads stay below the wait
     float v[64];
     const int p = perm32(rho);
 #pragma unroll
     for (int c = 0; c < 64; ++c) v[c] = bf2f(ob[obuf_off(64 * h + c, p)]);
-    if (kTail) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) tbuf[64 * q + lane] = traw[q];
-    }
     normalize_half_row(v, of);
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
       unpack8(xraw[s], v + 8 * s);
       xres[s] = xraw[s];
+    }
+    if (kTail) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) tres[q] = traw[q];
     }
     normalize_half_row(v, xf);
   };
@@ -300,7 +319,7 @@ __global__ __launch_bounds__(kOutThreads) void trimul_out_kernel(
   unsigned t = blockIdx.x * kOutWaves + wave;
   if (t < ntiles) {
     fetch(t);
-    prepare();
+    prepare(true);
   }
   for (; t < ntiles; t += stride) {
     const unsigned tn = t + stride;
@@ -319,7 +338,7 @@ __global__ __launch_bounds__(kOutThreads) void trimul_out_kernel(
       for (int u = 0; u < 16; ++u) r[u] = (pa[u] + cl[e0 + u]) * sigmoidf_fast(ga[u] + cl[D + e0 + u]);
       if (kTail) {
         float xv[16];
-        tail_decode16(xres[2 * cb], xres[2 * cb + 1], tbuf[64 * cb + lane], xv);
+        tail_decode16(xres[2 * cb], xres[2 * cb + 1], tres[cb], xv);
 #pragma unroll
         for (int u = 0; u < 16; ++u) r[u] += xv[u];
         int8_t* tdiscard = reinterpret_cast<int8_t*>(discard + 64 * D);
@@ -336,7 +355,7 @@ __global__ __launch_bounds__(kOutThreads) void trimul_out_kernel(
       }
       store16(valid ? out + pair * D + e0 : discard + lane * D + e0, r);
     }
-    if (tn < ntiles) prepare();
+    if (tn < ntiles) prepare(false);
   }
 }
 

@@ -3,9 +3,12 @@
     python -m bioemu2_amd.profiling stats  <kernel_stats.csv> --title T --cmd C [--out F]
     python -m bioemu2_amd.profiling traffic --fetch <counter_collection.csv> --write <counter_collection.csv>
                                             --workload block --calib-bytes B --cmd C [--out F] [--json J]
+    python -m bioemu2_amd.profiling pmc <counter_collection.csv>... --title T --cmd C [--flops k=GF,...]
 
 ``stats`` turns a ``--kernel-trace --stats -f csv`` kernel table into a short
-markdown table.  ``traffic`` turns two ``--pmc FETCH_SIZE`` / ``--pmc
+markdown table.  ``pmc`` averages any ``--pmc`` counters per kernel and adds
+the MFMA-busy fraction (rocprofv3's MfmaUtil formula) and the executed bf16
+MFMA flops.  ``traffic`` turns two ``--pmc FETCH_SIZE`` / ``--pmc
 WRITE_SIZE`` runs of ``bench.py --calibrate-bytes B`` into HBM bytes per launch
 for every kernel: each counter (KiB per dispatch) is scaled by what the same
 counter reads for torch's elementwise negation of a B-byte bf16 tensor, which
@@ -127,6 +130,72 @@ def traffic(fetch_csv: str, write_csv: str, calib_bytes: int) -> tuple[dict, flo
     return table, 1024.0 / f_scale, 1024.0 / w_scale
 
 
+def gpu_agent(counter_csv: str) -> tuple[int, int]:
+    """(SIMD count, XCD count) of the GPU from the ``*_agent_info.csv`` rocprofv3 writes next to the counters
+    (MI355X: 1024 SIMDs, 8 XCDs when the file is absent)."""
+    for f in sorted(Path(counter_csv).parent.glob("*agent_info.csv")):
+        for r in csv.DictReader(open(f)):
+            if r.get("Agent_Type") == "GPU":
+                return int(r["Simd_Count"]), int(r["Num_Xcc"])
+    return 1024, 8
+
+
+def pmc(csv_paths: list[str]) -> tuple[dict[str, dict[str, float]], int]:
+    """Per library kernel (base name): every counter averaged over its dispatches.
+
+    rocprofv3 writes one value per dispatch and counter, summed over the counter's instances (SEs,
+    SIMDs, XCDs); GRBM_GUI_ACTIVE, one per XCD over the same busy window, is therefore divided by the
+    XCD count to give the kernel's busy cycles, and MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES /
+    (busy cycles x SIMDs), rocprofv3's MfmaUtil."""
+    per: dict[str, dict[str, list]] = defaultdict(lambda: defaultdict(lambda: [0.0, set()]))
+    simds = 1024
+    for path in csv_paths:
+        simds, xcc = gpu_agent(path)
+        acc: dict[tuple, float] = defaultdict(float)
+        names: dict[int, str] = {}
+        for r in csv.DictReader(open(path)):
+            if not is_library_kernel(r["Kernel_Name"]):
+                continue
+            d = int(r["Dispatch_Id"])
+            names[d] = base_name(short_name(r["Kernel_Name"]))
+            v = float(r["Counter_Value"])
+            acc[(d, r["Counter_Name"])] += v / xcc if r["Counter_Name"].startswith("GRBM_") else v
+        for (d, c), v in acc.items():
+            e = per[names[d]][c]
+            e[0] += v
+            e[1].add((path, d))
+    out: dict[str, dict[str, float]] = {}
+    for k, counters in per.items():
+        row = {c: tot / len(ds) for c, (tot, ds) in counters.items()}
+        busy, active = row.get("SQ_VALU_MFMA_BUSY_CYCLES"), row.get("GRBM_GUI_ACTIVE")
+        if busy is not None and active:
+            row["mfma_busy_pct"] = 100.0 * busy / (active * simds)
+        if "SQ_INSTS_VALU_MFMA_MOPS_BF16" in row:
+            row["mfma_bf16_flops"] = 512.0 * row["SQ_INSTS_VALU_MFMA_MOPS_BF16"]
+        out[k] = row
+    return out, simds
+
+
+def pmc_markdown(table: dict, title: str, cmd: str, simds: int, flops: dict[str, float]) -> str:
+    counters = sorted({c for row in table.values() for c in row if c.isupper() or c.startswith(("SQ_", "GRBM_"))})
+    out = [f"# {title}", "", "Commands (from the repo root on the MI355X box):", "", "```", cmd, "```", "",
+           f"Per-dispatch averages over every dispatch of each kernel (GRBM_GUI_ACTIVE per XCD).  MFMA busy = "
+           f"SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x {simds} SIMDs) (rocprofv3's MfmaUtil); executed bf16 MFMA flops = "
+           "SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512 (includes non-algorithmic MFMAs); algorithmic = the kernel's "
+           "counted work per launch.", "",
+           "| kernel | MFMA busy % | executed bf16 MFMA GFLOP | algorithmic GFLOP | " + " | ".join(counters) + " |",
+           "|---|---|---|---|" + "---|" * len(counters)]
+    for k, row in sorted(table.items(), key=lambda kv: -kv[1].get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0)):
+        busy = row.get("mfma_busy_pct")
+        fl = row.get("mfma_bf16_flops")
+        alg = flops.get(k)
+        cells = [f"`{k}`", "" if busy is None else f"{busy:.1f}", "" if fl is None else f"{fl / 1e9:.1f}",
+                 "" if alg is None else f"{alg / 1e9:.1f}"]
+        cells += [f"{row[c]:.4g}" if c in row else "" for c in counters]
+        out.append("| " + " | ".join(cells) + " |")
+    return "\n".join(out) + "\n"
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd_name", required=True)
@@ -143,8 +212,18 @@ def main(argv=None) -> int:
     t.add_argument("--cmd", required=True, help="the two rocprofv3 commands, as run")
     t.add_argument("--out")
     t.add_argument("--json", default=str(TRAFFIC_JSON))
+    m = sub.add_parser("pmc")
+    m.add_argument("csv", nargs="+")
+    m.add_argument("--title", required=True)
+    m.add_argument("--cmd", required=True)
+    m.add_argument("--flops", default="", help="kernel=GFLOP,... algorithmic work per launch, for the table")
+    m.add_argument("--out")
     a = ap.parse_args(argv)
-    if a.cmd_name == "stats":
+    if a.cmd_name == "pmc":
+        flops = {kv.split("=")[0]: float(kv.split("=")[1]) * 1e9 for kv in a.flops.split(",") if kv}
+        table, simds = pmc(a.csv)
+        text = pmc_markdown(table, a.title, a.cmd, simds, flops)
+    elif a.cmd_name == "stats":
         text = stats_markdown(a.csv, a.title, a.cmd)
     else:
         table, f_per_kib, w_per_kib = traffic(a.fetch, a.write, a.calib_bytes)
