@@ -50,7 +50,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "bioemu_transition_token_workspace_bytes": (_c_size_t, [_c_int64] * 3),
     "bioemu_transition_token_fwd": (
         _c_int,
-        [_c_void_p] * 8 + [_c_void_p, _c_size_t] + [_c_int64] * 3 + [_c_int, _c_int, _c_void_p],
+        [_c_void_p] * 8 + [_c_void_p, _c_size_t] + [_c_int64] * 4 + [_c_int, _c_int, _c_void_p],
     ),
     "bioemu_pwa_workspace_bytes": (_c_size_t, [_c_int64] * 6),
     "bioemu_pwa_fwd": (

@@ -326,11 +326,12 @@ def launch_transition_token(
     M = x.numel() // D
     dev = x.device
     hidden = fc1_w.shape[0]
+    out_dim = fc3_w.shape[0]
     _check_tensor(x, "transition x", BF16, tuple(x.shape), dev)
-    _check_tensor(out, "transition out", BF16, tuple(x.shape), dev)
+    _check_tensor(out, "transition out", BF16, tuple(x.shape[:-1]) + (out_dim,), dev)
     _check_tensor(fc1_w, "transition fc1.weight", BF16, (hidden, D), dev)
     _check_tensor(fc2_w, "transition fc2.weight", BF16, (hidden, D), dev)
-    _check_tensor(fc3_w, "transition fc3.weight", BF16, (D, hidden), dev)
+    _check_tensor(fc3_w, "transition fc3.weight", BF16, (out_dim, hidden), dev)
     use_norm = norm_w is not None
     if use_norm:
         _check_tensor(norm_w, "transition norm.weight", torch.float32, (D,), dev)
@@ -341,7 +342,8 @@ def launch_transition_token(
         ws = workspace(need, dev)
     rc = lib().bioemu_transition_token_fwd(
         _ptr(x), _ptr(norm_w), _ptr(norm_b), _ptr(fc1_w), _ptr(fc2_w), _ptr(fc3_w), _ptr(out), _ptr(tail),
-        _ptr(ws), ctypes.c_size_t(ws.numel()), M, D, hidden, int(use_norm), int(bool(residual)), _stream(x),
+        _ptr(ws), ctypes.c_size_t(ws.numel()), M, D, hidden, out_dim, int(use_norm), int(bool(residual)),
+        _stream(x),
     )
     check(rc, "bioemu_transition_token_fwd")
     return out
@@ -358,12 +360,13 @@ def transition(
     x: Tensor, norm_w: Tensor | None, norm_b: Tensor | None, fc1_w: Tensor, fc2_w: Tensor, fc3_w: Tensor
 ) -> Tensor:
     xb = x.to(BF16).contiguous()
-    out = torch.empty_like(xb)
+    out_dim = fc3_w.shape[0]
+    out = torch.empty(*xb.shape[:-1], out_dim, dtype=BF16, device=xb.device)
     f32 = torch.float32
     nw = None if norm_w is None else norm_w.to(f32).contiguous()
     nb = None if norm_b is None else norm_b.to(f32).contiguous()
     w1, w2, w3 = (w.to(BF16).contiguous() for w in (fc1_w, fc2_w, fc3_w))
-    if _is_row_transition(xb, w1.shape[0]):
+    if out_dim == xb.shape[-1] and _is_row_transition(xb, w1.shape[0]):
         launch_transition_pair(xb, nw, nb, w1, w2, w3, out)
     else:
         launch_transition_token(xb, nw, nb, w1, w2, w3, out)
@@ -372,7 +375,7 @@ def transition(
 
 @transition.register_fake
 def _(x, norm_w, norm_b, fc1_w, fc2_w, fc3_w):
-    return torch.empty_like(x)
+    return x.new_empty(*x.shape[:-1], fc3_w.shape[0])
 
 
 # ----------------------------------------------------------------------------

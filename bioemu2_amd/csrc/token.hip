@@ -77,6 +77,45 @@ __global__ __launch_bounds__(256) void token_ln_kernel(const bf16* __restrict__ 
   }
 }
 
+// Any width K (a runtime loop over this lane's channels lane, lane + 64, ...):
+// the same rows and padding as token_ln_kernel, for widths outside its
+// compile-time set (the denoiser's token/atom mixers, dim = a_s + atom_s).
+__global__ __launch_bounds__(256) void token_ln_any_kernel(const bf16* __restrict__ x, const float* __restrict__ gamma,
+                                                           const float* __restrict__ beta, bf16* __restrict__ y, int B,
+                                                           int N, int Np, int K, float eps) {
+  const int lane = threadIdx.x & 63;
+  const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= (long long)B * Np) return;
+  const int b = (int)(row / Np), t = (int)(row % Np);
+  bf16* yr = y + (size_t)row * K;
+  if (t >= N) {
+    for (int c = lane; c < K; c += 64) yr[c] = f2bf(0.f);
+    return;
+  }
+  const bf16* xr = x + ((size_t)b * N + t) * K;
+  float s = 0.f;
+  for (int c = lane; c < K; c += 64) s += bf2f(xr[c]);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
+  const float mean = s / (float)K;
+  float ss = 0.f;
+  for (int c = lane; c < K; c += 64) {
+    const float d = bf2f(xr[c]) - mean;
+    ss += d * d;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+  const float rstd = rsqrtf(ss / (float)K + eps);
+  for (int c = lane; c < K; c += 64) {
+    float o = bf2f(xr[c]);
+    if (gamma) {
+      o = (o - mean) * rstd * gamma[c];
+      if (beta) o += beta[c];
+    }
+    yr[c] = f2bf(o);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // out = epilogue(A[M][K] * W[Nout][K]^T) on 32x32 output blocks, 4 waves per
 // workgroup.  The token GEMMs are skinny (a few hundred rows), so for K >= 256
@@ -228,7 +267,9 @@ int token_layernorm(const void* x, const float* gamma, const float* beta, void* 
                          static_cast<bf16*>(y), (int)B, (int)N, (int)Np, 1e-5f);
       break;
     default:
-      return set_error(BIOEMU_ERR_UNSUPPORTED, "token_layernorm: width %lld unsupported (64, 128 or 384)", (long long)K);
+      if (K <= 0) return set_error(BIOEMU_ERR_UNSUPPORTED, "token_layernorm: width %lld unsupported", (long long)K);
+      hipLaunchKernelGGL(token_ln_any_kernel, grid, dim3(256), 0, stream, static_cast<const bf16*>(x), gamma, beta,
+                         static_cast<bf16*>(y), (int)B, (int)N, (int)Np, (int)K, 1e-5f);
   }
   return check_launch("token_layernorm");
 }
@@ -275,11 +316,14 @@ extern "C" size_t bioemu_transition_token_workspace_bytes(int64_t M, int64_t Dc,
 extern "C" int bioemu_transition_token_fwd(const void* x, const float* norm_w, const float* norm_b,
                                            const void* fc1_w, const void* fc2_w, const void* fc3_w, void* out,
                                            int8_t* res_tail, void* workspace, size_t workspace_bytes, int64_t M,
-                                           int64_t Dc, int64_t hidden, int use_norm, int residual,
+                                           int64_t Dc, int64_t hidden, int64_t out_dim, int use_norm, int residual,
                                            hipStream_t stream) {
-  if (M <= 0 || (Dc != 64 && Dc != 128 && Dc != 384) || hidden <= 0 || hidden % 32)
-    return set_error(BIOEMU_ERR_UNSUPPORTED, "transition_token: dim %lld / hidden %lld unsupported", (long long)Dc,
-                     (long long)hidden);
+  if (M <= 0 || Dc <= 0 || Dc % 16 || hidden <= 0 || hidden % 32 || out_dim <= 0 || out_dim % 32)
+    return set_error(BIOEMU_ERR_UNSUPPORTED,
+                     "transition_token: dim %lld / hidden %lld / out_dim %lld unsupported (dim a multiple of 16, "
+                     "hidden and out_dim multiples of 32)", (long long)Dc, (long long)hidden, (long long)out_dim);
+  if (residual && out_dim != Dc)
+    return set_error(BIOEMU_ERR_INVALID_ARG, "transition_token: residual=1 needs out_dim == dim");
   if (!x || !fc1_w || !fc2_w || !fc3_w || !out || !workspace || (use_norm && !norm_w))
     return set_error(BIOEMU_ERR_INVALID_ARG, "transition_token: null pointer argument");
   if (!aligned16(x) || !aligned16(out) || !aligned16(fc1_w) || !aligned16(fc2_w) || !aligned16(fc3_w) ||
@@ -302,5 +346,5 @@ extern "C" int bioemu_transition_token_fwd(const void* x, const float* norm_w, c
                   "transition_token_swiglu");
   if (rc) return rc;
   return token_gemm(residual ? kEpiResidual : kEpiStore, false, hbuf, fc3_w, nullptr, nullptr, x, out, Mp, hidden,
-                    Dc, M, Mp, M, stream, "transition_token_out", res_tail);
+                    out_dim, M, Mp, M, stream, "transition_token_out", res_tail);
 }

@@ -6,7 +6,9 @@ and ``state_dict`` keys (``norm.{weight,bias}`` when ``use_norm``,
 same result ``fc3(silu(fc1(LN x)) * fc2(LN x))`` (:52-76).  Rows of width 128
 (hidden 512: the pair representation) or 64 (hidden 256: the MSA
 representation) run one fused HIP kernel; other widths (the single
-representation, 384) run the token LN + GEMM kernels.
+representation, 384) and ``out_dim != dim`` (the denoiser's token/atom
+mixers, diffusion.py:623-634: dim a multiple of 16, hidden and out_dim
+multiples of 32) run the token LN + GEMM kernels.
 ``chunk_size`` only tiled the hidden dimension for memory in the reference
 (:76-91): the fused kernel never materialises the hidden activations, so it
 is accepted and has no effect on the result.
@@ -33,8 +35,7 @@ class Transition(nn.Module):
     ) -> None:
         super().__init__()
         out_dim = out_dim or dim
-        if out_dim != dim:
-            raise ValueError(f"Transition: out_dim ({out_dim}) != dim ({dim}) is not supported by the HIP kernels")
+        self.out_dim = out_dim
         self.use_norm = use_norm
         self.chunk_size = chunk_size
         if use_norm:

@@ -146,17 +146,21 @@ int bioemu_transition_pair_fwd_noalloc(const void* x, const float* norm_w, const
                                        int residual, hipStream_t stream);
 
 /*
- * Token Transition (same op over [M, D] rows, D in {64, 128, 384}, hidden a
- * multiple of 32): LN kernel + two MFMA GEMMs.  Replaces Transition.forward
- * (transition.py:52-91) for the single representation s and any width /
- * hidden pair the fused row kernel does not take.
+ * Token Transition (same op over [M, D] rows): LN kernel + two MFMA GEMMs.
+ * Replaces Transition.forward (transition.py:52-91) for the single
+ * representation s and any width / hidden / output width the fused row kernel
+ * does not take, including out_dim != D (the denoiser's token/atom mixers,
+ * Transition(dim=a_s+atom_s, out_dim=atom_s or a_s, use_norm=False),
+ * diffusion.py:623-634).  D a multiple of 16; hidden and out_dim multiples of
+ * 32.  x: [M, D]; fc1_w, fc2_w: [hidden, D]; fc3_w: [out_dim, hidden];
+ * out: [M, out_dim].  residual=1 needs out_dim == D.
  * res_tail: NULL or the [M, D] int8 tail of the residual stream (residual=1).
  */
 size_t bioemu_transition_token_workspace_bytes(int64_t M, int64_t D, int64_t hidden);
 int bioemu_transition_token_fwd(const void* x, const float* norm_w, const float* norm_b,
                                 const void* fc1_w, const void* fc2_w, const void* fc3_w, void* out,
                                 int8_t* res_tail, void* workspace, size_t workspace_bytes, int64_t M, int64_t D,
-                                int64_t hidden, int use_norm, int residual, hipStream_t stream);
+                                int64_t hidden, int64_t out_dim, int use_norm, int residual, hipStream_t stream);
 
 /*
  * Pair-weighted averaging (MSA module), fused: LN_m -> v = Wm m', g = sigmoid(Wg m');

@@ -200,3 +200,25 @@ def test_pair_transition_residual_and_rowwise(gpu_device):
         _ops.launch_transition_pair(xx, *m.prepared_params(), xx, residual=True)
     ref = x.float() + upd.float()
     assert max_abs(xx.float(), ref) <= 2 ** -7 * ref.abs().max().item()
+
+
+@pytest.mark.parametrize(
+    "dim,hidden,out_dim,use_norm",
+    [(512, 1024, 128, False), (512, 1024, 384, False), (96, 192, 96, True), (160, 320, 64, True)],
+)
+def test_transition_out_dim_and_any_width(gpu_device, dim, hidden, out_dim, use_norm):
+    """Transition(dim, hidden, out_dim, use_norm) at the denoiser's mixer shapes (diffusion.py:623-634:
+    dim = a_s + atom_s, out_dim = atom_s or a_s, no LayerNorm) and widths outside the fused kernel's set."""
+    torch.manual_seed(3)
+    m = Transition(dim, hidden, out_dim=out_dim, use_norm=use_norm)
+    if use_norm:
+        with torch.no_grad():
+            m.norm.weight.normal_(1.0, 0.1)
+            m.norm.bias.normal_(0.0, 0.1)
+    m = m.to(gpu_device)
+    x = torch.randn(3, 37, dim, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16).to(gpu_device)
+    with torch.no_grad():
+        got = m(x).float().cpu()
+    assert got.shape == (3, 37, out_dim)
+    want = oracle.transition(x.cpu(), state(m), use_norm=use_norm)
+    _check(got, want, f"transition {dim}->{out_dim} hidden={hidden} norm={use_norm}")

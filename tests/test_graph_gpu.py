@@ -1,11 +1,12 @@
 """The in-place Pairformer block captured in a HIP graph and replayed.
 
 ``PairformerBlockHip.forward_`` launches only kernels on torch's current
-stream (no memsets, host copies or synchronisations) and reuses the workspace,
-masks and prepared weights it cached on its first call, so after one eager
-call at a shape it can be captured with ``torch.cuda.graph``.  Every replay
-must be bit-identical to the eager block on the same inputs, with unrelated
-eager work and synchronisations between replays.
+stream (no memsets, host copies or synchronisations).  ``capture()`` prepares
+the weights outside the capture, gives the graph a workspace of its own and
+keeps every buffer a replay touches alive.  Every replay must be bit-identical
+to the eager block on the same inputs, with unrelated eager work, eager blocks
+at a larger shape (which replace the block's cached workspace) and
+synchronisations between replays; with and without residual tails.
 """
 
 from __future__ import annotations
@@ -40,13 +41,12 @@ def _eager(blk, s, z, tok, steps):
 
 def test_block_graph_replays_match_eager(gpu_device):
     blk, s0, z0, tok = _setup(gpu_device)
-    want = _eager(blk, s0, z0, tok, steps=2)  # also caches workspace, masks and weights
+    want = _eager(blk, s0, z0, tok, steps=2)
 
     s_g, z_g = s0.clone(), z0.clone()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        blk.forward_(s_g, z_g, tok)
+    graph = blk.capture(s_g, z_g, tok)
     torch.cuda.synchronize()
+    big = _setup(gpu_device, n=160, n_pad=0)
 
     other = torch.randn(1 << 20, device=gpu_device)
     for rep in range(3):
@@ -59,6 +59,7 @@ def test_block_graph_replays_match_eager(gpu_device):
         # Eager work between replays: unrelated torch ops and an eager block on other buffers.
         other.mul_(1.0001).add_(0.5)
         _eager(blk, s0, z0, tok, steps=1)
+        _eager(blk, big[1], big[2], big[3], steps=1)
         torch.cuda.synchronize()
 
     # Chained replays: the second replay reads the first one's in-place output.
@@ -69,3 +70,23 @@ def test_block_graph_replays_match_eager(gpu_device):
     torch.cuda.synchronize()
     print("graph replay: two chained steps", flush=True)
     assert torch.equal(s_g, want[1][0]) and torch.equal(z_g, want[1][1])
+
+
+def test_block_graph_with_tails(gpu_device):
+    """The tail-carrying stream under a graph: replays equal the eager ``forward_`` with tails, bit for bit."""
+    from bioemu2_amd.residual import split_stream
+
+    blk, s0, z0, tok = _setup(gpu_device, n=64, n_pad=3, seed=4)
+    s0, z0 = s0.float() * 1.37, z0.float() * 0.71           # values with non-zero tails
+    (sh, st), (zh, zt) = split_stream(s0), split_stream(z0)
+    e = [t.clone() for t in (sh, zh, st, zt)]
+    blk.forward_(e[0], e[1], tok, e[2], e[3])
+    g = [t.clone() for t in (sh, zh, st, zt)]
+    graph = blk.capture(g[0], g[1], tok, g[2], g[3])
+    for rep in range(2):
+        for dst, src in zip(g, (sh, zh, st, zt)):
+            dst.copy_(src)
+        graph.replay()
+        torch.cuda.synchronize()
+        print(f"graph replay {rep} with tails", flush=True)
+        assert all(torch.equal(a, b) for a, b in zip(g, e))

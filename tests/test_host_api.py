@@ -143,6 +143,10 @@ def test_cpu_tensors_are_rejected_without_fallback():
         PairMixerMSALayerHip(384, 64, C, 0.15, 0.25)(None, z, m, pm, torch.ones(1, 4, 8, dtype=torch.bool))
 
 
-def test_transition_rejects_out_dim():
-    with pytest.raises(ValueError):
-        Transition(C, 4 * C, out_dim=64)
+def test_transition_out_dim_matches_reference_layout():
+    """Transition(dim, hidden, out_dim, use_norm=False) as the denoiser's mixers build it (diffusion.py:623-634):
+    no norm.* keys, fc3 maps hidden -> out_dim (transition.py:34-50)."""
+    t = Transition(512, 1024, out_dim=128, use_norm=False)
+    sd = t.state_dict()
+    assert sorted(sd) == ["fc1.weight", "fc2.weight", "fc3.weight"]
+    assert sd["fc1.weight"].shape == (1024, 512) and sd["fc3.weight"].shape == (128, 1024)
