@@ -191,6 +191,7 @@ def main() -> int:
             "launches_per_step": n / args.steps,
             "avg_ms": round(avg, 5),
             "bound": b,
+            "work": a,
             "rate": round(rate, 1),
             "frac": round(rate / (PEAK_BF16_TFLOPS if b == "mfma" else PEAK_HBM_GBS), 4),
         }

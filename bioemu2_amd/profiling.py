@@ -3,7 +3,7 @@
     python -m bioemu2_amd.profiling stats  <kernel_stats.csv> --title T --cmd C [--out F]
     python -m bioemu2_amd.profiling traffic --fetch <counter_collection.csv> --write <counter_collection.csv>
                                             --workload block --calib-bytes B --cmd C [--out F] [--json J]
-    python -m bioemu2_amd.profiling pmc <counter_collection.csv>... --title T --cmd C [--flops k=GF,...]
+    python -m bioemu2_amd.profiling pmc <counter_collection.csv>... --title T --cmd C [--bench F] [--flops k=GF,...]
 
 ``stats`` turns a ``--kernel-trace --stats -f csv`` kernel table into a short
 markdown table.  ``pmc`` averages any ``--pmc`` counters per kernel and adds
@@ -196,6 +196,22 @@ def pmc_markdown(table: dict, title: str, cmd: str, simds: int, flops: dict[str,
     return "\n".join(out) + "\n"
 
 
+def bench_flops(path: str) -> dict[str, float]:
+    """Algorithmic flops per launch of every MFMA-bound kernel in a ``bench.py`` output line (the last JSON
+    line of ``path``), keyed by kernel base name.  Timers that share a kernel (two transition shapes) are
+    averaged weighted by launches, as the counters average over every dispatch."""
+    line = [ln for ln in open(path) if ln.startswith("{")][-1]
+    acc: dict[str, list[float]] = defaultdict(lambda: [0.0, 0.0])
+    for timer, v in json.loads(line)["kernels"].items():
+        if v.get("bound") != "mfma":
+            continue
+        work = v["work"] if "work" in v else v["rate"] * v["avg_ms"] * 1e9
+        e = acc[TIMER_TO_KERNEL.get(timer, timer)]
+        e[0] += work * v["launches_per_step"]
+        e[1] += v["launches_per_step"]
+    return {k: tot / n for k, (tot, n) in acc.items()}
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd_name", required=True)
@@ -217,10 +233,12 @@ def main(argv=None) -> int:
     m.add_argument("--title", required=True)
     m.add_argument("--cmd", required=True)
     m.add_argument("--flops", default="", help="kernel=GFLOP,... algorithmic work per launch, for the table")
+    m.add_argument("--bench", help="a bench.py output file: algorithmic flops per launch of its MFMA kernels")
     m.add_argument("--out")
     a = ap.parse_args(argv)
     if a.cmd_name == "pmc":
-        flops = {kv.split("=")[0]: float(kv.split("=")[1]) * 1e9 for kv in a.flops.split(",") if kv}
+        flops = bench_flops(a.bench) if a.bench else {}
+        flops.update({kv.split("=")[0]: float(kv.split("=")[1]) * 1e9 for kv in a.flops.split(",") if kv})
         table, simds = pmc(a.csv)
         text = pmc_markdown(table, a.title, a.cmd, simds, flops)
     elif a.cmd_name == "stats":
