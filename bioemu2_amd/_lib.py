@@ -80,6 +80,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "bioemu_stream_split": (_c_int, [_c_void_p] * 3 + [_c_int64, _c_void_p]),
     "bioemu_stream_join": (_c_int, [_c_void_p] * 3 + [_c_int64, _c_void_p]),
+    "bioemu_pair_ln_linear_workspace_bytes": (_c_size_t, [_c_int64]),
+    "bioemu_pair_ln_linear_fwd": (_c_int, [_c_void_p] * 9 + [_c_size_t, _c_int64, _c_int64, _c_void_p]),
+    "bioemu_token_ln_linear_workspace_bytes": (_c_size_t, [_c_int64] * 2),
+    "bioemu_token_ln_linear_fwd": (_c_int, [_c_void_p] * 9 + [_c_size_t, _c_int64, _c_int64, _c_void_p]),
+    "bioemu_msa_embed_workspace_bytes": (_c_size_t, [_c_int64] * 2),
+    "bioemu_msa_embed_fwd": (_c_int, [_c_void_p] * 10 + [_c_size_t] + [_c_int64] * 6 + [_c_void_p]),
 }
 
 _lock = threading.Lock()

@@ -813,3 +813,82 @@ def outer_product_mean(
 def _(m, mask, norm_w, norm_b, w_ab, w_o, b_o):
     B, S, N, _ = m.shape
     return m.new_empty(B, N, N, w_o.shape[0])
+
+
+# ----------------------------------------------------------------------------
+# PairMixer trunk glue: recycling updates and the MSA input embedding
+# ----------------------------------------------------------------------------
+def launch_ln_linear(
+    x: Tensor,
+    norm_w: Tensor,
+    norm_b: Tensor,
+    w: Tensor,
+    base: Tensor,
+    out: Tensor,
+    base_tail: Tensor | None = None,
+    out_tail: Tensor | None = None,
+    ws: Tensor | None = None,
+) -> Tensor:
+    """``out = base + w LN(x)`` over rows (the recycling update, pairmixer.py:281-282): pair rows of 128
+    channels (4-d x) through the pair kernel, token rows (3-d x) through the token LayerNorm + GEMM."""
+    require_gpu(x, "ln_linear")
+    D = x.shape[-1]
+    M = x.numel() // D
+    dev = x.device
+    for t, what in ((x, "x"), (base, "base"), (out, "out")):
+        _check_tensor(t, f"ln_linear {what}", BF16, tuple(x.shape), dev)
+    _check_tensor(w, "ln_linear weight", BF16, (D, D), dev)
+    _check_tensor(norm_w, "ln_linear norm.weight", torch.float32, (D,), dev)
+    _check_tensor(norm_b, "ln_linear norm.bias", torch.float32, (D,), dev)
+    for t, what in ((base_tail, "base tail"), (out_tail, "out tail")):
+        if t is not None:
+            _check_tensor(t, f"ln_linear {what}", torch.int8, tuple(x.shape), dev)
+    pair = x.dim() == 4
+    need = (lib().bioemu_pair_ln_linear_workspace_bytes(D) if pair
+            else lib().bioemu_token_ln_linear_workspace_bytes(M, D))
+    if ws is None or ws.numel() < need:
+        ws = workspace(need, dev)
+    fn = lib().bioemu_pair_ln_linear_fwd if pair else lib().bioemu_token_ln_linear_fwd
+    rc = fn(_ptr(x), _ptr(norm_w), _ptr(norm_b), _ptr(w), _ptr(base), _ptr(base_tail), _ptr(out), _ptr(out_tail),
+            _ptr(ws), ctypes.c_size_t(ws.numel()), M, D, _stream(x))
+    check(rc, "bioemu_pair_ln_linear_fwd" if pair else "bioemu_token_ln_linear_fwd")
+    return out
+
+
+def launch_msa_embed(
+    msa: Tensor,
+    has_deletion: Tensor,
+    deletion_value: Tensor,
+    msa_paired: Tensor | None,
+    emb: Tensor,
+    w_msa: Tensor,
+    w_s: Tensor,
+    m: Tensor,
+    m_tail: Tensor,
+    ws: Tensor | None = None,
+) -> Tensor:
+    """MSA input embedding (pairmixer.py:591-599) into the MSA stream ``m`` (bf16) and its int8 tail."""
+    require_gpu(msa, "msa_embed")
+    B, R, T, F0 = msa.shape
+    E = emb.shape[-1]
+    C = w_msa.shape[0]
+    dev = msa.device
+    f32 = torch.float32
+    _check_tensor(msa, "msa_embed msa", f32, (B, R, T, F0), dev)
+    for t, what in ((has_deletion, "has_deletion"), (deletion_value, "deletion_value"), (msa_paired, "msa_paired")):
+        if t is not None:
+            _check_tensor(t, f"msa_embed {what}", f32, (B, R, T), dev)
+    _check_tensor(emb, "msa_embed emb", f32, (B, T, E), dev)
+    _check_tensor(w_msa, "msa_embed msa_proj.weight", f32, (C, F0 + 2 + int(msa_paired is not None)), dev)
+    _check_tensor(w_s, "msa_embed s_proj.weight", f32, (C, E), dev)
+    _check_tensor(m, "msa_embed m", BF16, (B, R, T, C), dev)
+    _check_tensor(m_tail, "msa_embed m tail", torch.int8, (B, R, T, C), dev)
+    need = lib().bioemu_msa_embed_workspace_bytes(B, T)
+    if ws is None or ws.numel() < need:
+        ws = workspace(need, dev)
+    rc = lib().bioemu_msa_embed_fwd(
+        _ptr(msa), _ptr(has_deletion), _ptr(deletion_value), _ptr(msa_paired), _ptr(emb), _ptr(w_msa), _ptr(w_s),
+        _ptr(m), _ptr(m_tail), _ptr(ws), ctypes.c_size_t(ws.numel()), B, R, T, F0, E, C, _stream(msa),
+    )
+    check(rc, "bioemu_msa_embed_fwd")
+    return m

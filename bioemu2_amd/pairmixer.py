@@ -72,12 +72,14 @@ class PairMixerLayerHip(nn.Module, _WorkspaceMixin):
 
     @torch.no_grad()
     def forward_(
-        self, s: Tensor, z: Tensor, pair_mask: Tensor, z_tail: Tensor | None = None
+        self, s: Tensor, z: Tensor, pair_mask: Tensor, z_tail: Tensor | None = None, ws: Tensor | None = None
     ) -> tuple[Tensor, Tensor]:
-        """In place on bf16 ``z [B,T,T,token_z]`` (and its int8 tail, if given); ``s`` passes through."""
+        """In place on bf16 ``z [B,T,T,token_z]`` (and its int8 tail, if given); ``s`` passes through.
+        ``ws``: a caller-owned workspace of ``workspace_bytes`` (default: one cached per layer)."""
         _ops.require_gpu(z, type(self).__name__)
         B, N = z.shape[0], z.shape[1]
-        ws = self._workspace(self.workspace_bytes(B, N), z.device)
+        if ws is None:
+            ws = self._workspace(self.workspace_bytes(B, N), z.device)
         pm = _ops.mask_u8(pair_mask)
         _ops.launch_trimul(z, pm, *self.tri_mul_out.prepared_params(), z, True, residual=True, ws=ws, tail=z_tail)
         _ops.launch_trimul(z, pm, *self.tri_mul_in.prepared_params(), z, False, residual=True, ws=ws, tail=z_tail)
@@ -141,12 +143,14 @@ class PairMixerMSALayerHip(nn.Module, _WorkspaceMixin):
         chunk_heads_pwa: bool = False,
         z_tail: Tensor | None = None,
         m_tail: Tensor | None = None,
+        ws: Tensor | None = None,
     ) -> tuple[Tensor, Tensor, Tensor]:
         """In place on bf16 ``z [B,T,T,token_z]`` and ``m [B,S,T,msa_s]`` (and their int8 tails, if given);
-        ``s`` passes through."""
+        ``s`` passes through.  ``ws``: a caller-owned workspace of ``workspace_bytes`` (default: cached)."""
         _ops.require_gpu(z, type(self).__name__)
         B, S, N = m.shape[0], m.shape[1], m.shape[2]
-        ws = self._workspace(self.workspace_bytes(B, S, N), z.device)
+        if ws is None:
+            ws = self._workspace(self.workspace_bytes(B, S, N), z.device)
         pm = _ops.mask_u8(token_mask)
         _ops.launch_pwa(m, z, pm, *self.pair_weighted_averaging.prepared_params(), m, 8, residual=True, ws=ws,
                         tail=m_tail)
@@ -165,3 +169,213 @@ class PairMixerMSALayerHip(nn.Module, _WorkspaceMixin):
         (z_hi, z_tail), (m_hi, m_tail) = split_stream(z), split_stream(m)
         self.forward_(s, z_hi, m_hi, token_mask, msa_mask, chunk_heads_pwa, z_tail, m_tail)
         return s, join_stream(z_hi, z_tail, z.dtype), join_stream(m_hi, m_tail, m.dtype)
+
+
+NUM_TOKENS = 33   # len(Token) of the reference's token vocabulary (data_interface/const.py:23-57)
+
+
+class PairMixerModuleHip(nn.Module, _WorkspaceMixin):
+    """``PairMixerModule`` (pairmixer.py:299-370): ``num_blocks`` PairMixer layers in order, with the same
+    constructor kwargs and ``layers.{i}.*`` keys.  ``forward_`` runs them in place on one z stream (and its
+    tail) with one workspace shared by every layer."""
+
+    def __init__(
+        self,
+        token_s: int,
+        token_z: int,
+        num_blocks: int,
+        dropout: float = 0.25,
+        trimul_variant: str = "cueq",
+        trimul_tile_size: int | None = None,
+        transition_chunk_size: int | None = None,
+        trimul_matmul_precision: str | None = None,
+    ) -> None:
+        super().__init__()
+        self.token_z = token_z
+        self.num_blocks = num_blocks
+        self.dropout = dropout
+        self.layers = nn.ModuleList([
+            PairMixerLayerHip(token_s, token_z, dropout, trimul_variant=trimul_variant,
+                              trimul_tile_size=trimul_tile_size, transition_chunk_size=transition_chunk_size,
+                              trimul_matmul_precision=trimul_matmul_precision)
+            for _ in range(num_blocks)
+        ])
+        self._ws = None
+
+    def workspace_bytes(self, B: int, N: int) -> int:
+        return self.layers[0].workspace_bytes(B, N) if len(self.layers) else 16
+
+    @torch.no_grad()
+    def forward_(self, s: Tensor, z: Tensor, pair_mask: Tensor, z_tail: Tensor | None = None,
+                 ws: Tensor | None = None) -> tuple[Tensor, Tensor]:
+        _ops.require_gpu(z, type(self).__name__)
+        if ws is None:
+            ws = self._workspace(self.workspace_bytes(z.shape[0], z.shape[1]), z.device)
+        pm = pair_mask.bool()
+        for layer in self.layers:   # pairmixer.py:368-369
+            layer.forward_(s, z, pm, z_tail, ws=ws)
+        return s, z
+
+    def forward(self, s: Tensor, z: Tensor, pair_mask: Tensor) -> tuple[Tensor, Tensor]:
+        z_hi, z_tail = split_stream(z)
+        self.forward_(s, z_hi, pair_mask, z_tail)
+        return s, join_stream(z_hi, z_tail, z.dtype)
+
+
+class PairMixerMSAModuleHip(nn.Module, _WorkspaceMixin):
+    """``PairMixerMSAModule`` (pairmixer.py:459-611): same constructor kwargs and keys (``s_proj``,
+    ``msa_proj``, ``layers.{i}.*``).  The input embedding m = msa_proj(cat(msa, has_deletion,
+    deletion_value[, msa_paired])) + s_proj(emb) is one fp32 HIP kernel writing the MSA stream (bf16 + tail);
+    the MSA layers then update z and m in place.  The projection weights are kept in fp32 like the reference's
+    parameters; the feature tensors are taken as fp32."""
+
+    def __init__(
+        self,
+        token_s: int,
+        msa_s: int,
+        token_z: int,
+        s_input_dim: int,
+        msa_blocks: int,
+        msa_dropout: float,
+        z_dropout: float,
+        use_paired_feature: bool = False,
+        trimul_variant: str = "cueq",
+        trimul_tile_size: int | None = None,
+        transition_chunk_size: int | None = None,
+        opm_variant: str = "vanilla",
+        opm_tile_size: int | None = None,
+        pwa_chunk_heads: bool = False,
+        opm_matmul_precision: str | None = None,
+        trimul_matmul_precision: str | None = None,
+        num_tokens: int = NUM_TOKENS,
+    ) -> None:
+        super().__init__()
+        self.msa_s, self.token_z = msa_s, token_z
+        self.msa_blocks = msa_blocks
+        self.msa_dropout = msa_dropout
+        self.z_dropout = z_dropout
+        self.use_paired_feature = use_paired_feature
+        self.pwa_chunk_heads = pwa_chunk_heads
+        self.s_proj = nn.Linear(s_input_dim, msa_s, bias=False)
+        self.msa_proj = nn.Linear(num_tokens + 2 + int(use_paired_feature), msa_s, bias=False)
+        self.layers = nn.ModuleList([
+            PairMixerMSALayerHip(token_s, msa_s, token_z, msa_dropout, z_dropout, trimul_variant=trimul_variant,
+                                 trimul_tile_size=trimul_tile_size, transition_chunk_size=transition_chunk_size,
+                                 opm_variant=opm_variant, opm_tile_size=opm_tile_size,
+                                 opm_matmul_precision=opm_matmul_precision,
+                                 trimul_matmul_precision=trimul_matmul_precision)
+            for _ in range(msa_blocks)
+        ])
+        self._ws = None
+
+    def workspace_bytes(self, B: int, S: int, N: int) -> int:
+        layer = self.layers[0].workspace_bytes(B, S, N) if len(self.layers) else 16
+        return max(layer, int(_ops.lib().bioemu_msa_embed_workspace_bytes(B, N)))
+
+    def embed(self, emb: Tensor, msa: Tensor, has_deletion: Tensor, deletion_value: Tensor, msa_paired: Tensor,
+              ws: Tensor | None = None) -> tuple[Tensor, Tensor]:
+        """The MSA stream (m [B,R,T,msa_s] bf16, its int8 tail) from the features (pairmixer.py:591-599)."""
+        B, R, T = msa.shape[:3]
+        f32 = torch.float32
+        m = torch.empty(B, R, T, self.msa_s, dtype=torch.bfloat16, device=msa.device)
+        m_tail = torch.empty(B, R, T, self.msa_s, dtype=torch.int8, device=msa.device)
+        _ops.launch_msa_embed(
+            msa.to(f32).contiguous(), has_deletion.to(f32).contiguous(), deletion_value.to(f32).contiguous(),
+            msa_paired.to(f32).contiguous() if self.use_paired_feature else None, emb.to(f32).contiguous(),
+            self.msa_proj.weight.to(f32).contiguous(), self.s_proj.weight.to(f32).contiguous(), m, m_tail, ws=ws)
+        return m, m_tail
+
+    @torch.no_grad()
+    def forward_(self, z: Tensor, emb: Tensor, msa: Tensor, msa_mask: Tensor, has_deletion: Tensor,
+                 deletion_value: Tensor, msa_paired: Tensor, token_pad_mask: Tensor, z_tail: Tensor | None = None,
+                 ws: Tensor | None = None) -> Tensor:
+        """In place on the bf16 pair stream ``z`` (and its tail); returns z."""
+        _ops.require_gpu(z, type(self).__name__)
+        B, R, T = msa.shape[:3]
+        if ws is None:
+            ws = self._workspace(self.workspace_bytes(B, R, T), z.device)
+        m, m_tail = self.embed(emb, msa, has_deletion, deletion_value, msa_paired, ws=ws)
+        tok = token_pad_mask.bool()
+        pm = tok[:, :, None] & tok[:, None, :]                       # :589
+        for layer in self.layers:                                     # :602-610
+            layer.forward_(None, z, m, pm, msa_mask, False, z_tail, m_tail, ws=ws)
+        return z
+
+    def forward(self, s, z, emb, msa, msa_mask, has_deletion, deletion_value, msa_paired, token_pad_mask):
+        z_hi, z_tail = split_stream(z)
+        self.forward_(z_hi, emb, msa, msa_mask, has_deletion, deletion_value, msa_paired, token_pad_mask, z_tail)
+        return s, join_stream(z_hi, z_tail, z.dtype)
+
+
+class PairMixerTrunkHip(nn.Module, _WorkspaceMixin):
+    """The trunk of ``PairMixerSequenceEmbedder`` (pairmixer.py:23-296) from the initial embeddings on.
+
+    Submodules carry the reference's names (``s_recycle``, ``z_recycle``, ``s_norm``, ``z_norm``,
+    ``msa_module``, ``pairmixer_module``), so the trunk part of a reference state_dict loads unchanged
+    (``strict=False`` skips the embedder's input layers, relative-position encoder and conditioning, which
+    stay with the caller).  ``forward(s_init, z_init, s_inputs, feats, num_steps_recycle)`` runs the recycling
+    loop of :275-296: s and z start at zero; every pass sets s = s_init + s_recycle(s_norm(s)) and
+    z = z_init + z_recycle(z_norm(z)), runs the MSA module (single updates off) and the PairMixer stack.
+    z is carried as one bf16 + tail stream through every pass; s and z come back in s_init's / z_init's dtype.
+    """
+
+    def __init__(
+        self,
+        token_s: int,
+        token_z: int,
+        s_input_dim: int,
+        msa_s: int = 64,
+        msa_blocks: int = 4,
+        msa_dropout: float = 0.15,
+        z_dropout: float = 0.25,
+        num_blocks: int = 48,
+        dropout: float = 0.0,
+        trimul_variant: str = "cueq",
+        opm_variant: str = "vanilla",
+        use_paired_feature: bool = True,
+        num_tokens: int = NUM_TOKENS,
+    ) -> None:
+        super().__init__()
+        self.msa_module = PairMixerMSAModuleHip(token_s, msa_s, token_z, s_input_dim, msa_blocks, msa_dropout,
+                                                z_dropout, use_paired_feature=use_paired_feature,
+                                                trimul_variant=trimul_variant, opm_variant=opm_variant,
+                                                num_tokens=num_tokens)
+        self.pairmixer_module = PairMixerModuleHip(token_s, token_z, num_blocks, dropout,
+                                                   trimul_variant=trimul_variant)
+        self.s_recycle = nn.Linear(token_s, token_s, bias=False)     # :186-191
+        self.z_recycle = nn.Linear(token_z, token_z, bias=False)
+        self.s_norm = nn.LayerNorm(token_s)
+        self.z_norm = nn.LayerNorm(token_z)
+        self._ws = None
+
+    def workspace_bytes(self, B: int, S: int, N: int, token_s: int) -> int:
+        return max(self.msa_module.workspace_bytes(B, S, N), self.pairmixer_module.workspace_bytes(B, N),
+                   int(_ops.lib().bioemu_pair_ln_linear_workspace_bytes(self.z_recycle.in_features)),
+                   int(_ops.lib().bioemu_token_ln_linear_workspace_bytes(B * N, token_s)))
+
+    @torch.no_grad()
+    def forward(self, s_init: Tensor, z_init: Tensor, s_inputs: Tensor, feats: dict,
+                num_steps_recycle: int = 0) -> tuple[Tensor, Tensor]:
+        if num_steps_recycle < 0:
+            raise ValueError("num_steps_recycle must be non-negative; use unconditional=True.")
+        _ops.require_gpu(z_init, type(self).__name__)
+        B, N = z_init.shape[:2]
+        S = feats["msa"].shape[1]
+        ws = self._workspace(self.workspace_bytes(B, S, N, s_init.shape[-1]), z_init.device)
+        bf16 = torch.bfloat16
+        (s0, s0_tail), (z0, z0_tail) = split_stream(s_init), split_stream(z_init)
+        s, s_tail = torch.zeros_like(s0), torch.zeros_like(s0_tail)   # :257-258
+        z, z_tail = torch.zeros_like(z0), torch.zeros_like(z0_tail)
+        tok = feats["token_pad_mask"].bool()
+        pm = tok[:, :, None] & tok[:, None, :]                          # :263-264
+        f32 = torch.float32
+        norm = lambda m: (m.weight.to(f32).contiguous(), m.bias.to(f32).contiguous())  # noqa: E731
+        w_s, w_z = self.s_recycle.weight.to(bf16).contiguous(), self.z_recycle.weight.to(bf16).contiguous()
+        for _ in range(num_steps_recycle + 1):                          # :275
+            _ops.launch_ln_linear(s, *norm(self.s_norm), w_s, s0, s, base_tail=s0_tail, out_tail=s_tail, ws=ws)
+            _ops.launch_ln_linear(z, *norm(self.z_norm), w_z, z0, z, base_tail=z0_tail, out_tail=z_tail, ws=ws)
+            self.msa_module.forward_(z, s_inputs, feats["msa"], feats["msa_mask"], feats["has_deletion"],
+                                     feats["deletion_value"], feats.get("msa_paired"), feats["token_pad_mask"],
+                                     z_tail, ws=ws)                     # :284-294
+            self.pairmixer_module.forward_(s, z, pm, z_tail, ws=ws)    # :296
+        return join_stream(s, s_tail, s_init.dtype), join_stream(z, z_tail, z_init.dtype)

@@ -1,7 +1,10 @@
 """Synthetic, HBM-resident workloads for the benchmark configs.
 
 Each workload owns its seeded inputs, random-init weights, preallocated
-outputs and workspaces, so ``step()`` launches kernels and allocates nothing.
+outputs and workspaces, so ``step()`` launches kernels and allocates nothing
+(except the out-of-place ones: config 1 and the PairMixer trunk pass build
+their fp32 <-> bf16 + tail streams through torch's caching allocator, as a
+caller of ``forward`` would).
 ``kernel_work(name)`` gives the algorithmic work of one launch of a named
 kernel at the workload's shape: ``("mfma", flops)`` or ``("hbm", bytes)``,
 chosen by comparing the kernel's flops per minimum HBM byte with the MI355X
@@ -289,6 +292,25 @@ class BlockWorkload(Workload):
         if kernel in token_bytes:
             return ("hbm", float(token_bytes[kernel]))
         raise KeyError(kernel)
+
+
+class Config1Workload(BlockWorkload):
+    """Config 1: the reference's CPU-runnable case, one block at N=64 with fp32 z [1,64,64,128] and
+    s [1,64,384], all tokens valid.  A step is the out-of-place ``forward``: fp32 in, streams split into
+    bf16 + tail, the block, fp32 out.  The CPU baseline is the whole fp32 oracle block at the same size."""
+
+    def __init__(self, device, n: int = 64, seed: int = 0):
+        super().__init__(device, n, seed)
+        self.n_pad = 0
+        self.tok = token_mask(n, 0, device)
+        self.name = f"pairformer_block_n{n}_fp32io"
+        self.metric = f"ms per Pairformer block at N={n}, fp32 in/out"
+        self.config = dict(self.config, workload=self.name, padded_tokens=0, io="fp32")
+        self.s32 = self.s_cpu.float().to(device)
+        self.z32 = self.z_cpu.float().to(device)
+
+    def step(self) -> None:
+        self.module(self.s32, self.z32, self.tok)
 
 
 class TrunkWorkload(BlockWorkload):
@@ -592,6 +614,128 @@ class PairMixerMsaWorkload(Workload):
         raise KeyError(kernel)
 
 
+class PairMixerTrunkWorkload(Workload):
+    """The reference's sequence trunk from its initial embeddings on (PairMixerSequenceEmbedder.forward,
+    pairmixer.py:275-296) at N=768 (76 padded tokens), S=1024 MSA rows (20 % masked): one pass
+    (num_steps_recycle = 0) = the recycling updates, the MSA module (input embedding + 4 MSA layers) and the
+    48-layer PairMixer stack, z carried as one bf16 + int8-tail stream."""
+
+    cpu_warmup = 0
+    cpu_calls = 1
+
+    def __init__(self, device, n: int = 768, S: int = 1024, blocks: int = 48, msa_blocks: int = 4,
+                 seed: int = 0):
+        from .pairmixer import NUM_TOKENS, PairMixerTrunkHip
+
+        self.n, self.S, self.blocks, self.msa_blocks = n, S, blocks, msa_blocks
+        self.name = f"pairmixer_trunk{blocks}_msa{msa_blocks}_s{S}_n{n}"
+        self.metric = f"ms per PairMixer trunk pass ({msa_blocks} MSA + {blocks} layers) at S={S}, N={n} bf16"
+        torch.manual_seed(seed)
+        self.module = init_module(PairMixerTrunkHip(384, 128, 455, msa_blocks=msa_blocks, num_blocks=blocks),
+                                  seed).to(device).eval()
+        g = torch.Generator().manual_seed(seed)
+        self.n_pad = n // 10
+        tok = token_mask(n, self.n_pad, "cpu")
+        rows = torch.rand(S, generator=g) >= 0.2
+        self.s_valid = int(rows.sum())
+        self.s_init = torch.randn(1, n, 384, generator=g).to(torch.bfloat16).to(device)
+        self.z_cpu = torch.randn(1, n, n, 128, generator=g).to(torch.bfloat16)
+        self.z_init = self.z_cpu.to(device)
+        self.emb = torch.randn(1, n, 455, generator=g).to(device)
+        aa = torch.randint(0, NUM_TOKENS, (1, S, n), generator=g)
+        self.feats_cpu = {
+            "msa": torch.nn.functional.one_hot(aa, NUM_TOKENS).float(),
+            "has_deletion": (torch.rand(1, S, n, generator=g) < 0.1).float(),
+            "deletion_value": torch.rand(1, S, n, generator=g),
+            "msa_paired": (torch.rand(1, S, n, generator=g) < 0.5).float(),
+            "msa_mask": rows[None, :, None] & tok[:, None, :],
+            "token_pad_mask": tok,
+        }
+        self.feats = {k: v.to(device) for k, v in self.feats_cpu.items()}
+        self.pm_cpu = tok[:, :, None] & tok[:, None, :]
+        self.config = {"workload": self.name, "N": n, "S": S, "msa_blocks": msa_blocks, "blocks": blocks,
+                       "num_steps_recycle": 0, "c_z": 128, "c_m": 64, "c_s": 384, "batch": 1,
+                       "padded_tokens": self.n_pad, "valid_msa_rows": self.s_valid,
+                       "residual_stream": "bf16 + int8 tail"}
+        P = n * n
+        trimul = 2.0 * P * 128 * 6 * 128 + 2.0 * 128 * n ** 3
+        layer = 2 * trimul + 2.0 * P * 128 * 12 * 128
+        pwa = 2.0 * S * n * 64 * 512 + 2.0 * 8 * n * n * S * 32 + 2.0 * S * n * 256 * 64
+        msa_tr = 2.0 * S * n * 64 * 12 * 64
+        opm = 2.0 * P * 1024 * self.s_valid + 2.0 * P * 1024 * 128
+        recycle = 2.0 * P * 128 * 128 + 2.0 * n * 384 * 384
+        self.flops = blocks * layer + msa_blocks * (pwa + msa_tr + opm + layer) + recycle
+
+    def step(self) -> None:
+        self.module(self.s_init, self.z_init, self.emb, self.feats, 0)
+
+    def cpu_sample(self, oracle):
+        """fp32 oracle ops, each timed once and scaled to the pass: one PairMixer layer at full N (x 48, and
+        the same three z updates inside each of the 4 MSA layers), PWA + MSA transition on 16 of S MSA rows
+        and the OPM on 64 of N output rows (x 4, scaled to the full sizes), the two recycling updates."""
+        rows, opm_rows = 16, 64
+        params = {k: v.detach().cpu() for k, v in self.module.state_dict().items()}
+
+        def sub(prefix):
+            return {k[len(prefix) + 1:]: v for k, v in params.items() if k.startswith(prefix + ".")}
+
+        z = self.z_cpu.float()
+        s = self.s_init.float().cpu()
+        msa = sub("msa_module")
+        layer0 = sub("msa_module.layers.0")
+
+        def fn():
+            t0 = time.perf_counter()
+            oracle.ln_linear(z, z, params, "z_norm", "z_recycle")
+            oracle.ln_linear(s, s, params, "s_norm", "s_recycle")
+            f = self.feats_cpu
+            m = oracle.msa_embed(f["msa"][:, :rows], f["has_deletion"][:, :rows], f["deletion_value"][:, :rows],
+                                 f["msa_paired"][:, :rows], self.emb.cpu(), msa)
+            t1 = time.perf_counter()
+            m = m + oracle.pair_weighted_averaging(m, z, self.pm_cpu, {k[len("pair_weighted_averaging") + 1:]: v
+                                                                       for k, v in layer0.items()
+                                                                       if k.startswith("pair_weighted_averaging.")})
+            m = m + oracle.transition(m, {k[len("msa_transition") + 1:]: v for k, v in layer0.items()
+                                          if k.startswith("msa_transition.")})
+            t2 = time.perf_counter()
+            m_full = torch.randn(1, self.S, self.n, 64)
+            oracle.outer_product_mean(m_full, f["msa_mask"], {k[len("outer_product_mean") + 1:]: v
+                                                              for k, v in layer0.items()
+                                                              if k.startswith("outer_product_mean.")},
+                                      i_chunk=opm_rows, i_stop=opm_rows)
+            t3 = time.perf_counter()
+            oracle.pairmixer_layer(s, z, self.pm_cpu, sub("pairmixer_module.layers.0"))
+            t4 = time.perf_counter()
+            return ((t1 - t0) + self.msa_blocks * ((t2 - t1) * self.S / rows + (t3 - t2) * self.n / opm_rows)
+                    + (self.blocks + self.msa_blocks) * (t4 - t3))
+
+        return fn, None, (f"fp32 oracle ops scaled to one pass: PairMixer layer at full N x "
+                          f"{self.blocks + self.msa_blocks}; PWA + MSA transition on {rows} of {self.S} rows and "
+                          f"OPM on {opm_rows} of {self.n} output rows x {self.msa_blocks}; recycling updates")
+
+    def kernel_work(self, kernel: str) -> tuple[str, float]:
+        n, S, L = self.n, self.S, self.blocks + self.msa_blocks
+        w = trimul_kernel_work(kernel, 1, n)
+        if w is not None:
+            return w
+        if kernel == "transition_pair":
+            return ("mfma", 2.0 * n * n * 128 * 12 * 128)
+        if kernel == "opm_fused":
+            return ("mfma", 2.0 * n * n * 1024 * self.s_valid + 2.0 * n * n * 1024 * 128)
+        if kernel in ("pwa_weights", "pwa_proj", "pwa_fused"):
+            return PwaWorkload.kernel_work(self, kernel)
+        if kernel == "transition_msa":
+            return ("mfma", 2.0 * S * n * 64 * 12 * 64)
+        if kernel == "pair_ln_linear":
+            return ("hbm", float(n * n * 128 * (2 + 3 + 3)))   # x, base + tail in; out + tail
+        if kernel == "msa_embed":
+            return ("hbm", float(S * n * (33 + 3) * 4 + S * n * 64 * 3))
+        if kernel == "fold_ln":   # pair transitions (L), PWA (3) + MSA transition per MSA layer, z recycle
+            mb = self.msa_blocks
+            return fold_kernel_work(kernel, L + 4 * mb + 1, L * 1024 + 8 * mb + 128, mb * 1024)
+        raise KeyError(kernel)
+
+
 class SwaWorkload(Workload):
     """The denoiser's atom transformer attention (AttentionPairBiasSlidingWindow as AttentionLayer builds it,
     transformer.py:96-105: initial_norm=False): NA = 6144 atoms (NW = 192 windows of W = 32, H = 128 keys),
@@ -816,6 +960,10 @@ def make(op: str, device, n: int | None = None) -> Workload:
         return BlockWorkload(device, n or 768)
     if op == "block_bf16stream":   # the same block with plain bf16 residual streams (no tails)
         return BlockWorkload(device, n or 768, tails=False)
+    if op == "config1":            # the reference's CPU case: N = 64, fp32 in/out
+        return Config1Workload(device, n or 64)
+    if op == "pairmixer_trunk":    # recycling + MSA module (4 layers) + 48 PairMixer layers, one pass
+        return PairMixerTrunkWorkload(device, n or 768)
     if op == "trunk":              # config 5: 48 blocks at N = 2048
         return TrunkWorkload(device, n or 2048)
     if op in ("triatt_start", "triatt_end"):

@@ -278,6 +278,48 @@ int bioemu_opm_fwd(const void* m, const uint8_t* mask, int mean_rows, const floa
 int bioemu_stream_split(const float* x, void* hi, int8_t* tail, int64_t n, hipStream_t stream);
 int bioemu_stream_join(const void* hi, const int8_t* tail, float* out, int64_t n, hipStream_t stream);
 
+/*
+ * Trunk recycling update, pair form: out = base + W LN(x) over P rows of 128
+ * channels.  Replaces `z = z_init + self.z_recycle(self.z_norm(z))`
+ * (src/bioemu2/biomoa/modules/pairmixer.py:282-283; LayerNorm(token_z) and
+ * Linear(token_z, token_z, bias=False) at :186-191).  x, base, out bf16
+ * [P][128]; norm_w/norm_b fp32 [128]; W bf16 [128][128].  base_tail / out_tail
+ * (int8, optional, independently) carry base and out as residual streams.
+ * out may alias x or base.  workspace: bioemu_pair_ln_linear_workspace_bytes.
+ */
+size_t bioemu_pair_ln_linear_workspace_bytes(int64_t Dc);
+int bioemu_pair_ln_linear_fwd(const void* x, const float* norm_w, const float* norm_b, const void* w,
+                              const void* base, const int8_t* base_tail, void* out, int8_t* out_tail,
+                              void* workspace, size_t workspace_bytes, int64_t P, int64_t Dc, hipStream_t stream);
+
+/*
+ * Trunk recycling update, token form: out = base + W LN(x) over M rows of Dc
+ * channels (Dc a multiple of 32).  Replaces `s = s_init + self.s_recycle(
+ * self.s_norm(s))` (pairmixer.py:281; LayerNorm(token_s), Linear(token_s,
+ * token_s, bias=False) at :186-190).  base_tail and out_tail (int8) are both
+ * given or both NULL; out may alias x.  workspace: *_workspace_bytes(M, Dc).
+ */
+size_t bioemu_token_ln_linear_workspace_bytes(int64_t M, int64_t Dc);
+int bioemu_token_ln_linear_fwd(const void* x, const float* norm_w, const float* norm_b, const void* w,
+                               const void* base, const int8_t* base_tail, void* out, int8_t* out_tail,
+                               void* workspace, size_t workspace_bytes, int64_t M, int64_t Dc, hipStream_t stream);
+
+/*
+ * MSA input embedding.  Replaces PairMixerMSAModule.forward's
+ *   m = msa_proj(cat(msa, has_deletion, deletion_value[, msa_paired])) + s_proj(emb)[:, None]
+ * (pairmixer.py:591-599; bias-free Linear layers at :527-532).  msa fp32
+ * [B][R][T][F0]; has_deletion, deletion_value, msa_paired (optional) fp32
+ * [B][R][T]; emb fp32 [B][T][E]; w_msa fp32 [msa_s][F0 + 2 (+1)]; w_s fp32
+ * [msa_s][E]; msa_s = 64, F0 + 3 <= 64.  m is written as the MSA residual
+ * stream: bf16 [B][R][T][64] plus its int8 tail.  Computed in fp32.
+ * workspace: bioemu_msa_embed_workspace_bytes(B, T).
+ */
+size_t bioemu_msa_embed_workspace_bytes(int64_t B, int64_t T);
+int bioemu_msa_embed_fwd(const float* msa, const float* has_deletion, const float* deletion_value,
+                         const float* msa_paired, const float* emb, const float* w_msa, const float* w_s, void* m,
+                         int8_t* m_tail, void* workspace, size_t workspace_bytes, int64_t B, int64_t R, int64_t T,
+                         int64_t F0, int64_t E, int64_t msa_s, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -61,12 +61,17 @@ from .pairformer_ref import (  # noqa: F401
     attention_pair_bias,
     attention_pair_bias_sliding_window,
     distogram,
+    ln_linear,
+    msa_embed,
     outer_product_mean,
     pair_mask_from_token_mask,
     pair_weighted_averaging,
     pairformer_block,
     pairmixer_layer,
+    pairmixer_module,
     pairmixer_msa_layer,
+    pairmixer_msa_module,
+    pairmixer_trunk,
     pairwise_conditioning,
     sliding_window_keys,
     transition,

@@ -27,6 +27,11 @@ __all__ = [
     "pairmixer_layer",
     "pairmixer_msa_layer",
     "pair_mask_from_token_mask",
+    "ln_linear",
+    "msa_embed",
+    "pairmixer_module",
+    "pairmixer_msa_module",
+    "pairmixer_trunk",
 ]
 
 
@@ -462,7 +467,7 @@ def pairmixer_msa_layer(
     pairmixer.py:589).  m += PWA(m, z, token_mask); m += Transition_m(m);
     z += OPM(m, msa_mask); z += TriMulOut; z += TriMulIn; z += Transition_z.
     """
-    s = _f32(s)
+    s = None if s is None else _f32(s)  # s may be None (the MSA module runs with s=None, :284-294)
     z = _f32(z)
     m = _f32(m)
     pm = token_mask.bool().cpu()
@@ -473,3 +478,81 @@ def pairmixer_msa_layer(
     z = z + trimul(z, pm, _sub(params, "tri_mul_in"), "incoming")  # :751-753
     z = z + transition(z, _sub(params, "z_transition"))  # :755
     return s, z, m
+
+
+# ----------------------------------------------------------------------------
+# PairMixer trunk above the layers
+# ----------------------------------------------------------------------------
+def ln_linear(x: Tensor, base: Tensor, params: dict, norm: str, linear: str) -> Tensor:
+    """``base + linear(norm(x))`` with LayerNorm (affine) and a bias-free Linear: the recycling updates
+    ``s = s_init + s_recycle(s_norm(s))`` and ``z = z_init + z_recycle(z_norm(z))``
+    (biomoa/modules/pairmixer.py:281-282; layers at :186-191)."""
+    x = _f32(x)
+    return _f32(base) + _ln(x, params, norm) @ _p(params, linear + ".weight").T
+
+
+def msa_embed(
+    msa: Tensor,
+    has_deletion: Tensor,
+    deletion_value: Tensor,
+    msa_paired: Tensor | None,
+    emb: Tensor,
+    params: dict,
+) -> Tensor:
+    """PairMixerMSAModule input projections (pairmixer.py:591-599):
+    m = msa_proj(cat(msa, has_deletion, deletion_value[, msa_paired])) + s_proj(emb)[:, None]."""
+    feats = [_f32(msa), _f32(has_deletion)[..., None], _f32(deletion_value)[..., None]]
+    if msa_paired is not None:
+        feats.append(_f32(msa_paired)[..., None])
+    m = torch.cat(feats, dim=-1) @ _p(params, "msa_proj.weight").T  # :591-598
+    return m + (_f32(emb) @ _p(params, "s_proj.weight").T).unsqueeze(1)  # :599
+
+
+def pairmixer_module(s: Tensor, z: Tensor, pair_mask: Tensor, params: dict, num_blocks: int) -> tuple[Tensor, Tensor]:
+    """PairMixerModule.forward (pairmixer.py:352-370): the layers in order, ``layers.{i}.*``."""
+    for i in range(num_blocks):
+        s, z = pairmixer_layer(s, z, pair_mask, _sub(params, f"layers.{i}"))
+    return _f32(s), _f32(z)
+
+
+def pairmixer_msa_module(
+    z: Tensor,
+    emb: Tensor,
+    feats: dict,
+    token_pad_mask: Tensor,
+    params: dict,
+    msa_blocks: int,
+) -> Tensor:
+    """PairMixerMSAModule.forward (pairmixer.py:553-611) with ``s=None``: embed the MSA, then run the MSA
+    layers (``layers.{i}.*``, :602-610) with the pair mask mask_i & mask_j (:589); returns z."""
+    m = msa_embed(feats["msa"], feats["has_deletion"], feats["deletion_value"], feats.get("msa_paired"), emb, params)
+    pm = pair_mask_from_token_mask(token_pad_mask.cpu())
+    z = _f32(z)
+    for i in range(msa_blocks):
+        _, z, m = pairmixer_msa_layer(None, z, m, pm, feats["msa_mask"], _sub(params, f"layers.{i}"))
+    return z
+
+
+def pairmixer_trunk(
+    s_init: Tensor,
+    z_init: Tensor,
+    s_inputs: Tensor,
+    feats: dict,
+    params: dict,
+    num_blocks: int,
+    msa_blocks: int,
+    num_steps_recycle: int = 0,
+) -> tuple[Tensor, Tensor]:
+    """The recycling loop of PairMixerSequenceEmbedder.forward (pairmixer.py:275-296) from the initial
+    embeddings on: s and z start at zero (:257-258); each pass recycles them (``s_norm``/``s_recycle``,
+    ``z_norm``/``z_recycle``), runs ``msa_module`` (s = None) and then ``pairmixer_module``."""
+    s_init, z_init = _f32(s_init), _f32(z_init)
+    s, z = torch.zeros_like(s_init), torch.zeros_like(z_init)  # :257-258
+    pm = pair_mask_from_token_mask(feats["token_pad_mask"].cpu())  # :263-264
+    for _ in range(num_steps_recycle + 1):
+        s = ln_linear(s, s_init, params, "s_norm", "s_recycle")  # :281
+        z = ln_linear(z, z_init, params, "z_norm", "z_recycle")  # :282
+        z = pairmixer_msa_module(z, s_inputs, feats, feats["token_pad_mask"], _sub(params, "msa_module"),
+                                 msa_blocks)  # :284-294
+        s, z = pairmixer_module(s, z, pm, _sub(params, "pairmixer_module"), num_blocks)  # :296
+    return s, z

@@ -1,0 +1,174 @@
+"""The PairMixer trunk above the layers on the GPU vs the fp32 CPU oracle.
+
+Covers the recycling updates (``bioemu_pair_ln_linear_fwd`` / ``bioemu_token_ln_linear_fwd``), the MSA input
+embedding (``bioemu_msa_embed_fwd``), ``PairMixerModuleHip`` (the layer stack), ``PairMixerMSAModuleHip``
+and the recycling loop of ``PairMixerTrunkHip`` (pairmixer.py:275-296, :352-370, :553-611).  Streams carry
+int8 tails, so the bf16 bound (max-abs 2e-2, rel-L2 1e-2) holds on every valid element; the MSA embedding is
+fp32 arithmetic and is held to ~2^-15 relative (its output is the bf16 + tail stream).
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import oracle
+from bioemu2_amd import _ops
+from bioemu2_amd.pairmixer import NUM_TOKENS, PairMixerModuleHip, PairMixerMSAModuleHip, PairMixerTrunkHip
+from bioemu2_amd.residual import join_stream, split_stream
+from bioemu2_amd.workloads import init_module
+from tests._helpers import max_abs, rel_l2, state
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(name, got, want, sel=None):
+    g, w = got.float().cpu(), want.float()
+    if sel is not None:
+        g, w = g[sel], w[sel]
+    err, rl2 = max_abs(g, w), rel_l2(g, w)
+    print(f"{name}: max_abs={err:.3e} rel_l2={rl2:.3e} |want|max={w.abs().max():.2f}", flush=True)
+    assert err <= 2e-2 and rl2 <= 1e-2, (name, err, rl2)
+
+
+def _randn(shape, g, scale=1.0):
+    return (torch.randn(*shape, generator=g) * scale).to(torch.bfloat16).float()
+
+
+def _tok(B, n, n_pad):
+    tok = torch.ones(B, n, dtype=torch.bool)
+    if n_pad:
+        tok[:, n - n_pad:] = False
+    return tok
+
+
+def _feats(B, R, T, n_pad, g, device):
+    tok = torch.randint(0, NUM_TOKENS, (B, R, T), generator=g)
+    f = {
+        "msa": torch.nn.functional.one_hot(tok, NUM_TOKENS).float(),
+        "has_deletion": (torch.rand(B, R, T, generator=g) < 0.3).float(),
+        "deletion_value": torch.rand(B, R, T, generator=g),
+        "msa_paired": (torch.rand(B, R, T, generator=g) < 0.5).float(),
+        "msa_mask": torch.rand(B, R, T, generator=g) > 0.2,
+        "token_pad_mask": _tok(B, T, n_pad),
+    }
+    return f, {k: v.to(device) for k, v in f.items()}
+
+
+@pytest.mark.parametrize("tails", [False, True])
+def test_pair_ln_linear_matches_oracle(gpu_device, tails):
+    g = torch.Generator().manual_seed(0)
+    P = 37 * 41                                     # not a multiple of the 32-row tile
+    x, base = _randn((1, 37, 41, 128), g), _randn((1, 37, 41, 128), g, 3.0)
+    prm = {"z_norm.weight": 1 + 0.1 * torch.randn(128, generator=g), "z_norm.bias": 0.1 * torch.randn(128, generator=g),
+           "z_recycle.weight": torch.randn(128, 128, generator=g) / 11.3}
+    want = oracle.ln_linear(x, base, prm, "z_norm", "z_recycle")
+    d = gpu_device
+    xs = x.to(torch.bfloat16).to(d)
+    w = prm["z_recycle.weight"].to(torch.bfloat16).to(d)
+    nw, nb = prm["z_norm.weight"].to(d), prm["z_norm.bias"].to(d)
+    if tails:
+        b_hi, b_tail = split_stream(base.to(d))
+        out, out_tail = torch.empty_like(b_hi), torch.empty_like(b_tail)
+        _ops.launch_ln_linear(xs, nw, nb, w, b_hi, out, base_tail=b_tail, out_tail=out_tail)
+        got = join_stream(out, out_tail)
+        # in place on x (z = z_init + z_recycle(z_norm(z)) overwrites z)
+        xi = xs.clone()
+        xi_tail = torch.empty(xi.shape, dtype=torch.int8, device=d)
+        _ops.launch_ln_linear(xi, nw, nb, w, b_hi, xi, base_tail=b_tail, out_tail=xi_tail)
+        assert torch.equal(xi, out) and torch.equal(xi_tail, out_tail)
+    else:
+        out = torch.empty_like(xs)
+        _ops.launch_ln_linear(xs, nw, nb, w, base.to(torch.bfloat16).to(d), out)
+        got = out
+    assert P == got[0].numel() // 128
+    _check(f"pair_ln_linear tails={tails}", got, want)
+
+
+def test_token_ln_linear_matches_oracle(gpu_device):
+    g = torch.Generator().manual_seed(1)
+    x, base = _randn((2, 50, 384), g), _randn((2, 50, 384), g, 2.0)
+    prm = {"s_norm.weight": 1 + 0.1 * torch.randn(384, generator=g), "s_norm.bias": 0.1 * torch.randn(384, generator=g),
+           "s_recycle.weight": torch.randn(384, 384, generator=g) / 19.6}
+    want = oracle.ln_linear(x, base, prm, "s_norm", "s_recycle")
+    d = gpu_device
+    xs = x.to(torch.bfloat16).to(d)
+    b_hi, b_tail = split_stream(base.to(d))
+    out, out_tail = torch.empty_like(b_hi), torch.empty_like(b_tail)
+    _ops.launch_ln_linear(xs, prm["s_norm.weight"].to(d), prm["s_norm.bias"].to(d),
+                          prm["s_recycle.weight"].to(torch.bfloat16).to(d), b_hi, out, base_tail=b_tail,
+                          out_tail=out_tail)
+    _check("token_ln_linear", join_stream(out, out_tail), want)
+    assert torch.equal(b_hi, split_stream(base.to(d))[0])       # base untouched
+
+
+@pytest.mark.parametrize("paired", [True, False])
+def test_msa_embed_matches_oracle(gpu_device, paired):
+    g = torch.Generator().manual_seed(2)
+    B, R, T, E = 2, 7, 45, 455
+    f, fd = _feats(B, R, T, 0, g, gpu_device)
+    emb = torch.randn(B, T, E, generator=g)
+    wm = torch.randn(64, NUM_TOKENS + 2 + int(paired), generator=g)
+    ws = torch.randn(64, E, generator=g) / 21.0
+    want = oracle.msa_embed(f["msa"], f["has_deletion"], f["deletion_value"], f["msa_paired"] if paired else None,
+                            emb, {"msa_proj.weight": wm, "s_proj.weight": ws})
+    m = torch.empty(B, R, T, 64, dtype=torch.bfloat16, device=gpu_device)
+    m_tail = torch.empty(B, R, T, 64, dtype=torch.int8, device=gpu_device)
+    _ops.launch_msa_embed(fd["msa"], fd["has_deletion"], fd["deletion_value"], fd["msa_paired"] if paired else None,
+                          emb.to(gpu_device), wm.to(gpu_device), ws.to(gpu_device), m, m_tail)
+    got = join_stream(m, m_tail).cpu()
+    err = (got - want).abs().max().item()
+    print(f"msa_embed paired={paired}: max_abs={err:.3e} |want|max={want.abs().max():.2f}", flush=True)
+    torch.testing.assert_close(got, want, rtol=1e-4, atol=1e-5)
+
+
+def test_pairmixer_module_matches_oracle(gpu_device):
+    n, n_pad, blocks = 64, 6, 2
+    torch.manual_seed(0)
+    mod = init_module(PairMixerModuleHip(384, 128, blocks), 0).to(gpu_device).eval()
+    g = torch.Generator().manual_seed(3)
+    s, z = _randn((1, n, 384), g), _randn((1, n, n, 128), g)
+    tok = _tok(1, n, n_pad)
+    pm = oracle.pair_mask_from_token_mask(tok)
+    s_got, z_got = mod(s.to(gpu_device), z.to(gpu_device), pm.to(gpu_device))
+    s_want, z_want = oracle.pairmixer_module(s, z, pm, state(mod), blocks)
+    assert torch.equal(s_got.cpu(), s)
+    _check("pairmixer_module z", z_got, z_want, pm)
+
+
+def test_pairmixer_msa_module_matches_oracle(gpu_device):
+    B, R, T, n_pad, E, blocks = 1, 16, 48, 5, 455, 2
+    torch.manual_seed(0)
+    mod = init_module(PairMixerMSAModuleHip(384, 64, 128, E, blocks, 0.15, 0.25, use_paired_feature=True), 0)
+    mod = mod.to(gpu_device).eval()
+    g = torch.Generator().manual_seed(4)
+    f, fd = _feats(B, R, T, n_pad, g, gpu_device)
+    emb = torch.randn(B, T, E, generator=g)
+    z = _randn((B, T, T, 128), g)
+    _, z_got = mod(None, z.to(gpu_device), emb.to(gpu_device), fd["msa"], fd["msa_mask"], fd["has_deletion"],
+                   fd["deletion_value"], fd["msa_paired"], fd["token_pad_mask"])
+    z_want = oracle.pairmixer_msa_module(z, emb, f, f["token_pad_mask"], state(mod), blocks)
+    _check("pairmixer_msa_module z", z_got, z_want, oracle.pair_mask_from_token_mask(f["token_pad_mask"]))
+
+
+@pytest.mark.parametrize("recycles", [0, 1])
+def test_pairmixer_trunk_matches_oracle(gpu_device, recycles):
+    B, R, T, n_pad, E = 1, 8, 40, 4, 455
+    torch.manual_seed(0)
+    mod = init_module(PairMixerTrunkHip(384, 128, E, msa_blocks=1, num_blocks=2), 0).to(gpu_device).eval()
+    g = torch.Generator().manual_seed(5)
+    f, fd = _feats(B, R, T, n_pad, g, gpu_device)
+    s_init, z_init = _randn((B, T, 384), g), _randn((B, T, T, 128), g)
+    emb = torch.randn(B, T, E, generator=g)
+    s_got, z_got = mod(s_init.to(gpu_device), z_init.to(gpu_device), emb.to(gpu_device), fd, recycles)
+    assert s_got.dtype == torch.float32 and z_got.dtype == torch.float32
+    s_want, z_want = oracle.pairmixer_trunk(s_init, z_init, emb, f, state(mod), 2, 1, recycles)
+    tok = f["token_pad_mask"]
+    _check(f"trunk recycles={recycles} z", z_got, z_want, oracle.pair_mask_from_token_mask(tok))
+    _check(f"trunk recycles={recycles} s", s_got, s_want, tok)
+
+
+def test_trunk_rejects_negative_recycles(gpu_device):
+    mod = PairMixerTrunkHip(384, 128, 455, msa_blocks=1, num_blocks=1).to(gpu_device)
+    with pytest.raises(ValueError, match="non-negative"):
+        mod(None, None, None, {}, -1)
