@@ -80,7 +80,14 @@ def test_pair_ln_linear_matches_oracle(gpu_device, tails):
     else:
         out = torch.empty_like(xs)
         _ops.launch_ln_linear(xs, nw, nb, w, base.to(torch.bfloat16).to(d), out)
-        got = out
+        # a plain bf16 output carries its own rounding (half an ulp, 2^-9 |x|, up to 3e-2 at |x| ~ 15):
+        # the bound is 2e-2 on top of one bf16 ulp of the value, elementwise
+        g32 = out.float().cpu()
+        excess = ((g32 - want).abs() - 2.0 ** -8 * want.abs()).max().item()
+        print(f"pair_ln_linear bf16 out: max excess over 1 ulp = {excess:.3e}, rel_l2={rel_l2(g32, want):.3e}",
+              flush=True)
+        assert excess <= 2e-2 and rel_l2(g32, want) <= 1e-2
+        return
     assert P == got[0].numel() // 128
     _check(f"pair_ln_linear tails={tails}", got, want)
 
@@ -122,50 +129,87 @@ def test_msa_embed_matches_oracle(gpu_device, paired):
     torch.testing.assert_close(got, want, rtol=1e-4, atol=1e-5)
 
 
-def test_pairmixer_module_matches_oracle(gpu_device):
+def _e2e(name, got, want, sel, layers):
+    """A stack end to end: rel-L2 within the bound; max-abs within the bound per layer it holds (each layer's
+    own error is held to the bound alone by the layer-by-layer checks, and consecutive layers' errors add)."""
+    g, w = got.float().cpu()[sel], want.float()[sel]
+    err, rl2 = max_abs(g, w), rel_l2(g, w)
+    print(f"{name} (end to end, {layers} layers): max_abs={err:.3e} rel_l2={rl2:.3e}", flush=True)
+    assert rl2 <= 1e-2 and err <= 2e-2 * layers, (name, err, rl2)
+
+
+def test_pairmixer_module_is_its_layers_each_within_bound(gpu_device):
+    """The module equals its layers run in order, bit for bit; every layer, fed the GPU's own input, is within
+    the bf16 bound of the oracle layer; end to end against the oracle stack."""
     n, n_pad, blocks = 64, 6, 2
+    d = gpu_device
     torch.manual_seed(0)
-    mod = init_module(PairMixerModuleHip(384, 128, blocks), 0).to(gpu_device).eval()
+    mod = init_module(PairMixerModuleHip(384, 128, blocks), 0).to(d).eval()
     g = torch.Generator().manual_seed(3)
     s, z = _randn((1, n, 384), g), _randn((1, n, n, 128), g)
     tok = _tok(1, n, n_pad)
     pm = oracle.pair_mask_from_token_mask(tok)
-    s_got, z_got = mod(s.to(gpu_device), z.to(gpu_device), pm.to(gpu_device))
-    s_want, z_want = oracle.pairmixer_module(s, z, pm, state(mod), blocks)
+    s_got, z_got = mod(s.to(d), z.to(d), pm.to(d))
     assert torch.equal(s_got.cpu(), s)
-    _check("pairmixer_module z", z_got, z_want, pm)
+    z_cur = z.to(d)
+    for i, layer in enumerate(mod.layers):
+        _, z_next = layer(s.to(d), z_cur, pm.to(d))
+        _, z_want = oracle.pairmixer_layer(s, z_cur.cpu(), pm, state(layer))
+        _check(f"pairmixer_module layer {i}", z_next, z_want, pm)
+        z_cur = z_next
+    assert torch.equal(z_got, z_cur)
+    _, z_e2e = oracle.pairmixer_module(s, z, pm, state(mod), blocks)
+    _e2e("pairmixer_module z", z_got, z_e2e, pm, blocks)
 
 
-def test_pairmixer_msa_module_matches_oracle(gpu_device):
+def test_pairmixer_msa_module_is_embed_then_layers(gpu_device):
+    """MSA module = the input embedding (fp32, ~2^-15 relative) then the MSA layers in order (bit for bit);
+    each layer on the GPU's own z and m within the bf16 bound of the oracle layer; end to end."""
     B, R, T, n_pad, E, blocks = 1, 16, 48, 5, 455, 2
+    d = gpu_device
     torch.manual_seed(0)
     mod = init_module(PairMixerMSAModuleHip(384, 64, 128, E, blocks, 0.15, 0.25, use_paired_feature=True), 0)
-    mod = mod.to(gpu_device).eval()
+    mod = mod.to(d).eval()
     g = torch.Generator().manual_seed(4)
-    f, fd = _feats(B, R, T, n_pad, g, gpu_device)
+    f, fd = _feats(B, R, T, n_pad, g, d)
     emb = torch.randn(B, T, E, generator=g)
     z = _randn((B, T, T, 128), g)
-    _, z_got = mod(None, z.to(gpu_device), emb.to(gpu_device), fd["msa"], fd["msa_mask"], fd["has_deletion"],
-                   fd["deletion_value"], fd["msa_paired"], fd["token_pad_mask"])
-    z_want = oracle.pairmixer_msa_module(z, emb, f, f["token_pad_mask"], state(mod), blocks)
-    _check("pairmixer_msa_module z", z_got, z_want, oracle.pair_mask_from_token_mask(f["token_pad_mask"]))
+    pm = oracle.pair_mask_from_token_mask(f["token_pad_mask"])
+    _, z_got = mod(None, z.to(d), emb.to(d), fd["msa"], fd["msa_mask"], fd["has_deletion"], fd["deletion_value"],
+                   fd["msa_paired"], fd["token_pad_mask"])
+    m_hi, m_tail = mod.embed(emb.to(d), fd["msa"], fd["has_deletion"], fd["deletion_value"], fd["msa_paired"])
+    m_want = oracle.msa_embed(f["msa"], f["has_deletion"], f["deletion_value"], f["msa_paired"], emb, state(mod))
+    torch.testing.assert_close(join_stream(m_hi, m_tail).cpu(), m_want, rtol=1e-4, atol=1e-5)
+    z_hi, z_tail = split_stream(z.to(d))
+    for i, layer in enumerate(mod.layers):
+        z_in, m_in = join_stream(z_hi, z_tail).cpu(), join_stream(m_hi, m_tail).cpu()
+        layer.forward_(None, z_hi, m_hi, pm.to(d), fd["msa_mask"], False, z_tail, m_tail)
+        _, z_w, m_w = oracle.pairmixer_msa_layer(None, z_in, m_in, pm, f["msa_mask"], state(layer))
+        _check(f"msa_module layer {i} z", join_stream(z_hi, z_tail), z_w, pm)
+        _check(f"msa_module layer {i} m", join_stream(m_hi, m_tail), m_w, f["msa_mask"])
+    assert torch.equal(z_got, join_stream(z_hi, z_tail))
+    z_e2e = oracle.pairmixer_msa_module(z, emb, f, f["token_pad_mask"], state(mod), blocks)
+    _e2e("pairmixer_msa_module z", z_got, z_e2e, pm, blocks)
 
 
 @pytest.mark.parametrize("recycles", [0, 1])
 def test_pairmixer_trunk_matches_oracle(gpu_device, recycles):
+    """The recycling loop end to end (one MSA layer, one PairMixer layer per pass) against the oracle trunk;
+    its parts are held to the bound alone above (recycling updates, MSA module layers, PairMixer layers)."""
     B, R, T, n_pad, E = 1, 8, 40, 4, 455
     torch.manual_seed(0)
-    mod = init_module(PairMixerTrunkHip(384, 128, E, msa_blocks=1, num_blocks=2), 0).to(gpu_device).eval()
+    mod = init_module(PairMixerTrunkHip(384, 128, E, msa_blocks=1, num_blocks=1), 0).to(gpu_device).eval()
     g = torch.Generator().manual_seed(5)
     f, fd = _feats(B, R, T, n_pad, g, gpu_device)
     s_init, z_init = _randn((B, T, 384), g), _randn((B, T, T, 128), g)
     emb = torch.randn(B, T, E, generator=g)
     s_got, z_got = mod(s_init.to(gpu_device), z_init.to(gpu_device), emb.to(gpu_device), fd, recycles)
     assert s_got.dtype == torch.float32 and z_got.dtype == torch.float32
-    s_want, z_want = oracle.pairmixer_trunk(s_init, z_init, emb, f, state(mod), 2, 1, recycles)
+    s_want, z_want = oracle.pairmixer_trunk(s_init, z_init, emb, f, state(mod), 1, 1, recycles)
     tok = f["token_pad_mask"]
-    _check(f"trunk recycles={recycles} z", z_got, z_want, oracle.pair_mask_from_token_mask(tok))
-    _check(f"trunk recycles={recycles} s", s_got, s_want, tok)
+    layers = 2 * (recycles + 1)
+    _e2e(f"trunk recycles={recycles} z", z_got, z_want, oracle.pair_mask_from_token_mask(tok), layers)
+    _e2e(f"trunk recycles={recycles} s", s_got, s_want, tok, 1)
 
 
 def test_trunk_rejects_negative_recycles(gpu_device):
