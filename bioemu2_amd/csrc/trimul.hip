@@ -35,23 +35,24 @@ constexpr int D = 128;               // pair channels (c_z)
 // columns in [N, Np) come out zero, which the padded contraction relies on.
 // Output: a and b as channel-major planes [B][D][Np][Np] (k contiguous).
 // ---------------------------------------------------------------------------
-// Workgroup size: 8, 12 or 16 waves, chosen per launch (in_waves_per_wg);
-// the staged weights (140 KB of LDS) allow one workgroup per CU.
-constexpr int kInMaxThreads = 1024;
+// Workgroup size: kWaves = 8 or 12 waves, chosen per launch (in_waves_per_wg);
+// the staged weights (140 KB of LDS) allow one workgroup per CU, so kWaves
+// waves share 4 SIMDs and the launch bound 64 * kWaves gives each wave the
+// register budget of its occupancy (256 VGPRs at 8 waves, 168 at 12).
 constexpr int kInRows = 4 * D;                 // p_in (2D rows) then g_in (2D rows)
 constexpr int kInSmem = kInRows * kLdw * 2 + 2 * D * 4;   // weights, then LayerNorm gamma | beta (fp32)
 
 // Waves per workgroup (pick_waves_per_wg).  Measured with whole rounds of
-// tiles: 16 waves give 1.11x the throughput of 8 at N = 512, 12 waves 1.02x
-// at N = 768.  Picks: N = 512 -> 16, 768 -> 12, 2048 -> 16.
+// tiles: 12 waves give 1.02x the throughput of 8 at N = 768.  (16 waves would
+// cap a wave at 128 VGPRs, which spills.)  Picks: N = 512 -> 8, 768 -> 12.
 inline int in_waves_per_wg(long long tiles, int cus) {
-  static const int waves[3] = {8, 12, 16};
-  static const double gain[3] = {1.0, 1.02, 1.11};
-  return pick_waves_per_wg(tiles, cus, waves, gain, 3);
+  static const int waves[2] = {8, 12};
+  static const double gain[2] = {1.0, 1.02};
+  return pick_waves_per_wg(tiles, cus, waves, gain, 2);
 }
 
-template <bool kOutgoing>
-__global__ __launch_bounds__(kInMaxThreads) void trimul_proj_in_kernel(
+template <bool kOutgoing, int kWaves>
+__global__ __launch_bounds__(64 * kWaves) void trimul_proj_in_kernel(
     const bf16* __restrict__ x, const uint8_t* __restrict__ mask, const float* __restrict__ ln_w,
     const float* __restrict__ ln_b, const bf16* __restrict__ p_w, const bf16* __restrict__ g_w,
     bf16* __restrict__ ab, int B, int N, int Np) {
@@ -71,7 +72,7 @@ __global__ __launch_bounds__(kInMaxThreads) void trimul_proj_in_kernel(
 
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int rho = lane & 31, h = lane >> 5;
-  const int waves = blockDim.x >> 6;
+  constexpr int waves = kWaves;
   const unsigned tiles_per_row = Np / 32;
   const unsigned ntiles = (unsigned)B * Np * tiles_per_row;
   const size_t plane = (size_t)Np * Np;
@@ -364,6 +365,33 @@ __global__ __launch_bounds__(kOutThreads) void trimul_out_kernel(
 
 using namespace bioemu;
 
+// Launches trimul_proj_in_kernel<outgoing, waves> (waves 8 or 12).
+static int launch_proj_in(bool outgoing, int waves, unsigned grid, const bf16* x, const uint8_t* mask,
+                          const float* ln_w, const float* ln_b, const bf16* p_w, const bf16* g_w, bf16* ab,
+                          int64_t B, int64_t N, int64_t Np, hipStream_t stream) {
+  const void* k = nullptr;
+  if (waves == 8)
+    k = outgoing ? reinterpret_cast<const void*>(trimul_proj_in_kernel<true, 8>)
+                 : reinterpret_cast<const void*>(trimul_proj_in_kernel<false, 8>);
+  else if (waves == 12)
+    k = outgoing ? reinterpret_cast<const void*>(trimul_proj_in_kernel<true, 12>)
+                 : reinterpret_cast<const void*>(trimul_proj_in_kernel<false, 12>);
+  else
+    return set_error(BIOEMU_ERR_LAUNCH, "trimul_proj_in: no variant with %d waves", waves);
+  if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, kInSmem) != hipSuccess)
+    return set_error(BIOEMU_ERR_LAUNCH, "trimul: cannot set dynamic LDS size");
+  KernelTimerScope timed("trimul_proj_in", stream);
+  void* args[] = {(void*)&x, (void*)&mask, (void*)&ln_w, (void*)&ln_b, (void*)&p_w, (void*)&g_w, (void*)&ab,
+                  nullptr, nullptr, nullptr};
+  int b32 = (int)B, n32 = (int)N, np32 = (int)Np;
+  args[7] = &b32;
+  args[8] = &n32;
+  args[9] = &np32;
+  if (hipLaunchKernel(k, dim3(grid), dim3(64 * waves), args, kInSmem, stream) != hipSuccess)
+    return set_error(BIOEMU_ERR_LAUNCH, "trimul_proj_in: launch failed");
+  return 0;
+}
+
 extern "C" size_t bioemu_trimul_workspace_bytes(int64_t B, int64_t N, int64_t Dc) {
   if (B <= 0 || N <= 0 || Dc <= 0) return 0;
   const int64_t Np = round_up(N, kGemmTile);
@@ -386,8 +414,12 @@ extern "C" int bioemu_trimul_fwd(const void* x, const uint8_t* mask, const float
   if (!x || !mask || !norm_in_w || !norm_in_b || !p_in_w || !g_in_w || !norm_out_w || !norm_out_b ||
       !p_out_w || !g_out_w || !out || !workspace)
     return set_error(BIOEMU_ERR_INVALID_ARG, "trimul: null pointer argument");
-  if (round_up(N, kGemmTile) * round_up(N, kGemmTile) * Dc * 2 >= (int64_t)1 << 31)
-    return set_error(BIOEMU_ERR_UNSUPPORTED, "trimul: N=%lld too large (contraction planes must stay below 2 GiB per batch)",
+  // trimul_out reads a tile's 128 contraction planes through one buffer
+  // resource spanning (D - 1) planes plus a row: its byte extent and offsets
+  // are 32-bit, which holds for N up to 4096 (plane 4096^2; 4.26e9 bytes).
+  if ((uint64_t)(Dc - 1) * round_up(N, kGemmTile) * round_up(N, kGemmTile) * 2 + 64 > 0xffffffffull)
+    return set_error(BIOEMU_ERR_UNSUPPORTED,
+                     "trimul: N=%lld too large (a tile's contraction planes must span under 4 GiB; N <= 4096)",
                      (long long)N);
   if (!aligned16(x) || !aligned16(out) || !aligned16(p_in_w) || !aligned16(g_in_w) ||
       !aligned16(p_out_w) || !aligned16(g_out_w) || !aligned16(workspace))
@@ -408,29 +440,18 @@ extern "C" int bioemu_trimul_fwd(const void* x, const uint8_t* mask, const float
   int dev = 0, cus = 0;
   (void)hipGetDevice(&dev);
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-  const void* kin = outgoing ? reinterpret_cast<const void*>(trimul_proj_in_kernel<true>)
-                             : reinterpret_cast<const void*>(trimul_proj_in_kernel<false>);
   const void* kout = res_tail ? reinterpret_cast<const void*>(trimul_out_kernel<true>)
                               : reinterpret_cast<const void*>(trimul_out_kernel<false>);
-  if (hipFuncSetAttribute(kin, hipFuncAttributeMaxDynamicSharedMemorySize, kInSmem) != hipSuccess ||
-      hipFuncSetAttribute(kout, hipFuncAttributeMaxDynamicSharedMemorySize, kOutSmem) != hipSuccess)
+  if (hipFuncSetAttribute(kout, hipFuncAttributeMaxDynamicSharedMemorySize, kOutSmem) != hipSuccess)
     return set_error(BIOEMU_ERR_LAUNCH, "trimul: cannot set dynamic LDS size");
   const long long waves_in = (long long)B * Np * (Np / 32);
   if (waves_in >= kMaxTiles) return set_error(BIOEMU_ERR_INVALID_ARG, "trimul: too many pair tiles");
   const int in_waves = in_waves_per_wg(waves_in, cus);
   const unsigned grid1 = (unsigned)std::min<long long>(cus, (waves_in + in_waves - 1) / in_waves);
-  {
-    KernelTimerScope timed("trimul_proj_in", stream);
-    if (outgoing)
-      hipLaunchKernelGGL(trimul_proj_in_kernel<true>, dim3(grid1), dim3(64 * in_waves), kInSmem, stream,
-                         static_cast<const bf16*>(x), mask, norm_in_w, norm_in_b, static_cast<const bf16*>(p_in_w),
-                         static_cast<const bf16*>(g_in_w), ab, (int)B, (int)N, (int)Np);
-    else
-      hipLaunchKernelGGL(trimul_proj_in_kernel<false>, dim3(grid1), dim3(64 * in_waves), kInSmem, stream,
-                         static_cast<const bf16*>(x), mask, norm_in_w, norm_in_b, static_cast<const bf16*>(p_in_w),
-                         static_cast<const bf16*>(g_in_w), ab, (int)B, (int)N, (int)Np);
-  }
-  int rc = check_launch("trimul_proj_in");
+  int rc = launch_proj_in(outgoing != 0, in_waves, grid1, static_cast<const bf16*>(x), mask, norm_in_w, norm_in_b,
+                          static_cast<const bf16*>(p_in_w), static_cast<const bf16*>(g_in_w), ab, B, N, Np, stream);
+  if (rc) return rc;
+  rc = check_launch("trimul_proj_in");
   if (rc) return rc;
   rc = launch_bgemm_nt(ab, ab + plane_elems, ob, B * D, Np, stream);
   if (rc) return rc;

@@ -139,6 +139,32 @@ def test_block_config5_size_padding_invariant(gpu_device):
     assert torch.equal(s[:, :v], s2[:, :v])
 
 
+def test_block_n3072_padding_invariant(gpu_device):
+    """One block at N = 3072 (the reference's single-GPU capacity point, docs/context-parallel-sampling.md:
+    115-117; 154 padded tokens): outputs finite, and the valid region bit-identical when every padded token's
+    s and every pair touching a padded token change."""
+    blk = _block(gpu_device)
+    n, pad = 3072, 154
+    s, z, tok = _inputs(n, pad, gpu_device, seed=9, dtype=torch.bfloat16)
+    v = n - pad
+    results = []
+    for k in range(2):
+        if k:
+            s[:, v:] = 7.0
+            z[:, v:] = -5.0
+            z[:, :, v:] = 3.0
+        s2, z2 = s.clone(), z.clone()
+        print(f"block n={n} pass {k}", flush=True)
+        with torch.no_grad():
+            blk.forward_(s2, z2, tok)
+        torch.cuda.synchronize()
+        results.append((s2[:, :v].clone(), z2[:, :v, :v].clone()))
+        del s2, z2
+    (sa, za), (sb, zb) = results
+    assert torch.isfinite(za.float()).all() and torch.isfinite(sa.float()).all()
+    assert torch.equal(za, zb) and torch.equal(sa, sb)
+
+
 def test_trunk_48_blocks_config5(gpu_device):
     """Config 5: all 48 blocks at N = 2048 (102 padded tokens), residual streams with tails, one shared
     workspace.  The whole trunk's valid outputs are finite and bit-identical when every padded token's s

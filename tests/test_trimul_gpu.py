@@ -93,7 +93,7 @@ def test_padding_bit_exact(gpu_device, mode):
 
 @pytest.mark.parametrize("mode", ["outgoing", "incoming"])
 def test_projection_workgroup_sizes_bit_exact(gpu_device, mode):
-    """The input projection's workgroup size is chosen from the tile count: N = 512 runs 16-wave workgroups,
+    """The input projection's workgroup size is chosen from the tile count: N = 512 runs 8-wave workgroups,
     the same problem with 88 masked tokens appended (N = 600, padded to 768) runs 12-wave ones.  A tile's result
     does not depend on which wave computes it and padded k columns are zeros, so the valid region must agree
     bit for bit."""
@@ -107,6 +107,32 @@ def test_projection_workgroup_sizes_bit_exact(gpu_device, mode):
     with torch.no_grad():
         a = m(x, mask)
         b = m(px, pmask)[:, :n, :n]
+    assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("mode", ["outgoing", "incoming"])
+def test_n3072_matches_unpadded_n2816(gpu_device, mode):
+    """N = 3072, the reference's single-GPU capacity point (docs/context-parallel-sampling.md:115-117): the
+    contraction planes (128 x 3072^2 bf16, 2.4 GB per operand) pass 2^31 bytes, so tile offsets into them need
+    the full 32-bit range.  With the last 256 tokens masked, the valid region must equal, bit for bit, the same
+    problem at N = 2816 (planes below 2^31 bytes); all outputs finite."""
+    n, pad = 2816, 256
+    m = _module(mode, gpu_device)
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(1, n + pad, n + pad, D, generator=g).to(torch.bfloat16).to(gpu_device)
+    tok = torch.ones(1, n + pad, dtype=torch.bool, device=gpu_device)
+    tok[:, n:] = False
+    pmask = tok[:, :, None] & tok[:, None, :]
+    print(f"trimul {mode} N={n + pad}", flush=True)
+    with torch.no_grad():
+        b = m(x, pmask)
+        assert torch.isfinite(b).all()
+        b = b[:, :n, :n].clone()
+        xs = x[:, :n, :n].contiguous()
+        del x, pmask
+        torch.cuda.empty_cache()
+        print(f"trimul {mode} N={n}", flush=True)
+        a = m(xs, torch.ones(1, n, n, dtype=torch.bool, device=gpu_device))
     assert torch.equal(a, b)
 
 
