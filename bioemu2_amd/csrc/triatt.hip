@@ -39,8 +39,11 @@ constexpr int kProjRows = 4 * C + H;       // q, k, v, g, bias rows of the packe
 constexpr int kProjRowsPad = 4 * C + 32;   // bias block padded to one 32-row MFMA block
 constexpr int kProjThreads = 512;
 constexpr int kProjSmem = kProjRowsPad * kLdw * 2 + kProjRowsPad * 2 * 2;
-constexpr int kFlashThreads = 256;         // 4 waves x 64 queries (two 32-query tiles each)
-constexpr int kFlashQueries = 256;         // queries per workgroup
+constexpr int kFlashThreads = 256;         // 4 waves
+constexpr int kFlashTiles = 2;             // 32-query tiles per wave (1 tile at 3 waves per SIMD measured slower)
+constexpr int kFlashQueries = 4 * 32 * kFlashTiles;   // queries per workgroup
+constexpr int kFlashWavesPerEu = kFlashTiles == 1 ? 3 : 2;
+constexpr int kMaxKeyBlocks = 16384 / 64;  // 64-key blocks of the longest row (N <= 16384)
 
 // Softmax in base 2: q is stored pre-scaled by log2(e)/sqrt(d) and the bias by
 // log2(e), so QK^T + bias comes out of the MFMA directly in log2 units.
@@ -202,8 +205,12 @@ __global__ __launch_bounds__(kProjThreads) void triatt_proj_kernel(
 
 // ---------------------------------------------------------------------------
 // Flash attention kernel.  Workgroup = (b, frame row i, 256 queries); wave w
-// owns the two 32-query tiles q0 and q0 + 32, q0 = 256 qb + 64 w, which share
-// every K / V fragment the wave reads from LDS.
+// owns the kFlashTiles = 2 32-query tiles q0 and q0 + 32, q0 = 256 qb + 64 w,
+// which share every K / V fragment the wave reads from LDS.
+//
+// Rows whose keys are all masked take a closed form (uniform weights: o / l is
+// the mean of v), and 64-key blocks without a valid key are skipped: their
+// logits (-1e30 or -inf) add exact zeros, so o and l are bit-identical.
 //
 // At head dim 32 the attention is bound by vector-ALU and issue work, not by
 // the matrix cores, so everything that can ride on an MFMA does:
@@ -246,7 +253,8 @@ __device__ __forceinline__ int t_off(int r, int chunk) { return r * TLD + ((chun
 // With kTail the residual stream z carries an int8 tail plane (common.h),
 // read with z and rewritten with out (in place).
 template <bool kStarting, bool kTail>
-__global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
+__global__ __launch_bounds__(kFlashThreads) __attribute__((amdgpu_waves_per_eu(kFlashWavesPerEu, kFlashWavesPerEu)))
+void triatt_flash_kernel(
     TriAttBuffers buf, const bf16* __restrict__ wo, const bf16* zres, bf16* out, int8_t* tail, int N, int Np,
     int residual, int nitems) {
   __shared__ __attribute__((aligned(16))) bf16 smem[2 * kStage];
@@ -254,25 +262,25 @@ __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 31, hh = lane >> 5;
-  // XCD-aware mapping: workgroup w runs on XCD w % 8.  Work items are
-  // (b, row i, query block) with the query block fastest; each XCD gets a
-  // contiguous range, so the query blocks of one row (which read the same K
-  // and V) share an L2.
+  // XCD-aware mapping: workgroup w runs on XCD w % 8.  Frame rows (b, i)
+  // are dealt to the XCDs round-robin (row r to XCD r % 8) and each XCD runs
+  // a row's query blocks one after another, so the blocks of a row (which read
+  // the same K and V) share an L2, and rows of every kind (padded rows are
+  // nearly free) spread evenly over the XCDs.
   const int nq = (Np + kFlashQueries - 1) / kFlashQueries;
-  const int total = gridDim.x;  // = padded item count, a multiple of 8
-  const int per_xcd = total / 8;
-  const int item = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
-  if (item >= nitems) return;   // before any barrier: the whole workgroup leaves
-  const int qb = item % nq;
-  const int i = (item / nq) % N;
-  const int b = item / (nq * N);
-  // This wave's two 32-query tiles: q0 + 32t (Np is a multiple of 64, so both
-  // exist or neither does).
-  const int q0 = qb * kFlashQueries + wave * 64;
+  const int xcd = blockIdx.x % 8, local = blockIdx.x / 8;
+  const int row = (local / nq) * 8 + xcd;   // b * N + i
+  if (row >= nitems / nq) return;           // before any barrier: the whole workgroup leaves
+  const int qb = local % nq;
+  const int i = row % N;
+  const int b = row / N;
+  // This wave's 32-query tiles: q0 + 32t (Np is a multiple of 64, so all of
+  // them exist or none does).
+  const int q0 = qb * kFlashQueries + wave * 32 * kFlashTiles;
   const bool active = q0 < Np;          // idle waves still stage tiles and meet every barrier
-  int qrow[2];
+  int qrow[kFlashTiles];
 #pragma unroll
-  for (int t = 0; t < 2; ++t) qrow[t] = active ? q0 + 32 * t + n : 0;
+  for (int t = 0; t < kFlashTiles; ++t) qrow[t] = active ? q0 + 32 * t + n : 0;
 
   const size_t frow = ((size_t)b * Np + i) * Np;
   const unsigned plane = (unsigned)Np * (unsigned)Np;
@@ -284,14 +292,15 @@ __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
   // 32-channel slot holds that head's normalised output o / l (bf16) until
   // the epilogue (each lane rewrites only the slot it read itself).
   bf16* qio = buf.q + frow * C;                                             // [Np][C]
-  // Key-mask row.  A row whose keys are all masked attends uniformly to its
-  // N keys (every logit replaced by the same value); it runs with zero q and
-  // zero bias so that all its logits are exactly 0 instead.
+  // Key-mask row (additive: 0 valid, -1e30 masked, -inf beyond N).  A row
+  // whose keys are all masked ("dead") attends uniformly to its N keys
+  // (every logit replaced by the same value): o / l is the mean of v.
   int any_valid = 0;
   for (int t = tid; t < N; t += kFlashThreads) any_valid |= buf.mask[frow + t];
   const bool dead = __syncthreads_or(any_valid) == 0;
   for (int t = tid; t < Np; t += kFlashThreads)
-    kadd[t] = f2bf(t >= N ? -INFINITY : (dead || buf.mask[frow + t]) ? 0.f : -1e30f);
+    kadd[t] = f2bf(t >= N ? -INFINITY : buf.mask[frow + t] ? 0.f : -1e30f);
+  __syncthreads();
 
   // Operand fetches through buffer resources: per-lane byte offsets are fixed,
   // the (head, key block) part is a wave-uniform scalar offset.
@@ -333,53 +342,111 @@ __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
   bf16x8 ident[2], zero8;
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
-    ident[0][t] = f2bf(!dead && krow == 8 * hh + t ? 1.f : 0.f);
-    ident[1][t] = f2bf(!dead && krow == 16 + 8 * hh + t ? 1.f : 0.f);
+    ident[0][t] = f2bf(krow == 8 * hh + t ? 1.f : 0.f);
+    ident[1][t] = f2bf(krow == 16 + 8 * hh + t ? 1.f : 0.f);
     zero8[t] = f2bf(0.f);
   }
 
+  if (dead) {
+    // Uniform weights over the N keys: o / l = mean of v (v is exactly 0 for
+    // keys in [N, Np)), the same for every query of the row.
+    float* vmean = reinterpret_cast<float*>(smem);
+    for (int c = wave; c < C; c += kFlashThreads / 64) {
+      const bf16* vr = vg + (size_t)c * Np;
+      float acc = 0.f;
+      for (int k = lane * 8; k < Np; k += 512) {
+        float v8[8];
+        unpack8(load8(vr + k), v8);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc += v8[u];
+      }
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off);
+      if (lane == 0) vmean[c] = acc * (1.0f / N);
+    }
+    __syncthreads();
+#pragma unroll 1
+    for (int hd = 0; hd < H; ++hd) {
+#pragma unroll
+      for (int t = 0; t < kFlashTiles; ++t) {
+        float r[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) r[u] = vmean[hd * DH + 16 * hh + u];
+        if (active) store16(qio + (unsigned)qrow[t] * C + hd * DH + 16 * hh, r);
+      }
+    }
+  } else {
+  // Key blocks with at least one valid key, in order.  A block whose keys are
+  // all masked adds exact zeros (its logits are -1e30 or -inf below any
+  // unmasked logit), so skipping it leaves o and l bit-identical.
+  __shared__ short act[kMaxKeyBlocks];
+  __shared__ uint8_t kflag[kMaxKeyBlocks];
+  __shared__ int nact_s;
   const int nk = Np / 64;
-  bf16x8 bias[2][4];   // per query tile: bias slice of the block being consumed, then of the next one
+  for (int kb = wave; kb < nk; kb += kFlashThreads / 64) {
+    const bool ok = __builtin_bit_cast(uint16_t, kadd[64 * kb + lane]) == 0;
+    const bool any_ok = __any(ok);
+    if (lane == 0) kflag[kb] = any_ok;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    int base = 0;
+    for (int c0 = 0; c0 < nk; c0 += 64) {
+      const int kb = c0 + lane;
+      const bool f = kb < nk && kflag[kb] != 0;
+      const unsigned long long bal = __ballot(f);
+      if (f) act[base + __popcll(bal & ((1ull << lane) - 1ull))] = (short)kb;
+      base += __popcll(bal);
+    }
+    if (lane == 0) nact_s = base;
+  }
+  __syncthreads();
+  const int nact = nact_s;   // >= 1: the row has a valid key
+  bf16x8 bias[kFlashTiles][4];   // per query tile: bias slice of the block being consumed, then of the next one
 
-  gload(0, 0);
-  bload(0, 0, 0, bias[0]);
-  bload(0, 0, 1, bias[1]);
+  gload(0, act[0] * 64);
+#pragma unroll
+  for (int t = 0; t < kFlashTiles; ++t) bload(0, act[0] * 64, t, bias[t]);
   lstore(0);
   __syncthreads();
   int st = 0;
 #pragma unroll 1
   for (int hd = 0; hd < H; ++hd) {
-    bf16x8 qf[2][2];
+    bf16x8 qf[kFlashTiles][2];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      qf[t][0] = zero8;
-      qf[t][1] = zero8;
-      if (!dead) {
-        qf[t][0] = load8(qio + (unsigned)qrow[t] * C + hd * DH + 8 * hh);
-        qf[t][1] = load8(qio + (unsigned)qrow[t] * C + hd * DH + 16 + 8 * hh);
-      }
+    for (int t = 0; t < kFlashTiles; ++t) {
+      qf[t][0] = load8(qio + (unsigned)qrow[t] * C + hd * DH + 8 * hh);
+      qf[t][1] = load8(qio + (unsigned)qrow[t] * C + hd * DH + 16 + 8 * hh);
     }
-    f32x16 o[2] = {zero16(), zero16()};
-    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
-    bool m_set[2] = {false, false};   // m is the (bf16-rounded) max of some unmasked logit
+    f32x16 o[kFlashTiles];
+    float m[kFlashTiles], l[kFlashTiles];
+    bool m_set[kFlashTiles];   // m is the (bf16-rounded) max of some unmasked logit
+#pragma unroll
+    for (int t = 0; t < kFlashTiles; ++t) {
+      o[t] = zero16();
+      m[t] = -INFINITY;
+      l[t] = 0.f;
+      m_set[t] = false;
+    }
     // B operand of the rank-2 mask / shift product: k = 0 -> 1 (picks the key
     // column kadd), k = 1 -> -m (against a key column of ones).
-    bf16x8 qm[2] = {zero8, zero8};
-    if (hh == 0) {
-      qm[0][0] = f2bf(1.f);
-      qm[1][0] = f2bf(1.f);
+    bf16x8 qm[kFlashTiles];
+#pragma unroll
+    for (int t = 0; t < kFlashTiles; ++t) {
+      qm[t] = zero8;
+      if (hh == 0) qm[t][0] = f2bf(1.f);
     }
-    // One 64-key block: fetch the next K/V tile, consume the current one.
-    auto block = [&](int kb) {
-      const int k0 = kb * 64;
-      // next tile: (hd, kb + 1) or (hd + 1, 0); the very last iteration refetches itself
-      int hn = hd, kn = k0 + 64;
-      if (kn == Np) {
-        kn = 0;
-        hn = hd + 1 < H ? hd + 1 : hd;
-        if (hd + 1 == H) kn = k0;
-      }
+    // One 64-key block (the ib-th active one): fetch the next K/V tile,
+    // consume the current one.  k0 and the next tile's first key (kn) come in
+    // registers; the key after that is read from the list during the block
+    // (a read at the block's start would stall the K/V fetch on it).
+    auto block = [&](int ib, int k0, int& kn) {
+      // next tile: the next active block of this head, else the first of the
+      // next head; the very last iteration refetches itself
+      const int hn = ib + 1 < nact || hd + 1 == H ? hd : hd + 1;
       gload(hn, kn);
+      const int ia = ib + 2 < nact ? ib + 2 : ib + 2 - nact;    // block after the next (wraps to the next head)
+      const int kafter = act[ia < nact ? ia : 0] * 64;
       // Every wave runs the block, idle ones (q0 >= Np, only when Np is not a
       // multiple of 256) on row 0 queries whose results they never store: with
       // a branch here the compiler's wait before the K / V staging store below
@@ -400,9 +467,9 @@ __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
         // Logits minus the running max m, all on MFMA (no shift while m is
         // not yet set), for both query tiles before any softmax work so that
         // one tile's exponentials overlap the other tile's matrix products.
-        f32x16 s[2][2];
+        f32x16 s[kFlashTiles][2];
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
+        for (int t = 0; t < kFlashTiles; ++t) {
           bf16x8 qs = qm[t];
           if (!m_set[t]) qs[1] = f2bf(0.f);
           s[t][0] = mfma32(ka0, qf[t][0], zero16());
@@ -418,7 +485,7 @@ __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
           bload(hn, kn, t, bias[t]);
         }
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
+        for (int t = 0; t < kFlashTiles; ++t) {
           f32x16& s0 = s[t][0];
           f32x16& s1 = s[t][1];
           bf16x8 pa[2], pb[2];
@@ -471,12 +538,18 @@ __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
       lstore(st ^ 1);
       st ^= 1;
       __syncthreads();
+      kn = (ib + 2 < nact || hd + 1 < H) ? kafter : kn;
     };
+    int kcur = act[0] * 64, knext = nact > 1 ? act[1] * 64 : (hd + 1 < H ? kcur : kcur);
 #pragma unroll 1
-    for (int kb = 0; kb < nk; ++kb) block(kb);
+    for (int ib = 0; ib < nact; ++ib) {
+      const int k = kcur;
+      kcur = knext;
+      block(ib, k, knext);
+    }
     // head finished: o / l (bf16) parked in this head's q slot
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
+    for (int t = 0; t < kFlashTiles; ++t) {
       const float inv = 1.0f / (l[t] + __shfl_xor(l[t], 32));
       float r[16];
 #pragma unroll
@@ -484,10 +557,11 @@ __global__ __launch_bounds__(kFlashThreads) void triatt_flash_kernel(
       if (active) store16(qio + (unsigned)qrow[t] * C + hd * DH + 16 * hh, r);
     }
   }
+  }
   if (!active) return;
 
 #pragma unroll 1
-  for (int t = 0; t < 2; ++t) {
+  for (int t = 0; t < kFlashTiles; ++t) {
     // The residual (and its tail) of each output block is requested one block
     // ahead, so that its latency hides behind the gate loads and the previous
     // block's MFMAs.  Lanes of queries past N read pair 0 and store nothing.
@@ -646,7 +720,7 @@ extern "C" int bioemu_triatt_fwd(const void* z, const uint8_t* mask, const float
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(kflash), hipFuncAttributeMaxDynamicSharedMemorySize,
                           (int)flash_smem) != hipSuccess)
     return set_error(BIOEMU_ERR_LAUNCH, "triatt_flash: cannot set dynamic LDS size");
-  const long long grid2 = (nitems + 7) / 8 * 8;
+  const long long grid2 = ((long long)B * N + 7) / 8 * 8 * ((Np + kFlashQueries - 1) / kFlashQueries);
   if (grid2 > 0x7fffffffLL) return set_error(BIOEMU_ERR_INVALID_ARG, "triatt: too many work items");
   {
     KernelTimerScope timed("triatt_flash", stream);

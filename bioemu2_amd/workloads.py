@@ -95,14 +95,19 @@ def fold_kernel_work(name: str, launches: int, rows128: int, rows64: int = 0,
     return None
 
 
-def triatt_kernel_work(name: str, B: int, N: int, c: int = 128, H: int = 4) -> tuple[str, float] | None:
+def triatt_kernel_work(name: str, B: int, N: int, c: int = 128, H: int = 4,
+                       n_valid: int | None = None) -> tuple[str, float] | None:
+    """``n_valid``: valid (unpadded) tokens; the attention counts only frame rows with a valid key and, in
+    them, the valid keys (a masked key adds an exact zero and the kernel skips whole blocks of them; a row
+    without valid keys is the closed-form mean of v), for every query."""
     P = B * N * N
     if name == "triatt_proj":
         # LN + q,k,v,g (c -> 4c) + bias (c -> H); reads z, writes q,k,v,g (+ bias)
         return ("hbm", float(P * (c * 2 + 4 * c * 2 + H * 2)))
     if name == "triatt_flash":
-        # QK^T and PV over all keys for every (row, query, head) + output projection
-        return ("mfma", 2.0 * B * N * N * N * c * 2 + 2.0 * P * c * c)
+        # QK^T and PV over the valid keys for every (valid row, query, head) + output projection
+        nv = N if n_valid is None else n_valid
+        return ("mfma", 2.0 * B * nv * N * nv * c * 2 + 2.0 * P * c * c)
     return None
 
 
@@ -187,7 +192,8 @@ class TriAttWorkload(Workload):
         self.out = torch.empty_like(self.x)
         self.ws = _ops.workspace(_ops.triatt_workspace_bytes(1, n), device)
         self.params = self.module.prepared_params()
-        self.flops = 2.0 * n * n * 128 * (4 * 128 + 4 + 128) + 2.0 * 2 * n ** 3 * 128
+        nv = n - self.n_pad
+        self.flops = 2.0 * n * n * 128 * (4 * 128 + 4 + 128) + 2.0 * 2 * nv * n * nv * 128
 
     def step(self) -> None:
         _ops.launch_triatt(self.x, self.pair_mask, *self.params, self.out, self.starting, ws=self.ws)
@@ -200,17 +206,21 @@ class TriAttWorkload(Workload):
         return fn, 1.0, f"oracle.triangle_attention fp32, full N={self.n} (64-row chunks)"
 
     def kernel_work(self, kernel: str) -> tuple[str, float]:
-        w = triatt_kernel_work(kernel, 1, self.n) or fold_kernel_work(kernel, 1, 4 * 128 + 4)
+        w = (triatt_kernel_work(kernel, 1, self.n, n_valid=self.n - self.n_pad)
+             or fold_kernel_work(kernel, 1, 4 * 128 + 4))
         if w is None:
             raise KeyError(kernel)
         return w
 
 
-def block_flops(n: int, c: int = 128, cs: int = 384) -> float:
-    """Algorithmic flops of one Pairformer block at N = n (B = 1)."""
+def block_flops(n: int, c: int = 128, cs: int = 384, n_valid: int | None = None) -> float:
+    """Algorithmic flops of one Pairformer block at N = n (B = 1).  With ``n_valid`` valid tokens the
+    triangle attentions count their valid keys in valid rows only (masked keys add exact zeros), as the
+    OPM counts its valid MSA rows; every other term is dense (1361.3 GF at N = 768 when all are valid)."""
     P = n * n
+    nv = n if n_valid is None else n_valid
     trimul = 2.0 * P * c * 6 * c + 2.0 * c * n ** 3
-    triatt = 2.0 * P * c * (5 * c + 4) + 4.0 * n ** 3 * c
+    triatt = 2.0 * P * c * (5 * c + 4) + 4.0 * nv * n * nv * c
     trans_z = 2.0 * P * c * 12 * c
     apb = 2.0 * P * c * 16 + 2.0 * n * cs * 5 * cs + 4.0 * n * n * cs
     trans_s = 2.0 * n * cs * 12 * cs
@@ -251,7 +261,7 @@ class BlockWorkload(Workload):
         self.s_tail = torch.zeros(self.s.shape, dtype=torch.int8, device=device) if tails else None
         self.tok = token_mask(n, self.n_pad, device)
         self.ws = _ops.workspace(self.module.workspace_bytes(1, n), device)
-        self.flops = block_flops(n)
+        self.flops = block_flops(n, n_valid=n - self.n_pad)
 
     def step(self) -> None:
         self.module.forward_(self.s, self.z, self.tok, self.s_tail, self.z_tail, ws=self.ws)
@@ -266,10 +276,9 @@ class BlockWorkload(Workload):
 
     def kernel_work(self, kernel: str) -> tuple[str, float]:
         n, c, cs = self.n, 128, 384
-        for fn in (trimul_kernel_work, triatt_kernel_work):
-            w = fn(kernel, 1, n)
-            if w is not None:
-                return w
+        w = trimul_kernel_work(kernel, 1, n) or triatt_kernel_work(kernel, 1, n, n_valid=n - self.n_pad)
+        if w is not None:
+            return w
         if kernel == "fold_ln":  # triatt (516 rows) x2, APB bias (16 rows), transition fc1 and fc2 (512 rows each)
             return fold_kernel_work(kernel, 5, 2 * 516 + 16 + 1024)
         if kernel == "transition_pair":
@@ -302,6 +311,7 @@ class Config1Workload(BlockWorkload):
     def __init__(self, device, n: int = 64, seed: int = 0):
         super().__init__(device, n, seed)
         self.n_pad = 0
+        self.flops = block_flops(n)
         self.tok = token_mask(n, 0, device)
         self.name = f"pairformer_block_n{n}_fp32io"
         self.metric = f"ms per Pairformer block at N={n}, fp32 in/out"
@@ -330,7 +340,7 @@ class TrunkWorkload(BlockWorkload):
         self.name = f"pairformer_trunk{blocks}_n{n}"
         self.metric = f"ms per {blocks}-block Pairformer trunk pass at N={n} bf16"
         self.config = dict(self.config, workload=self.name, blocks=blocks)
-        self.flops = blocks * block_flops(n)
+        self.flops = blocks * block_flops(n, n_valid=n - self.n_pad)
 
     def step(self) -> None:
         for blk in self.blocks:

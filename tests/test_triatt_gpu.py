@@ -81,6 +81,33 @@ def test_config4_shape_n768(gpu_device, starting):
 
 
 @pytest.mark.parametrize("starting", [True, False])
+def test_masked_key_blocks_match_oracle(gpu_device, starting):
+    """Frame rows whose valid keys sit in scattered 64-key blocks: the first block fully masked, holes of
+    whole blocks, a single valid key, and rows with no valid key at all.  The kernel skips key blocks
+    without a valid key (they add exact zeros) and gives a row without any its uniform mean of v; both
+    against the oracle on every element."""
+    n = 320                                     # 5 key blocks of 64
+    g = torch.Generator().manual_seed(11)
+    fm = torch.zeros(1, n, n, dtype=torch.bool)   # frame mask: [row i][key k]
+    blocks = {0: [1, 3], 1: [0, 4], 2: [0, 1, 2, 3, 4], 3: [2], 4: []}
+    for i in range(n):
+        for kb in blocks[i % 5]:
+            fm[0, i, 64 * kb:64 * kb + 64] = torch.rand(64, generator=g) < 0.7
+        if i % 5 == 3:
+            fm[0, i] = False
+            fm[0, i, 130] = True
+    mask = fm if starting else fm.transpose(1, 2).contiguous()
+    m = _module(starting, gpu_device)
+    z = torch.randn(1, n, n, C, generator=g).to(torch.bfloat16)
+    with torch.no_grad():
+        got = m(z.to(gpu_device), mask.to(gpu_device)).float().cpu()
+    want = oracle.triangle_attention(z.float(), mask, state(m), H, starting, row_chunk=80)
+    err, rl2 = max_abs(got, want), rel_l2(got, want)
+    print(f"triatt masked key blocks starting={starting}: max_abs={err:.3e} rel_l2={rl2:.3e}")
+    assert err <= ATOL and rl2 <= RTOL_L2
+
+
+@pytest.mark.parametrize("starting", [True, False])
 def test_masking_bit_exact(gpu_device, starting):
     """Values under masked pairs never reach valid outputs... except through
     their own row/col: for the starting node a masked pair (i,k) is a masked key
