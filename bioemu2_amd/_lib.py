@@ -86,6 +86,17 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "bioemu_token_ln_linear_fwd": (_c_int, [_c_void_p] * 9 + [_c_size_t, _c_int64, _c_int64, _c_void_p]),
     "bioemu_msa_embed_workspace_bytes": (_c_size_t, [_c_int64] * 2),
     "bioemu_msa_embed_fwd": (_c_int, [_c_void_p] * 10 + [_c_size_t] + [_c_int64] * 6 + [_c_void_p]),
+    "bioemu_apb_f32_workspace_bytes": (_c_size_t, [_c_int64] * 5),
+    "bioemu_apb_fwd_f32": (_c_int, [_c_void_p] * 14 + [_c_size_t] + [_c_int64] * 6 + [_c_int, _c_void_p]),
+    "bioemu_swa_f32_workspace_bytes": (_c_size_t, [_c_int64] * 7),
+    "bioemu_swa_fwd_f32": (_c_int, [_c_void_p] * 14 + [_c_size_t] + [_c_int64] * 8 + [_c_int, _c_void_p]),
+    "bioemu_transition_f32_workspace_bytes": (_c_size_t, [_c_int64] * 3),
+    "bioemu_transition_fwd_f32": (
+        _c_int,
+        [_c_void_p] * 8 + [_c_size_t] + [_c_int64] * 4 + [_c_int, _c_int, _c_void_p],
+    ),
+    "bioemu_pair_cond_f32_workspace_bytes": (_c_size_t, [_c_int64] * 3),
+    "bioemu_pair_cond_proj_fwd_f32": (_c_int, [_c_void_p] * 7 + [_c_size_t] + [_c_int64] * 4 + [_c_void_p]),
 }
 
 _lock = threading.Lock()

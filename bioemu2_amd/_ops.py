@@ -583,6 +583,293 @@ def _(s, z, mask, norm_s_w, norm_s_b, w_qkv, q_bias, w_g, norm_z_w, norm_z_b, w_
 
 
 # ----------------------------------------------------------------------------
+# fp32 arithmetic path (the reference's denoiser runs with autocast off)
+# ----------------------------------------------------------------------------
+F32 = torch.float32
+
+
+def fp32_mode(x: Tensor) -> bool:
+    """True where the reference computes in fp32: fp32 inputs with CUDA autocast off.
+
+    The reference's denoiser disables autocast (score_model.py:355, model.py:387), so its attention and
+    transitions run fp32 on fp32 activations; under bf16 autocast (the trunk) they run bf16 matmuls.
+    """
+    return x.dtype == F32 and not torch.is_autocast_enabled("cuda")
+
+
+def _check_attn_params_f32(what, c_s, c_z, num_heads, dev, norm_s_w, norm_s_b, w_qkv, q_bias, w_g, norm_z_w,
+                           norm_z_b, w_z, w_o) -> None:
+    if norm_s_w is not None:
+        _check_tensor(norm_s_w, f"{what} norm_s.weight", F32, (c_s,), dev)
+        _check_tensor(norm_s_b, f"{what} norm_s.bias", F32, (c_s,), dev)
+    _check_tensor(w_qkv, f"{what} proj_qkv.weight", F32, (3 * c_s, c_s), dev)
+    _check_tensor(q_bias, f"{what} proj_q_bias", F32, (c_s,), dev)
+    _check_tensor(w_g, f"{what} proj_g.weight", F32, (c_s, c_s), dev)
+    _check_tensor(norm_z_w, f"{what} norm_z.weight", F32, (c_z,), dev)
+    if norm_z_b is not None:
+        _check_tensor(norm_z_b, f"{what} norm_z.bias", F32, (c_z,), dev)
+    _check_tensor(w_z, f"{what} proj_z.weight", F32, (num_heads, c_z), dev)
+    _check_tensor(w_o, f"{what} proj_o.weight", F32, (c_s, c_s), dev)
+
+
+def apb_f32_workspace_bytes(B: int, mult: int, N: int, c_s: int, H: int) -> int:
+    return int(lib().bioemu_apb_f32_workspace_bytes(B, mult, N, c_s, H))
+
+
+def launch_apb_f32(
+    s: Tensor,
+    z: Tensor,
+    mask: Tensor,
+    norm_s_w: Tensor | None,
+    norm_s_b: Tensor | None,
+    w_qkv: Tensor,
+    q_bias: Tensor,
+    w_g: Tensor,
+    norm_z_w: Tensor,
+    norm_z_b: Tensor | None,
+    w_z: Tensor,
+    w_o: Tensor,
+    out: Tensor,
+    num_heads: int,
+    multiplicity: int = 1,
+    residual: bool = False,
+    ws: Tensor | None = None,
+) -> Tensor:
+    """fp32 AttentionPairBias (attention_pair_bias.py:128-225): every tensor fp32, mask [B,N] uint8."""
+    require_gpu(s, "attention_pair_bias_f32")
+    if s.ndim != 3 or z.ndim != 4 or mask.ndim != 2:
+        raise AssertionError(f"{tuple(s.shape)}, {tuple(z.shape)}, {tuple(mask.shape)}")
+    if s.shape[0] != z.shape[0] * multiplicity:
+        raise AssertionError(f"{tuple(s.shape)}, {tuple(z.shape)}, multiplicity={multiplicity}")
+    BM, N, c_s = s.shape
+    B, _, _, c_z = z.shape
+    dev = s.device
+    _check_tensor(s, "apb_f32 s", F32, (BM, N, c_s), dev)
+    _check_tensor(out, "apb_f32 out", F32, (BM, N, c_s), dev)
+    _check_tensor(z, "apb_f32 z", F32, (B, N, N, c_z), dev)
+    _check_tensor(mask, "apb_f32 mask", torch.uint8, (B, N), dev)
+    _check_attn_params_f32("apb_f32", c_s, c_z, num_heads, dev, norm_s_w, norm_s_b, w_qkv, q_bias, w_g, norm_z_w,
+                           norm_z_b, w_z, w_o)
+    need = apb_f32_workspace_bytes(B, multiplicity, N, c_s, num_heads)
+    if ws is None or ws.numel() < need:
+        ws = workspace(need, dev)
+    rc = lib().bioemu_apb_fwd_f32(
+        _ptr(s), _ptr(z), _ptr(mask), _ptr(norm_s_w), _ptr(norm_s_b), _ptr(w_qkv), _ptr(q_bias), _ptr(w_g),
+        _ptr(norm_z_w), _ptr(norm_z_b), _ptr(w_z), _ptr(w_o), _ptr(out), _ptr(ws), ctypes.c_size_t(ws.numel()),
+        B, multiplicity, N, c_s, c_z, num_heads, int(bool(residual)), _stream(s),
+    )
+    check(rc, "bioemu_apb_fwd_f32")
+    return out
+
+
+def _f32c(t: Tensor | None) -> Tensor | None:
+    return None if t is None else t.to(F32).contiguous()
+
+
+@torch.library.custom_op("bioemu_mi355x::attention_pair_bias_f32", mutates_args=(), device_types="cuda")
+def attention_pair_bias_f32(
+    s: Tensor,
+    z: Tensor,
+    mask: Tensor,
+    norm_s_w: Tensor | None,
+    norm_s_b: Tensor | None,
+    w_qkv: Tensor,
+    q_bias: Tensor,
+    w_g: Tensor,
+    norm_z_w: Tensor,
+    norm_z_b: Tensor | None,
+    w_z: Tensor,
+    w_o: Tensor,
+    num_heads: int,
+    multiplicity: int,
+) -> Tensor:
+    sf = s.to(F32).contiguous()
+    out = torch.empty_like(sf)
+    launch_apb_f32(
+        sf, _f32c(z), mask_u8(mask), _f32c(norm_s_w), _f32c(norm_s_b), _f32c(w_qkv), _f32c(q_bias), _f32c(w_g),
+        _f32c(norm_z_w), _f32c(norm_z_b), _f32c(w_z), _f32c(w_o), out, num_heads, multiplicity,
+    )
+    return out.to(s.dtype)
+
+
+@attention_pair_bias_f32.register_fake
+def _(s, z, mask, norm_s_w, norm_s_b, w_qkv, q_bias, w_g, norm_z_w, norm_z_b, w_z, w_o, num_heads, multiplicity):
+    return torch.empty_like(s)
+
+
+def swa_f32_workspace_bytes(B: int, mult: int, NW: int, W: int, H: int, c_s: int, heads: int) -> int:
+    return int(lib().bioemu_swa_f32_workspace_bytes(B, mult, NW, W, H, c_s, heads))
+
+
+def launch_swa_f32(
+    s: Tensor,
+    z: Tensor,
+    mask: Tensor,
+    norm_s_w: Tensor | None,
+    norm_s_b: Tensor | None,
+    w_qkv: Tensor,
+    q_bias: Tensor,
+    w_g: Tensor,
+    norm_z_w: Tensor,
+    norm_z_b: Tensor | None,
+    w_z: Tensor,
+    w_o: Tensor,
+    out: Tensor,
+    num_heads: int,
+    multiplicity: int = 1,
+    residual: bool = False,
+    ws: Tensor | None = None,
+) -> Tensor:
+    """fp32 sliding-window attention (attention_pair_bias.py:277-340): s [B*M*NW, W, c_s], z [B, NW, W, H, c_z],
+    mask [B*NW, W] uint8, every other tensor fp32."""
+    require_gpu(s, "attention_pair_bias_sliding_window_f32")
+    if s.ndim != 3 or z.ndim != 5 or mask.ndim != 2:
+        raise AssertionError(f"{tuple(s.shape)}, {tuple(z.shape)}, {tuple(mask.shape)}")
+    B, NW, W, H, c_z = z.shape
+    folded, _, c_s = s.shape
+    if folded != B * multiplicity * NW:
+        raise AssertionError(f"{tuple(s.shape)}, {tuple(z.shape)}, multiplicity={multiplicity}")
+    dev = s.device
+    _check_tensor(s, "swa_f32 s", F32, (folded, W, c_s), dev)
+    _check_tensor(out, "swa_f32 out", F32, (folded, W, c_s), dev)
+    _check_tensor(z, "swa_f32 z", F32, (B, NW, W, H, c_z), dev)
+    _check_tensor(mask, "swa_f32 mask", torch.uint8, (B * NW, W), dev)
+    _check_attn_params_f32("swa_f32", c_s, c_z, num_heads, dev, norm_s_w, norm_s_b, w_qkv, q_bias, w_g, norm_z_w,
+                           norm_z_b, w_z, w_o)
+    need = swa_f32_workspace_bytes(B, multiplicity, NW, W, H, c_s, num_heads)
+    if ws is None or ws.numel() < need:
+        ws = workspace(need, dev)
+    rc = lib().bioemu_swa_fwd_f32(
+        _ptr(s), _ptr(z), _ptr(mask), _ptr(norm_s_w), _ptr(norm_s_b), _ptr(w_qkv), _ptr(q_bias), _ptr(w_g),
+        _ptr(norm_z_w), _ptr(norm_z_b), _ptr(w_z), _ptr(w_o), _ptr(out), _ptr(ws), ctypes.c_size_t(ws.numel()),
+        B, multiplicity, NW, W, H, c_s, c_z, num_heads, int(bool(residual)), _stream(s),
+    )
+    check(rc, "bioemu_swa_fwd_f32")
+    return out
+
+
+@torch.library.custom_op(
+    "bioemu_mi355x::attention_pair_bias_sliding_window_f32", mutates_args=(), device_types="cuda"
+)
+def attention_pair_bias_sliding_window_f32(
+    s: Tensor,
+    z: Tensor,
+    mask: Tensor,
+    norm_s_w: Tensor | None,
+    norm_s_b: Tensor | None,
+    w_qkv: Tensor,
+    q_bias: Tensor,
+    w_g: Tensor,
+    norm_z_w: Tensor,
+    norm_z_b: Tensor | None,
+    w_z: Tensor,
+    w_o: Tensor,
+    num_heads: int,
+    multiplicity: int,
+) -> Tensor:
+    sf = s.to(F32).contiguous()
+    out = torch.empty_like(sf)
+    launch_swa_f32(
+        sf, _f32c(z), mask_u8(mask), _f32c(norm_s_w), _f32c(norm_s_b), _f32c(w_qkv), _f32c(q_bias), _f32c(w_g),
+        _f32c(norm_z_w), _f32c(norm_z_b), _f32c(w_z), _f32c(w_o), out, num_heads, multiplicity,
+    )
+    return out.to(s.dtype)
+
+
+@attention_pair_bias_sliding_window_f32.register_fake
+def _(s, z, mask, norm_s_w, norm_s_b, w_qkv, q_bias, w_g, norm_z_w, norm_z_b, w_z, w_o, num_heads, multiplicity):
+    return torch.empty_like(s)
+
+
+def transition_f32_workspace_bytes(M: int, D: int, hidden: int) -> int:
+    return int(lib().bioemu_transition_f32_workspace_bytes(M, D, hidden))
+
+
+def launch_transition_f32(
+    x: Tensor,
+    norm_w: Tensor | None,
+    norm_b: Tensor | None,
+    fc1_w: Tensor,
+    fc2_w: Tensor,
+    fc3_w: Tensor,
+    out: Tensor,
+    residual: bool = False,
+    ws: Tensor | None = None,
+) -> Tensor:
+    """fp32 Transition (transition.py:52-76) over the rows of x [..., D]; out [..., out_dim]."""
+    require_gpu(x, "transition_f32")
+    D = x.shape[-1]
+    M = x.numel() // D
+    dev = x.device
+    hidden = fc1_w.shape[0]
+    out_dim = fc3_w.shape[0]
+    _check_tensor(x, "transition_f32 x", F32, tuple(x.shape), dev)
+    _check_tensor(out, "transition_f32 out", F32, tuple(x.shape[:-1]) + (out_dim,), dev)
+    _check_tensor(fc1_w, "transition_f32 fc1.weight", F32, (hidden, D), dev)
+    _check_tensor(fc2_w, "transition_f32 fc2.weight", F32, (hidden, D), dev)
+    _check_tensor(fc3_w, "transition_f32 fc3.weight", F32, (out_dim, hidden), dev)
+    use_norm = norm_w is not None
+    if use_norm:
+        _check_tensor(norm_w, "transition_f32 norm.weight", F32, (D,), dev)
+        _check_tensor(norm_b, "transition_f32 norm.bias", F32, (D,), dev)
+    need = transition_f32_workspace_bytes(M, D, hidden)
+    if ws is None or ws.numel() < need:
+        ws = workspace(need, dev)
+    rc = lib().bioemu_transition_fwd_f32(
+        _ptr(x), _ptr(norm_w), _ptr(norm_b), _ptr(fc1_w), _ptr(fc2_w), _ptr(fc3_w), _ptr(out), _ptr(ws),
+        ctypes.c_size_t(ws.numel()), M, D, hidden, out_dim, int(use_norm), int(bool(residual)), _stream(x),
+    )
+    check(rc, "bioemu_transition_fwd_f32")
+    return out
+
+
+@torch.library.custom_op("bioemu_mi355x::transition_f32", mutates_args=(), device_types="cuda")
+def transition_f32(
+    x: Tensor, norm_w: Tensor | None, norm_b: Tensor | None, fc1_w: Tensor, fc2_w: Tensor, fc3_w: Tensor
+) -> Tensor:
+    xf = x.to(F32).contiguous()
+    out = torch.empty(*xf.shape[:-1], fc3_w.shape[0], dtype=F32, device=xf.device)
+    launch_transition_f32(xf, _f32c(norm_w), _f32c(norm_b), _f32c(fc1_w), _f32c(fc2_w), _f32c(fc3_w), out)
+    return out.to(x.dtype)
+
+
+@transition_f32.register_fake
+def _(x, norm_w, norm_b, fc1_w, fc2_w, fc3_w):
+    return x.new_empty(*x.shape[:-1], fc3_w.shape[0])
+
+
+def pair_cond_f32_workspace_bytes(P: int, token_z: int, c_rel: int) -> int:
+    return int(lib().bioemu_pair_cond_f32_workspace_bytes(P, token_z, c_rel))
+
+
+def launch_pair_cond_proj_f32(
+    z_trunk: Tensor, rel: Tensor, ln_w: Tensor, ln_b: Tensor, w: Tensor, out: Tensor, ws: Tensor | None = None
+) -> Tensor:
+    """fp32 LayerNorm over [z_trunk | rel] + LinearNoBias (PairwiseConditioning, diffusion.py:521-524)."""
+    require_gpu(z_trunk, "pair_cond_f32")
+    token_z, c_rel = z_trunk.shape[-1], rel.shape[-1]
+    lead = tuple(z_trunk.shape[:-1])
+    P = z_trunk.numel() // token_z
+    a_z = w.shape[0]
+    dev = z_trunk.device
+    _check_tensor(z_trunk, "pair_cond_f32 z_trunk", F32, lead + (token_z,), dev)
+    _check_tensor(rel, "pair_cond_f32 rel", F32, lead + (c_rel,), dev)
+    _check_tensor(ln_w, "pair_cond_f32 norm.weight", F32, (token_z + c_rel,), dev)
+    _check_tensor(ln_b, "pair_cond_f32 norm.bias", F32, (token_z + c_rel,), dev)
+    _check_tensor(w, "pair_cond_f32 proj.weight", F32, (a_z, token_z + c_rel), dev)
+    _check_tensor(out, "pair_cond_f32 out", F32, lead + (a_z,), dev)
+    need = pair_cond_f32_workspace_bytes(P, token_z, c_rel)
+    if ws is None or ws.numel() < need:
+        ws = workspace(need, dev)
+    rc = lib().bioemu_pair_cond_proj_fwd_f32(
+        _ptr(z_trunk), _ptr(rel), _ptr(ln_w), _ptr(ln_b), _ptr(w), _ptr(out), _ptr(ws), ctypes.c_size_t(ws.numel()),
+        P, token_z, c_rel, a_z, _stream(z_trunk),
+    )
+    check(rc, "bioemu_pair_cond_proj_fwd_f32")
+    return out
+
+
+# ----------------------------------------------------------------------------
 # Pair glue: distogram head, pairwise-conditioning projection
 # ----------------------------------------------------------------------------
 def launch_distogram(z: Tensor, w: Tensor, b: Tensor, out: Tensor) -> Tensor:

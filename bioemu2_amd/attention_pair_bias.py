@@ -18,6 +18,12 @@ transformer): constructor ``(c_s, c_z, num_heads, window_queries=32,
 window_keys=128, inf, initial_norm, tile_size, zero_init_output,
 use_bias_in_layer_norm)``, the same parameters, and
 ``forward(s [B*M*NW, W, c_s], z [B, NW, W, H, c_z], mask [B*NW, W], multiplicity)``.
+
+Arithmetic follows the caller's precision: fp32 inputs with autocast off (the
+reference's denoiser, score_model.py:355, model.py:387) run the fp32 path
+(fp32 operands and accumulation, ``bioemu_apb_fwd_f32`` / ``bioemu_swa_fwd_f32``);
+anything else runs bf16 MFMA operands with fp32 accumulation, as the
+reference's bf16-autocast trunk.
 """
 
 from __future__ import annotations
@@ -78,15 +84,23 @@ class AttentionPairBias(nn.Module):
             spec += [("norm_z.bias", f32)]
         spec += [("proj_z.weight", bf), ("proj_o.weight", bf)]
         self._prepared = PreparedParams(spec)
+        self._prepared32 = PreparedParams([(name, f32) for name, _ in spec])
 
-    def prepared_params(self) -> tuple[Tensor | None, ...]:
-        """(norm_s_w, norm_s_b, w_qkv, q_bias, w_g, norm_z_w, norm_z_b, w_z, w_o) in kernel dtypes."""
-        p = list(self._prepared.get(self))
+    def _arrange(self, p: tuple[Tensor, ...]) -> tuple[Tensor | None, ...]:
+        p = list(p)
         if not self.initial_norm:
             p = [None, None] + p
         if not self.use_bias_in_layer_norm:
             p.insert(6, None)
         return tuple(p)
+
+    def prepared_params(self) -> tuple[Tensor | None, ...]:
+        """(norm_s_w, norm_s_b, w_qkv, q_bias, w_g, norm_z_w, norm_z_b, w_z, w_o) in kernel dtypes."""
+        return self._arrange(self._prepared.get(self))
+
+    def prepared_params_f32(self) -> tuple[Tensor | None, ...]:
+        """The same parameters, all fp32, for the fp32 arithmetic path."""
+        return self._arrange(self._prepared32.get(self))
 
     def forward(self, s: Tensor, z: Tensor, mask: Tensor, multiplicity: int = 1) -> Tensor:
         assert s.ndim == 3 and z.ndim == 4 and mask.ndim == 2, f"{s.shape}, {z.shape}, {mask.shape}"
@@ -94,6 +108,10 @@ class AttentionPairBias(nn.Module):
         _ops.require_gpu(s, type(self).__name__)
         if self.inf != 1e6:
             raise ValueError("AttentionPairBias (HIP): only inf=1e6, the reference default, is supported")
+        if _ops.fp32_mode(s):
+            return torch.ops.bioemu_mi355x.attention_pair_bias_f32(
+                s, z, _ops.mask_u8(mask), *self.prepared_params_f32(), self.num_heads, multiplicity
+            )
         return torch.ops.bioemu_mi355x.attention_pair_bias(
             s, z, _ops.mask_u8(mask), *self.prepared_params(), self.num_heads, multiplicity
         )
@@ -125,6 +143,10 @@ class AttentionPairBiasSlidingWindow(AttentionPairBias):
         _ops.require_gpu(s, type(self).__name__)
         if self.inf != 1e6:
             raise ValueError("AttentionPairBiasSlidingWindow (HIP): only inf=1e6, the reference default, is supported")
+        if _ops.fp32_mode(s):
+            return torch.ops.bioemu_mi355x.attention_pair_bias_sliding_window_f32(
+                s, z, _ops.mask_u8(mask), *self.prepared_params_f32(), self.num_heads, multiplicity
+            )
         return torch.ops.bioemu_mi355x.attention_pair_bias_sliding_window(
             s, z, _ops.mask_u8(mask), *self.prepared_params(), self.num_heads, multiplicity
         )

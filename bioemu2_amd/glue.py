@@ -12,7 +12,10 @@
   LinearNoBias) and ``transitions.{k}``; ``forward(z_trunk, token_rel_pos_feats)``.
   The LN + projection is one HIP kernel that reads both inputs in place (no
   concatenated copy); each transition is the fused row kernel with its residual
-  add fused, in place.
+  add fused, in place.  fp32 inputs with autocast off (the reference runs its
+  denoiser so, score_model.py:355) take the fp32 path: fp32 LN over the
+  concatenation read in place, fp32 MFMA projection, fp32 transitions with the
+  residual fused; any token_z + c_rel multiple of 8 and a_z multiple of 32.
 """
 
 from __future__ import annotations
@@ -76,10 +79,18 @@ class PairwiseConditioning(nn.Module):
             ("dim_pairwise_init_proj.0.bias", torch.float32),
             ("dim_pairwise_init_proj.1.weight", BF16),
         ])
+        self._prepared32 = PreparedParams([
+            ("dim_pairwise_init_proj.0.weight", torch.float32),
+            ("dim_pairwise_init_proj.0.bias", torch.float32),
+            ("dim_pairwise_init_proj.1.weight", torch.float32),
+        ])
         self._ws: Tensor | None = None
 
     def prepared_params(self) -> tuple[Tensor, Tensor, Tensor]:
         return self._prepared.get(self)
+
+    def prepared_params_f32(self) -> tuple[Tensor, Tensor, Tensor]:
+        return self._prepared32.get(self)
 
     def _workspace(self, device) -> Tensor:
         t0 = self.transitions[0] if len(self.transitions) else None
@@ -90,9 +101,25 @@ class PairwiseConditioning(nn.Module):
             self._ws = _ops.workspace(need, device)
         return self._ws
 
+    def _forward_f32(self, z_trunk: Tensor, token_rel_pos_feats: Tensor) -> Tensor:
+        z = z_trunk.contiguous()
+        rel = token_rel_pos_feats.to(torch.float32).contiguous()
+        P = z.numel() // z.shape[-1]
+        need = _ops.pair_cond_f32_workspace_bytes(P, self.token_z, self.c_rel)
+        for t in self.transitions:
+            need = max(need, _ops.transition_f32_workspace_bytes(P, self.a_z, t.hidden))
+        ws = _ops.workspace(need, z.device)
+        out = torch.empty(*z.shape[:-1], self.a_z, dtype=torch.float32, device=z.device)
+        _ops.launch_pair_cond_proj_f32(z, rel, *self.prepared_params_f32(), out, ws=ws)
+        for transition in self.transitions:   # z = transition(z) + z, residual fused, in place
+            _ops.launch_transition_f32(out, *transition.prepared_params_f32(), out, residual=True, ws=ws)
+        return out
+
     @torch.no_grad()
     def forward(self, z_trunk: Tensor, token_rel_pos_feats: Tensor) -> Tensor:
         _ops.require_gpu(z_trunk, type(self).__name__)
+        if _ops.fp32_mode(z_trunk):
+            return self._forward_f32(z_trunk, token_rel_pos_feats)
         z = z_trunk.to(BF16).contiguous()
         rel = token_rel_pos_feats.to(BF16).contiguous()
         ws = self._workspace(z.device)

@@ -11,7 +11,9 @@ mixers, diffusion.py:623-634: dim a multiple of 16, hidden and out_dim
 multiples of 32) run the token LN + GEMM kernels.
 ``chunk_size`` only tiled the hidden dimension for memory in the reference
 (:76-91): the fused kernel never materialises the hidden activations, so it
-is accepted and has no effect on the result.
+is accepted and has no effect on the result.  fp32 inputs with autocast off
+(the reference's denoiser) run the fp32 path (``bioemu_transition_fwd_f32``:
+fp32 operands and accumulation, any row count; dim a multiple of 8).
 """
 
 from __future__ import annotations
@@ -48,11 +50,18 @@ class Transition(nn.Module):
         if use_norm:
             spec = [("norm.weight", torch.float32), ("norm.bias", torch.float32)] + spec
         self._prepared = PreparedParams(spec)
+        self._prepared32 = PreparedParams([(name, torch.float32) for name, _ in spec])
 
     def prepared_params(self) -> tuple[Tensor | None, ...]:
         p = self._prepared.get(self)
         return p if self.use_norm else (None, None) + p
 
+    def prepared_params_f32(self) -> tuple[Tensor | None, ...]:
+        p = self._prepared32.get(self)
+        return p if self.use_norm else (None, None) + p
+
     def forward(self, x: Tensor) -> Tensor:
         _ops.require_gpu(x, type(self).__name__)
+        if _ops.fp32_mode(x):
+            return torch.ops.bioemu_mi355x.transition_f32(x, *self.prepared_params_f32())
         return torch.ops.bioemu_mi355x.transition(x, *self.prepared_params())

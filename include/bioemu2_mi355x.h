@@ -320,6 +320,47 @@ int bioemu_msa_embed_fwd(const float* msa, const float* has_deletion, const floa
                          int8_t* m_tail, void* workspace, size_t workspace_bytes, int64_t B, int64_t R, int64_t T,
                          int64_t F0, int64_t E, int64_t msa_s, hipStream_t stream);
 
+/*
+ * fp32 arithmetic (fp32 operands, fp32 MFMA accumulation, fp32 softmax) for the
+ * ops the reference's denoiser runs with autocast off (src/bioemu2/biomoa/
+ * models/score_model.py:355, model.py:387).  Same arguments and semantics as the
+ * bf16 entry points above, with every activation, weight and output fp32:
+ *   bioemu_apb_fwd_f32       AttentionPairBias.forward (attention_pair_bias.py:128-225);
+ *                            head dim 24 or 32, c_s a multiple of 32, c_z in {16, 32, 128}.
+ *   bioemu_swa_fwd_f32       AttentionPairBiasSlidingWindow.forward (:277-340); W = 32,
+ *                            H a multiple of 32, head dim 32.
+ *   bioemu_transition_fwd_f32  Transition.forward (transition.py:52-91) on M rows:
+ *                            dim a multiple of 8, hidden and out_dim multiples of 32.
+ *   bioemu_pair_cond_proj_fwd_f32  the LayerNorm + LinearNoBias of PairwiseConditioning
+ *                            (biomoa/modules/diffusion.py:521-524) over P pair rows: the
+ *                            concatenation [z_trunk row | rel row] is read in place;
+ *                            token_z + c_rel a multiple of 8, a_z of 32.  Its transitions
+ *                            (:526-527) are bioemu_transition_fwd_f32 with residual=1.
+ * Residual tails do not apply (the stream is fp32).
+ */
+size_t bioemu_apb_f32_workspace_bytes(int64_t B, int64_t mult, int64_t N, int64_t c_s, int64_t H);
+int bioemu_apb_fwd_f32(const float* s, const float* z, const uint8_t* mask, const float* norm_s_w,
+                       const float* norm_s_b, const float* w_qkv, const float* q_bias, const float* w_g,
+                       const float* norm_z_w, const float* norm_z_b, const float* w_z, const float* w_o, float* out,
+                       void* workspace, size_t workspace_bytes, int64_t B, int64_t mult, int64_t N, int64_t c_s,
+                       int64_t c_z, int64_t H, int residual, hipStream_t stream);
+size_t bioemu_swa_f32_workspace_bytes(int64_t B, int64_t mult, int64_t NW, int64_t W, int64_t H, int64_t c_s,
+                                      int64_t heads);
+int bioemu_swa_fwd_f32(const float* s, const float* z, const uint8_t* mask, const float* norm_s_w,
+                       const float* norm_s_b, const float* w_qkv, const float* q_bias, const float* w_g,
+                       const float* norm_z_w, const float* norm_z_b, const float* w_z, const float* w_o, float* out,
+                       void* workspace, size_t workspace_bytes, int64_t B, int64_t mult, int64_t NW, int64_t W,
+                       int64_t H, int64_t c_s, int64_t c_z, int64_t heads, int residual, hipStream_t stream);
+size_t bioemu_transition_f32_workspace_bytes(int64_t M, int64_t Dc, int64_t hidden);
+int bioemu_transition_fwd_f32(const float* x, const float* norm_w, const float* norm_b, const float* fc1_w,
+                              const float* fc2_w, const float* fc3_w, float* out, void* workspace,
+                              size_t workspace_bytes, int64_t M, int64_t Dc, int64_t hidden, int64_t out_dim,
+                              int use_norm, int residual, hipStream_t stream);
+size_t bioemu_pair_cond_f32_workspace_bytes(int64_t P, int64_t token_z, int64_t c_rel);
+int bioemu_pair_cond_proj_fwd_f32(const float* z_trunk, const float* rel, const float* ln_w, const float* ln_b,
+                                  const float* w, float* out, void* workspace, size_t workspace_bytes, int64_t P,
+                                  int64_t token_z, int64_t c_rel, int64_t a_z, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,264 @@
+"""fp32 arithmetic path of the denoiser's ops vs the fp32 CPU oracle at 1e-5 relative.
+
+The reference runs its denoiser with autocast off (score_model.py:355, model.py:387):
+AttentionPairBias, AttentionPairBiasSlidingWindow and Transition see fp32 inputs
+there and compute in fp32.  The modules route fp32 inputs (autocast off) to the
+``*_f32`` entry points; these tests hold them to the fp32-mode bound (relative
+L2 error and max-abs error relative to the output's magnitude, both <= 1e-5),
+and masking/padding to bit-exactness.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import oracle
+from bioemu2_amd import _ops
+from bioemu2_amd.attention_pair_bias import AttentionPairBias, AttentionPairBiasSlidingWindow
+from bioemu2_amd.transition import Transition
+from tests._helpers import max_abs, randomize_params, rel_l2, state
+
+pytestmark = pytest.mark.gpu
+
+REL = 1e-5  # fp32-mode bound: relative L2, and max-abs relative to max |want|
+F32 = torch.float32
+W = 32
+
+
+def _check(got, want, tag):
+    err, rl2 = max_abs(got, want), rel_l2(got, want)
+    scale = max(float(want.abs().max()), 1.0)
+    print(f"{tag}: max_abs={err:.3e} rel_l2={rl2:.3e} |want|max={scale:.3f}")
+    assert got.dtype == F32
+    assert rl2 <= REL and err <= REL * scale
+
+
+# ----------------------------------------------------------------------------
+# AttentionPairBias
+# ----------------------------------------------------------------------------
+def _apb(device, c_s=384, c_z=128, H=16, initial_norm=True, ln_bias=False, seed=11):
+    torch.manual_seed(seed)
+    m = AttentionPairBias(c_s, c_z, H, initial_norm=initial_norm, use_bias_in_layer_norm=ln_bias)
+    return randomize_params(m, seed).to(device).eval()
+
+
+def _apb_inputs(B, n, device, mult=1, c_s=384, c_z=128, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    s = torch.randn(B * mult, n, c_s, generator=g)
+    z = torch.randn(B, n, n, c_z, generator=g)
+    mask = torch.ones(B, n, dtype=torch.bool)
+    for b in range(B):  # test_attention_pair_bias.py:76-95: min((b+1)*3, n-4) padded keys
+        mask[b, n - min((b + 1) * 3, n - 4):] = False
+    return s.to(device), z.to(device), mask.to(device)
+
+
+@pytest.mark.parametrize("initial_norm", [True, False])
+@pytest.mark.parametrize("n", [17, 64, 130])
+def test_apb_f32_matches_oracle(gpu_device, initial_norm, n):
+    """Token attention of the denoiser: c_s 384, 16 heads of 24, c_z 128."""
+    m = _apb(gpu_device, initial_norm=initial_norm)
+    s, z, mask = _apb_inputs(2, n, gpu_device)
+    with torch.no_grad():
+        got = m(s, z, mask).cpu()
+    want = oracle.attention_pair_bias(s.cpu(), z.cpu(), mask.cpu(), state(m), 16, initial_norm=initial_norm)
+    _check(got, want, f"apb_f32 n={n} initial_norm={initial_norm}")
+
+
+@pytest.mark.parametrize("mult", [1, 3])
+def test_apb_f32_atom_width_multiplicity(gpu_device, mult):
+    """Head dim 32 (c_s 128, 4 heads), c_z 16 with a norm_z bias, M copies sharing one pair bias."""
+    m = _apb(gpu_device, c_s=128, c_z=16, H=4, ln_bias=True)
+    s, z, mask = _apb_inputs(2, 70, gpu_device, mult=mult, c_s=128, c_z=16)
+    with torch.no_grad():
+        got = m(s, z, mask, multiplicity=mult).cpu()
+    want = oracle.attention_pair_bias(s.cpu(), z.cpu(), mask.cpu(), state(m), 4, multiplicity=mult)
+    _check(got, want, f"apb_f32 c_s=128 mult={mult}")
+
+
+def test_apb_f32_fully_masked_row(gpu_device):
+    """No valid key: every logit is the fill value, the softmax is uniform (as masked_fill + softmax gives)."""
+    m = _apb(gpu_device)
+    s, z, mask = _apb_inputs(1, 33, gpu_device)
+    mask[:] = False
+    with torch.no_grad():
+        got = m(s, z, mask).cpu()
+    want = oracle.attention_pair_bias(s.cpu(), z.cpu(), mask.cpu(), state(m), 16)
+    _check(got, want, "apb_f32 fully masked")
+
+
+def test_apb_f32_padding_and_masked_keys_bit_exact(gpu_device):
+    m = _apb(gpu_device)
+    n, pad = 45, 40
+    s, z, mask = _apb_inputs(1, n, gpu_device)
+    ps = torch.cat([s, torch.full((1, pad, 384), 7.0, device=gpu_device)], 1)
+    pz = torch.full((1, n + pad, n + pad, 128), 1000.0, device=gpu_device)
+    pz[:, :n, :n] = z
+    pm = torch.cat([mask, torch.zeros(1, pad, dtype=torch.bool, device=gpu_device)], 1)
+    s2, z2 = s.clone(), z.clone()
+    s2[0, ~mask[0]] = 50.0
+    z2[0][:, ~mask[0]] = 1000.0
+    with torch.no_grad():
+        a = m(s, z, mask)
+        assert torch.equal(a, m(ps, pz, pm)[:, :n])
+        assert torch.equal(a[mask], m(s2, z2, mask)[mask])
+
+
+def test_apb_f32_fused_residual_and_rows(gpu_device):
+    m = _apb(gpu_device)
+    s, z, mask = _apb_inputs(2, 50, gpu_device, mult=2)
+    with torch.no_grad():
+        upd = m(s, z, mask, multiplicity=2)
+        assert torch.equal(m(s[2:3], z[1:2], mask[1:2]), upd[2:3])
+        ss = s.clone()
+        _ops.launch_apb_f32(ss, z, _ops.mask_u8(mask), *m.prepared_params_f32(), ss, 16, multiplicity=2,
+                            residual=True)
+    assert torch.equal(ss, s + upd)
+
+
+def test_apb_autocast_takes_bf16_path(gpu_device):
+    """Under bf16 autocast (the reference trunk) fp32 inputs compute like the bf16 path."""
+    m = _apb(gpu_device)
+    s, z, mask = _apb_inputs(1, 40, gpu_device)
+    with torch.no_grad():
+        assert _ops.fp32_mode(s)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            assert not _ops.fp32_mode(s)
+            auto = m(s, z, mask)
+        bf = m(s.bfloat16(), z.bfloat16(), mask)
+    assert auto.dtype == F32
+    assert torch.equal(auto, bf.float())
+
+
+# ----------------------------------------------------------------------------
+# AttentionPairBiasSlidingWindow
+# ----------------------------------------------------------------------------
+def _swa(device, c_s=128, c_z=16, heads=4, H=128, initial_norm=True, ln_bias=False, seed=11):
+    torch.manual_seed(seed)
+    m = AttentionPairBiasSlidingWindow(c_s, c_z, heads, window_queries=W, window_keys=H,
+                                       initial_norm=initial_norm, use_bias_in_layer_norm=ln_bias)
+    return randomize_params(m, seed).to(device).eval()
+
+
+def _swa_inputs(B, M, NW, H, c_s, c_z, device, pad=0, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    s = torch.randn(B * M * NW, W, c_s, generator=g)
+    z = torch.randn(B, NW, W, H, c_z, generator=g)
+    mask = torch.ones(B, NW * W, dtype=torch.bool)
+    if pad:
+        mask[:, NW * W - pad:] = False
+    if B > 1:
+        mask[1, 5:9] = False
+    return s.to(device), z.to(device), mask.view(B * NW, W).to(device)
+
+
+@pytest.mark.parametrize(
+    "B,M,NW,H,c_s,heads,c_z,pad,initial_norm,ln_bias",
+    [
+        (1, 1, 4, 128, 128, 4, 16, 0, True, False),
+        (2, 2, 5, 128, 128, 4, 16, 40, True, False),
+        (1, 3, 3, 64, 64, 2, 32, 7, False, True),
+        (1, 1, 2, 96, 384, 12, 16, 3, True, True),
+        (1, 1, 1, 128, 128, 4, 16, 0, True, False),
+    ],
+)
+def test_swa_f32_matches_oracle(gpu_device, B, M, NW, H, c_s, heads, c_z, pad, initial_norm, ln_bias):
+    mod = _swa(gpu_device, c_s, c_z, heads, H, initial_norm, ln_bias)
+    s, z, mask = _swa_inputs(B, M, NW, H, c_s, c_z, gpu_device, pad)
+    with torch.no_grad():
+        got = mod(s, z, mask, multiplicity=M).cpu()
+    want = oracle.attention_pair_bias_sliding_window(s.cpu(), z.cpu(), mask.cpu(), state(mod), heads,
+                                                     multiplicity=M, initial_norm=initial_norm)
+    _check(got, want, f"swa_f32 B={B} M={M} NW={NW} H={H} c_s={c_s} c_z={c_z} pad={pad}")
+
+
+def test_swa_f32_masked_atoms_and_residual(gpu_device):
+    mod = _swa(gpu_device)
+    NW, pad = 6, 45
+    s, z, mask = _swa_inputs(1, 1, NW, 128, 128, 16, gpu_device, pad)
+    s2 = s.clone()
+    s2.view(NW * W, 128)[NW * W - pad:] = 3.0
+    with torch.no_grad():
+        upd = mod(s, z, mask)
+        assert torch.equal(upd.view(NW * W, 128)[: NW * W - pad], mod(s2, z, mask).view(NW * W, 128)[: NW * W - pad])
+        res = s.clone()
+        _ops.launch_swa_f32(res, z, _ops.mask_u8(mask), *mod.prepared_params_f32(), res, 4, residual=True)
+    assert torch.equal(res, s + upd)
+
+
+# ----------------------------------------------------------------------------
+# Transition
+# ----------------------------------------------------------------------------
+def _transition(device, dim, hidden, out_dim=None, use_norm=True, seed=4):
+    torch.manual_seed(seed)
+    return randomize_params(Transition(dim, hidden, out_dim=out_dim, use_norm=use_norm), seed).to(device).eval()
+
+
+@pytest.mark.parametrize(
+    "dim,hidden,out_dim,use_norm,shape",
+    [
+        (384, 768, None, True, (1, 37)),      # token transition of the denoiser
+        (384, 1536, None, False, (2, 100)),
+        (128, 256, None, True, (1, 20, 20)),  # pair-shaped rows (pairwise conditioning)
+        (128, 256, 384, True, (1, 200)),      # dim -> out_dim mixer
+        (384, 256, 128, False, (1, 1)),
+    ],
+)
+def test_transition_f32_matches_oracle(gpu_device, dim, hidden, out_dim, use_norm, shape):
+    m = _transition(gpu_device, dim, hidden, out_dim, use_norm)
+    x = torch.randn(*shape, dim).to(gpu_device)
+    with torch.no_grad():
+        got = m(x).cpu()
+    want = oracle.transition(x.cpu(), state(m), use_norm=use_norm)
+    assert got.shape == want.shape
+    _check(got, want, f"transition_f32 {dim}->{hidden}->{out_dim or dim} {shape} use_norm={use_norm}")
+
+
+def test_transition_f32_rowwise_and_residual(gpu_device):
+    m = _transition(gpu_device, 384, 768)
+    x = torch.randn(3, 41, 384, device=gpu_device)
+    with torch.no_grad():
+        upd = m(x)
+        assert torch.equal(m(x[1:2, 7:30]), upd[1:2, 7:30])
+        xx = x.clone()
+        _ops.launch_transition_f32(xx, *m.prepared_params_f32(), xx, residual=True)
+    assert torch.equal(xx, x + upd)
+
+
+def test_transition_f32_rejects_bad_widths(gpu_device):
+    m = _transition(gpu_device, 384, 768)
+    x = torch.randn(1, 4, 384, device=gpu_device)
+    nw, nb, w1, w2, w3 = m.prepared_params_f32()
+    with pytest.raises(ValueError):
+        _ops.launch_transition_f32(x, nw, nb, w1, w2, w3, torch.empty(1, 4, 100, device=gpu_device))
+    with pytest.raises(ValueError, match="hidden"):   # 760 is not a multiple of 32: the library refuses it
+        _ops.launch_transition_f32(x, nw, nb, w1[:760].contiguous(), w2[:760].contiguous(),
+                                   w3[:, :760].contiguous(), torch.empty_like(x))
+
+
+# ----------------------------------------------------------------------------
+# PairwiseConditioning (diffusion.py:509-535)
+# ----------------------------------------------------------------------------
+@pytest.mark.parametrize(
+    "token_z,c_rel,a_z,num_transitions,shape",
+    [
+        (128, 128, 128, 2, (1, 24, 24)),   # the denoiser's widths
+        (128, 136, 64, 1, (2, 9, 9)),      # a concatenation width (264) that is not a multiple of 64
+        (128, 128, 128, 0, (1, 5, 5)),
+    ],
+)
+def test_pairwise_conditioning_f32_matches_oracle(gpu_device, token_z, c_rel, a_z, num_transitions, shape):
+    from bioemu2_amd.glue import PairwiseConditioning
+
+    torch.manual_seed(0)
+    mod = randomize_params(PairwiseConditioning(token_z, c_rel, a_z=a_z, num_transitions=num_transitions), 5)
+    mod = mod.to(gpu_device)
+    g = torch.Generator().manual_seed(2)
+    z = torch.randn(*shape, token_z, generator=g).to(gpu_device)
+    rel = torch.randn(*shape, c_rel, generator=g).to(gpu_device)
+    got = mod(z, rel).cpu()
+    want = oracle.pairwise_conditioning(z.cpu(), rel.cpu(), state(mod), num_transitions)
+    assert got.shape == want.shape
+    _check(got, want, f"pair_cond_f32 {token_z}+{c_rel}->{a_z} T={num_transitions} {shape}")
+    # row-wise: a sub-block of pairs gives identical bits
+    assert torch.equal(mod(z[:, 1:3].contiguous(), rel[:, 1:3].contiguous()).cpu(), got[:, 1:3])
