@@ -28,7 +28,17 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_F32_TFLOPS = 157.3  # MI355X dense fp32 MFMA
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
+
+
+def _peak(bound: str) -> tuple[float, str, float]:
+    """(published peak, unit, divisor of work/s) for a kernel's bound: bf16 MFMA, fp32 MFMA or HBM."""
+    if bound == "mfma":
+        return PEAK_BF16_TFLOPS, "TFLOP/s", 1e12
+    if bound == "mfma_f32":
+        return PEAK_F32_TFLOPS, "TFLOP/s", 1e12
+    return PEAK_HBM_GBS, "GB/s", 1e9
 
 
 def _parse() -> argparse.Namespace:
@@ -160,12 +170,8 @@ def main() -> int:
     dom_avg_ms = dom_ms / dom_launches
     work = wl.kernel_work(dom_name)  # (bound, algorithmic amount per launch)
     bound, amount = work
-    if bound == "mfma":
-        achieved = amount / (dom_avg_ms * 1e-3) / 1e12
-        peak, unit = PEAK_BF16_TFLOPS, "TFLOP/s"
-    else:
-        achieved = amount / (dom_avg_ms * 1e-3) / 1e9
-        peak, unit = PEAK_HBM_GBS, "GB/s"
+    peak, unit, div = _peak(bound)
+    achieved = amount / (dom_avg_ms * 1e-3) / div
     roofline = {
         "kernel": dom_name,
         "bound": bound,
@@ -186,14 +192,15 @@ def main() -> int:
             per_kernel[name] = {"launches_per_step": n / args.steps, "avg_ms": round(ms / n, 5)}
             continue
         avg = ms / n
-        rate = a / (avg * 1e-3) / (1e12 if b == "mfma" else 1e9)
+        pk, _, div = _peak(b)
+        rate = a / (avg * 1e-3) / div
         per_kernel[name] = {
             "launches_per_step": n / args.steps,
             "avg_ms": round(avg, 5),
             "bound": b,
             "work": a,
             "rate": round(rate, 1),
-            "frac": round(rate / (PEAK_BF16_TFLOPS if b == "mfma" else PEAK_HBM_GBS), 4),
+            "frac": round(rate / pk, 4),
         }
     if args.kernels:
         for k, v in per_kernel.items():
@@ -214,7 +221,7 @@ def main() -> int:
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": getattr(wl, "dtype", "bf16"),
         "data": "synthetic (seeded randn inputs, seeded random-init weights)",
         "config": wl.config,
         "tflops": round(wl.flops / (ms_per_step * 1e-3) / 1e12, 1),

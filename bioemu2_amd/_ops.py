@@ -734,6 +734,8 @@ def launch_swa_f32(
     _check_tensor(out, "swa_f32 out", F32, (folded, W, c_s), dev)
     _check_tensor(z, "swa_f32 z", F32, (B, NW, W, H, c_z), dev)
     _check_tensor(mask, "swa_f32 mask", torch.uint8, (B * NW, W), dev)
+    if mask.data_ptr() % 4:   # the kernel reads the mask 4 keys at a time
+        mask = mask.clone()
     _check_attn_params_f32("swa_f32", c_s, c_z, num_heads, dev, norm_s_w, norm_s_b, w_qkv, q_bias, w_g, norm_z_w,
                            norm_z_b, w_z, w_o)
     need = swa_f32_workspace_bytes(B, multiplicity, NW, W, H, c_s, num_heads)

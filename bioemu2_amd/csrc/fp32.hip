@@ -6,7 +6,8 @@
 // token transitions (transition.py:52-91) compute in fp32 on fp32 inputs.  These
 // entry points do the same: fp32 operands and fp32 accumulation throughout.
 //
-//   gemm_f32      out = epi(A W^T) on v_mfma_f32_32x32x2_f32.  A wave owns a
+//   gemm_f32      out = epi(A W^T) on v_mfma_f32_32x32x2_f32 (qkvg_f32: the four
+//                 token projections of an attention in one launch).  A wave owns a
 //                 32 x 32 output block: weight rows (output channels) are the
 //                 MFMA A operand in perm32 order (pairtile.h), token rows the B
 //                 operand, so a lane ends with 16 consecutive channels of one
@@ -18,10 +19,11 @@
 //   pair_proj_f32 pair bias: LN(z) W^T per pair row, one thread per row, written
 //                 head-major ([outer][head][inner]).
 //   attn_f32      softmax(q k^T / sqrt(d) + bias; masked keys -> -1e6) v, gated by
-//                 g: one thread per query, 64-key blocks of K and V in LDS,
-//                 blockwise online softmax.
+//                 g: flash attention on the same fp32 MFMA, a wave per 32
+//                 queries, 32-key blocks, online softmax in registers.
 //   swa_attn_f32  the same over the sliding key window of each 32-atom window.
 #include <algorithm>
+#include <cmath>
 
 #include "common.h"
 #include "internal.h"
@@ -33,6 +35,9 @@ namespace {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kGemmEpiStore = 0, kGemmEpiSigmoid = 1, kGemmEpiSwiGLU = 2, kGemmEpiResidual = 3;
+// kGemmEpiStoreT writes the transpose per sequence: row m = s * T + t, channel
+// c -> out[(s * N + c) * ldT + t] (keys contiguous, for the P.V operand).
+constexpr int kGemmEpiStoreT = 4;
 
 __device__ __forceinline__ f32x16 mfma_f32(float a, float b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
@@ -47,7 +52,8 @@ __device__ __forceinline__ float wave_sum(float v) {
 template <int kEpi>
 __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ W,
                                                        const float* __restrict__ W2, const float* __restrict__ bias,
-                                                       const float* res, float* out, long long M, int K, int N) {
+                                                       const float* res, float* out, long long M, int K, int N,
+                                                       int T, int ldT) {
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int n = lane & 31, h = lane >> 5;
   const int nbc = N / 32;
@@ -86,6 +92,13 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__
     if (kEpi == kGemmEpiSwiGLU) x = x / (1.0f + __expf(-x)) * acc2[u];
     v[u] = x;
   }
+  if (kEpi == kGemmEpiStoreT) {
+    const long long sq = m / T, t = m % T;
+    float* col = out + ((size_t)sq * N + c0) * ldT + t;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) col[(size_t)u * ldT] = v[u];
+    return;
+  }
   float* dst = out + (size_t)m * N + c0;
   if (kEpi == kGemmEpiResidual) {
     const float* r = res + (size_t)m * N + c0;
@@ -102,6 +115,65 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__
 #pragma unroll
     for (int e = 0; e < 4; ++e) o4[e] = v[4 * q + e];
     *reinterpret_cast<f32x4*>(dst + 4 * q) = o4;
+  }
+}
+
+// The four token projections of an attention in one launch: column blocks
+// [0, c_s) -> q (+ q bias), [c_s, 2c_s) -> k, [2c_s, 3c_s) -> v stored
+// transposed per sequence (as kGemmEpiStoreT), [3c_s, 4c_s) -> sigmoid(g).
+// Same wave tiling as gemm_f32_kernel; the column block picks weight rows and
+// epilogue (wave-uniform).
+__global__ __launch_bounds__(256) void qkvg_f32_kernel(const float* __restrict__ A, const float* __restrict__ w_qkv,
+                                                       const float* __restrict__ w_g, const float* __restrict__ q_bias,
+                                                       float* __restrict__ q, float* __restrict__ k,
+                                                       float* __restrict__ vt, float* __restrict__ g, long long M,
+                                                       int c_s, int T, int ldT) {
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int n = lane & 31, h = lane >> 5;
+  const int nbc = c_s / 32;
+  const long long blk = (long long)blockIdx.x * 4 + wave;
+  const long long mblocks = (M + 31) / 32;
+  if (blk >= mblocks * 4 * nbc) return;   // no barriers in this kernel
+  const long long mb = blk / (4 * nbc);
+  const int cbt = (int)(blk % (4 * nbc));
+  const int part = cbt / nbc, cb = cbt % nbc;
+  const long long m = mb * 32 + n;
+  const bool mvalid = m < M;
+  const int K = c_s;
+  const float* arow = A + (size_t)(mvalid ? m : 0) * K + 4 * h;
+  const float* wbase = part < 3 ? w_qkv + (size_t)part * c_s * c_s : w_g;
+  const float* wrow = wbase + (size_t)(cb * 32 + perm32(n)) * K + 4 * h;
+  f32x16 acc = zero16();
+  for (int k0 = 0; k0 < K; k0 += 8) {
+    const f32x4 a4 = *reinterpret_cast<const f32x4*>(arow + k0);
+    const f32x4 w4 = *reinterpret_cast<const f32x4*>(wrow + k0);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc = mfma_f32(w4[e], a4[e], acc);
+  }
+  if (!mvalid) return;
+  const int c0 = cb * 32 + 16 * h;
+  if (part == 2) {
+    const long long sq = m / T, t = m % T;
+    float* col = vt + ((size_t)sq * c_s + c0) * ldT + t;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) col[(size_t)u * ldT] = acc[u];
+    return;
+  }
+  float v[16];
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {
+    float x = acc[u];
+    if (part == 0) x += q_bias[c0 + u];
+    if (part == 3) x = 1.0f / (1.0f + __expf(-x));
+    v[u] = x;
+  }
+  float* dst = (part == 0 ? q : part == 1 ? k : g) + (size_t)m * c_s + c0;
+#pragma unroll
+  for (int qd = 0; qd < 4; ++qd) {
+    f32x4 o4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o4[e] = v[4 * qd + e];
+    *reinterpret_cast<f32x4*>(dst + 4 * qd) = o4;
   }
 }
 
@@ -130,11 +202,13 @@ __global__ __launch_bounds__(256) void rows_ln_f32_kernel(const float* __restric
   for (int k = lane; k < K; k += 64) yr[k] = (at(k) - mean) * rstd * g[k] + (b ? b[k] : 0.f);
 }
 
+// Pair bias LN(z) W^T, one thread per pair row: every lane reads the same
+// weight, so the head loop's weight reads are wave-uniform.
 template <int CZ>
 __global__ __launch_bounds__(256) void pair_proj_f32_kernel(const float* __restrict__ z, const float* __restrict__ g,
                                                             const float* __restrict__ b, const float* __restrict__ w,
-                                                            float* __restrict__ out, long long P, long long inner,
-                                                            int H) {
+                                                            float* __restrict__ out, long long P, int nrows, int ncols,
+                                                            int ld, int H) {
   const long long p = (long long)blockIdx.x * 256 + threadIdx.x;
   if (p >= P) return;
   float v[CZ];
@@ -158,185 +232,278 @@ __global__ __launch_bounds__(256) void pair_proj_f32_kernel(const float* __restr
   const float rstd = 1.0f / sqrtf(ss / (float)CZ + 1e-5f);
 #pragma unroll
   for (int c = 0; c < CZ; ++c) v[c] = (v[c] - mean) * rstd * g[c] + (b ? b[c] : 0.f);
+  const long long inner = (long long)nrows * ncols;
   const long long outer = p / inner, idx = p % inner;
+  const long long r = idx / ncols, col = idx % ncols;
   for (int hh = 0; hh < H; ++hh) {
     float acc = 0.f;
 #pragma unroll
     for (int c = 0; c < CZ; ++c) acc += w[hh * CZ + c] * v[c];
-    out[((size_t)outer * H + hh) * inner + idx] = acc;
+    out[(((size_t)outer * H + hh) * nrows + r) * ld + col] = acc;
   }
 }
 
-// Full attention: grid (ceil(N / 128), H, B * mult); thread = query.
+// ---------------------------------------------------------------------------
+// Flash attention on fp32 MFMA.  A wave owns 32 queries of one (copy, head)
+// and walks 32-key blocks:
+//   S^T = K Q^T       d/2 MFMAs; lane (r, h) supplies key row r, d-slots
+//                     h*d/2 + e (A) and query r's same d-slots (B), so lane
+//                     (n, h) ends with query n's logits for keys
+//                     8*(u/4) + 4h + u%4 (register u);
+//   softmax           blockwise online softmax in registers (max over the
+//                     lane pair n, n+32 by one shuffle);
+//   O^T = V^T P^T     16 MFMAs of 2 keys: MFMA e takes register e of P (key
+//                     8*(e/4) + 4h + e%4 in lane half h) and, as A, V^T at
+//                     channel c = lane % 32 (zero for c >= d) and that key.
+// Lane (n, h) ends with channels 8*(u/4) + 4h + u%4 of query n.
+// Logits follow the reference: q.k / sqrt(d) + bias, a masked key's logit
+// replaced by -1e6; keys past the sequence are left out (weight 0).
+// ---------------------------------------------------------------------------
 template <int D>
-__global__ __launch_bounds__(128) void attn_f32_kernel(const float* __restrict__ q, const float* __restrict__ k,
-                                                       const float* __restrict__ v, const float* __restrict__ g,
+struct F32KeyBlock {
+  f32x4 k[D / 8];     // K row (key k0 + n), d-slots h*d/2 ..
+  f32x4 bias[4];      // bias of query n at keys k0 + 8j + 4h + 0..3
+  f32x4 v[4];         // V^T at channel n, keys k0 + 8j + 4h + 0..3
+  unsigned keep;      // bit u: key of register u unmasked
+  unsigned live;      // bit u: key of register u exists (else weight 0)
+};
+
+// Mask bytes of keys 8j + 4h + 0..3 (one 32-bit word per j) -> keep bits.
+__device__ __forceinline__ unsigned keep_bits(const unsigned (&w)[4]) {
+  unsigned keep = 0u;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) keep |= (unsigned)(((w[j] >> (8 * t)) & 0xffu) != 0u) << (4 * j + t);
+  return keep;
+}
+
+template <int D>
+__device__ __forceinline__ void f32_attend_block(const F32KeyBlock<D>& kb, const float (&qv)[D / 2], float rsq,
+                                                 f32x16& o, float& m, float& l) {
+  f32x16 s = zero16();
+#pragma unroll
+  for (int e = 0; e < D / 2; ++e) s = mfma_f32(kb.k[e >> 2][e & 3], qv[e], s);
+  float x[16];
+  float bmax = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {
+    const float logit = ((kb.keep >> u) & 1u) ? s[u] * rsq + kb.bias[u >> 2][u & 3] : -1e6f;
+    x[u] = ((kb.live >> u) & 1u) ? logit : -INFINITY;
+    bmax = fmaxf(bmax, x[u]);
+  }
+  bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+  const float m_new = fmaxf(m, bmax);
+  const float alpha = __expf(m - m_new);
+  l *= alpha;
+#pragma unroll
+  for (int u = 0; u < 16; ++u) o[u] *= alpha;
+  float p[16];
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {
+    p[u] = __expf(x[u] - m_new);
+    l += p[u];
+  }
+#pragma unroll
+  for (int e = 0; e < 16; ++e) o = mfma_f32(kb.v[e >> 2][e & 3], p[e], o);
+  m = m_new;
+}
+
+// Writes g * o / l for this lane's channels (lane (n, h): 8j + 4h + 0..3).
+template <int D>
+__device__ __forceinline__ void f32_attend_store(const f32x16& o, float l, const float* g, float* go, bool store) {
+  l += __shfl_xor(l, 32);
+  if (!store) return;
+  const float inv = 1.0f / l;
+  const int h = (threadIdx.x & 63) >> 5;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = 8 * j + 4 * h;
+    if (c < D) {
+      const f32x4 gv = *reinterpret_cast<const f32x4*>(g + c);
+      f32x4 r;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) r[t] = gv[t] * (o[4 * j + t] * inv);
+      *reinterpret_cast<f32x4*>(go + c) = r;
+    }
+  }
+}
+
+template <int D>
+__device__ __forceinline__ void load_q_f32(const float* qr, float (&qv)[D / 2]) {
+#pragma unroll
+  for (int j = 0; j < D / 8; ++j) {
+    const f32x4 t = *reinterpret_cast<const f32x4*>(qr + 4 * j);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) qv[4 * j + e] = t[e];
+  }
+}
+
+// Full attention: grid (ceil(N / 128), H, B * mult), 4 waves of 32 queries
+// sharing each 32-key block of K, V^T and the mask through LDS (staged once
+// per workgroup, double-buffered).  bias [B][H][N][ld], V^T [B*mult][c_s][ld]
+// (ld = N rounded up to 32; columns >= N unused).
+template <int D>
+__global__ __launch_bounds__(256) void attn_f32_kernel(const float* __restrict__ q, const float* __restrict__ k,
+                                                       const float* __restrict__ vt, const float* __restrict__ g,
                                                        const float* __restrict__ bias,
                                                        const uint8_t* __restrict__ mask, float* __restrict__ go,
-                                                       int N, int H, int c_s, int mult) {
-  __shared__ float ks[64][D], vs[64][D];
-  __shared__ uint8_t ms[64];
+                                                       int N, int ld, int H, int c_s, int mult, float rsq) {
+  constexpr int KS = D + 4, VS = 36, KQ = D / 4;
+  __shared__ __attribute__((aligned(16))) float ks[2][32][KS];
+  __shared__ __attribute__((aligned(16))) float vs[2][D][VS];
+  __shared__ __attribute__((aligned(16))) uint8_t ms[2][32];
+  const int tid = threadIdx.x, lane = tid & 63, n = lane & 31, h = lane >> 5;
   const int hd = blockIdx.y, bm = blockIdx.z, b = bm / mult;
-  const int i = blockIdx.x * 128 + threadIdx.x;
-  const bool qvalid = i < N;
-  const int ic = qvalid ? i : 0;
-  float qv[D], o[D];
-  const float* qr = q + ((size_t)bm * N + ic) * c_s + hd * D;
+  const int q0 = (blockIdx.x * 4 + wave_id()) * 32;
+  // waves past N run on a clamped row and store nothing: they stage their
+  // share of every block and meet every barrier
+  const int qi = min(q0 + n, N - 1);
+  float qv[D / 2];
+  load_q_f32<D>(q + ((size_t)bm * N + qi) * c_s + hd * D + h * (D / 2), qv);
+  const float* brow = bias + (((size_t)b * H + hd) * N + qi) * ld;
+  const float* kbase = k + (size_t)bm * N * c_s + hd * D;
+  const float* vtb = vt + ((size_t)bm * c_s + hd * D) * ld;
+  const uint8_t* mrow = mask + (size_t)b * N;
+  // staging: thread tid moves K float4 (key tid / KQ, chunk tid % KQ) and
+  // V^T float4 (channel tid / 8, keys 4 (tid % 8) ..), thread tid < 32 a mask byte
+  const int sk_key = tid / KQ, sk_chunk = tid % KQ;
+  const int sv_row = tid >> 3, sv_chunk = tid & 7;
+  f32x4 rk, rv;
+  uint8_t rm = 0;
+  auto gload = [&](int k0) {
+    if (tid < 32 * KQ) rk = *reinterpret_cast<const f32x4*>(kbase + (size_t)min(k0 + sk_key, N - 1) * c_s + 4 * sk_chunk);
+    if (tid < D * 8) {
+      rv = *reinterpret_cast<const f32x4*>(vtb + (size_t)sv_row * ld + k0 + 4 * sv_chunk);
 #pragma unroll
-  for (int d = 0; d < D; ++d) {
-    qv[d] = qr[d];
-    o[d] = 0.f;
-  }
-  const float sqrt_d = sqrtf((float)D);
-  const float* brow = bias + (((size_t)b * H + hd) * N + ic) * N;
+      for (int e = 0; e < 4; ++e)
+        if (k0 + 4 * sv_chunk + e >= N) rv[e] = 0.f;   // unwritten columns past N
+    }
+    if (tid < 32) rm = k0 + tid < N ? mrow[k0 + tid] : 0;
+  };
+  auto lstore = [&](int st) {
+    if (tid < 32 * KQ) *reinterpret_cast<f32x4*>(&ks[st][sk_key][4 * sk_chunk]) = rk;
+    if (tid < D * 8) *reinterpret_cast<f32x4*>(&vs[st][sv_row][4 * sv_chunk]) = rv;
+    if (tid < 32) ms[st][tid] = rm;
+  };
+  auto bload = [&](int k0, f32x4 (&bb)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bb[j] = *reinterpret_cast<const f32x4*>(brow + k0 + 8 * j + 4 * h);
+  };
+  f32x16 o = zero16();
   float m = -INFINITY, l = 0.f;
-  for (int j0 = 0; j0 < N; j0 += 64) {
+  F32KeyBlock<D> kb;
+  f32x4 bnext[4];
+  gload(0);
+  bload(0, kb.bias);
+  lstore(0);
+  __syncthreads();
+  int st = 0;
+#pragma unroll 1
+  for (int k0 = 0; k0 < N; k0 += 32) {
+    const bool more = k0 + 32 < N;
+    if (more) {
+      gload(k0 + 32);
+      bload(k0 + 32, bnext);
+    }
+#pragma unroll
+    for (int j = 0; j < D / 8; ++j) kb.k[j] = *reinterpret_cast<const f32x4*>(&ks[st][n][h * (D / 2) + 4 * j]);
+    unsigned w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      kb.v[j] = n < D ? *reinterpret_cast<const f32x4*>(&vs[st][n < D ? n : 0][8 * j + 4 * h]) : f32x4{0.f, 0.f, 0.f, 0.f};
+      w[j] = *reinterpret_cast<const unsigned*>(&ms[st][8 * j + 4 * h]);
+    }
+    kb.keep = keep_bits(w);
+    kb.live = 0u;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) kb.live |= (unsigned)(k0 + 8 * (u >> 2) + 4 * h + (u & 3) < N) << u;
+    f32_attend_block<D>(kb, qv, rsq, o, m, l);
+    if (more) {
+      lstore(st ^ 1);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) kb.bias[j] = bnext[j];
+    }
     __syncthreads();
-    for (int t = threadIdx.x; t < 64 * D; t += 128) {
-      const int kk = t / D, d = t % D, j = j0 + kk;
-      const size_t off = ((size_t)bm * N + (j < N ? j : 0)) * c_s + hd * D + d;
-      ks[kk][d] = j < N ? k[off] : 0.f;
-      vs[kk][d] = j < N ? v[off] : 0.f;
-    }
-    if (threadIdx.x < 64) ms[threadIdx.x] = j0 + threadIdx.x < N ? mask[(size_t)b * N + j0 + threadIdx.x] : 0;
-    __syncthreads();
-    const int jn = min(64, N - j0);
-    float lg[64];
-    float bmax = -INFINITY;
-#pragma unroll
-    for (int jj = 0; jj < 64; ++jj) {
-      if (jj < jn) {
-        float dot = 0.f;
-#pragma unroll
-        for (int d = 0; d < D; ++d) dot += qv[d] * ks[jj][d];
-        const float x = ms[jj] ? dot / sqrt_d + brow[j0 + jj] : -1e6f;
-        lg[jj] = x;
-        bmax = fmaxf(bmax, x);
-      }
-    }
-    const float m_new = fmaxf(m, bmax);
-    const float alpha = __expf(m - m_new);
-    l *= alpha;
-#pragma unroll
-    for (int d = 0; d < D; ++d) o[d] *= alpha;
-#pragma unroll
-    for (int jj = 0; jj < 64; ++jj) {
-      if (jj < jn) {
-        const float p = __expf(lg[jj] - m_new);
-        l += p;
-#pragma unroll
-        for (int d = 0; d < D; ++d) o[d] += p * vs[jj][d];
-      }
-    }
-    m = m_new;
+    st ^= 1;
   }
-  if (!qvalid) return;
-  const size_t off = ((size_t)bm * N + i) * c_s + hd * D;
-  const float inv = 1.0f / l;
-#pragma unroll
-  for (int d = 0; d < D; ++d) go[off + d] = g[off + d] * (o[d] * inv);
+  const size_t off = ((size_t)bm * N + qi) * c_s + hd * D;
+  f32_attend_store<D>(o, l, g + off, go + off, q0 + n < N);
 }
 
-// Sliding-window attention: grid (NW, ceil(heads / 4), B * mult); thread = (head in group, query in window).
-template <int D>
-__global__ __launch_bounds__(128) void swa_attn_f32_kernel(const float* __restrict__ q, const float* __restrict__ k,
-                                                           const float* __restrict__ v, const float* __restrict__ g,
+// Sliding-window attention: grid (NW, ceil(heads / 4), B * mult); wave = head,
+// its 32 queries are window w's atoms, its keys the Hk positions starting
+// (Hk - 32) / 2 before the window (outside the sequence: masked, v = 0; a
+// group of 4 keys 4-aligned is wholly inside or outside).  bias
+// [B * NW][heads][32][Hk], V^T [B*mult][c_s][NA].
+__global__ __launch_bounds__(256) void swa_attn_f32_kernel(const float* __restrict__ q, const float* __restrict__ k,
+                                                           const float* __restrict__ vt, const float* __restrict__ g,
                                                            const float* __restrict__ bias,
                                                            const uint8_t* __restrict__ mask, float* __restrict__ go,
-                                                           int NW, int Hk, int heads, int c_s, int mult) {
-  constexpr int W = 32;
-  __shared__ float ks[4][W][D], vs[4][W][D];
-  __shared__ uint8_t ms[W];
+                                                           int NW, int Hk, int heads, int c_s, int mult, float rsq) {
+  constexpr int D = 32, W = 32;
+  const int lane = threadIdx.x & 63, n = lane & 31, h = lane >> 5;
   const int w = blockIdx.x, bm = blockIdx.z, b = bm / mult;
-  const int hq = threadIdx.x / W, iq = threadIdx.x % W;
-  const int hd = blockIdx.y * 4 + hq;
-  const bool hvalid = hd < heads;
-  const int hc = hvalid ? hd : 0;
+  const int hd = blockIdx.y * 4 + wave_id();
+  if (hd >= heads) return;   // no barriers in this kernel
   const int NA = NW * W, ctx = (Hk - W) / 2;
-  const int aq = w * W + iq;
-  float qv[D], o[D];
-  const float* qr = q + ((size_t)bm * NA + aq) * c_s + hc * D;
+  const int aq = w * W + n;
+  float qv[D / 2];
+  load_q_f32<D>(q + ((size_t)bm * NA + aq) * c_s + hd * D + h * (D / 2), qv);
+  const float* brow = bias + ((((size_t)b * NW + w) * heads + hd) * W + n) * Hk;
+  const float* kbase = k + (size_t)bm * NA * c_s + hd * D;
+  const float* vtrow = vt + ((size_t)bm * c_s + hd * D + n) * NA;
+  const uint8_t* mrow = mask + (size_t)b * NA;
+  const int a0 = w * W - ctx;
+  auto fetch = [&](int t0, F32KeyBlock<D>& kb) {
+    const float* kr = kbase + (size_t)min(max(a0 + t0 + n, 0), NA - 1) * c_s + h * (D / 2);
 #pragma unroll
-  for (int d = 0; d < D; ++d) {
-    qv[d] = qr[d];
-    o[d] = 0.f;
-  }
-  const float sqrt_d = sqrtf((float)D);
-  const float* brow = bias + ((((size_t)b * NW + w) * heads + hc) * W + iq) * Hk;
+    for (int j = 0; j < D / 8; ++j) kb.k[j] = *reinterpret_cast<const f32x4*>(kr + 4 * j);
+    unsigned mw[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      kb.bias[j] = *reinterpret_cast<const f32x4*>(brow + t0 + 8 * j + 4 * h);
+      const int a = a0 + t0 + 8 * j + 4 * h;
+      const bool in = a >= 0 && a < NA;
+      kb.v[j] = in ? *reinterpret_cast<const f32x4*>(vtrow + a) : f32x4{0.f, 0.f, 0.f, 0.f};
+      mw[j] = in ? *reinterpret_cast<const unsigned*>(mrow + a) : 0u;
+    }
+    kb.keep = keep_bits(mw);
+    kb.live = 0xffffu;
+  };
+  f32x16 o = zero16();
   float m = -INFINITY, l = 0.f;
-  for (int t0 = 0; t0 < Hk; t0 += W) {
-    __syncthreads();
-    for (int t = threadIdx.x; t < 4 * W * D; t += 128) {
-      const int gh = t / (W * D), kk = (t / D) % W, d = t % D;
-      const int a = w * W - ctx + t0 + kk, hh = blockIdx.y * 4 + gh;
-      const bool ok = a >= 0 && a < NA && hh < heads;
-      const size_t off = ((size_t)bm * NA + (ok ? a : 0)) * c_s + (hh < heads ? hh : 0) * D + d;
-      ks[gh][kk][d] = ok ? k[off] : 0.f;
-      vs[gh][kk][d] = ok ? v[off] : 0.f;
-    }
-    if (threadIdx.x < W) {
-      const int a = w * W - ctx + t0 + threadIdx.x;
-      ms[threadIdx.x] = (a >= 0 && a < NA) ? mask[(size_t)b * NA + a] : 0;
-    }
-    __syncthreads();
-    float lg[W];
-    float bmax = -INFINITY;
-#pragma unroll
-    for (int jj = 0; jj < W; ++jj) {
-      float dot = 0.f;
-#pragma unroll
-      for (int d = 0; d < D; ++d) dot += qv[d] * ks[hq][jj][d];
-      const float x = ms[jj] ? dot / sqrt_d + brow[t0 + jj] : -1e6f;
-      lg[jj] = x;
-      bmax = fmaxf(bmax, x);
-    }
-    const float m_new = fmaxf(m, bmax);
-    const float alpha = __expf(m - m_new);
-    l *= alpha;
-#pragma unroll
-    for (int d = 0; d < D; ++d) o[d] *= alpha;
-#pragma unroll
-    for (int jj = 0; jj < W; ++jj) {
-      const float p = __expf(lg[jj] - m_new);
-      l += p;
-#pragma unroll
-      for (int d = 0; d < D; ++d) o[d] += p * vs[hq][jj][d];
-    }
-    m = m_new;
+  F32KeyBlock<D> cur, nxt;
+  fetch(0, cur);
+#pragma unroll 1
+  for (int t0 = 0; t0 < Hk; t0 += 32) {
+    if (t0 + 32 < Hk) fetch(t0 + 32, nxt);
+    f32_attend_block<D>(cur, qv, rsq, o, m, l);
+    cur = nxt;
   }
-  if (!hvalid) return;
   const size_t off = ((size_t)bm * NA + aq) * c_s + hd * D;
-  const float inv = 1.0f / l;
-#pragma unroll
-  for (int d = 0; d < D; ++d) go[off + d] = g[off + d] * (o[d] * inv);
+  f32_attend_store<D>(o, l, g + off, go + off, true);
 }
 
 int gemm_f32(int epi, const float* A, const float* W, const float* W2, const float* bias, const float* res, float* out,
-             long long M, int K, int N, hipStream_t stream, const char* name) {
+             long long M, int K, int N, hipStream_t stream, const char* name, int T = 1, int ldT = 1) {
   if (K % 8 || N % 32 || M <= 0)
     return set_error(BIOEMU_ERR_UNSUPPORTED, "%s: fp32 GEMM needs K %% 8 == 0 and N %% 32 == 0 (K=%d N=%d)", name, K,
                      N);
   const long long blocks = (M + 31) / 32 * (N / 32);
   const unsigned grid = (unsigned)((blocks + 3) / 4);
   KernelTimerScope timed(name, stream);
+#define BIOEMU_GEMM_F32(E)                                                                                      \
+  hipLaunchKernelGGL(gemm_f32_kernel<E>, dim3(grid), dim3(256), 0, stream, A, W, W2, bias, res, out, M, K, N, T, \
+                     ldT)
   switch (epi) {
-    case kGemmEpiStore:
-      hipLaunchKernelGGL(gemm_f32_kernel<kGemmEpiStore>, dim3(grid), dim3(256), 0, stream, A, W, W2, bias, res, out, M,
-                         K, N);
-      break;
-    case kGemmEpiSigmoid:
-      hipLaunchKernelGGL(gemm_f32_kernel<kGemmEpiSigmoid>, dim3(grid), dim3(256), 0, stream, A, W, W2, bias, res, out,
-                         M, K, N);
-      break;
-    case kGemmEpiSwiGLU:
-      hipLaunchKernelGGL(gemm_f32_kernel<kGemmEpiSwiGLU>, dim3(grid), dim3(256), 0, stream, A, W, W2, bias, res, out,
-                         M, K, N);
-      break;
-    default:
-      hipLaunchKernelGGL(gemm_f32_kernel<kGemmEpiResidual>, dim3(grid), dim3(256), 0, stream, A, W, W2, bias, res,
-                         out, M, K, N);
-      break;
+    case kGemmEpiStore: BIOEMU_GEMM_F32(kGemmEpiStore); break;
+    case kGemmEpiSigmoid: BIOEMU_GEMM_F32(kGemmEpiSigmoid); break;
+    case kGemmEpiSwiGLU: BIOEMU_GEMM_F32(kGemmEpiSwiGLU); break;
+    case kGemmEpiStoreT: BIOEMU_GEMM_F32(kGemmEpiStoreT); break;
+    default: BIOEMU_GEMM_F32(kGemmEpiResidual); break;
   }
+#undef BIOEMU_GEMM_F32
   return check_launch(name);
 }
 
@@ -348,16 +515,20 @@ int rows_ln_f32(const float* x, const float* g, const float* b, float* y, long l
   return check_launch(name);
 }
 
+// Bias rows: P pair rows = outer x nrows x ncols -> out[outer][head][row][col] with row stride ld.
 int pair_proj_f32(const float* z, const float* g, const float* b, const float* w, float* out, long long P,
-                  long long inner, int H, int c_z, hipStream_t stream, const char* name) {
+                  int nrows, int ncols, int ld, int H, int c_z, hipStream_t stream, const char* name) {
   const unsigned grid = (unsigned)((P + 255) / 256);
   KernelTimerScope timed(name, stream);
   if (c_z == 128)
-    hipLaunchKernelGGL(pair_proj_f32_kernel<128>, dim3(grid), dim3(256), 0, stream, z, g, b, w, out, P, inner, H);
+    hipLaunchKernelGGL(pair_proj_f32_kernel<128>, dim3(grid), dim3(256), 0, stream, z, g, b, w, out, P, nrows, ncols,
+                       ld, H);
   else if (c_z == 32)
-    hipLaunchKernelGGL(pair_proj_f32_kernel<32>, dim3(grid), dim3(256), 0, stream, z, g, b, w, out, P, inner, H);
+    hipLaunchKernelGGL(pair_proj_f32_kernel<32>, dim3(grid), dim3(256), 0, stream, z, g, b, w, out, P, nrows, ncols,
+                       ld, H);
   else if (c_z == 16)
-    hipLaunchKernelGGL(pair_proj_f32_kernel<16>, dim3(grid), dim3(256), 0, stream, z, g, b, w, out, P, inner, H);
+    hipLaunchKernelGGL(pair_proj_f32_kernel<16>, dim3(grid), dim3(256), 0, stream, z, g, b, w, out, P, nrows, ncols,
+                       ld, H);
   else
     return set_error(BIOEMU_ERR_UNSUPPORTED, "%s: c_z %d unsupported (16, 32 or 128)", name, c_z);
   return check_launch(name);
@@ -368,7 +539,9 @@ struct AttnF32Buffers {
   float *sn, *q, *k, *v, *g, *go, *bias;
 };
 
-size_t attn_f32_layout(long long rows, int c_s, long long bias_elems, bool norm, AttnF32Buffers* buf, char* base) {
+// v is stored transposed per sequence ([sequence][c_s][ldv], keys contiguous): v_elems = sequences * c_s * ldv.
+size_t attn_f32_layout(long long rows, int c_s, long long v_elems, long long bias_elems, bool norm,
+                       AttnF32Buffers* buf, char* base) {
   size_t off = 0;
   auto take = [&](float** p, size_t elems) {
     if (buf) *p = reinterpret_cast<float*>(base + off);
@@ -379,7 +552,7 @@ size_t attn_f32_layout(long long rows, int c_s, long long bias_elems, bool norm,
   take(&b->sn, norm ? (size_t)rows * c_s : 0);
   take(&b->q, (size_t)rows * c_s);
   take(&b->k, (size_t)rows * c_s);
-  take(&b->v, (size_t)rows * c_s);
+  take(&b->v, (size_t)v_elems);
   take(&b->g, (size_t)rows * c_s);
   take(&b->go, (size_t)rows * c_s);
   take(&b->bias, (size_t)bias_elems);
@@ -388,22 +561,20 @@ size_t attn_f32_layout(long long rows, int c_s, long long bias_elems, bool norm,
 
 int attn_f32_projections(const float* s, const float* norm_s_w, const float* norm_s_b, const float* w_qkv,
                          const float* q_bias, const float* w_g, AttnF32Buffers& buf, long long rows, int c_s,
-                         hipStream_t stream) {
+                         int seq_len, int ldv, hipStream_t stream) {
   const float* src = s;
   int rc = 0;
   if (norm_s_w) {
     rc = rows_ln_f32(s, norm_s_w, norm_s_b, buf.sn, rows, c_s, stream, "f32_layernorm");
     src = buf.sn;
   }
-  const size_t cc = (size_t)c_s * c_s;
-  if (!rc) rc = gemm_f32(kGemmEpiStore, src, w_qkv, nullptr, q_bias, nullptr, buf.q, rows, c_s, c_s, stream, "f32_proj_q");
-  if (!rc)
-    rc = gemm_f32(kGemmEpiStore, src, w_qkv + cc, nullptr, nullptr, nullptr, buf.k, rows, c_s, c_s, stream, "f32_proj_k");
-  if (!rc)
-    rc = gemm_f32(kGemmEpiStore, src, w_qkv + 2 * cc, nullptr, nullptr, nullptr, buf.v, rows, c_s, c_s, stream,
-                  "f32_proj_v");
-  if (!rc) rc = gemm_f32(kGemmEpiSigmoid, src, w_g, nullptr, nullptr, nullptr, buf.g, rows, c_s, c_s, stream, "f32_proj_g");
-  return rc;
+  if (rc) return rc;
+  if (c_s % 32) return set_error(BIOEMU_ERR_UNSUPPORTED, "f32 attention: c_s %d is not a multiple of 32", c_s);
+  const long long blocks = (rows + 31) / 32 * (4 * (c_s / 32));
+  KernelTimerScope timed("f32_proj_qkvg", stream);
+  hipLaunchKernelGGL(qkvg_f32_kernel, dim3((unsigned)((blocks + 3) / 4)), dim3(256), 0, stream, src, w_qkv, w_g, q_bias,
+                     buf.q, buf.k, buf.v, buf.g, rows, c_s, seq_len, ldv);
+  return check_launch("f32_proj_qkvg");
 }
 
 }  // namespace
@@ -413,7 +584,8 @@ using namespace bioemu;
 
 extern "C" size_t bioemu_apb_f32_workspace_bytes(int64_t B, int64_t mult, int64_t N, int64_t c_s, int64_t H) {
   if (B <= 0 || mult <= 0 || N <= 0 || c_s <= 0 || H <= 0) return 0;
-  return attn_f32_layout(B * mult * N, (int)c_s, B * H * N * N, true, nullptr, nullptr);
+  const int64_t ld = round_up(N, 32);
+  return attn_f32_layout(B * mult * N, (int)c_s, B * mult * c_s * ld, B * H * N * ld, true, nullptr, nullptr);
 }
 
 extern "C" int bioemu_apb_fwd_f32(const float* s, const float* z, const uint8_t* mask, const float* norm_s_w,
@@ -440,21 +612,24 @@ extern "C" int bioemu_apb_fwd_f32(const float* s, const float* z, const uint8_t*
     return set_error(BIOEMU_ERR_WORKSPACE, "apb_f32: workspace too small");
   const long long rows = B * mult * N;
   AttnF32Buffers buf;
-  attn_f32_layout(rows, (int)c_s, B * H * N * N, true, &buf, static_cast<char*>(workspace));
-  int rc = attn_f32_projections(s, norm_s_w, norm_s_b, w_qkv, q_bias, w_g, buf, rows, (int)c_s, stream);
+  const int ldb = (int)round_up(N, 32);
+  attn_f32_layout(rows, (int)c_s, B * mult * c_s * ldb, B * H * N * ldb, true, &buf, static_cast<char*>(workspace));
+  int rc = attn_f32_projections(s, norm_s_w, norm_s_b, w_qkv, q_bias, w_g, buf, rows, (int)c_s, (int)N, ldb, stream);
   if (rc) return rc;
-  rc = pair_proj_f32(z, norm_z_w, norm_z_b, w_z, buf.bias, B * N * N, N * N, (int)H, (int)c_z, stream,
+  rc = pair_proj_f32(z, norm_z_w, norm_z_b, w_z, buf.bias, B * N * N, (int)N, (int)N, ldb, (int)H, (int)c_z, stream,
                      "f32_pair_bias");
   if (rc) return rc;
   {
     KernelTimerScope timed("f32_attention", stream);
     const dim3 grid((unsigned)((N + 127) / 128), (unsigned)H, (unsigned)(B * mult));
-    if (c_s / H == 24)
-      hipLaunchKernelGGL(attn_f32_kernel<24>, grid, dim3(128), 0, stream, buf.q, buf.k, buf.v, buf.g, buf.bias, mask,
-                         buf.go, (int)N, (int)H, (int)c_s, (int)mult);
+    const int d = (int)(c_s / H);
+    const float rsq = 1.0f / std::sqrt((float)d);
+    if (d == 24)
+      hipLaunchKernelGGL(attn_f32_kernel<24>, grid, dim3(256), 0, stream, buf.q, buf.k, buf.v, buf.g, buf.bias, mask,
+                         buf.go, (int)N, ldb, (int)H, (int)c_s, (int)mult, rsq);
     else
-      hipLaunchKernelGGL(attn_f32_kernel<32>, grid, dim3(128), 0, stream, buf.q, buf.k, buf.v, buf.g, buf.bias, mask,
-                         buf.go, (int)N, (int)H, (int)c_s, (int)mult);
+      hipLaunchKernelGGL(attn_f32_kernel<32>, grid, dim3(256), 0, stream, buf.q, buf.k, buf.v, buf.g, buf.bias, mask,
+                         buf.go, (int)N, ldb, (int)H, (int)c_s, (int)mult, rsq);
   }
   rc = check_launch("f32_attention");
   if (rc) return rc;
@@ -465,7 +640,8 @@ extern "C" int bioemu_apb_fwd_f32(const float* s, const float* z, const uint8_t*
 extern "C" size_t bioemu_swa_f32_workspace_bytes(int64_t B, int64_t mult, int64_t NW, int64_t W, int64_t H,
                                                  int64_t c_s, int64_t heads) {
   if (B <= 0 || mult <= 0 || NW <= 0 || W != 32 || H <= 0 || c_s <= 0 || heads <= 0) return 0;
-  return attn_f32_layout(B * mult * NW * W, (int)c_s, B * NW * heads * W * H, true, nullptr, nullptr);
+  return attn_f32_layout(B * mult * NW * W, (int)c_s, B * mult * NW * W * c_s, B * NW * heads * W * H, true, nullptr,
+                         nullptr);
 }
 
 extern "C" int bioemu_swa_fwd_f32(const float* s, const float* z, const uint8_t* mask, const float* norm_s_w,
@@ -489,23 +665,26 @@ extern "C" int bioemu_swa_fwd_f32(const float* s, const float* z, const uint8_t*
   if (!aligned16(s) || !aligned16(z) || !aligned16(out) || !aligned16(w_qkv) || !aligned16(w_g) || !aligned16(w_o) ||
       !aligned16(workspace))
     return set_error(BIOEMU_ERR_INVALID_ARG, "swa_f32: tensors must be 16-byte aligned");
+  if (reinterpret_cast<uintptr_t>(mask) & 3)
+    return set_error(BIOEMU_ERR_INVALID_ARG, "swa_f32: mask must be 4-byte aligned (it is read 4 keys at a time)");
   if (out == s && !residual)
     return set_error(BIOEMU_ERR_INVALID_ARG, "swa_f32: out may alias s only with residual=1");
   if (workspace_bytes < bioemu_swa_f32_workspace_bytes(B, mult, NW, W, H, c_s, heads))
     return set_error(BIOEMU_ERR_WORKSPACE, "swa_f32: workspace too small");
   const long long rows = B * mult * NW * W;
   AttnF32Buffers buf;
-  attn_f32_layout(rows, (int)c_s, B * NW * heads * W * H, true, &buf, static_cast<char*>(workspace));
-  int rc = attn_f32_projections(s, norm_s_w, norm_s_b, w_qkv, q_bias, w_g, buf, rows, (int)c_s, stream);
+  attn_f32_layout(rows, (int)c_s, rows * c_s, B * NW * heads * W * H, true, &buf, static_cast<char*>(workspace));
+  int rc = attn_f32_projections(s, norm_s_w, norm_s_b, w_qkv, q_bias, w_g, buf, rows, (int)c_s, (int)(NW * W),
+                                (int)(NW * W), stream);
   if (rc) return rc;
-  rc = pair_proj_f32(z, norm_z_w, norm_z_b, w_z, buf.bias, B * NW * W * H, W * H, (int)heads, (int)c_z, stream,
-                     "f32_swa_pair_bias");
+  rc = pair_proj_f32(z, norm_z_w, norm_z_b, w_z, buf.bias, B * NW * W * H, (int)W, (int)H, (int)H, (int)heads,
+                     (int)c_z, stream, "f32_swa_pair_bias");
   if (rc) return rc;
   {
     KernelTimerScope timed("f32_swa_attention", stream);
-    hipLaunchKernelGGL(swa_attn_f32_kernel<32>, dim3((unsigned)NW, (unsigned)((heads + 3) / 4), (unsigned)(B * mult)),
-                       dim3(128), 0, stream, buf.q, buf.k, buf.v, buf.g, buf.bias, mask, buf.go, (int)NW, (int)H,
-                       (int)heads, (int)c_s, (int)mult);
+    hipLaunchKernelGGL(swa_attn_f32_kernel, dim3((unsigned)NW, (unsigned)((heads + 3) / 4), (unsigned)(B * mult)),
+                       dim3(256), 0, stream, buf.q, buf.k, buf.v, buf.g, buf.bias, mask, buf.go, (int)NW, (int)H,
+                       (int)heads, (int)c_s, (int)mult, 1.0f / std::sqrt(32.0f));
   }
   rc = check_launch("f32_swa_attention");
   if (rc) return rc;

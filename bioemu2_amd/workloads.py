@@ -116,6 +116,7 @@ class Workload:
     metric: str
     config: dict
     flops: float
+    dtype: str = "bf16"   # the arithmetic the timed kernels compute in
 
     def step(self) -> None:
         raise NotImplementedError
@@ -751,19 +752,21 @@ class SwaWorkload(Workload):
     transformer.py:96-105: initial_norm=False): NA = 6144 atoms (NW = 192 windows of W = 32, H = 128 keys),
     c_s = 128, 4 heads, c_z = 16, multiplicity M = 8, trailing 40 atoms padded."""
 
-    def __init__(self, device, nw: int = 192, mult: int = 8, seed: int = 0):
+    def __init__(self, device, nw: int = 192, mult: int = 8, seed: int = 0, fp32: bool = False):
         from .attention_pair_bias import AttentionPairBiasSlidingWindow
 
-        self.nw, self.mult = nw, mult
+        self.nw, self.mult, self.fp32 = nw, mult, fp32
         self.na = nw * 32
-        self.name = f"swa_na{self.na}_m{mult}"
-        self.metric = f"ms per sliding-window pair-bias attention at {self.na} atoms, M={mult} bf16"
+        self.dtype = "f32" if fp32 else "bf16"
+        self.name = f"swa_na{self.na}_m{mult}" + ("_f32" if fp32 else "")
+        self.metric = f"ms per sliding-window pair-bias attention at {self.na} atoms, M={mult} {self.dtype}"
         torch.manual_seed(seed)
         self.module = init_module(AttentionPairBiasSlidingWindow(128, 16, 4, initial_norm=False), seed)
         self.module = self.module.to(device).eval()
         g = torch.Generator().manual_seed(seed)
-        self.s_cpu = torch.randn(mult * nw, 32, 128, generator=g).to(torch.bfloat16)
-        self.z_cpu = torch.randn(1, nw, 32, 128, 16, generator=g).to(torch.bfloat16)
+        dt = torch.float32 if fp32 else torch.bfloat16
+        self.s_cpu = torch.randn(mult * nw, 32, 128, generator=g).to(dt)
+        self.z_cpu = torch.randn(1, nw, 32, 128, 16, generator=g).to(dt)
         mask = torch.ones(1, self.na, dtype=torch.bool)
         mask[:, -40:] = False
         self.mask_cpu = mask.view(nw, 32)
@@ -771,8 +774,10 @@ class SwaWorkload(Workload):
         self.z = self.z_cpu.to(device)
         self.mask = _ops.mask_u8(self.mask_cpu.to(device))
         self.out = torch.empty_like(self.s)
-        self.ws = _ops.workspace(_ops.swa_workspace_bytes(1, mult, nw, 32, 128, 128, 4), device)
-        self.params = self.module.prepared_params()
+        ws_bytes = (_ops.swa_f32_workspace_bytes if fp32 else _ops.swa_workspace_bytes)(1, mult, nw, 32, 128, 128, 4)
+        self.ws = _ops.workspace(ws_bytes, device)
+        self.params = self.module.prepared_params_f32() if fp32 else self.module.prepared_params()
+        self.launch = _ops.launch_swa_f32 if fp32 else _ops.launch_swa
         self.config = {"workload": self.name, "atoms": self.na, "windows": nw, "window_queries": 32,
                        "window_keys": 128, "c_s": 128, "c_z": 16, "heads": 4, "multiplicity": mult,
                        "initial_norm": False, "padded_atoms": 40}
@@ -780,7 +785,7 @@ class SwaWorkload(Workload):
         self.flops = 2.0 * rows * 128 * 128 * 5 + 2.0 * mult * nw * 4 * 32 * 128 * 32 * 2 + 2.0 * nw * 32 * 128 * 16 * 4
 
     def step(self) -> None:
-        _ops.launch_swa(self.s, self.z, self.mask, *self.params, self.out, 4, multiplicity=self.mult, ws=self.ws)
+        self.launch(self.s, self.z, self.mask, *self.params, self.out, 4, multiplicity=self.mult, ws=self.ws)
 
     def cpu_sample(self, oracle):
         s = self.s_cpu[: self.nw].float()   # copy 0 of M (copies are independent)
@@ -794,6 +799,16 @@ class SwaWorkload(Workload):
 
     def kernel_work(self, kernel: str) -> tuple[str, float]:
         rows = self.mult * self.na
+        if self.fp32:
+            if kernel == "f32_proj_qkvg":
+                return ("mfma_f32", 4 * 2.0 * rows * 128 * 128)
+            if kernel == "f32_proj_o":
+                return ("mfma_f32", 2.0 * rows * 128 * 128)
+            if kernel == "f32_swa_pair_bias":   # reads z, writes the 4-head bias
+                return ("hbm", float(self.nw * 32 * 128 * (16 + 4) * 4))
+            if kernel == "f32_swa_attention":   # QK^T and PV over the 128-key window, every copy and head
+                return ("mfma_f32", 2.0 * 2 * rows * 128 * 128)
+            raise KeyError(kernel)
         tok = rows * 128 * 2
         bias = self.nw * 4 * 32 * 128 * 2
         if kernel == "swa_attn":
@@ -812,18 +827,21 @@ class ApbWorkload(Workload):
     """Config 2: pair-bias attention, s [8,512,384] bf16, z [8,512,512,128], 16 heads of 24, last 51 keys
     masked (initial_norm=True); with ``mult`` > 1 the denoiser form: B=1, M copies sharing one z."""
 
-    def __init__(self, device, n: int = 512, B: int = 8, mult: int = 1, initial_norm: bool = True, seed: int = 0):
+    def __init__(self, device, n: int = 512, B: int = 8, mult: int = 1, initial_norm: bool = True, seed: int = 0,
+                 fp32: bool = False):
         from .attention_pair_bias import AttentionPairBias
 
-        self.n, self.B, self.mult = n, B, mult
-        self.name = f"apb_b{B}_m{mult}_n{n}" + ("" if initial_norm else "_nonorm")
-        self.metric = f"ms per pair-bias attention at B={B}, M={mult}, N={n} bf16"
+        self.n, self.B, self.mult, self.fp32 = n, B, mult, fp32
+        self.dtype = "f32" if fp32 else "bf16"
+        self.name = f"apb_b{B}_m{mult}_n{n}" + ("" if initial_norm else "_nonorm") + ("_f32" if fp32 else "")
+        self.metric = f"ms per pair-bias attention at B={B}, M={mult}, N={n} {self.dtype}"
         torch.manual_seed(seed)
         self.module = init_module(AttentionPairBias(384, 128, 16, initial_norm=initial_norm), seed).to(device)
         self.module = self.module.eval()
         g = torch.Generator().manual_seed(seed)
-        self.s_cpu = torch.randn(B * mult, n, 384, generator=g).to(torch.bfloat16)
-        self.z_cpu = torch.randn(B, n, n, 128, generator=g).to(torch.bfloat16)
+        dt = torch.float32 if fp32 else torch.bfloat16
+        self.s_cpu = torch.randn(B * mult, n, 384, generator=g).to(dt)
+        self.z_cpu = torch.randn(B, n, n, 128, generator=g).to(dt)
         self.mask_cpu = torch.ones(B, n, dtype=torch.bool)
         self.mask_cpu[:, n - n // 10:] = False
         self.initial_norm = initial_norm
@@ -831,8 +849,10 @@ class ApbWorkload(Workload):
         self.z = self.z_cpu.to(device)
         self.mask = _ops.mask_u8(self.mask_cpu.to(device))
         self.out = torch.empty_like(self.s)
-        self.ws = _ops.workspace(_ops.apb_workspace_bytes(B, mult, n, 384, 16), device)
-        self.params = self.module.prepared_params()
+        ws_bytes = (_ops.apb_f32_workspace_bytes if fp32 else _ops.apb_workspace_bytes)(B, mult, n, 384, 16)
+        self.ws = _ops.workspace(ws_bytes, device)
+        self.params = self.module.prepared_params_f32() if fp32 else self.module.prepared_params()
+        self.launch = _ops.launch_apb_f32 if fp32 else _ops.launch_apb
         self.config = {"workload": self.name, "batch": B, "multiplicity": mult, "N": n, "c_s": 384, "c_z": 128,
                        "heads": 16, "head_dim": 24, "masked_keys": n // 10, "initial_norm": initial_norm}
         rows = B * mult * n
@@ -840,7 +860,7 @@ class ApbWorkload(Workload):
                       + 2.0 * 2 * B * mult * n * n * 384)
 
     def step(self) -> None:
-        _ops.launch_apb(self.s, self.z, self.mask, *self.params, self.out, 16, self.mult, ws=self.ws)
+        self.launch(self.s, self.z, self.mask, *self.params, self.out, 16, self.mult, ws=self.ws)
 
     def cpu_sample(self, oracle):
         s = self.s_cpu[: self.mult].float()   # batch element 0 with its M copies
@@ -855,6 +875,19 @@ class ApbWorkload(Workload):
 
     def kernel_work(self, kernel: str) -> tuple[str, float]:
         n, B, M = self.n, self.B, self.mult
+        if self.fp32:
+            rows = B * M * n
+            if kernel == "f32_proj_qkvg":
+                return ("mfma_f32", 4 * 2.0 * rows * 384 * 384)
+            if kernel == "f32_proj_o":
+                return ("mfma_f32", 2.0 * rows * 384 * 384)
+            if kernel == "f32_layernorm":
+                return ("hbm", float(2 * rows * 384 * 4))
+            if kernel == "f32_pair_bias":   # reads z, writes the 16-head bias
+                return ("hbm", float(B * n * n * (128 + 16) * 4))
+            if kernel == "f32_attention":   # QK^T and PV: 4 N^2 c_s per copy
+                return ("mfma_f32", 4.0 * B * M * n * n * 384)
+            raise KeyError(kernel)
         np_ = -(-n // 32) * 32
         tok = B * M * np_ * 384 * 2
         if kernel == "apb_pair_bias":
@@ -906,17 +939,19 @@ class DistogramWorkload(Workload):
 class PairCondWorkload(Workload):
     """The denoiser's PairwiseConditioning (token_z = rel = a_z = 128, 2 transitions of hidden 256) at N=768."""
 
-    def __init__(self, device, n: int = 768, seed: int = 0):
+    def __init__(self, device, n: int = 768, seed: int = 0, fp32: bool = False):
         from .glue import PairwiseConditioning
 
-        self.n = n
-        self.name = f"pair_cond_n{n}"
-        self.metric = f"ms per pairwise conditioning at N={n} bf16"
+        self.n, self.fp32 = n, fp32
+        self.dtype = "f32" if fp32 else "bf16"
+        self.name = f"pair_cond_n{n}" + ("_f32" if fp32 else "")
+        self.metric = f"ms per pairwise conditioning at N={n} {self.dtype}"
         torch.manual_seed(seed)
         self.module = init_module(PairwiseConditioning(128, 128), seed).to(device)
         g = torch.Generator().manual_seed(seed)
-        self.z_cpu = torch.randn(1, n, n, 128, generator=g).to(torch.bfloat16)
-        self.rel_cpu = torch.randn(1, n, n, 128, generator=g).to(torch.bfloat16)
+        dt = torch.float32 if fp32 else torch.bfloat16
+        self.z_cpu = torch.randn(1, n, n, 128, generator=g).to(dt)
+        self.rel_cpu = torch.randn(1, n, n, 128, generator=g).to(dt)
         self.z = self.z_cpu.to(device)
         self.rel = self.rel_cpu.to(device)
         self.config = {"workload": self.name, "N": n, "token_z": 128, "rel_pos": 128, "a_z": 128,
@@ -936,6 +971,18 @@ class PairCondWorkload(Workload):
 
     def kernel_work(self, kernel: str) -> tuple[str, float]:
         P = self.n * self.n
+        if self.fp32:
+            if kernel == "f32_pair_cond_layernorm":   # reads both inputs, writes the normalised concatenation
+                return ("hbm", float(P * 256 * 4 * 2))
+            if kernel == "f32_layernorm":
+                return ("hbm", float(P * 128 * 4 * 2))
+            if kernel == "f32_pair_cond_proj":
+                return ("mfma_f32", 2.0 * P * 256 * 128)
+            if kernel == "f32_transition_swiglu":   # fc1 and fc2, 128 -> 256 each
+                return ("mfma_f32", 2.0 * 2 * P * 128 * 256)
+            if kernel == "f32_transition_out":
+                return ("mfma_f32", 2.0 * P * 256 * 128)
+            raise KeyError(kernel)
         if kernel == "pair_cond_proj":
             return ("hbm", float(P * (256 + 128) * 2))
         if kernel == "transition_pair":
@@ -958,6 +1005,13 @@ def make(op: str, device, n: int | None = None) -> Workload:
         return ApbWorkload(device, n or 512, initial_norm=False)
     if op == "apb_denoiser":
         return ApbWorkload(device, n or 768, B=1, mult=8, initial_norm=False)
+    # the denoiser's ops on the fp32 path (the reference runs its denoiser with autocast off)
+    if op == "apb_denoiser_f32":
+        return ApbWorkload(device, n or 768, B=1, mult=8, initial_norm=False, fp32=True)
+    if op == "swa_f32":
+        return SwaWorkload(device, fp32=True)
+    if op == "pair_cond_f32":
+        return PairCondWorkload(device, n or 768, fp32=True)
     if op == "distogram":
         return DistogramWorkload(device, n or 768)
     if op == "pair_cond":
