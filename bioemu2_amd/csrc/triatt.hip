@@ -581,7 +581,7 @@ void triatt_flash_kernel(
     bf16x8 gob[2 * H];
     {
       const bf16* grow = buf.g + (frow + q0 + 32 * t + n) * C + 16 * hh;
-      const bf16* orow = qio + (unsigned)qrow[t] * C + 16 * hh;
+      const bf16* orow = qio + (unsigned)(q0 + 32 * t + n) * C + 16 * hh;   // qrow[t] of an active wave
 #pragma unroll
       for (int hd = 0; hd < H; ++hd) {
         const bf16x8 g0 = load8(grow + hd * DH), g1 = load8(grow + hd * DH + 8);
