@@ -123,11 +123,30 @@ __global__ __launch_bounds__(64 * kWaves) void trimul_proj_in_kernel(
     for (int blk = 0; blk < 8; ++blk) {   // a: blk 0..3, b: blk 4..7 (32 channels each)
       const f32x16 pa = proj_block_cm(xf, wl, blk * 32, rho, h);
       const f32x16 ga = proj_block_cm(xf, wl, 2 * D + blk * 32, rho, h);
-      float v[16];
+      // Lane (rho, h) holds columns 16h .. 16h + 15 of channel ch as two
+      // 8-column chunks.  Lanes rho and rho ^ 16 swap their second chunks, so
+      // that each of the two stores writes whole 64-byte column runs: the
+      // first those of channels with rho < 16 (4 lanes each), the second
+      // those of the other 16 channels.
+      bf16x8 first, second, recv;
 #pragma unroll
-      for (int u = 0; u < 16; ++u) v[u] = pa[u] * sigmoidf_fast(ga[u]);
+      for (int u = 0; u < 8; ++u) {
+        first[u] = f2bf(pa[u] * sigmoidf_fast(ga[u]));
+        second[u] = f2bf(pa[8 + u] * sigmoidf_fast(ga[8 + u]));
+      }
+      {
+        const u32x4 sw = __builtin_bit_cast(u32x4, second);
+        u32x4 rw;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) rw[d] = (unsigned)__shfl_xor((int)sw[d], 16);
+        recv = __builtin_bit_cast(bf16x8, rw);
+      }
       const int which = blk >> 2, ch = (blk & 3) * 32 + rho;
-      store16(ab + ((size_t)(which * B + b) * D + ch) * plane + (size_t)i * Np + k0 + 16 * h, v);
+      bf16* own = ab + ((size_t)(which * B + b) * D + ch) * plane + (size_t)i * Np + k0 + 16 * h;
+      bf16* partner = own + (rho < 16 ? 16 : -16) * (long long)plane + 8;   // channel ch ^ 16, columns + 8
+      const bool low = rho < 16;   // per-lane selects: two store instructions for the whole wave
+      store8(low ? own : partner, low ? first : recv);
+      store8(low ? partner : own, low ? recv : first);
     }
     if (tn < ntiles) prepare();
   }
