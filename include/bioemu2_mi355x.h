@@ -11,7 +11,8 @@
  *   LayerNorm    gamma/beta fp32
  *   Linear       weights bf16, row-major [out, in] (torch nn.Linear layout)
  * Arithmetic: bf16 MFMA operands with fp32 accumulation; LayerNorm statistics,
- * softmax and gates in fp32.
+ * softmax and gates in fp32.  The *_f32 entry points (end of this file) take
+ * fp32 activations and weights and compute in fp32 throughout.
  *
  * Scratch memory is caller-owned: each op with intermediates has a
  * *_workspace_bytes() query and takes (workspace, workspace_bytes).

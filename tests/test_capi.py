@@ -81,3 +81,13 @@ def test_invalid_arguments_rejected_without_gpu():
     assert b"null" in lib.bioemu_last_error()
     rc = lib.bioemu_trimul_fwd(*([None] * 12), None, 0, 1, 16, 64, 1, 0, None)
     assert rc == -2
+
+
+def test_integration_doc_argtypes_match_binding():
+    """Every `lib.<entry>.argtypes = ...` line in INTEGRATION.md declares the binding's signature."""
+    text = (ROOT / "INTEGRATION.md").read_text().replace("\\\n", " ")
+    found = re.findall(r"lib\.(bioemu_\w+)\.argtypes\s*=\s*([^\n]+)", text)
+    assert found
+    for name, expr in found:
+        got = eval(expr, {"ctypes": ctypes})   # the document's own expression, ctypes only
+        assert got == _lib.SIGNATURES[name][1], (name, got)
