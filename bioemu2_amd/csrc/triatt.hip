@@ -292,15 +292,33 @@ void triatt_flash_kernel(
   // 32-channel slot holds that head's normalised output o / l (bf16) until
   // the epilogue (each lane rewrites only the slot it read itself).
   bf16* qio = buf.q + frow * C;                                             // [Np][C]
+  // q fragments of the head being processed; head 0's are requested first
+  // thing, each later head's during the previous head's last key block.
+  bf16x8 qf[kFlashTiles][2];
+  auto qload = [&](int hq) {
+#pragma unroll
+    for (int t = 0; t < kFlashTiles; ++t) {
+      qf[t][0] = load8(qio + (unsigned)qrow[t] * C + hq * DH + 8 * hh);
+      qf[t][1] = load8(qio + (unsigned)qrow[t] * C + hq * DH + 16 + 8 * hh);
+    }
+  };
+  qload(0);
   // Key-mask row (additive: 0 valid, -1e30 masked, -inf beyond N).  A row
   // whose keys are all masked ("dead") attends uniformly to its N keys
   // (every logit replaced by the same value): o / l is the mean of v.
+  // One pass over the mask row also flags the 64-key blocks holding a valid
+  // key (wave w covers keys [256 j + 64 w, +64): block 4 j + w; Np is a
+  // multiple of 64, so the trip count is the same for the 64 lanes).
+  __shared__ uint8_t kflag[kMaxKeyBlocks];
   int any_valid = 0;
-  for (int t = tid; t < N; t += kFlashThreads) any_valid |= buf.mask[frow + t];
+  for (int t = tid; t < Np; t += kFlashThreads) {
+    const bool valid = t < N && buf.mask[frow + t] != 0;
+    any_valid |= valid;
+    kadd[t] = f2bf(valid ? 0.f : t >= N ? -INFINITY : -1e30f);
+    const bool any_ok = __any(valid);
+    if (lane == 0) kflag[t >> 6] = any_ok;
+  }
   const bool dead = __syncthreads_or(any_valid) == 0;
-  for (int t = tid; t < Np; t += kFlashThreads)
-    kadd[t] = f2bf(t >= N ? -INFINITY : buf.mask[frow + t] ? 0.f : -1e30f);
-  __syncthreads();
 
   // Operand fetches through buffer resources: per-lane byte offsets are fixed,
   // the (head, key block) part is a wave-uniform scalar offset.
@@ -351,18 +369,29 @@ void triatt_flash_kernel(
     // Uniform weights over the N keys: o / l = mean of v (v is exactly 0 for
     // keys in [N, Np)), the same for every query of the row.
     float* vmean = reinterpret_cast<float*>(smem);
-    for (int c = wave; c < C; c += kFlashThreads / 64) {
-      const bf16* vr = vg + (size_t)c * Np;
-      float acc = 0.f;
-      for (int k = lane * 8; k < Np; k += 512) {
-        float v8[8];
-        unpack8(load8(vr + k), v8);
+    constexpr int kWaves = kFlashThreads / 64, kChan = 8;   // channels whose loads are in flight together
+    for (int c0 = wave; c0 < C; c0 += kChan * kWaves) {
+      float acc[kChan];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) acc += v8[u];
+      for (int j = 0; j < kChan; ++j) acc[j] = 0.f;
+      for (int k = lane * 8; k < Np; k += 512) {
+        bf16x8 x[kChan];
+#pragma unroll
+        for (int j = 0; j < kChan; ++j) x[j] = load8(vg + (size_t)(c0 + kWaves * j) * Np + k);
+#pragma unroll
+        for (int j = 0; j < kChan; ++j) {
+          float v8[8];
+          unpack8(x[j], v8);
+#pragma unroll
+          for (int u = 0; u < 8; ++u) acc[j] += v8[u];
+        }
       }
 #pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off);
-      if (lane == 0) vmean[c] = acc * (1.0f / N);
+      for (int j = 0; j < kChan; ++j) {
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) acc[j] += __shfl_xor(acc[j], off);
+        if (lane == 0) vmean[c0 + kWaves * j] = acc[j] * (1.0f / N);
+      }
     }
     __syncthreads();
 #pragma unroll 1
@@ -380,15 +409,8 @@ void triatt_flash_kernel(
   // all masked adds exact zeros (its logits are -1e30 or -inf below any
   // unmasked logit), so skipping it leaves o and l bit-identical.
   __shared__ short act[kMaxKeyBlocks];
-  __shared__ uint8_t kflag[kMaxKeyBlocks];
   __shared__ int nact_s;
   const int nk = Np / 64;
-  for (int kb = wave; kb < nk; kb += kFlashThreads / 64) {
-    const bool ok = __builtin_bit_cast(uint16_t, kadd[64 * kb + lane]) == 0;
-    const bool any_ok = __any(ok);
-    if (lane == 0) kflag[kb] = any_ok;
-  }
-  __syncthreads();
   if (wave == 0) {
     int base = 0;
     for (int c0 = 0; c0 < nk; c0 += 64) {
@@ -412,12 +434,6 @@ void triatt_flash_kernel(
   int st = 0;
 #pragma unroll 1
   for (int hd = 0; hd < H; ++hd) {
-    bf16x8 qf[kFlashTiles][2];
-#pragma unroll
-    for (int t = 0; t < kFlashTiles; ++t) {
-      qf[t][0] = load8(qio + (unsigned)qrow[t] * C + hd * DH + 8 * hh);
-      qf[t][1] = load8(qio + (unsigned)qrow[t] * C + hd * DH + 16 + 8 * hh);
-    }
     f32x16 o[kFlashTiles];
     float m[kFlashTiles], l[kFlashTiles];
     bool m_set[kFlashTiles];   // m is the (bf16-rounded) max of some unmasked logit
@@ -484,6 +500,7 @@ void triatt_flash_kernel(
           s[t][1] = mfma32(km1, qs, s[t][1]);
           bload(hn, kn, t, bias[t]);
         }
+        if (ib + 1 == nact && hd + 1 < H) qload(hd + 1);
 #pragma unroll
         for (int t = 0; t < kFlashTiles; ++t) {
           f32x16& s0 = s[t][0];
@@ -560,6 +577,15 @@ void triatt_flash_kernel(
   }
   if (!active) return;
 
+  // Out-projection weights (A operand: row cb*32 + perm32(n), k-step s2),
+  // fetched once for both tiles, together with the first tile's gate inputs.
+  bf16x8 wf[4][8];
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb) {
+    const bf16* wrow = wo + (size_t)(cb * 32 + perm32(n)) * C + 16 * hh;
+#pragma unroll
+    for (int s2 = 0; s2 < 8; ++s2) wf[cb][s2] = load8(wrow + 32 * (s2 >> 1) + 8 * (s2 & 1));
+  }
 #pragma unroll 1
   for (int t = 0; t < kFlashTiles; ++t) {
     // The residual (and its tail) of each output block is requested one block
@@ -602,9 +628,8 @@ void triatt_flash_kernel(
       __builtin_amdgcn_sched_barrier(0);
       if (residual && cb + 1 < 4) zload(cb + 1);
       f32x16 acc = zero16();
-      const bf16* wrow = wo + (size_t)(cb * 32 + perm32(n)) * C + 16 * hh;
 #pragma unroll
-      for (int s2 = 0; s2 < 8; ++s2) acc = mfma32(load8(wrow + 32 * (s2 >> 1) + 8 * (s2 & 1)), gob[s2], acc);
+      for (int s2 = 0; s2 < 8; ++s2) acc = mfma32(wf[cb][s2], gob[s2], acc);
       if (store) {
         const size_t off = zpair * C + cb * 32 + 16 * hh;
         float v[16];
