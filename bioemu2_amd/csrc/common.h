@@ -145,10 +145,9 @@ __device__ __forceinline__ void tail_decode16(bf16x8 r0, bf16x8 r1, u32x4 tb, fl
   }
 }
 
-// Sixteen fp32 values -> bf16 halves (stored at dst, dst + 8) and tail bytes.
-__device__ __forceinline__ void tail_store16(bf16* dst, int8_t* tdst, const float* v) {
-  bf16x8 a, b;
-  u32x4 tb = {0u, 0u, 0u, 0u};
+// Sixteen fp32 values -> bf16 halves a (values 0-7), b (8-15) and their tail bytes.
+__device__ __forceinline__ void tail_encode16(const float* v, bf16x8& a, bf16x8& b, u32x4& tb) {
+  tb = u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
   for (int u = 0; u < 16; ++u) {
     int t;
@@ -156,6 +155,13 @@ __device__ __forceinline__ void tail_store16(bf16* dst, int8_t* tdst, const floa
     if (u < 8) a[u] = hi; else b[u - 8] = hi;
     tb[u >> 2] |= ((uint32_t)t & 0xffu) << (8 * (u & 3));
   }
+}
+
+// Sixteen fp32 values -> bf16 halves (stored at dst, dst + 8) and tail bytes.
+__device__ __forceinline__ void tail_store16(bf16* dst, int8_t* tdst, const float* v) {
+  bf16x8 a, b;
+  u32x4 tb;
+  tail_encode16(v, a, b, tb);
   *reinterpret_cast<bf16x8*>(dst) = a;
   *reinterpret_cast<bf16x8*>(dst + 8) = b;
   *reinterpret_cast<u32x4*>(tdst) = tb;

@@ -216,11 +216,19 @@ __device__ __forceinline__ void normalize_half_row(const float* v, bf16x8 out[8]
 // registers against the folded weights, which sit in LDS with the folded
 // biases.
 //
-// Output lanes: LDS row 32 cb + m of each folded weight half holds weight row
-// 64 (m >> 4) + 16 cb + (m & 15), so that lane (rho, h) of output block cb
-// holds channels 64 h + 16 cb + u (u < 16) of its pair: over the four blocks a
-// lane produces exactly the 64 channels of its own x half-row, and the
-// residual comes from registers.
+// Channel interleave: the two lanes (rho, 0) and (rho, 1) of a pair hold
+// alternate 8-channel chunks, lane h chunk s = channels 16 s + 8 h + (0..7).
+// Each 16-byte load or store instruction then covers 32 bytes of one cache
+// line per pair (32 lines per instruction instead of 64 for contiguous half
+// rows), and chunk s is already the MFMA B operand of k-step s once the
+// weight columns are staged in the matching order (LDS chunk 8 h + s <-
+// weight chunk 2 s + h).  Output lanes: LDS row 32 cb + m of each folded
+// weight half holds weight row 32 cb + 16 ((m & 15) >> 3) + 8 (m >> 4) +
+// (m & 7), so that lane (rho, h) of output block cb holds channels
+// 32 cb + 8 h + u and 32 cb + 16 + 8 h + u (u < 8): x chunks 2 cb and
+// 2 cb + 1 of its own registers, which supply the residual.  Tail bytes
+// (16 per load or store, contiguous channels 32 cb + 16 h + 0..15) are
+// exchanged between the two lanes of a pair.
 //
 // Software pipeline: tile t + stride's x and o loads are issued before tile
 // t's stores and consumed after them; vector-memory counters retire in issue
@@ -232,11 +240,31 @@ constexpr int kOutTile = D * 32 + 32;   // per-wave o buffer, bf16 elements
 constexpr int kOutSmem = 2 * D * kLdw * 2 + 2 * D * 4 + kOutWaves * kOutTile * 2;
 
 // Element offset of (channel c, column j) in a wave's o buffer: 64-byte
-// channel rows, the upper 64 channels 64 bytes further on, so that the two
-// half-waves' reads (channels c and c + 64 of the same 32 columns) use
-// different LDS banks; the 16-byte writes of one instruction cover 1 KB
-// contiguously.
-__device__ __forceinline__ int obuf_off(int c, int j) { return c * 32 + j + ((c >> 6) << 5); }
+// channel rows in eight 1 KB blocks, block q holding channels
+// 32 (q & 3) + 8 (q >> 2) + {0..7, 16..23}, and blocks 4..7 (channel bit 3
+// set) 64 bytes further on, so that the two half-waves' reads (channels c and
+// c + 8 of the same 32 columns) use different LDS banks; each block is what
+// one 16-byte copy instruction writes.
+__device__ __forceinline__ int obuf_off(int c, int j) {
+  const int q = 4 * ((c >> 3) & 1) + (c >> 5), slot = 8 * ((c >> 4) & 1) + (c & 7);
+  return q * 512 + slot * 32 + j + ((q >> 2) << 5);
+}
+
+// Tail words of 16 channels between the two lanes of a pair: lane h = 0 keeps
+// words 0-1 and takes the partner's 0-1 as 2-3; lane h = 1 takes the
+// partner's 2-3 as 0-1 and keeps 2-3.  The same exchange turns loaded bytes
+// (contiguous channels 32 cb + 16 h + 0..15) into the lane's interleaved
+// order and the lane's encoded bytes back into contiguous ones.
+__device__ __forceinline__ u32x4 exchange_tail_halves(u32x4 d, int h) {
+  const int s0 = (int)(h ? d[0] : d[2]), s1 = (int)(h ? d[1] : d[3]);
+  const unsigned r0 = (unsigned)__shfl_xor(s0, 32), r1 = (unsigned)__shfl_xor(s1, 32);
+  u32x4 o;
+  o[0] = h ? r0 : d[0];
+  o[1] = h ? r1 : d[1];
+  o[2] = h ? d[2] : r0;
+  o[3] = h ? d[3] : r1;
+  return o;
+}
 
 // Lanes of pair slots past N store into `discard` (a dead workspace region,
 // 16 KB) instead of skipping the store: a conditional store would hide the
@@ -255,10 +283,15 @@ __global__ __launch_bounds__(kOutThreads) void trimul_out_kernel(
   for (int q = threadIdx.x; q < 2 * D * (D / 8); q += blockDim.x) {
     const int r = q >> 4, part = q & 15;
     const int half = r / D, cb = (r % D) >> 5, m = r & 31;
-    const int src = half * D + 64 * (m >> 4) + 16 * cb + (m & 15);
-    store8(wl + r * kLdw + part * 8, load8(wfold + (size_t)src * D + part * 8));
+    const int src = half * D + 32 * cb + 16 * ((m & 15) >> 3) + 8 * (m >> 4) + (m & 7);
+    const int src_part = 2 * (part & 7) + (part >> 3);
+    store8(wl + r * kLdw + part * 8, load8(wfold + (size_t)src * D + src_part * 8));
   }
-  for (int t = threadIdx.x; t < 2 * D; t += blockDim.x) cl[t] = cfold[t];
+  // cl[half D + 64 h + 16 cb + u]: bias of the channel lane h holds in register u of block cb
+  for (int t = threadIdx.x; t < 2 * D; t += blockDim.x) {
+    const int e = t % D, h = e >> 6, cb = (e >> 4) & 3, u = e & 15;
+    cl[t] = cfold[t - e + 32 * cb + 16 * (u >> 3) + 8 * h + (u & 7)];
+  }
   __syncthreads();
 
   const int lane = threadIdx.x & 63, wave = wave_id();
@@ -269,11 +302,11 @@ __global__ __launch_bounds__(kOutThreads) void trimul_out_kernel(
   const size_t plane = (size_t)Np * Np;
   bf16* ob = obuf + wave * kOutTile;
 
-  // Next tile's raw inputs.  o channels 16 q + (lane >> 2), columns
-  // j0 + 8 (lane & 3) .. + 7 go straight from global memory into the wave's
-  // o buffer (buffer loads that write LDS: no registers; instruction q writes
-  // 1 KB contiguously, lane l at obuf_off(16 q + (l >> 2), 8 (l & 3))); this
-  // lane's x half-row (and its tail bytes) go to registers.  Columns of the
+  // Next tile's raw inputs.  o channel 32 (q & 3) + 8 (q >> 2) + 16 (s >> 3) +
+  // (s & 7), s = lane >> 2, columns j0 + 8 (lane & 3) .. + 7 go straight from
+  // global memory into the wave's o buffer (buffer loads that write LDS: no
+  // registers; instruction q writes block q, 1 KB contiguously); this lane's
+  // x chunks (and the tail bytes) go to registers.  Columns of the
   // last tile of a row may reach past N but stay below Np (o is Np wide).
   // The o copies are issued first, so the wait for them in prepare() counts
   // the x / tail loads and the current tile's stores issued after them.
@@ -284,23 +317,24 @@ __global__ __launch_bounds__(kOutThreads) void trimul_out_kernel(
     const int i = ti.row, b = ti.b, j0 = ti.col * 32;
     const __amdgpu_buffer_rsrc_t ors =
         buffer_rsrc(o + (size_t)b * D * plane + (size_t)i * Np + j0, (unsigned)(((D - 1) * plane + 32) * 2));
-    const unsigned ovoff = ((unsigned)(lane >> 2) * (unsigned)plane + 8u * (lane & 3)) * 2u;
+    const int slot = lane >> 2;
+    const unsigned ovoff = ((unsigned)(16 * (slot >> 3) + (slot & 7)) * (unsigned)plane + 8u * (lane & 3)) * 2u;
 #pragma unroll
     for (int q = 0; q < 8; ++q)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           ors, (__attribute__((address_space(3))) void*)(ob + 512 * q + (q >= 4 ? 32 : 0)), 16, ovoff,
-          (unsigned)(16 * q) * (unsigned)plane * 2u, 0, 0);
+          (unsigned)(32 * (q & 3) + 8 * (q >> 2)) * (unsigned)plane * 2u, 0, 0);
     // Nothing may be scheduled above the copies: the wait in prepare() counts
     // every vector-memory operation issued after them.
     __builtin_amdgcn_sched_barrier(0);
     const int jj = j0 + perm32(rho);
     const size_t pair = ((size_t)b * N + i) * N + (jj < N ? jj : 0);
-    const bf16* xr = x + pair * D + 64 * h;
+    const bf16* xr = x + pair * D + 8 * h;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) xraw[s] = load8(xr + 8 * s);
+    for (int s = 0; s < 8; ++s) xraw[s] = load8(xr + 16 * s);
     if (kTail) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) traw[q] = load_tail16(tail + pair * D + 64 * h + 16 * q);
+      for (int q = 0; q < 4; ++q) traw[q] = load_tail16(tail + pair * D + 32 * q + 16 * h);
     }
   };
   // Vector-memory operations issued after a tile's o copies and before its
@@ -309,7 +343,7 @@ __global__ __launch_bounds__(kOutThreads) void trimul_out_kernel(
   // per output block.
   constexpr int kAfterLoads = 8 + (kTail ? 4 : 0);
   constexpr int kAfterOCopies = kAfterLoads + 4 * (kTail ? 3 : 2);
-  // Current tile's operands: normalised o and x rows, the raw x half-row and its tail.
+  // Current tile's operands: normalised o and x rows, the raw x chunks and their tails.
   bf16x8 of[8], xf[8], xres[8];
   u32x4 tres[4];
   auto prepare = [&](bool first) {
@@ -322,7 +356,7 @@ __global__ __launch_bounds__(kOutThreads) void trimul_out_kernel(
     float v[64];
     const int p = perm32(rho);
 #pragma unroll
-    for (int c = 0; c < 64; ++c) v[c] = bf2f(ob[obuf_off(64 * h + c, p)]);
+    for (int c = 0; c < 64; ++c) v[c] = bf2f(ob[obuf_off(16 * (c >> 3) + 8 * h + (c & 7), p)]);
     normalize_half_row(v, of);
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
@@ -331,7 +365,7 @@ __global__ __launch_bounds__(kOutThreads) void trimul_out_kernel(
     }
     if (kTail) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) tres[q] = traw[q];
+      for (int q = 0; q < 4; ++q) tres[q] = exchange_tail_halves(traw[q], h);
     }
     normalize_half_row(v, xf);
   };
@@ -362,8 +396,14 @@ __global__ __launch_bounds__(kOutThreads) void trimul_out_kernel(
 #pragma unroll
         for (int u = 0; u < 16; ++u) r[u] += xv[u];
         int8_t* tdiscard = reinterpret_cast<int8_t*>(discard + 64 * D);
-        tail_store16(valid ? out + pair * D + e0 : discard + lane * D + e0,
-                     valid ? tail + pair * D + e0 : tdiscard + lane * D + e0, r);
+        bf16x8 lo, hi;
+        u32x4 tb;
+        tail_encode16(r, lo, hi, tb);
+        bf16* dst = valid ? out + pair * D : discard + lane * D;
+        store8(dst + 32 * cb + 8 * h, lo);
+        store8(dst + 32 * cb + 16 + 8 * h, hi);
+        int8_t* tdst = valid ? tail + pair * D : tdiscard + lane * D;
+        *reinterpret_cast<u32x4*>(tdst + 32 * cb + 16 * h) = exchange_tail_halves(tb, h);
         continue;
       }
       if (residual) {
@@ -373,7 +413,15 @@ __global__ __launch_bounds__(kOutThreads) void trimul_out_kernel(
           r[8 + u] += bf2f(xres[2 * cb + 1][u]);
         }
       }
-      store16(valid ? out + pair * D + e0 : discard + lane * D + e0, r);
+      bf16x8 lo, hi;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        lo[u] = f2bf(r[u]);
+        hi[u] = f2bf(r[8 + u]);
+      }
+      bf16* dst = valid ? out + pair * D : discard + lane * D;
+      store8(dst + 32 * cb + 8 * h, lo);
+      store8(dst + 32 * cb + 16 + 8 * h, hi);
     }
     if (tn < ntiles) prepare(false);
   }
