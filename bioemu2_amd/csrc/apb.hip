@@ -55,9 +55,9 @@ __global__ __launch_bounds__(kBiasThreads) void pair_bias_kernel(const bf16* __r
     const TileIdx ti = split_tile(tt, tiles_per_row, Np);
     const int kk = ti.col * 32 + perm32(rho);
     const bool valid = ti.row < N && kk < N;
-    const bf16* row = z + (((size_t)ti.b * N + (valid ? ti.row : 0)) * N + (valid ? kk : 0)) * CZ + 64 * h;
+    const bf16* row = z + (((size_t)ti.b * N + (valid ? ti.row : 0)) * N + (valid ? kk : 0)) * CZ + 8 * h;
 #pragma unroll
-    for (int s8 = 0; s8 < 8; ++s8) raw[s8] = load8(row + 8 * s8);
+    for (int s8 = 0; s8 < 8; ++s8) raw[s8] = load8(row + 16 * s8);
   };
   bf16x8 x[8], xb;
   auto prepare = [&](unsigned tt) {

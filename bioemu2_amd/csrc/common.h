@@ -169,4 +169,23 @@ __device__ __forceinline__ void tail_store16(bf16* dst, int8_t* tdst, const floa
 
 __device__ __forceinline__ u32x4 load_tail16(const int8_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 
+// Pair-interleaved channel layout (the two lanes l and l ^ 32 of a pair slot
+// hold alternate 8-channel chunks, lane h chunk s = channels 16 s + 8 h + 0..7):
+// tail words of 16 channels exchanged between the two lanes.  Lane h = 0 keeps
+// words 0-1 and takes the partner's 0-1 as 2-3; lane h = 1 takes the
+// partner's 2-3 as 0-1 and keeps 2-3.  The same exchange turns loaded bytes
+// (contiguous channels 32 cb + 16 h + 0..15) into the lane's interleaved
+// order (32 cb + 8 h + 0..7, then 32 cb + 16 + 8 h + 0..7) and the lane's
+// encoded bytes back into contiguous ones.  Both lanes must be active.
+__device__ __forceinline__ u32x4 exchange_tail_halves(u32x4 d, int h) {
+  const int s0 = (int)(h ? d[0] : d[2]), s1 = (int)(h ? d[1] : d[3]);
+  const unsigned r0 = (unsigned)__shfl_xor(s0, 32), r1 = (unsigned)__shfl_xor(s1, 32);
+  u32x4 o;
+  o[0] = h ? r0 : d[0];
+  o[1] = h ? r1 : d[1];
+  o[2] = h ? d[2] : r0;
+  o[3] = h ? d[3] : r1;
+  return o;
+}
+
 }  // namespace bioemu

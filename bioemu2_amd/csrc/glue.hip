@@ -27,7 +27,8 @@ constexpr int kMaxBins = 128;
 
 // ---------------------------------------------------------------------------
 // Distogram.  Wave tile = (b, row i, 32 keys j0 .. j0 + 31); lane (n, hh) holds
-// channel half hh of pair (i, j0 + n).  Tiles entirely below the diagonal exit.
+// channel chunks 2s + hh of pair (i, j0 + n) (pairtile.h).  Tiles entirely
+// below the diagonal exit.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kThreads) void distogram_kernel(const bf16* __restrict__ z, const bf16* __restrict__ wd,
                                                              const float* __restrict__ bd, bf16* __restrict__ out,
@@ -48,11 +49,11 @@ __global__ __launch_bounds__(kThreads) void distogram_kernel(const bf16* __restr
     const bool valid = j < N && j >= i;
     bf16x8 x[8];
     {
-      const bf16* zij = z + (((size_t)b * N + i) * N + (valid ? j : i)) * CZ + 64 * hh;
-      const bf16* zji = z + (((size_t)b * N + (valid ? j : i)) * N + i) * CZ + 64 * hh;
+      const bf16* zij = z + (((size_t)b * N + i) * N + (valid ? j : i)) * CZ + 8 * hh;
+      const bf16* zji = z + (((size_t)b * N + (valid ? j : i)) * N + i) * CZ + 8 * hh;
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
-        const bf16x8 a = load8(zij + 8 * s), c = load8(zji + 8 * s);
+        const bf16x8 a = load8(zij + 16 * s), c = load8(zji + 16 * s);
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[s][e] = f2bf(bf2f(a[e]) + bf2f(c[e]));   // one bf16 rounding of z + z^T
       }

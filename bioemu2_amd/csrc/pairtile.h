@@ -1,10 +1,13 @@
 // Register-resident pair tiles for the 32x32x16 bf16 MFMA.
 //
 // A wave holds a tile of 32 pairs x 128 channels as MFMA operands: lane l
-// (rho = l & 31, h = l >> 5) owns pair slot rho and channel half h, i.e.
-// channels [64h, 64h + 64).  For the 8 MFMA k-steps s the lane supplies
-// channels 64h + 8s .. 64h + 8s + 7 (a k-permutation of the 128 channels;
-// the weight operand reads the same channels, so the product is unchanged).
+// (rho = l & 31, h = l >> 5) owns pair slot rho and the alternate 8-channel
+// chunks 2s + h, i.e. for the 8 MFMA k-steps s the lane supplies channels
+// 16s + 8h .. 16s + 8h + 7 (a k-permutation of the 128 channels; the weight
+// operand reads the same channels, so the product is unchanged).  A pair's two
+// lanes thus read adjacent 16-byte chunks: each 16-byte row-load instruction
+// covers 32 bytes of one cache line per pair, 32 lines per instruction (64 for
+// contiguous half rows, which cost measurably more vector-L1 time).
 //
 // Pair slots are filled in the order perm32(rho), which makes the
 // accumulator of an MFMA whose rows are pair slots come out with every lane
@@ -47,14 +50,13 @@ __device__ __forceinline__ void layernorm_half_row(const bf16x8 raw[8], const fl
   }
   ss += __shfl_xor(ss, 32);
   const float rstd = rsqrtf(ss * (1.0f / kPairC) + eps);
-  const float4* g4 = reinterpret_cast<const float4*>(gamma + 64 * h);
-  const float4* b4 = beta ? reinterpret_cast<const float4*>(beta + 64 * h) : nullptr;
+  // v[8s + e] is channel 16s + 8h + e
 #pragma unroll
   for (int q = 0; q < 16; ++q) {
-    const float4 g = g4[q];
+    const int t = 4 * q, ch = 16 * (t >> 3) + 8 * h + (t & 7);
+    const float4 g = *reinterpret_cast<const float4*>(gamma + ch);
     float4 b = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (b4) b = b4[q];
-    const int t = 4 * q;
+    if (beta) b = *reinterpret_cast<const float4*>(beta + ch);
     out[t >> 3][(t & 7) + 0] = f2bf((v[t + 0] - mean) * rstd * g.x + b.x);
     out[t >> 3][(t & 7) + 1] = f2bf((v[t + 1] - mean) * rstd * g.y + b.y);
     out[t >> 3][(t & 7) + 2] = f2bf((v[t + 2] - mean) * rstd * g.z + b.z);
@@ -68,9 +70,9 @@ __device__ __forceinline__ void layernorm_half_row(const bf16x8 raw[8], const fl
 __device__ __forceinline__ f32x16 proj_block_cm(const bf16x8 x[8], const bf16* wl, int row0, int n,
                                                 int h) {
   f32x16 acc = zero16();
-  const bf16* w = wl + (row0 + n) * kLdw + 64 * h;
+  const bf16* w = wl + (row0 + n) * kLdw + 8 * h;
 #pragma unroll
-  for (int s = 0; s < 8; ++s) acc = mfma32(x[s], load8(w + 8 * s), acc);
+  for (int s = 0; s < 8; ++s) acc = mfma32(x[s], load8(w + 16 * s), acc);
   return acc;
 }
 
@@ -80,9 +82,9 @@ __device__ __forceinline__ f32x16 proj_block_cm(const bf16x8 x[8], const bf16* w
 __device__ __forceinline__ f32x16 proj_block_pm(const bf16x8 x[8], const bf16* wl, int row0, int n,
                                                 int h) {
   f32x16 acc = zero16();
-  const bf16* w = wl + (row0 + perm32(n)) * kLdw + 64 * h;
+  const bf16* w = wl + (row0 + perm32(n)) * kLdw + 8 * h;
 #pragma unroll
-  for (int s = 0; s < 8; ++s) acc = mfma32(load8(w + 8 * s), x[s], acc);
+  for (int s = 0; s < 8; ++s) acc = mfma32(load8(w + 16 * s), x[s], acc);
   return acc;
 }
 
@@ -120,13 +122,14 @@ __device__ __forceinline__ void normalize_half_row(const float* v, bool keep, bf
   for (int c = 0; c < 64; ++c) out[c >> 3][c & 7] = f2bf((v[c] - mean) * rstd);
 }
 
-// Loads this lane's channel half of a pair row as fp32 (zeros when !valid).
+// Loads this lane's 64 channels of a pair row (chunks 2s + h) as fp32 (zeros
+// when !valid).
 __device__ __forceinline__ void load_half_row_f32(const bf16* row, int h, bool valid, float* v) {
 #pragma unroll
   for (int s = 0; s < 8; ++s) {
     bf16x8 raw;
     if (valid) {
-      raw = load8(row + 64 * h + 8 * s);
+      raw = load8(row + 8 * h + 16 * s);
     } else {
 #pragma unroll
       for (int t = 0; t < 8; ++t) raw[t] = f2bf(0.f);
@@ -135,7 +138,7 @@ __device__ __forceinline__ void load_half_row_f32(const bf16* row, int h, bool v
   }
 }
 
-// x-side operand of the bias k-step: [keep, keep, 0, ...] in channel half 0.
+// x-side operand of the bias k-step: [keep, keep, 0, ...] in the lanes h = 0 (k slots 0 and 1).
 __device__ __forceinline__ bf16x8 bias_step_x(bool keep, int h) {
   bf16x8 r;
 #pragma unroll
@@ -163,9 +166,9 @@ __device__ __forceinline__ bf16x8 bias_step_w(const bf16* cl, int row, int h) {
 __device__ __forceinline__ f32x16 proj_block_cm_f(const bf16x8 x[8], bf16x8 xb, const bf16* wl, const bf16* cl,
                                                   int row0, int n, int h) {
   f32x16 acc = zero16();
-  const bf16* w = wl + (row0 + n) * kLdw + 64 * h;
+  const bf16* w = wl + (row0 + n) * kLdw + 8 * h;
 #pragma unroll
-  for (int s = 0; s < 8; ++s) acc = mfma32(x[s], load8(w + 8 * s), acc);
+  for (int s = 0; s < 8; ++s) acc = mfma32(x[s], load8(w + 16 * s), acc);
   return mfma32(xb, bias_step_w(cl, row0 + n, h), acc);
 }
 
@@ -174,9 +177,9 @@ __device__ __forceinline__ f32x16 proj_block_pm_f(const bf16x8 x[8], bf16x8 xb, 
                                                   int row0, int n, int h) {
   f32x16 acc = zero16();
   const int r = row0 + perm32(n);
-  const bf16* w = wl + r * kLdw + 64 * h;
+  const bf16* w = wl + r * kLdw + 8 * h;
 #pragma unroll
-  for (int s = 0; s < 8; ++s) acc = mfma32(load8(w + 8 * s), x[s], acc);
+  for (int s = 0; s < 8; ++s) acc = mfma32(load8(w + 16 * s), x[s], acc);
   return mfma32(bias_step_w(cl, r, h), xb, acc);
 }
 

@@ -13,9 +13,15 @@
 // extra MFMA k-step (pairtile.h).
 //
 // One workgroup = 4 waves x 32 rows.  Each wave keeps its normalised row
-// tile in registers as MFMA operands (lane (n, hh) holds channels
-// [hh c/2, (hh + 1) c/2) of row slot n) and its 32 x c output accumulator in
-// registers; the hidden dimension is walked in chunks of 32.  A chunk's weight
+// tile in registers as MFMA operands and its 32 x c output accumulator in
+// registers; the hidden dimension is walked in chunks of 32.  The two lanes
+// (n, 0) and (n, 1) of row slot n hold alternate 8-channel chunks (lane hh
+// chunk s = channels 16 s + 8 hh + 0..7), so that each 16-byte row load or
+// store instruction covers 32 bytes of one cache line per row (32 lines per
+// instruction rather than 64 for contiguous half rows); the fc1 / fc2 operand
+// reads take weight chunk 2 s + hh to match, and the fc3 rows are staged so
+// that output block cb gives lane hh the channels 32 cb + 8 hh + 0..7 and
+// 32 cb + 16 + 8 hh + 0..7.  A chunk's weight
 // slices (fc1 and fc2 rows, the fc3 columns and the two bias columns; 24.25 KB
 // at c = 128, 12.25 KB at c = 64) are copied by buffer loads straight into LDS
 // (no registers), double-buffered: chunk h + 1 is in flight while chunk h is
@@ -107,8 +113,10 @@ __global__ __launch_bounds__(kThreads) void transition_rows_kernel(
         copy16_to_lds(second ? r2 : r1, st + (second ? G::W12Tile : 0) + j * 512, (unsigned)(r * C + c * 8) * 2,
                       (unsigned)(hc * HC * C) * 2);
       } else if (k < 2 * G::W12Copies + G::W3Copies) {
+        // LDS row 32 cb + m <- fc3 row 32 cb + 16 ((m & 15) >> 3) + 8 (m >> 4) + (m & 7)
         const int j = k - 2 * G::W12Copies, p = j * 64 + lane, r = p >> 2, c = (p & 3) ^ swz4(r);
-        copy16_to_lds(r3, st + 2 * G::W12Tile + j * 512, (unsigned)(r * HID + c * 8) * 2, (unsigned)(hc * HC) * 2);
+        const int m = r & 31, rg = (r & ~31) + 16 * ((m & 15) >> 3) + 8 * (m >> 4) + (m & 7);
+        copy16_to_lds(r3, st + 2 * G::W12Tile + j * 512, (unsigned)(rg * HID + c * 8) * 2, (unsigned)(hc * HC) * 2);
       } else if (use_norm) {
         const int which = lane >> 5, row = lane & 31;
         copy4_to_lds(rc, st + 2 * G::W12Tile + G::W3Tile, (unsigned)((which * HID + row) * 2) * 2,
@@ -119,19 +127,19 @@ __global__ __launch_bounds__(kThreads) void transition_rows_kernel(
 
   stage_chunk(0);
 
-  // This wave's 32 rows: lane (n, hh) holds channel half hh of row p0 + n.
+  // This wave's 32 rows: lane (n, hh) holds chunks 2 s + hh of row p0 + n.
   const long long p0 = (long long)blockIdx.x * kRowsPerWg + wave * 32;
   const long long pair = p0 + n;
   const bool valid = pair < P;
   bf16x8 xf[KS];
   {
     float v[C / 2];
-    const bf16* row = x + (size_t)(valid ? pair : 0) * C + hh * (C / 2);
+    const bf16* row = x + (size_t)(valid ? pair : 0) * C + 8 * hh;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       bf16x8 raw;
       if (valid) {
-        raw = load8(row + 8 * s);
+        raw = load8(row + 16 * s);
       } else {
 #pragma unroll
         for (int t = 0; t < 8; ++t) raw[t] = f2bf(0.f);
@@ -181,8 +189,8 @@ __global__ __launch_bounds__(kThreads) void transition_rows_kernel(
     f32x16 a = zero16(), g = zero16();
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      a = mfma32(load8(s1 + w12_off<C>(rw, KS * hh + s)), xf[s], a);
-      g = mfma32(load8(s2 + w12_off<C>(rw, KS * hh + s)), xf[s], g);
+      a = mfma32(load8(s1 + w12_off<C>(rw, 2 * s + hh)), xf[s], a);
+      g = mfma32(load8(s2 + w12_off<C>(rw, 2 * s + hh)), xf[s], g);
     }
     if (use_norm) {
       a = mfma32(bias_step_w(cl, rw, hh), xb, a);
@@ -199,31 +207,46 @@ __global__ __launch_bounds__(kThreads) void transition_rows_kernel(
     }
   }
 
-  // D lane (n, hh) of block cb: output channel cb*32 + 16hh + u of row p0 + n
+  // D lane (n, hh) of block cb, register u: output channel
+  // 32 cb + 16 (u >> 3) + 8 hh + (u & 7) of row p0 + n.  The two lanes of a
+  // row are valid together (the tail exchange pairs them).
   if (!valid) return;
 #pragma unroll
   for (int cb = 0; cb < C / 32; ++cb) {
-    const size_t off = (size_t)pair * C + cb * 32 + 16 * hh;
+    const size_t off0 = (size_t)pair * C + cb * 32 + 8 * hh, off1 = off0 + 16;
     float v[16];
 #pragma unroll
     for (int u = 0; u < 16; ++u) v[u] = acc[cb][u];
     if (kTail) {
       float xv[16];
-      tail_decode16(load8(x + off), load8(x + off + 8), load_tail16(tail + off), xv);
+      const size_t toff = (size_t)pair * C + cb * 32 + 16 * hh;
+      tail_decode16(load8(x + off0), load8(x + off1), exchange_tail_halves(load_tail16(tail + toff), hh), xv);
 #pragma unroll
       for (int u = 0; u < 16; ++u) v[u] += xv[u];
-      tail_store16(out + off, tail + off, v);
+      bf16x8 lo, hi;
+      u32x4 tb;
+      tail_encode16(v, lo, hi, tb);
+      store8(out + off0, lo);
+      store8(out + off1, hi);
+      *reinterpret_cast<u32x4*>(tail + toff) = exchange_tail_halves(tb, hh);
       continue;
     }
     if (residual) {
-      const bf16x8 q0 = load8(x + off), q1 = load8(x + off + 8);
+      const bf16x8 q0 = load8(x + off0), q1 = load8(x + off1);
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         v[u] += bf2f(q0[u]);
         v[8 + u] += bf2f(q1[u]);
       }
     }
-    store16(out + off, v);
+    bf16x8 lo, hi;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      lo[u] = f2bf(v[u]);
+      hi[u] = f2bf(v[8 + u]);
+    }
+    store8(out + off0, lo);
+    store8(out + off1, hi);
   }
 }
 

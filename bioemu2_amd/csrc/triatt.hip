@@ -114,9 +114,9 @@ __global__ __launch_bounds__(kProjThreads) void triatt_proj_kernel(
     // wait for those stores.
     const bool valid = i < N && kk < N;
     const size_t zpair = !valid ? 0 : kStarting ? ((size_t)b * N + i) * N + kk : ((size_t)b * N + kk) * N + i;
-    const bf16* row = z + zpair * C + 64 * h;
+    const bf16* row = z + zpair * C + 8 * h;
 #pragma unroll
-    for (int s8 = 0; s8 < 8; ++s8) raw[s8] = load8(row + 8 * s8);
+    for (int s8 = 0; s8 < 8; ++s8) raw[s8] = load8(row + 16 * s8);
   };
   // Tile operands: normalised row x, the bias k-step operand xb and the mask byte.
   bf16x8 x[8], xb;

@@ -95,9 +95,9 @@ __global__ __launch_bounds__(64 * kWaves) void trimul_proj_in_kernel(
     inb_next = i < N && kk < N;
     const size_t pair = !inb_next ? 0 : kOutgoing ? ((size_t)b * N + i) * N + kk : ((size_t)b * N + kk) * N + i;
     mraw = mask[pair];
-    const bf16* row = x + pair * D + 64 * h;
+    const bf16* row = x + pair * D + 8 * h;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) raw[s] = load8(row + 8 * s);
+    for (int s = 0; s < 8; ++s) raw[s] = load8(row + 16 * s);
   };
   bf16x8 xf[8];
   auto prepare = [&]() {
@@ -216,13 +216,10 @@ __device__ __forceinline__ void normalize_half_row(const float* v, bf16x8 out[8]
 // registers against the folded weights, which sit in LDS with the folded
 // biases.
 //
-// Channel interleave: the two lanes (rho, 0) and (rho, 1) of a pair hold
-// alternate 8-channel chunks, lane h chunk s = channels 16 s + 8 h + (0..7).
-// Each 16-byte load or store instruction then covers 32 bytes of one cache
-// line per pair (32 lines per instruction instead of 64 for contiguous half
-// rows), and chunk s is already the MFMA B operand of k-step s once the
-// weight columns are staged in the matching order (LDS chunk 8 h + s <-
-// weight chunk 2 s + h).  Output lanes: LDS row 32 cb + m of each folded
+// Channel interleave (pairtile.h): the two lanes (rho, 0) and (rho, 1) of a
+// pair hold alternate 8-channel chunks, lane h chunk s = channels
+// 16 s + 8 h + (0..7), which is the MFMA B operand of k-step s.  The output
+// stores use the same interleave.  Output lanes: LDS row 32 cb + m of each folded
 // weight half holds weight row 32 cb + 16 ((m & 15) >> 3) + 8 (m >> 4) +
 // (m & 7), so that lane (rho, h) of output block cb holds channels
 // 32 cb + 8 h + u and 32 cb + 16 + 8 h + u (u < 8): x chunks 2 cb and
@@ -250,22 +247,6 @@ __device__ __forceinline__ int obuf_off(int c, int j) {
   return q * 512 + slot * 32 + j + ((q >> 2) << 5);
 }
 
-// Tail words of 16 channels between the two lanes of a pair: lane h = 0 keeps
-// words 0-1 and takes the partner's 0-1 as 2-3; lane h = 1 takes the
-// partner's 2-3 as 0-1 and keeps 2-3.  The same exchange turns loaded bytes
-// (contiguous channels 32 cb + 16 h + 0..15) into the lane's interleaved
-// order and the lane's encoded bytes back into contiguous ones.
-__device__ __forceinline__ u32x4 exchange_tail_halves(u32x4 d, int h) {
-  const int s0 = (int)(h ? d[0] : d[2]), s1 = (int)(h ? d[1] : d[3]);
-  const unsigned r0 = (unsigned)__shfl_xor(s0, 32), r1 = (unsigned)__shfl_xor(s1, 32);
-  u32x4 o;
-  o[0] = h ? r0 : d[0];
-  o[1] = h ? r1 : d[1];
-  o[2] = h ? d[2] : r0;
-  o[3] = h ? d[3] : r1;
-  return o;
-}
-
 // Lanes of pair slots past N store into `discard` (a dead workspace region,
 // 16 KB) instead of skipping the store: a conditional store would hide the
 // number of stores from the compiler's wait counting, which would then wait
@@ -284,8 +265,7 @@ __global__ __launch_bounds__(kOutThreads) void trimul_out_kernel(
     const int r = q >> 4, part = q & 15;
     const int half = r / D, cb = (r % D) >> 5, m = r & 31;
     const int src = half * D + 32 * cb + 16 * ((m & 15) >> 3) + 8 * (m >> 4) + (m & 7);
-    const int src_part = 2 * (part & 7) + (part >> 3);
-    store8(wl + r * kLdw + part * 8, load8(wfold + (size_t)src * D + src_part * 8));
+    store8(wl + r * kLdw + part * 8, load8(wfold + (size_t)src * D + part * 8));
   }
   // cl[half D + 64 h + 16 cb + u]: bias of the channel lane h holds in register u of block cb
   for (int t = threadIdx.x; t < 2 * D; t += blockDim.x) {

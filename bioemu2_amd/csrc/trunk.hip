@@ -30,8 +30,8 @@ constexpr int kSmem = C * kLdw * 2 + C * 2 * 2;
 // ---------------------------------------------------------------------------
 // out[p] = base[p] + W LN(x[p]) over tiles of 32 pair rows per wave.  The
 // folded weights W' = W diag(gamma) and the bias W beta (hi, lo) sit in LDS;
-// a lane (n, h) loads channel half h of pair p0 + n, and the pair-major
-// product leaves it 16 consecutive output channels of that pair, so base,
+// a lane (n, h) loads channel chunks 2s + h of pair p0 + n (pairtile.h), and
+// the pair-major product leaves it 16 consecutive output channels of that pair, so base,
 // its tail and the output are 32-byte contiguous per lane.  out may alias x
 // or base: a pair's row is read entirely before the lane that owns it writes.
 // ---------------------------------------------------------------------------
