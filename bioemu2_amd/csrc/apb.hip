@@ -17,6 +17,7 @@
 #include <algorithm>
 
 #include "common.h"
+#include "gemm_nt.h"
 #include "internal.h"
 #include "pairtile.h"
 
@@ -26,8 +27,9 @@ namespace {
 constexpr int CZ = 128;
 constexpr int kBiasThreads = 256;
 
-// bias[b][h][i][j] = LN(z[b][i][j]) . Wz[h] for i, j < Np (zero pair rows outside [0, N)),
-// with the LayerNorm folded into Wz (wf, cf from launch_fold_ln).
+// bias[b][h][i][j] = log2(e) * LN(z[b][i][j]) . Wz[h] for i, j < Np (zero pair rows outside
+// [0, N)), with the LayerNorm folded into Wz (wf, cf from launch_fold_ln).  The
+// attention's softmax runs in base 2, so the bias is stored in log2 units.
 __global__ __launch_bounds__(kBiasThreads) void pair_bias_kernel(const bf16* __restrict__ z,
                                                                  const bf16* __restrict__ wf,
                                                                  const bf16* __restrict__ cf, bf16* __restrict__ bias,
@@ -84,8 +86,8 @@ __global__ __launch_bounds__(kBiasThreads) void pair_bias_kernel(const bf16* __r
     bf16x8 o[2];   // tile t's bias, packed while tile t + stride is normalised
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      o[0][u] = f2bf(acc[u]);
-      o[1][u] = f2bf(acc[8 + u]);
+      o[0][u] = f2bf(acc[u] * kLog2e);
+      o[1][u] = f2bf(acc[8 + u] * kLog2e);
     }
     if (tn < ntiles) prepare(tn);
     if (rho < H) {
@@ -105,6 +107,7 @@ __global__ __launch_bounds__(kBiasThreads) void pair_bias_kernel(const bf16* __r
 // O^T = V^T P^T (lane holds d = 16hh + u).
 // ---------------------------------------------------------------------------
 constexpr int DH = 24;
+constexpr float kQScale = 0.20412414523193154f * kLog2e;   // log2(e) / sqrt(DH)
 constexpr int kMaxMaskN = 16384;
 
 __global__ __launch_bounds__(256) void apb_flash_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
@@ -112,10 +115,21 @@ __global__ __launch_bounds__(256) void apb_flash_kernel(const bf16* __restrict__
                                                         const bf16* __restrict__ bias,
                                                         const uint8_t* __restrict__ mask, bf16* __restrict__ go,
                                                         int N, int Np, int H, int mult) {
-  __shared__ __attribute__((aligned(16))) uint8_t mrow[kMaxMaskN];
+  // Per key t: the logit is x = kv[t] * (q.k + bias) + c0[t], i.e. unchanged
+  // for a valid key (kv = 1, c0 = 0), replaced by the reference's -1e6 (in
+  // log2 units) for a masked one (kv = 0), and -inf past N (no such key).
+  // (dynamic LDS: kv[Np] then c0[Np])
+  extern __shared__ __attribute__((aligned(16))) float key_terms[];
+  float* kvl = key_terms;
+  float* c0l = key_terms + Np;
   const int bm = blockIdx.z, b = bm / mult;
   const int CS = H * DH;
-  for (int t = threadIdx.x; t < Np; t += blockDim.x) mrow[t] = (t < N) ? (mask[(size_t)b * N + t] != 0) : 0;
+  const float masked_logit = -1e6f * kLog2e;
+  for (int t = threadIdx.x; t < Np; t += blockDim.x) {
+    const bool valid = t < N && mask[(size_t)b * N + t] != 0;
+    kvl[t] = valid ? 1.f : 0.f;
+    c0l[t] = valid ? 0.f : t < N ? masked_logit : -INFINITY;
+  }
   __syncthreads();
 
   const int lane = threadIdx.x & 63, wave = wave_id();
@@ -123,8 +137,6 @@ __global__ __launch_bounds__(256) void apb_flash_kernel(const bf16* __restrict__
   const int hd = blockIdx.y * 4 + wave;
   if (hd >= H) return;  // after the only barrier
   const int q0 = blockIdx.x * 32;
-  const float qk_scale = kLog2e / sqrtf((float)DH);
-  const float masked_logit = -1e6f * kLog2e;
 
   bf16x8 zero8;
 #pragma unroll
@@ -141,22 +153,51 @@ __global__ __launch_bounds__(256) void apb_flash_kernel(const bf16* __restrict__
   const bf16* vbase = vt + ((size_t)bm * CS + hd * DH + (dslot < DH ? dslot : 0)) * Np;
   const bf16* brow = bias + (((size_t)b * H + hd) * Np + q0 + n) * Np;
 
-  for (int k0 = 0; k0 < Np; k0 += 32) {
-    const bf16* kr = kbase + (size_t)(k0 + perm32(n)) * CS;
+  // Operands of one 32-key block: K fragments, the bias row slice and the V^T
+  // fragments.  The next block's are requested before the current block is
+  // consumed, so each block's global-memory latency hides behind the previous
+  // block's work.
+  const bool dvalid = dslot < DH;
+  struct Frag {
+    bf16x8 k0, k1, b0, b1, v0, v1;
+  };
+  auto fetch = [&](int kb) {
+    Frag f;
+    const bf16* kr = kbase + (size_t)(kb + perm32(n)) * CS;
+    // every address is valid (vbase is clamped to a real d row); lanes whose
+    // fragment is zero (k1 of hh = 1, V of d >= 24) select it at use, so that
+    // no load sits in a branch
+    f.k0 = load8(kr + 8 * hh);
+    f.k1 = load8(kr + 16);
+    f.b0 = load8(brow + kb + 16 * hh);
+    f.b1 = load8(brow + kb + 16 * hh + 8);
+    const bf16* vp = vbase + kb + 16 * hh;
+    f.v0 = load8(vp);
+    f.v1 = load8(vp + 8);
+    return f;
+  };
+  // Two fixed fragment sets used alternately (the loop is unrolled by two):
+  // a copy between them would make the compiler wait for the new loads.
+  auto consume = [&](const Frag& f, int k0) {
     f32x16 s = zero16();
-    s = mfma32(load8(kr + 8 * hh), qf0, s);
-    s = mfma32(hh == 0 ? load8(kr + 16) : zero8, qf1, s);
-    const bf16x8 b0 = load8(brow + k0 + 16 * hh), b1 = load8(brow + k0 + 16 * hh + 8);
-    const uint4 mk = *reinterpret_cast<const uint4*>(mrow + k0 + 16 * hh);
-    const uint32_t mw[4] = {mk.x, mk.y, mk.z, mk.w};
+    s = mfma32(f.k0, qf0, s);
+    s = mfma32(hh == 0 ? f.k1 : zero8, qf1, s);
+    const bf16x8 b0 = f.b0, b1 = f.b1;
+    const float4* kv4 = reinterpret_cast<const float4*>(kvl + k0 + 16 * hh);
+    const float4* c04 = reinterpret_cast<const float4*>(c0l + k0 + 16 * hh);
+    float kv[16], c0[16];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float4 a = kv4[e], c = c04[e];
+      kv[4 * e] = a.x, kv[4 * e + 1] = a.y, kv[4 * e + 2] = a.z, kv[4 * e + 3] = a.w;
+      c0[4 * e] = c.x, c0[4 * e + 1] = c.y, c0[4 * e + 2] = c.z, c0[4 * e + 3] = c.w;
+    }
     float t[16];
     float bmax = -INFINITY;
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
-      const float bv = bf2f(u < 8 ? b0[u] : b1[u - 8]);
-      float x = s[u] * qk_scale + bv * kLog2e;
-      if (((mw[u >> 2] >> (8 * (u & 3))) & 0xff) == 0) x = masked_logit;
-      if (k0 + 16 * hh + u >= N) x = -INFINITY;
+      // q carries log2(e)/sqrt(d) and the bias log2(e): s + bias is the logit in log2 units
+      const float x = __builtin_fmaf(s[u] + bf2f(u < 8 ? b0[u] : b1[u - 8]), kv[u], c0[u]);
       t[u] = x;
       bmax = fmaxf(bmax, x);
     }
@@ -175,10 +216,16 @@ __global__ __launch_bounds__(256) void apb_flash_kernel(const bf16* __restrict__
     l = l * alpha + psum;
 #pragma unroll
     for (int u = 0; u < 16; ++u) o[u] *= alpha;
-    const bf16* vp = vbase + k0 + 16 * hh;
-    const bool dvalid = dslot < DH;
-    o = mfma32(dvalid ? load8(vp) : zero8, pb[0], o);
-    o = mfma32(dvalid ? load8(vp + 8) : zero8, pb[1], o);
+    o = mfma32(dvalid ? f.v0 : zero8, pb[0], o);
+    o = mfma32(dvalid ? f.v1 : zero8, pb[1], o);
+  };
+  Frag fa = fetch(0), fb;
+  for (int k0 = 0; k0 < Np; k0 += 64) {
+    fb = fetch(k0 + 32 < Np ? k0 + 32 : k0);   // the last block refetches itself
+    consume(fa, k0);
+    if (k0 + 32 >= Np) break;
+    fa = fetch(k0 + 64 < Np ? k0 + 64 : k0 + 32);
+    consume(fb, k0 + 32);
   }
 
   const float inv = 1.0f / (l + __shfl_xor(l, 32));
@@ -198,6 +245,67 @@ __global__ __launch_bounds__(256) void apb_flash_kernel(const bf16* __restrict__
 #pragma unroll
     for (int u = 0; u < 8; ++u) r[u] = f2bf(bf2f(g0[u]) * (o[u] * inv));
     store8(go + off, r);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// q | k | v^T | g in one launch: 256 x 256 tiles of LN(s)[M][c_s] times
+// [Wq; Wk; Wv; Wg]^T ([4 c_s][c_s], weights staged through LDS by the tile loop
+// of gemm_nt.h; tile rows past M read as zero and are not stored).  The output
+// is picked per 32-column block: q ((+ q_bias) * log2(e) / sqrt(d), the
+// attention's softmax scale in base 2), k and g (sigmoid) row-major
+// [M][c_s]; v transposed, [B * mult][c_s][Np] (the attention reads V^T).  Lane
+// (ln, lh) of block (ib, jb) holds token row wi*64 + ib*32 + ln and 16
+// consecutive output columns (gemm_nt.h).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kNtThreads) void apb_qkvg_kernel(const bf16* __restrict__ sn,
+                                                              const bf16* __restrict__ wqkv,
+                                                              const bf16* __restrict__ wg,
+                                                              const float* __restrict__ q_bias, bf16* __restrict__ q,
+                                                              bf16* __restrict__ k, bf16* __restrict__ vt,
+                                                              bf16* __restrict__ g, int M, int CS, int Np) {
+  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+  bf16* smem = reinterpret_cast<bf16*>(smem_raw);
+  const int ntj = 4 * CS / kNtTile;
+  const int ti = blockIdx.x / ntj, tj = blockIdx.x % ntj;
+  const int row0 = ti * kNtTile, col0 = tj * kNtTile;
+  // weight rows col0 .. col0 + 255: [0, 3 c_s) are wqkv's, [3 c_s, 4 c_s) wg's
+  const int split = min(max(3 * CS - col0, 0), kNtTile);
+  const bf16* b1 = wqkv + (size_t)min(col0, 3 * CS) * CS;
+  const bf16* b2 = wg + (size_t)max(col0 - 3 * CS, 0) * CS;
+  f32x16 acc[4][2];
+  gemm_nt_tile(sn + (size_t)row0 * CS, min(M - row0, kNtTile), b1, b2, split, CS, smem, acc);
+
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int ln = lane & 31, lh = lane >> 5;
+  const int wi = wave & 3, wj = wave >> 2;
+#pragma unroll
+  for (int jb = 0; jb < 4; ++jb) {
+    const int col = col0 + wj * 128 + jb * 32;   // wave-uniform 32-column block
+    const int which = col / CS, c0 = col % CS + 16 * lh;
+#pragma unroll
+    for (int ib = 0; ib < 2; ++ib) {
+      const int r = row0 + wi * 64 + ib * 32 + ln;
+      if (r >= M) continue;
+      float v[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) v[u] = acc[jb][ib][u];
+      if (which == 2) {
+        const int bm = r / Np, t = r % Np;
+        bf16* dst = vt + ((size_t)bm * CS + c0) * Np + t;
+#pragma unroll
+        for (int u = 0; u < 16; ++u) dst[(size_t)u * Np] = f2bf(v[u]);
+        continue;
+      }
+      if (which == 0) {   // q carries the softmax scale in log2 units
+#pragma unroll
+        for (int u = 0; u < 16; ++u) v[u] = (v[u] + q_bias[c0 + u]) * kQScale;
+      } else if (which == 3) {
+#pragma unroll
+        for (int u = 0; u < 16; ++u) v[u] = sigmoidf_fast(v[u]);
+      }
+      store16((which == 0 ? q : which == 1 ? k : g) + (size_t)r * CS + c0, v);
+    }
   }
 }
 
@@ -274,14 +382,17 @@ extern "C" int bioemu_apb_fwd(const void* s, const void* z, const uint8_t* mask,
   const bf16* wqkv = static_cast<const bf16*>(w_qkv);
 
   int rc = token_layernorm(s, norm_s_w, norm_s_b, buf.sn, BM, N, Np, c_s, stream);
-  if (!rc) rc = token_gemm(kEpiStoreId, false, buf.sn, wqkv, nullptr, q_bias, nullptr, buf.q, M, c_s, c_s, N, Np, Np,
-                           stream, "apb_proj_q");
-  if (!rc) rc = token_gemm(kEpiStoreId, false, buf.sn, wqkv + c_s * c_s, nullptr, nullptr, nullptr, buf.k, M, c_s,
-                           c_s, N, Np, Np, stream, "apb_proj_k");
-  if (!rc) rc = token_gemm(kEpiStoreId, true, buf.sn, wqkv + 2 * c_s * c_s, nullptr, nullptr, nullptr, buf.vt, M,
-                           c_s, c_s, N, Np, Np, stream, "apb_proj_v");
-  if (!rc) rc = token_gemm(kEpiSigmoidId, false, buf.sn, w_g, nullptr, nullptr, nullptr, buf.g, M, c_s, c_s, N, Np,
-                           Np, stream, "apb_proj_g");
+  if (rc) return rc;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(apb_qkvg_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          kNtSmem) != hipSuccess)
+    return set_error(BIOEMU_ERR_LAUNCH, "apb_proj_qkvg: cannot set dynamic LDS size");
+  {
+    const long long tiles = (M + kNtTile - 1) / kNtTile * (4 * c_s / kNtTile);
+    KernelTimerScope timed("apb_proj_qkvg", stream);
+    hipLaunchKernelGGL(apb_qkvg_kernel, dim3((unsigned)tiles), dim3(kNtThreads), kNtSmem, stream, buf.sn, wqkv,
+                       static_cast<const bf16*>(w_g), q_bias, buf.q, buf.k, buf.vt, buf.g, (int)M, (int)c_s, (int)Np);
+  }
+  rc = check_launch("apb_proj_qkvg");
   if (rc) return rc;
 
   int dev = 0, cus = 0;
@@ -300,9 +411,13 @@ extern "C" int bioemu_apb_fwd(const void* s, const void* z, const uint8_t* mask,
   rc = check_launch("apb_pair_bias");
   if (rc) return rc;
   {
+    const size_t key_lds = (size_t)2 * Np * sizeof(float);   // <= 128 KB (N <= 16384)
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(apb_flash_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)key_lds) != hipSuccess)
+      return set_error(BIOEMU_ERR_LAUNCH, "apb_flash: cannot set dynamic LDS size");
     KernelTimerScope timed("apb_flash", stream);
     hipLaunchKernelGGL(apb_flash_kernel, dim3((unsigned)(Np / 32), (unsigned)((H + 3) / 4), (unsigned)BM), dim3(256),
-                       0, stream, buf.q, buf.k, buf.vt, buf.g, buf.bias, mask, buf.go, (int)N, (int)Np, (int)H,
+                       key_lds, stream, buf.q, buf.k, buf.vt, buf.g, buf.bias, mask, buf.go, (int)N, (int)Np, (int)H,
                        (int)mult);
   }
   rc = check_launch("apb_flash");

@@ -44,24 +44,34 @@ __device__ __forceinline__ void nt_copy16_to_lds(__amdgpu_buffer_rsrc_t r, const
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(lds), 16, voff, soff, 0, 0);
 }
 
-// A points at the tile's first row of A (256 rows of K), B at the tile's first
-// row of B; K % 64 == 0 and 256 * K * 2 < 2^32.  Whole workgroup; smem holds
-// kNtSmem bytes.  Ends with a barrier-free epilogue-ready acc.
-__device__ __forceinline__ void gemm_nt_tile(const bf16* A, const bf16* B, int K, bf16* smem, f32x16 (&acc)[4][2]) {
+// A points at the tile's first row of A, of which a_rows (<= 256) exist: the
+// rest read as zero through the buffer bound (their C rows are garbage-free
+// zeros times B, never needed by a caller that skips them).  B rows [0,
+// b_split) come from B, rows [b_split, 256) from B2 (its row 0 = tile row
+// b_split); b_split is a multiple of 8.  K % 64 == 0 and 256 * K * 2 < 2^32.
+// Whole workgroup; smem holds kNtSmem bytes.  Ends with a barrier-free
+// epilogue-ready acc.
+__device__ __forceinline__ void gemm_nt_tile(const bf16* A, int a_rows, const bf16* B, const bf16* B2, int b_split,
+                                             int K, bf16* smem, f32x16 (&acc)[4][2]) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ln = lane & 31, lh = lane >> 5;
   const int wi = wave & 3, wj = wave >> 2;
-  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(A, (unsigned)kNtTile * K * 2);
-  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(B, (unsigned)kNtTile * K * 2);
+  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(A, (unsigned)a_rows * K * 2);
+  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(B, (unsigned)b_split * K * 2);
+  const __amdgpu_buffer_rsrc_t rb2 = buffer_rsrc(B2, (unsigned)(kNtTile - b_split) * K * 2);
   // Each operand tile (256 rows x 128 B) is 32 copies of 1 KB; wave w moves
   // copies w, w + 8, w + 16, w + 24 of A and of B.  Copy j writes LDS chunk
-  // 64 j + lane = (row, swizzled chunk) of the tile.
-  unsigned voff[4];
+  // 64 j + lane = (row, swizzled chunk) of the tile: rows 8 j .. 8 j + 7, all
+  // on one side of b_split.
+  unsigned voff[4], voffb[4];
+  bool second[4];
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int p = (wave + 8 * q) * 64 + lane, r = p >> 3, c = (p & 7) ^ nt_swz(p >> 3);
     voff[q] = (unsigned)(r * K + c * 8) * 2;
+    second[q] = b_split < kNtTile && (wave + 8 * q) * 8 >= b_split;
+    voffb[q] = second[q] ? (unsigned)((r - b_split) * K + c * 8) * 2 : voff[q];
   }
   auto stage = [&](int kt) {
     bf16* st = smem + (kt & 1) * kNtStage;
@@ -69,7 +79,7 @@ __device__ __forceinline__ void gemm_nt_tile(const bf16* A, const bf16* B, int K
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       nt_copy16_to_lds(ra, st + (wave + 8 * q) * 512, voff[q], soff);
-      nt_copy16_to_lds(rb, st + kNtTileElems + (wave + 8 * q) * 512, voff[q], soff);
+      nt_copy16_to_lds(second[q] ? rb2 : rb, st + kNtTileElems + (wave + 8 * q) * 512, voffb[q], soff);
     }
   };
 
@@ -112,6 +122,11 @@ __device__ __forceinline__ void gemm_nt_tile(const bf16* A, const bf16* B, int K
         for (int ib = 0; ib < 2; ++ib) acc[jb][ib] = mfma32(fj[ks][jb], fi[ks][ib], acc[jb][ib]);
     __builtin_amdgcn_sched_barrier(0);
   }
+}
+
+// Full tiles from one B matrix.
+__device__ __forceinline__ void gemm_nt_tile(const bf16* A, const bf16* B, int K, bf16* smem, f32x16 (&acc)[4][2]) {
+  gemm_nt_tile(A, kNtTile, B, B, kNtTile, K, smem, acc);
 }
 
 // XCD-aware work-item order: workgroup w runs on XCD w % 8; each XCD gets a

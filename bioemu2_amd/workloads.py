@@ -291,10 +291,7 @@ class BlockWorkload(Workload):
         # token-side kernels: tiny; report against HBM with their operand bytes
         token_bytes = {
             "token_layernorm": 2 * n * cs * 2,
-            "apb_proj_q": n * cs * 2 * 2 + cs * cs * 2,
-            "apb_proj_k": n * cs * 2 * 2 + cs * cs * 2,
-            "apb_proj_v": n * cs * 2 * 2 + cs * cs * 2,
-            "apb_proj_g": n * cs * 2 * 2 + cs * cs * 2,
+            "apb_proj_qkvg": n * cs * 2 * 5 + 4 * cs * cs * 2,
             "apb_proj_o": n * cs * 2 * 3 + cs * cs * 2,
             "transition_token_swiglu": n * cs * 2 + n * 4 * cs * 2 + 2 * 4 * cs * cs * 2,
             "transition_token_out": n * 4 * cs * 2 + 2 * n * cs * 2 + 4 * cs * cs * 2,
@@ -895,7 +892,9 @@ class ApbWorkload(Workload):
         if kernel == "apb_flash":
             # reads q, k, v, g and the bias, writes g*o; the QK^T / PV products are 4 N^2 c_s flops per copy
             return ("hbm", float(5 * tok + B * 16 * np_ * np_ * 2))
-        if kernel in ("apb_proj_q", "apb_proj_k", "apb_proj_v", "apb_proj_g", "apb_proj_o", "token_layernorm"):
+        if kernel == "apb_proj_qkvg":   # the four token projections in one launch
+            return ("mfma", 4 * 2.0 * B * M * np_ * 384 * 384)
+        if kernel in ("apb_proj_o", "token_layernorm"):
             return ("hbm", float(2 * tok + 384 * 384 * 2))
         if kernel == "fold_ln":
             return fold_kernel_work(kernel, 1, 16)
