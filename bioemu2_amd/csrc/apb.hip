@@ -99,9 +99,11 @@ __global__ __launch_bounds__(kBiasThreads) void pair_bias_kernel(const bf16* __r
 }
 
 // ---------------------------------------------------------------------------
-// Flash kernel.  Block = (32 queries, 4 heads, batch*M row bm); wave w owns
-// head 4*blockIdx.y + w.  Head dim 24 is zero-padded to 32 for the 16-deep
-// MFMA k-steps (k-step 1, half 1 carries d = 24..31 = 0).
+// Flash kernel.  Workgroup = (128 queries, one head, batch*M row bm): wave w
+// owns queries q0 = 128 blockIdx.x + 32 w of head blockIdx.y.  Per 32-key
+// block the workgroup stages K [32 keys][d] and V^T [d][32 keys] once in LDS
+// (double-buffered, head dim 24 zero-padded to 32 there), so its four waves
+// share them; each wave fetches its own bias rows one block ahead.
 // Same register dataflow as the triangle-attention flash kernel:
 // S^T = K Q^T (lane (n, hh) holds keys k0 + 16hh + u of query q0 + n),
 // O^T = V^T P^T (lane holds d = 16hh + u).
@@ -109,6 +111,11 @@ __global__ __launch_bounds__(kBiasThreads) void pair_bias_kernel(const bf16* __r
 constexpr int DH = 24;
 constexpr float kQScale = 0.20412414523193154f * kLog2e;   // log2(e) / sqrt(DH)
 constexpr int kMaxMaskN = 16384;
+constexpr int kFlashQ = 128;                  // queries per workgroup
+constexpr int kKvLd = 40;                     // LDS row stride (bf16) of the K and V^T tiles
+constexpr int kKvTile = 32 * kKvLd;           // one tile: 32 rows
+constexpr int kKvStage = 2 * kKvTile;         // K then V^T
+constexpr int kKvChunks = 32 * 3 + 24 * 4;    // 16-byte global chunks per block: K 32 x 3, V^T 24 x 4
 
 __global__ __launch_bounds__(256) void apb_flash_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
                                                         const bf16* __restrict__ vt, const bf16* __restrict__ g,
@@ -120,69 +127,74 @@ __global__ __launch_bounds__(256) void apb_flash_kernel(const bf16* __restrict__
   // log2 units) for a masked one (kv = 0), and -inf past N (no such key).
   // (dynamic LDS: kv[Np] then c0[Np])
   extern __shared__ __attribute__((aligned(16))) float key_terms[];
+  __shared__ __attribute__((aligned(16))) bf16 kvs[2 * kKvStage];
   float* kvl = key_terms;
   float* c0l = key_terms + Np;
-  const int bm = blockIdx.z, b = bm / mult;
+  const int bm = blockIdx.z, b = bm / mult, hd = blockIdx.y;
   const int CS = H * DH;
+  const int tid = threadIdx.x;
   const float masked_logit = -1e6f * kLog2e;
-  for (int t = threadIdx.x; t < Np; t += blockDim.x) {
+  for (int t = tid; t < Np; t += blockDim.x) {
     const bool valid = t < N && mask[(size_t)b * N + t] != 0;
     kvl[t] = valid ? 1.f : 0.f;
     c0l[t] = valid ? 0.f : t < N ? masked_logit : -INFINITY;
   }
-  __syncthreads();
+  // zero the padding of both stages once (d 24..31 of K rows, V^T rows 24..31);
+  // the staging below never writes it
+  for (int e = tid; e < 2 * kKvStage; e += blockDim.x) {
+    const int w = e % kKvStage, row = (w % kKvTile) / kKvLd, col = w % kKvLd;
+    const bool is_k = w < kKvTile;
+    if ((is_k && col >= DH) || (!is_k && row >= DH)) kvs[e] = f2bf(0.f);
+  }
 
-  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 31, hh = lane >> 5;
-  const int hd = blockIdx.y * 4 + wave;
-  if (hd >= H) return;  // after the only barrier
-  const int q0 = blockIdx.x * 32;
+  const int q0 = blockIdx.x * kFlashQ + 32 * wave;
+  const bool active = q0 < Np;   // idle waves stage tiles and meet every barrier
+  const int qr = active ? q0 + n : n;
 
   bf16x8 zero8;
 #pragma unroll
   for (int t = 0; t < 8; ++t) zero8[t] = f2bf(0.f);
-
-  const bf16* qrow = q + ((size_t)bm * Np + q0 + n) * CS + hd * DH;
+  const bf16* qrow = q + ((size_t)bm * Np + qr) * CS + hd * DH;
   const bf16x8 qf0 = load8(qrow + 8 * hh);
   const bf16x8 qf1 = hh == 0 ? load8(qrow + 16) : zero8;
 
+  // Staging: thread tid < 96 moves K chunk (key tid / 3, d 8 (tid % 3)),
+  // 96 <= tid < 192 V^T chunk (d (tid - 96) / 4, keys 8 ((tid - 96) % 4)).
+  const bool stager = tid < kKvChunks;
+  const bool kpart = tid < 96;
+  const int srow = kpart ? tid / 3 : (tid - 96) / 4, spart = kpart ? tid % 3 : (tid - 96) % 4;
+  const bf16* ksrc = k + ((size_t)bm * Np + srow) * CS + hd * DH + 8 * spart;
+  const bf16* vsrc = vt + ((size_t)bm * CS + hd * DH + srow) * Np + 8 * spart;
+  const int sdst = (kpart ? 0 : kKvTile) + srow * kKvLd + 8 * spart;
+  bf16x8 sreg = zero8;
+  auto gload = [&](int kb) {
+    if (stager) sreg = kpart ? load8(ksrc + (size_t)kb * CS) : load8(vsrc + kb);
+  };
+  auto lstore = [&](int st) {
+    if (stager) store8(kvs + st * kKvStage + sdst, sreg);
+  };
+  const bf16* brow = bias + (((size_t)b * H + hd) * Np + qr) * Np + 16 * hh;
+  bf16x8 bc0 = load8(brow), bc1 = load8(brow + 8);   // bias of the block being consumed
+
+  gload(0);
+  lstore(0);
+  __syncthreads();
+
   f32x16 o = zero16();
   float m = -INFINITY, l = 0.f;
-  const bf16* kbase = k + (size_t)bm * Np * CS + hd * DH;
-  const int dslot = perm32(n);
-  const bf16* vbase = vt + ((size_t)bm * CS + hd * DH + (dslot < DH ? dslot : 0)) * Np;
-  const bf16* brow = bias + (((size_t)b * H + hd) * Np + q0 + n) * Np;
-
-  // Operands of one 32-key block: K fragments, the bias row slice and the V^T
-  // fragments.  The next block's are requested before the current block is
-  // consumed, so each block's global-memory latency hides behind the previous
-  // block's work.
-  const bool dvalid = dslot < DH;
-  struct Frag {
-    bf16x8 k0, k1, b0, b1, v0, v1;
-  };
-  auto fetch = [&](int kb) {
-    Frag f;
-    const bf16* kr = kbase + (size_t)(kb + perm32(n)) * CS;
-    // every address is valid (vbase is clamped to a real d row); lanes whose
-    // fragment is zero (k1 of hh = 1, V of d >= 24) select it at use, so that
-    // no load sits in a branch
-    f.k0 = load8(kr + 8 * hh);
-    f.k1 = load8(kr + 16);
-    f.b0 = load8(brow + kb + 16 * hh);
-    f.b1 = load8(brow + kb + 16 * hh + 8);
-    const bf16* vp = vbase + kb + 16 * hh;
-    f.v0 = load8(vp);
-    f.v1 = load8(vp + 8);
-    return f;
-  };
-  // Two fixed fragment sets used alternately (the loop is unrolled by two):
-  // a copy between them would make the compiler wait for the new loads.
-  auto consume = [&](const Frag& f, int k0) {
+  const int kslot = perm32(n);   // K row / V^T row (d) of this lane's MFMA operand
+  int st = 0;
+  for (int k0 = 0; k0 < Np; k0 += 32) {
+    const int kn = k0 + 32 < Np ? k0 + 32 : k0;   // the last block refetches itself
+    gload(kn);
+    const bf16x8 bn0 = load8(brow + kn), bn1 = load8(brow + kn + 8);
+    const bf16* ks = kvs + st * kKvStage;
+    const bf16* vs = ks + kKvTile;
     f32x16 s = zero16();
-    s = mfma32(f.k0, qf0, s);
-    s = mfma32(hh == 0 ? f.k1 : zero8, qf1, s);
-    const bf16x8 b0 = f.b0, b1 = f.b1;
+    s = mfma32(load8(ks + kslot * kKvLd + 8 * hh), qf0, s);
+    s = mfma32(load8(ks + kslot * kKvLd + 16 + 8 * hh), qf1, s);
     const float4* kv4 = reinterpret_cast<const float4*>(kvl + k0 + 16 * hh);
     const float4* c04 = reinterpret_cast<const float4*>(c0l + k0 + 16 * hh);
     float kv[16], c0[16];
@@ -197,7 +209,7 @@ __global__ __launch_bounds__(256) void apb_flash_kernel(const bf16* __restrict__
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
       // q carries log2(e)/sqrt(d) and the bias log2(e): s + bias is the logit in log2 units
-      const float x = __builtin_fmaf(s[u] + bf2f(u < 8 ? b0[u] : b1[u - 8]), kv[u], c0[u]);
+      const float x = __builtin_fmaf(s[u] + bf2f(u < 8 ? bc0[u] : bc1[u - 8]), kv[u], c0[u]);
       t[u] = x;
       bmax = fmaxf(bmax, x);
     }
@@ -216,17 +228,15 @@ __global__ __launch_bounds__(256) void apb_flash_kernel(const bf16* __restrict__
     l = l * alpha + psum;
 #pragma unroll
     for (int u = 0; u < 16; ++u) o[u] *= alpha;
-    o = mfma32(dvalid ? f.v0 : zero8, pb[0], o);
-    o = mfma32(dvalid ? f.v1 : zero8, pb[1], o);
-  };
-  Frag fa = fetch(0), fb;
-  for (int k0 = 0; k0 < Np; k0 += 64) {
-    fb = fetch(k0 + 32 < Np ? k0 + 32 : k0);   // the last block refetches itself
-    consume(fa, k0);
-    if (k0 + 32 >= Np) break;
-    fa = fetch(k0 + 64 < Np ? k0 + 64 : k0 + 32);
-    consume(fb, k0 + 32);
+    o = mfma32(load8(vs + kslot * kKvLd + 16 * hh), pb[0], o);
+    o = mfma32(load8(vs + kslot * kKvLd + 16 * hh + 8), pb[1], o);
+    bc0 = bn0;
+    bc1 = bn1;
+    lstore(st ^ 1);
+    st ^= 1;
+    __syncthreads();
   }
+  if (!active) return;
 
   const float inv = 1.0f / (l + __shfl_xor(l, 32));
   const size_t off = ((size_t)bm * Np + q0 + n) * CS + hd * DH + 16 * hh;
@@ -416,7 +426,7 @@ extern "C" int bioemu_apb_fwd(const void* s, const void* z, const uint8_t* mask,
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)key_lds) != hipSuccess)
       return set_error(BIOEMU_ERR_LAUNCH, "apb_flash: cannot set dynamic LDS size");
     KernelTimerScope timed("apb_flash", stream);
-    hipLaunchKernelGGL(apb_flash_kernel, dim3((unsigned)(Np / 32), (unsigned)((H + 3) / 4), (unsigned)BM), dim3(256),
+    hipLaunchKernelGGL(apb_flash_kernel, dim3((unsigned)((Np + kFlashQ - 1) / kFlashQ), (unsigned)H, (unsigned)BM), dim3(256),
                        key_lds, stream, buf.q, buf.k, buf.vt, buf.g, buf.bias, mask, buf.go, (int)N, (int)Np, (int)H,
                        (int)mult);
   }
