@@ -17,7 +17,6 @@
 #include <algorithm>
 
 #include "common.h"
-#include "gemm_nt.h"
 #include "internal.h"
 #include "pairtile.h"
 
@@ -258,67 +257,6 @@ __global__ __launch_bounds__(256) void apb_flash_kernel(const bf16* __restrict__
   }
 }
 
-// ---------------------------------------------------------------------------
-// q | k | v^T | g in one launch: 256 x 256 tiles of LN(s)[M][c_s] times
-// [Wq; Wk; Wv; Wg]^T ([4 c_s][c_s], weights staged through LDS by the tile loop
-// of gemm_nt.h; tile rows past M read as zero and are not stored).  The output
-// is picked per 32-column block: q ((+ q_bias) * log2(e) / sqrt(d), the
-// attention's softmax scale in base 2), k and g (sigmoid) row-major
-// [M][c_s]; v transposed, [B * mult][c_s][Np] (the attention reads V^T).  Lane
-// (ln, lh) of block (ib, jb) holds token row wi*64 + ib*32 + ln and 16
-// consecutive output columns (gemm_nt.h).
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kNtThreads) void apb_qkvg_kernel(const bf16* __restrict__ sn,
-                                                              const bf16* __restrict__ wqkv,
-                                                              const bf16* __restrict__ wg,
-                                                              const float* __restrict__ q_bias, bf16* __restrict__ q,
-                                                              bf16* __restrict__ k, bf16* __restrict__ vt,
-                                                              bf16* __restrict__ g, int M, int CS, int Np) {
-  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
-  bf16* smem = reinterpret_cast<bf16*>(smem_raw);
-  const int ntj = 4 * CS / kNtTile;
-  const int ti = blockIdx.x / ntj, tj = blockIdx.x % ntj;
-  const int row0 = ti * kNtTile, col0 = tj * kNtTile;
-  // weight rows col0 .. col0 + 255: [0, 3 c_s) are wqkv's, [3 c_s, 4 c_s) wg's
-  const int split = min(max(3 * CS - col0, 0), kNtTile);
-  const bf16* b1 = wqkv + (size_t)min(col0, 3 * CS) * CS;
-  const bf16* b2 = wg + (size_t)max(col0 - 3 * CS, 0) * CS;
-  f32x16 acc[4][2];
-  gemm_nt_tile(sn + (size_t)row0 * CS, min(M - row0, kNtTile), b1, b2, split, CS, smem, acc);
-
-  const int lane = threadIdx.x & 63, wave = wave_id();
-  const int ln = lane & 31, lh = lane >> 5;
-  const int wi = wave & 3, wj = wave >> 2;
-#pragma unroll
-  for (int jb = 0; jb < 4; ++jb) {
-    const int col = col0 + wj * 128 + jb * 32;   // wave-uniform 32-column block
-    const int which = col / CS, c0 = col % CS + 16 * lh;
-#pragma unroll
-    for (int ib = 0; ib < 2; ++ib) {
-      const int r = row0 + wi * 64 + ib * 32 + ln;
-      if (r >= M) continue;
-      float v[16];
-#pragma unroll
-      for (int u = 0; u < 16; ++u) v[u] = acc[jb][ib][u];
-      if (which == 2) {
-        const int bm = r / Np, t = r % Np;
-        bf16* dst = vt + ((size_t)bm * CS + c0) * Np + t;
-#pragma unroll
-        for (int u = 0; u < 16; ++u) dst[(size_t)u * Np] = f2bf(v[u]);
-        continue;
-      }
-      if (which == 0) {   // q carries the softmax scale in log2 units
-#pragma unroll
-        for (int u = 0; u < 16; ++u) v[u] = (v[u] + q_bias[c0 + u]) * kQScale;
-      } else if (which == 3) {
-#pragma unroll
-        for (int u = 0; u < 16; ++u) v[u] = sigmoidf_fast(v[u]);
-      }
-      store16((which == 0 ? q : which == 1 ? k : g) + (size_t)r * CS + c0, v);
-    }
-  }
-}
-
 struct ApbBuffers {
   bf16 *sn, *q, *k, *vt, *g, *go, *bias, *wf, *cf;
 };
@@ -393,16 +331,9 @@ extern "C" int bioemu_apb_fwd(const void* s, const void* z, const uint8_t* mask,
 
   int rc = token_layernorm(s, norm_s_w, norm_s_b, buf.sn, BM, N, Np, c_s, stream);
   if (rc) return rc;
-  if (hipFuncSetAttribute(reinterpret_cast<const void*>(apb_qkvg_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                          kNtSmem) != hipSuccess)
-    return set_error(BIOEMU_ERR_LAUNCH, "apb_proj_qkvg: cannot set dynamic LDS size");
-  {
-    const long long tiles = (M + kNtTile - 1) / kNtTile * (4 * c_s / kNtTile);
-    KernelTimerScope timed("apb_proj_qkvg", stream);
-    hipLaunchKernelGGL(apb_qkvg_kernel, dim3((unsigned)tiles), dim3(kNtThreads), kNtSmem, stream, buf.sn, wqkv,
-                       static_cast<const bf16*>(w_g), q_bias, buf.q, buf.k, buf.vt, buf.g, (int)M, (int)c_s, (int)Np);
-  }
-  rc = check_launch("apb_proj_qkvg");
+  // q carries the attention's softmax scale in base 2 (apb_flash_kernel)
+  rc = token_qkvg(buf.sn, wqkv, w_g, q_bias, kQScale, buf.q, buf.k, buf.vt, buf.g, M, c_s, Np, stream,
+                  "apb_proj_qkvg");
   if (rc) return rc;
 
   int dev = 0, cus = 0;

@@ -81,5 +81,11 @@ int token_gemm(int epi, bool trans, const void* A, const void* W, const void* W2
                const void* res, void* out, int64_t M, int64_t K, int64_t Nout, int64_t N, int64_t Np,
                int64_t out_rows, hipStream_t stream, const char* name, int8_t* tail = nullptr);
 constexpr int kEpiStoreId = 0, kEpiSigmoidId = 1, kEpiSwiGLUId = 2, kEpiResidualId = 3;
+// q | k | v^T | g = sn [Wq; Wk; Wv; Wg]^T in one launch (w_qkv [3 c_s][c_s], w_g
+// [c_s][c_s]): q = (. + q_bias) * q_scale, g = sigmoid(.), v written
+// transposed per sequence of seq_rows rows; c_s % 64 == 0, M % seq_rows == 0.
+int token_qkvg(const void* sn, const void* wqkv, const void* w_g, const float* q_bias, float q_scale, void* q,
+               void* k, void* vt, void* g, int64_t M, int64_t CS, int64_t seq_rows, hipStream_t stream,
+               const char* name);
 
 }  // namespace bioemu

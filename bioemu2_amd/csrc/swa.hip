@@ -255,14 +255,8 @@ extern "C" int bioemu_swa_fwd(const void* s, const void* z, const uint8_t* mask,
     rc = token_layernorm(s, norm_s_w, norm_s_b, buf.sn, BM, NA, NA, c_s, stream);
     sn = buf.sn;
   }
-  if (!rc) rc = token_gemm(kEpiStoreId, false, sn, wqkv, nullptr, q_bias, nullptr, buf.q, M, c_s, c_s, NA, NA, NA,
-                           stream, "swa_proj_q");
-  if (!rc) rc = token_gemm(kEpiStoreId, false, sn, wqkv + c_s * c_s, nullptr, nullptr, nullptr, buf.k, M, c_s, c_s,
-                           NA, NA, NA, stream, "swa_proj_k");
-  if (!rc) rc = token_gemm(kEpiStoreId, true, sn, wqkv + 2 * c_s * c_s, nullptr, nullptr, nullptr, buf.vt, M, c_s,
-                           c_s, NA, NA, NA, stream, "swa_proj_v");
-  if (!rc) rc = token_gemm(kEpiSigmoidId, false, sn, w_g, nullptr, nullptr, nullptr, buf.g, M, c_s, c_s, NA, NA, NA,
-                           stream, "swa_proj_g");
+  if (!rc) rc = token_qkvg(sn, wqkv, w_g, q_bias, 1.0f, buf.q, buf.k, buf.vt, buf.g, M, c_s, NA, stream,
+                          "swa_proj_qkvg");
   if (rc) return rc;
 
   const long long pairs = B * NW * WQ * H;

@@ -12,6 +12,7 @@
 // [B][N] layout (padded rows are then dropped).  Transposed outputs are laid
 // out [B][Nout][Np].
 #include "common.h"
+#include "gemm_nt.h"
 #include "internal.h"
 #include "pairtile.h"
 
@@ -231,6 +232,68 @@ __global__ __launch_bounds__(64 * kSplitK) void token_gemm_kernel(const bf16* __
   }
 }
 
+// ---------------------------------------------------------------------------
+// q | k | v^T | g of an attention in one launch: 256 x 256 tiles of
+// sn[M][c_s] times [Wq; Wk; Wv; Wg]^T ([4 c_s][c_s], weights staged through
+// LDS by the tile loop of gemm_nt.h; tile rows past M read as zero and are not
+// stored).  The output is picked per 32-column block: q ((+ q_bias) * q_scale),
+// k and g (sigmoid) row-major [M][c_s]; v transposed per sequence of
+// seq_rows rows, [M / seq_rows][c_s][seq_rows] (row r = sequence r / seq_rows,
+// position r % seq_rows).  Lane (ln, lh) of block (ib, jb) holds row
+// wi*64 + ib*32 + ln and 16 consecutive output columns (gemm_nt.h).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kNtThreads) void token_qkvg_kernel(const bf16* __restrict__ sn,
+                                                                const bf16* __restrict__ wqkv,
+                                                                const bf16* __restrict__ wg,
+                                                                const float* __restrict__ q_bias, float q_scale,
+                                                                bf16* __restrict__ q, bf16* __restrict__ k,
+                                                                bf16* __restrict__ vt, bf16* __restrict__ g, int M,
+                                                                int CS, int seq_rows) {
+  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+  bf16* smem = reinterpret_cast<bf16*>(smem_raw);
+  const int ntj = 4 * CS / kNtTile;
+  const int ti = blockIdx.x / ntj, tj = blockIdx.x % ntj;
+  const int row0 = ti * kNtTile, col0 = tj * kNtTile;
+  // weight rows col0 .. col0 + 255: [0, 3 c_s) are wqkv's, [3 c_s, 4 c_s) wg's
+  const int split = min(max(3 * CS - col0, 0), kNtTile);
+  const bf16* b1 = wqkv + (size_t)min(col0, 3 * CS) * CS;
+  const bf16* b2 = wg + (size_t)max(col0 - 3 * CS, 0) * CS;
+  f32x16 acc[4][2];
+  gemm_nt_tile(sn + (size_t)row0 * CS, min(M - row0, kNtTile), b1, b2, split, CS, smem, acc);
+
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int ln = lane & 31, lh = lane >> 5;
+  const int wi = wave & 3, wj = wave >> 2;
+#pragma unroll
+  for (int jb = 0; jb < 4; ++jb) {
+    const int col = col0 + wj * 128 + jb * 32;   // wave-uniform 32-column block
+    const int which = col / CS, c0 = col % CS + 16 * lh;
+#pragma unroll
+    for (int ib = 0; ib < 2; ++ib) {
+      const int r = row0 + wi * 64 + ib * 32 + ln;
+      if (r >= M) continue;
+      float v[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) v[u] = acc[jb][ib][u];
+      if (which == 2) {
+        const int sq = r / seq_rows, t = r % seq_rows;
+        bf16* dst = vt + ((size_t)sq * CS + c0) * seq_rows + t;
+#pragma unroll
+        for (int u = 0; u < 16; ++u) dst[(size_t)u * seq_rows] = f2bf(v[u]);
+        continue;
+      }
+      if (which == 0) {
+#pragma unroll
+        for (int u = 0; u < 16; ++u) v[u] = (v[u] + q_bias[c0 + u]) * q_scale;
+      } else if (which == 3) {
+#pragma unroll
+        for (int u = 0; u < 16; ++u) v[u] = sigmoidf_fast(v[u]);
+      }
+      store16((which == 0 ? q : which == 1 ? k : g) + (size_t)r * CS + c0, v);
+    }
+  }
+}
+
 template <int kEpi, bool kTrans>
 int launch_gemm(const void* A, const void* W, const void* W2, const float* col_bias, const void* res, void* out,
                 int8_t* tail, int64_t M, int64_t K, int64_t Nout, int64_t N, int64_t Np, int64_t out_rows,
@@ -298,6 +361,26 @@ int token_gemm(int epi, bool trans, const void* A, const void* W, const void* W2
     default:
       return set_error(BIOEMU_ERR_INVALID_ARG, "%s: unknown epilogue %d", name, epi);
   }
+}
+
+
+int token_qkvg(const void* sn, const void* wqkv, const void* w_g, const float* q_bias, float q_scale, void* q,
+               void* k, void* vt, void* g, int64_t M, int64_t CS, int64_t seq_rows, hipStream_t stream,
+               const char* name) {
+  if (M <= 0 || CS <= 0 || CS % 64 || seq_rows <= 0 || M % seq_rows || M > 0x7fffffffLL ||
+      (long long)kNtTile * CS * 2 > 0xffffffffLL)
+    return set_error(BIOEMU_ERR_INVALID_ARG, "%s: bad shape M=%lld c_s=%lld rows per sequence=%lld", name,
+                     (long long)M, (long long)CS, (long long)seq_rows);
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(token_qkvg_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          kNtSmem) != hipSuccess)
+    return set_error(BIOEMU_ERR_LAUNCH, "%s: cannot set dynamic LDS size", name);
+  const long long tiles = (M + kNtTile - 1) / kNtTile * (4 * CS / kNtTile);
+  KernelTimerScope timed(name, stream);
+  hipLaunchKernelGGL(token_qkvg_kernel, dim3((unsigned)tiles), dim3(kNtThreads), kNtSmem, stream,
+                     static_cast<const bf16*>(sn), static_cast<const bf16*>(wqkv), static_cast<const bf16*>(w_g), q_bias,
+                     q_scale, static_cast<bf16*>(q), static_cast<bf16*>(k), static_cast<bf16*>(vt),
+                     static_cast<bf16*>(g), (int)M, (int)CS, (int)seq_rows);
+  return check_launch(name);
 }
 
 }  // namespace bioemu

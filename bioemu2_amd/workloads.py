@@ -813,8 +813,8 @@ class SwaWorkload(Workload):
             return ("hbm", float(5 * tok + bias))
         if kernel == "swa_pair_bias":
             return ("hbm", float(self.nw * 32 * 128 * 16 * 2 + bias))
-        if kernel in ("swa_proj_q", "swa_proj_k", "swa_proj_v", "swa_proj_g"):
-            return ("hbm", float(2 * tok + 128 * 128 * 2))
+        if kernel == "swa_proj_qkvg":   # the four per-atom projections in one launch: read s, write q, k, v^T, g
+            return ("hbm", float(5 * tok + 4 * 128 * 128 * 2))
         if kernel == "swa_proj_o":
             return ("hbm", float(2 * tok + 128 * 128 * 2))
         raise KeyError(kernel)
