@@ -363,6 +363,5 @@ extern "C" int bioemu_apb_fwd(const void* s, const void* z, const uint8_t* mask,
   }
   rc = check_launch("apb_flash");
   if (rc) return rc;
-  return token_gemm(residual ? kEpiResidualId : kEpiStoreId, false, buf.go, w_o, nullptr, nullptr, s, out, M, c_s,
-                    c_s, N, Np, N, stream, "apb_proj_o", res_tail);
+  return token_out_proj(buf.go, w_o, s, out, res_tail, M, c_s, c_s, Np, N, residual != 0, stream, "apb_proj_o");
 }

@@ -84,6 +84,10 @@ constexpr int kEpiStoreId = 0, kEpiSigmoidId = 1, kEpiSwiGLUId = 2, kEpiResidual
 // q | k | v^T | g = sn [Wq; Wk; Wv; Wg]^T in one launch (w_qkv [3 c_s][c_s], w_g
 // [c_s][c_s]): q = (. + q_bias) * q_scale, g = sigmoid(.), v written
 // transposed per sequence of seq_rows rows; c_s % 64 == 0, M % seq_rows == 0.
+// out = A W^T (+ res, with an optional int8 tail) on LDS-staged 256 x 256 tiles;
+// rows and out_rows as token_gemm; K % 64 == 0, Nout % 32 == 0.
+int token_out_proj(const void* A, const void* W, const void* res, void* out, int8_t* tail, int64_t M, int64_t K,
+                   int64_t Nout, int64_t Np, int64_t out_rows, bool residual, hipStream_t stream, const char* name);
 int token_qkvg(const void* sn, const void* wqkv, const void* w_g, const float* q_bias, float q_scale, void* q,
                void* k, void* vt, void* g, int64_t M, int64_t CS, int64_t seq_rows, hipStream_t stream,
                const char* name);

@@ -279,6 +279,5 @@ extern "C" int bioemu_swa_fwd(const void* s, const void* z, const uint8_t* mask,
   }
   rc = check_launch("swa_attn");
   if (rc) return rc;
-  return token_gemm(residual ? kEpiResidualId : kEpiStoreId, false, buf.go, w_o, nullptr, nullptr, s, out, M, c_s,
-                    c_s, NA, NA, NA, stream, "swa_proj_o");
+  return token_out_proj(buf.go, w_o, s, out, nullptr, M, c_s, c_s, NA, NA, residual != 0, stream, "swa_proj_o");
 }

@@ -294,6 +294,66 @@ __global__ __launch_bounds__(kNtThreads) void token_qkvg_kernel(const bf16* __re
   }
 }
 
+// ---------------------------------------------------------------------------
+// out = A[M][K] W[Nout][K]^T (+ res) on 256 x 256 tiles (gemm_nt.h tile loop,
+// operands staged through LDS; rows past M read as zero, columns past Nout
+// are computed on repeated weight rows and not stored).  Rows are batches of
+// Np padded rows; with out_rows < Np the output / residual use the compact
+// [B][out_rows] layout and padded rows are dropped (as token_gemm_kernel).
+// With a tail (kTail) the residual stream carries int8 tails, in place.
+// ---------------------------------------------------------------------------
+template <bool kResidual, bool kTail>
+__global__ __launch_bounds__(kNtThreads) void token_out_kernel(const bf16* __restrict__ A, const bf16* __restrict__ W,
+                                                               const bf16* res, bf16* out, int8_t* tail, int M, int K,
+                                                               int Nout, int Np, int out_rows) {
+  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+  bf16* smem = reinterpret_cast<bf16*>(smem_raw);
+  const int ntj = (Nout + kNtTile - 1) / kNtTile;
+  const int ti = blockIdx.x / ntj, tj = blockIdx.x % ntj;
+  const int row0 = ti * kNtTile, col0 = tj * kNtTile;
+  const int valid_cols = min(Nout - col0, kNtTile);   // a multiple of 32
+  f32x16 acc[4][2];
+  gemm_nt_tile(A + (size_t)row0 * K, min(M - row0, kNtTile), W + (size_t)col0 * K, W, valid_cols, K, smem, acc);
+
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int ln = lane & 31, lh = lane >> 5;
+  const int wi = wave & 3, wj = wave >> 2;
+#pragma unroll
+  for (int jb = 0; jb < 4; ++jb) {
+    const int cl = wj * 128 + jb * 32;   // wave-uniform 32-column block of the tile
+    if (cl >= valid_cols) continue;
+    const int c0 = col0 + cl + 16 * lh;
+#pragma unroll
+    for (int ib = 0; ib < 2; ++ib) {
+      const int r = row0 + wi * 64 + ib * 32 + ln;
+      if (r >= M) continue;
+      const int b = r / Np, t = r % Np;
+      if (t >= out_rows) continue;
+      const size_t off = ((size_t)b * out_rows + t) * Nout + c0;
+      float v[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) v[u] = acc[jb][ib][u];
+      if (kTail) {
+        float rv[16];
+        tail_decode16(load8(res + off), load8(res + off + 8), load_tail16(tail + off), rv);
+#pragma unroll
+        for (int u = 0; u < 16; ++u) v[u] += rv[u];
+        tail_store16(out + off, tail + off, v);
+        continue;
+      }
+      if (kResidual) {
+        const bf16x8 r0 = load8(res + off), r1 = load8(res + off + 8);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          v[u] += bf2f(r0[u]);
+          v[8 + u] += bf2f(r1[u]);
+        }
+      }
+      store16(out + off, v);
+    }
+  }
+}
+
 template <int kEpi, bool kTrans>
 int launch_gemm(const void* A, const void* W, const void* W2, const float* col_bias, const void* res, void* out,
                 int8_t* tail, int64_t M, int64_t K, int64_t Nout, int64_t N, int64_t Np, int64_t out_rows,
@@ -380,6 +440,46 @@ int token_qkvg(const void* sn, const void* wqkv, const void* w_g, const float* q
                      static_cast<const bf16*>(sn), static_cast<const bf16*>(wqkv), static_cast<const bf16*>(w_g), q_bias,
                      q_scale, static_cast<bf16*>(q), static_cast<bf16*>(k), static_cast<bf16*>(vt),
                      static_cast<bf16*>(g), (int)M, (int)CS, (int)seq_rows);
+  return check_launch(name);
+}
+
+
+constexpr long long kTiledMinOutputs = 2000000;
+
+int token_out_proj(const void* A, const void* W, const void* res, void* out, int8_t* tail, int64_t M, int64_t K,
+                   int64_t Nout, int64_t Np, int64_t out_rows, bool residual, hipStream_t stream, const char* name) {
+  if (M <= 0 || K <= 0 || K % 64 || Nout <= 0 || Nout % 32 || Np <= 0 || Np % 32 || M % Np || out_rows > Np ||
+      M > 0x7fffffffLL || (long long)kNtTile * K * 2 > 0xffffffffLL)
+    return set_error(BIOEMU_ERR_INVALID_ARG, "%s: bad shape M=%lld K=%lld Nout=%lld Np=%lld", name, (long long)M,
+                     (long long)K, (long long)Nout, (long long)Np);
+  if (tail && !residual) return set_error(BIOEMU_ERR_INVALID_ARG, "%s: a residual tail needs residual=1", name);
+  // A 256 x 256 tile takes about as long as the per-block GEMM needs for ~2M
+  // outputs (measured: 0.016 vs 0.020 ms at M = 6144, c_s = 384; 0.018 vs
+  // 0.015 ms at M = 4096; slower still at M = 768): fewer outputs take the
+  // per-block kernel.
+  if (M * Nout < kTiledMinOutputs)
+    return token_gemm(residual ? kEpiResidualId : kEpiStoreId, false, A, W, nullptr, nullptr, res, out, M, K, Nout,
+                      out_rows, Np, out_rows, stream, name, tail);
+  const void* k = tail ? reinterpret_cast<const void*>(token_out_kernel<true, true>)
+                       : residual ? reinterpret_cast<const void*>(token_out_kernel<true, false>)
+                                  : reinterpret_cast<const void*>(token_out_kernel<false, false>);
+  if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, kNtSmem) != hipSuccess)
+    return set_error(BIOEMU_ERR_LAUNCH, "%s: cannot set dynamic LDS size", name);
+  const long long tiles = (M + kNtTile - 1) / kNtTile * ((Nout + kNtTile - 1) / kNtTile);
+  KernelTimerScope timed(name, stream);
+  const bf16* a = static_cast<const bf16*>(A);
+  const bf16* w = static_cast<const bf16*>(W);
+  const bf16* r = static_cast<const bf16*>(res);
+  bf16* o = static_cast<bf16*>(out);
+  if (tail)
+    hipLaunchKernelGGL((token_out_kernel<true, true>), dim3((unsigned)tiles), dim3(kNtThreads), kNtSmem, stream, a, w,
+                       r, o, tail, (int)M, (int)K, (int)Nout, (int)Np, (int)out_rows);
+  else if (residual)
+    hipLaunchKernelGGL((token_out_kernel<true, false>), dim3((unsigned)tiles), dim3(kNtThreads), kNtSmem, stream, a,
+                       w, r, o, nullptr, (int)M, (int)K, (int)Nout, (int)Np, (int)out_rows);
+  else
+    hipLaunchKernelGGL((token_out_kernel<false, false>), dim3((unsigned)tiles), dim3(kNtThreads), kNtSmem, stream, a,
+                       w, r, o, nullptr, (int)M, (int)K, (int)Nout, (int)Np, (int)out_rows);
   return check_launch(name);
 }
 
