@@ -34,7 +34,7 @@ constexpr int WQ = 32;   // queries per window
 constexpr int kMaxHeads = 12;   // c_s = 32 heads in {64, 128, 384}
 
 // ---------------------------------------------------------------------------
-// bias[b][w][h][i][j] = LN_z(z[b][w][i][j]) . Wz[h]; one thread per pair
+// bias[b][w][h][i][j] = log2(e) * LN_z(z[b][w][i][j]) . Wz[h]; one thread per pair
 // (consecutive lanes = consecutive keys: coalesced 32-byte reads, and each
 // head's 2-byte stores of a wave form one 128-byte run).
 // ---------------------------------------------------------------------------
@@ -77,7 +77,7 @@ __global__ __launch_bounds__(256) void swa_bias_kernel(const bf16* __restrict__ 
     float acc = 0.f;
 #pragma unroll
     for (int c = 0; c < CZ; ++c) acc += v[c] * wl[h * CZ + c];
-    bias[(((size_t)bw * HEADS + h) * WQ + i) * HK + j] = f2bf(acc);
+    bias[(((size_t)bw * HEADS + h) * WQ + i) * HK + j] = f2bf(acc * kLog2e);   // log2 units (base-2 softmax)
   }
 }
 
@@ -98,22 +98,41 @@ void launch_swa_bias(int heads, const bf16* z, const float* gamma, const float* 
 
 // ---------------------------------------------------------------------------
 // Attention.  Block = (window w, 4 heads, copy bm); wave -> head 4 blockIdx.y + wave.
+// q arrives pre-scaled by log2(e)/sqrt(d) and the bias in log2 units, so
+// q.k + bias is the logit in base 2.  Per window key j (atom kstart + j) the
+// workgroup keeps in LDS kv[j] = 1, c0[j] = 0 for a valid key and kv = 0,
+// c0 = -1e6 log2(e) for a masked one or one outside the sequence (the
+// reference's replacement): x = kv (q.k + bias) + c0.  Key blocks are read
+// kChunk at a time, every operand of a chunk requested before its first use;
+// addresses of keys outside the sequence are clamped to atom 0 (their logit is
+// replaced, and their V is selected as zero, so the values read do not matter).
 // ---------------------------------------------------------------------------
+constexpr int kChunk = 2;   // 32-key blocks whose operands are fetched together
+
 __global__ __launch_bounds__(256) void swa_attn_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
                                                        const bf16* __restrict__ vt, const bf16* __restrict__ g,
                                                        const bf16* __restrict__ bias,
                                                        const uint8_t* __restrict__ mask, bf16* __restrict__ go,
                                                        int NW, int HK, int heads, int mult) {
+  extern __shared__ __attribute__((aligned(16))) float key_terms[];   // kv[HK] then c0[HK]
+  float* kvl = key_terms;
+  float* c0l = key_terms + HK;
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int n = lane & 31, hh = lane >> 5;
-  const int hd = blockIdx.y * 4 + wave;
-  if (hd >= heads) return;
   const int w = blockIdx.x, bm = blockIdx.z, b = bm / mult;
-  const int CS = heads * DH;
   const int NA = NW * WQ;
   const int kstart = w * WQ - (HK - WQ) / 2;
-  const float qk_scale = kLog2e / sqrtf((float)DH);
   const float masked_logit = -1e6f * kLog2e;
+  for (int j = threadIdx.x; j < HK; j += blockDim.x) {
+    const int kp = kstart + j;
+    const bool valid = kp >= 0 && kp < NA && mask[(size_t)b * NA + kp] != 0;
+    kvl[j] = valid ? 1.f : 0.f;
+    c0l[j] = valid ? 0.f : masked_logit;
+  }
+  __syncthreads();
+  const int hd = blockIdx.y * 4 + wave;
+  if (hd >= heads) return;   // after the only barrier
+  const int CS = heads * DH;
 
   bf16x8 zero8;
 #pragma unroll
@@ -125,54 +144,73 @@ __global__ __launch_bounds__(256) void swa_attn_kernel(const bf16* __restrict__ 
   const bf16* kbase = k + (size_t)bm * NA * CS + hd * DH;
   const bf16* vbase = vt + ((size_t)bm * CS + hd * DH + perm32(n)) * NA;
   const bf16* brow = bias + ((((size_t)b * NW + w) * heads + hd) * WQ + n) * HK;
-  const uint8_t* mrow = mask + (size_t)b * NA;
 
   f32x16 o = zero16();
   float m = -INFINITY, l = 0.f;
-  for (int kb = 0; kb < HK; kb += 32) {
-    // S^T: lane (n, hh) register u <-> window key kb + 16 hh + u of query n
-    const int krow = kstart + kb + perm32(n);
-    const bool kin = krow >= 0 && krow < NA;
-    const bf16* kr = kbase + (size_t)(kin ? krow : 0) * CS;
-    f32x16 s = zero16();
-    s = mfma32(kin ? load8(kr + 8 * hh) : zero8, qf0, s);
-    s = mfma32(kin ? load8(kr + 16 + 8 * hh) : zero8, qf1, s);
-    // this lane's 16 keys are one run of atoms, entirely inside or outside the sequence
-    const int kp = kstart + kb + 16 * hh;
-    const bool run_in = kp >= 0 && kp < NA;
-    uint4 mk = make_uint4(0u, 0u, 0u, 0u);
-    if (run_in) mk = *reinterpret_cast<const uint4*>(mrow + kp);
-    const uint32_t mw[4] = {mk.x, mk.y, mk.z, mk.w};
-    const bf16x8 b0 = load8(brow + kb + 16 * hh), b1 = load8(brow + kb + 16 * hh + 8);
-    float t[16];
-    float bmax = -INFINITY;
+  for (int kc = 0; kc < HK; kc += 32 * kChunk) {
+    // operands of the chunk's blocks (a block past HK repeats the last one and is skipped)
+    bf16x8 kf[kChunk][2], vf[kChunk][2], bf[kChunk][2];
+    bool run_in[kChunk];
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      const float bv = bf2f(u < 8 ? b0[u] : b1[u - 8]);
-      float x = s[u] * qk_scale + bv * kLog2e;
-      if (((mw[u >> 2] >> (8 * (u & 3))) & 0xff) == 0) x = masked_logit;
-      t[u] = x;
-      bmax = fmaxf(bmax, x);
+    for (int c = 0; c < kChunk; ++c) {
+      const int kb = min(kc + 32 * c, HK - 32);
+      const int krow = kstart + kb + perm32(n);
+      const bf16* kr = kbase + (size_t)(krow >= 0 && krow < NA ? krow : 0) * CS;
+      kf[c][0] = load8(kr + 8 * hh);
+      kf[c][1] = load8(kr + 16 + 8 * hh);
+      // this lane's 16 keys are one run of atoms, entirely inside or outside the sequence
+      const int kp = kstart + kb + 16 * hh;
+      run_in[c] = kp >= 0 && kp < NA;
+      const bf16* vp = vbase + (run_in[c] ? kp : 0);
+      vf[c][0] = load8(vp);
+      vf[c][1] = load8(vp + 8);
+      bf[c][0] = load8(brow + kb + 16 * hh);
+      bf[c][1] = load8(brow + kb + 16 * hh + 8);
     }
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
-    const float m_new = fmaxf(m, bmax);
-    const float alpha = fast_exp2(m - m_new);
-    m = m_new;
-    float psum = 0.f;
-    bf16x8 pb[2];
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      const float p = fast_exp2(t[u] - m_new);
-      psum += p;
-      pb[u >> 3][u & 7] = f2bf(p);
+    for (int c = 0; c < kChunk; ++c) {
+      const int kb = kc + 32 * c;
+      if (kb >= HK) break;   // uniform
+      // S^T: lane (n, hh) register u <-> window key kb + 16 hh + u of query n
+      f32x16 s = zero16();
+      s = mfma32(kf[c][0], qf0, s);
+      s = mfma32(kf[c][1], qf1, s);
+      const float4* kv4 = reinterpret_cast<const float4*>(kvl + kb + 16 * hh);
+      const float4* c04 = reinterpret_cast<const float4*>(c0l + kb + 16 * hh);
+      float kv[16], c0[16];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float4 a = kv4[e], cc = c04[e];
+        kv[4 * e] = a.x, kv[4 * e + 1] = a.y, kv[4 * e + 2] = a.z, kv[4 * e + 3] = a.w;
+        c0[4 * e] = cc.x, c0[4 * e + 1] = cc.y, c0[4 * e + 2] = cc.z, c0[4 * e + 3] = cc.w;
+      }
+      float t[16];
+      float bmax = -INFINITY;
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const float x = __builtin_fmaf(s[u] + bf2f(u < 8 ? bf[c][0][u] : bf[c][1][u - 8]), kv[u], c0[u]);
+        t[u] = x;
+        bmax = fmaxf(bmax, x);
+      }
+      bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+      const float m_new = fmaxf(m, bmax);
+      const float alpha = fast_exp2(m - m_new);
+      m = m_new;
+      float psum = 0.f;
+      bf16x8 pb[2];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const float p = fast_exp2(t[u] - m_new);
+        psum += p;
+        pb[u >> 3][u & 7] = f2bf(p);
+      }
+      l = l * alpha + psum;
+#pragma unroll
+      for (int u = 0; u < 16; ++u) o[u] *= alpha;
+      // O^T += V^T P^T: lane (d slot, hh) supplies v^T[d][kp .. kp + 15] (zero outside)
+      o = mfma32(run_in[c] ? vf[c][0] : zero8, pb[0], o);
+      o = mfma32(run_in[c] ? vf[c][1] : zero8, pb[1], o);
     }
-    l = l * alpha + psum;
-#pragma unroll
-    for (int u = 0; u < 16; ++u) o[u] *= alpha;
-    // O^T += V^T P^T: lane (d slot, hh) supplies v^T[d][kp .. kp + 15] (zero outside)
-    const bf16* vp = vbase + (run_in ? kp : 0);
-    o = mfma32(run_in ? load8(vp) : zero8, pb[0], o);
-    o = mfma32(run_in ? load8(vp + 8) : zero8, pb[1], o);
   }
 
   // D lane (n, hh) register u <-> channel 16 hh + u of query n
@@ -221,10 +259,10 @@ extern "C" int bioemu_swa_fwd(const void* s, const void* z, const uint8_t* mask,
                               void* out, void* workspace, size_t workspace_bytes, int64_t B, int64_t mult,
                               int64_t NW, int64_t W, int64_t H, int64_t c_s, int64_t c_z, int64_t heads,
                               int residual, hipStream_t stream) {
-  if (W != WQ || H < WQ || H % 32 || (H - W) % 32 || heads <= 0 || heads > kMaxHeads || c_s != heads * DH ||
+  if (W != WQ || H < WQ || H > 16384 || H % 32 || (H - W) % 32 || heads <= 0 || heads > kMaxHeads || c_s != heads * DH ||
       (heads != 2 && heads != 4 && heads != 12) || (c_z != 16 && c_z != 32))
     return set_error(BIOEMU_ERR_UNSUPPORTED,
-                     "swa: supported shapes are W=32, H a multiple of 32 with H-W a multiple of 32, head dim 32 "
+                     "swa: supported shapes are W=32, H <= 16384 a multiple of 32 with H-W a multiple of 32, head dim 32 "
                      "with c_s in {64, 128, 384}, c_z in {16, 32} (got W=%lld H=%lld c_s=%lld heads=%lld c_z=%lld)",
                      (long long)W, (long long)H, (long long)c_s, (long long)heads, (long long)c_z);
   if (B <= 0 || mult <= 0 || NW <= 0 || B * mult > 65535 || NW > 65535 || NW * WQ * c_s > (1LL << 30))
@@ -255,8 +293,9 @@ extern "C" int bioemu_swa_fwd(const void* s, const void* z, const uint8_t* mask,
     rc = token_layernorm(s, norm_s_w, norm_s_b, buf.sn, BM, NA, NA, c_s, stream);
     sn = buf.sn;
   }
-  if (!rc) rc = token_qkvg(sn, wqkv, w_g, q_bias, 1.0f, buf.q, buf.k, buf.vt, buf.g, M, c_s, NA, stream,
-                          "swa_proj_qkvg");
+  // q carries the attention's softmax scale in base 2 (swa_attn_kernel)
+  if (!rc) rc = token_qkvg(sn, wqkv, w_g, q_bias, 0.17677669529663687f * kLog2e, buf.q, buf.k, buf.vt, buf.g, M, c_s,
+                          NA, stream, "swa_proj_qkvg");
   if (rc) return rc;
 
   const long long pairs = B * NW * WQ * H;
@@ -272,10 +311,14 @@ extern "C" int bioemu_swa_fwd(const void* s, const void* z, const uint8_t* mask,
   rc = check_launch("swa_pair_bias");
   if (rc) return rc;
   {
+    const size_t key_lds = (size_t)2 * H * sizeof(float);
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(swa_attn_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)key_lds) != hipSuccess)
+      return set_error(BIOEMU_ERR_LAUNCH, "swa_attn: cannot set dynamic LDS size");
     KernelTimerScope timed("swa_attn", stream);
-    hipLaunchKernelGGL(swa_attn_kernel, dim3((unsigned)NW, (unsigned)((heads + 3) / 4), (unsigned)BM), dim3(256), 0,
-                       stream, buf.q, buf.k, buf.vt, buf.g, buf.bias, mask, buf.go, (int)NW, (int)H, (int)heads,
-                       (int)mult);
+    hipLaunchKernelGGL(swa_attn_kernel, dim3((unsigned)NW, (unsigned)((heads + 3) / 4), (unsigned)BM), dim3(256),
+                       key_lds, stream, buf.q, buf.k, buf.vt, buf.g, buf.bias, mask, buf.go, (int)NW, (int)H,
+                       (int)heads, (int)mult);
   }
   rc = check_launch("swa_attn");
   if (rc) return rc;
