@@ -17,15 +17,19 @@
 //   opm_proj  : LN + proj_ab on MFMA; masked entries are zeroed *before* the
 //               bias-free projection (0 * W = 0 exactly, the same as
 //               masked_fill after it).  Writes aT[b][n][c][r], bT[b][n][d][r]
-//               with the compacted row r contiguous (zero for r >= count).
-//   opm_fused : one workgroup per (b, 8 i, 8 j) pair tile.  X^T[(j,d),(i,c)] =
-//               sum_r bT[(j,d)][r] aT[(i,c)][r] (256 x 256 MFMA tile over the
-//               valid rows, operands double-buffered through LDS), times
-//               1/num_valid, cast to bf16 into LDS as [pair][c*32+d], then
-//               out^T = Wo * X^T + bias (+ z) from LDS on MFMA.
+//               with the compacted row r contiguous (zero for r >= count,
+//               rows padded to Sp = S rounded up to 64).
+//   opm_fused : one workgroup per (b, 8 i, 8 j) pair tile.  X[(i,c),(j,d)] =
+//               sum_r aT[(i,c)][r] bT[(j,d)][r] as one 256 x 256 tile of the
+//               NT tile loop (gemm_nt.h: operands copied straight into LDS in
+//               64-row stages, double-buffered) over the valid rows rounded
+//               up to 64, times 1/num_valid, cast to bf16 into LDS as
+//               [pair][c*32+d], then out^T = Wo * X^T + bias (+ z) from LDS on
+//               MFMA.
 #include <algorithm>
 
 #include "common.h"
+#include "gemm_nt.h"
 #include "internal.h"
 #include "pairtile.h"
 
@@ -165,13 +169,9 @@ __global__ __launch_bounds__(kProjThreads) void opm_proj_kernel(
 // ---------------------------------------------------------------------------
 constexpr int kFusedThreads = 512;
 constexpr int TI = 8, TJ = 8;            // pair tile
-constexpr int TR = 32;                   // rows per K stage
-constexpr int LDK = TR + 8;              // LDS row stride of the operand stages
 constexpr int LDX = CH2 + 8;             // LDS row stride of the mean tile
-constexpr int kStageElems = 2 * 256 * LDK;
-constexpr int kFusedSmemA = 2 * kStageElems * 2;
 constexpr int kFusedSmemB = TI * TJ * LDX * 2;
-constexpr int kFusedSmem = kFusedSmemA > kFusedSmemB ? kFusedSmemA : kFusedSmemB;
+constexpr int kFusedSmem = kNtSmem > kFusedSmemB ? kNtSmem : kFusedSmemB;
 
 __global__ __launch_bounds__(kFusedThreads) void opm_fused_kernel(
     const bf16* __restrict__ aT, const bf16* __restrict__ bT, const int* __restrict__ count, int mean_rows,
@@ -186,82 +186,37 @@ __global__ __launch_bounds__(kFusedThreads) void opm_fused_kernel(
   const int b = blockIdx.z;
   const int i0 = blockIdx.y * TI, j0 = blockIdx.x * TJ;
   const int nv = count[b];
-  const int kend = (nv + TR - 1) / TR * TR;
+  const int kend = (nv + kNtBK - 1) / kNtBK * kNtBK;   // rows >= nv of aT / bT are zero
 
-  // A rows = (j, d) from bT, B rows = (i, c) from aT: 256 contiguous rows each.
-  const bf16* Ag = bT + ((size_t)b * Nt + j0) * CH * Sp;
-  const bf16* Bg = aT + ((size_t)b * Nt + i0) * CH * Sp;
-
-  // Staging: 256 rows x 32 r (64 B) per operand = 1024 16-byte chunks each.
-  bf16x8 ra[2], rb[2];
-  auto gload = [&](int k0) {
-#pragma unroll
-    for (int it = 0; it < 2; ++it) {
-      const int q = it * kFusedThreads + tid;
-      const int row = q >> 2, part = q & 3;
-      ra[it] = load8(Ag + (size_t)row * Sp + k0 + part * 8);
-      rb[it] = load8(Bg + (size_t)row * Sp + k0 + part * 8);
-    }
-  };
-  auto lstore = [&](int buf) {
-    bf16* sa = stage + buf * kStageElems;
-    bf16* sb = sa + 256 * LDK;
-#pragma unroll
-    for (int it = 0; it < 2; ++it) {
-      const int q = it * kFusedThreads + tid;
-      const int row = q >> 2, part = q & 3;
-      store8(sa + row * LDK + part * 8, ra[it]);
-      store8(sb + row * LDK + part * 8, rb[it]);
-    }
-  };
-
-  // Wave tile: rows [128*wr, +128) (4 blocks), cols [64*wc, +64) (2 blocks).
-  const int wr = wave >> 2, wc = wave & 3;
+  // X[(i,c),(j,d)] = sum_r aT[(i,c)][r] bT[(j,d)][r]: one 256 x 256 tile of the
+  // NT tile loop (gemm_nt.h; operands staged straight into LDS, 64-deep
+  // stages), rows Sp apart.  acc[jb][ib], lane (n, h), register u <->
+  // row (i,c) = wi*64 + ib*32 + n, column (j,d) = wj*128 + jb*32 + 16h + u.
   f32x16 acc[4][2];
-#pragma unroll
-  for (int x = 0; x < 4; ++x)
-#pragma unroll
-    for (int y = 0; y < 2; ++y) acc[x][y] = zero16();
-
   if (kend > 0) {
-    gload(0);
-    lstore(0);
+    gemm_nt_tile(aT + ((size_t)b * Nt + i0) * CH * Sp, kNtTile, bT + ((size_t)b * Nt + j0) * CH * Sp,
+                 bT + ((size_t)b * Nt + j0) * CH * Sp, kNtTile, kend, Sp, stage, acc);
+  } else {
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+#pragma unroll
+      for (int y = 0; y < 2; ++y) acc[x][y] = zero16();
   }
-  __syncthreads();
-  for (int k0 = 0; k0 < kend; k0 += TR) {
-    const int cur = (k0 / TR) & 1;
-    const bool more = k0 + TR < kend;
-    if (more) gload(k0 + TR);
-    const bf16* sa = stage + cur * kStageElems;
-    const bf16* sb = sa + 256 * LDK;
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      bf16x8 af[4], bfr[2];
-#pragma unroll
-      for (int x = 0; x < 4; ++x) af[x] = load8(sa + (wr * 128 + x * 32 + perm32(n)) * LDK + ks * 16 + 8 * h);
-#pragma unroll
-      for (int y = 0; y < 2; ++y) bfr[y] = load8(sb + (wc * 64 + y * 32 + n) * LDK + ks * 16 + 8 * h);
-#pragma unroll
-      for (int x = 0; x < 4; ++x)
-#pragma unroll
-        for (int y = 0; y < 2; ++y) acc[x][y] = mfma32(af[x], bfr[y], acc[x][y]);
-    }
-    if (more) lstore(cur ^ 1);
-    __syncthreads();
-  }
+  __syncthreads();   // the last stage's reads are done before xb overwrites it
 
   // Mean before the cast: xb[pair (ii, jj)][c*32 + d] = X[(i,c),(j,d)] / num_valid.
   const float inv = mean_rows ? 1.0f / (float)max(nv, 1) : 1.0f;
+  const int wi = wave & 3, wj = wave >> 2;
 #pragma unroll
-  for (int x = 0; x < 4; ++x)
+  for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
-    for (int y = 0; y < 2; ++y) {
-      const int jj = wr * 4 + x;          // row block = one j, d = 16h + u
-      const int col = wc * 64 + y * 32 + n;
-      const int ii = col >> 5, c = col & 31;
+    for (int ib = 0; ib < 2; ++ib) {
+      const int row = wi * 64 + ib * 32 + n;   // (i, c)
+      const int ii = row >> 5, c = row & 31;
+      const int jj = wj * 4 + jb;              // column block = one j, d = 16h + u
       float v[16];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) v[u] = acc[x][y][u] * inv;
+      for (int u = 0; u < 16; ++u) v[u] = acc[jb][ib][u] * inv;
       store16(xb + (ii * TJ + jj) * LDX + c * CH + 16 * h, v);
     }
   __syncthreads();
@@ -307,7 +262,7 @@ struct OpmLayout {
 };
 
 size_t opm_layout(int64_t B, int64_t S, int64_t N, OpmLayout* L, char* base) {
-  const size_t Nt = (size_t)round_up(N, 8), Sp = (size_t)round_up(S, 32);
+  const size_t Nt = (size_t)round_up(N, 8), Sp = (size_t)round_up(S, 64);
   const size_t idx_b = round_up((size_t)B * S * 4, 256), cnt_b = round_up((size_t)B * 4, 256);
   const size_t ab_b = round_up((size_t)B * Nt * CH * Sp * 2, 256);
   if (L) {
@@ -351,7 +306,7 @@ extern "C" int bioemu_opm_fwd(const void* m, const uint8_t* mask, int mean_rows,
     return set_error(BIOEMU_ERR_WORKSPACE, "opm: workspace too small");
   OpmLayout L;
   opm_layout(B, S, N, &L, static_cast<char*>(workspace));
-  const int64_t Nt = round_up(N, 8), Sp = round_up(S, 32);
+  const int64_t Nt = round_up(N, 8), Sp = round_up(S, 64);
   if (B * Nt * (Sp / 32) >= kMaxTiles) return set_error(BIOEMU_ERR_INVALID_ARG, "opm: too many row tiles");
 
   {

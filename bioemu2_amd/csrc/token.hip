@@ -259,7 +259,7 @@ __global__ __launch_bounds__(kNtThreads) void token_qkvg_kernel(const bf16* __re
   const bf16* b1 = wqkv + (size_t)min(col0, 3 * CS) * CS;
   const bf16* b2 = wg + (size_t)max(col0 - 3 * CS, 0) * CS;
   f32x16 acc[4][2];
-  gemm_nt_tile(sn + (size_t)row0 * CS, min(M - row0, kNtTile), b1, b2, split, CS, smem, acc);
+  gemm_nt_tile(sn + (size_t)row0 * CS, min(M - row0, kNtTile), b1, b2, split, CS, CS, smem, acc);
 
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int ln = lane & 31, lh = lane >> 5;
@@ -313,7 +313,8 @@ __global__ __launch_bounds__(kNtThreads) void token_out_kernel(const bf16* __res
   const int row0 = ti * kNtTile, col0 = tj * kNtTile;
   const int valid_cols = min(Nout - col0, kNtTile);   // a multiple of 32
   f32x16 acc[4][2];
-  gemm_nt_tile(A + (size_t)row0 * K, min(M - row0, kNtTile), W + (size_t)col0 * K, W, valid_cols, K, smem, acc);
+  gemm_nt_tile(A + (size_t)row0 * K, min(M - row0, kNtTile), W + (size_t)col0 * K, W, valid_cols, K, K, smem,
+               acc);
 
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int ln = lane & 31, lh = lane >> 5;
