@@ -1,10 +1,15 @@
-// Token-side (single representation) kernels for gfx950: row LayerNorm and a
-// small MFMA GEMM with fused epilogues.  These carry the per-token parts of
+// Token-side (single representation) kernels for gfx950: row LayerNorm, a
+// small MFMA GEMM with fused epilogues, and two GEMMs on the LDS-staged
+// 256 x 256 tile loop of gemm_nt.h.  These carry the per-token parts of
 // AttentionPairBias (src/bioemu2/biomoa/ops/attention_pair_bias.py:150-161,
-// :224-225) and the single-representation Transition
-// (src/bioemu2/biomoa/ops/transition.py:52-91).  The token dimension is small
-// (B * N rows of c_s = 384), so one wave computes one 32x32 output block with
-// operands read straight from L2.
+// :224-225), of the sliding-window attention, and the single-representation
+// Transition (src/bioemu2/biomoa/ops/transition.py:52-91).  In the trunk the
+// token dimension is small (B * N rows of c_s = 384): there one wave computes
+// one 32x32 output block with operands read straight from L2
+// (token_gemm_kernel).  The denoiser's copies make it large (M = 8 copies of
+// 768 tokens, 8 x 6144 atoms): the attention's four input projections always
+// run as one tiled launch (token_qkvg_kernel) and its output projection takes
+// the tiled kernel above a measured size (token_out_kernel).
 //
 // Row spaces.  A GEMM runs over M = B * Np "padded" rows (Np = N rounded up to
 // 32, rows t >= N of each batch are zero).  Row-major outputs/residuals use
