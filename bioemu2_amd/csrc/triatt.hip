@@ -432,6 +432,7 @@ void triatt_flash_kernel(
   lstore(0);
   __syncthreads();
   int st = 0;
+  bf16 kma = kadd[act[0] * 64 + krow], kmb = kadd[act[0] * 64 + 32 + krow];   // key-mask column of the block consumed next
 #pragma unroll 1
   for (int hd = 0; hd < H; ++hd) {
     f32x16 o[kFlashTiles];
@@ -456,7 +457,7 @@ void triatt_flash_kernel(
     // consume the current one.  k0 and the next tile's first key (kn) come in
     // registers; the key after that is read from the list during the block
     // (a read at the block's start would stall the K/V fetch on it).
-    auto block = [&](int ib, int k0, int& kn) {
+    auto block = [&](int ib, int k0, int& kn, bf16& kma, bf16& kmb) {
       // next tile: the next active block of this head, else the first of the
       // next head; the very last iteration refetches itself
       const int hn = ib + 1 < nact || hd + 1 == H ? hd : hd + 1;
@@ -473,11 +474,14 @@ void triatt_flash_kernel(
         const bf16* vs = ks + 2 * kTile;
         bf16x8 km0 = zero8, km1 = zero8;
         if (hh == 0) {
-          km0[0] = kadd[k0 + krow];
-          km1[0] = kadd[k0 + 32 + krow];
+          km0[0] = kma;
+          km1[0] = kmb;
           km0[1] = f2bf(1.f);
           km1[1] = f2bf(1.f);
         }
+        // the next block's key-mask column, read now so the read is not waited on at its start
+        kma = kadd[kn + krow];
+        kmb = kadd[kn + 32 + krow];
         const bf16x8 ka0 = load8(ks + t_off(krow, hh)), ka1 = load8(ks + kTile + t_off(krow, hh));
         const bf16x8 kb0 = load8(ks + t_off(krow, 2 + hh)), kb1 = load8(ks + kTile + t_off(krow, 2 + hh));
         // Logits minus the running max m, all on MFMA (no shift while m is
@@ -562,7 +566,7 @@ void triatt_flash_kernel(
     for (int ib = 0; ib < nact; ++ib) {
       const int k = kcur;
       kcur = knext;
-      block(ib, k, knext);
+      block(ib, k, knext, kma, kmb);
     }
     // head finished: o / l (bf16) parked in this head's q slot
 #pragma unroll
