@@ -217,14 +217,18 @@ __global__ __launch_bounds__(kProjThreads) void triatt_proj_kernel(
 //   S^T = K Q^T               2 MFMAs (k-steps over d)
 //       + bias               2 MFMAs: A = one-hot "identity" fragments,
 //                             B = the bias tile in B-operand layout
-//       + key mask           1 MFMA:  rank-1 product of a per-key column
-//                             (0 valid, -1e30 masked, -inf beyond N) with e_0
+//       + key mask - m       1 MFMA:  rank-2 product of a per-key column
+//                             (0 valid, -1e30 masked, -inf beyond N) and a
+//                             column of ones with (1, -m); skipped for a block
+//                             without masked keys while no shift is in use
 // A masked key's logit is -1e30 + (q.k + bias) = -1e30 exactly in fp32, so a
 // fully masked row gets equal logits (uniform weights, the reference's
 // masked_fill(-1e6) result) and a partially masked row gets exact zeros.
-// The running max m is set from the first block with an unmasked key and then
-// only moved (o and l rescaled) when a block's weight sum exceeds 2^16 (a
-// weight above 2^16 may be present), so most blocks skip the max search.
+// Softmax shift: when the first block's row maxima all lie in [-64, 16] (log2
+// units) the logits enter exp2 unshifted; otherwise the running max m is set
+// from that block.  After the first block, m is only set or moved (o and l
+// rescaled) when a block's weight sum exceeds 2^16 (a weight above 2^16 may be
+// present), so most blocks skip the max search.
 //
 // Loops: heads outermost (one head's accumulator live; a finished head leaves
 // o/l as 8 packed-bf16 registers), then 64-key blocks.  A block is two
@@ -437,13 +441,18 @@ void triatt_flash_kernel(
   for (int hd = 0; hd < H; ++hd) {
     f32x16 o[kFlashTiles];
     float m[kFlashTiles], l[kFlashTiles];
-    bool m_set[kFlashTiles];   // m is the (bf16-rounded) max of some unmasked logit
+    // Per tile, three modes: fresh (no block consumed), unshifted (the
+    // logits enter exp2 as they are: the first block's maxima were all in
+    // [-64, 16]) and shifted (m_set: the MFMA subtracts m, the bf16-rounded
+    // max of some unmasked logit).
+    bool m_set[kFlashTiles], fresh[kFlashTiles];
 #pragma unroll
     for (int t = 0; t < kFlashTiles; ++t) {
       o[t] = zero16();
       m[t] = -INFINITY;
       l[t] = 0.f;
       m_set[t] = false;
+      fresh[t] = true;
     }
     // B operand of the rank-2 mask / shift product: k = 0 -> 1 (picks the key
     // column kadd), k = 1 -> -m (against a key column of ones).
@@ -472,6 +481,8 @@ void triatt_flash_kernel(
       {
         const bf16* ks = smem + st * kStage;
         const bf16* vs = ks + 2 * kTile;
+        // the key-mask column matters only for a block holding a masked key
+        const bool need_mask = __any(bf2f(kma) != 0.f || bf2f(kmb) != 0.f);
         bf16x8 km0 = zero8, km1 = zero8;
         if (hh == 0) {
           km0[0] = kma;
@@ -484,9 +495,10 @@ void triatt_flash_kernel(
         kmb = kadd[kn + 32 + krow];
         const bf16x8 ka0 = load8(ks + t_off(krow, hh)), ka1 = load8(ks + kTile + t_off(krow, hh));
         const bf16x8 kb0 = load8(ks + t_off(krow, 2 + hh)), kb1 = load8(ks + kTile + t_off(krow, 2 + hh));
-        // Logits minus the running max m, all on MFMA (no shift while m is
-        // not yet set), for both query tiles before any softmax work so that
-        // one tile's exponentials overlap the other tile's matrix products.
+        // Logits minus the running max m, all on MFMA (no shift unless m is
+        // set; the rank-2 product only when there is a mask or a shift), for
+        // both query tiles before any softmax work so that one tile's
+        // exponentials overlap the other tile's matrix products.
         f32x16 s[kFlashTiles][2];
 #pragma unroll
         for (int t = 0; t < kFlashTiles; ++t) {
@@ -500,8 +512,10 @@ void triatt_flash_kernel(
           s[t][1] = mfma32(ident[0], bias[t][2], s[t][1]);
           s[t][0] = mfma32(ident[1], bias[t][1], s[t][0]);
           s[t][1] = mfma32(ident[1], bias[t][3], s[t][1]);
-          s[t][0] = mfma32(km0, qs, s[t][0]);
-          s[t][1] = mfma32(km1, qs, s[t][1]);
+          if (m_set[t] || need_mask) {
+            s[t][0] = mfma32(km0, qs, s[t][0]);
+            s[t][1] = mfma32(km1, qs, s[t][1]);
+          }
           bload(hn, kn, t, bias[t]);
         }
         if (ib + 1 == nact && hd + 1 < H) qload(hd + 1);
@@ -511,7 +525,7 @@ void triatt_flash_kernel(
           f32x16& s1 = s[t][1];
           bf16x8 pa[2], pb[2];
           float psum;
-          bool slow = !m_set[t];
+          bool slow = fresh[t];
           if (!slow) {
 #pragma unroll
             for (int u = 0; u < 16; ++u) {
@@ -531,17 +545,28 @@ void triatt_flash_kernel(
 #pragma unroll
             for (int u = 1; u < 16; ++u) bmax = __builtin_fmaxf(bmax, __builtin_fmaxf(s0[u], s1[u]));
             bmax = fmaxf(bmax, __shfl_xor(bmax, 32)) + shift;
-            // the shift is kept bf16-representable: it enters the MFMA as -m
-            const float m_new = bf2f(f2bf(fmaxf(m[t], bmax)));
-            const float alpha = fast_exp2(m[t] - m_new);
-            const float delta = m_new - shift;
-            m[t] = m_new;
-            l[t] *= alpha;
+            float delta = 0.f;
+            if (fresh[t] && __all(bmax >= -64.f && bmax <= 16.f)) {
+              // unshifted from here on: every weight is at most 2^16 until a
+              // block sum says otherwise, and each row keeps a weight of at
+              // least 2^-64 (nothing is accumulated yet)
+              fresh[t] = false;
+            } else {
+              // The shift is kept bf16-representable: it enters the MFMA as -m.
+              // Leaving the unshifted mode, the running max is at least -64.
+              const float floor_m = m_set[t] ? m[t] : fresh[t] ? -INFINITY : -64.f;
+              const float m_new = bf2f(f2bf(fmaxf(floor_m, bmax)));
+              const float alpha = fresh[t] ? 0.f : fast_exp2(shift - m_new);
+              delta = m_new - shift;
+              m[t] = m_new;
+              l[t] *= alpha;
 #pragma unroll
-            for (int u = 0; u < 16; ++u) o[t][u] *= alpha;
-            // a block of masked keys only (logits ~ -1e30) does not set m
-            m_set[t] = m_set[t] || __all(m[t] > -1e29f);
-            if (hh == 0) qm[t][1] = f2bf(-m[t]);
+              for (int u = 0; u < 16; ++u) o[t][u] *= alpha;
+              // a block of masked keys only (logits ~ -1e30) does not set m
+              m_set[t] = m_set[t] || __all(m[t] > -1e29f);
+              fresh[t] = fresh[t] && !m_set[t];
+              if (hh == 0) qm[t][1] = f2bf(-m[t]);
+            }
 #pragma unroll
             for (int u = 0; u < 16; ++u) {
               pa[u >> 3][u & 7] = f2bf(fast_exp2(s0[u] - delta));

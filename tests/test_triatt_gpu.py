@@ -142,18 +142,21 @@ def test_padding_bit_exact(gpu_device, starting):
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("scale", [2.0, 10.0])
 @pytest.mark.parametrize("starting", [True, False])
-def test_running_max_moves_key_order_invariant(gpu_device, starting):
-    """Logits that rise with the key index by far more than 16 log2 units make the kernel move its running max
-    after it has been set: the ascending order takes the max-moving path in later 64-key blocks, the reversed
-    token order (the same problem, relabelled) meets its max in the first block.  Relabelling every token is
-    an exact symmetry of triangle attention, so the two runs must agree to the north_star bf16 bar.  (Against
-    the fp32 oracle these logits are not a fair case: the ×log2e bias is stored in bf16, whose rounding at
-    |logit| ≈ 20 is worth several percent of an attention weight, in any bf16 implementation.)"""
+def test_running_max_moves_key_order_invariant(gpu_device, starting, scale):
+    """Logits that rise with the key index by far more than 16 log2 units make the kernel leave its unshifted
+    softmax or move its running max: the ascending order meets its larger logits in later 64-key blocks, the
+    reversed token order (the same problem, relabelled) in the first block.  At scale 2 head 0's first block in
+    ascending order has maxima in [-64, 16] (unshifted start, then a shift), reversed above 16 (shifted start);
+    at scale 10 the ascending first block lies below -64 (shifted start at a negative max).  Relabelling every
+    token is an exact symmetry of triangle attention, so the two runs must agree to the north_star bf16 bar.
+    (Against the fp32 oracle these logits are not a fair case: the ×log2e bias is stored in bf16, whose
+    rounding at |logit| ≈ 20 is worth several percent of an attention weight, in any bf16 implementation.)"""
     n = 250
     m = _module(starting, gpu_device)
     with torch.no_grad():
-        m.proj_b.weight.mul_(2.0)
+        m.proj_b.weight.mul_(scale)
     w = m.proj_b.weight[0].detach().float().cpu()
     g = torch.Generator().manual_seed(11)
     u = w - w.mean()
@@ -171,6 +174,7 @@ def test_running_max_moves_key_order_invariant(gpu_device, starting):
     lnz = torch.nn.functional.layer_norm(zk, (C,))
     b2 = (lnz @ w) * 1.4426950408889634
     assert b2[64:].max() - b2[:64].max() > 24.0
+    assert b2.max() > 16.0 and (b2[:64].max() < -64.0) == (scale > 5.0)
     mask = torch.ones(1, n, n, dtype=torch.bool)
     mask[:, :, 5] = False
     mask[:, 7, :] = False
@@ -180,7 +184,7 @@ def test_running_max_moves_key_order_invariant(gpu_device, starting):
         rev = m(z.flip(1, 2).contiguous(), mask.flip(1, 2).contiguous()).flip(1, 2).float()
     assert torch.isfinite(fwd).all()
     err, rl2 = max_abs(fwd, rev), rel_l2(fwd, rev)
-    print(f"triatt rising logits starting={starting}: ascending vs reversed max_abs={err:.3e} rel_l2={rl2:.3e} "
+    print(f"triatt rising logits starting={starting} scale={scale}: ascending vs reversed max_abs={err:.3e} rel_l2={rl2:.3e} "
           f"|out|max={fwd.abs().max():.3f}")
     assert err <= ATOL and rl2 <= RTOL_L2
 
