@@ -69,6 +69,10 @@ int launch_bgemm_nt(const void* A, const void* B, void* C, int64_t batch, int64_
 // width 128 (default), 64 or 256.
 int launch_fold_ln(const void* w, const float* gamma, const float* beta, void* wf, void* cf, int64_t rows,
                    hipStream_t stream, int width = 128);
+// The same for two matrices that share gamma and beta, in one launch: rows
+// [0, rows1) of the output fold w, rows [rows1, rows) fold w2 (its row r - rows1).
+int launch_fold_ln2(const void* w, const void* w2, int64_t rows1, const float* gamma, const float* beta, void* wf,
+                    void* cf, int64_t rows, hipStream_t stream, int width = 128);
 inline size_t fold_bytes(int64_t rows, int64_t width = 128) {
   return (size_t)round_up(rows * width * 2, 256) + (size_t)round_up(rows * 4, 256);
 }

@@ -477,8 +477,7 @@ extern "C" int bioemu_pwa_fwd(const void* m, const void* z, const uint8_t* mask,
 
   if (B * L.S8 * (L.Np / 32) >= kMaxTiles) return set_error(BIOEMU_ERR_INVALID_ARG, "pwa: too many row tiles");
   int rc = launch_fold_ln(w_z, norm_z_w, norm_z_b, wzf, czf, NH, stream);
-  if (!rc) rc = launch_fold_ln(w_m, norm_m_w, norm_m_b, wmf, cmf, HC, stream, CM);
-  if (!rc) rc = launch_fold_ln(w_g, norm_m_w, norm_m_b, wmf + HC * CM, cmf + HC * 2, HC, stream, CM);
+  if (!rc) rc = launch_fold_ln2(w_m, w_g, HC, norm_m_w, norm_m_b, wmf, cmf, 2 * HC, stream, CM);
   if (rc) return rc;
 
   int dev = 0, cus = 0;

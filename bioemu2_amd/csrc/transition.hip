@@ -310,8 +310,7 @@ extern "C" int bioemu_transition_pair_fwd(const void* x, const float* norm_w, co
   const bf16* w1 = static_cast<const bf16*>(fc1_w);
   const bf16* w2 = static_cast<const bf16*>(fc2_w);
   if (use_norm) {
-    int rc = launch_fold_ln(fc1_w, norm_w, norm_b, wf, cf, hidden, stream, (int)Dc);
-    if (!rc) rc = launch_fold_ln(fc2_w, norm_w, norm_b, wf + hidden * Dc, cf + hidden * 2, hidden, stream, (int)Dc);
+    const int rc = launch_fold_ln2(fc1_w, fc2_w, hidden, norm_w, norm_b, wf, cf, 2 * hidden, stream, (int)Dc);
     if (rc) return rc;
     w1 = wf;
     w2 = wf + hidden * Dc;

@@ -280,8 +280,8 @@ class BlockWorkload(Workload):
         w = trimul_kernel_work(kernel, 1, n) or triatt_kernel_work(kernel, 1, n, n_valid=n - self.n_pad)
         if w is not None:
             return w
-        if kernel == "fold_ln":  # triatt (516 rows) x2, APB bias (16 rows), transition fc1 and fc2 (512 rows each)
-            return fold_kernel_work(kernel, 5, 2 * 516 + 16 + 1024)
+        if kernel == "fold_ln":  # triatt (516 rows) x2, APB bias (16 rows), transition fc1 + fc2 (1024 rows, one launch)
+            return fold_kernel_work(kernel, 4, 2 * 516 + 16 + 1024)
         if kernel == "transition_pair":
             return ("mfma", 2.0 * n * n * c * 12 * c)
         if kernel == "apb_pair_bias":
@@ -468,8 +468,8 @@ class PwaWorkload(Workload):
         if kernel == "pwa_proj":
             # reads m, writes v^T and g (256 channels each)
             return ("hbm", float(S * n * 64 * 2 + 2 * S * npad * 256 * 2))
-        if kernel == "fold_ln":  # w_z (8 rows), w_m and w_g (256 rows of width 64 each)
-            return fold_kernel_work(kernel, 3, 8, 512)
+        if kernel == "fold_ln":  # w_z (8 rows); w_m and w_g (256 rows of width 64 each, one launch)
+            return fold_kernel_work(kernel, 2, 8, 512)
         raise KeyError(kernel)
 
 
@@ -520,8 +520,8 @@ class PairMixerWorkload(Workload):
             return w
         if kernel == "transition_pair":
             return ("mfma", 2.0 * self.n * self.n * 128 * 12 * 128)
-        if kernel == "fold_ln":  # transition fc1 and fc2 (512 rows each)
-            return fold_kernel_work(kernel, 2, 1024)
+        if kernel == "fold_ln":  # transition fc1 and fc2 (512 rows each, one launch)
+            return fold_kernel_work(kernel, 1, 1024)
         raise KeyError(kernel)
 
 
@@ -617,8 +617,8 @@ class PairMixerMsaWorkload(Workload):
             return PwaWorkload.kernel_work(self, kernel)
         if kernel == "transition_msa":
             return ("mfma", 2.0 * S * n * 64 * 12 * 64)
-        if kernel == "fold_ln":  # PWA (3 folds), MSA transition and pair transition fc1, fc2
-            return fold_kernel_work(kernel, 7, 8 + 1024, 512 + 512)
+        if kernel == "fold_ln":  # PWA (2 launches), MSA transition and pair transition (one launch each)
+            return fold_kernel_work(kernel, 4, 8 + 1024, 512 + 512)
         raise KeyError(kernel)
 
 
@@ -738,9 +738,9 @@ class PairMixerTrunkWorkload(Workload):
             return ("hbm", float(n * n * 128 * (2 + 3 + 3)))   # x, base + tail in; out + tail
         if kernel == "msa_embed":
             return ("hbm", float(S * n * (33 + 3) * 4 + S * n * 64 * 3))
-        if kernel == "fold_ln":   # pair transitions (L), PWA (3) + MSA transition per MSA layer, z recycle
+        if kernel == "fold_ln":   # launches: pair transitions (L), PWA (2) + MSA transition per MSA layer, z recycle
             mb = self.msa_blocks
-            return fold_kernel_work(kernel, L + 4 * mb + 1, L * 1024 + 8 * mb + 128, mb * 1024)
+            return fold_kernel_work(kernel, L + 3 * mb + 1, L * 1024 + 8 * mb + 128, mb * 1024)
         raise KeyError(kernel)
 
 
