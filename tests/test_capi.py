@@ -84,7 +84,8 @@ def test_invalid_arguments_rejected_without_gpu():
 
 
 def test_integration_doc_argtypes_match_binding():
-    """Every `lib.<entry>.argtypes = ...` line in INTEGRATION.md declares the binding's signature."""
+    """Every `lib.<entry>.argtypes = ...` line of the integration guide at the repository root declares the
+    binding's signature."""
     text = (ROOT / "INTEGRATION.md").read_text().replace("\\\n", " ")
     found = re.findall(r"lib\.(bioemu_\w+)\.argtypes\s*=\s*([^\n]+)", text)
     assert found
