@@ -64,6 +64,24 @@ def test_matches_oracle_n768_token_padding(gpu_device, mode):
     assert err <= ATOL and rl2 <= RTOL_L2
 
 
+def test_matches_oracle_n2048_token_padding(gpu_device):
+    """Config 5's pair shape: N=2048, last 102 tokens padded (planes padded to 2048, eight 256-wide contraction
+    tiles), outgoing, against the fp32 oracle."""
+    n = 2048
+    m = _module("outgoing", gpu_device)
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(1, n, n, D, generator=g).to(torch.bfloat16)
+    tok = torch.ones(1, n, dtype=torch.bool)
+    tok[:, n - 102:] = False
+    pm = oracle.pair_mask_from_token_mask(tok)
+    with torch.no_grad():
+        got = m(x.to(gpu_device), pm.to(gpu_device)).float().cpu()
+    want = oracle.trimul(x.float(), pm, state(m), "outgoing")
+    err, rl2 = max_abs(got, want), rel_l2(got, want)
+    print(f"trimul outgoing n=2048: max_abs={err:.3e} rel_l2={rl2:.3e}", flush=True)
+    assert err <= ATOL and rl2 <= RTOL_L2
+
+
 @pytest.mark.parametrize("mode", ["outgoing", "incoming"])
 def test_masking_bit_exact(gpu_device, mode):
     m = _module(mode, gpu_device)
