@@ -75,6 +75,16 @@ def test_apb_config2_shape(gpu_device):
     _check(got[:2], want, "apb config2")
 
 
+def test_apb_config5_shape(gpu_device):
+    """The Pairformer block's attention at config 5's size: B=1, N=2048 with the last 102 keys masked."""
+    m = _apb(gpu_device)
+    s, z, mask = _apb_inputs(1, 2048, gpu_device, pad_keys=102, seed=5)
+    with torch.no_grad():
+        got = m(s, z, mask).float().cpu()
+    want = oracle.attention_pair_bias(s.cpu(), z.cpu(), mask.cpu(), state(m), 16)
+    _check(got, want, "apb n=2048")
+
+
 def test_apb_multiplicity_equals_separate(gpu_device):
     m = _apb(gpu_device)
     mult = 3
