@@ -67,11 +67,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _c_int,
         [_c_void_p] * 13 + [_c_void_p, _c_size_t] + [_c_int64] * 8 + [_c_int, _c_void_p],
     ),
-    "bioemu_distogram_fwd": (_c_int, [_c_void_p] * 4 + [_c_int64] * 4 + [_c_void_p]),
+    "bioemu_distogram_fwd": (_c_int, [_c_void_p] * 4 + [_c_int64] * 4 + [_c_int, _c_void_p]),
     "bioemu_pair_cond_workspace_bytes": (_c_size_t, [_c_int64] * 3),
     "bioemu_pair_cond_proj_fwd": (
         _c_int,
-        [_c_void_p] * 7 + [_c_size_t] + [_c_int64] * 4 + [_c_void_p],
+        [_c_void_p] * 8 + [_c_size_t] + [_c_int64] * 4 + [_c_void_p],
     ),
     "bioemu_opm_workspace_bytes": (_c_size_t, [_c_int64] * 5),
     "bioemu_opm_fwd": (
@@ -84,6 +84,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "bioemu_pair_ln_linear_fwd": (_c_int, [_c_void_p] * 9 + [_c_size_t, _c_int64, _c_int64, _c_void_p]),
     "bioemu_token_ln_linear_workspace_bytes": (_c_size_t, [_c_int64] * 2),
     "bioemu_token_ln_linear_fwd": (_c_int, [_c_void_p] * 9 + [_c_size_t, _c_int64, _c_int64, _c_void_p]),
+    "bioemu_trunk_uncond_workspace_bytes": (_c_size_t, [_c_int64] * 3),
+    "bioemu_trunk_uncond_fwd": (_c_int, [_c_void_p] * 12 + [_c_size_t] + [_c_int64] * 3 + [_c_void_p]),
     "bioemu_msa_embed_workspace_bytes": (_c_size_t, [_c_int64] * 2),
     "bioemu_msa_embed_fwd": (_c_int, [_c_void_p] * 10 + [_c_size_t] + [_c_int64] * 6 + [_c_void_p]),
     "bioemu_apb_f32_workspace_bytes": (_c_size_t, [_c_int64] * 5),

@@ -597,6 +597,23 @@ def fp32_mode(x: Tensor) -> bool:
     return x.dtype == F32 and not torch.is_autocast_enabled("cuda")
 
 
+def require_mixed_precision(x: Tensor, what: str) -> None:
+    """Refuse the reference's fp32 mode (fp32 inputs with CUDA autocast off) for an op that has no fp32
+    arithmetic.  Those ops compute with bf16 MFMA operands and fp32 accumulation, which is what the reference's
+    trunk does under bf16 autocast (model.py:222, utils/precision.py:9-26); an fp32 caller outside autocast asks
+    for IEEE fp32 (``TriangleMultiplicationCueq``'s default ``matmul_precision="ieee"``, triangle_multiplication
+    .py:117; OPM's fp32 contraction, outer_product_mean.py:64-74) and gets an error instead of bf16-level
+    results.  Running under ``torch.autocast("cuda", dtype=torch.bfloat16)`` or passing bf16 tensors selects the
+    bf16 path explicitly.  Host tensors fail first, as everywhere (there is no CPU path)."""
+    require_gpu(x, what)
+    if fp32_mode(x):
+        raise ValueError(
+            f"{what}: fp32 inputs with autocast off ask for fp32 arithmetic, which this op does not have (it computes "
+            "with bf16 MFMA operands and fp32 accumulation); run it under torch.autocast('cuda', "
+            "dtype=torch.bfloat16), the reference trunk's policy, or pass bf16 tensors"
+        )
+
+
 def _check_attn_params_f32(what, c_s, c_z, num_heads, dev, norm_s_w, norm_s_b, w_qkv, q_bias, w_g, norm_z_w,
                            norm_z_b, w_z, w_o) -> None:
     if norm_s_w is not None:
@@ -884,8 +901,11 @@ def launch_distogram(z: Tensor, w: Tensor, b: Tensor, out: Tensor) -> Tensor:
     _check_tensor(z, "distogram z", BF16, (B, N, N, c_z), dev)
     _check_tensor(w, "distogram.weight", BF16, (nb, c_z), dev)
     _check_tensor(b, "distogram.bias", torch.float32, (nb,), dev)
-    _check_tensor(out, "distogram out", BF16, (B, N, N, nb), dev)
-    rc = lib().bioemu_distogram_fwd(_ptr(z), _ptr(w), _ptr(b), _ptr(out), B, N, c_z, nb, _stream(z))
+    if out.dtype not in (BF16, torch.float32):
+        raise ValueError(f"distogram out: dtype {out.dtype} (bf16 or fp32)")
+    _check_tensor(out, "distogram out", out.dtype, (B, N, N, nb), dev)
+    rc = lib().bioemu_distogram_fwd(_ptr(z), _ptr(w), _ptr(b), _ptr(out), B, N, c_z, nb,
+                                    int(out.dtype == torch.float32), _stream(z))
     check(rc, "bioemu_distogram_fwd")
     return out
 
@@ -895,7 +915,8 @@ def pair_cond_workspace_bytes(token_z: int, c_rel: int, a_z: int) -> int:
 
 
 def launch_pair_cond_proj(
-    z: Tensor, rel: Tensor, ln_w: Tensor, ln_b: Tensor, w: Tensor, out: Tensor, ws: Tensor | None = None
+    z: Tensor, rel: Tensor, ln_w: Tensor, ln_b: Tensor, w: Tensor, out: Tensor, ws: Tensor | None = None,
+    out_tail: Tensor | None = None,
 ) -> Tensor:
     require_gpu(z, "pairwise_conditioning")
     token_z, c_rel, a_z = z.shape[-1], rel.shape[-1], w.shape[0]
@@ -907,12 +928,14 @@ def launch_pair_cond_proj(
     _check_tensor(ln_b, "pair_cond norm.bias", torch.float32, (token_z + c_rel,), dev)
     _check_tensor(w, "pair_cond proj.weight", BF16, (a_z, token_z + c_rel), dev)
     _check_tensor(out, "pair_cond out", BF16, tuple(z.shape[:-1]) + (a_z,), dev)
+    if out_tail is not None:
+        _check_tensor(out_tail, "pair_cond out tail", torch.int8, tuple(out.shape), dev)
     need = pair_cond_workspace_bytes(token_z, c_rel, a_z)
     if ws is None or ws.numel() < need:
         ws = workspace(max(need, 1), dev)
     rc = lib().bioemu_pair_cond_proj_fwd(
-        _ptr(z), _ptr(rel), _ptr(ln_w), _ptr(ln_b), _ptr(w), _ptr(out), _ptr(ws), ctypes.c_size_t(ws.numel()),
-        P, token_z, c_rel, a_z, _stream(z),
+        _ptr(z), _ptr(rel), _ptr(ln_w), _ptr(ln_b), _ptr(w), _ptr(out), _ptr(out_tail), _ptr(ws),
+        ctypes.c_size_t(ws.numel()), P, token_z, c_rel, a_z, _stream(z),
     )
     check(rc, "bioemu_pair_cond_proj_fwd")
     return out
@@ -1141,6 +1164,56 @@ def launch_ln_linear(
     rc = fn(_ptr(x), _ptr(norm_w), _ptr(norm_b), _ptr(w), _ptr(base), _ptr(base_tail), _ptr(out), _ptr(out_tail),
             _ptr(ws), ctypes.c_size_t(ws.numel()), M, D, _stream(x))
     check(rc, "bioemu_pair_ln_linear_fwd" if pair else "bioemu_token_ln_linear_fwd")
+    return out
+
+
+def trunk_uncond_workspace_bytes(P: int, D: int, hidden: int) -> int:
+    return int(lib().bioemu_trunk_uncond_workspace_bytes(P, D, hidden))
+
+
+def launch_trunk_uncond(
+    z_init: Tensor,
+    z_norm_w: Tensor,
+    z_norm_b: Tensor,
+    t_norm_w: Tensor,
+    t_norm_b: Tensor,
+    fc1_w: Tensor,
+    fc2_w: Tensor,
+    fc3_w: Tensor,
+    out: Tensor,
+    z_init_tail: Tensor | None = None,
+    out_tail: Tensor | None = None,
+    ws: Tensor | None = None,
+) -> Tensor:
+    """``out = z_init + uncond_transition(z_norm(z_init))`` over pair rows of 128 channels (the unconditional
+    branch, pairmixer.py:266-273); the tails carry z_init and out as residual streams (both or neither)."""
+    require_gpu(z_init, "trunk_uncond")
+    D = z_init.shape[-1]
+    P = z_init.numel() // D
+    dev = z_init.device
+    hidden = fc1_w.shape[0]
+    _check_tensor(z_init, "trunk_uncond z_init", BF16, tuple(z_init.shape), dev)
+    _check_tensor(out, "trunk_uncond out", BF16, tuple(z_init.shape), dev)
+    for t, what in ((z_norm_w, "z_norm.weight"), (z_norm_b, "z_norm.bias"), (t_norm_w, "norm.weight"),
+                    (t_norm_b, "norm.bias")):
+        _check_tensor(t, f"trunk_uncond {what}", torch.float32, (D,), dev)
+    _check_tensor(fc1_w, "trunk_uncond fc1.weight", BF16, (hidden, D), dev)
+    _check_tensor(fc2_w, "trunk_uncond fc2.weight", BF16, (hidden, D), dev)
+    _check_tensor(fc3_w, "trunk_uncond fc3.weight", BF16, (D, hidden), dev)
+    if (z_init_tail is None) != (out_tail is None):
+        raise ValueError("trunk_uncond: z_init_tail and out_tail go together")
+    for t, what in ((z_init_tail, "z_init tail"), (out_tail, "out tail")):
+        if t is not None:
+            _check_tensor(t, f"trunk_uncond {what}", torch.int8, tuple(z_init.shape), dev)
+    need = trunk_uncond_workspace_bytes(P, D, hidden)
+    if ws is None or ws.numel() < need:
+        ws = workspace(need, dev)
+    rc = lib().bioemu_trunk_uncond_fwd(
+        _ptr(z_init), _ptr(z_init_tail), _ptr(z_norm_w), _ptr(z_norm_b), _ptr(t_norm_w), _ptr(t_norm_b), _ptr(fc1_w),
+        _ptr(fc2_w), _ptr(fc3_w), _ptr(out), _ptr(out_tail), _ptr(ws), ctypes.c_size_t(ws.numel()), P, D, hidden,
+        _stream(z_init),
+    )
+    check(rc, "bioemu_trunk_uncond_fwd")
     return out
 
 

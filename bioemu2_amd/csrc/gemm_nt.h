@@ -48,20 +48,21 @@ __device__ __forceinline__ void nt_copy16_to_lds(__amdgpu_buffer_rsrc_t r, const
 // rest read as zero through the buffer bound (their C rows are garbage-free
 // zeros times B, never needed by a caller that skips them).  B rows [0,
 // b_split) come from B, rows [b_split, 256) from B2 (its row 0 = tile row
-// b_split); b_split is a multiple of 8.  Rows are ld elements apart, of which
+// b_split), of which b2_rows exist (rows past them read as zero through the
+// buffer bound); b_split is a multiple of 8.  Rows are ld elements apart, of which
 // the first K (K % 64 == 0, K <= ld) are reduced; 256 * ld * 2 < 2^32.  Whole
 // workgroup; smem holds kNtSmem bytes.  Ends with an epilogue-ready acc and no
 // copy in flight; other waves may still read the last stage (an epilogue that
 // reuses smem starts with a barrier).
 __device__ __forceinline__ void gemm_nt_tile(const bf16* A, int a_rows, const bf16* B, const bf16* B2, int b_split,
-                                             int K, int ld, bf16* smem, f32x16 (&acc)[4][2]) {
+                                             int b2_rows, int K, int ld, bf16* smem, f32x16 (&acc)[4][2]) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ln = lane & 31, lh = lane >> 5;
   const int wi = wave & 3, wj = wave >> 2;
   const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(A, (unsigned)a_rows * ld * 2);
   const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(B, (unsigned)b_split * ld * 2);
-  const __amdgpu_buffer_rsrc_t rb2 = buffer_rsrc(B2, (unsigned)(kNtTile - b_split) * ld * 2);
+  const __amdgpu_buffer_rsrc_t rb2 = buffer_rsrc(B2, (unsigned)min(kNtTile - b_split, b2_rows) * ld * 2);
   // Each operand tile (256 rows x 128 B) is 32 copies of 1 KB; wave w moves
   // copies w, w + 8, w + 16, w + 24 of A and of B.  Copy j writes LDS chunk
   // 64 j + lane = (row, swizzled chunk) of the tile: rows 8 j .. 8 j + 7, all
@@ -128,7 +129,7 @@ __device__ __forceinline__ void gemm_nt_tile(const bf16* A, int a_rows, const bf
 
 // Full tiles from one B matrix.
 __device__ __forceinline__ void gemm_nt_tile(const bf16* A, const bf16* B, int K, bf16* smem, f32x16 (&acc)[4][2]) {
-  gemm_nt_tile(A, kNtTile, B, B, kNtTile, K, K, smem, acc);
+  gemm_nt_tile(A, kNtTile, B, B, kNtTile, 0, K, K, smem, acc);
 }
 
 // XCD-aware work-item order: workgroup w runs on XCD w % 8; each XCD gets a

@@ -28,10 +28,12 @@ constexpr int kMaxBins = 128;
 // ---------------------------------------------------------------------------
 // Distogram.  Wave tile = (b, row i, 32 keys j0 .. j0 + 31); lane (n, hh) holds
 // channel chunks 2s + hh of pair (i, j0 + n) (pairtile.h).  Tiles entirely
-// below the diagonal exit.
+// below the diagonal exit.  The output is bf16 (OutT = bf16) or fp32 (the
+// fp32 accumulator plus the bias, unrounded).
 // ---------------------------------------------------------------------------
+template <typename OutT>
 __global__ __launch_bounds__(kThreads) void distogram_kernel(const bf16* __restrict__ z, const bf16* __restrict__ wd,
-                                                             const float* __restrict__ bd, bf16* __restrict__ out,
+                                                             const float* __restrict__ bd, OutT* __restrict__ out,
                                                              int B, int N, int NB, int NBp) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   bf16* wl = reinterpret_cast<bf16*>(smem);
@@ -65,9 +67,14 @@ __global__ __launch_bounds__(kThreads) void distogram_kernel(const bf16* __restr
         float v[16];
 #pragma unroll
         for (int u = 0; u < 16; ++u) v[u] = acc[u] + (c0 + u < NB ? bd[c0 + u] : 0.f);
-        bf16* o1 = out + (((size_t)b * N + i) * N + j) * NB + c0;
-        bf16* o2 = out + (((size_t)b * N + j) * N + i) * NB + c0;
-        if ((NB & 7) == 0 && c0 + 16 <= NB) {
+        OutT* o1 = out + (((size_t)b * N + i) * N + j) * NB + c0;
+        OutT* o2 = out + (((size_t)b * N + j) * N + i) * NB + c0;
+        if constexpr (std::is_same<OutT, float>::value) {
+          for (int u = 0; u < 16 && c0 + u < NB; ++u) {
+            o1[u] = v[u];
+            if (j != i) o2[u] = v[u];
+          }
+        } else if ((NB & 7) == 0 && c0 + 16 <= NB) {
           store16(o1, v);
           if (j != i) store16(o2, v);
         } else {
@@ -83,7 +90,9 @@ __global__ __launch_bounds__(kThreads) void distogram_kernel(const bf16* __restr
 
 // ---------------------------------------------------------------------------
 // Pairwise-conditioning input projection: 4 waves x 32 pairs per workgroup;
-// folded weights [128][256] (row stride 264) + bias pairs in LDS.
+// folded weights [128][256] (row stride 264) + bias pairs in LDS.  With a
+// tail (out_tail != null) the output is written as a residual stream, bf16
+// value + int8 tail (common.h), for the transitions that follow.
 // ---------------------------------------------------------------------------
 constexpr int kCin = 2 * CZ;            // 256 concatenated channels
 constexpr int kOut = CZ;                // a_z = 128
@@ -94,7 +103,7 @@ __global__ __launch_bounds__(kThreads) void pair_cond_proj_kernel(const bf16* __
                                                                   const bf16* __restrict__ rel,
                                                                   const bf16* __restrict__ wf,
                                                                   const bf16* __restrict__ cf, bf16* __restrict__ out,
-                                                                  long long P) {
+                                                                  int8_t* __restrict__ out_tail, long long P) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   bf16* wl = reinterpret_cast<bf16*>(smem);
   bf16* cl = wl + kOut * kLdw2;
@@ -152,7 +161,11 @@ __global__ __launch_bounds__(kThreads) void pair_cond_proj_kernel(const bf16* __
       float o[16];
 #pragma unroll
       for (int u = 0; u < 16; ++u) o[u] = acc[u];
-      store16(out + (size_t)p * kOut + ob * 32 + 16 * hh, o);
+      const size_t off = (size_t)p * kOut + ob * 32 + 16 * hh;
+      if (out_tail)
+        tail_store16(out + off, out_tail + off, o);
+      else
+        store16(out + off, o);
     }
   }
 }
@@ -163,7 +176,7 @@ __global__ __launch_bounds__(kThreads) void pair_cond_proj_kernel(const bf16* __
 using namespace bioemu;
 
 extern "C" int bioemu_distogram_fwd(const void* z, const void* w, const float* b, void* out, int64_t B, int64_t N,
-                                    int64_t c_z, int64_t num_bins, hipStream_t stream) {
+                                    int64_t c_z, int64_t num_bins, int out_f32, hipStream_t stream) {
   if (c_z != CZ || num_bins <= 0 || num_bins > kMaxBins)
     return set_error(BIOEMU_ERR_UNSUPPORTED, "distogram: supported c_z = 128, 1 <= num_bins <= %d (got %lld, %lld)",
                      kMaxBins, (long long)c_z, (long long)num_bins);
@@ -172,6 +185,8 @@ extern "C" int bioemu_distogram_fwd(const void* z, const void* w, const float* b
   if (!z || !w || !b || !out) return set_error(BIOEMU_ERR_INVALID_ARG, "distogram: null pointer argument");
   if (!aligned16(z) || !aligned16(w) || !aligned16(out))
     return set_error(BIOEMU_ERR_INVALID_ARG, "distogram: tensors must be 16-byte aligned");
+  if (out_f32 != 0 && out_f32 != 1)
+    return set_error(BIOEMU_ERR_INVALID_ARG, "distogram: out_f32 must be 0 or 1 (got %d)", out_f32);
   const int NBp = (int)round_up(num_bins, 32);
   const size_t smem = (size_t)NBp * kLdw * 2;
   int dev = 0, cus = 0;
@@ -181,8 +196,12 @@ extern "C" int bioemu_distogram_fwd(const void* z, const void* w, const float* b
   if (ntiles >= kMaxTiles) return set_error(BIOEMU_ERR_INVALID_ARG, "distogram: too many pair tiles");
   const unsigned grid = (unsigned)std::max<long long>(1, std::min<long long>(8LL * cus, (ntiles + 3) / 4));
   KernelTimerScope timed("distogram", stream);
-  hipLaunchKernelGGL(distogram_kernel, dim3(grid), dim3(kThreads), smem, stream, static_cast<const bf16*>(z),
-                     static_cast<const bf16*>(w), b, static_cast<bf16*>(out), (int)B, (int)N, (int)num_bins, NBp);
+  if (out_f32)
+    hipLaunchKernelGGL(distogram_kernel<float>, dim3(grid), dim3(kThreads), smem, stream, static_cast<const bf16*>(z),
+                       static_cast<const bf16*>(w), b, static_cast<float*>(out), (int)B, (int)N, (int)num_bins, NBp);
+  else
+    hipLaunchKernelGGL(distogram_kernel<bf16>, dim3(grid), dim3(kThreads), smem, stream, static_cast<const bf16*>(z),
+                       static_cast<const bf16*>(w), b, static_cast<bf16*>(out), (int)B, (int)N, (int)num_bins, NBp);
   return check_launch("distogram");
 }
 
@@ -192,16 +211,17 @@ extern "C" size_t bioemu_pair_cond_workspace_bytes(int64_t token_z, int64_t c_re
 }
 
 extern "C" int bioemu_pair_cond_proj_fwd(const void* z_trunk, const void* rel, const float* ln_w, const float* ln_b,
-                                         const void* w, void* out, void* workspace, size_t workspace_bytes,
-                                         int64_t P, int64_t token_z, int64_t c_rel, int64_t a_z,
-                                         hipStream_t stream) {
+                                         const void* w, void* out, int8_t* out_tail, void* workspace,
+                                         size_t workspace_bytes, int64_t P, int64_t token_z, int64_t c_rel,
+                                         int64_t a_z, hipStream_t stream) {
   if (token_z != CZ || c_rel != CZ || a_z != kOut)
     return set_error(BIOEMU_ERR_UNSUPPORTED, "pair_cond: supported token_z = rel = a_z = 128 (got %lld, %lld, %lld)",
                      (long long)token_z, (long long)c_rel, (long long)a_z);
   if (P <= 0) return set_error(BIOEMU_ERR_INVALID_ARG, "pair_cond: bad row count %lld", (long long)P);
   if (!z_trunk || !rel || !ln_w || !ln_b || !w || !out || !workspace)
     return set_error(BIOEMU_ERR_INVALID_ARG, "pair_cond: null pointer argument");
-  if (!aligned16(z_trunk) || !aligned16(rel) || !aligned16(w) || !aligned16(out) || !aligned16(workspace))
+  if (!aligned16(z_trunk) || !aligned16(rel) || !aligned16(w) || !aligned16(out) || !aligned16(workspace) ||
+      (out_tail && !aligned16(out_tail)))
     return set_error(BIOEMU_ERR_INVALID_ARG, "pair_cond: tensors must be 16-byte aligned");
   if (workspace_bytes < bioemu_pair_cond_workspace_bytes(token_z, c_rel, a_z))
     return set_error(BIOEMU_ERR_WORKSPACE, "pair_cond: workspace too small");
@@ -218,6 +238,6 @@ extern "C" int bioemu_pair_cond_proj_fwd(const void* z_trunk, const void* rel, c
   KernelTimerScope timed("pair_cond_proj", stream);
   hipLaunchKernelGGL(pair_cond_proj_kernel, dim3((unsigned)nwg), dim3(kThreads), kPcSmem, stream,
                      static_cast<const bf16*>(z_trunk), static_cast<const bf16*>(rel), wf, cf,
-                     static_cast<bf16*>(out), (long long)P);
+                     static_cast<bf16*>(out), out_tail, (long long)P);
   return check_launch("pair_cond_proj");
 }

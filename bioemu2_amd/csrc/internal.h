@@ -96,4 +96,13 @@ int token_qkvg(const void* sn, const void* wqkv, const void* w_g, const float* q
                void* k, void* vt, void* g, int64_t M, int64_t CS, int64_t seq_rows, hipStream_t stream,
                const char* name);
 
+// Row transition out = res + fc3(silu(fc1 LN x) * fc2 LN x) (transition.hip): the
+// arguments of bioemu_transition_pair_fwd plus the residual base res (x for
+// the in-place block update; with res_tail, res is its hi part and out_tail
+// = res_tail is rewritten in place).
+int transition_pair_res(const void* x, const void* res, const float* norm_w, const float* norm_b, const void* fc1_w,
+                        const void* fc2_w, const void* fc3_w, void* out, int8_t* res_tail, void* workspace,
+                        size_t workspace_bytes, int64_t P, int64_t Dc, int64_t hidden, int use_norm, int residual,
+                        hipStream_t stream);
+
 }  // namespace bioemu

@@ -195,7 +195,7 @@ __global__ __launch_bounds__(kFusedThreads) void opm_fused_kernel(
   f32x16 acc[4][2];
   if (kend > 0) {
     gemm_nt_tile(aT + ((size_t)b * Nt + i0) * CH * Sp, kNtTile, bT + ((size_t)b * Nt + j0) * CH * Sp,
-                 bT + ((size_t)b * Nt + j0) * CH * Sp, kNtTile, kend, Sp, stage, acc);
+                 bT + ((size_t)b * Nt + j0) * CH * Sp, kNtTile, 0, kend, Sp, stage, acc);
   } else {
 #pragma unroll
     for (int x = 0; x < 4; ++x)

@@ -264,7 +264,8 @@ __global__ __launch_bounds__(kNtThreads) void token_qkvg_kernel(const bf16* __re
   const bf16* b1 = wqkv + (size_t)min(col0, 3 * CS) * CS;
   const bf16* b2 = wg + (size_t)max(col0 - 3 * CS, 0) * CS;
   f32x16 acc[4][2];
-  gemm_nt_tile(sn + (size_t)row0 * CS, min(M - row0, kNtTile), b1, b2, split, CS, CS, smem, acc);
+  gemm_nt_tile(sn + (size_t)row0 * CS, min(M - row0, kNtTile), b1, b2, split, CS - max(col0 - 3 * CS, 0), CS, CS,
+               smem, acc);
 
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int ln = lane & 31, lh = lane >> 5;
@@ -302,7 +303,8 @@ __global__ __launch_bounds__(kNtThreads) void token_qkvg_kernel(const bf16* __re
 // ---------------------------------------------------------------------------
 // out = A[M][K] W[Nout][K]^T (+ res) on 256 x 256 tiles (gemm_nt.h tile loop,
 // operands staged through LDS; rows past M read as zero, columns past Nout
-// are computed on repeated weight rows and not stored).  Rows are batches of
+// are computed on W's rows from row 0 again, or zeros past W's end, and are
+// not stored).  Rows are batches of
 // Np padded rows; with out_rows < Np the output / residual use the compact
 // [B][out_rows] layout and padded rows are dropped (as token_gemm_kernel).
 // With a tail (kTail) the residual stream carries int8 tails, in place.
@@ -318,7 +320,9 @@ __global__ __launch_bounds__(kNtThreads) void token_out_kernel(const bf16* __res
   const int row0 = ti * kNtTile, col0 = tj * kNtTile;
   const int valid_cols = min(Nout - col0, kNtTile);   // a multiple of 32
   f32x16 acc[4][2];
-  gemm_nt_tile(A + (size_t)row0 * K, min(M - row0, kNtTile), W + (size_t)col0 * K, W, valid_cols, K, K, smem,
+  // columns past Nout take W's rows from row 0 again (W has Nout rows; the
+  // rest of the tile reads as zero) and are not stored
+  gemm_nt_tile(A + (size_t)row0 * K, min(M - row0, kNtTile), W + (size_t)col0 * K, W, valid_cols, Nout, K, K, smem,
                acc);
 
   const int lane = threadIdx.x & 63, wave = wave_id();

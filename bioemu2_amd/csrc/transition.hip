@@ -81,12 +81,15 @@ __device__ __forceinline__ void copy4_to_lds(__amdgpu_buffer_rsrc_t r, const bf1
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(lds), 4, voff, soff, 0, 0);
 }
 
-// With kTail the residual stream x carries an int8 tail plane (common.h),
-// read with x and rewritten with out (in place).
+// The residual base is res (x itself for the block's "x += T(x)"; another
+// stream for "z = z_init + T(LN(z_init))").  With kTail the residual stream
+// res carries an int8 tail plane (common.h), read with res and rewritten
+// with out (in place).
 template <int C, int HIDDEN, bool kTail>
 __global__ __launch_bounds__(kThreads) void transition_rows_kernel(
-    const bf16* x, const bf16* __restrict__ w1, const bf16* __restrict__ w2, const bf16* __restrict__ w3,
-    const bf16* __restrict__ cf, bf16* out, int8_t* tail, long long P, int use_norm, int residual) {
+    const bf16* x, const bf16* res, const bf16* __restrict__ w1, const bf16* __restrict__ w2,
+    const bf16* __restrict__ w3, const bf16* __restrict__ cf, bf16* out, int8_t* tail, long long P, int use_norm,
+    int residual) {
   using G = Geo<C, HIDDEN>;
   constexpr int HID = G::HID, KS = G::KS;
   extern __shared__ __attribute__((aligned(16))) char smem_raw[];
@@ -220,7 +223,7 @@ __global__ __launch_bounds__(kThreads) void transition_rows_kernel(
     if (kTail) {
       float xv[16];
       const size_t toff = (size_t)pair * C + cb * 32 + 16 * hh;
-      tail_decode16(load8(x + off0), load8(x + off1), exchange_tail_halves(load_tail16(tail + toff), hh), xv);
+      tail_decode16(load8(res + off0), load8(res + off1), exchange_tail_halves(load_tail16(tail + toff), hh), xv);
 #pragma unroll
       for (int u = 0; u < 16; ++u) v[u] += xv[u];
       bf16x8 lo, hi;
@@ -232,7 +235,7 @@ __global__ __launch_bounds__(kThreads) void transition_rows_kernel(
       continue;
     }
     if (residual) {
-      const bf16x8 q0 = load8(x + off0), q1 = load8(x + off1);
+      const bf16x8 q0 = load8(res + off0), q1 = load8(res + off1);
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         v[u] += bf2f(q0[u]);
@@ -251,8 +254,8 @@ __global__ __launch_bounds__(kThreads) void transition_rows_kernel(
 }
 
 template <int C, int HIDDEN>
-int launch_rows(const bf16* x, const bf16* w1, const bf16* w2, const bf16* w3, const bf16* cf, bf16* out,
-                int8_t* tail, long long P, int use_norm, int residual, hipStream_t stream) {
+int launch_rows(const bf16* x, const bf16* res, const bf16* w1, const bf16* w2, const bf16* w3, const bf16* cf,
+                bf16* out, int8_t* tail, long long P, int use_norm, int residual, hipStream_t stream) {
   auto* kern = tail ? transition_rows_kernel<C, HIDDEN, true> : transition_rows_kernel<C, HIDDEN, false>;
   constexpr int smem = Geo<C, HIDDEN>::Smem;
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, smem) !=
@@ -261,30 +264,21 @@ int launch_rows(const bf16* x, const bf16* w1, const bf16* w2, const bf16* w3, c
   const long long nwg = (P + kRowsPerWg - 1) / kRowsPerWg;
   if (nwg > 0x7fffffffLL) return set_error(BIOEMU_ERR_INVALID_ARG, "transition_pair: too many rows");
   KernelTimerScope timed(C == 128 ? "transition_pair" : "transition_msa", stream);
-  hipLaunchKernelGGL(kern, dim3((unsigned)nwg), dim3(kThreads), smem, stream, x, w1, w2, w3, cf, out, tail, P,
+  hipLaunchKernelGGL(kern, dim3((unsigned)nwg), dim3(kThreads), smem, stream, x, res, w1, w2, w3, cf, out, tail, P,
                      use_norm, residual);
   return check_launch("transition_pair");
 }
 
 }  // namespace
-}  // namespace bioemu
-
-using namespace bioemu;
 
 static bool supported(int64_t Dc, int64_t hidden) {
   return (Dc == 64 || Dc == 128) && (hidden == 4 * Dc || hidden == 2 * Dc);
 }
 
-extern "C" size_t bioemu_transition_pair_workspace_bytes(int64_t Dc, int64_t hidden) {
-  if (!supported(Dc, hidden)) return 0;
-  return fold_bytes(2 * hidden, Dc);
-}
-
-extern "C" int bioemu_transition_pair_fwd(const void* x, const float* norm_w, const float* norm_b,
-                                          const void* fc1_w, const void* fc2_w, const void* fc3_w,
-                                          void* out, int8_t* res_tail, void* workspace, size_t workspace_bytes,
-                                          int64_t P, int64_t Dc, int64_t hidden, int use_norm, int residual,
-                                          hipStream_t stream) {
+int transition_pair_res(const void* x, const void* res, const float* norm_w, const float* norm_b, const void* fc1_w,
+                        const void* fc2_w, const void* fc3_w, void* out, int8_t* res_tail, void* workspace,
+                        size_t workspace_bytes, int64_t P, int64_t Dc, int64_t hidden, int use_norm, int residual,
+                        hipStream_t stream) {
   if (!supported(Dc, hidden))
     return set_error(BIOEMU_ERR_UNSUPPORTED,
                      "transition_pair: dim must be 64 or 128 with hidden 4*dim or 2*dim (got %lld, %lld)",
@@ -299,7 +293,9 @@ extern "C" int bioemu_transition_pair_fwd(const void* x, const float* norm_w, co
     return set_error(BIOEMU_ERR_INVALID_ARG, "transition_pair: tensors must be 16-byte aligned");
   if (out == x && !residual)
     return set_error(BIOEMU_ERR_INVALID_ARG, "transition_pair: out may alias x only with residual=1");
-  const size_t need = bioemu_transition_pair_workspace_bytes(Dc, hidden);
+  if (residual && (!res || !aligned16(res)))
+    return set_error(BIOEMU_ERR_INVALID_ARG, "transition_pair: the residual base must be a 16-byte aligned tensor");
+  const size_t need = supported(Dc, hidden) ? fold_bytes(2 * hidden, Dc) : 0;
   if (workspace_bytes < need)
     return set_error(BIOEMU_ERR_WORKSPACE, "transition_pair: workspace %zu < required %zu", workspace_bytes, need);
 
@@ -316,14 +312,34 @@ extern "C" int bioemu_transition_pair_fwd(const void* x, const float* norm_w, co
     w2 = wf + hidden * Dc;
   }
   const bf16* xb = static_cast<const bf16*>(x);
+  const bf16* rb = static_cast<const bf16*>(res);
   const bf16* w3 = static_cast<const bf16*>(fc3_w);
   bf16* ob = static_cast<bf16*>(out);
   const long long rows = (long long)P;
   if (Dc == 128)
-    return hidden == 512 ? launch_rows<128, 512>(xb, w1, w2, w3, cf, ob, res_tail, rows, use_norm, residual, stream)
-                         : launch_rows<128, 256>(xb, w1, w2, w3, cf, ob, res_tail, rows, use_norm, residual, stream);
-  return hidden == 256 ? launch_rows<64, 256>(xb, w1, w2, w3, cf, ob, res_tail, rows, use_norm, residual, stream)
-                       : launch_rows<64, 128>(xb, w1, w2, w3, cf, ob, res_tail, rows, use_norm, residual, stream);
+    return hidden == 512
+               ? launch_rows<128, 512>(xb, rb, w1, w2, w3, cf, ob, res_tail, rows, use_norm, residual, stream)
+               : launch_rows<128, 256>(xb, rb, w1, w2, w3, cf, ob, res_tail, rows, use_norm, residual, stream);
+  return hidden == 256 ? launch_rows<64, 256>(xb, rb, w1, w2, w3, cf, ob, res_tail, rows, use_norm, residual, stream)
+                       : launch_rows<64, 128>(xb, rb, w1, w2, w3, cf, ob, res_tail, rows, use_norm, residual, stream);
+}
+
+}  // namespace bioemu
+
+using namespace bioemu;
+
+extern "C" size_t bioemu_transition_pair_workspace_bytes(int64_t Dc, int64_t hidden) {
+  if (!supported(Dc, hidden)) return 0;
+  return fold_bytes(2 * hidden, Dc);
+}
+
+extern "C" int bioemu_transition_pair_fwd(const void* x, const float* norm_w, const float* norm_b,
+                                          const void* fc1_w, const void* fc2_w, const void* fc3_w,
+                                          void* out, int8_t* res_tail, void* workspace, size_t workspace_bytes,
+                                          int64_t P, int64_t Dc, int64_t hidden, int use_norm, int residual,
+                                          hipStream_t stream) {
+  return transition_pair_res(x, x, norm_w, norm_b, fc1_w, fc2_w, fc3_w, out, res_tail, workspace, workspace_bytes,
+                             P, Dc, hidden, use_norm, residual, stream);
 }
 
 // ---------------------------------------------------------------------------

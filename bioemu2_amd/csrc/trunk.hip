@@ -10,6 +10,12 @@
 // and the 128x128 product on MFMA; the token form is the token LayerNorm and
 // the token GEMM with its residual epilogue (token.hip).
 //
+// Unconditional branch (classifier-free guidance, pairmixer.py:266-273):
+//   z = z_init + uncond_transition(z_norm(z_init))
+// is the token LayerNorm kernel over the pair rows (z_norm, affine, written
+// bf16 into the workspace) and the fused row transition with z_init (and its
+// tail) as the residual base.
+//
 // MSA input embedding (PairMixerMSAModule.forward, pairmixer.py:591-599):
 //   m[b,r,t,:] = msa_proj(cat(msa, has_deletion, deletion_value[, msa_paired]))
 //              + s_proj(emb)[b,t,:]
@@ -210,6 +216,48 @@ extern "C" int bioemu_token_ln_linear_fwd(const void* x, const float* norm_w, co
     return set_error(BIOEMU_ERR_LAUNCH, "token_ln_linear: tail copy failed");
   return token_gemm(kEpiResidualId, false, xn, w, nullptr, nullptr, base, out, Mp, Dc, Dc, M, Mp, M, stream,
                     "token_ln_linear", out_tail);
+}
+
+extern "C" size_t bioemu_trunk_uncond_workspace_bytes(int64_t P, int64_t Dc, int64_t hidden) {
+  const size_t fold = bioemu_transition_pair_workspace_bytes(Dc, hidden);
+  if (P <= 0 || Dc != C || fold == 0) return 0;
+  return (size_t)round_up(P * Dc * 2, 256) + fold;
+}
+
+extern "C" int bioemu_trunk_uncond_fwd(const void* z_init, const int8_t* z_init_tail, const float* z_norm_w,
+                                       const float* z_norm_b, const float* t_norm_w, const float* t_norm_b,
+                                       const void* fc1_w, const void* fc2_w, const void* fc3_w, void* out,
+                                       int8_t* out_tail, void* workspace, size_t workspace_bytes, int64_t P,
+                                       int64_t Dc, int64_t hidden, hipStream_t stream) {
+  if (Dc != C || (hidden != 4 * Dc && hidden != 2 * Dc))
+    return set_error(BIOEMU_ERR_UNSUPPORTED, "trunk_uncond: only 128 channels with hidden 512 or 256 (got %lld, %lld)",
+                     (long long)Dc, (long long)hidden);
+  if (P <= 0 || P > 0x7fffffffLL)
+    return set_error(BIOEMU_ERR_INVALID_ARG, "trunk_uncond: bad row count %lld", (long long)P);
+  if (!z_init || !z_norm_w || !z_norm_b || !t_norm_w || !t_norm_b || !fc1_w || !fc2_w || !fc3_w || !out ||
+      !workspace)
+    return set_error(BIOEMU_ERR_INVALID_ARG, "trunk_uncond: null pointer argument");
+  if ((z_init_tail != nullptr) != (out_tail != nullptr))
+    return set_error(BIOEMU_ERR_INVALID_ARG, "trunk_uncond: z_init_tail and out_tail go together");
+  if (!aligned16(z_init) || !aligned16(out) || !aligned16(workspace) ||
+      (out_tail && (!aligned16(out_tail) || !aligned16(z_init_tail))))
+    return set_error(BIOEMU_ERR_INVALID_ARG, "trunk_uncond: buffers must be 16-byte aligned");
+  if (out == z_init && out_tail != z_init_tail)
+    return set_error(BIOEMU_ERR_INVALID_ARG, "trunk_uncond: in place, out_tail must be z_init_tail");
+  const size_t need = bioemu_trunk_uncond_workspace_bytes(P, Dc, hidden);
+  if (workspace_bytes < need)
+    return set_error(BIOEMU_ERR_WORKSPACE, "trunk_uncond: workspace %zu < required %zu", workspace_bytes, need);
+  char* p = static_cast<char*>(workspace);
+  void* zn = p;
+  const size_t zn_bytes = (size_t)round_up(P * Dc * 2, 256);
+  int rc = token_layernorm(z_init, z_norm_w, z_norm_b, zn, 1, P, P, Dc, stream);
+  if (rc) return rc;
+  // The residual epilogue reads and rewrites one tail buffer: give it z_init's tail first.
+  if (out_tail && out_tail != z_init_tail &&
+      hipMemcpyAsync(out_tail, z_init_tail, (size_t)P * Dc, hipMemcpyDeviceToDevice, stream) != hipSuccess)
+    return set_error(BIOEMU_ERR_LAUNCH, "trunk_uncond: tail copy failed");
+  return transition_pair_res(zn, z_init, t_norm_w, t_norm_b, fc1_w, fc2_w, fc3_w, out, out_tail, p + zn_bytes,
+                             workspace_bytes - zn_bytes, P, Dc, hidden, 1, 1, stream);
 }
 
 extern "C" size_t bioemu_msa_embed_workspace_bytes(int64_t B, int64_t T) {

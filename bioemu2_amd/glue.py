@@ -26,6 +26,7 @@ from torch import Tensor
 
 from . import _ops
 from ._params import PreparedParams
+from .residual import join_stream
 from .transition import Transition
 
 BF16 = torch.bfloat16
@@ -43,9 +44,12 @@ class DistogramModule(nn.Module):
     @torch.no_grad()
     def forward(self, z: Tensor) -> Tensor:
         _ops.require_gpu(z, type(self).__name__)
+        _ops.require_mixed_precision(z, type(self).__name__)
         zb = z.to(BF16).contiguous()
         w, b = self.prepared_params()
-        out = torch.empty(*zb.shape[:-1], w.shape[0], dtype=BF16, device=zb.device)
+        # fp32 callers get the fp32 accumulator (no output rounding); others a bf16 output
+        odt = torch.float32 if z.dtype == torch.float32 else BF16
+        out = torch.empty(*zb.shape[:-1], w.shape[0], dtype=odt, device=zb.device)
         _ops.launch_distogram(zb, w, b, out)
         return out.to(z.dtype)
 
@@ -123,8 +127,11 @@ class PairwiseConditioning(nn.Module):
         z = z_trunk.to(BF16).contiguous()
         rel = token_rel_pos_feats.to(BF16).contiguous()
         ws = self._workspace(z.device)
+        # the conditioning stream is carried as bf16 + int8 tail through the residual transitions and
+        # rounded once at the end (to bf16, or not at all for an fp32 caller under autocast)
         out = torch.empty(*z.shape[:-1], self.a_z, dtype=BF16, device=z.device)
-        _ops.launch_pair_cond_proj(z, rel, *self.prepared_params(), out, ws=ws)
+        tail = torch.empty(out.shape, dtype=torch.int8, device=z.device)
+        _ops.launch_pair_cond_proj(z, rel, *self.prepared_params(), out, ws=ws, out_tail=tail)
         for transition in self.transitions:   # z = transition(z) + z, fused and in place
-            _ops.launch_transition_pair(out, *transition.prepared_params(), out, residual=True, ws=ws)
-        return out.to(z_trunk.dtype)
+            _ops.launch_transition_pair(out, *transition.prepared_params(), out, residual=True, ws=ws, tail=tail)
+        return join_stream(out, tail, z_trunk.dtype)

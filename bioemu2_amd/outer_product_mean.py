@@ -58,6 +58,7 @@ class OuterProductMeanHip(nn.Module):
 
     def forward(self, m: Tensor, mask: Tensor) -> Tensor:
         _ops.require_gpu(m, type(self).__name__)
+        _ops.require_mixed_precision(m, type(self).__name__)
         return torch.ops.bioemu_mi355x.outer_product_mean(m, mask, *self.prepared_params())
 
 

@@ -64,6 +64,7 @@ class PairWeightedAveraging(nn.Module):
 
     def forward(self, m: Tensor, z: Tensor, mask: Tensor, chunk_heads: bool = False) -> Tensor:
         _ops.require_gpu(m, type(self).__name__)
+        _ops.require_mixed_precision(m, type(self).__name__)
         if self.inf != 1e6:
             raise ValueError(f"PairWeightedAveraging: only inf=1e6 is supported (got {self.inf})")
         return torch.ops.bioemu_mi355x.pair_weighted_averaging(m, z, mask, *self.prepared_params(), self.num_heads)

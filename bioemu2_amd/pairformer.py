@@ -115,7 +115,9 @@ class PairformerBlockHip(nn.Module):
         return s, z
 
     def forward(self, s: Tensor, z: Tensor, token_mask: Tensor) -> tuple[Tensor, Tensor]:
-        """Out-of-place block: returns new ``(s, z)`` in the input dtypes (streams carried with tails)."""
+        """Out-of-place block: returns new ``(s, z)`` in the input dtypes (streams carried with tails).  fp32
+        inputs need bf16 autocast (the block has no fp32 arithmetic)."""
+        _ops.require_mixed_precision(z, type(self).__name__)
         (s_hi, s_tail), (z_hi, z_tail) = split_stream(s), split_stream(z)
         self.forward_(s_hi, z_hi, token_mask, s_tail, z_tail)
         return join_stream(s_hi, s_tail, s.dtype), join_stream(z_hi, z_tail, z.dtype)

@@ -87,6 +87,7 @@ class PairMixerLayerHip(nn.Module, _WorkspaceMixin):
         return s, z
 
     def forward(self, s: Tensor, z: Tensor, pair_mask: Tensor) -> tuple[Tensor, Tensor]:
+        _ops.require_mixed_precision(z, type(self).__name__)
         z_hi, z_tail = split_stream(z)
         self.forward_(s, z_hi, pair_mask, z_tail)
         return s, join_stream(z_hi, z_tail, z.dtype)
@@ -166,6 +167,7 @@ class PairMixerMSALayerHip(nn.Module, _WorkspaceMixin):
     def forward(
         self, s: Tensor, z: Tensor, m: Tensor, token_mask: Tensor, msa_mask: Tensor, chunk_heads_pwa: bool = False
     ) -> tuple[Tensor, Tensor, Tensor]:
+        _ops.require_mixed_precision(z, type(self).__name__)
         (z_hi, z_tail), (m_hi, m_tail) = split_stream(z), split_stream(m)
         self.forward_(s, z_hi, m_hi, token_mask, msa_mask, chunk_heads_pwa, z_tail, m_tail)
         return s, join_stream(z_hi, z_tail, z.dtype), join_stream(m_hi, m_tail, m.dtype)
@@ -217,6 +219,7 @@ class PairMixerModuleHip(nn.Module, _WorkspaceMixin):
         return s, z
 
     def forward(self, s: Tensor, z: Tensor, pair_mask: Tensor) -> tuple[Tensor, Tensor]:
+        _ops.require_mixed_precision(z, type(self).__name__)
         z_hi, z_tail = split_stream(z)
         self.forward_(s, z_hi, pair_mask, z_tail)
         return s, join_stream(z_hi, z_tail, z.dtype)
@@ -302,6 +305,7 @@ class PairMixerMSAModuleHip(nn.Module, _WorkspaceMixin):
         return z
 
     def forward(self, s, z, emb, msa, msa_mask, has_deletion, deletion_value, msa_paired, token_pad_mask):
+        _ops.require_mixed_precision(z, type(self).__name__)
         z_hi, z_tail = split_stream(z)
         self.forward_(z_hi, emb, msa, msa_mask, has_deletion, deletion_value, msa_paired, token_pad_mask, z_tail)
         return s, join_stream(z_hi, z_tail, z.dtype)
@@ -317,6 +321,9 @@ class PairMixerTrunkHip(nn.Module, _WorkspaceMixin):
     loop of :275-296: s and z start at zero; every pass sets s = s_init + s_recycle(s_norm(s)) and
     z = z_init + z_recycle(z_norm(z)), runs the MSA module (single updates off) and the PairMixer stack.
     z is carried as one bf16 + tail stream through every pass; s and z come back in s_init's / z_init's dtype.
+    With ``use_unconditional_branch=True`` the trunk also holds ``uncond_transition`` (:193-200), and
+    ``forward(..., unconditional=True)`` returns s_init and z_init + uncond_transition(z_norm(z_init))
+    (:266-273) without running the recycling loop.
     """
 
     def __init__(
@@ -334,6 +341,8 @@ class PairMixerTrunkHip(nn.Module, _WorkspaceMixin):
         opm_variant: str = "vanilla",
         use_paired_feature: bool = True,
         num_tokens: int = NUM_TOKENS,
+        use_unconditional_branch: bool = False,
+        transition_chunk_size: int | None = None,
     ) -> None:
         super().__init__()
         self.msa_module = PairMixerMSAModuleHip(token_s, msa_s, token_z, s_input_dim, msa_blocks, msa_dropout,
@@ -346,6 +355,10 @@ class PairMixerTrunkHip(nn.Module, _WorkspaceMixin):
         self.z_recycle = nn.Linear(token_z, token_z, bias=False)
         self.s_norm = nn.LayerNorm(token_s)
         self.z_norm = nn.LayerNorm(token_z)
+        # Unconditional branch (:193-200): z = z_init + uncond_transition(z_norm(z_init)).
+        self.use_unconditional_branch = use_unconditional_branch
+        if use_unconditional_branch:
+            self.uncond_transition = Transition(dim=token_z, hidden=token_z * 4, chunk_size=transition_chunk_size)
         self._ws = None
 
     def workspace_bytes(self, B: int, S: int, N: int, token_s: int) -> int:
@@ -354,11 +367,37 @@ class PairMixerTrunkHip(nn.Module, _WorkspaceMixin):
                    int(_ops.lib().bioemu_token_ln_linear_workspace_bytes(B * N, token_s)))
 
     @torch.no_grad()
-    def forward(self, s_init: Tensor, z_init: Tensor, s_inputs: Tensor, feats: dict,
-                num_steps_recycle: int = 0) -> tuple[Tensor, Tensor]:
-        if num_steps_recycle < 0:
-            raise ValueError("num_steps_recycle must be non-negative; use unconditional=True.")
+    def forward_unconditional(self, s_init: Tensor, z_init: Tensor) -> tuple[Tensor, Tensor]:
+        """The unconditional branch (pairmixer.py:266-273): s = s_init and z = z_init + uncond_transition(
+        z_norm(z_init)), one HIP entry (LayerNorm, fused row transition with z_init as the residual base)."""
+        if not self.use_unconditional_branch:
+            raise ValueError(
+                "Passing unconditional=True at inference time requires use_unconditional_branch=True at __init__"
+            )
         _ops.require_gpu(z_init, type(self).__name__)
+        _ops.require_mixed_precision(z_init, type(self).__name__)
+        D = z_init.shape[-1]
+        P = z_init.numel() // D
+        t = self.uncond_transition
+        bf16, f32 = torch.bfloat16, torch.float32
+        z0, z0_tail = split_stream(z_init)
+        ws = self._workspace(_ops.trunk_uncond_workspace_bytes(P, D, t.hidden), z_init.device)
+        _ops.launch_trunk_uncond(
+            z0, self.z_norm.weight.to(f32).contiguous(), self.z_norm.bias.to(f32).contiguous(),
+            t.norm.weight.to(f32).contiguous(), t.norm.bias.to(f32).contiguous(), t.fc1.weight.to(bf16).contiguous(),
+            t.fc2.weight.to(bf16).contiguous(), t.fc3.weight.to(bf16).contiguous(), z0, z_init_tail=z0_tail,
+            out_tail=z0_tail, ws=ws)
+        return s_init, join_stream(z0, z0_tail, z_init.dtype)
+
+    @torch.no_grad()
+    def forward(self, s_init: Tensor, z_init: Tensor, s_inputs: Tensor, feats: dict,
+                num_steps_recycle: int = 0, unconditional: bool = False) -> tuple[Tensor, Tensor]:
+        if not unconditional and num_steps_recycle < 0:
+            raise ValueError("num_steps_recycle must be non-negative; use unconditional=True.")
+        if unconditional:
+            return self.forward_unconditional(s_init, z_init)
+        _ops.require_gpu(z_init, type(self).__name__)
+        _ops.require_mixed_precision(z_init, type(self).__name__)
         B, N = z_init.shape[:2]
         S = feats["msa"].shape[1]
         ws = self._workspace(self.workspace_bytes(B, S, N, s_init.shape[-1]), z_init.device)

@@ -99,6 +99,7 @@ class TriangleAttentionHip(nn.Module):
 
     def forward(self, z: Tensor, mask: Tensor) -> Tensor:
         _ops.require_gpu(z, type(self).__name__)
+        _ops.require_mixed_precision(z, type(self).__name__)
         if self.inf != 1e6:
             raise ValueError("TriangleAttentionHip: only inf=1e6 (the reference masking value) is supported")
         return torch.ops.bioemu_mi355x.triangle_attention(

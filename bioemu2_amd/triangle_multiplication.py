@@ -101,6 +101,7 @@ class TriangleMultiplicationHip(_TriMulBase):
 
     def forward(self, x: Tensor, mask: Tensor) -> Tensor:
         _ops.require_gpu(x, type(self).__name__)
+        _ops.require_mixed_precision(x, type(self).__name__)
         return torch.ops.bioemu_mi355x.trimul(
             x, _ops.mask_u8(mask), *self.prepared_params(), self.mode == "outgoing"
         )

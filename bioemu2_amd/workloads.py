@@ -303,8 +303,9 @@ class BlockWorkload(Workload):
 
 class Config1Workload(BlockWorkload):
     """Config 1: the reference's CPU-runnable case, one block at N=64 with fp32 z [1,64,64,128] and
-    s [1,64,384], all tokens valid.  A step is the out-of-place ``forward``: fp32 in, streams split into
-    bf16 + tail, the block, fp32 out.  The CPU baseline is the whole fp32 oracle block at the same size."""
+    s [1,64,384], all tokens valid.  A step is the out-of-place ``forward`` under bf16 autocast (the trunk's
+    policy; the block has no fp32 arithmetic): fp32 in, streams split into bf16 + tail, the block, fp32 out.
+    The CPU baseline is the whole fp32 oracle block at the same size."""
 
     def __init__(self, device, n: int = 64, seed: int = 0):
         super().__init__(device, n, seed)
@@ -318,7 +319,8 @@ class Config1Workload(BlockWorkload):
         self.z32 = self.z_cpu.float().to(device)
 
     def step(self) -> None:
-        self.module(self.s32, self.z32, self.tok)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            self.module(self.s32, self.z32, self.tok)
 
 
 class TrunkWorkload(BlockWorkload):

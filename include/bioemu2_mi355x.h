@@ -228,11 +228,12 @@ int bioemu_swa_fwd(const void* s, const void* z, const uint8_t* mask, const floa
  * Distogram head: out[b,i,j,:] = (z[b,i,j] + z[b,j,i]) w^T + b.
  * Replaces DistogramModule.forward (src/bioemu2/biomoa/modules/embedders.py:191-206).
  * z: [B, N, N, c_z] bf16; w: [num_bins, c_z] bf16; b: [num_bins] fp32;
- * out: [B, N, N, num_bins] bf16 (exactly symmetric in i, j).
+ * out: [B, N, N, num_bins], bf16 (out_f32 = 0) or fp32 (out_f32 = 1: the fp32
+ * accumulator plus the bias, unrounded), exactly symmetric in i, j.
  * Supported: c_z = 128, 1 <= num_bins <= 128.
  */
 int bioemu_distogram_fwd(const void* z, const void* w, const float* b, void* out, int64_t B, int64_t N,
-                         int64_t c_z, int64_t num_bins, hipStream_t stream);
+                         int64_t c_z, int64_t num_bins, int out_f32, hipStream_t stream);
 
 /*
  * PairwiseConditioning input projection: out = LN([z_trunk, rel]) w^T (LayerNorm
@@ -241,13 +242,15 @@ int bioemu_distogram_fwd(const void* z, const void* w, const float* b, void* out
  * (src/bioemu2/biomoa/modules/diffusion.py:509-525); its transitions run
  * bioemu_transition_pair_fwd (hidden = 2*a_z) with residual=1.
  * z_trunk, rel: [P, 128] bf16 rows; ln_w, ln_b: [256] fp32; w: [a_z, 256] bf16;
- * out: [P, a_z] bf16.  The workspace holds w with the LayerNorm folded in.
+ * out: [P, a_z] bf16; with out_tail (int8 [P, a_z], optional) out is written as
+ * a residual stream (bf16 value + int8 tail, the form the transitions' res_tail
+ * updates in place).  The workspace holds w with the LayerNorm folded in.
  * Supported: token_z = c_rel = a_z = 128.
  */
 size_t bioemu_pair_cond_workspace_bytes(int64_t token_z, int64_t c_rel, int64_t a_z);
 int bioemu_pair_cond_proj_fwd(const void* z_trunk, const void* rel, const float* ln_w, const float* ln_b,
-                              const void* w, void* out, void* workspace, size_t workspace_bytes, int64_t P,
-                              int64_t token_z, int64_t c_rel, int64_t a_z, hipStream_t stream);
+                              const void* w, void* out, int8_t* out_tail, void* workspace, size_t workspace_bytes,
+                              int64_t P, int64_t token_z, int64_t c_rel, int64_t a_z, hipStream_t stream);
 
 /*
  * Fused OuterProductMean.
@@ -304,6 +307,25 @@ size_t bioemu_token_ln_linear_workspace_bytes(int64_t M, int64_t Dc);
 int bioemu_token_ln_linear_fwd(const void* x, const float* norm_w, const float* norm_b, const void* w,
                                const void* base, const int8_t* base_tail, void* out, int8_t* out_tail,
                                void* workspace, size_t workspace_bytes, int64_t M, int64_t Dc, hipStream_t stream);
+
+/*
+ * Trunk unconditional branch (classifier-free guidance): out = z_init +
+ * uncond_transition(z_norm(z_init)).  Replaces `z = z_init + self.uncond_
+ * transition(self.z_norm(z_init))` (PairMixerSequenceEmbedder.forward,
+ * src/bioemu2/biomoa/modules/pairmixer.py:266-273; z_norm = LayerNorm(token_z)
+ * at :190, uncond_transition = Transition(token_z, 4 token_z) at :194-200,
+ * transition.py:52-91).  z_init, out bf16 [P][128]; z_norm_w/b and the
+ * transition's norm.weight/bias t_norm_w/b fp32 [128]; fc1_w, fc2_w bf16
+ * [hidden][128]; fc3_w bf16 [128][hidden]; hidden = 512 or 256.  z_init_tail /
+ * out_tail (int8 [P][128]) carry z_init and out as residual streams, both given
+ * or both NULL; the LayerNorm reads z_init's bf16 part.  out may alias z_init
+ * (then out_tail must be z_init_tail).  workspace: *_workspace_bytes(P, 128, hidden).
+ */
+size_t bioemu_trunk_uncond_workspace_bytes(int64_t P, int64_t Dc, int64_t hidden);
+int bioemu_trunk_uncond_fwd(const void* z_init, const int8_t* z_init_tail, const float* z_norm_w,
+                            const float* z_norm_b, const float* t_norm_w, const float* t_norm_b, const void* fc1_w,
+                            const void* fc2_w, const void* fc3_w, void* out, int8_t* out_tail, void* workspace,
+                            size_t workspace_bytes, int64_t P, int64_t Dc, int64_t hidden, hipStream_t stream);
 
 /*
  * MSA input embedding.  Replaces PairMixerMSAModule.forward's

@@ -72,6 +72,7 @@ from .pairformer_ref import (  # noqa: F401
     pairmixer_msa_layer,
     pairmixer_msa_module,
     pairmixer_trunk,
+    pairmixer_uncond,
     pairwise_conditioning,
     sliding_window_keys,
     transition,

@@ -32,6 +32,7 @@ __all__ = [
     "pairmixer_module",
     "pairmixer_msa_module",
     "pairmixer_trunk",
+    "pairmixer_uncond",
 ]
 
 
@@ -531,6 +532,15 @@ def pairmixer_msa_module(
     for i in range(msa_blocks):
         _, z, m = pairmixer_msa_layer(None, z, m, pm, feats["msa_mask"], _sub(params, f"layers.{i}"))
     return z
+
+
+def pairmixer_uncond(s_init: Tensor, z_init: Tensor, params: dict) -> tuple[Tensor, Tensor]:
+    """The unconditional branch of PairMixerSequenceEmbedder.forward (pairmixer.py:266-273): s = s_init and
+    z = z_init + uncond_transition(z_norm(z_init)), the transition being Transition(token_z, 4 token_z) with its
+    own LayerNorm (:194-200; transition.py:52-91)."""
+    s_init, z_init = _f32(s_init), _f32(z_init)
+    zn = _ln(z_init, params, "z_norm")  # :272
+    return s_init, z_init + transition(zn, _sub(params, "uncond_transition"))
 
 
 def pairmixer_trunk(

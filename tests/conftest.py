@@ -27,6 +27,15 @@ def gpu_device() -> torch.device:
     return torch.device("cuda")
 
 
+@pytest.fixture
+def bf16_autocast():
+    """bf16 autocast on the GPU for the test: the trunk ops and their compositions have no fp32 arithmetic and
+    refuse fp32 inputs outside autocast; under it (the reference trunk's policy) fp32 inputs take their bf16
+    path with fp32 in and out."""
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        yield
+
+
 def pytest_runtest_setup(item):
     # Name the case before any GPU work so a crash log identifies it.
     if item.get_closest_marker("gpu") is not None:

@@ -3,7 +3,8 @@
 The block carries its residual streams with int8 tails (~16 significant bits)
 and returns fp32 for fp32 inputs, so it is held to the bf16 bound itself:
 max-abs <= 2e-2 and rel-L2 <= 1e-2 on every valid element, at the headline
-shape (N = 768, 76 padded tokens) too.
+shape (N = 768, 76 padded tokens) too.  The tests run under bf16 autocast (the
+reference trunk's policy), which fp32 inputs need.
 """
 
 from __future__ import annotations
@@ -16,7 +17,7 @@ from bioemu2_amd.pairformer import PairformerBlockHip
 from bioemu2_amd.workloads import init_module
 from tests._helpers import max_abs, rel_l2, state
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("bf16_autocast")]
 
 MAX_ABS = 2e-2   # north_star bf16 bound
 REL_L2 = 1e-2
@@ -195,3 +196,13 @@ def test_trunk_48_blocks_config5(gpu_device):
     assert torch.isfinite(za).all() and torch.isfinite(sa).all()
     print(f"trunk |z|max={za.abs().max().item():.2f} |s|max={sa.abs().max().item():.2f}", flush=True)
     assert torch.equal(za, zb) and torch.equal(sa, sb)
+
+
+def test_block_fp32_outside_autocast_is_refused(gpu_device):
+    """The block has no fp32 arithmetic: fp32 inputs with autocast off raise instead of computing in bf16."""
+    blk = _block(gpu_device)
+    s, z, tok = _inputs(32, 0, gpu_device)
+    with torch.autocast("cuda", enabled=False):
+        with pytest.raises(ValueError, match="autocast"):
+            blk(s, z, tok)
+        blk(s.to(torch.bfloat16), z.to(torch.bfloat16), tok)   # bf16 inputs select the bf16 path explicitly

@@ -15,6 +15,10 @@
 * ``pairmixer_msa_module``: 1 block equals msa_embed + the MSA layer (with s = None and the pair mask).
 * ``pairmixer_trunk``: with 0 PairMixer blocks and 0 MSA blocks, one pass is the two recycling updates of
   zero; a second pass recycles the first pass's output (closed forms from ``ln_linear``).
+* ``pairmixer_uncond``: brute-force numpy loops; a zero ``fc3`` returns z_init (and s_init) exactly; a
+  ``z_norm`` with zero weight feeds every row the constant ``z_norm.bias``, whose own LayerNorm is the
+  transition norm's bias, so every row gains the same closed-form vector; skipping ``z_norm`` (a negative
+  control) changes the result.
 """
 
 from __future__ import annotations
@@ -177,3 +181,51 @@ def test_trunk_modules_state_dict_layout():
     assert {k.split(".")[2] for k in sd if k.startswith("msa_module.layers.")} == {"0", "1"}
     assert "pairmixer_module.layers.2.tri_mul_in.p_out.weight" in sd
     assert "msa_module.layers.1.outer_product_mean.proj_o.bias" in sd
+
+
+def _np_transition(x, P, prefix):
+    w1, w2, w3 = (P[f"{prefix}.fc{i}.weight"].double().numpy() for i in (1, 2, 3))
+    xn = np_ln(x, P[f"{prefix}.norm.weight"].double().numpy(), P[f"{prefix}.norm.bias"].double().numpy())
+    a = w1 @ xn
+    return w3 @ (a / (1 + np.exp(-a)) * (w2 @ xn))
+
+
+def test_pairmixer_uncond_closed_forms():
+    torch.manual_seed(0)
+    mod = PairMixerTrunkHip(32, 128, 20, msa_blocks=0, num_blocks=0, use_unconditional_branch=True)
+    P = state(randomize_params(mod, 3))
+    g = torch.Generator().manual_seed(5)
+    s_init, z_init = torch.randn(1, 5, 32, generator=g), torch.randn(1, 5, 5, 128, generator=g) * 2
+    s, z = oracle.pairmixer_uncond(s_init, z_init, P)
+    assert torch.equal(s, s_init)
+    zw, zb = P["z_norm.weight"].double().numpy(), P["z_norm.bias"].double().numpy()
+    for i in range(5):
+        for j in range(5):
+            row = z_init[0, i, j].double().numpy()
+            want = row + _np_transition(np_ln(row, zw, zb), P, "uncond_transition")
+            np.testing.assert_allclose(z[0, i, j].numpy(), want, rtol=1e-5, atol=1e-5)
+    Z = dict(P, **{"uncond_transition.fc3.weight": torch.zeros(128, 512)})
+    assert torch.equal(oracle.pairmixer_uncond(s_init, z_init, Z)[1], z_init)
+    # z_norm with zero weight and a constant bias makes every transition input the row (0.7, ..., 0.7), whose
+    # LayerNorm is exactly the transition norm's bias: every row gains W3 (silu(W1 b) * (W2 b)), b that bias
+    C = dict(P, **{"z_norm.weight": torch.zeros(128), "z_norm.bias": torch.full((128,), 0.7)})
+    tb = P["uncond_transition.norm.bias"].double().numpy()
+    w1, w2, w3 = (P[f"uncond_transition.fc{i}.weight"].double().numpy() for i in (1, 2, 3))
+    a = w1 @ tb
+    const = w3 @ (a / (1 + np.exp(-a)) * (w2 @ tb))
+    zc = oracle.pairmixer_uncond(s_init, z_init, C)[1]
+    np.testing.assert_allclose((zc - z_init).reshape(-1, 128).numpy(), np.broadcast_to(const, (25, 128)),
+                               rtol=1e-4, atol=1e-4)
+    skip = z_init + oracle.transition(z_init, {k[len("uncond_transition."):]: v for k, v in P.items()
+                                               if k.startswith("uncond_transition.")})
+    assert (skip - z).abs().max() > 1e-2
+
+
+def test_trunk_unconditional_state_dict_layout():
+    """uncond_transition = Transition(token_z, 4 token_z) exists only with use_unconditional_branch (:193-200)."""
+    sd = PairMixerTrunkHip(64, 128, 20, msa_blocks=0, num_blocks=0, use_unconditional_branch=True).state_dict()
+    assert tuple(sd["uncond_transition.fc1.weight"].shape) == (512, 128)
+    assert tuple(sd["uncond_transition.fc3.weight"].shape) == (128, 512)
+    assert tuple(sd["uncond_transition.norm.weight"].shape) == (128,)
+    plain = PairMixerTrunkHip(64, 128, 20, msa_blocks=0, num_blocks=0).state_dict()
+    assert not any(k.startswith("uncond_transition.") for k in plain)

@@ -15,7 +15,7 @@ from bioemu2_amd.pairmixer import PairMixerLayerHip, PairMixerMSALayerHip
 from bioemu2_amd.workloads import init_module
 from tests._helpers import max_abs, rel_l2, state
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("bf16_autocast")]
 
 
 def _tok(B, n, n_pad, device):

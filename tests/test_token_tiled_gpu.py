@@ -79,3 +79,16 @@ def test_swa_denoiser_shape_residual(gpu_device):
         _ops.launch_swa(res, z, _ops.mask_u8(mask), *P, res, 4, multiplicity=8, residual=True)
     want = s.float() + upd.float()
     assert max_abs(res.float().cpu(), want.cpu()) <= 2 ** -7 * (want.abs().max().item() + 1)
+
+
+def test_swa_denoiser_shape_narrow(gpu_device):
+    """c_s = 64 (2 heads) at 6144 atoms x 8 copies: 49152 x 64 outputs take the tiled output projection with fewer
+    output columns than half a tile, whose columns past the 64 weight rows must read as zero, not past the weight."""
+    print("swa narrow: c_s=64 heads=2 atoms=6144 M=8", flush=True)
+    mod = _swa_module(gpu_device, c_s=64, c_z=16, heads=2, initial_norm=False)
+    s, z, mask = _swa_inputs(1, 8, 192, 128, 64, 16, gpu_device, pad=40, seed=5)
+    with torch.no_grad():
+        got = mod(s, z, mask, multiplicity=8).float().cpu()
+    want = oracle.attention_pair_bias_sliding_window(s.cpu(), z.cpu(), mask.cpu(), state(mod), 2, multiplicity=8,
+                                                     initial_norm=False)
+    _check(got, want, "swa 6144 atoms x 8, c_s 64")

@@ -80,11 +80,13 @@ def test_config4_shape_n768(gpu_device, starting):
     assert err <= ATOL and rl2 <= RTOL_L2
 
 
-def test_config5_shape_n2048(gpu_device):
+@pytest.mark.parametrize("starting", [True, False])
+def test_config5_shape_n2048(gpu_device, starting):
     """Config 5's pair shape: N=2048 with the last 102 tokens padded (32 key blocks, the last one partly masked),
-    starting node, against the row-chunked fp32 oracle."""
+    starting and ending node, against the row-chunked fp32 oracle."""
     n, n_pad = 2048, 102
-    m = _module(True, gpu_device)
+    print(f"triatt n=2048 starting={starting}: GPU", flush=True)
+    m = _module(starting, gpu_device)
     g = torch.Generator().manual_seed(5)
     z = torch.randn(1, n, n, C, generator=g).to(torch.bfloat16)
     tok = torch.ones(1, n, dtype=torch.bool)
@@ -92,9 +94,9 @@ def test_config5_shape_n2048(gpu_device):
     pm = oracle.pair_mask_from_token_mask(tok)
     with torch.no_grad():
         got = m(z.to(gpu_device), pm.to(gpu_device)).float().cpu()
-    want = oracle.triangle_attention(z.float(), pm, state(m), H, True, row_chunk=32)
+    want = oracle.triangle_attention(z.float(), pm, state(m), H, starting, row_chunk=32)
     err, rl2 = max_abs(got, want), rel_l2(got, want)
-    print(f"triatt n=2048 padded starting=True: max_abs={err:.3e} rel_l2={rl2:.3e}", flush=True)
+    print(f"triatt n=2048 padded starting={starting}: max_abs={err:.3e} rel_l2={rl2:.3e}", flush=True)
     assert err <= ATOL and rl2 <= RTOL_L2
 
 

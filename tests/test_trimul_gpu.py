@@ -64,11 +64,13 @@ def test_matches_oracle_n768_token_padding(gpu_device, mode):
     assert err <= ATOL and rl2 <= RTOL_L2
 
 
-def test_matches_oracle_n2048_token_padding(gpu_device):
+@pytest.mark.parametrize("mode", ["outgoing", "incoming"])
+def test_matches_oracle_n2048_token_padding(gpu_device, mode):
     """Config 5's pair shape: N=2048, last 102 tokens padded (planes padded to 2048, eight 256-wide contraction
-    tiles), outgoing, against the fp32 oracle."""
+    tiles), both directions, against the fp32 oracle."""
     n = 2048
-    m = _module("outgoing", gpu_device)
+    print(f"trimul {mode} n=2048: GPU", flush=True)
+    m = _module(mode, gpu_device)
     g = torch.Generator().manual_seed(5)
     x = torch.randn(1, n, n, D, generator=g).to(torch.bfloat16)
     tok = torch.ones(1, n, dtype=torch.bool)
@@ -76,9 +78,9 @@ def test_matches_oracle_n2048_token_padding(gpu_device):
     pm = oracle.pair_mask_from_token_mask(tok)
     with torch.no_grad():
         got = m(x.to(gpu_device), pm.to(gpu_device)).float().cpu()
-    want = oracle.trimul(x.float(), pm, state(m), "outgoing")
+    want = oracle.trimul(x.float(), pm, state(m), mode)
     err, rl2 = max_abs(got, want), rel_l2(got, want)
-    print(f"trimul outgoing n=2048: max_abs={err:.3e} rel_l2={rl2:.3e}", flush=True)
+    print(f"trimul {mode} n=2048: max_abs={err:.3e} rel_l2={rl2:.3e}", flush=True)
     assert err <= ATOL and rl2 <= RTOL_L2
 
 
@@ -183,16 +185,6 @@ def test_fused_residual_in_place(gpu_device, mode):
     assert max_abs(z.float(), ref) <= 2 ** -7 * ref.abs().max().item()
 
 
-def test_fp32_input_roundtrip(gpu_device):
-    m = _module("outgoing", gpu_device)
-    x, mask = _inputs(40, gpu_device)
-    with torch.no_grad():
-        a = m(x.float(), mask)
-        b = m(x, mask)
-    assert a.dtype == torch.float32
-    assert torch.equal(a, b.float())
-
-
 def test_rejects_cpu_tensors():
     m = TriangleMultiplicationHip(dim=D)
     with pytest.raises(RuntimeError):
@@ -203,3 +195,18 @@ def test_rejects_unsupported_dim(gpu_device):
     m = TriangleMultiplicationHip(dim=64).to(gpu_device)
     with pytest.raises(ValueError):
         m(torch.zeros(1, 8, 8, 64, device=gpu_device), torch.ones(1, 8, 8, dtype=torch.bool, device=gpu_device))
+
+
+def test_fp32_outside_autocast_is_refused(gpu_device):
+    """fp32 inputs with autocast off ask for the reference's IEEE fp32 contraction (TriangleMultiplicationCueq's
+    default matmul_precision="ieee", triangle_multiplication.py:117), which this op does not compute: ValueError.
+    Under bf16 autocast the same fp32 input takes the bf16 path and returns fp32."""
+    m = _module("outgoing", gpu_device)
+    x, mask = _inputs(40, gpu_device)
+    with torch.no_grad():
+        with pytest.raises(ValueError, match="autocast"):
+            m(x.float(), mask)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            got = m(x.float(), mask)
+        want = m(x, mask)
+    assert got.dtype == torch.float32 and torch.equal(got.to(torch.bfloat16), want)

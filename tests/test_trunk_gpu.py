@@ -19,7 +19,7 @@ from bioemu2_amd.residual import join_stream, split_stream
 from bioemu2_amd.workloads import init_module
 from tests._helpers import max_abs, rel_l2, state
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("bf16_autocast")]
 
 
 def _check(name, got, want, sel=None):
@@ -130,12 +130,19 @@ def test_msa_embed_matches_oracle(gpu_device, paired):
 
 
 def _e2e(name, got, want, sel, layers):
-    """A stack end to end: rel-L2 within the bound; max-abs within the bound per layer it holds (each layer's
-    own error is held to the bound alone by the layer-by-layer checks, and consecutive layers' errors add)."""
+    """A stack end to end against the oracle stack: rel-L2 at the plain bound (1e-2); max-abs at 2e-2 sqrt(layers).
+
+    Each layer is held to the plain bound alone, on its own input, by the layer-by-layer checks.  Its error is
+    the rounding of its MFMA operands (LayerNorm outputs and weights to bf16; the residual streams carry ~16
+    bits and add nothing), independent from layer to layer, so end to end the errors add in quadrature:
+    measured 1.3-1.6e-2 for one layer, 1.9-2.2e-2 over two and 2.4e-2 over four.  The bound 2e-2 sqrt(layers)
+    is the per-layer bound grown that way; rel-L2 stays at 1e-2 (measured <= 3.9e-3 over four layers)."""
     g, w = got.float().cpu()[sel], want.float()[sel]
     err, rl2 = max_abs(g, w), rel_l2(g, w)
-    print(f"{name} (end to end, {layers} layers): max_abs={err:.3e} rel_l2={rl2:.3e}", flush=True)
-    assert rl2 <= 1e-2 and err <= 2e-2 * layers, (name, err, rl2)
+    bound = 2e-2 * layers ** 0.5
+    print(f"{name} (end to end, {layers} layers): max_abs={err:.3e} (bound {bound:.2e}) rel_l2={rl2:.3e}",
+          flush=True)
+    assert rl2 <= 1e-2 and err <= bound, (name, err, rl2)
 
 
 def test_pairmixer_module_is_its_layers_each_within_bound(gpu_device):
@@ -210,6 +217,38 @@ def test_pairmixer_trunk_matches_oracle(gpu_device, recycles):
     layers = 2 * (recycles + 1)
     _e2e(f"trunk recycles={recycles} z", z_got, z_want, oracle.pair_mask_from_token_mask(tok), layers)
     _e2e(f"trunk recycles={recycles} s", s_got, s_want, tok, 1)
+
+
+@pytest.mark.parametrize("bf16_exact", [True, False])
+def test_trunk_unconditional_branch_matches_oracle(gpu_device, bf16_exact):
+    """z = z_init + uncond_transition(z_norm(z_init)) and s = s_init (pairmixer.py:266-273) against the oracle;
+    the recycling loop does not run.  z_init is bf16-representable or a general fp32 stream (its LayerNorm then
+    reads the bf16 part of the stream)."""
+    B, T, d = 2, 50, gpu_device
+    print(f"trunk uncond: B={B} T={T} bf16_exact={bf16_exact}", flush=True)
+    torch.manual_seed(0)
+    mod = init_module(PairMixerTrunkHip(384, 128, 455, msa_blocks=0, num_blocks=0, use_unconditional_branch=True), 0)
+    mod = mod.to(d).eval()
+    g = torch.Generator().manual_seed(6)
+    s_init = _randn((B, T, 384), g)
+    z_init = _randn((B, T, T, 128), g, 2.0) if bf16_exact else torch.randn(B, T, T, 128, generator=g) * 2.0
+    s_got, z_got = mod(s_init.to(d), z_init.to(d), None, {}, unconditional=True)
+    assert torch.equal(s_got.cpu(), s_init)
+    assert z_got.dtype == torch.float32
+    _, z_want = oracle.pairmixer_uncond(s_init, z_init, state(mod))
+    _check(f"trunk uncond z (bf16_exact={bf16_exact})", z_got, z_want)
+    if bf16_exact:
+        with torch.no_grad():
+            mod.uncond_transition.fc3.weight.zero_()
+        _, z_zero = mod(s_init.to(d), z_init.to(d), None, {}, unconditional=True)
+        assert torch.equal(z_zero.cpu(), z_init)   # a zero transition output leaves z_init bit for bit
+
+
+def test_trunk_unconditional_requires_branch(gpu_device):
+    mod = PairMixerTrunkHip(384, 128, 455, msa_blocks=0, num_blocks=0).to(gpu_device)
+    with pytest.raises(ValueError, match="use_unconditional_branch=True"):
+        mod(torch.zeros(1, 4, 384, device=gpu_device), torch.zeros(1, 4, 4, 128, device=gpu_device), None, {},
+            unconditional=True)
 
 
 def test_trunk_rejects_negative_recycles(gpu_device):
