@@ -15,12 +15,15 @@
 //   update[i, j] = (g[i,j] * o[i,j]) Wo^T      (written back in z's frame)
 //
 // Two kernels:
-//   triatt_proj  : LN + all five projections (q, k, v, g, bias) on MFMA with
+//   triatt_proj  : LN + the key-side projections (k, v, bias) on MFMA with
 //                  weights staged once per workgroup in LDS; writes the frame-
-//                  ordered operands of the attention and a frame-ordered mask.
-//   triatt_flash : per (b, row i, 256 queries) online-softmax attention over
-//                  all keys, 4 heads, with the gate and the output projection
-//                  fused in the epilogue and the residual added in place.
+//                  ordered keys and values of every frame row, the bias and a
+//                  frame-ordered mask.
+//   triatt_flash : per (b, row i, 256 queries): the query side from z (LN, q
+//                  for the 4 heads), online-softmax attention over all keys,
+//                  and in the epilogue the gate (LN, g), the output projection
+//                  and the residual, added in place.  q and g never leave the
+//                  chip.
 // H = 4 heads of d = 32 over c = 128 channels.
 #include <algorithm>
 #include <type_traits>
@@ -36,9 +39,10 @@ constexpr int C = 128;
 constexpr int H = 4;
 constexpr int DH = 32;
 constexpr int kProjRows = 4 * C + H;       // q, k, v, g, bias rows of the packed weight
-constexpr int kProjRowsPad = 4 * C + 32;   // bias block padded to one 32-row MFMA block
+constexpr int kRowQ = 0, kRowK = C, kRowG = 3 * C, kRowB = 4 * C;   // first rows of q, k (v follows), g, bias
+constexpr int kProjRowsLds = 2 * C + 32;   // k, v and the bias block (padded to 32 rows) staged by triatt_proj
 constexpr int kProjThreads = 512;
-constexpr int kProjSmem = kProjRowsPad * kLdw * 2 + kProjRowsPad * 2 * 2;
+constexpr int kProjSmem = kProjRowsLds * kLdw * 2 + kProjRowsLds * 2 * 2;
 constexpr int kFlashThreads = 256;         // 4 waves
 constexpr int kFlashTiles = 2;             // 32-query tiles per wave (1 tile at 3 waves per SIMD measured slower)
 constexpr int kFlashQueries = 4 * 32 * kFlashTiles;   // queries per workgroup
@@ -50,9 +54,7 @@ constexpr int kMaxKeyBlocks = 16384 / 64;  // 64-key blocks of the longest row (
 constexpr float kQScale = 0.17677669529663687f * kLog2e;
 
 struct TriAttBuffers {
-  bf16* q;       // [B][Np][Np][C]  frame-ordered, pair-major, times kQScale
   bf16* k;       // [B][Np][H][Np][DH]  per frame row and head: keys x head channels
-  bf16* g;       // [B][Np][Np][C]  sigmoid already applied
   bf16* vt;      // [B][Np][C][Np]  channel-major per frame row
   bf16* bias;    // [B][H][Np/32][Np/64][4][64][8]  times log2(e), in MFMA B-operand tiles
                  //   (see bias_tile_index)
@@ -77,11 +79,14 @@ template <bool kStarting>
 __global__ __launch_bounds__(kProjThreads) void triatt_proj_kernel(
     const bf16* __restrict__ z, const uint8_t* __restrict__ mask, const bf16* __restrict__ wf,
     const bf16* __restrict__ cf, TriAttBuffers buf, int B, int N, int Np) {
+  // LDS rows: k (0 .. C-1), v (C .. 2C-1), bias (2C .. 2C+H-1, zero-padded to 32 rows).
   extern __shared__ __attribute__((aligned(16))) char smem[];
   bf16* wl = reinterpret_cast<bf16*>(smem);
-  bf16* cl = wl + kProjRowsPad * kLdw;
-  stage_weights(wl, wf, kProjRows, kProjRowsPad);
-  stage_bias(cl, cf, kProjRows, kProjRowsPad);
+  bf16* cl = wl + kProjRowsLds * kLdw;
+  stage_weights(wl, wf + (size_t)kRowK * C, 2 * C, 2 * C);
+  stage_weights(wl + 2 * C * kLdw, wf + (size_t)kRowB * C, H, 32);
+  stage_bias(cl, cf + 2 * kRowK, 2 * C, 2 * C);
+  stage_bias(cl + 2 * 2 * C, cf + 2 * kRowB, H, 32);
   __syncthreads();
 
   const int lane = threadIdx.x & 63, wave = wave_id();
@@ -148,40 +153,31 @@ __global__ __launch_bounds__(kProjThreads) void triatt_proj_kernel(
     const int kk = k0 + perm32(rho);
 
     const size_t frow = ((size_t)b * Np + i) * Np;  // frame row base (pairs)
-    // q (times the softmax scale), k, g: pair-major; lane holds pair slot
-    // perm32(rho), channels blk*32 + 16h .. +15.
-    const size_t pm_off = (frow + kk) * C;
-    // One loop per output (the output kind is a compile-time constant, so the
-    // per-element select and the store address need no branches).
-    auto project = [&](auto which_tag) {
-      constexpr int which = decltype(which_tag)::value;   // 0: q, 1: k, 2: g
+    // Frame rows past N: the attention kernel reads only their bias (the
+    // bias row of query i, used by waves whose queries straddle N) and mask.
+    if (i < N) {
+      // k: head-major per frame row, [H][Np][DH]; lane holds pair slot
+      // perm32(rho), head cb's channels 16h .. 16h + 15.
 #pragma unroll 1
       for (int cb = 0; cb < 4; ++cb) {
-        const int row0 = (which == 2 ? 3 * C : which * C) + cb * 32;
-        const f32x16 a = proj_block_pm_f(x, xb, wl, cl, row0, rho, h);
-        float vq[16];
+        const f32x16 a = proj_block_pm_f(x, xb, wl, cl, cb * 32, rho, h);
+        float vk[16];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) vq[u] = which == 0 ? a[u] * kQScale : which == 1 ? a[u] : sigmoidf_fast(a[u]);
-        // k is head-major per frame row: [H][Np][DH]
-        bf16* base = which == 0 ? buf.q : which == 1 ? buf.k : buf.g;
-        const size_t dst = which == 1 ? (frow * H + (size_t)cb * Np + kk) * DH + 16 * h : pm_off + cb * 32 + 16 * h;
-        store16(base + dst, vq);
+        for (int u = 0; u < 16; ++u) vk[u] = a[u];
+        store16(buf.k + (frow * H + (size_t)cb * Np + kk) * DH + 16 * h, vk);
       }
-    };
-    project(std::integral_constant<int, 0>{});
-    project(std::integral_constant<int, 1>{});
-    project(std::integral_constant<int, 2>{});
-    // v^T: channel-major.  Lane (n, h) holds channel cb*32+n, pairs k0+16h..+15.
+      // v^T: channel-major.  Lane (n, h) holds channel cb*32+n, pairs k0+16h..+15.
 #pragma unroll 1
-    for (int cb = 0; cb < 4; ++cb) {
-      const f32x16 av = proj_block_cm_f(x, xb, wl, cl, 2 * C + cb * 32, rho, h);
-      float vv[16];
+      for (int cb = 0; cb < 4; ++cb) {
+        const f32x16 av = proj_block_cm_f(x, xb, wl, cl, C + cb * 32, rho, h);
+        float vv[16];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) vv[u] = av[u];
-      store16(buf.vt + (((size_t)b * Np + i) * C + cb * 32 + rho) * Np + k0 + 16 * h, vv);
+        for (int u = 0; u < 16; ++u) vv[u] = av[u];
+        store16(buf.vt + (((size_t)b * Np + i) * C + cb * 32 + rho) * Np + k0 + 16 * h, vv);
+      }
     }
     {
-      const f32x16 ab = proj_block_cm_f(x, xb, wl, cl, 4 * C, rho, h);
+      const f32x16 ab = proj_block_cm_f(x, xb, wl, cl, 2 * C, rho, h);
       if (rho < H) {
         float vb[16];
 #pragma unroll
@@ -208,6 +204,12 @@ __global__ __launch_bounds__(kProjThreads) void triatt_proj_kernel(
 // owns the kFlashTiles = 2 32-query tiles q0 and q0 + 32, q0 = 256 qb + 64 w,
 // which share every K / V fragment the wave reads from LDS.
 //
+// Query side and gate in the kernel: the prologue reads the z rows of the
+// wave's queries, normalises them and projects q for the four heads on MFMA
+// (head 0's into registers, the others into LDS slots); the epilogue reads the
+// same rows again for the residual and projects the gate g from them.  Only
+// the keys, values, bias and mask come from the projection kernel.
+//
 // Rows whose keys are all masked take a closed form (uniform weights: o / l is
 // the mean of v), and 64-key blocks without a valid key are skipped: their
 // logits (-1e30 or -inf) add exact zeros, so o and l are bit-identical.
@@ -230,15 +232,18 @@ __global__ __launch_bounds__(kProjThreads) void triatt_proj_kernel(
 // rescaled) when a block's weight sum exceeds 2^16 (a weight above 2^16 may be
 // present), so most blocks skip the max search.
 //
-// Loops: heads outermost (one head's accumulator live; a finished head leaves
-// o/l as 8 packed-bf16 registers), then 64-key blocks.  A block is two
+// Loops: heads outermost (one head's accumulator live; a finished head parks
+// o/l as bf16 in the LDS slot its successor's q has just left, the last
+// head's stays in registers), then 64-key blocks.  A block is two
 // independent 32-key halves whose MFMA chains and softmax interleave.  The 4
 // waves share frame row i, so each (head, 64-key) tile of K and V^T is staged
 // once per workgroup in LDS, double-buffered; the next tile and the next
 // bias slice are fetched while the current block is consumed.
 //
-// Layouts: S^T D lane (n, hh) register u <-> key k0 + 16hh + u of query q0+n
-// (A rows = keys k0 + perm32(rho)); O^T = V^T P^T with P^T taken straight
+// Layouts: q fragments lane (n, hh) <-> channels 16hh .. 16hh + 15 of query
+// q0 + n (k-step j: 8 of them, against K chunk 2hh + j); S^T D lane (n, hh)
+// register u <-> key k0 + 16hh + u of query q0+n (A rows = keys
+// k0 + perm32(rho)); O^T = V^T P^T with P^T taken straight
 // from the softmax registers (k-step s, half hh, t <-> key k0 + 16hh + 8s + t),
 // D lane (n, hh) register u <-> d = 16hh + u; the epilogue feeds g*o back as
 // the B operand of update^T = Wo (g*o)^T.  LDS tiles are [32][32] bf16,
@@ -256,12 +261,21 @@ __device__ __forceinline__ int t_off(int r, int chunk) { return r * TLD + ((chun
 
 // With kTail the residual stream z carries an int8 tail plane (common.h),
 // read with z and rewritten with out (in place).
+// wf / cf: the packed projection with the LayerNorm folded in (rows
+// [q | k | v | g | bias], fold.hip), of which this kernel uses the q and g
+// rows; z is read for the query side, the gate and the residual (z = zres;
+// out may alias it: every workgroup reads and writes only its own pairs).
 template <bool kStarting, bool kTail>
 __global__ __launch_bounds__(kFlashThreads) __attribute__((amdgpu_waves_per_eu(kFlashWavesPerEu, kFlashWavesPerEu)))
 void triatt_flash_kernel(
-    TriAttBuffers buf, const bf16* __restrict__ wo, const bf16* zres, bf16* out, int8_t* tail, int N, int Np,
-    int residual, int nitems) {
+    TriAttBuffers buf, const bf16* __restrict__ wf, const bf16* __restrict__ cf, const bf16* __restrict__ wo,
+    const bf16* zres, bf16* out, int8_t* tail, int N, int Np, int residual, int nitems) {
   __shared__ __attribute__((aligned(16))) bf16 smem[2 * kStage];
+  // H - 1 slots of [kFlashQueries][DH] bf16: slot s holds q of head s + 1 (times
+  // kQScale) until that head starts, then o / l of head s until the epilogue
+  // (head 0's q goes straight to registers, head H-1's o / l stays in them).
+  // A lane reads and writes only its own 32 bytes of a slot.
+  __shared__ __attribute__((aligned(16))) bf16 qo[(H - 1) * kFlashQueries * DH];
   extern __shared__ __attribute__((aligned(16))) bf16 kadd[];   // [Np] additive key mask
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -281,10 +295,20 @@ void triatt_flash_kernel(
   // This wave's 32-query tiles: q0 + 32t (Np is a multiple of 64, so all of
   // them exist or none does).
   const int q0 = qb * kFlashQueries + wave * 32 * kFlashTiles;
-  const bool active = q0 < Np;          // idle waves still stage tiles and meet every barrier
+  const bool active = q0 < Np;
+  // A wave none of whose queries lies in [0, N) has nothing to store: it
+  // still stages tiles, fetches operands and meets every barrier, but skips
+  // the matrix products and the softmax (the operand fetches stay, so the
+  // memory-counter waits of both kinds of wave are the same).
+  const bool compute = q0 < N;
   int qrow[kFlashTiles];
 #pragma unroll
   for (int t = 0; t < kFlashTiles; ++t) qrow[t] = active ? q0 + 32 * t + n : 0;
+  // This lane's 16 channels (16 hh .. 16 hh + 15) of query q0 + 32 t + n in LDS slot sl
+  auto slot_at = [&](int sl, int t) {
+    return qo + ((size_t)sl * kFlashQueries + wave * 32 * kFlashTiles + 32 * t + n) * DH + 16 * hh;
+  };
+  bf16x8 olast[kFlashTiles][2];   // o / l of the last head
 
   const size_t frow = ((size_t)b * Np + i) * Np;
   const unsigned plane = (unsigned)Np * (unsigned)Np;
@@ -292,21 +316,23 @@ void triatt_flash_kernel(
   const bf16* __restrict__ kg = buf.k + frow * C;                           // [H][Np keys][DH]
   const bf16* __restrict__ vg = buf.vt + ((size_t)b * Np + i) * C * Np;     // [C][Np keys]
   const bf16* __restrict__ bg = buf.bias + (size_t)b * H * plane;           // [H][Np][Np]
-  // q row of this workgroup's frame row; once a head's q has been read, its
-  // 32-channel slot holds that head's normalised output o / l (bf16) until
-  // the epilogue (each lane rewrites only the slot it read itself).
-  bf16* qio = buf.q + frow * C;                                             // [Np][C]
-  // q fragments of the head being processed; head 0's are requested first
-  // thing, each later head's during the previous head's last key block.
+  // z pair of frame pair (i, q) (pair 0 for q >= N: read, never stored)
+  auto zpair_of = [&](int q) -> size_t {
+    return q >= N ? 0 : kStarting ? ((size_t)b * N + i) * N + q : ((size_t)b * N + q) * N + i;
+  };
+  // q fragments of the head being processed: lane (n, hh) holds channels
+  // 16 hh .. 16 hh + 15 of query q0 + 32 t + n (as the K fragments pair them:
+  // k-step 0 <-> K chunk 2 hh, k-step 1 <-> K chunk 2 hh + 1).  Head 0's come
+  // from the prologue, each later head's from its LDS slot during the
+  // previous head's last key block.
   bf16x8 qf[kFlashTiles][2];
   auto qload = [&](int hq) {
 #pragma unroll
     for (int t = 0; t < kFlashTiles; ++t) {
-      qf[t][0] = load8(qio + (unsigned)qrow[t] * C + hq * DH + 8 * hh);
-      qf[t][1] = load8(qio + (unsigned)qrow[t] * C + hq * DH + 16 + 8 * hh);
+      qf[t][0] = load8(slot_at(hq - 1, t));
+      qf[t][1] = load8(slot_at(hq - 1, t) + 8);
     }
   };
-  qload(0);
   // Key-mask row (additive: 0 valid, -1e30 masked, -inf beyond N).  A row
   // whose keys are all masked ("dead") attends uniformly to its N keys
   // (every logit replaced by the same value): o / l is the mean of v.
@@ -398,17 +424,73 @@ void triatt_flash_kernel(
       }
     }
     __syncthreads();
-#pragma unroll 1
+#pragma unroll
     for (int hd = 0; hd < H; ++hd) {
+      bf16x8 r[2];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) r[u >> 3][u & 7] = f2bf(vmean[hd * DH + 16 * hh + u]);
 #pragma unroll
       for (int t = 0; t < kFlashTiles; ++t) {
-        float r[16];
-#pragma unroll
-        for (int u = 0; u < 16; ++u) r[u] = vmean[hd * DH + 16 * hh + u];
-        if (active) store16(qio + (unsigned)qrow[t] * C + hd * DH + 16 * hh, r);
+        if (hd + 1 < H) {
+          store8(slot_at(hd, t), r[0]);
+          store8(slot_at(hd, t) + 8, r[1]);
+        } else {
+          olast[t][0] = r[0];
+          olast[t][1] = r[1];
+        }
       }
     }
   } else {
+  if (compute) {
+    // Query side: LN(z) (affine-free; gamma and beta are folded into the q
+    // rows of wf / cf) and q = LN(z) Wq^T * kQScale for the four heads, on
+    // MFMA with the weight rows as the A operand (pair-major blocks: lane
+    // (n, hh) ends with query n's channels 16 hh + u).  A query past N has a
+    // zero row and q = 0, as the reference's padded pairs project to.
+    bf16x8 xq[kFlashTiles][8], xbq[kFlashTiles];
+#pragma unroll
+    for (int t = 0; t < kFlashTiles; ++t) {
+      const int q = q0 + 32 * t + n;
+      float v[64];
+      load_half_row_f32(zres + zpair_of(q) * C, hh, true, v);
+      normalize_half_row(v, q < N, xq[t]);
+      xbq[t] = bias_step_x(q < N, hh);
+    }
+    const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(wf, (unsigned)kProjRows * C * 2);
+    const unsigned wq_voff = (unsigned)(perm32(n) * C + 8 * hh) * 2;
+#pragma unroll 1
+    for (int hd = 0; hd < H; ++hd) {
+      const int r = kRowQ + hd * DH + perm32(n);
+      bf16x8 wq[8], wb = zero8;
+#pragma unroll
+      for (int s2 = 0; s2 < 8; ++s2)
+        wq[s2] = buffer_load8(wrs, wq_voff + 32 * s2, (unsigned)(kRowQ + hd * DH) * C * 2);
+      if (hh == 0) {
+        wb[0] = cf[2 * r];
+        wb[1] = cf[2 * r + 1];
+      }
+#pragma unroll
+      for (int t = 0; t < kFlashTiles; ++t) {
+        f32x16 acc = zero16();
+#pragma unroll
+        for (int s2 = 0; s2 < 8; ++s2) acc = mfma32(wq[s2], xq[t][s2], acc);
+        acc = mfma32(wb, xbq[t], acc);
+        bf16x8 r0, r1;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          r0[u] = f2bf(acc[u] * kQScale);
+          r1[u] = f2bf(acc[8 + u] * kQScale);
+        }
+        if (hd == 0) {
+          qf[t][0] = r0;
+          qf[t][1] = r1;
+        } else {
+          store8(slot_at(hd - 1, t), r0);
+          store8(slot_at(hd - 1, t) + 8, r1);
+        }
+      }
+    }
+  }
   // Key blocks with at least one valid key, in order.  A block whose keys are
   // all masked adds exact zeros (its logits are -1e30 or -inf below any
   // unmasked logit), so skipping it leaves o and l bit-identical.
@@ -493,8 +575,8 @@ void triatt_flash_kernel(
         // the next block's key-mask column, read now so the read is not waited on at its start
         kma = kadd[kn + krow];
         kmb = kadd[kn + 32 + krow];
-        const bf16x8 ka0 = load8(ks + t_off(krow, hh)), ka1 = load8(ks + kTile + t_off(krow, hh));
-        const bf16x8 kb0 = load8(ks + t_off(krow, 2 + hh)), kb1 = load8(ks + kTile + t_off(krow, 2 + hh));
+        const bf16x8 ka0 = load8(ks + t_off(krow, 2 * hh)), ka1 = load8(ks + kTile + t_off(krow, 2 * hh));
+        const bf16x8 kb0 = load8(ks + t_off(krow, 2 * hh + 1)), kb1 = load8(ks + kTile + t_off(krow, 2 * hh + 1));
         // Logits minus the running max m, all on MFMA (no shift unless m is
         // set; the rank-2 product only when there is a mask or a shift), for
         // both query tiles before any softmax work so that one tile's
@@ -502,83 +584,87 @@ void triatt_flash_kernel(
         f32x16 s[kFlashTiles][2];
 #pragma unroll
         for (int t = 0; t < kFlashTiles; ++t) {
-          bf16x8 qs = qm[t];
-          if (!m_set[t]) qs[1] = f2bf(0.f);
-          s[t][0] = mfma32(ka0, qf[t][0], zero16());
-          s[t][1] = mfma32(ka1, qf[t][0], zero16());
-          s[t][0] = mfma32(kb0, qf[t][1], s[t][0]);
-          s[t][1] = mfma32(kb1, qf[t][1], s[t][1]);
-          s[t][0] = mfma32(ident[0], bias[t][0], s[t][0]);
-          s[t][1] = mfma32(ident[0], bias[t][2], s[t][1]);
-          s[t][0] = mfma32(ident[1], bias[t][1], s[t][0]);
-          s[t][1] = mfma32(ident[1], bias[t][3], s[t][1]);
-          if (m_set[t] || need_mask) {
-            s[t][0] = mfma32(km0, qs, s[t][0]);
-            s[t][1] = mfma32(km1, qs, s[t][1]);
+          if (compute) {
+            bf16x8 qs = qm[t];
+            if (!m_set[t]) qs[1] = f2bf(0.f);
+            s[t][0] = mfma32(ka0, qf[t][0], zero16());
+            s[t][1] = mfma32(ka1, qf[t][0], zero16());
+            s[t][0] = mfma32(kb0, qf[t][1], s[t][0]);
+            s[t][1] = mfma32(kb1, qf[t][1], s[t][1]);
+            s[t][0] = mfma32(ident[0], bias[t][0], s[t][0]);
+            s[t][1] = mfma32(ident[0], bias[t][2], s[t][1]);
+            s[t][0] = mfma32(ident[1], bias[t][1], s[t][0]);
+            s[t][1] = mfma32(ident[1], bias[t][3], s[t][1]);
+            if (m_set[t] || need_mask) {
+              s[t][0] = mfma32(km0, qs, s[t][0]);
+              s[t][1] = mfma32(km1, qs, s[t][1]);
+            }
           }
           bload(hn, kn, t, bias[t]);
         }
         if (ib + 1 == nact && hd + 1 < H) qload(hd + 1);
+        if (compute) {
 #pragma unroll
-        for (int t = 0; t < kFlashTiles; ++t) {
-          f32x16& s0 = s[t][0];
-          f32x16& s1 = s[t][1];
-          bf16x8 pa[2], pb[2];
-          float psum;
-          bool slow = fresh[t];
-          if (!slow) {
+          for (int t = 0; t < kFlashTiles; ++t) {
+            f32x16& s0 = s[t][0];
+            f32x16& s1 = s[t][1];
+            bf16x8 pa[2], pb[2];
+            float psum;
+            bool slow = fresh[t];
+            if (!slow) {
 #pragma unroll
-            for (int u = 0; u < 16; ++u) {
-              pa[u >> 3][u & 7] = f2bf(fast_exp2(s0[u]));
-              pb[u >> 3][u & 7] = f2bf(fast_exp2(s1[u]));
+              for (int u = 0; u < 16; ++u) {
+                pa[u >> 3][u & 7] = f2bf(fast_exp2(s0[u]));
+                pb[u >> 3][u & 7] = f2bf(fast_exp2(s1[u]));
+              }
+              psum = sum8_bf16(pa[1], sum8_bf16(pa[0], 0.f)) + sum8_bf16(pb[1], sum8_bf16(pb[0], 0.f));
+              // a sum above 2^16 may hold a weight above 2^16: move m (rare)
+              slow = __any(psum > kSlackSum);
             }
-            psum = sum8_bf16(pa[1], sum8_bf16(pa[0], 0.f)) + sum8_bf16(pb[1], sum8_bf16(pb[0], 0.f));
-            // a sum above 2^16 may hold a weight above 2^16: move m (rare)
-            slow = __any(psum > kSlackSum);
+            if (slow) {
+              // s0, s1 hold the logits minus `shift` (the MFMA subtracts m
+              // once m is set).  Everything here works on those shifted values,
+              // so the fast path above never needs the unshifted logits.
+              const float shift = m_set[t] ? m[t] : 0.f;
+              float bmax = fmaxf(s0[0], s1[0]);
+#pragma unroll
+              for (int u = 1; u < 16; ++u) bmax = __builtin_fmaxf(bmax, __builtin_fmaxf(s0[u], s1[u]));
+              bmax = fmaxf(bmax, __shfl_xor(bmax, 32)) + shift;
+              float delta = 0.f;
+              if (fresh[t] && __all(bmax >= -64.f && bmax <= 16.f)) {
+                // unshifted from here on: every weight is at most 2^16 until a
+                // block sum says otherwise, and each row keeps a weight of at
+                // least 2^-64 (nothing is accumulated yet)
+                fresh[t] = false;
+              } else {
+                // The shift is kept bf16-representable: it enters the MFMA as -m.
+                // Leaving the unshifted mode, the running max is at least -64.
+                const float floor_m = m_set[t] ? m[t] : fresh[t] ? -INFINITY : -64.f;
+                const float m_new = bf2f(f2bf(fmaxf(floor_m, bmax)));
+                const float alpha = fresh[t] ? 0.f : fast_exp2(shift - m_new);
+                delta = m_new - shift;
+                m[t] = m_new;
+                l[t] *= alpha;
+#pragma unroll
+                for (int u = 0; u < 16; ++u) o[t][u] *= alpha;
+                // a block of masked keys only (logits ~ -1e30) does not set m
+                m_set[t] = m_set[t] || __all(m[t] > -1e29f);
+                fresh[t] = fresh[t] && !m_set[t];
+                if (hh == 0) qm[t][1] = f2bf(-m[t]);
+              }
+#pragma unroll
+              for (int u = 0; u < 16; ++u) {
+                pa[u >> 3][u & 7] = f2bf(fast_exp2(s0[u] - delta));
+                pb[u >> 3][u & 7] = f2bf(fast_exp2(s1[u] - delta));
+              }
+              psum = sum8_bf16(pa[1], sum8_bf16(pa[0], 0.f)) + sum8_bf16(pb[1], sum8_bf16(pb[0], 0.f));
+            }
+            l[t] += psum;
+            o[t] = mfma32(load8(vs + t_off(krow, 2 * hh)), pa[0], o[t]);
+            o[t] = mfma32(load8(vs + t_off(krow, 2 * hh + 1)), pa[1], o[t]);
+            o[t] = mfma32(load8(vs + kTile + t_off(krow, 2 * hh)), pb[0], o[t]);
+            o[t] = mfma32(load8(vs + kTile + t_off(krow, 2 * hh + 1)), pb[1], o[t]);
           }
-          if (slow) {
-            // s0, s1 hold the logits minus `shift` (the MFMA subtracts m
-            // once m is set).  Everything here works on those shifted values,
-            // so the fast path above never needs the unshifted logits.
-            const float shift = m_set[t] ? m[t] : 0.f;
-            float bmax = fmaxf(s0[0], s1[0]);
-#pragma unroll
-            for (int u = 1; u < 16; ++u) bmax = __builtin_fmaxf(bmax, __builtin_fmaxf(s0[u], s1[u]));
-            bmax = fmaxf(bmax, __shfl_xor(bmax, 32)) + shift;
-            float delta = 0.f;
-            if (fresh[t] && __all(bmax >= -64.f && bmax <= 16.f)) {
-              // unshifted from here on: every weight is at most 2^16 until a
-              // block sum says otherwise, and each row keeps a weight of at
-              // least 2^-64 (nothing is accumulated yet)
-              fresh[t] = false;
-            } else {
-              // The shift is kept bf16-representable: it enters the MFMA as -m.
-              // Leaving the unshifted mode, the running max is at least -64.
-              const float floor_m = m_set[t] ? m[t] : fresh[t] ? -INFINITY : -64.f;
-              const float m_new = bf2f(f2bf(fmaxf(floor_m, bmax)));
-              const float alpha = fresh[t] ? 0.f : fast_exp2(shift - m_new);
-              delta = m_new - shift;
-              m[t] = m_new;
-              l[t] *= alpha;
-#pragma unroll
-              for (int u = 0; u < 16; ++u) o[t][u] *= alpha;
-              // a block of masked keys only (logits ~ -1e30) does not set m
-              m_set[t] = m_set[t] || __all(m[t] > -1e29f);
-              fresh[t] = fresh[t] && !m_set[t];
-              if (hh == 0) qm[t][1] = f2bf(-m[t]);
-            }
-#pragma unroll
-            for (int u = 0; u < 16; ++u) {
-              pa[u >> 3][u & 7] = f2bf(fast_exp2(s0[u] - delta));
-              pb[u >> 3][u & 7] = f2bf(fast_exp2(s1[u] - delta));
-            }
-            psum = sum8_bf16(pa[1], sum8_bf16(pa[0], 0.f)) + sum8_bf16(pb[1], sum8_bf16(pb[0], 0.f));
-          }
-          l[t] += psum;
-          o[t] = mfma32(load8(vs + t_off(krow, 2 * hh)), pa[0], o[t]);
-          o[t] = mfma32(load8(vs + t_off(krow, 2 * hh + 1)), pa[1], o[t]);
-          o[t] = mfma32(load8(vs + kTile + t_off(krow, 2 * hh)), pb[0], o[t]);
-          o[t] = mfma32(load8(vs + kTile + t_off(krow, 2 * hh + 1)), pb[1], o[t]);
         }
       }
       lstore(st ^ 1);
@@ -593,72 +679,126 @@ void triatt_flash_kernel(
       kcur = knext;
       block(ib, k, knext, kma, kmb);
     }
-    // head finished: o / l (bf16) parked in this head's q slot
+    // head finished: o / l (bf16) parked in LDS, the last head's kept in registers
 #pragma unroll
     for (int t = 0; t < kFlashTiles; ++t) {
       const float inv = 1.0f / (l[t] + __shfl_xor(l[t], 32));
-      float r[16];
+      bf16x8 r[2];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) r[u] = o[t][u] * inv;
-      if (active) store16(qio + (unsigned)qrow[t] * C + hd * DH + 16 * hh, r);
+      for (int u = 0; u < 16; ++u) r[u >> 3][u & 7] = f2bf(o[t][u] * inv);
+      olast[t][0] = r[0];
+      olast[t][1] = r[1];
+      if (hd + 1 < H && compute) {
+        store8(slot_at(hd, t), r[0]);
+        store8(slot_at(hd, t) + 8, r[1]);
+      }
     }
   }
   }
-  if (!active) return;
+  if (!compute) return;
 
-  // Out-projection weights (A operand: row cb*32 + perm32(n), k-step s2),
-  // fetched once for both tiles, together with the first tile's gate inputs.
-  bf16x8 wf[4][8];
+  // Epilogue, per 32-query tile.  Lane (n, hh) loads the z row of query
+  // q0 + 32 t + n in the update's layout (channels 32 cb + 16 hh + 0..15,
+  // cb = 0..3): the residual, and normalised (affine-free, gamma and beta
+  // folded into the g rows of wf / cf) the gate's input, whose k-step
+  // s2 = 2 cb + j carries channels 32 cb + 16 h + 8 j + e on both operands.
+  // g = sigmoid(LN(z) Wg^T) times o / l per head is the B operand of
+  // update^T = Wo (g o)^T; the residual is added and the result stored in z's
+  // frame.  Weight fragments are read per block (L2-resident) to keep the
+  // register budget; lanes of queries past N read pair 0 and store nothing.
+  // Weight fragments through buffer resources: lane (n, hh) reads row
+  // perm32(n) of a 32-row block at channel 16 hh + 32 (s2 >> 1) + 8 (s2 & 1);
+  // the block is a wave-uniform offset.
+  const unsigned we_voff = (unsigned)(perm32(n) * C + 16 * hh) * 2;
 #pragma unroll
-  for (int cb = 0; cb < 4; ++cb) {
-    const bf16* wrow = wo + (size_t)(cb * 32 + perm32(n)) * C + 16 * hh;
-#pragma unroll
-    for (int s2 = 0; s2 < 8; ++s2) wf[cb][s2] = load8(wrow + 32 * (s2 >> 1) + 8 * (s2 & 1));
-  }
-#pragma unroll 1
   for (int t = 0; t < kFlashTiles; ++t) {
-    // The residual (and its tail) of each output block is requested one block
-    // ahead, so that its latency hides behind the gate loads and the previous
-    // block's MFMAs.  Lanes of queries past N read pair 0 and store nothing.
+    // Opaque copies of the weight pointers: the fragments are loop-invariant,
+    // and hoisted out of this loop (64 of them) they would not fit the
+    // register budget.
+    const bf16* wfe = wf;
+    const bf16* woe = wo;
+    asm volatile("" : "+s"(wfe), "+s"(woe));
+    const __amdgpu_buffer_rsrc_t wgrs = buffer_rsrc(wfe, (unsigned)kProjRows * C * 2);
+    const __amdgpu_buffer_rsrc_t wors = buffer_rsrc(woe, (unsigned)C * C * 2);
     const int q = q0 + 32 * t + n;
     const bool store = q < N;
-    const size_t zpair = !store ? 0 : kStarting ? ((size_t)b * N + i) * N + q : ((size_t)b * N + q) * N + i;
-    bf16x8 zr[2][2];
-    u32x4 zt[2];
-    auto zload = [&](int cb) {
+    const size_t zpair = zpair_of(q);
+    bf16x8 zr[4][2];
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) {
       const size_t off = zpair * C + cb * 32 + 16 * hh;
-      zr[cb & 1][0] = load8(zres + off);
-      zr[cb & 1][1] = load8(zres + off + 8);
-      if (kTail) zt[cb & 1] = load_tail16(tail + off);
-    };
-    if (residual) zload(0);
-    // Gate: g * (o / l) per head, as the out-projection's B operand.
-    bf16x8 gob[2 * H];
+      zr[cb][0] = load8(zres + off);
+      zr[cb][1] = load8(zres + off + 8);
+    }
+    // affine-free LayerNorm straight from the bf16 row (two-pass, fp32; no
+    // fp32 copy of the row is kept, which the register budget has no room for)
+    bf16x8 xg[8];
     {
-      const bf16* grow = buf.g + (frow + q0 + 32 * t + n) * C + 16 * hh;
-      const bf16* orow = qio + (unsigned)(q0 + 32 * t + n) * C + 16 * hh;   // qrow[t] of an active wave
+      float sum = 0.f;
 #pragma unroll
-      for (int hd = 0; hd < H; ++hd) {
-        const bf16x8 g0 = load8(grow + hd * DH), g1 = load8(grow + hd * DH + 8);
-        const bf16x8 o0 = load8(orow + hd * DH), o1 = load8(orow + hd * DH + 8);
+      for (int s2 = 0; s2 < 8; ++s2)
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          gob[2 * hd][u] = f2bf(bf2f(g0[u]) * bf2f(o0[u]));
-          gob[2 * hd + 1][u] = f2bf(bf2f(g1[u]) * bf2f(o1[u]));
+        for (int e = 0; e < 8; ++e) sum += bf2f(zr[s2 >> 1][s2 & 1][e]);
+      sum += __shfl_xor(sum, 32);
+      const float mean = sum * (1.0f / C);
+      float ss = 0.f;
+#pragma unroll
+      for (int s2 = 0; s2 < 8; ++s2)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float d = bf2f(zr[s2 >> 1][s2 & 1][e]) - mean;
+          ss += d * d;
         }
+      ss += __shfl_xor(ss, 32);
+      const float rstd = rsqrtf(ss * (1.0f / C) + 1e-5f);
+#pragma unroll
+      for (int s2 = 0; s2 < 8; ++s2)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xg[s2][e] = f2bf((bf2f(zr[s2 >> 1][s2 & 1][e]) - mean) * rstd);
+    }
+    const bf16x8 xbg = bias_step_x(true, hh);
+    bf16x8 gob[2 * H];
+#pragma unroll
+    for (int hd = 0; hd < H; ++hd) {
+      __builtin_amdgcn_sched_barrier(0);
+      const int r = kRowG + hd * DH + perm32(n);
+      f32x16 acc = zero16();
+#pragma unroll
+      for (int s2 = 0; s2 < 8; ++s2)
+        acc = mfma32(buffer_load8(wgrs, we_voff + (32 * (s2 >> 1) + 8 * (s2 & 1)) * 2, (unsigned)(kRowG + hd * DH) * C * 2),
+                     xg[s2], acc);
+      bf16x8 wb = zero8;
+      if (hh == 0) {
+        wb[0] = cf[2 * r];
+        wb[1] = cf[2 * r + 1];
+      }
+      acc = mfma32(wb, xbg, acc);
+      // D lane (n, hh), register u: gate channel hd * DH + 16 hh + u of query n
+      // (the last head's o / l selected, not indexed: t is a runtime index)
+      const bf16x8 o0 = hd + 1 < H ? load8(slot_at(hd, t)) : t == 0 ? olast[0][0] : olast[1][0];
+      const bf16x8 o1 = hd + 1 < H ? load8(slot_at(hd, t) + 8) : t == 0 ? olast[0][1] : olast[1][1];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        gob[2 * hd][u] = f2bf(sigmoidf_fast(acc[u]) * bf2f(o0[u]));
+        gob[2 * hd + 1][u] = f2bf(sigmoidf_fast(acc[8 + u]) * bf2f(o1[u]));
       }
     }
 
-    // update^T = Wo (g*o)^T, residual add, store in z's frame.  The scheduling
-    // barrier keeps the four output blocks apart (interleaved, their weight
-    // loads and accumulators would not fit the register budget).
+    // update^T = Wo (g*o)^T (A operand: Wo row cb*32 + perm32(n), k-step s2),
+    // residual add, store in z's frame.  The scheduling barrier keeps the four
+    // output blocks apart (interleaved, their weight loads and accumulators
+    // would not fit the register budget).
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb) {
       __builtin_amdgcn_sched_barrier(0);
-      if (residual && cb + 1 < 4) zload(cb + 1);
+      // the residual's tail, requested ahead of this block's products
+      u32x4 zt;
+      if (kTail) zt = load_tail16(tail + zpair * C + cb * 32 + 16 * hh);
       f32x16 acc = zero16();
 #pragma unroll
-      for (int s2 = 0; s2 < 8; ++s2) acc = mfma32(wf[cb][s2], gob[s2], acc);
+      for (int s2 = 0; s2 < 8; ++s2)
+        acc = mfma32(buffer_load8(wors, we_voff + (32 * (s2 >> 1) + 8 * (s2 & 1)) * 2, (unsigned)(cb * 32) * C * 2),
+                     gob[s2], acc);
       if (store) {
         const size_t off = zpair * C + cb * 32 + 16 * hh;
         float v[16];
@@ -666,7 +806,7 @@ void triatt_flash_kernel(
         for (int u = 0; u < 16; ++u) v[u] = acc[u];
         if (kTail) {
           float zv[16];
-          tail_decode16(zr[cb & 1][0], zr[cb & 1][1], zt[cb & 1], zv);
+          tail_decode16(zr[cb][0], zr[cb][1], zt, zv);
 #pragma unroll
           for (int u = 0; u < 16; ++u) v[u] += zv[u];
           tail_store16(out + off, tail + off, v);
@@ -675,8 +815,8 @@ void triatt_flash_kernel(
         if (residual) {
 #pragma unroll
           for (int u = 0; u < 8; ++u) {
-            v[u] += bf2f(zr[cb & 1][0][u]);
-            v[8 + u] += bf2f(zr[cb & 1][1][u]);
+            v[u] += bf2f(zr[cb][0][u]);
+            v[8 + u] += bf2f(zr[cb][1][u]);
           }
         }
         store16(out + off, v);
@@ -696,8 +836,8 @@ extern "C" size_t bioemu_triatt_workspace_bytes(int64_t B, int64_t N, int64_t Dc
   if (B <= 0 || N <= 0 || Dc != C || Hc != H) return 0;
   const size_t Np = triatt_np(N);
   const size_t pairs = (size_t)B * Np * Np;
-  // q, k, g, v^T (bf16 x C each) + bias (bf16 x H) + mask (u8), each 256-byte aligned
-  return round_up(pairs * C * 2, 256) * 4 + round_up(pairs * H * 2, 256) + round_up(pairs, 256) +
+  // k, v^T (bf16 x C each) + bias (bf16 x H) + mask (u8), each 256-byte aligned
+  return round_up(pairs * C * 2, 256) * 2 + round_up(pairs * H * 2, 256) + round_up(pairs, 256) +
          fold_bytes(kProjRows);
 }
 
@@ -727,11 +867,7 @@ extern "C" int bioemu_triatt_fwd(const void* z, const uint8_t* mask, const float
   const size_t pairs = (size_t)B * Np * Np;
   char* p = static_cast<char*>(workspace);
   TriAttBuffers buf;
-  buf.q = reinterpret_cast<bf16*>(p);
-  p += round_up(pairs * C * 2, 256);
   buf.k = reinterpret_cast<bf16*>(p);
-  p += round_up(pairs * C * 2, 256);
-  buf.g = reinterpret_cast<bf16*>(p);
   p += round_up(pairs * C * 2, 256);
   buf.vt = reinterpret_cast<bf16*>(p);
   p += round_up(pairs * C * 2, 256);
@@ -778,7 +914,7 @@ extern "C" int bioemu_triatt_fwd(const void* z, const uint8_t* mask, const float
   if (grid2 > 0x7fffffffLL) return set_error(BIOEMU_ERR_INVALID_ARG, "triatt: too many work items");
   {
     KernelTimerScope timed("triatt_flash", stream);
-    hipLaunchKernelGGL(kflash, dim3((unsigned)grid2), dim3(kFlashThreads), flash_smem, stream, buf,
+    hipLaunchKernelGGL(kflash, dim3((unsigned)grid2), dim3(kFlashThreads), flash_smem, stream, buf, wf, cf,
                        static_cast<const bf16*>(w_o), static_cast<const bf16*>(z), static_cast<bf16*>(out), res_tail,
                        (int)N, (int)Np, residual, (int)nitems);
   }

@@ -101,13 +101,14 @@ def triatt_kernel_work(name: str, B: int, N: int, c: int = 128, H: int = 4,
     them, the valid keys (a masked key adds an exact zero and the kernel skips whole blocks of them; a row
     without valid keys is the closed-form mean of v), for every query."""
     P = B * N * N
+    nv = N if n_valid is None else n_valid
     if name == "triatt_proj":
-        # LN + q,k,v,g (c -> 4c) + bias (c -> H); reads z, writes q,k,v,g (+ bias)
-        return ("hbm", float(P * (c * 2 + 4 * c * 2 + H * 2)))
+        # LN + the key side, k, v (c -> 2c) + bias (c -> H): reads z, writes k, v, the bias and the frame mask
+        return ("hbm", float(P * (c * 2 + 2 * c * 2 + H * 2 + 1)))
     if name == "triatt_flash":
-        # QK^T and PV over the valid keys for every (valid row, query, head) + output projection
-        nv = N if n_valid is None else n_valid
-        return ("mfma", 2.0 * B * nv * N * nv * c * 2 + 2.0 * P * c * c)
+        # q (c -> c) for the queries of rows with a valid key; QK^T and PV over the valid keys for every
+        # (valid row, query, head); the gate g (c -> c) and the output projection for every pair
+        return ("mfma", 2.0 * B * nv * N * nv * c * 2 + 2.0 * B * nv * N * c * c + 2 * 2.0 * P * c * c)
     return None
 
 
