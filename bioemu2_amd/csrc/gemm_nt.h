@@ -44,6 +44,63 @@ __device__ __forceinline__ void nt_copy16_to_lds(__amdgpu_buffer_rsrc_t r, const
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(lds), 16, voff, soff, 0, 0);
 }
 
+// Staging of one operand pair into LDS.  Each operand tile (256 rows x 128 B)
+// is 32 copies of 1 KB; wave w moves copies w, w + 8, w + 16, w + 24 of A and
+// of B.  Copy j writes LDS chunk 64 j + lane = (row, swizzled chunk) of the
+// tile: rows 8 j .. 8 j + 7, all on one side of b_split (B rows [0, b_split)
+// from rb, the rest from rb2, whose row 0 is tile row b_split).  Rows are ld
+// elements apart.
+struct NtStaging {
+  unsigned voff[4], voffb[4];
+  bool second[4];
+  __device__ __forceinline__ NtStaging(int wave, int lane, int ld, int b_split) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int p = (wave + 8 * q) * 64 + lane, r = p >> 3, c = (p & 7) ^ nt_swz(p >> 3);
+      voff[q] = (unsigned)(r * ld + c * 8) * 2;
+      second[q] = b_split < kNtTile && (wave + 8 * q) * 8 >= b_split;
+      voffb[q] = second[q] ? (unsigned)((r - b_split) * ld + c * 8) * 2 : voff[q];
+    }
+  }
+  // k-tile starting at element k0 of every row into stage st (A tile | B tile)
+  __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb,
+                                        __amdgpu_buffer_rsrc_t rb2, bf16* st, int wave, int k0) const {
+    const unsigned soff = (unsigned)k0 * 2;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      nt_copy16_to_lds(ra, st + (wave + 8 * q) * 512, voff[q], soff);
+      nt_copy16_to_lds(second[q] ? rb2 : rb, st + kNtTileElems + (wave + 8 * q) * 512, voffb[q], soff);
+    }
+  }
+};
+
+// The 32 MFMAs of one staged k-tile (64 deep) for this wave's 64 x 128 block:
+// acc[jb][ib] += B rows (wj*128 + jb*32 + perm32(.)) x A rows (wi*64 + ib*32 + .).
+// All 24 operand fragments of the k-tile are requested before the first MFMA
+// (the scheduler otherwise recycles a few registers and waits on every read);
+// the MFMAs then consume them as they land.
+__device__ __forceinline__ void nt_ktile(const bf16* st, const int (&offj)[4], const int (&offi)[2], int lh,
+                                         f32x16 (&acc)[4][2]) {
+  const bf16* sa = st;
+  const bf16* sb = st + kNtTileElems;
+  bf16x8 fj[4][4], fi[4][2];
+#pragma unroll
+  for (int ks = 0; ks < kNtBK / 16; ++ks) {
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) fj[ks][jb] = load8(sb + nt_off(offj[jb], 2 * ks + lh));
+#pragma unroll
+    for (int ib = 0; ib < 2; ++ib) fi[ks][ib] = load8(sa + nt_off(offi[ib], 2 * ks + lh));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int ks = 0; ks < kNtBK / 16; ++ks)
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+      for (int ib = 0; ib < 2; ++ib) acc[jb][ib] = mfma32(fj[ks][jb], fi[ks][ib], acc[jb][ib]);
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 // A points at the tile's first row of A, of which a_rows (<= 256) exist: the
 // rest read as zero through the buffer bound (their C rows are garbage-free
 // zeros times B, never needed by a caller that skips them).  B rows [0,
@@ -63,28 +120,7 @@ __device__ __forceinline__ void gemm_nt_tile(const bf16* A, int a_rows, const bf
   const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(A, (unsigned)a_rows * ld * 2);
   const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(B, (unsigned)b_split * ld * 2);
   const __amdgpu_buffer_rsrc_t rb2 = buffer_rsrc(B2, (unsigned)min(kNtTile - b_split, b2_rows) * ld * 2);
-  // Each operand tile (256 rows x 128 B) is 32 copies of 1 KB; wave w moves
-  // copies w, w + 8, w + 16, w + 24 of A and of B.  Copy j writes LDS chunk
-  // 64 j + lane = (row, swizzled chunk) of the tile: rows 8 j .. 8 j + 7, all
-  // on one side of b_split.
-  unsigned voff[4], voffb[4];
-  bool second[4];
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int p = (wave + 8 * q) * 64 + lane, r = p >> 3, c = (p & 7) ^ nt_swz(p >> 3);
-    voff[q] = (unsigned)(r * ld + c * 8) * 2;
-    second[q] = b_split < kNtTile && (wave + 8 * q) * 8 >= b_split;
-    voffb[q] = second[q] ? (unsigned)((r - b_split) * ld + c * 8) * 2 : voff[q];
-  }
-  auto stage = [&](int kt) {
-    bf16* st = smem + (kt & 1) * kNtStage;
-    const unsigned soff = (unsigned)(kt * kNtBK) * 2;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      nt_copy16_to_lds(ra, st + (wave + 8 * q) * 512, voff[q], soff);
-      nt_copy16_to_lds(second[q] ? rb2 : rb, st + kNtTileElems + (wave + 8 * q) * 512, voffb[q], soff);
-    }
-  };
+  const NtStaging stg(wave, lane, ld, b_split);
 
 #pragma unroll
   for (int jb = 0; jb < 4; ++jb)
@@ -92,7 +128,7 @@ __device__ __forceinline__ void gemm_nt_tile(const bf16* A, int a_rows, const bf
     for (int ib = 0; ib < 2; ++ib) acc[jb][ib] = zero16();
 
   const int nk = K / kNtBK;
-  stage(0);
+  stg.issue(ra, rb, rb2, smem, wave, 0);
   int offj[4], offi[2];
 #pragma unroll
   for (int jb = 0; jb < 4; ++jb) offj[jb] = wj * 128 + jb * 32 + perm32(ln);
@@ -102,28 +138,8 @@ __device__ __forceinline__ void gemm_nt_tile(const bf16* A, int a_rows, const bf
   for (int kt = 0; kt < nk; ++kt) {
     __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's copies of k-tile kt landed
     __syncthreads();                       // ... and everyone's; the other stage is free again
-    if (kt + 1 < nk) stage(kt + 1);
-    const bf16* sa = smem + (kt & 1) * kNtStage;
-    const bf16* sb = sa + kNtTileElems;
-    // All 24 operand fragments of the k-tile are requested before the first
-    // MFMA (the scheduler otherwise recycles a few registers and waits on
-    // every read); the 32 MFMAs then consume them as they land.
-    bf16x8 fj[4][4], fi[4][2];
-#pragma unroll
-    for (int ks = 0; ks < kNtBK / 16; ++ks) {
-#pragma unroll
-      for (int jb = 0; jb < 4; ++jb) fj[ks][jb] = load8(sb + nt_off(offj[jb], 2 * ks + lh));
-#pragma unroll
-      for (int ib = 0; ib < 2; ++ib) fi[ks][ib] = load8(sa + nt_off(offi[ib], 2 * ks + lh));
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int ks = 0; ks < kNtBK / 16; ++ks)
-#pragma unroll
-      for (int jb = 0; jb < 4; ++jb)
-#pragma unroll
-        for (int ib = 0; ib < 2; ++ib) acc[jb][ib] = mfma32(fj[ks][jb], fi[ks][ib], acc[jb][ib]);
-    __builtin_amdgcn_sched_barrier(0);
+    if (kt + 1 < nk) stg.issue(ra, rb, rb2, smem + ((kt + 1) & 1) * kNtStage, wave, (kt + 1) * kNtBK);
+    nt_ktile(smem + (kt & 1) * kNtStage, offj, offi, lh, acc);
   }
 }
 
