@@ -22,6 +22,7 @@ from torch import Tensor
 from ._lib import check, lib
 
 BF16 = torch.bfloat16
+F32 = torch.float32
 
 
 def _ptr(t: Tensor | None) -> int | None:
@@ -184,6 +185,81 @@ def trimul(
 
 
 @trimul.register_fake
+def _(x, mask, norm_in_w, norm_in_b, p_in_w, g_in_w, norm_out_w, norm_out_b, p_out_w, g_out_w, outgoing):
+    return torch.empty_like(x)
+
+
+def trimul_f32_workspace_bytes(B: int, N: int, D: int) -> int:
+    return int(lib().bioemu_trimul_f32_workspace_bytes(B, N, D))
+
+
+def launch_trimul_f32(
+    x: Tensor,
+    mask: Tensor,
+    norm_in_w: Tensor,
+    norm_in_b: Tensor,
+    p_in_w: Tensor,
+    g_in_w: Tensor,
+    norm_out_w: Tensor,
+    norm_out_b: Tensor,
+    p_out_w: Tensor,
+    g_out_w: Tensor,
+    out: Tensor,
+    outgoing: bool,
+    residual: bool = False,
+    ws: Tensor | None = None,
+) -> Tensor:
+    """The triangle multiplicative update in IEEE fp32 (``bioemu_trimul_fwd_f32``): every tensor fp32."""
+    require_gpu(x, "trimul_f32")
+    if x.ndim != 4 or x.shape[1] != x.shape[2]:
+        raise ValueError(f"trimul_f32: x must be [B,N,N,D], got {tuple(x.shape)}")
+    B, N, _, D = x.shape
+    dev = x.device
+    _check_tensor(x, "trimul_f32 x", F32, (B, N, N, D), dev)
+    _check_tensor(out, "trimul_f32 out", F32, (B, N, N, D), dev)
+    _check_tensor(mask, "trimul_f32 mask", torch.uint8, (B, N, N), dev)
+    for name, t, shp in (
+        ("norm_in.weight", norm_in_w, (D,)), ("norm_in.bias", norm_in_b, (D,)),
+        ("p_in.weight", p_in_w, (2 * D, D)), ("g_in.weight", g_in_w, (2 * D, D)),
+        ("norm_out.weight", norm_out_w, (D,)), ("norm_out.bias", norm_out_b, (D,)),
+        ("p_out.weight", p_out_w, (D, D)), ("g_out.weight", g_out_w, (D, D)),
+    ):
+        _check_tensor(t, f"trimul_f32 {name}", F32, shp, dev)
+    need = trimul_f32_workspace_bytes(B, N, D)
+    if ws is None or ws.numel() < need:
+        ws = workspace(need, dev)
+    rc = lib().bioemu_trimul_fwd_f32(
+        _ptr(x), _ptr(mask), _ptr(norm_in_w), _ptr(norm_in_b), _ptr(p_in_w), _ptr(g_in_w),
+        _ptr(norm_out_w), _ptr(norm_out_b), _ptr(p_out_w), _ptr(g_out_w), _ptr(out),
+        _ptr(ws), ctypes.c_size_t(ws.numel()), B, N, D, int(bool(outgoing)), int(bool(residual)), _stream(x),
+    )
+    check(rc, "bioemu_trimul_fwd_f32")
+    return out
+
+
+@torch.library.custom_op("bioemu_mi355x::trimul_f32", mutates_args=(), device_types="cuda")
+def trimul_f32(
+    x: Tensor,
+    mask: Tensor,
+    norm_in_w: Tensor,
+    norm_in_b: Tensor,
+    p_in_w: Tensor,
+    g_in_w: Tensor,
+    norm_out_w: Tensor,
+    norm_out_b: Tensor,
+    p_out_w: Tensor,
+    g_out_w: Tensor,
+    outgoing: bool,
+) -> Tensor:
+    xf = x.contiguous()
+    out = torch.empty_like(xf)
+    f32c = lambda t: t.to(F32).contiguous()  # noqa: E731
+    launch_trimul_f32(xf, mask_u8(mask), f32c(norm_in_w), f32c(norm_in_b), f32c(p_in_w), f32c(g_in_w),
+                      f32c(norm_out_w), f32c(norm_out_b), f32c(p_out_w), f32c(g_out_w), out, outgoing)
+    return out
+
+
+@trimul_f32.register_fake
 def _(x, mask, norm_in_w, norm_in_b, p_in_w, g_in_w, norm_out_w, norm_out_b, p_out_w, g_out_w, outgoing):
     return torch.empty_like(x)
 
@@ -585,7 +661,6 @@ def _(s, z, mask, norm_s_w, norm_s_b, w_qkv, q_bias, w_g, norm_z_w, norm_z_b, w_
 # ----------------------------------------------------------------------------
 # fp32 arithmetic path (the reference's denoiser runs with autocast off)
 # ----------------------------------------------------------------------------
-F32 = torch.float32
 
 
 def fp32_mode(x: Tensor) -> bool:

@@ -485,6 +485,122 @@ __global__ __launch_bounds__(256) void swa_attn_f32_kernel(const float* __restri
   f32_attend_store<D>(o, l, g + off, go + off, true);
 }
 
+// ---------------------------------------------------------------------------
+// Triangle multiplicative update in fp32 (TriangleMultiplicationFull.forward,
+// src/bioemu2/biomoa/ops/triangle_multiplication.py:89-99, which upcasts the
+// projections before its einsum; TriangleMultiplicationCueq's default
+// matmul_precision "ieee", :117).  The same wave tiling as gemm_f32_kernel:
+// a wave owns a 32 x 32 block, weight rows in perm32 order as the A operand,
+// so lane (n, h) ends with 16 consecutive output columns 16 h + u of row n.
+// ---------------------------------------------------------------------------
+// acc (+ acc2 with a second weight matrix) over K (a multiple of 8); arow and
+// wrow / w2row already point at this lane's row and its k offset 4 h.
+template <bool kTwo>
+__device__ __forceinline__ void f32_block(const float* arow, const float* wrow, const float* w2row, int K, f32x16& acc,
+                                          f32x16& acc2) {
+  for (int k0 = 0; k0 < K; k0 += 8) {
+    const f32x4 a4 = *reinterpret_cast<const f32x4*>(arow + k0);
+    const f32x4 w4 = *reinterpret_cast<const f32x4*>(wrow + k0);
+    f32x4 v4;
+    if (kTwo) v4 = *reinterpret_cast<const f32x4*>(w2row + k0);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      acc = mfma_f32(w4[e], a4[e], acc);
+      if (kTwo) acc2 = mfma_f32(v4[e], a4[e], acc2);
+    }
+  }
+}
+
+// Gated, masked input projection p = (xn Wp^T) * sigmoid(xn Wg^T) * mask of
+// the pair rows m = (b, r1, r2), written channel-major into the contraction's
+// planes [b * 2D + c][i][k] (Np x Np each): (i, k) = (r1, r2) outgoing,
+// (r2, r1) incoming, so both directions contract planes as C = A B^T.
+__global__ __launch_bounds__(256) void trimul_proj_f32_kernel(const float* __restrict__ xn,
+                                                              const float* __restrict__ wp,
+                                                              const float* __restrict__ wg,
+                                                              const uint8_t* __restrict__ mask,
+                                                              float* __restrict__ planes, int N, int Np, int D,
+                                                              long long M, int outgoing) {
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int n = lane & 31, h = lane >> 5;
+  const int nbc = 2 * D / 32;
+  const long long blk = (long long)blockIdx.x * 4 + wave;
+  if (blk >= (M + 31) / 32 * nbc) return;   // no barriers in this kernel
+  const long long m = blk / nbc * 32 + n;
+  const int cb = (int)(blk % nbc);
+  const bool mvalid = m < M;
+  const size_t wr = (size_t)(cb * 32 + perm32(n)) * D + 4 * h;
+  f32x16 acc = zero16(), acc2 = zero16();
+  f32_block<true>(xn + (size_t)(mvalid ? m : 0) * D + 4 * h, wp + wr, wg + wr, D, acc, acc2);
+  if (!mvalid) return;
+  const float keep = mask[m] ? 1.f : 0.f;
+  const long long b = m / ((long long)N * N), rr = m % ((long long)N * N);
+  const int r1 = (int)(rr / N), r2 = (int)(rr % N);
+  const int i = outgoing ? r1 : r2, k = outgoing ? r2 : r1;
+  const size_t pl = (size_t)Np * Np;
+  float* dst = planes + ((size_t)b * 2 * D + cb * 32 + 16 * h) * pl + (size_t)i * Np + k;
+#pragma unroll
+  for (int u = 0; u < 16; ++u) dst[(size_t)u * pl] = acc[u] / (1.0f + expf(-acc2[u])) * keep;
+}
+
+// o[b, i, j, d] = sum_k A[z][i][k] B[z][j][k], z = b * D + d (planes Np x Np,
+// zero past N in k): a wave per 32 x 32 block of a plane; written pair-major.
+__global__ __launch_bounds__(256) void trimul_contract_f32_kernel(const float* __restrict__ planes,
+                                                                  float* __restrict__ o, int N, int Np, int Kp, int D) {
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int n = lane & 31, h = lane >> 5;
+  const int nb = Np / 32;
+  const long long blk = (long long)blockIdx.x * 4 + wave;
+  if (blk >= (long long)nb * nb) return;   // no barriers in this kernel
+  const int ib = (int)(blk / nb), jb = (int)(blk % nb);
+  const int z = blockIdx.y, b = z / D, d = z % D;
+  const size_t pl = (size_t)Np * Np;
+  const float* A = planes + ((size_t)b * 2 * D + d) * pl;
+  const float* Bm = A + (size_t)D * pl;
+  f32x16 acc = zero16(), unused = zero16();
+  const int i = ib * 32 + n;
+  f32_block<false>(A + (size_t)i * Np + 4 * h, Bm + (size_t)(jb * 32 + perm32(n)) * Np + 4 * h, nullptr, Kp, acc,
+                   unused);
+  if (i >= N) return;
+  float* dst = o + (((size_t)b * N + i) * N) * D + d;
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {
+    const int j = jb * 32 + 16 * h + u;
+    if (j < N) dst[(size_t)j * D] = acc[u];
+  }
+}
+
+// out = (on Wp_out^T) * gate (+ x): pair rows, D channels.
+__global__ __launch_bounds__(256) void trimul_out_f32_kernel(const float* __restrict__ on,
+                                                             const float* __restrict__ wo,
+                                                             const float* __restrict__ gate, const float* x,
+                                                             float* out, long long M, int D, int residual) {
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int n = lane & 31, h = lane >> 5;
+  const int nbc = D / 32;
+  const long long blk = (long long)blockIdx.x * 4 + wave;
+  if (blk >= (M + 31) / 32 * nbc) return;   // no barriers in this kernel
+  const long long m = blk / nbc * 32 + n;
+  const int cb = (int)(blk % nbc);
+  const bool mvalid = m < M;
+  f32x16 acc = zero16(), unused = zero16();
+  f32_block<false>(on + (size_t)(mvalid ? m : 0) * D + 4 * h, wo + (size_t)(cb * 32 + perm32(n)) * D + 4 * h, nullptr,
+                   D, acc, unused);
+  if (!mvalid) return;
+  const size_t off = (size_t)m * D + cb * 32 + 16 * h;
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {
+    float v = acc[u] * gate[off + u];
+    if (residual) v += x[off + u];
+    out[off + u] = v;
+  }
+}
+
+__global__ __launch_bounds__(256) void fill_zero_f32_kernel(float* __restrict__ p, long long count) {
+  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (i < count) p[i] = 0.f;
+}
+
 int gemm_f32(int epi, const float* A, const float* W, const float* W2, const float* bias, const float* res, float* out,
              long long M, int K, int N, hipStream_t stream, const char* name, int T = 1, int ldT = 1) {
   if (K % 8 || N % 32 || M <= 0)
@@ -757,4 +873,85 @@ extern "C" int bioemu_pair_cond_proj_fwd_f32(const float* z_trunk, const float* 
   if (rc) return rc;
   return gemm_f32(kGemmEpiStore, xn, w, nullptr, nullptr, nullptr, out, P, (int)(token_z + c_rel), (int)a_z, stream,
                   "f32_pair_cond_proj");
+}
+
+// ---------------------------------------------------------------------------
+// Triangle multiplicative update, fp32 arithmetic.
+// ---------------------------------------------------------------------------
+static int64_t trimul_f32_np(int64_t N) { return round_up(N, 32); }
+
+extern "C" size_t bioemu_trimul_f32_workspace_bytes(int64_t B, int64_t N, int64_t Dc) {
+  if (B <= 0 || N <= 0 || Dc <= 0 || Dc % 32) return 0;
+  const size_t P = (size_t)B * N * N, Np = (size_t)trimul_f32_np(N);
+  // xn (then LN_out(o)), the output gate, o: [P][D] each; the planes [B][2D][Np][Np]
+  return (size_t)round_up(P * Dc * 4, 256) * 3 + (size_t)round_up(B * 2 * Dc * Np * Np * 4, 256);
+}
+
+extern "C" int bioemu_trimul_fwd_f32(const float* x, const uint8_t* mask, const float* norm_in_w,
+                                     const float* norm_in_b, const float* p_in_w, const float* g_in_w,
+                                     const float* norm_out_w, const float* norm_out_b, const float* p_out_w,
+                                     const float* g_out_w, float* out, void* workspace, size_t workspace_bytes,
+                                     int64_t B, int64_t N, int64_t Dc, int outgoing, int residual,
+                                     hipStream_t stream) {
+  if (Dc <= 0 || Dc % 32)
+    return set_error(BIOEMU_ERR_UNSUPPORTED, "trimul_f32: dim must be a multiple of 32 (got %lld)", (long long)Dc);
+  if (B <= 0 || N <= 0 || B * Dc > 65535 || N > 16384)
+    return set_error(BIOEMU_ERR_INVALID_ARG, "trimul_f32: bad shape B=%lld N=%lld (B * dim <= 65535)", (long long)B,
+                     (long long)N);
+  if (!x || !mask || !norm_in_w || !norm_in_b || !p_in_w || !g_in_w || !norm_out_w || !norm_out_b || !p_out_w ||
+      !g_out_w || !out || !workspace)
+    return set_error(BIOEMU_ERR_INVALID_ARG, "trimul_f32: null pointer argument");
+  if (!aligned16(x) || !aligned16(out) || !aligned16(p_in_w) || !aligned16(g_in_w) || !aligned16(p_out_w) ||
+      !aligned16(g_out_w) || !aligned16(workspace))
+    return set_error(BIOEMU_ERR_INVALID_ARG, "trimul_f32: tensors must be 16-byte aligned");
+  if (out == x && !residual)
+    return set_error(BIOEMU_ERR_INVALID_ARG, "trimul_f32: out may alias x only with residual=1");
+  if (workspace_bytes < bioemu_trimul_f32_workspace_bytes(B, N, Dc))
+    return set_error(BIOEMU_ERR_WORKSPACE, "trimul_f32: workspace too small");
+  const long long P = B * N * N;
+  const int64_t Np = trimul_f32_np(N);
+  const int D = (int)Dc;
+  char* p = static_cast<char*>(workspace);
+  float* xn = reinterpret_cast<float*>(p);
+  p += round_up(P * Dc * 4, 256);
+  float* gate = reinterpret_cast<float*>(p);
+  p += round_up(P * Dc * 4, 256);
+  float* o = reinterpret_cast<float*>(p);
+  p += round_up(P * Dc * 4, 256);
+  float* planes = reinterpret_cast<float*>(p);
+  const long long plane_count = B * 2 * Dc * Np * Np;
+
+  int rc = rows_ln_f32(x, norm_in_w, norm_in_b, xn, P, D, stream, "f32_trimul_ln_in");
+  if (rc) return rc;
+  {
+    KernelTimerScope timed("f32_fill", stream);
+    hipLaunchKernelGGL(fill_zero_f32_kernel, dim3((unsigned)((plane_count + 255) / 256)), dim3(256), 0, stream,
+                       planes, plane_count);
+  }
+  if ((rc = check_launch("f32_fill"))) return rc;
+  {
+    const long long blocks = (P + 31) / 32 * (2 * D / 32);
+    KernelTimerScope timed("f32_trimul_proj", stream);
+    hipLaunchKernelGGL(trimul_proj_f32_kernel, dim3((unsigned)((blocks + 3) / 4)), dim3(256), 0, stream, xn, p_in_w,
+                       g_in_w, mask, planes, (int)N, (int)Np, D, P, outgoing);
+  }
+  if ((rc = check_launch("f32_trimul_proj"))) return rc;
+  rc = gemm_f32(kGemmEpiSigmoid, xn, g_out_w, nullptr, nullptr, nullptr, gate, P, D, D, stream, "f32_trimul_gate");
+  if (rc) return rc;
+  {
+    const long long nb = Np / 32;
+    KernelTimerScope timed("f32_trimul_contract", stream);
+    hipLaunchKernelGGL(trimul_contract_f32_kernel, dim3((unsigned)((nb * nb + 3) / 4), (unsigned)(B * Dc)), dim3(256), 0,
+                       stream, planes, o, (int)N, (int)Np, (int)round_up(N, 8), D);
+  }
+  if ((rc = check_launch("f32_trimul_contract"))) return rc;
+  rc = rows_ln_f32(o, norm_out_w, norm_out_b, xn, P, D, stream, "f32_trimul_ln_out");
+  if (rc) return rc;
+  {
+    const long long blocks = (P + 31) / 32 * (D / 32);
+    KernelTimerScope timed("f32_trimul_out", stream);
+    hipLaunchKernelGGL(trimul_out_f32_kernel, dim3((unsigned)((blocks + 3) / 4)), dim3(256), 0, stream, xn, p_out_w,
+                       gate, x, out, P, D, residual);
+  }
+  return check_launch("f32_trimul_out");
 }

@@ -70,6 +70,10 @@ class PairMixerLayerHip(nn.Module, _WorkspaceMixin):
         return max(_ops.trimul_workspace_bytes(B, N, self.token_z),
                    _ops.transition_pair_workspace_bytes(self.token_z, self.transition_z.hidden))
 
+    def workspace_bytes_f32(self, B: int, N: int) -> int:
+        return max(_ops.trimul_f32_workspace_bytes(B, N, self.token_z),
+                   _ops.transition_f32_workspace_bytes(B * N * N, self.token_z, self.transition_z.hidden))
+
     @torch.no_grad()
     def forward_(
         self, s: Tensor, z: Tensor, pair_mask: Tensor, z_tail: Tensor | None = None, ws: Tensor | None = None
@@ -86,8 +90,28 @@ class PairMixerLayerHip(nn.Module, _WorkspaceMixin):
         _ops.launch_transition_pair(z, *self.transition_z.prepared_params(), z, residual=True, ws=ws, tail=z_tail)
         return s, z
 
+    @torch.no_grad()
+    def forward_f32_(self, s: Tensor, z: Tensor, pair_mask: Tensor, ws: Tensor | None = None
+                     ) -> tuple[Tensor, Tensor]:
+        """In place on fp32 ``z`` in IEEE fp32 arithmetic (the reference run with autocast off): the two
+        triangle multiplications and the transition, each adding its update into z."""
+        _ops.require_gpu(z, type(self).__name__)
+        if ws is None:
+            ws = self._workspace(self.workspace_bytes_f32(z.shape[0], z.shape[1]), z.device)
+        pm = _ops.mask_u8(pair_mask)
+        _ops.launch_trimul_f32(z, pm, *self.tri_mul_out.prepared_params_f32(), z, True, residual=True, ws=ws)
+        _ops.launch_trimul_f32(z, pm, *self.tri_mul_in.prepared_params_f32(), z, False, residual=True, ws=ws)
+        _ops.launch_transition_f32(z, *self.transition_z.prepared_params_f32(), z, residual=True, ws=ws)
+        return s, z
+
     def forward(self, s: Tensor, z: Tensor, pair_mask: Tensor) -> tuple[Tensor, Tensor]:
-        _ops.require_mixed_precision(z, type(self).__name__)
+        """bf16 (or fp32 under bf16 autocast): the bf16 path with z carried as bf16 + int8 tail; fp32 with
+        autocast off: IEEE fp32 arithmetic."""
+        _ops.require_gpu(z, type(self).__name__)
+        if _ops.fp32_mode(z):
+            z32 = z.contiguous().clone()
+            self.forward_f32_(s, z32, pair_mask)
+            return s, z32
         z_hi, z_tail = split_stream(z)
         self.forward_(s, z_hi, pair_mask, z_tail)
         return s, join_stream(z_hi, z_tail, z.dtype)
@@ -219,7 +243,16 @@ class PairMixerModuleHip(nn.Module, _WorkspaceMixin):
         return s, z
 
     def forward(self, s: Tensor, z: Tensor, pair_mask: Tensor) -> tuple[Tensor, Tensor]:
-        _ops.require_mixed_precision(z, type(self).__name__)
+        """bf16 (or fp32 under bf16 autocast): one bf16 + int8-tail z stream through every layer; fp32 with
+        autocast off: every layer in IEEE fp32 arithmetic on one fp32 z."""
+        _ops.require_gpu(z, type(self).__name__)
+        if _ops.fp32_mode(z):
+            z32 = z.contiguous().clone()
+            ws = self._workspace(self.layers[0].workspace_bytes_f32(z.shape[0], z.shape[1]), z.device) \
+                if len(self.layers) else None
+            for layer in self.layers:   # pairmixer.py:368-369
+                layer.forward_f32_(s, z32, pair_mask, ws=ws)
+            return s, z32
         z_hi, z_tail = split_stream(z)
         self.forward_(s, z_hi, pair_mask, z_tail)
         return s, join_stream(z_hi, z_tail, z.dtype)

@@ -74,9 +74,13 @@ class TriangleMultiplicationHip(_TriMulBase):
     (``dim, mode, tile_size, matmul_precision``).  ``tile_size`` is accepted
     for registry compatibility and unused (the kernels tile internally and
     keep N^2 scratch in HBM).  ``matmul_precision`` is validated and
-    recorded; the contraction always runs as bf16 MFMA with fp32
-    accumulation.  Input/output dtype follows ``x`` (fp32 inputs are
-    computed in that bf16 mode).  Inference only: there is no backward.
+    recorded.  bf16 inputs, or fp32 inputs under bf16 autocast (the
+    reference trunk's policy), run the bf16 path: bf16 MFMA operands, fp32
+    accumulation, output in x's dtype.  fp32 inputs with autocast off run
+    IEEE fp32 arithmetic throughout (``bioemu_trimul_fwd_f32``), as the
+    reference's ``"ieee"`` default and TriangleMultiplicationFull's fp32
+    einsum do (triangle_multiplication.py:94, :117).  Inference only: there is
+    no backward.
     """
 
     def __init__(
@@ -95,13 +99,20 @@ class TriangleMultiplicationHip(_TriMulBase):
         self.tile_size = tile_size
         self._matmul_precision = matmul_precision
         self._prepared = PreparedParams(TRIMUL_PARAM_SPEC)
+        self._prepared32 = PreparedParams([(name, _F32) for name, _ in TRIMUL_PARAM_SPEC])
 
     def prepared_params(self) -> tuple[Tensor, ...]:
         return self._prepared.get(self)
 
+    def prepared_params_f32(self) -> tuple[Tensor, ...]:
+        return self._prepared32.get(self)
+
     def forward(self, x: Tensor, mask: Tensor) -> Tensor:
         _ops.require_gpu(x, type(self).__name__)
-        _ops.require_mixed_precision(x, type(self).__name__)
+        if _ops.fp32_mode(x):
+            return torch.ops.bioemu_mi355x.trimul_f32(
+                x, _ops.mask_u8(mask), *self.prepared_params_f32(), self.mode == "outgoing"
+            )
         return torch.ops.bioemu_mi355x.trimul(
             x, _ops.mask_u8(mask), *self.prepared_params(), self.mode == "outgoing"
         )

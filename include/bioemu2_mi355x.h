@@ -359,6 +359,12 @@ int bioemu_msa_embed_fwd(const float* msa, const float* has_deletion, const floa
  *                            concatenation [z_trunk row | rel row] is read in place;
  *                            token_z + c_rel a multiple of 8, a_z of 32.  Its transitions
  *                            (:526-527) are bioemu_transition_fwd_f32 with residual=1.
+ *   bioemu_trimul_fwd_f32    the triangle multiplicative update in IEEE fp32, for a trunk run
+ *                            with autocast off (TriangleMultiplicationFull.forward,
+ *                            triangle_multiplication.py:89-99; TriangleMultiplicationCueq with
+ *                            its default matmul_precision="ieee", :104-125): the arguments of
+ *                            bioemu_trimul_fwd without res_tail; dim a multiple of 32,
+ *                            B * dim <= 65535.
  * Residual tails do not apply (the stream is fp32).
  */
 size_t bioemu_apb_f32_workspace_bytes(int64_t B, int64_t mult, int64_t N, int64_t c_s, int64_t H);
@@ -383,6 +389,12 @@ size_t bioemu_pair_cond_f32_workspace_bytes(int64_t P, int64_t token_z, int64_t 
 int bioemu_pair_cond_proj_fwd_f32(const float* z_trunk, const float* rel, const float* ln_w, const float* ln_b,
                                   const float* w, float* out, void* workspace, size_t workspace_bytes, int64_t P,
                                   int64_t token_z, int64_t c_rel, int64_t a_z, hipStream_t stream);
+size_t bioemu_trimul_f32_workspace_bytes(int64_t B, int64_t N, int64_t Dc);
+int bioemu_trimul_fwd_f32(const float* x, const uint8_t* mask, const float* norm_in_w, const float* norm_in_b,
+                          const float* p_in_w, const float* g_in_w, const float* norm_out_w, const float* norm_out_b,
+                          const float* p_out_w, const float* g_out_w, float* out, void* workspace,
+                          size_t workspace_bytes, int64_t B, int64_t N, int64_t Dc, int outgoing, int residual,
+                          hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -1,11 +1,14 @@
-"""fp32 arithmetic path of the denoiser's ops vs the fp32 CPU oracle at 1e-5 relative.
+"""fp32 arithmetic paths vs the fp32 CPU oracle at 1e-5 relative.
 
 The reference runs its denoiser with autocast off (score_model.py:355, model.py:387):
 AttentionPairBias, AttentionPairBiasSlidingWindow and Transition see fp32 inputs
-there and compute in fp32.  The modules route fp32 inputs (autocast off) to the
-``*_f32`` entry points; these tests hold them to the fp32-mode bound (relative
-L2 error and max-abs error relative to the output's magnitude, both <= 1e-5),
-and masking/padding to bit-exactness.
+there and compute in fp32.  A trunk run with autocast off computes the triangle
+multiplication in IEEE fp32 (TriangleMultiplicationCueq's default
+matmul_precision="ieee", triangle_multiplication.py:117; the Full variant's
+fp32 einsum, :94), so the PairMixer layers do too.  The modules route fp32
+inputs (autocast off) to the ``*_f32`` entry points; these tests hold them to
+the fp32-mode bound (relative L2 error and max-abs error relative to the
+output's magnitude, both <= 1e-5), and masking/padding to bit-exactness.
 """
 
 from __future__ import annotations
@@ -262,3 +265,79 @@ def test_pairwise_conditioning_f32_matches_oracle(gpu_device, token_z, c_rel, a_
     _check(got, want, f"pair_cond_f32 {token_z}+{c_rel}->{a_z} T={num_transitions} {shape}")
     # row-wise: a sub-block of pairs gives identical bits
     assert torch.equal(mod(z[:, 1:3].contiguous(), rel[:, 1:3].contiguous()).cpu(), got[:, 1:3])
+
+
+# ----------------------------------------------------------------------------
+# Triangle multiplication and the PairMixer layers in fp32
+# ----------------------------------------------------------------------------
+def _trimul(device, mode, dim=128, seed=42):
+    from bioemu2_amd.triangle_multiplication import TriangleMultiplicationHip
+
+    torch.manual_seed(seed)
+    m = TriangleMultiplicationHip(dim=dim, mode=mode, matmul_precision="ieee")
+    return randomize_params(m, seed).to(device).eval()
+
+
+@pytest.mark.parametrize("mode", ["outgoing", "incoming"])
+@pytest.mark.parametrize("n,dim", [(16, 128), (37, 128), (100, 64), (130, 128)])
+def test_trimul_f32_matches_oracle(gpu_device, mode, n, dim):
+    print(f"trimul_f32 {mode} n={n} dim={dim}", flush=True)
+    m = _trimul(gpu_device, mode, dim)
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(1, n, n, dim, generator=g)
+    mask = torch.rand(1, n, n, generator=g) < 0.75
+    with torch.no_grad():
+        got = m(x.to(gpu_device), mask.to(gpu_device)).cpu()
+    _check(got, oracle.trimul(x, mask, state(m), mode), f"trimul_f32 {mode} n={n} dim={dim}")
+
+
+@pytest.mark.parametrize("mode", ["outgoing", "incoming"])
+def test_trimul_f32_padding_batch_and_residual(gpu_device, mode):
+    """Token padding (pair mask = outer AND) at N = 48, two systems in a batch: each system alone gives its
+    batch slice bit for bit; the padded tokens' values do not reach the valid outputs (bit-exact); the fused
+    residual equals x + update bit for bit."""
+    m = _trimul(gpu_device, mode)
+    n, d = 48, gpu_device
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(2, n, n, 128, generator=g)
+    tok = torch.ones(2, n, dtype=torch.bool)
+    tok[0, n - 5:] = False
+    tok[1, n - 11:] = False
+    pm = oracle.pair_mask_from_token_mask(tok)
+    with torch.no_grad():
+        both = m(x.to(d), pm.to(d))
+        _check(both.cpu(), oracle.trimul(x, pm, state(m), mode), f"trimul_f32 {mode} padded batch")
+        for b in range(2):
+            assert torch.equal(m(x[b:b + 1].contiguous().to(d), pm[b:b + 1].contiguous().to(d)), both[b:b + 1])
+        x2 = x.clone()
+        x2[1, n - 11:] = 7.0
+        x2[1, :, n - 11:] = -3.0
+        v = n - 11
+        assert torch.equal(m(x2.to(d), pm.to(d))[1, :v, :v], both[1, :v, :v])
+        xr = x.to(d).contiguous()
+        _ops.launch_trimul_f32(xr, _ops.mask_u8(pm.to(d)), *m.prepared_params_f32(), xr, mode == "outgoing",
+                               residual=True)
+        assert torch.equal(xr, x.to(d) + both)
+
+
+def test_pairmixer_layer_and_module_f32_match_oracle(gpu_device):
+    """PairMixerLayer / PairMixerModule with autocast off: both triangle multiplications and the transition in
+    fp32 (pairmixer.py:446-456, :368-369), against the oracle at the fp32 bound."""
+    from bioemu2_amd.pairmixer import PairMixerLayerHip, PairMixerModuleHip
+
+    n, d = 40, gpu_device
+    g = torch.Generator().manual_seed(5)
+    s = torch.randn(1, n, 384, generator=g)
+    z = torch.randn(1, n, n, 128, generator=g)
+    tok = torch.ones(1, n, dtype=torch.bool)
+    tok[:, n - 4:] = False
+    pm = oracle.pair_mask_from_token_mask(tok)
+    torch.manual_seed(0)
+    layer = randomize_params(PairMixerLayerHip(384, 128), 1).to(d).eval()
+    _, got = layer(s.to(d), z.to(d), pm.to(d))
+    _, want = oracle.pairmixer_layer(s, z, pm, state(layer))
+    _check(got.cpu(), want, "pairmixer_layer_f32")
+    mod = randomize_params(PairMixerModuleHip(384, 128, 2), 2).to(d).eval()
+    _, got = mod(s.to(d), z.to(d), pm.to(d))
+    _, want = oracle.pairmixer_module(s, z, pm, state(mod), 2)
+    _check(got.cpu(), want, "pairmixer_module_f32 (2 layers)")

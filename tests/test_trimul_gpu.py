@@ -192,20 +192,20 @@ def test_rejects_cpu_tensors():
 
 
 def test_rejects_unsupported_dim(gpu_device):
+    """The bf16 path supports dim 128 only (the fp32 path takes any multiple of 32)."""
     m = TriangleMultiplicationHip(dim=64).to(gpu_device)
     with pytest.raises(ValueError):
-        m(torch.zeros(1, 8, 8, 64, device=gpu_device), torch.ones(1, 8, 8, dtype=torch.bool, device=gpu_device))
+        m(torch.zeros(1, 8, 8, 64, device=gpu_device, dtype=torch.bfloat16),
+          torch.ones(1, 8, 8, dtype=torch.bool, device=gpu_device))
 
 
-def test_fp32_outside_autocast_is_refused(gpu_device):
-    """fp32 inputs with autocast off ask for the reference's IEEE fp32 contraction (TriangleMultiplicationCueq's
-    default matmul_precision="ieee", triangle_multiplication.py:117), which this op does not compute: ValueError.
-    Under bf16 autocast the same fp32 input takes the bf16 path and returns fp32."""
+def test_fp32_autocast_selects_the_bf16_path(gpu_device):
+    """fp32 inputs under bf16 autocast (the reference trunk's policy) take the bf16 path and return fp32: the bf16
+    result of the same (bf16-representable) input, cast.  With autocast off they take the fp32 path
+    (tests/test_fp32_gpu.py)."""
     m = _module("outgoing", gpu_device)
     x, mask = _inputs(40, gpu_device)
     with torch.no_grad():
-        with pytest.raises(ValueError, match="autocast"):
-            m(x.float(), mask)
         with torch.autocast("cuda", dtype=torch.bfloat16):
             got = m(x.float(), mask)
         want = m(x, mask)
