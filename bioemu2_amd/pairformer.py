@@ -90,19 +90,21 @@ class PairformerBlockHip(nn.Module):
         s_tail: Tensor | None = None,
         z_tail: Tensor | None = None,
         ws: Tensor | None = None,
+        masks: tuple[Tensor, Tensor] | None = None,
     ) -> tuple[Tensor, Tensor]:
         """In-place block on bf16 ``s [B,N,c_s]``, ``z [B,N,N,c_z]``, ``token_mask [B,N]``.
 
         ``s_tail`` / ``z_tail``: int8 tails of the residual streams (same shapes), updated in place;
         ``None`` keeps that stream in plain bf16.  ``ws``: a caller-owned workspace of at least
-        ``workspace_bytes(B, N)`` bytes (default: one the block caches per shape).  The masks are
-        built from ``token_mask`` on every call.
+        ``workspace_bytes(B, N)`` bytes (default: one the block caches per shape).  ``masks``: the
+        ``pair_masks(token_mask)`` pair, built once by a caller that runs many blocks or steps on the
+        same mask (default: built from ``token_mask`` here, two small allocations per call).
         """
         _ops.require_gpu(z, type(self).__name__)
         B, N = token_mask.shape
         if ws is None:
             ws = self._workspace(B, N, z.device)
-        tok, pm = pair_masks(token_mask)
+        tok, pm = masks if masks is not None else pair_masks(token_mask)
         _ops.launch_trimul(z, pm, *self.tri_mul_out.prepared_params(), z, True, residual=True, ws=ws, tail=z_tail)
         _ops.launch_trimul(z, pm, *self.tri_mul_in.prepared_params(), z, False, residual=True, ws=ws, tail=z_tail)
         _ops.launch_triatt(z, pm, *self.tri_att_start.prepared_params(), z, True, residual=True, ws=ws, tail=z_tail)

@@ -1,10 +1,10 @@
 """Synthetic, HBM-resident workloads for the benchmark configs.
 
 Each workload owns its seeded inputs, random-init weights, preallocated
-outputs and workspaces, so ``step()`` launches kernels and allocates nothing
-(except the out-of-place ones: config 1 and the PairMixer trunk pass build
-their fp32 <-> bf16 + tail streams through torch's caching allocator, as a
-caller of ``forward`` would).
+outputs, workspaces and masks, so ``step()`` launches kernels and allocates
+nothing (except the out-of-place ones: config 1 and the PairMixer trunk pass
+build their fp32 <-> bf16 + tail streams and masks through torch's caching
+allocator, as a caller of ``forward`` would).
 ``kernel_work(name)`` gives the algorithmic work of one launch of a named
 kernel at the workload's shape: ``("mfma", flops)`` or ``("hbm", bytes)``,
 chosen by comparing the kernel's flops per minimum HBM byte with the MI355X
@@ -240,7 +240,7 @@ class BlockWorkload(Workload):
     cpu_calls = 3
 
     def __init__(self, device, n: int = 768, seed: int = 0, tails: bool = True):
-        from .pairformer import PairformerBlockHip
+        from .pairformer import PairformerBlockHip, pair_masks
 
         self.n = n
         self.tails = tails
@@ -262,11 +262,12 @@ class BlockWorkload(Workload):
         self.z_tail = torch.zeros(self.z.shape, dtype=torch.int8, device=device) if tails else None
         self.s_tail = torch.zeros(self.s.shape, dtype=torch.int8, device=device) if tails else None
         self.tok = token_mask(n, self.n_pad, device)
+        self.masks = pair_masks(self.tok)
         self.ws = _ops.workspace(self.module.workspace_bytes(1, n), device)
         self.flops = block_flops(n, n_valid=n - self.n_pad)
 
     def step(self) -> None:
-        self.module.forward_(self.s, self.z, self.tok, self.s_tail, self.z_tail, ws=self.ws)
+        self.module.forward_(self.s, self.z, self.tok, self.s_tail, self.z_tail, ws=self.ws, masks=self.masks)
 
     def cpu_sample(self, oracle):
         s = self.s_cpu.float()
@@ -312,7 +313,10 @@ class Config1Workload(BlockWorkload):
         super().__init__(device, n, seed)
         self.n_pad = 0
         self.flops = block_flops(n)
+        from .pairformer import pair_masks
+
         self.tok = token_mask(n, 0, device)
+        self.masks = pair_masks(self.tok)
         self.name = f"pairformer_block_n{n}_fp32io"
         self.metric = f"ms per Pairformer block at N={n}, fp32 in/out"
         self.config = dict(self.config, workload=self.name, padded_tokens=0, io="fp32")
@@ -345,7 +349,7 @@ class TrunkWorkload(BlockWorkload):
 
     def step(self) -> None:
         for blk in self.blocks:
-            blk.forward_(self.s, self.z, self.tok, self.s_tail, self.z_tail, ws=self.ws)
+            blk.forward_(self.s, self.z, self.tok, self.s_tail, self.z_tail, ws=self.ws, masks=self.masks)
 
     def cpu_sample(self, oracle):
         """One fp32 oracle block at N=512 (5 % padded), scaled to the trunk by algorithmic flops
