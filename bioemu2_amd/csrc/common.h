@@ -118,42 +118,60 @@ __device__ __forceinline__ void unpack8(bf16x8 v, float* out) {
 // residual read hi + tail and write the sum back as a new (hi, tail).  Tail
 // planes have the layout of their stream with one byte per element.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ int bf16_exp_field(bf16 v) {
-  return (int)((__builtin_bit_cast(uint16_t, v) >> 7) & 0xffu);
-}
+// The helpers work on the fp32 bit pattern of hi (a bf16 widened to fp32 is
+// its 16 bits shifted up), so the exponent field is one bit-field extract of a
+// 32-bit register.
+__device__ __forceinline__ int f32_exp_field(uint32_t bits) { return (int)((bits >> 23) & 0xffu); }
 
-// hi + t * 2^(E(hi) - 142)
-__device__ __forceinline__ float tail_decode(bf16 hi, int t) {
-  return bf2f(hi) + __builtin_amdgcn_ldexpf((float)t, bf16_exp_field(hi) - 142);
-}
-
-// Splits v into (hi, t); returns hi, writes t in [-127, 127].
-__device__ __forceinline__ bf16 tail_encode(float v, int& t) {
-  const bf16 hi = f2bf(v);
-  const float r = __builtin_amdgcn_ldexpf(v - bf2f(hi), 142 - bf16_exp_field(hi));
-  t = (int)__builtin_amdgcn_fmed3f(__builtin_rintf(r), -127.f, 127.f);
-  return hi;
+// hi + t * 2^(E(hi) - 142), hi given as its fp32 bit pattern
+__device__ __forceinline__ float tail_decode_bits(uint32_t hb, int t) {
+  return __builtin_bit_cast(float, hb) + __builtin_amdgcn_ldexpf((float)t, f32_exp_field(hb) - 142);
 }
 
 // Sixteen consecutive elements: raw bf16 halves r0, r1 and their 16 tail bytes
 // -> fp32 values.
 __device__ __forceinline__ void tail_decode16(bf16x8 r0, bf16x8 r1, u32x4 tb, float* v) {
+  const u32x4 w0 = __builtin_bit_cast(u32x4, r0), w1 = __builtin_bit_cast(u32x4, r1);
 #pragma unroll
   for (int u = 0; u < 16; ++u) {
+    const uint32_t w = u < 8 ? w0[(u >> 1) & 3] : w1[(u >> 1) & 3];
+    const uint32_t hb = (u & 1) ? (w & 0xffff0000u) : (w << 16);
     const int t = __builtin_amdgcn_sbfe((int)tb[u >> 2], 8 * (u & 3), 8);
-    v[u] = tail_decode(u < 8 ? r0[u] : r1[u - 8], t);
+    v[u] = tail_decode_bits(hb, t);
   }
 }
 
 // Sixteen fp32 values -> bf16 halves a (values 0-7), b (8-15) and their tail bytes.
+// t = clamp(round(r * 2^(142 - E)), -127, 127) with r = v - hi exact: the
+// remainder is clamped first and rounded to nearest even by adding 1.5 * 2^23,
+// which leaves t in the low byte of the sum's bit pattern (two's complement);
+// clamping before or after rounding gives the same integer.
 __device__ __forceinline__ void tail_encode16(const float* v, bf16x8& a, bf16x8& b, u32x4& tb) {
-  tb = u32x4{0u, 0u, 0u, 0u};
+  uint32_t y[16];
 #pragma unroll
-  for (int u = 0; u < 16; ++u) {
-    int t;
-    const bf16 hi = tail_encode(v[u], t);
-    if (u < 8) a[u] = hi; else b[u - 8] = hi;
-    tb[u >> 2] |= ((uint32_t)t & 0xffu) << (8 * (u & 3));
+  for (int u = 0; u < 16; u += 2) {
+    const bf16x2 hp = {f2bf(v[u]), f2bf(v[u + 1])};
+    const uint32_t w = __builtin_bit_cast(uint32_t, hp);
+    if (u < 8) {
+      a[u] = hp[0];
+      a[u + 1] = hp[1];
+    } else {
+      b[u - 8] = hp[0];
+      b[u - 7] = hp[1];
+    }
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const uint32_t hb = e ? (w & 0xffff0000u) : (w << 16);
+      const float r = __builtin_amdgcn_ldexpf(v[u + e] - __builtin_bit_cast(float, hb), 142 - f32_exp_field(hb));
+      y[u + e] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_fmed3f(r, -127.f, 127.f) + 12582912.0f);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    // low bytes of y[4k .. 4k + 3] -> bytes 0..3 of word k
+    const uint32_t lo = __builtin_amdgcn_perm(y[4 * k + 1], y[4 * k], 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm(y[4 * k + 3], y[4 * k + 2], 0x0c0c0400u);
+    tb[k] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
   }
 }
 
