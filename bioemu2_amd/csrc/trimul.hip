@@ -233,6 +233,7 @@ __device__ __forceinline__ void normalize_half_row(const float* v, bf16x8 out[8]
 // ---------------------------------------------------------------------------
 constexpr int kOutThreads = 512;
 constexpr int kOutWaves = kOutThreads / 64;
+constexpr int kOutPlaneSpan = 23;       // planes past its base that one o copy instruction reaches
 constexpr int kOutTile = D * 32 + 32;   // per-wave o buffer, bf16 elements
 constexpr int kOutSmem = 2 * D * kLdw * 2 + 2 * D * 4 + kOutWaves * kOutTile * 2;
 
@@ -292,18 +293,22 @@ __global__ __launch_bounds__(kOutThreads) void trimul_out_kernel(
   // the x / tail loads and the current tile's stores issued after them.
   bf16x8 xraw[8];
   u32x4 traw[4];
+  // Copy instruction q reads channels c_q + 16 (slot >> 3) + (slot & 7),
+  // c_q = 32 (q & 3) + 8 (q >> 2), through a buffer resource based at its own
+  // first plane: 24 planes from that base, so 32-bit offsets hold for
+  // 23 Np^2 + 32 elements (N <= 9472), the whole 128-plane span need not.
+  const unsigned o_extent = (unsigned)((kOutPlaneSpan * plane + 32) * 2);
   auto fetch = [&](unsigned tt) {
     const TileIdx ti = split_tile(tt, tiles_per_row, N);
     const int i = ti.row, b = ti.b, j0 = ti.col * 32;
-    const __amdgpu_buffer_rsrc_t ors =
-        buffer_rsrc(o + (size_t)b * D * plane + (size_t)i * Np + j0, (unsigned)(((D - 1) * plane + 32) * 2));
+    const bf16* obase = o + (size_t)b * D * plane + (size_t)i * Np + j0;
     const int slot = lane >> 2;
     const unsigned ovoff = ((unsigned)(16 * (slot >> 3) + (slot & 7)) * (unsigned)plane + 8u * (lane & 3)) * 2u;
 #pragma unroll
     for (int q = 0; q < 8; ++q)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          ors, (__attribute__((address_space(3))) void*)(ob + 512 * q + (q >= 4 ? 32 : 0)), 16, ovoff,
-          (unsigned)(32 * (q & 3) + 8 * (q >> 2)) * (unsigned)plane * 2u, 0, 0);
+          buffer_rsrc(obase + (size_t)(32 * (q & 3) + 8 * (q >> 2)) * plane, o_extent),
+          (__attribute__((address_space(3))) void*)(ob + 512 * q + (q >= 4 ? 32 : 0)), 16, ovoff, 0u, 0, 0);
     // Nothing may be scheduled above the copies: the wait in prepare() counts
     // every vector-memory operation issued after them.
     __builtin_amdgcn_sched_barrier(0);
@@ -461,13 +466,11 @@ extern "C" int bioemu_trimul_fwd(const void* x, const uint8_t* mask, const float
   if (!x || !mask || !norm_in_w || !norm_in_b || !p_in_w || !g_in_w || !norm_out_w || !norm_out_b ||
       !p_out_w || !g_out_w || !out || !workspace)
     return set_error(BIOEMU_ERR_INVALID_ARG, "trimul: null pointer argument");
-  // trimul_out reads a tile's 128 contraction planes through one buffer
-  // resource spanning (D - 1) planes plus a row: its byte extent and offsets
-  // are 32-bit, which holds for N up to 4096 (plane 4096^2; 4.26e9 bytes).
-  if ((uint64_t)(Dc - 1) * round_up(N, kGemmTile) * round_up(N, kGemmTile) * 2 + 64 > 0xffffffffull)
-    return set_error(BIOEMU_ERR_UNSUPPORTED,
-                     "trimul: N=%lld too large (a tile's contraction planes must span under 4 GiB; N <= 4096)",
-                     (long long)N);
+  // trimul_out reads a tile's contraction planes through buffer resources that
+  // span 23 planes plus a row each: byte extents and offsets are 32-bit, which
+  // holds for N up to 9472 (padded plane 9472^2).
+  if (((uint64_t)kOutPlaneSpan * round_up(N, kGemmTile) * round_up(N, kGemmTile) + 32) * 2 > 0xffffffffull)
+    return set_error(BIOEMU_ERR_UNSUPPORTED, "trimul: N=%lld too large (N <= 9472)", (long long)N);
   if (!aligned16(x) || !aligned16(out) || !aligned16(p_in_w) || !aligned16(g_in_w) ||
       !aligned16(p_out_w) || !aligned16(g_out_w) || !aligned16(workspace))
     return set_error(BIOEMU_ERR_INVALID_ARG, "trimul: x/out/weights/workspace must be 16-byte aligned");

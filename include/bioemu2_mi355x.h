@@ -74,7 +74,7 @@ int bioemu_timer_query(int idx, char* name, size_t name_len, int64_t* launches, 
  *   o[i,j] = sum_k a[k,i] * b[k,j]       (incoming)
  *   out = p_out(LN_out(o)) * sigmoid(g_out(xn))   (+ x when residual != 0)
  * x, out: [B,N,N,D] bf16 (out may equal x when residual != 0); mask [B,N,N].
- * p_in_w, g_in_w: [2D, D]; p_out_w, g_out_w: [D, D].  D must be 128.
+ * p_in_w, g_in_w: [2D, D]; p_out_w, g_out_w: [D, D].  D must be 128; N <= 9472.
  * res_tail: NULL or the [B,N,N,D] int8 tail of the residual stream (residual=1).
  */
 size_t bioemu_trimul_workspace_bytes(int64_t B, int64_t N, int64_t D);

@@ -156,6 +156,44 @@ def test_n3072_matches_unpadded_n2816(gpu_device, mode):
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("mode", ["outgoing", "incoming"])
+def test_n4352_matches_unpadded_n4096(gpu_device, mode):
+    """Past N = 4096 (the reference runs its tiled kernel beyond 5000 tokens, triangle_multiplication.py:355-367):
+    the 128 contraction planes of an N = 4352 problem span 4.8 GB, more than a 32-bit offset reaches from one base.
+    With the last 256 tokens masked, the valid region must equal, bit for bit, the same problem at N = 4096; all
+    outputs finite."""
+    n, pad = 4096, 256
+    m = _module(mode, gpu_device)
+    g = torch.Generator(device=gpu_device).manual_seed(11)
+    x = torch.randn(1, n + pad, n + pad, D, generator=g, device=gpu_device, dtype=torch.bfloat16)
+    tok = torch.ones(1, n + pad, dtype=torch.bool, device=gpu_device)
+    tok[:, n:] = False
+    pmask = tok[:, :, None] & tok[:, None, :]
+    print(f"trimul {mode} N={n + pad}", flush=True)
+    with torch.no_grad():
+        b = m(x, pmask)
+        assert torch.isfinite(b).all()
+        b = b[:, :n, :n].clone()
+        xs = x[:, :n, :n].contiguous()
+        del x, pmask
+        torch.cuda.empty_cache()
+        print(f"trimul {mode} N={n}", flush=True)
+        a = m(xs, torch.ones(1, n, n, dtype=torch.bool, device=gpu_device))
+    assert torch.equal(a, b)
+
+
+def test_rejects_n_past_the_offset_range(gpu_device):
+    """N = 9728 would need offsets past 32 bits in the output stage: the C entry point refuses the shape before it
+    reads any argument buffer or launches anything (the buffers passed here are small on purpose)."""
+    from bioemu2_amd._lib import lib
+
+    buf = torch.zeros(1 << 16, dtype=torch.bfloat16, device=gpu_device)
+    p = buf.data_ptr()
+    rc = lib().bioemu_trimul_fwd(p, p, p, p, p, p, p, p, p, p, p, None, p, buf.numel() * 2, 1, 9728, D, 1, 0,
+                                 torch.cuda.current_stream().cuda_stream)
+    assert rc != 0 and b"N <= 9472" in lib().bioemu_last_error()
+
+
 def test_batch_equals_separate(gpu_device):
     m = _module("incoming", gpu_device)
     x0, m0 = _inputs(48, gpu_device, seed=1)
