@@ -50,14 +50,14 @@ def test_matches_oracle(gpu_device, B, S, N):
     _check(got, want, f"opm B={B} S={S} N={N}")
 
 
-def test_config3_shape_rows_subset(gpu_device):
-    """Config 3 shapes (S=1024, N=512, 20% rows masked), oracle on a 64-row i-slice."""
+def test_config3_shape(gpu_device):
+    """Config 3 shapes (S=1024, N=512, 20% rows masked): every output pair against the oracle."""
     m_ = _module(gpu_device)
     m, mask = _inputs(1, 1024, 512, gpu_device)
     with torch.no_grad():
-        got = m_(m, mask)[:, :64].float().cpu()
-    want = oracle.outer_product_mean(m.cpu(), mask.cpu(), state(m_), i_chunk=64)[:, :64]
-    _check(got, want, "opm config3 (64 rows)")
+        got = m_(m, mask).float().cpu()
+    want = oracle.outer_product_mean(m.cpu(), mask.cpu(), state(m_), i_chunk=64)
+    _check(got, want, "opm config3")
 
 
 def test_2d_mask(gpu_device):
