@@ -104,6 +104,16 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _c_int,
         [_c_void_p] * 12 + [_c_size_t] + [_c_int64] * 3 + [_c_int, _c_int, _c_void_p],
     ),
+    "bioemu_opm_f32_workspace_bytes": (_c_size_t, [_c_int64] * 5),
+    "bioemu_opm_fwd_f32": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_int] + [_c_void_p] * 8 + [_c_size_t] + [_c_int64] * 6 + [_c_void_p],
+    ),
+    "bioemu_pwa_f32_workspace_bytes": (_c_size_t, [_c_int64] * 6),
+    "bioemu_pwa_fwd_f32": (
+        _c_int,
+        [_c_void_p] * 13 + [_c_size_t] + [_c_int64] * 7 + [ctypes.c_float, _c_int, _c_void_p],
+    ),
 }
 
 _lock = threading.Lock()

@@ -1202,6 +1202,160 @@ def _(m, mask, norm_w, norm_b, w_ab, w_o, b_o):
     return m.new_empty(B, N, N, w_o.shape[0])
 
 
+def opm_f32_workspace_bytes(B: int, S: int, N: int, c_in: int, c_h: int) -> int:
+    return int(lib().bioemu_opm_f32_workspace_bytes(B, S, N, c_in, c_h))
+
+
+def launch_opm_f32(
+    m: Tensor,
+    mask3: Tensor,
+    mean_rows: bool,
+    norm_w: Tensor,
+    norm_b: Tensor,
+    w_ab: Tensor,
+    w_o: Tensor,
+    b_o: Tensor,
+    out: Tensor,
+    z_res: Tensor | None = None,
+    ws: Tensor | None = None,
+) -> Tensor:
+    """OuterProductMean in IEEE fp32 (``bioemu_opm_fwd_f32``): every tensor fp32; ``out`` = OPM(m) (+ z_res)."""
+    require_gpu(m, "outer_product_mean_f32")
+    if m.ndim != 4:
+        raise ValueError(f"opm_f32: m must be [B,S,N,C], got {tuple(m.shape)}")
+    B, S, N, c_in = m.shape
+    c_h = w_ab.shape[0] // 2
+    c_out = w_o.shape[0]
+    dev = m.device
+    _check_tensor(m, "opm_f32 m", F32, (B, S, N, c_in), dev)
+    _check_tensor(mask3, "opm_f32 mask", torch.uint8, (B, S, N), dev)
+    for name, t, shp in (
+        ("norm.weight", norm_w, (c_in,)), ("norm.bias", norm_b, (c_in,)), ("proj_ab.weight", w_ab, (2 * c_h, c_in)),
+        ("proj_o.weight", w_o, (c_out, c_h * c_h)), ("proj_o.bias", b_o, (c_out,)),
+    ):
+        _check_tensor(t, f"opm_f32 {name}", F32, shp, dev)
+    _check_tensor(out, "opm_f32 out", F32, (B, N, N, c_out), dev)
+    if z_res is not None:
+        _check_tensor(z_res, "opm_f32 z_res", F32, (B, N, N, c_out), dev)
+    need = opm_f32_workspace_bytes(B, S, N, c_in, c_h)
+    if need == 0:
+        raise ValueError(f"opm_f32: unsupported widths c_in={c_in} c_hidden={c_h} (c_hidden must be 32)")
+    if ws is None or ws.numel() < need:
+        ws = workspace(need, dev)
+    rc = lib().bioemu_opm_fwd_f32(
+        _ptr(m), _ptr(mask3), int(bool(mean_rows)), _ptr(norm_w), _ptr(norm_b), _ptr(w_ab), _ptr(w_o), _ptr(b_o),
+        _ptr(z_res), _ptr(out), _ptr(ws), ctypes.c_size_t(ws.numel()), B, S, N, c_in, c_h, c_out, _stream(m),
+    )
+    check(rc, "bioemu_opm_fwd_f32")
+    return out
+
+
+@torch.library.custom_op("bioemu_mi355x::outer_product_mean_f32", mutates_args=(), device_types="cuda")
+def outer_product_mean_f32(
+    m: Tensor, mask: Tensor, norm_w: Tensor, norm_b: Tensor, w_ab: Tensor, w_o: Tensor, b_o: Tensor
+) -> Tensor:
+    mf = m.to(F32).contiguous()
+    B, S, N, _ = mf.shape
+    mask3, mean_rows = opm_mask3(mask, B, S, N)
+    out = torch.empty(B, N, N, w_o.shape[0], dtype=F32, device=m.device)
+    f32c = lambda t: t.to(F32).contiguous()  # noqa: E731
+    launch_opm_f32(mf, mask3, mean_rows, f32c(norm_w), f32c(norm_b), f32c(w_ab), f32c(w_o), f32c(b_o), out)
+    return out
+
+
+@outer_product_mean_f32.register_fake
+def _(m, mask, norm_w, norm_b, w_ab, w_o, b_o):
+    B, S, N, _ = m.shape
+    return m.new_empty(B, N, N, w_o.shape[0], dtype=F32)
+
+
+def pwa_f32_workspace_bytes(B: int, S: int, N: int, c_m: int, c_h: int, H: int) -> int:
+    return int(lib().bioemu_pwa_f32_workspace_bytes(B, S, N, c_m, c_h, H))
+
+
+def launch_pwa_f32(
+    m: Tensor,
+    z: Tensor,
+    mask_u8: Tensor,
+    norm_m_w: Tensor,
+    norm_m_b: Tensor,
+    w_m: Tensor,
+    w_g: Tensor,
+    norm_z_w: Tensor,
+    norm_z_b: Tensor | None,
+    w_z: Tensor,
+    w_o: Tensor,
+    out: Tensor,
+    num_heads: int,
+    residual: bool = False,
+    inf: float = 1e6,
+    ws: Tensor | None = None,
+) -> Tensor:
+    """PairWeightedAveraging in IEEE fp32 (``bioemu_pwa_fwd_f32``): every tensor fp32; ``out`` = PWA(m, z)
+    (+ m with ``residual``; ``out`` may be ``m`` then)."""
+    require_gpu(m, "pair_weighted_averaging_f32")
+    if m.ndim != 4 or z.ndim != 4:
+        raise ValueError(f"pwa_f32: m must be [B,S,N,c_m] and z [B,N,N,c_z], got {tuple(m.shape)}, {tuple(z.shape)}")
+    B, S, N, c_m = m.shape
+    c_z = z.shape[-1]
+    H = num_heads
+    c_h = w_m.shape[0] // H
+    dev = m.device
+    _check_tensor(m, "pwa_f32 m", F32, (B, S, N, c_m), dev)
+    _check_tensor(z, "pwa_f32 z", F32, (B, N, N, c_z), dev)
+    _check_tensor(mask_u8, "pwa_f32 mask", torch.uint8, (B, N, N), dev)
+    for name, t, shp in (
+        ("norm_m.weight", norm_m_w, (c_m,)), ("norm_m.bias", norm_m_b, (c_m,)), ("proj_m.weight", w_m, (H * c_h, c_m)),
+        ("proj_g.weight", w_g, (H * c_h, c_m)), ("norm_z.weight", norm_z_w, (c_z,)), ("proj_z.weight", w_z, (H, c_z)),
+        ("proj_o.weight", w_o, (c_m, H * c_h)),
+    ):
+        _check_tensor(t, f"pwa_f32 {name}", F32, shp, dev)
+    if norm_z_b is not None:
+        _check_tensor(norm_z_b, "pwa_f32 norm_z.bias", F32, (c_z,), dev)
+    _check_tensor(out, "pwa_f32 out", F32, (B, S, N, c_m), dev)
+    need = pwa_f32_workspace_bytes(B, S, N, c_m, c_h, H)
+    if need == 0:
+        raise ValueError(f"pwa_f32: unsupported widths c_m={c_m} c_h={c_h} heads={H} (c_h must be 32)")
+    if ws is None or ws.numel() < need:
+        ws = workspace(need, dev)
+    rc = lib().bioemu_pwa_fwd_f32(
+        _ptr(m), _ptr(z), _ptr(mask_u8), _ptr(norm_m_w), _ptr(norm_m_b), _ptr(norm_z_w), _ptr(norm_z_b), _ptr(w_m),
+        _ptr(w_g), _ptr(w_z), _ptr(w_o), _ptr(out), _ptr(ws), ctypes.c_size_t(ws.numel()), B, S, N, c_m, c_z, c_h, H,
+        float(inf), int(bool(residual)), _stream(m),
+    )
+    check(rc, "bioemu_pwa_fwd_f32")
+    return out
+
+
+@torch.library.custom_op("bioemu_mi355x::pair_weighted_averaging_f32", mutates_args=(), device_types="cuda")
+def pair_weighted_averaging_f32(
+    m: Tensor,
+    z: Tensor,
+    mask: Tensor,
+    norm_m_w: Tensor,
+    norm_m_b: Tensor,
+    w_m: Tensor,
+    w_g: Tensor,
+    norm_z_w: Tensor,
+    norm_z_b: Tensor | None,
+    w_z: Tensor,
+    w_o: Tensor,
+    num_heads: int,
+    inf: float,
+) -> Tensor:
+    mf = m.to(F32).contiguous()
+    out = torch.empty_like(mf)
+    f32c = lambda t: None if t is None else t.to(F32).contiguous()  # noqa: E731
+    launch_pwa_f32(mf, f32c(z), mask_u8(mask), f32c(norm_m_w), f32c(norm_m_b), f32c(w_m), f32c(w_g), f32c(norm_z_w),
+                   f32c(norm_z_b), f32c(w_z), f32c(w_o), out, num_heads, inf=inf)
+    return out
+
+
+@pair_weighted_averaging_f32.register_fake
+def _(m, z, mask, norm_m_w, norm_m_b, w_m, w_g, norm_z_w, norm_z_b, w_z, w_o, num_heads, inf):
+    return m.new_empty(m.shape, dtype=F32)
+
+
 # ----------------------------------------------------------------------------
 # PairMixer trunk glue: recycling updates and the MSA input embedding
 # ----------------------------------------------------------------------------

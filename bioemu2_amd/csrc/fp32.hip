@@ -955,3 +955,380 @@ extern "C" int bioemu_trimul_fwd_f32(const float* x, const uint8_t* mask, const 
   }
   return check_launch("f32_trimul_out");
 }
+
+// ---------------------------------------------------------------------------
+// OuterProductMean, fp32 arithmetic (outer_product_mean.py:45-75 with autocast
+// off: LayerNorm, proj_ab, the masked contraction over the MSA rows, the mean
+// and proj_o all in fp32).
+//   mn = LN(m);  [a | b] = mn W_ab^T, zeroed where mask[b,s,n] == 0
+//   aT[b][(n, c)][s], bT[b][(n, d)][s]   (s contiguous, zero for s >= S)
+//   Y[(b, i, j)][c * C_H + d] = sum_s aT[b][(i, c)][s] bT[b][(j, d)][s] * inv[b]
+//   out = Y W_o^T + b_o (+ z)
+// A 32 x 32 block of the contraction (rows (i, c), columns (j, d)) is exactly
+// one pair's C_H x C_H outer-product matrix (C_H = 32), which the epilogue
+// stores as that pair's row of Y.  inv[b] = 1 / max(valid rows, 1) with a
+// [B,S,N] mask, 1 for the broadcast [B,N] one (mean_rows = 0).
+// ---------------------------------------------------------------------------
+namespace bioemu {
+namespace {
+
+constexpr int kOpmCH = 32;
+
+// The proj_ab block of 32 rows m = (b, s, n) x 32 output channels (cb = 0: a, 1: b),
+// masked and stored transposed into aT / bT.
+__global__ __launch_bounds__(256) void opm_proj_f32_kernel(const float* __restrict__ mn, const float* __restrict__ wab,
+                                                           const uint8_t* __restrict__ mask, float* __restrict__ aT,
+                                                           float* __restrict__ bT, int S, int N, int Sp, int cin,
+                                                           long long M) {
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int n = lane & 31, h = lane >> 5;
+  const long long blk = (long long)blockIdx.x * 4 + wave;
+  if (blk >= (M + 31) / 32 * 2) return;   // no barriers in this kernel
+  const long long m = blk / 2 * 32 + n;
+  const int cb = (int)(blk % 2);
+  const bool mvalid = m < M;
+  f32x16 acc = zero16(), unused = zero16();
+  f32_block<false>(mn + (size_t)(mvalid ? m : 0) * cin + 4 * h, wab + (size_t)(cb * 32 + perm32(n)) * cin + 4 * h,
+                   nullptr, cin, acc, unused);
+  if (!mvalid) return;
+  const float keep = mask[m] ? 1.f : 0.f;
+  const long long b = m / ((long long)S * N), r = m % ((long long)S * N);
+  const int s = (int)(r / N), tok = (int)(r % N);
+  float* dst = (cb ? bT : aT) + (((size_t)b * N + tok) * kOpmCH + 16 * h) * Sp + s;
+#pragma unroll
+  for (int u = 0; u < 16; ++u) dst[(size_t)u * Sp] = acc[u] * keep;
+}
+
+// inv[b] = 1 / max(#rows s with any mask[b, s, :], 1), or 1 when !mean_rows.  One workgroup per batch.
+__global__ __launch_bounds__(256) void opm_inv_f32_kernel(const uint8_t* __restrict__ mask, float* __restrict__ inv,
+                                                          int S, int N, int mean_rows) {
+  __shared__ int cnt;
+  if (threadIdx.x == 0) cnt = 0;
+  __syncthreads();
+  const uint8_t* mb = mask + (size_t)blockIdx.x * S * N;
+  int local = 0;
+  for (int s = threadIdx.x; s < S; s += blockDim.x) {
+    bool any = false;
+    for (int t = 0; t < N && !any; ++t) any = mb[(size_t)s * N + t] != 0;
+    local += any;
+  }
+  atomicAdd(&cnt, local);
+  __syncthreads();
+  if (threadIdx.x == 0) inv[blockIdx.x] = mean_rows ? 1.0f / (float)max(cnt, 1) : 1.0f;
+}
+
+// One wave per pair (i, j) of batch blockIdx.y: Y row = the 32 x 32 block (i, j) of aT bT^T, times inv[b].
+__global__ __launch_bounds__(256) void opm_contract_f32_kernel(const float* __restrict__ aT, const float* __restrict__ bT,
+                                                               const float* __restrict__ inv, float* __restrict__ Y,
+                                                               int N, int Sp) {
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int n = lane & 31, h = lane >> 5;
+  const long long pair = (long long)blockIdx.x * 4 + wave;
+  if (pair >= (long long)N * N) return;   // no barriers in this kernel
+  const int i = (int)(pair / N), j = (int)(pair % N), b = blockIdx.y;
+  const float* A = aT + (((size_t)b * N + i) * kOpmCH + n) * Sp + 4 * h;
+  const float* Bm = bT + (((size_t)b * N + j) * kOpmCH + perm32(n)) * Sp + 4 * h;
+  f32x16 acc = zero16(), unused = zero16();
+  f32_block<false>(A, Bm, nullptr, Sp, acc, unused);
+  // lane (n, h): row c = n, register u <-> column d = 16 h + u
+  const float scale = inv[b];
+  float* dst = Y + (((size_t)b * N + i) * N + j) * (kOpmCH * kOpmCH) + n * kOpmCH + 16 * h;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    f32x4 o4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o4[e] = acc[4 * q + e] * scale;
+    *reinterpret_cast<f32x4*>(dst + 4 * q) = o4;
+  }
+}
+
+struct OpmF32Layout {
+  size_t mn, aT, bT, inv, Y, total;
+};
+
+OpmF32Layout opm_f32_layout(int64_t B, int64_t S, int64_t N, int64_t c_in) {
+  OpmF32Layout L;
+  const size_t Sp = (size_t)round_up(S, 8);
+  size_t off = 0;
+  L.mn = off;
+  off += round_up((size_t)B * S * N * c_in * 4, 256);
+  L.aT = off;
+  off += round_up((size_t)B * N * kOpmCH * Sp * 4, 256);
+  L.bT = off;
+  off += round_up((size_t)B * N * kOpmCH * Sp * 4, 256);
+  L.inv = off;
+  off += round_up((size_t)B * 4, 256);
+  L.Y = off;
+  off += round_up((size_t)B * N * N * kOpmCH * kOpmCH * 4, 256);
+  L.total = off;
+  return L;
+}
+
+}  // namespace
+}  // namespace bioemu
+
+using namespace bioemu;
+
+extern "C" size_t bioemu_opm_f32_workspace_bytes(int64_t B, int64_t S, int64_t N, int64_t c_in, int64_t c_hidden) {
+  if (B <= 0 || S <= 0 || N <= 0 || c_in <= 0 || c_hidden != kOpmCH) return 0;
+  return opm_f32_layout(B, S, N, c_in).total;
+}
+
+extern "C" int bioemu_opm_fwd_f32(const float* m, const uint8_t* mask, int mean_rows, const float* norm_w,
+                                  const float* norm_b, const float* w_ab, const float* w_o, const float* b_o,
+                                  const float* z_res, float* out, void* workspace, size_t workspace_bytes, int64_t B,
+                                  int64_t S, int64_t N, int64_t c_in, int64_t c_hidden, int64_t c_out,
+                                  hipStream_t stream) {
+  if (c_hidden != kOpmCH || c_in <= 0 || c_in % 8 || c_out <= 0 || c_out % 32)
+    return set_error(BIOEMU_ERR_UNSUPPORTED,
+                     "opm_f32: c_hidden must be 32, c_in a multiple of 8 and c_out of 32 (got %lld/%lld/%lld)",
+                     (long long)c_in, (long long)c_hidden, (long long)c_out);
+  if (B <= 0 || S <= 0 || N <= 0 || B > 65535 || N > 16384 || S > (1 << 24))
+    return set_error(BIOEMU_ERR_INVALID_ARG, "opm_f32: bad shape B=%lld S=%lld N=%lld", (long long)B, (long long)S,
+                     (long long)N);
+  if (!m || !mask || !norm_w || !norm_b || !w_ab || !w_o || !out || !workspace)
+    return set_error(BIOEMU_ERR_INVALID_ARG, "opm_f32: null pointer argument");
+  if (!aligned16(m) || !aligned16(w_ab) || !aligned16(w_o) || !aligned16(out) || !aligned16(workspace) ||
+      (z_res && !aligned16(z_res)))
+    return set_error(BIOEMU_ERR_INVALID_ARG, "opm_f32: tensors must be 16-byte aligned");
+  const OpmF32Layout L = opm_f32_layout(B, S, N, c_in);
+  if (workspace_bytes < L.total) return set_error(BIOEMU_ERR_WORKSPACE, "opm_f32: workspace too small");
+  char* p = static_cast<char*>(workspace);
+  float* mn = reinterpret_cast<float*>(p + L.mn);
+  float* aT = reinterpret_cast<float*>(p + L.aT);
+  float* bT = reinterpret_cast<float*>(p + L.bT);
+  float* inv = reinterpret_cast<float*>(p + L.inv);
+  float* Y = reinterpret_cast<float*>(p + L.Y);
+  const long long M = B * S * N;
+  const int Sp = (int)round_up(S, 8);
+
+  int rc = rows_ln_f32(m, norm_w, norm_b, mn, M, (int)c_in, stream, "f32_opm_layernorm");
+  if (rc) return rc;
+  {
+    // aT and bT are adjacent: one fill zeroes both (the rows s in [S, Sp) stay zero)
+    const long long count = (long long)((L.bT - L.aT) / 4) * 2;
+    KernelTimerScope timed("f32_fill", stream);
+    hipLaunchKernelGGL(fill_zero_f32_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, stream, aT, count);
+  }
+  if ((rc = check_launch("f32_fill"))) return rc;
+  {
+    const long long blocks = (M + 31) / 32 * 2;
+    KernelTimerScope timed("f32_opm_proj", stream);
+    hipLaunchKernelGGL(opm_proj_f32_kernel, dim3((unsigned)((blocks + 3) / 4)), dim3(256), 0, stream, mn, w_ab, mask,
+                       aT, bT, (int)S, (int)N, Sp, (int)c_in, M);
+  }
+  if ((rc = check_launch("f32_opm_proj"))) return rc;
+  {
+    KernelTimerScope timed("f32_opm_count", stream);
+    hipLaunchKernelGGL(opm_inv_f32_kernel, dim3((unsigned)B), dim3(256), 0, stream, mask, inv, (int)S, (int)N,
+                       mean_rows);
+  }
+  if ((rc = check_launch("f32_opm_count"))) return rc;
+  {
+    const long long pairs = N * N;
+    KernelTimerScope timed("f32_opm_contract", stream);
+    hipLaunchKernelGGL(opm_contract_f32_kernel, dim3((unsigned)((pairs + 3) / 4), (unsigned)B), dim3(256), 0, stream,
+                       aT, bT, inv, Y, (int)N, Sp);
+  }
+  if ((rc = check_launch("f32_opm_contract"))) return rc;
+  return gemm_f32(z_res ? kGemmEpiResidual : kGemmEpiStore, Y, w_o, nullptr, b_o, z_res, out, B * N * N,
+                  kOpmCH * kOpmCH, (int)c_out, stream, "f32_opm_out");
+}
+
+// ---------------------------------------------------------------------------
+// Pair-weighted averaging, fp32 arithmetic (pair_weighted_averaging.py:125-154
+// with autocast off).
+//   mn = LN_m(m);  vT[b][h][(s, d)][j] = (mn W_m^T)[b, s, j, h*32 + d]   (j contiguous)
+//   g = sigmoid(mn W_g^T);  logits[b][h][i][j] = LN_z(z[b, i, j]) W_z^T [h]
+//   w = softmax_j(logits, masked keys -> -1e6)
+//   go[b, s, i, h*32 + d] = g * sum_j w[b][h][i][j] vT[b][h][(s, d)][j]
+//   out = go W_o^T (+ m)
+// Keys are padded to Np8 = N rounded up to 8 with zero weights and zero v.
+// ---------------------------------------------------------------------------
+namespace bioemu {
+namespace {
+
+constexpr int kPwaCH = 32;
+
+// v block of 32 rows m = (b, s, j) x 32 channels (head hd = cb), stored transposed into vT.
+__global__ __launch_bounds__(256) void pwa_v_f32_kernel(const float* __restrict__ mn, const float* __restrict__ wm,
+                                                        float* __restrict__ vT, int S, int N, int Np8, int cm, int H,
+                                                        long long M) {
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int n = lane & 31, h = lane >> 5;
+  const long long blk = (long long)blockIdx.x * 4 + wave;
+  if (blk >= (M + 31) / 32 * H) return;   // no barriers in this kernel
+  const long long m = blk / H * 32 + n;
+  const int hd = (int)(blk % H);
+  const bool mvalid = m < M;
+  f32x16 acc = zero16(), unused = zero16();
+  f32_block<false>(mn + (size_t)(mvalid ? m : 0) * cm + 4 * h, wm + (size_t)(hd * 32 + perm32(n)) * cm + 4 * h,
+                   nullptr, cm, acc, unused);
+  if (!mvalid) return;
+  const long long b = m / ((long long)S * N), r = m % ((long long)S * N);
+  const int s = (int)(r / N), j = (int)(r % N);
+  float* dst = vT + ((((size_t)b * H + hd) * S + s) * kPwaCH + 16 * h) * Np8 + j;
+#pragma unroll
+  for (int u = 0; u < 16; ++u) dst[(size_t)u * Np8] = acc[u];
+}
+
+// In place over logits rows [b][h][i][0, Np8): masked keys -> -inf_value, softmax over the N keys, 0 past N.
+// One wave per row.
+__global__ __launch_bounds__(256) void pwa_softmax_f32_kernel(float* __restrict__ lg, const uint8_t* __restrict__ mask,
+                                                              int N, int Np8, int H, long long rows, float neg) {
+  const int lane = threadIdx.x & 63;
+  const long long row = (long long)blockIdx.x * 4 + wave_id();
+  if (row >= rows) return;
+  const long long bh = row / N;
+  const int i = (int)(row % N);
+  const long long b = bh / H;
+  float* x = lg + (size_t)row * Np8;
+  const uint8_t* mk = mask + ((size_t)b * N + i) * N;
+  float mx = -INFINITY;
+  for (int j = lane; j < N; j += 64) {
+    const float v = mk[j] ? x[j] : neg;
+    x[j] = v;
+    mx = fmaxf(mx, v);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+  float sum = 0.f;
+  for (int j = lane; j < N; j += 64) {
+    const float e = expf(x[j] - mx);
+    x[j] = e;
+    sum += e;
+  }
+  sum = wave_sum(sum);
+  const float r = 1.0f / sum;
+  for (int j = lane; j < Np8; j += 64) x[j] = j < N ? x[j] * r : 0.f;
+}
+
+// One wave per 32 x 32 block (query rows i, columns (s, d) = one MSA row s) of head hd = blockIdx.y % H:
+// go[b, s, i, hd*32 + d] = g[same] * sum_j w[b][hd][i][j] vT[b][hd][(s, d)][j].
+__global__ __launch_bounds__(256) void pwa_avg_f32_kernel(const float* __restrict__ w, const float* __restrict__ vT,
+                                                          const float* __restrict__ g, float* __restrict__ go, int S,
+                                                          int N, int Np8, int H) {
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int n = lane & 31, h = lane >> 5;
+  const int nib = (N + 31) / 32;
+  const long long blk = (long long)blockIdx.x * 4 + wave;
+  if (blk >= (long long)nib * S) return;   // no barriers in this kernel
+  const int ib = (int)(blk % nib), s = (int)(blk / nib);
+  const int bh = blockIdx.y, b = bh / H, hd = bh % H;
+  const int i = ib * 32 + n;
+  const bool ivalid = i < N;
+  const float* A = w + ((size_t)bh * N + (ivalid ? i : 0)) * Np8 + 4 * h;
+  const float* Bm = vT + (((size_t)bh * S + s) * kPwaCH + perm32(n)) * Np8 + 4 * h;
+  f32x16 acc = zero16(), unused = zero16();
+  f32_block<false>(A, Bm, nullptr, Np8, acc, unused);
+  if (!ivalid) return;
+  // lane (n, h): query i, register u <-> d = 16 h + u
+  const size_t off = (((size_t)b * S + s) * N + i) * (size_t)(H * kPwaCH) + hd * kPwaCH + 16 * h;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const f32x4 g4 = *reinterpret_cast<const f32x4*>(g + off + 4 * q);
+    f32x4 o4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o4[e] = acc[4 * q + e] * g4[e];
+    *reinterpret_cast<f32x4*>(go + off + 4 * q) = o4;
+  }
+}
+
+struct PwaF32Layout {
+  size_t mn, vT, g, go, lg, total;
+};
+
+PwaF32Layout pwa_f32_layout(int64_t B, int64_t S, int64_t N, int64_t c_m, int64_t H) {
+  PwaF32Layout L;
+  const size_t Np8 = (size_t)round_up(N, 8), rows = (size_t)B * S * N, hc = (size_t)H * kPwaCH;
+  size_t off = 0;
+  L.mn = off;
+  off += round_up(rows * c_m * 4, 256);
+  L.vT = off;
+  off += round_up((size_t)B * H * S * kPwaCH * Np8 * 4, 256);
+  L.g = off;
+  off += round_up(rows * hc * 4, 256);
+  L.go = off;
+  off += round_up(rows * hc * 4, 256);
+  L.lg = off;
+  off += round_up((size_t)B * H * N * Np8 * 4, 256);
+  L.total = off;
+  return L;
+}
+
+}  // namespace
+}  // namespace bioemu
+
+extern "C" size_t bioemu_pwa_f32_workspace_bytes(int64_t B, int64_t S, int64_t N, int64_t c_m, int64_t c_h, int64_t H) {
+  if (B <= 0 || S <= 0 || N <= 0 || c_m <= 0 || c_h != kPwaCH || H <= 0) return 0;
+  return pwa_f32_layout(B, S, N, c_m, H).total;
+}
+
+extern "C" int bioemu_pwa_fwd_f32(const float* m, const float* z, const uint8_t* mask, const float* norm_m_w,
+                                  const float* norm_m_b, const float* norm_z_w, const float* norm_z_b,
+                                  const float* w_m, const float* w_g, const float* w_z, const float* w_o, float* out,
+                                  void* workspace, size_t workspace_bytes, int64_t B, int64_t S, int64_t N,
+                                  int64_t c_m, int64_t c_z, int64_t c_h, int64_t H, float inf, int residual,
+                                  hipStream_t stream) {
+  if (c_h != kPwaCH || c_m <= 0 || c_m % 32 || H <= 0 || H > 64 || (c_z != 128 && c_z != 32 && c_z != 16))
+    return set_error(BIOEMU_ERR_UNSUPPORTED,
+                     "pwa_f32: c_h must be 32, c_m a multiple of 32, c_z 16, 32 or 128 (got c_m=%lld c_z=%lld c_h=%lld "
+                     "H=%lld)", (long long)c_m, (long long)c_z, (long long)c_h, (long long)H);
+  if (B <= 0 || S <= 0 || N <= 0 || B * H > 65535 || N > 16384)
+    return set_error(BIOEMU_ERR_INVALID_ARG, "pwa_f32: bad shape B=%lld S=%lld N=%lld", (long long)B, (long long)S,
+                     (long long)N);
+  if (!m || !z || !mask || !norm_m_w || !norm_z_w || !w_m || !w_g || !w_z || !w_o || !out || !workspace)
+    return set_error(BIOEMU_ERR_INVALID_ARG, "pwa_f32: null pointer argument");
+  if (!aligned16(m) || !aligned16(z) || !aligned16(w_m) || !aligned16(w_g) || !aligned16(w_o) || !aligned16(out) ||
+      !aligned16(workspace))
+    return set_error(BIOEMU_ERR_INVALID_ARG, "pwa_f32: tensors must be 16-byte aligned");
+  if (out == m && !residual)
+    return set_error(BIOEMU_ERR_INVALID_ARG, "pwa_f32: out may alias m only with residual=1");
+  const PwaF32Layout L = pwa_f32_layout(B, S, N, c_m, H);
+  if (workspace_bytes < L.total) return set_error(BIOEMU_ERR_WORKSPACE, "pwa_f32: workspace too small");
+  char* p = static_cast<char*>(workspace);
+  float* mn = reinterpret_cast<float*>(p + L.mn);
+  float* vT = reinterpret_cast<float*>(p + L.vT);
+  float* g = reinterpret_cast<float*>(p + L.g);
+  float* go = reinterpret_cast<float*>(p + L.go);
+  float* lg = reinterpret_cast<float*>(p + L.lg);
+  const long long M = B * S * N;
+  const int Np8 = (int)round_up(N, 8), hc = (int)(H * kPwaCH);
+
+  int rc = rows_ln_f32(m, norm_m_w, norm_m_b, mn, M, (int)c_m, stream, "f32_pwa_layernorm");
+  if (rc) return rc;
+  {
+    const long long count = (long long)((L.g - L.vT) / 4);   // vT, zero past N in j
+    KernelTimerScope timed("f32_fill", stream);
+    hipLaunchKernelGGL(fill_zero_f32_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, stream, vT, count);
+  }
+  if ((rc = check_launch("f32_fill"))) return rc;
+  {
+    const long long blocks = (M + 31) / 32 * H;
+    KernelTimerScope timed("f32_pwa_v", stream);
+    hipLaunchKernelGGL(pwa_v_f32_kernel, dim3((unsigned)((blocks + 3) / 4)), dim3(256), 0, stream, mn, w_m, vT,
+                       (int)S, (int)N, Np8, (int)c_m, (int)H, M);
+  }
+  if ((rc = check_launch("f32_pwa_v"))) return rc;
+  rc = gemm_f32(kGemmEpiSigmoid, mn, w_g, nullptr, nullptr, nullptr, g, M, (int)c_m, hc, stream, "f32_pwa_gate");
+  if (rc) return rc;
+  rc = pair_proj_f32(z, norm_z_w, norm_z_b, w_z, lg, B * N * N, (int)N, (int)N, Np8, (int)H, (int)c_z, stream,
+                     "f32_pwa_logits");
+  if (rc) return rc;
+  {
+    const long long rows = B * H * N;
+    KernelTimerScope timed("f32_pwa_softmax", stream);
+    hipLaunchKernelGGL(pwa_softmax_f32_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, stream, lg, mask,
+                       (int)N, Np8, (int)H, rows, -inf);
+  }
+  if ((rc = check_launch("f32_pwa_softmax"))) return rc;
+  {
+    const long long blocks = (N + 31) / 32 * S;
+    KernelTimerScope timed("f32_pwa_average", stream);
+    hipLaunchKernelGGL(pwa_avg_f32_kernel, dim3((unsigned)((blocks + 3) / 4), (unsigned)(B * H)), dim3(256), 0, stream,
+                       lg, vT, g, go, (int)S, (int)N, Np8, (int)H);
+  }
+  if ((rc = check_launch("f32_pwa_average"))) return rc;
+  return gemm_f32(residual ? kGemmEpiResidual : kGemmEpiStore, go, w_o, nullptr, nullptr, m, out, M, hc, (int)c_m,
+                  stream, "f32_pwa_out");
+}

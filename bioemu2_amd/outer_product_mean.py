@@ -10,6 +10,11 @@ reference's ``OPMVariant`` values so ``make(REGISTRY, "vanilla" |
 "triton_memory_saving", ...)`` resolves to the HIP class.  ``tile_size``
 bounded the reference's memory (:23, :107-127); the fused kernel never
 materialises the [N,N,C_H^2] intermediate, so it is accepted and unused.
+fp32 inputs with autocast off (a ``--precision 32-true`` run) take the IEEE
+fp32 entry point ``bioemu_opm_fwd_f32`` (LayerNorm, projections, contraction,
+mean and proj_o all fp32; c_hidden = 32); fp32 inputs under bf16 autocast take
+the bf16 path, whose contraction accumulates in fp32 as the reference's
+forced-fp32 einsum does (:64-74).
 """
 
 from __future__ import annotations
@@ -52,13 +57,21 @@ class OuterProductMeanHip(nn.Module):
             [("norm.weight", f32), ("norm.bias", f32), ("proj_ab.weight", bf), ("proj_o.weight", bf),
              ("proj_o.bias", f32)]
         )
+        self._prepared32 = PreparedParams(
+            [(name, f32) for name in ("norm.weight", "norm.bias", "proj_ab.weight", "proj_o.weight", "proj_o.bias")]
+        )
 
     def prepared_params(self) -> tuple[Tensor, ...]:
         return self._prepared.get(self)
 
+    def prepared_params_f32(self) -> tuple[Tensor, ...]:
+        """The same parameters, all fp32, for the fp32 arithmetic path."""
+        return self._prepared32.get(self)
+
     def forward(self, m: Tensor, mask: Tensor) -> Tensor:
         _ops.require_gpu(m, type(self).__name__)
-        _ops.require_mixed_precision(m, type(self).__name__)
+        if _ops.fp32_mode(m):
+            return torch.ops.bioemu_mi355x.outer_product_mean_f32(m, mask, *self.prepared_params_f32())
         return torch.ops.bioemu_mi355x.outer_product_mean(m, mask, *self.prepared_params())
 
 

@@ -10,8 +10,11 @@ use_bias_in_layer_norm=True)`` constructor (:9-57), its parameters and
 memory (both of its paths compute the same values); the HIP path never
 materialises the per-head [B,H,S,N,c_h] tensors, so it is accepted and unused.
 
-The HIP kernels support the reference trunk's widths (PairMixerMSALayer,
+The bf16 kernels support the reference trunk's widths (PairMixerMSALayer,
 biomoa/modules/pairmixer.py:673-678): c_m = 64, c_z = 128, c_h = 32, 8 heads.
+fp32 inputs with autocast off (a ``--precision 32-true`` run) take the IEEE
+fp32 entry point ``bioemu_pwa_fwd_f32`` (c_h = 32; c_m a multiple of 32; any
+head count and ``inf``); fp32 inputs under bf16 autocast take the bf16 path.
 """
 
 from __future__ import annotations
@@ -54,17 +57,24 @@ class PairWeightedAveraging(nn.Module):
             spec.append(("norm_z.bias", f32))
         spec += [("proj_z.weight", bf), ("proj_o.weight", bf)]
         self._prepared = PreparedParams(spec)
+        self._prepared32 = PreparedParams([(name, f32) for name, _ in spec])
+
+    def _arrange(self, p: tuple[Tensor, ...]) -> tuple[Tensor | None, ...]:
+        return p if self.use_bias_in_layer_norm else p[:5] + (None,) + p[5:]
 
     def prepared_params(self) -> tuple[Tensor | None, ...]:
         """(norm_m.w, norm_m.b, w_m, w_g, norm_z.w, norm_z.b or None, w_z, w_o) on the device."""
-        p = self._prepared.get(self)
-        if self.use_bias_in_layer_norm:
-            return p
-        return p[:5] + (None,) + p[5:]
+        return self._arrange(self._prepared.get(self))
+
+    def prepared_params_f32(self) -> tuple[Tensor | None, ...]:
+        """The same parameters, all fp32, for the fp32 arithmetic path."""
+        return self._arrange(self._prepared32.get(self))
 
     def forward(self, m: Tensor, z: Tensor, mask: Tensor, chunk_heads: bool = False) -> Tensor:
         _ops.require_gpu(m, type(self).__name__)
-        _ops.require_mixed_precision(m, type(self).__name__)
+        if _ops.fp32_mode(m):
+            return torch.ops.bioemu_mi355x.pair_weighted_averaging_f32(
+                m, z, mask, *self.prepared_params_f32(), self.num_heads, float(self.inf))
         if self.inf != 1e6:
             raise ValueError(f"PairWeightedAveraging: only inf=1e6 is supported (got {self.inf})")
         return torch.ops.bioemu_mi355x.pair_weighted_averaging(m, z, mask, *self.prepared_params(), self.num_heads)

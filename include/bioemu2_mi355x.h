@@ -365,6 +365,16 @@ int bioemu_msa_embed_fwd(const float* msa, const float* has_deletion, const floa
  *                            its default matmul_precision="ieee", :104-125): the arguments of
  *                            bioemu_trimul_fwd without res_tail; dim a multiple of 32,
  *                            B * dim <= 65535.
+ *   bioemu_opm_fwd_f32       OuterProductMeanVanilla.forward (outer_product_mean.py:45-75) in
+ *                            IEEE fp32 for a trunk run with autocast off: the arguments of
+ *                            bioemu_opm_fwd as fp32 without res_tail (out = OPM(m) + z_res when
+ *                            z_res is given); c_hidden = 32, c_in a multiple of 8, c_out of 32.
+ *                            Its workspace holds the [B, N, N, 32 * 32] outer-product means.
+ *   bioemu_pwa_fwd_f32       PairWeightedAveraging.forward (pair_weighted_averaging.py:59-154)
+ *                            in IEEE fp32: the arguments of bioemu_pwa_fwd as fp32 without
+ *                            res_tail, plus the masking constant inf (the module's inf; masked
+ *                            logits become -inf); c_h = 32, c_m a multiple of 32, c_z 16, 32 or
+ *                            128, B * H <= 65535.
  * Residual tails do not apply (the stream is fp32).
  */
 size_t bioemu_apb_f32_workspace_bytes(int64_t B, int64_t mult, int64_t N, int64_t c_s, int64_t H);
@@ -395,6 +405,17 @@ int bioemu_trimul_fwd_f32(const float* x, const uint8_t* mask, const float* norm
                           const float* p_out_w, const float* g_out_w, float* out, void* workspace,
                           size_t workspace_bytes, int64_t B, int64_t N, int64_t Dc, int outgoing, int residual,
                           hipStream_t stream);
+size_t bioemu_opm_f32_workspace_bytes(int64_t B, int64_t S, int64_t N, int64_t c_in, int64_t c_hidden);
+int bioemu_opm_fwd_f32(const float* m, const uint8_t* mask, int mean_rows, const float* norm_w, const float* norm_b,
+                       const float* w_ab, const float* w_o, const float* b_o, const float* z_res, float* out,
+                       void* workspace, size_t workspace_bytes, int64_t B, int64_t S, int64_t N, int64_t c_in,
+                       int64_t c_hidden, int64_t c_out, hipStream_t stream);
+size_t bioemu_pwa_f32_workspace_bytes(int64_t B, int64_t S, int64_t N, int64_t c_m, int64_t c_h, int64_t H);
+int bioemu_pwa_fwd_f32(const float* m, const float* z, const uint8_t* mask, const float* norm_m_w,
+                       const float* norm_m_b, const float* norm_z_w, const float* norm_z_b, const float* w_m,
+                       const float* w_g, const float* w_z, const float* w_o, float* out, void* workspace,
+                       size_t workspace_bytes, int64_t B, int64_t S, int64_t N, int64_t c_m, int64_t c_z,
+                       int64_t c_h, int64_t H, float inf, int residual, hipStream_t stream);
 
 #ifdef __cplusplus
 }

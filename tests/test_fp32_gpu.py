@@ -341,3 +341,123 @@ def test_pairmixer_layer_and_module_f32_match_oracle(gpu_device):
     _, got = mod(s.to(d), z.to(d), pm.to(d))
     _, want = oracle.pairmixer_module(s, z, pm, state(mod), 2)
     _check(got.cpu(), want, "pairmixer_module_f32 (2 layers)")
+
+
+# ----------------------------------------------------------------------------
+# OuterProductMean / PairWeightedAveraging (the MSA module's ops)
+# ----------------------------------------------------------------------------
+def _opm(device, c_in=64, c_out=128, seed=4):
+    from bioemu2_amd.outer_product_mean import OuterProductMeanHip
+
+    torch.manual_seed(seed)
+    return randomize_params(OuterProductMeanHip(c_in, 32, c_out), seed).to(device).eval()
+
+
+def _msa_inputs(B, S, N, c, seed=0, p_row_masked=0.25):
+    g = torch.Generator().manual_seed(seed)
+    m = torch.randn(B, S, N, c, generator=g)
+    rows = torch.rand(B, S, generator=g) >= p_row_masked
+    mask = rows[:, :, None].expand(B, S, N).clone()
+    return m, mask
+
+
+@pytest.mark.parametrize("B,S,N,c_in", [(1, 40, 16, 64), (2, 37, 23, 64), (1, 129, 64, 32)])
+def test_opm_f32_matches_oracle(gpu_device, B, S, N, c_in):
+    """OuterProductMean with autocast off: LayerNorm, projections, the masked contraction over the MSA rows, the
+    mean over valid rows and proj_o in fp32 (outer_product_mean.py:45-75), with ragged entries inside valid rows
+    (test_outer_product_mean.py:102-114) and an all-masked batch row."""
+    mod = _opm(gpu_device, c_in)
+    m, mask = _msa_inputs(B, S, N, c_in)
+    mask[:, 1, -3:] = False
+    mask[:, 2] = False
+    print(f"opm_f32 B={B} S={S} N={N} c_in={c_in}", flush=True)
+    with torch.no_grad():
+        got = mod(m.to(gpu_device), mask.to(gpu_device)).cpu()
+    _check(got, oracle.outer_product_mean(m, mask, state(mod)), f"opm_f32 B={B} S={S} N={N}")
+
+
+def test_opm_f32_2d_mask_no_valid_rows_and_residual(gpu_device):
+    """A [B,N] mask divides by 1 (outer_product_mean.py:69-70); a batch with no valid row divides by 1 and gives
+    proj_o's bias; the fused residual z + OPM(m) equals the sum of the two, bit for bit."""
+    mod = _opm(gpu_device)
+    d = gpu_device
+    m, _ = _msa_inputs(1, 6, 20, 64, seed=1)
+    tok = torch.ones(1, 20, dtype=torch.bool)
+    tok[:, 15:] = False
+    with torch.no_grad():
+        got = mod(m.to(d), tok.to(d)).cpu()
+        _check(got, oracle.outer_product_mean(m, tok, state(mod)), "opm_f32 2d mask")
+        none = torch.zeros(1, 6, 20, dtype=torch.bool)
+        got0 = mod(m.to(d), none.to(d)).cpu()
+        assert torch.equal(got0, mod.proj_o.bias.detach().cpu().expand_as(got0))
+        z = torch.randn(1, 20, 20, 128, generator=torch.Generator().manual_seed(2)).to(d)
+        mask3, mean_rows = _ops.opm_mask3(tok.to(d), 1, 6, 20)
+        out = torch.empty_like(z)
+        _ops.launch_opm_f32(m.to(d), mask3, mean_rows, *mod.prepared_params_f32(), out, z_res=z)
+        assert torch.equal(out, z + got.to(d))
+
+
+def _pwa(device, bias=True, seed=3, inf=1e6):
+    from bioemu2_amd.pair_weighted_averaging import PairWeightedAveraging
+
+    torch.manual_seed(seed)
+    return randomize_params(PairWeightedAveraging(64, 128, 32, 8, inf=inf, use_bias_in_layer_norm=bias),
+                            seed).to(device).eval()
+
+
+@pytest.mark.parametrize("bias", [True, False])
+@pytest.mark.parametrize("B,S,N,n_pad", [(1, 5, 16, 0), (2, 3, 37, 6), (1, 9, 70, 11)])
+def test_pwa_f32_matches_oracle(gpu_device, bias, B, S, N, n_pad):
+    """PairWeightedAveraging with autocast off (pair_weighted_averaging.py:125-154 in fp32): masked keys replaced
+    by -inf, softmax over keys, the per-head average and the gated output projection, against the oracle."""
+    mod = _pwa(gpu_device, bias)
+    g = torch.Generator().manual_seed(7)
+    m = torch.randn(B, S, N, 64, generator=g)
+    z = torch.randn(B, N, N, 128, generator=g)
+    tok = torch.ones(B, N, dtype=torch.bool)
+    if n_pad:
+        tok[:, N - n_pad:] = False
+    mask = tok[:, :, None] & tok[:, None, :]
+    print(f"pwa_f32 bias={bias} B={B} S={S} N={N}", flush=True)
+    with torch.no_grad():
+        got = mod(m.to(gpu_device), z.to(gpu_device), mask.to(gpu_device)).cpu()
+    want = oracle.pair_weighted_averaging(m, z, mask, state(mod), num_heads=8, c_h=32)
+    _check(got, want, f"pwa_f32 bias={bias} B={B} S={S} N={N}")
+
+
+def test_pwa_f32_masked_rows_inf_and_residual(gpu_device):
+    """A query row with every key masked averages uniformly (all logits -inf); another inf than the default is
+    honoured; the fused residual equals m + PWA(m, z) bit for bit."""
+    d = gpu_device
+    g = torch.Generator().manual_seed(8)
+    B, S, N = 1, 4, 24
+    m = torch.randn(B, S, N, 64, generator=g)
+    z = torch.randn(B, N, N, 128, generator=g)
+    mask = torch.rand(B, N, N, generator=g) < 0.7
+    mask[:, 5] = False
+    for inf in (1e6, 1e4):
+        mod = _pwa(d, inf=inf)
+        with torch.no_grad():
+            got = mod(m.to(d), z.to(d), mask.to(d))
+        want = oracle.pair_weighted_averaging(m, z, mask, state(mod), num_heads=8, c_h=32, inf=inf)
+        _check(got.cpu(), want, f"pwa_f32 masked row inf={inf}")
+    mr = m.to(d).contiguous()
+    _ops.launch_pwa_f32(mr, z.to(d), _ops.mask_u8(mask.to(d)), *mod.prepared_params_f32(), mr, 8, residual=True,
+                        inf=1e4)
+    assert torch.equal(mr, m.to(d) + got)
+
+
+def test_opm_pwa_autocast_take_bf16_path(gpu_device):
+    """fp32 inputs under bf16 autocast take the bf16 kernels (the reference trunk's policy)."""
+    d = gpu_device
+    opm, pwa = _opm(d), _pwa(d)
+    m, mask = _msa_inputs(1, 8, 16, 64, seed=3)
+    z = torch.randn(1, 16, 16, 128, generator=torch.Generator().manual_seed(4))
+    pm = torch.ones(1, 16, 16, dtype=torch.bool)
+    with torch.no_grad():
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            a = opm(m.to(d), mask.to(d))
+            b = pwa(m.to(d), z.to(d), pm.to(d))
+        a16 = opm(m.to(d).to(torch.bfloat16), mask.to(d))
+        b16 = pwa(m.to(d).to(torch.bfloat16), z.to(d).to(torch.bfloat16), pm.to(d))
+    assert torch.equal(a.to(torch.bfloat16), a16) and torch.equal(b.to(torch.bfloat16), b16)
