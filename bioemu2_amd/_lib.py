@@ -114,6 +114,13 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _c_int,
         [_c_void_p] * 13 + [_c_size_t] + [_c_int64] * 7 + [ctypes.c_float, _c_int, _c_void_p],
     ),
+    "bioemu_msa_embed_fwd_f32": (_c_int, [_c_void_p] * 9 + [_c_size_t] + [_c_int64] * 6 + [_c_void_p]),
+    "bioemu_ln_linear_f32_workspace_bytes": (_c_size_t, [_c_int64] * 2),
+    "bioemu_ln_linear_fwd_f32": (_c_int, [_c_void_p] * 7 + [_c_size_t] + [_c_int64] * 3 + [_c_void_p]),
+    "bioemu_trunk_uncond_f32_workspace_bytes": (_c_size_t, [_c_int64] * 3),
+    "bioemu_trunk_uncond_fwd_f32": (_c_int, [_c_void_p] * 10 + [_c_size_t] + [_c_int64] * 3 + [_c_void_p]),
+    "bioemu_distogram_f32_workspace_bytes": (_c_size_t, [_c_int64] * 3),
+    "bioemu_distogram_fwd_f32": (_c_int, [_c_void_p] * 5 + [_c_size_t] + [_c_int64] * 4 + [_c_void_p]),
 }
 
 _lock = threading.Lock()

@@ -1396,6 +1396,115 @@ def launch_ln_linear(
     return out
 
 
+def launch_ln_linear_f32(
+    x: Tensor, norm_w: Tensor, norm_b: Tensor, w: Tensor, base: Tensor | None, out: Tensor, ws: Tensor | None = None
+) -> Tensor:
+    """``out = (base +) w LN(x)`` over rows in IEEE fp32 (``bioemu_ln_linear_fwd_f32``; the recycling updates of
+    a trunk run with autocast off, pairmixer.py:281-282)."""
+    require_gpu(x, "ln_linear_f32")
+    K = x.shape[-1]
+    N = w.shape[0]
+    M = x.numel() // K
+    dev = x.device
+    _check_tensor(x, "ln_linear_f32 x", F32, tuple(x.shape), dev)
+    _check_tensor(w, "ln_linear_f32 weight", F32, (N, K), dev)
+    _check_tensor(norm_w, "ln_linear_f32 norm.weight", F32, (K,), dev)
+    _check_tensor(norm_b, "ln_linear_f32 norm.bias", F32, (K,), dev)
+    oshape = tuple(x.shape[:-1]) + (N,)
+    _check_tensor(out, "ln_linear_f32 out", F32, oshape, dev)
+    if base is not None:
+        _check_tensor(base, "ln_linear_f32 base", F32, oshape, dev)
+    need = int(lib().bioemu_ln_linear_f32_workspace_bytes(M, K))
+    if ws is None or ws.numel() < need:
+        ws = workspace(need, dev)
+    rc = lib().bioemu_ln_linear_fwd_f32(_ptr(x), _ptr(norm_w), _ptr(norm_b), _ptr(w), _ptr(base), _ptr(out),
+                                        _ptr(ws), ctypes.c_size_t(ws.numel()), M, K, N, _stream(x))
+    check(rc, "bioemu_ln_linear_fwd_f32")
+    return out
+
+
+def trunk_uncond_f32_workspace_bytes(P: int, D: int, hidden: int) -> int:
+    return int(lib().bioemu_trunk_uncond_f32_workspace_bytes(P, D, hidden))
+
+
+def launch_trunk_uncond_f32(
+    z_init: Tensor, z_norm_w: Tensor, z_norm_b: Tensor, t_norm_w: Tensor, t_norm_b: Tensor, fc1_w: Tensor,
+    fc2_w: Tensor, fc3_w: Tensor, out: Tensor, ws: Tensor | None = None,
+) -> Tensor:
+    """``out = z_init + uncond_transition(z_norm(z_init))`` in IEEE fp32 (pairmixer.py:266-273)."""
+    require_gpu(z_init, "trunk_uncond_f32")
+    D = z_init.shape[-1]
+    P = z_init.numel() // D
+    hidden = fc1_w.shape[0]
+    dev = z_init.device
+    _check_tensor(z_init, "trunk_uncond_f32 z_init", F32, tuple(z_init.shape), dev)
+    _check_tensor(out, "trunk_uncond_f32 out", F32, tuple(z_init.shape), dev)
+    for name, t, shp in (
+        ("z_norm.weight", z_norm_w, (D,)), ("z_norm.bias", z_norm_b, (D,)), ("norm.weight", t_norm_w, (D,)),
+        ("norm.bias", t_norm_b, (D,)), ("fc1.weight", fc1_w, (hidden, D)), ("fc2.weight", fc2_w, (hidden, D)),
+        ("fc3.weight", fc3_w, (D, hidden)),
+    ):
+        _check_tensor(t, f"trunk_uncond_f32 {name}", F32, shp, dev)
+    need = trunk_uncond_f32_workspace_bytes(P, D, hidden)
+    if ws is None or ws.numel() < need:
+        ws = workspace(need, dev)
+    rc = lib().bioemu_trunk_uncond_fwd_f32(
+        _ptr(z_init), _ptr(z_norm_w), _ptr(z_norm_b), _ptr(t_norm_w), _ptr(t_norm_b), _ptr(fc1_w), _ptr(fc2_w),
+        _ptr(fc3_w), _ptr(out), _ptr(ws), ctypes.c_size_t(ws.numel()), P, D, hidden, _stream(z_init))
+    check(rc, "bioemu_trunk_uncond_fwd_f32")
+    return out
+
+
+def launch_distogram_f32(z: Tensor, w: Tensor, b: Tensor, out: Tensor, ws: Tensor | None = None) -> Tensor:
+    """``out = (z + z^T) w^T + b`` in IEEE fp32 (embedders.py:191-206)."""
+    require_gpu(z, "distogram_f32")
+    if z.ndim != 4 or z.shape[1] != z.shape[2]:
+        raise ValueError(f"distogram_f32: z must be [B,N,N,c_z], got {tuple(z.shape)}")
+    B, N, _, c_z = z.shape
+    nb = w.shape[0]
+    dev = z.device
+    _check_tensor(z, "distogram_f32 z", F32, (B, N, N, c_z), dev)
+    _check_tensor(w, "distogram_f32 weight", F32, (nb, c_z), dev)
+    _check_tensor(b, "distogram_f32 bias", F32, (nb,), dev)
+    _check_tensor(out, "distogram_f32 out", F32, (B, N, N, nb), dev)
+    need = int(lib().bioemu_distogram_f32_workspace_bytes(B, N, c_z))
+    if ws is None or ws.numel() < need:
+        ws = workspace(need, dev)
+    rc = lib().bioemu_distogram_fwd_f32(_ptr(z), _ptr(w), _ptr(b), _ptr(out), _ptr(ws), ctypes.c_size_t(ws.numel()),
+                                        B, N, c_z, nb, _stream(z))
+    check(rc, "bioemu_distogram_fwd_f32")
+    return out
+
+
+def launch_msa_embed_f32(
+    msa: Tensor, has_deletion: Tensor, deletion_value: Tensor, msa_paired: Tensor | None, emb: Tensor,
+    w_msa: Tensor, w_s: Tensor, m: Tensor, ws: Tensor | None = None,
+) -> Tensor:
+    """MSA input embedding (pairmixer.py:591-599) into an fp32 ``m`` (a trunk run with autocast off)."""
+    require_gpu(msa, "msa_embed_f32")
+    B, R, T, F0 = msa.shape
+    E = emb.shape[-1]
+    C = w_msa.shape[0]
+    dev = msa.device
+    _check_tensor(msa, "msa_embed_f32 msa", F32, (B, R, T, F0), dev)
+    for t, what in ((has_deletion, "has_deletion"), (deletion_value, "deletion_value"), (msa_paired, "msa_paired")):
+        if t is not None:
+            _check_tensor(t, f"msa_embed_f32 {what}", F32, (B, R, T), dev)
+    _check_tensor(emb, "msa_embed_f32 emb", F32, (B, T, E), dev)
+    _check_tensor(w_msa, "msa_embed_f32 msa_proj.weight", F32, (C, F0 + 2 + int(msa_paired is not None)), dev)
+    _check_tensor(w_s, "msa_embed_f32 s_proj.weight", F32, (C, E), dev)
+    _check_tensor(m, "msa_embed_f32 m", F32, (B, R, T, C), dev)
+    need = lib().bioemu_msa_embed_workspace_bytes(B, T)
+    if ws is None or ws.numel() < need:
+        ws = workspace(need, dev)
+    rc = lib().bioemu_msa_embed_fwd_f32(
+        _ptr(msa), _ptr(has_deletion), _ptr(deletion_value), _ptr(msa_paired), _ptr(emb), _ptr(w_msa), _ptr(w_s),
+        _ptr(m), _ptr(ws), ctypes.c_size_t(ws.numel()), B, R, T, F0, E, C, _stream(msa),
+    )
+    check(rc, "bioemu_msa_embed_fwd_f32")
+    return m
+
+
 def trunk_uncond_workspace_bytes(P: int, D: int, hidden: int) -> int:
     return int(lib().bioemu_trunk_uncond_workspace_bytes(P, D, hidden))
 

@@ -808,6 +808,28 @@ extern "C" int bioemu_swa_fwd_f32(const float* s, const float* z, const uint8_t*
                   (int)c_s, stream, "f32_proj_o");
 }
 
+// out = (res +) Transition(x) over M rows; res may differ from x (the trunk's unconditional branch adds the
+// transition of LN(z_init) to z_init).  workspace: the LN rows [M][Dc], then the hidden rows [M][hidden].
+static int transition_f32_res(const float* x, const float* res, const float* norm_w, const float* norm_b,
+                              const float* fc1_w, const float* fc2_w, const float* fc3_w, float* out, void* workspace,
+                              int64_t M, int64_t Dc, int64_t hidden, int64_t out_dim, int use_norm, int residual,
+                              hipStream_t stream) {
+  float* xn = static_cast<float*>(workspace);
+  float* hbuf = reinterpret_cast<float*>(static_cast<char*>(workspace) + round_up(M * Dc * 4, 256));
+  const float* src = x;
+  int rc = 0;
+  if (use_norm) {
+    rc = rows_ln_f32(x, norm_w, norm_b, xn, M, (int)Dc, stream, "f32_layernorm");
+    src = xn;
+  }
+  if (!rc)
+    rc = gemm_f32(kGemmEpiSwiGLU, src, fc1_w, fc2_w, nullptr, nullptr, hbuf, M, (int)Dc, (int)hidden, stream,
+                  "f32_transition_swiglu");
+  if (rc) return rc;
+  return gemm_f32(residual ? kGemmEpiResidual : kGemmEpiStore, hbuf, fc3_w, nullptr, nullptr, res, out, M,
+                  (int)hidden, (int)out_dim, stream, "f32_transition_out");
+}
+
 extern "C" size_t bioemu_transition_f32_workspace_bytes(int64_t M, int64_t Dc, int64_t hidden) {
   if (M <= 0 || Dc <= 0 || hidden <= 0) return 0;
   return (size_t)round_up(M * Dc * 4, 256) + (size_t)round_up(M * hidden * 4, 256);
@@ -832,20 +854,8 @@ extern "C" int bioemu_transition_fwd_f32(const float* x, const float* norm_w, co
     return set_error(BIOEMU_ERR_INVALID_ARG, "transition_f32: out may alias x only with residual=1");
   if (workspace_bytes < bioemu_transition_f32_workspace_bytes(M, Dc, hidden))
     return set_error(BIOEMU_ERR_WORKSPACE, "transition_f32: workspace too small");
-  float* xn = static_cast<float*>(workspace);
-  float* hbuf = reinterpret_cast<float*>(static_cast<char*>(workspace) + round_up(M * Dc * 4, 256));
-  const float* src = x;
-  int rc = 0;
-  if (use_norm) {
-    rc = rows_ln_f32(x, norm_w, norm_b, xn, M, (int)Dc, stream, "f32_layernorm");
-    src = xn;
-  }
-  if (!rc)
-    rc = gemm_f32(kGemmEpiSwiGLU, src, fc1_w, fc2_w, nullptr, nullptr, hbuf, M, (int)Dc, (int)hidden, stream,
-                  "f32_transition_swiglu");
-  if (rc) return rc;
-  return gemm_f32(residual ? kGemmEpiResidual : kGemmEpiStore, hbuf, fc3_w, nullptr, nullptr, x, out, M, (int)hidden,
-                  (int)out_dim, stream, "f32_transition_out");
+  return transition_f32_res(x, x, norm_w, norm_b, fc1_w, fc2_w, fc3_w, out, workspace, M, Dc, hidden, out_dim,
+                            use_norm, residual, stream);
 }
 
 extern "C" size_t bioemu_pair_cond_f32_workspace_bytes(int64_t P, int64_t token_z, int64_t c_rel) {
@@ -1331,4 +1341,116 @@ extern "C" int bioemu_pwa_fwd_f32(const float* m, const float* z, const uint8_t*
   if ((rc = check_launch("f32_pwa_average"))) return rc;
   return gemm_f32(residual ? kGemmEpiResidual : kGemmEpiStore, go, w_o, nullptr, nullptr, m, out, M, hc, (int)c_m,
                   stream, "f32_pwa_out");
+}
+
+// ---------------------------------------------------------------------------
+// PairMixer trunk glue, fp32 arithmetic (a trunk run with autocast off).
+//   bioemu_ln_linear_fwd_f32   out = (base +) LN(x) W^T over M rows: the recycling
+//                              updates s = s_init + s_recycle(s_norm(s)) and
+//                              z = z_init + z_recycle(z_norm(z)) (pairmixer.py:276-283)
+//   bioemu_trunk_uncond_fwd_f32  z_init + uncond_transition(z_norm(z_init)) (:266-273)
+//   bioemu_distogram_fwd_f32   (z + z^T) W^T + b (embedders.py:191-206)
+// ---------------------------------------------------------------------------
+namespace bioemu {
+namespace {
+
+// sym[b, i, j, :] = z[b, i, j, :] + z[b, j, i, :]; one thread per 4 channels.
+__global__ __launch_bounds__(256) void symmetrize_f32_kernel(const float* __restrict__ z, float* __restrict__ sym,
+                                                             int N, int C, long long quads) {
+  const long long q = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (q >= quads) return;
+  const int cq = C / 4;
+  const long long pair = q / cq;
+  const int c = (int)(q % cq) * 4;
+  const long long b = pair / ((long long)N * N), r = pair % ((long long)N * N);
+  const int i = (int)(r / N), j = (int)(r % N);
+  const f32x4 a = *reinterpret_cast<const f32x4*>(z + (size_t)pair * C + c);
+  const f32x4 t = *reinterpret_cast<const f32x4*>(z + (((size_t)b * N + j) * N + i) * C + c);
+  *reinterpret_cast<f32x4*>(sym + (size_t)pair * C + c) = a + t;
+}
+
+}  // namespace
+}  // namespace bioemu
+
+extern "C" size_t bioemu_ln_linear_f32_workspace_bytes(int64_t M, int64_t K) {
+  if (M <= 0 || K <= 0) return 0;
+  return (size_t)round_up(M * K * 4, 256);
+}
+
+extern "C" int bioemu_ln_linear_fwd_f32(const float* x, const float* norm_w, const float* norm_b, const float* w,
+                                        const float* base, float* out, void* workspace, size_t workspace_bytes,
+                                        int64_t M, int64_t K, int64_t N, hipStream_t stream) {
+  if (M <= 0 || K <= 0 || K % 8 || N <= 0 || N % 32)
+    return set_error(BIOEMU_ERR_UNSUPPORTED, "ln_linear_f32: in dim a multiple of 8, out dim of 32 (got %lld, %lld)",
+                     (long long)K, (long long)N);
+  if (!x || !norm_w || !w || !out || !workspace)
+    return set_error(BIOEMU_ERR_INVALID_ARG, "ln_linear_f32: null pointer argument");
+  if (!aligned16(x) || !aligned16(w) || !aligned16(out) || !aligned16(workspace) || (base && !aligned16(base)))
+    return set_error(BIOEMU_ERR_INVALID_ARG, "ln_linear_f32: tensors must be 16-byte aligned");
+  if (workspace_bytes < bioemu_ln_linear_f32_workspace_bytes(M, K))
+    return set_error(BIOEMU_ERR_WORKSPACE, "ln_linear_f32: workspace too small");
+  float* xn = static_cast<float*>(workspace);
+  const int rc = rows_ln_f32(x, norm_w, norm_b, xn, M, (int)K, stream, "f32_ln_linear_layernorm");
+  if (rc) return rc;
+  return gemm_f32(base ? kGemmEpiResidual : kGemmEpiStore, xn, w, nullptr, nullptr, base, out, M, (int)K, (int)N,
+                  stream, "f32_ln_linear");
+}
+
+extern "C" size_t bioemu_trunk_uncond_f32_workspace_bytes(int64_t P, int64_t Dc, int64_t hidden) {
+  if (P <= 0 || Dc <= 0 || hidden <= 0) return 0;
+  return (size_t)round_up(P * Dc * 4, 256) + bioemu_transition_f32_workspace_bytes(P, Dc, hidden);
+}
+
+extern "C" int bioemu_trunk_uncond_fwd_f32(const float* z_init, const float* z_norm_w, const float* z_norm_b,
+                                           const float* t_norm_w, const float* t_norm_b, const float* fc1_w,
+                                           const float* fc2_w, const float* fc3_w, float* out, void* workspace,
+                                           size_t workspace_bytes, int64_t P, int64_t Dc, int64_t hidden,
+                                           hipStream_t stream) {
+  if (P <= 0 || Dc <= 0 || Dc % 32 || hidden <= 0 || hidden % 32)
+    return set_error(BIOEMU_ERR_UNSUPPORTED, "trunk_uncond_f32: dim and hidden must be multiples of 32 (got %lld, %lld)",
+                     (long long)Dc, (long long)hidden);
+  if (!z_init || !z_norm_w || !t_norm_w || !fc1_w || !fc2_w || !fc3_w || !out || !workspace)
+    return set_error(BIOEMU_ERR_INVALID_ARG, "trunk_uncond_f32: null pointer argument");
+  if (!aligned16(z_init) || !aligned16(out) || !aligned16(fc1_w) || !aligned16(fc2_w) || !aligned16(fc3_w) ||
+      !aligned16(workspace))
+    return set_error(BIOEMU_ERR_INVALID_ARG, "trunk_uncond_f32: tensors must be 16-byte aligned");
+  if (workspace_bytes < bioemu_trunk_uncond_f32_workspace_bytes(P, Dc, hidden))
+    return set_error(BIOEMU_ERR_WORKSPACE, "trunk_uncond_f32: workspace too small");
+  float* zn = static_cast<float*>(workspace);
+  void* tws = static_cast<char*>(workspace) + round_up(P * Dc * 4, 256);
+  const int rc = rows_ln_f32(z_init, z_norm_w, z_norm_b, zn, P, (int)Dc, stream, "f32_trunk_z_norm");
+  if (rc) return rc;
+  return transition_f32_res(zn, z_init, t_norm_w, t_norm_b, fc1_w, fc2_w, fc3_w, out, tws, P, Dc, hidden, Dc, 1, 1,
+                            stream);
+}
+
+extern "C" size_t bioemu_distogram_f32_workspace_bytes(int64_t B, int64_t N, int64_t c_z) {
+  if (B <= 0 || N <= 0 || c_z <= 0) return 0;
+  return (size_t)round_up(B * N * N * c_z * 4, 256);
+}
+
+extern "C" int bioemu_distogram_fwd_f32(const float* z, const float* w, const float* b, float* out, void* workspace,
+                                        size_t workspace_bytes, int64_t B, int64_t N, int64_t c_z, int64_t num_bins,
+                                        hipStream_t stream) {
+  if (c_z <= 0 || c_z % 8 || num_bins <= 0 || num_bins % 32)
+    return set_error(BIOEMU_ERR_UNSUPPORTED, "distogram_f32: c_z a multiple of 8, num_bins of 32 (got %lld, %lld)",
+                     (long long)c_z, (long long)num_bins);
+  if (B <= 0 || N <= 0) return set_error(BIOEMU_ERR_INVALID_ARG, "distogram_f32: bad shape B=%lld N=%lld",
+                                         (long long)B, (long long)N);
+  if (!z || !w || !b || !out || !workspace) return set_error(BIOEMU_ERR_INVALID_ARG, "distogram_f32: null pointer");
+  if (!aligned16(z) || !aligned16(w) || !aligned16(out) || !aligned16(workspace))
+    return set_error(BIOEMU_ERR_INVALID_ARG, "distogram_f32: tensors must be 16-byte aligned");
+  if (workspace_bytes < bioemu_distogram_f32_workspace_bytes(B, N, c_z))
+    return set_error(BIOEMU_ERR_WORKSPACE, "distogram_f32: workspace too small");
+  float* sym = static_cast<float*>(workspace);
+  const long long quads = B * N * N * c_z / 4;
+  {
+    KernelTimerScope timed("f32_symmetrize", stream);
+    hipLaunchKernelGGL(symmetrize_f32_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream, z, sym,
+                       (int)N, (int)c_z, quads);
+  }
+  const int rc = check_launch("f32_symmetrize");
+  if (rc) return rc;
+  return gemm_f32(kGemmEpiStore, sym, w, nullptr, b, nullptr, out, B * N * N, (int)c_z, (int)num_bins, stream,
+                  "f32_distogram");
 }

@@ -92,7 +92,8 @@ __global__ __launch_bounds__(kThreads) void pair_ln_linear_kernel(const bf16* x,
 // MSA embedding.  sproj: one thread per (token, output channel), fp32 dot over
 // the E input features.  msa_embed: one thread per MSA position (b, r, t):
 // the F = F0 + 2 (+1) features are read once, the [C][F] weight sits in LDS,
-// and the 64 outputs plus the token's s_proj row are written as value + tail.
+// and the 64 outputs plus the token's s_proj row are written as value + tail
+// (kF32: as fp32 values, for a run with autocast off).
 // ---------------------------------------------------------------------------
 constexpr int kMsaC = 64;
 constexpr int kMaxFeat = 64;
@@ -111,12 +112,13 @@ __global__ __launch_bounds__(kThreads) void msa_sproj_kernel(const float* __rest
   sp[idx] = acc;
 }
 
+template <bool kF32>
 __global__ __launch_bounds__(kThreads) void msa_embed_kernel(const float* __restrict__ msa,
                                                              const float* __restrict__ has_del,
                                                              const float* __restrict__ del_val,
                                                              const float* __restrict__ paired,
                                                              const float* __restrict__ wm, const float* __restrict__ sp,
-                                                             bf16* __restrict__ m, int8_t* __restrict__ m_tail,
+                                                             void* __restrict__ m_out, int8_t* __restrict__ m_tail,
                                                              long long positions, int R, int T, int F0) {
   __shared__ float wl[kMsaC * kMaxFeat];
   const int F = F0 + 2 + (paired ? 1 : 0);
@@ -139,6 +141,13 @@ __global__ __launch_bounds__(kThreads) void msa_embed_kernel(const float* __rest
 #pragma unroll
     for (int c = 0; c < kMsaC; ++c) o[c] = __builtin_fmaf(wl[c * F + k], fk, o[c]);
   }
+  if (kF32) {
+    float* m = static_cast<float*>(m_out) + pos * kMsaC;
+#pragma unroll
+    for (int c0 = 0; c0 < kMsaC; c0 += 4) *reinterpret_cast<f32x4*>(m + c0) = f32x4{o[c0], o[c0 + 1], o[c0 + 2], o[c0 + 3]};
+    return;
+  }
+  bf16* m = static_cast<bf16*>(m_out);
 #pragma unroll
   for (int c0 = 0; c0 < kMsaC; c0 += 16) tail_store16(m + pos * kMsaC + c0, m_tail + pos * kMsaC + c0, o + c0);
 }
@@ -265,18 +274,18 @@ extern "C" size_t bioemu_msa_embed_workspace_bytes(int64_t B, int64_t T) {
   return (size_t)round_up(B * T * kMsaC * 4, 256);
 }
 
-extern "C" int bioemu_msa_embed_fwd(const float* msa, const float* has_deletion, const float* deletion_value,
-                                    const float* msa_paired, const float* emb, const float* w_msa, const float* w_s,
-                                    void* m, int8_t* m_tail, void* workspace, size_t workspace_bytes, int64_t B,
-                                    int64_t R, int64_t T, int64_t F0, int64_t E, int64_t msa_s, hipStream_t stream) {
+static int msa_embed(const float* msa, const float* has_deletion, const float* deletion_value,
+                     const float* msa_paired, const float* emb, const float* w_msa, const float* w_s, void* m,
+                     int8_t* m_tail, bool f32, void* workspace, size_t workspace_bytes, int64_t B, int64_t R,
+                     int64_t T, int64_t F0, int64_t E, int64_t msa_s, hipStream_t stream) {
   if (msa_s != kMsaC)
     return set_error(BIOEMU_ERR_UNSUPPORTED, "msa_embed: only msa_s = 64 (got %lld)", (long long)msa_s);
   if (B <= 0 || R <= 0 || T <= 0 || F0 <= 0 || E <= 0 || F0 + 3 > kMaxFeat)
     return set_error(BIOEMU_ERR_INVALID_ARG, "msa_embed: bad shape B=%lld R=%lld T=%lld F0=%lld E=%lld",
                      (long long)B, (long long)R, (long long)T, (long long)F0, (long long)E);
-  if (!msa || !has_deletion || !deletion_value || !emb || !w_msa || !w_s || !m || !m_tail || !workspace)
+  if (!msa || !has_deletion || !deletion_value || !emb || !w_msa || !w_s || !m || (!f32 && !m_tail) || !workspace)
     return set_error(BIOEMU_ERR_INVALID_ARG, "msa_embed: null pointer argument");
-  if (!aligned16(m) || !aligned16(m_tail))
+  if (!aligned16(m) || (!f32 && !aligned16(m_tail)))
     return set_error(BIOEMU_ERR_INVALID_ARG, "msa_embed: m and its tail must be 16-byte aligned");
   if (workspace_bytes < bioemu_msa_embed_workspace_bytes(B, T))
     return set_error(BIOEMU_ERR_WORKSPACE, "msa_embed: workspace too small");
@@ -292,9 +301,30 @@ extern "C" int bioemu_msa_embed_fwd(const float* msa, const float* has_deletion,
   const long long positions = B * R * T;
   {
     KernelTimerScope timed("msa_embed", stream);
-    hipLaunchKernelGGL(msa_embed_kernel, dim3((unsigned)((positions + kThreads - 1) / kThreads)), dim3(kThreads), 0,
-                       stream, msa, has_deletion, deletion_value, msa_paired, w_msa, sp, static_cast<bf16*>(m),
-                       m_tail, positions, (int)R, (int)T, (int)F0);
+    const dim3 grid((unsigned)((positions + kThreads - 1) / kThreads));
+    if (f32)
+      hipLaunchKernelGGL(msa_embed_kernel<true>, grid, dim3(kThreads), 0, stream, msa, has_deletion, deletion_value,
+                         msa_paired, w_msa, sp, m, nullptr, positions, (int)R, (int)T, (int)F0);
+    else
+      hipLaunchKernelGGL(msa_embed_kernel<false>, grid, dim3(kThreads), 0, stream, msa, has_deletion, deletion_value,
+                         msa_paired, w_msa, sp, m, m_tail, positions, (int)R, (int)T, (int)F0);
   }
   return check_launch("msa_embed");
+}
+
+extern "C" int bioemu_msa_embed_fwd(const float* msa, const float* has_deletion, const float* deletion_value,
+                                    const float* msa_paired, const float* emb, const float* w_msa, const float* w_s,
+                                    void* m, int8_t* m_tail, void* workspace, size_t workspace_bytes, int64_t B,
+                                    int64_t R, int64_t T, int64_t F0, int64_t E, int64_t msa_s, hipStream_t stream) {
+  return msa_embed(msa, has_deletion, deletion_value, msa_paired, emb, w_msa, w_s, m, m_tail, false, workspace,
+                   workspace_bytes, B, R, T, F0, E, msa_s, stream);
+}
+
+extern "C" int bioemu_msa_embed_fwd_f32(const float* msa, const float* has_deletion, const float* deletion_value,
+                                        const float* msa_paired, const float* emb, const float* w_msa,
+                                        const float* w_s, float* m, void* workspace, size_t workspace_bytes,
+                                        int64_t B, int64_t R, int64_t T, int64_t F0, int64_t E, int64_t msa_s,
+                                        hipStream_t stream) {
+  return msa_embed(msa, has_deletion, deletion_value, msa_paired, emb, w_msa, w_s, m, nullptr, true, workspace,
+                   workspace_bytes, B, R, T, F0, E, msa_s, stream);
 }

@@ -37,14 +37,20 @@ class DistogramModule(nn.Module):
         super().__init__()
         self.distogram = nn.Linear(token_z, num_bins)
         self._prepared = PreparedParams([("distogram.weight", BF16), ("distogram.bias", torch.float32)])
+        self._prepared32 = PreparedParams([("distogram.weight", torch.float32), ("distogram.bias", torch.float32)])
 
     def prepared_params(self) -> tuple[Tensor, Tensor]:
         return self._prepared.get(self)
 
     @torch.no_grad()
     def forward(self, z: Tensor) -> Tensor:
+        """bf16 z (or fp32 under bf16 autocast): the bf16 kernel, fp32 accumulation, output in z's dtype; fp32 z
+        with autocast off: IEEE fp32 arithmetic."""
         _ops.require_gpu(z, type(self).__name__)
-        _ops.require_mixed_precision(z, type(self).__name__)
+        if _ops.fp32_mode(z):
+            w, b = self._prepared32.get(self)
+            out = torch.empty(*z.shape[:-1], w.shape[0], dtype=torch.float32, device=z.device)
+            return _ops.launch_distogram_f32(z.contiguous(), w, b, out)
         zb = z.to(BF16).contiguous()
         w, b = self.prepared_params()
         # fp32 callers get the fp32 accumulator (no output rounding); others a bf16 output

@@ -157,6 +157,37 @@ class PairMixerMSALayerHip(nn.Module, _WorkspaceMixin):
             _ops.transition_pair_workspace_bytes(self.token_z, self.z_transition.hidden),
         )
 
+    def workspace_bytes_f32(self, B: int, S: int, N: int) -> int:
+        return max(
+            _ops.pwa_f32_workspace_bytes(B, S, N, self.msa_s, 32, 8),
+            _ops.transition_f32_workspace_bytes(B * S * N, self.msa_s, self.msa_transition.hidden),
+            _ops.opm_f32_workspace_bytes(B, S, N, self.msa_s, 32),
+            _ops.trimul_f32_workspace_bytes(B, N, self.token_z),
+            _ops.transition_f32_workspace_bytes(B * N * N, self.token_z, self.z_transition.hidden),
+        )
+
+    @torch.no_grad()
+    def forward_f32_(self, s: Tensor, z: Tensor, m: Tensor, token_mask: Tensor, msa_mask: Tensor,
+                     ws: Tensor | None = None) -> tuple[Tensor, Tensor, Tensor]:
+        """In place on fp32 ``z`` and ``m`` in IEEE fp32 arithmetic (the reference run with autocast off),
+        in the order of ``forward_``: pair-weighted averaging and the MSA transition into m, the outer-product
+        mean into z, then the two triangle multiplications and the pair transition."""
+        _ops.require_gpu(z, type(self).__name__)
+        B, S, N = m.shape[0], m.shape[1], m.shape[2]
+        if ws is None:
+            ws = self._workspace(self.workspace_bytes_f32(B, S, N), z.device)
+        pm = _ops.mask_u8(token_mask)
+        pwa = self.pair_weighted_averaging
+        _ops.launch_pwa_f32(m, z, pm, *pwa.prepared_params_f32(), m, pwa.num_heads, residual=True, inf=pwa.inf,
+                            ws=ws)
+        _ops.launch_transition_f32(m, *self.msa_transition.prepared_params_f32(), m, residual=True, ws=ws)
+        mask3, mean_rows = _ops.opm_mask3(msa_mask, B, S, N)
+        _ops.launch_opm_f32(m, mask3, mean_rows, *self.outer_product_mean.prepared_params_f32(), out=z, z_res=z, ws=ws)
+        _ops.launch_trimul_f32(z, pm, *self.tri_mul_out.prepared_params_f32(), z, True, residual=True, ws=ws)
+        _ops.launch_trimul_f32(z, pm, *self.tri_mul_in.prepared_params_f32(), z, False, residual=True, ws=ws)
+        _ops.launch_transition_f32(z, *self.z_transition.prepared_params_f32(), z, residual=True, ws=ws)
+        return s, z, m
+
     @torch.no_grad()
     def forward_(
         self,
@@ -191,7 +222,13 @@ class PairMixerMSALayerHip(nn.Module, _WorkspaceMixin):
     def forward(
         self, s: Tensor, z: Tensor, m: Tensor, token_mask: Tensor, msa_mask: Tensor, chunk_heads_pwa: bool = False
     ) -> tuple[Tensor, Tensor, Tensor]:
-        _ops.require_mixed_precision(z, type(self).__name__)
+        """bf16 (or fp32 under bf16 autocast): z and m carried as bf16 + int8 tails; fp32 with autocast off:
+        IEEE fp32 arithmetic on fp32 copies of z and m."""
+        _ops.require_gpu(z, type(self).__name__)
+        if _ops.fp32_mode(z):
+            z32, m32 = z.contiguous().clone(), m.to(torch.float32).contiguous().clone()
+            self.forward_f32_(s, z32, m32, token_mask, msa_mask)
+            return s, z32, m32
         (z_hi, z_tail), (m_hi, m_tail) = split_stream(z), split_stream(m)
         self.forward_(s, z_hi, m_hi, token_mask, msa_mask, chunk_heads_pwa, z_tail, m_tail)
         return s, join_stream(z_hi, z_tail, z.dtype), join_stream(m_hi, m_tail, m.dtype)
@@ -308,6 +345,32 @@ class PairMixerMSAModuleHip(nn.Module, _WorkspaceMixin):
         layer = self.layers[0].workspace_bytes(B, S, N) if len(self.layers) else 16
         return max(layer, int(_ops.lib().bioemu_msa_embed_workspace_bytes(B, N)))
 
+    def workspace_bytes_f32(self, B: int, S: int, N: int) -> int:
+        layer = self.layers[0].workspace_bytes_f32(B, S, N) if len(self.layers) else 16
+        return max(layer, int(_ops.lib().bioemu_msa_embed_workspace_bytes(B, N)))
+
+    @torch.no_grad()
+    def forward_f32_(self, z: Tensor, emb: Tensor, msa: Tensor, msa_mask: Tensor, has_deletion: Tensor,
+                     deletion_value: Tensor, msa_paired: Tensor, token_pad_mask: Tensor,
+                     ws: Tensor | None = None) -> Tensor:
+        """In place on fp32 ``z`` in IEEE fp32 arithmetic (a trunk run with autocast off): the fp32 MSA stream
+        from the features, then every MSA layer's fp32 path."""
+        _ops.require_gpu(z, type(self).__name__)
+        B, R, T = msa.shape[:3]
+        if ws is None:
+            ws = self._workspace(self.workspace_bytes_f32(B, R, T), z.device)
+        f32 = torch.float32
+        m = torch.empty(B, R, T, self.msa_s, dtype=f32, device=msa.device)
+        _ops.launch_msa_embed_f32(
+            msa.to(f32).contiguous(), has_deletion.to(f32).contiguous(), deletion_value.to(f32).contiguous(),
+            msa_paired.to(f32).contiguous() if self.use_paired_feature else None, emb.to(f32).contiguous(),
+            self.msa_proj.weight.to(f32).contiguous(), self.s_proj.weight.to(f32).contiguous(), m, ws=ws)
+        tok = token_pad_mask.bool()
+        pm = tok[:, :, None] & tok[:, None, :]                       # :589
+        for layer in self.layers:                                     # :602-610
+            layer.forward_f32_(None, z, m, pm, msa_mask, ws=ws)
+        return z
+
     def embed(self, emb: Tensor, msa: Tensor, has_deletion: Tensor, deletion_value: Tensor, msa_paired: Tensor,
               ws: Tensor | None = None) -> tuple[Tensor, Tensor]:
         """The MSA stream (m [B,R,T,msa_s] bf16, its int8 tail) from the features (pairmixer.py:591-599)."""
@@ -338,7 +401,13 @@ class PairMixerMSAModuleHip(nn.Module, _WorkspaceMixin):
         return z
 
     def forward(self, s, z, emb, msa, msa_mask, has_deletion, deletion_value, msa_paired, token_pad_mask):
-        _ops.require_mixed_precision(z, type(self).__name__)
+        """bf16 (or fp32 under bf16 autocast): z carried as bf16 + int8 tail; fp32 with autocast off: IEEE fp32
+        arithmetic on an fp32 copy of z."""
+        _ops.require_gpu(z, type(self).__name__)
+        if _ops.fp32_mode(z):
+            z32 = z.contiguous().clone()
+            self.forward_f32_(z32, emb, msa, msa_mask, has_deletion, deletion_value, msa_paired, token_pad_mask)
+            return s, z32
         z_hi, z_tail = split_stream(z)
         self.forward_(z_hi, emb, msa, msa_mask, has_deletion, deletion_value, msa_paired, token_pad_mask, z_tail)
         return s, join_stream(z_hi, z_tail, z.dtype)
@@ -399,6 +468,13 @@ class PairMixerTrunkHip(nn.Module, _WorkspaceMixin):
                    int(_ops.lib().bioemu_pair_ln_linear_workspace_bytes(self.z_recycle.in_features)),
                    int(_ops.lib().bioemu_token_ln_linear_workspace_bytes(B * N, token_s)))
 
+    def workspace_bytes_f32(self, B: int, S: int, N: int, token_s: int) -> int:
+        return max(self.msa_module.workspace_bytes_f32(B, S, N),
+                   self.pairmixer_module.layers[0].workspace_bytes_f32(B, N) if len(self.pairmixer_module.layers)
+                   else 16,
+                   int(_ops.lib().bioemu_ln_linear_f32_workspace_bytes(B * N * N, self.z_recycle.in_features)),
+                   int(_ops.lib().bioemu_ln_linear_f32_workspace_bytes(B * N, token_s)))
+
     @torch.no_grad()
     def forward_unconditional(self, s_init: Tensor, z_init: Tensor) -> tuple[Tensor, Tensor]:
         """The unconditional branch (pairmixer.py:266-273): s = s_init and z = z_init + uncond_transition(
@@ -408,11 +484,18 @@ class PairMixerTrunkHip(nn.Module, _WorkspaceMixin):
                 "Passing unconditional=True at inference time requires use_unconditional_branch=True at __init__"
             )
         _ops.require_gpu(z_init, type(self).__name__)
-        _ops.require_mixed_precision(z_init, type(self).__name__)
         D = z_init.shape[-1]
         P = z_init.numel() // D
         t = self.uncond_transition
         bf16, f32 = torch.bfloat16, torch.float32
+        if _ops.fp32_mode(z_init):
+            c = lambda x: x.to(f32).contiguous()  # noqa: E731
+            out = torch.empty_like(z_init, dtype=f32)
+            ws = self._workspace(_ops.trunk_uncond_f32_workspace_bytes(P, D, t.hidden), z_init.device)
+            _ops.launch_trunk_uncond_f32(
+                c(z_init), c(self.z_norm.weight), c(self.z_norm.bias), c(t.norm.weight), c(t.norm.bias),
+                c(t.fc1.weight), c(t.fc2.weight), c(t.fc3.weight), out, ws=ws)
+            return s_init, out
         z0, z0_tail = split_stream(z_init)
         ws = self._workspace(_ops.trunk_uncond_workspace_bytes(P, D, t.hidden), z_init.device)
         _ops.launch_trunk_uncond(
@@ -430,7 +513,8 @@ class PairMixerTrunkHip(nn.Module, _WorkspaceMixin):
         if unconditional:
             return self.forward_unconditional(s_init, z_init)
         _ops.require_gpu(z_init, type(self).__name__)
-        _ops.require_mixed_precision(z_init, type(self).__name__)
+        if _ops.fp32_mode(z_init):
+            return self._forward_f32(s_init, z_init, s_inputs, feats, num_steps_recycle)
         B, N = z_init.shape[:2]
         S = feats["msa"].shape[1]
         ws = self._workspace(self.workspace_bytes(B, S, N, s_init.shape[-1]), z_init.device)
@@ -451,3 +535,28 @@ class PairMixerTrunkHip(nn.Module, _WorkspaceMixin):
                                      z_tail, ws=ws)                     # :284-294
             self.pairmixer_module.forward_(s, z, pm, z_tail, ws=ws)    # :296
         return join_stream(s, s_tail, s_init.dtype), join_stream(z, z_tail, z_init.dtype)
+
+    def _forward_f32(self, s_init: Tensor, z_init: Tensor, s_inputs: Tensor, feats: dict,
+                     num_steps_recycle: int) -> tuple[Tensor, Tensor]:
+        """The recycling loop of :275-296 in IEEE fp32 (autocast off): fp32 s and z, fp32 recycling updates,
+        the MSA module's and the PairMixer layers' fp32 paths."""
+        B, N = z_init.shape[:2]
+        S = feats["msa"].shape[1]
+        f32 = torch.float32
+        ws = self._workspace(self.workspace_bytes_f32(B, S, N, s_init.shape[-1]), z_init.device)
+        s0, z0 = s_init.to(f32).contiguous(), z_init.to(f32).contiguous()
+        s, z = torch.zeros_like(s0), torch.zeros_like(z0)                 # :257-258
+        tok = feats["token_pad_mask"].bool()
+        pm = tok[:, :, None] & tok[:, None, :]                            # :263-264
+        c = lambda x: x.to(f32).contiguous()  # noqa: E731
+        for _ in range(num_steps_recycle + 1):                            # :275
+            _ops.launch_ln_linear_f32(s, c(self.s_norm.weight), c(self.s_norm.bias), c(self.s_recycle.weight), s0, s,
+                                      ws=ws)
+            _ops.launch_ln_linear_f32(z, c(self.z_norm.weight), c(self.z_norm.bias), c(self.z_recycle.weight), z0, z,
+                                      ws=ws)
+            self.msa_module.forward_f32_(z, s_inputs, feats["msa"], feats["msa_mask"], feats["has_deletion"],
+                                         feats["deletion_value"], feats.get("msa_paired"), feats["token_pad_mask"],
+                                         ws=ws)                            # :284-294
+            for layer in self.pairmixer_module.layers:                     # :296 (pairmixer.py:368-369)
+                layer.forward_f32_(s, z, pm, ws=ws)
+        return s, z

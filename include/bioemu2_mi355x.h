@@ -375,6 +375,15 @@ int bioemu_msa_embed_fwd(const float* msa, const float* has_deletion, const floa
  *                            res_tail, plus the masking constant inf (the module's inf; masked
  *                            logits become -inf); c_h = 32, c_m a multiple of 32, c_z 16, 32 or
  *                            128, B * H <= 65535.
+ *   bioemu_msa_embed_fwd_f32 bioemu_msa_embed_fwd writing m as fp32 (no tail).
+ *   bioemu_ln_linear_fwd_f32 out = (base +) LN(x) W^T over M rows (x [M][K], w [N][K]; base
+ *                            may be null): the recycling updates of the trunk
+ *                            (pairmixer.py:276-283), replacing bioemu_pair_ln_linear_fwd and
+ *                            bioemu_token_ln_linear_fwd; K a multiple of 8, N of 32.
+ *   bioemu_trunk_uncond_fwd_f32  bioemu_trunk_uncond_fwd in fp32 (z_init + uncond_transition(
+ *                            z_norm(z_init)), :266-273); dim and hidden multiples of 32.
+ *   bioemu_distogram_fwd_f32 DistogramModule.forward (embedders.py:191-206) on fp32 z:
+ *                            (z + z^T) W^T + b; c_z a multiple of 8, num_bins of 32.
  * Residual tails do not apply (the stream is fp32).
  */
 size_t bioemu_apb_f32_workspace_bytes(int64_t B, int64_t mult, int64_t N, int64_t c_s, int64_t H);
@@ -416,6 +425,23 @@ int bioemu_pwa_fwd_f32(const float* m, const float* z, const uint8_t* mask, cons
                        const float* w_g, const float* w_z, const float* w_o, float* out, void* workspace,
                        size_t workspace_bytes, int64_t B, int64_t S, int64_t N, int64_t c_m, int64_t c_z,
                        int64_t c_h, int64_t H, float inf, int residual, hipStream_t stream);
+int bioemu_msa_embed_fwd_f32(const float* msa, const float* has_deletion, const float* deletion_value,
+                             const float* msa_paired, const float* emb, const float* w_msa, const float* w_s,
+                             float* m, void* workspace, size_t workspace_bytes, int64_t B, int64_t R, int64_t T,
+                             int64_t F0, int64_t E, int64_t msa_s, hipStream_t stream);
+size_t bioemu_ln_linear_f32_workspace_bytes(int64_t M, int64_t K);
+int bioemu_ln_linear_fwd_f32(const float* x, const float* norm_w, const float* norm_b, const float* w,
+                             const float* base, float* out, void* workspace, size_t workspace_bytes, int64_t M,
+                             int64_t K, int64_t N, hipStream_t stream);
+size_t bioemu_trunk_uncond_f32_workspace_bytes(int64_t P, int64_t Dc, int64_t hidden);
+int bioemu_trunk_uncond_fwd_f32(const float* z_init, const float* z_norm_w, const float* z_norm_b,
+                                const float* t_norm_w, const float* t_norm_b, const float* fc1_w, const float* fc2_w,
+                                const float* fc3_w, float* out, void* workspace, size_t workspace_bytes, int64_t P,
+                                int64_t Dc, int64_t hidden, hipStream_t stream);
+size_t bioemu_distogram_f32_workspace_bytes(int64_t B, int64_t N, int64_t c_z);
+int bioemu_distogram_fwd_f32(const float* z, const float* w, const float* b, float* out, void* workspace,
+                             size_t workspace_bytes, int64_t B, int64_t N, int64_t c_z, int64_t num_bins,
+                             hipStream_t stream);
 
 #ifdef __cplusplus
 }

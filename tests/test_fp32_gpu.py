@@ -461,3 +461,93 @@ def test_opm_pwa_autocast_take_bf16_path(gpu_device):
         a16 = opm(m.to(d).to(torch.bfloat16), mask.to(d))
         b16 = pwa(m.to(d).to(torch.bfloat16), z.to(d).to(torch.bfloat16), pm.to(d))
     assert torch.equal(a.to(torch.bfloat16), a16) and torch.equal(b.to(torch.bfloat16), b16)
+
+
+# ----------------------------------------------------------------------------
+# PairMixer trunk with autocast off: MSA layer, MSA module, recycling loop,
+# unconditional branch, distogram
+# ----------------------------------------------------------------------------
+def _trunk_feats(B, R, T, n_pad, g):
+    from bioemu2_amd.pairmixer import NUM_TOKENS
+
+    tok = torch.randint(0, NUM_TOKENS, (B, R, T), generator=g)
+    pad = torch.ones(B, T, dtype=torch.bool)
+    if n_pad:
+        pad[:, T - n_pad:] = False
+    return {
+        "msa": torch.nn.functional.one_hot(tok, NUM_TOKENS).float(),
+        "has_deletion": (torch.rand(B, R, T, generator=g) < 0.3).float(),
+        "deletion_value": torch.rand(B, R, T, generator=g),
+        "msa_paired": (torch.rand(B, R, T, generator=g) < 0.5).float(),
+        "msa_mask": torch.rand(B, R, T, generator=g) > 0.2,
+        "token_pad_mask": pad,
+    }
+
+
+def test_msa_layer_f32_matches_oracle(gpu_device):
+    """PairMixerMSALayer with autocast off (pairmixer.py:612-680): PWA and the MSA transition into m, the
+    outer-product mean into z, both triangle multiplications and the pair transition, all in fp32."""
+    from bioemu2_amd.pairmixer import PairMixerMSALayerHip
+
+    B, S, N, d = 1, 12, 30, gpu_device
+    g = torch.Generator().manual_seed(9)
+    z = torch.randn(B, N, N, 128, generator=g)
+    m = torch.randn(B, S, N, 64, generator=g)
+    tok = torch.ones(B, N, dtype=torch.bool)
+    tok[:, N - 3:] = False
+    pm = oracle.pair_mask_from_token_mask(tok)
+    msa_mask = torch.rand(B, S, N, generator=g) > 0.2
+    torch.manual_seed(0)
+    layer = randomize_params(PairMixerMSALayerHip(384, 64, 128, 0.15, 0.25), 2).to(d).eval()
+    print("msa_layer_f32", flush=True)
+    _, z_got, m_got = layer(None, z.to(d), m.to(d), pm.to(d), msa_mask.to(d))
+    _, z_want, m_want = oracle.pairmixer_msa_layer(None, z, m, pm, msa_mask, state(layer))
+    _check(z_got.cpu(), z_want, "msa_layer_f32 z")
+    _check(m_got.cpu(), m_want, "msa_layer_f32 m")
+
+
+def test_msa_module_and_trunk_f32_match_oracle(gpu_device):
+    """The MSA module (fp32 input embedding, then its layers) and the whole recycling loop (pairmixer.py:275-296)
+    with autocast off, against the oracle at the fp32 bound; the unconditional branch (:266-273) too."""
+    from bioemu2_amd.pairmixer import PairMixerMSAModuleHip, PairMixerTrunkHip
+
+    B, R, T, n_pad, E, d = 1, 8, 24, 3, 455, gpu_device
+    g = torch.Generator().manual_seed(10)
+    f = _trunk_feats(B, R, T, n_pad, g)
+    fd = {k: v.to(d) for k, v in f.items()}
+    emb = torch.randn(B, T, E, generator=g)
+    z = torch.randn(B, T, T, 128, generator=g)
+    torch.manual_seed(0)
+    mod = randomize_params(PairMixerMSAModuleHip(384, 64, 128, E, 2, 0.15, 0.25, use_paired_feature=True), 3)
+    mod = mod.to(d).eval()
+    print("msa_module_f32", flush=True)
+    _, z_got = mod(None, z.to(d), emb.to(d), fd["msa"], fd["msa_mask"], fd["has_deletion"], fd["deletion_value"],
+                   fd["msa_paired"], fd["token_pad_mask"])
+    z_want = oracle.pairmixer_msa_module(z, emb, f, f["token_pad_mask"], state(mod), 2)
+    _check(z_got.cpu(), z_want, "msa_module_f32 z (2 layers)")
+
+    trunk = randomize_params(PairMixerTrunkHip(384, 128, E, msa_blocks=1, num_blocks=1,
+                                               use_unconditional_branch=True), 4).to(d).eval()
+    s_init, z_init = torch.randn(B, T, 384, generator=g), torch.randn(B, T, T, 128, generator=g)
+    for recycles in (0, 1):
+        print(f"trunk_f32 recycles={recycles}", flush=True)
+        s_got, z_got = trunk(s_init.to(d), z_init.to(d), emb.to(d), fd, recycles)
+        s_want, z_want = oracle.pairmixer_trunk(s_init, z_init, emb, f, state(trunk), 1, 1, recycles)
+        _check(z_got.cpu(), z_want, f"trunk_f32 recycles={recycles} z")
+        _check(s_got.cpu(), s_want, f"trunk_f32 recycles={recycles} s")
+    s_got, z_got = trunk(s_init.to(d), z_init.to(d), None, {}, unconditional=True)
+    _, z_want = oracle.pairmixer_uncond(s_init, z_init, state(trunk))
+    assert torch.equal(s_got.cpu(), s_init)
+    _check(z_got.cpu(), z_want, "trunk_f32 unconditional z")
+
+
+def test_distogram_f32_matches_oracle(gpu_device):
+    """DistogramModule with autocast off: (z + z^T) W^T + b in fp32 (embedders.py:191-206)."""
+    from bioemu2_amd.glue import DistogramModule
+
+    g = torch.Generator().manual_seed(11)
+    z = torch.randn(2, 37, 37, 128, generator=g)
+    torch.manual_seed(0)
+    mod = randomize_params(DistogramModule(128, 64), 5).to(gpu_device).eval()
+    got = mod(z.to(gpu_device))
+    _check(got.cpu(), oracle.distogram(z, state(mod)), "distogram_f32")
