@@ -99,6 +99,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "bioemu_pair_cond_f32_workspace_bytes": (_c_size_t, [_c_int64] * 3),
     "bioemu_pair_cond_proj_fwd_f32": (_c_int, [_c_void_p] * 7 + [_c_size_t] + [_c_int64] * 4 + [_c_void_p]),
+    "bioemu_triatt_f32_workspace_bytes": (_c_size_t, [_c_int64] * 4),
+    "bioemu_triatt_fwd_f32": (
+        _c_int,
+        [_c_void_p] * 8 + [_c_size_t] + [_c_int64] * 4 + [_c_int, _c_int, _c_void_p],
+    ),
     "bioemu_trimul_f32_workspace_bytes": (_c_size_t, [_c_int64] * 3),
     "bioemu_trimul_fwd_f32": (
         _c_int,

@@ -336,6 +336,72 @@ def _(z, mask, norm_w, norm_b, w_proj, w_o, starting, num_heads):
     return torch.empty_like(z)
 
 
+def triatt_f32_workspace_bytes(B: int, N: int, D: int = 128, H: int = 4) -> int:
+    return int(lib().bioemu_triatt_f32_workspace_bytes(B, N, D, H))
+
+
+def launch_triatt_f32(
+    z: Tensor,
+    mask: Tensor,
+    norm_w: Tensor,
+    norm_b: Tensor,
+    w_proj: Tensor,
+    w_o: Tensor,
+    out: Tensor,
+    starting: bool,
+    num_heads: int = 4,
+    residual: bool = False,
+    ws: Tensor | None = None,
+) -> Tensor:
+    """Triangle attention in fp32 (``bioemu_triatt_fwd_f32``): the arguments of ``launch_triatt``, every
+    tensor fp32 (the mask uint8), no tail."""
+    require_gpu(z, "triatt_f32")
+    if z.ndim != 4 or z.shape[1] != z.shape[2]:
+        raise ValueError(f"triatt_f32: z must be [B,N,N,D], got {tuple(z.shape)}")
+    B, N, _, D = z.shape
+    dev = z.device
+    _check_tensor(z, "triatt_f32 z", F32, (B, N, N, D), dev)
+    _check_tensor(out, "triatt_f32 out", F32, (B, N, N, D), dev)
+    _check_tensor(mask, "triatt_f32 mask", torch.uint8, (B, N, N), dev)
+    _check_tensor(norm_w, "triatt_f32 norm.weight", F32, (D,), dev)
+    _check_tensor(norm_b, "triatt_f32 norm.bias", F32, (D,), dev)
+    _check_tensor(w_proj, "triatt_f32 packed projection", F32, (4 * D + num_heads, D), dev)
+    _check_tensor(w_o, "triatt_f32 proj_o.weight", F32, (D, D), dev)
+    need = triatt_f32_workspace_bytes(B, N, D, num_heads)
+    if ws is None or ws.numel() < need:
+        ws = workspace(need, dev)
+    rc = lib().bioemu_triatt_fwd_f32(
+        _ptr(z), _ptr(mask), _ptr(norm_w), _ptr(norm_b), _ptr(w_proj), _ptr(w_o), _ptr(out), _ptr(ws),
+        ctypes.c_size_t(ws.numel()), B, N, D, num_heads, int(bool(starting)), int(bool(residual)), _stream(z),
+    )
+    check(rc, "bioemu_triatt_fwd_f32")
+    return out
+
+
+@torch.library.custom_op("bioemu_mi355x::triangle_attention_f32", mutates_args=(), device_types="cuda")
+def triangle_attention_f32(
+    z: Tensor,
+    mask: Tensor,
+    norm_w: Tensor,
+    norm_b: Tensor,
+    w_proj: Tensor,
+    w_o: Tensor,
+    starting: bool,
+    num_heads: int,
+) -> Tensor:
+    zf = z.contiguous()
+    out = torch.empty_like(zf)
+    f32c = lambda t: t.to(F32).contiguous()  # noqa: E731
+    launch_triatt_f32(zf, mask_u8(mask), f32c(norm_w), f32c(norm_b), f32c(w_proj), f32c(w_o), out, starting,
+                      num_heads)
+    return out
+
+
+@triangle_attention_f32.register_fake
+def _(z, mask, norm_w, norm_b, w_proj, w_o, starting, num_heads):
+    return torch.empty_like(z)
+
+
 # ----------------------------------------------------------------------------
 # Transition (SwiGLU MLP)
 # ----------------------------------------------------------------------------
@@ -670,23 +736,6 @@ def fp32_mode(x: Tensor) -> bool:
     transitions run fp32 on fp32 activations; under bf16 autocast (the trunk) they run bf16 matmuls.
     """
     return x.dtype == F32 and not torch.is_autocast_enabled("cuda")
-
-
-def require_mixed_precision(x: Tensor, what: str) -> None:
-    """Refuse the reference's fp32 mode (fp32 inputs with CUDA autocast off) for an op that has no fp32
-    arithmetic.  Those ops compute with bf16 MFMA operands and fp32 accumulation, which is what the reference's
-    trunk does under bf16 autocast (model.py:222, utils/precision.py:9-26); an fp32 caller outside autocast asks
-    for IEEE fp32 (``TriangleMultiplicationCueq``'s default ``matmul_precision="ieee"``, triangle_multiplication
-    .py:117; OPM's fp32 contraction, outer_product_mean.py:64-74) and gets an error instead of bf16-level
-    results.  Running under ``torch.autocast("cuda", dtype=torch.bfloat16)`` or passing bf16 tensors selects the
-    bf16 path explicitly.  Host tensors fail first, as everywhere (there is no CPU path)."""
-    require_gpu(x, what)
-    if fp32_mode(x):
-        raise ValueError(
-            f"{what}: fp32 inputs with autocast off ask for fp32 arithmetic, which this op does not have (it computes "
-            "with bf16 MFMA operands and fp32 accumulation); run it under torch.autocast('cuda', "
-            "dtype=torch.bfloat16), the reference trunk's policy, or pass bf16 tensors"
-        )
 
 
 def _check_attn_params_f32(what, c_s, c_z, num_heads, dev, norm_s_w, norm_s_b, w_qkv, q_bias, w_g, norm_z_w,

@@ -163,7 +163,7 @@ __global__ __launch_bounds__(256) void qkvg_f32_kernel(const float* __restrict__
 #pragma unroll
   for (int u = 0; u < 16; ++u) {
     float x = acc[u];
-    if (part == 0) x += q_bias[c0 + u];
+    if (part == 0 && q_bias) x += q_bias[c0 + u];
     if (part == 3) x = 1.0f / (1.0f + __expf(-x));
     v[u] = x;
   }
@@ -342,13 +342,16 @@ __device__ __forceinline__ void load_q_f32(const float* qr, float (&qv)[D / 2]) 
 // Full attention: grid (ceil(N / 128), H, B * mult), 4 waves of 32 queries
 // sharing each 32-key block of K, V^T and the mask through LDS (staged once
 // per workgroup, double-buffered).  bias [B][H][N][ld], V^T [B*mult][c_s][ld]
-// (ld = N rounded up to 32; columns >= N unused).
+// (ld = N rounded up to 32; columns >= N unused).  Key mask: one row of N
+// bytes per batch ([B][N], mask_per_copy = 0) or per copy ([B*mult][N],
+// mask_per_copy = 1: triangle attention's per-sequence mask).
 template <int D>
 __global__ __launch_bounds__(256) void attn_f32_kernel(const float* __restrict__ q, const float* __restrict__ k,
                                                        const float* __restrict__ vt, const float* __restrict__ g,
                                                        const float* __restrict__ bias,
                                                        const uint8_t* __restrict__ mask, float* __restrict__ go,
-                                                       int N, int ld, int H, int c_s, int mult, float rsq) {
+                                                       int N, int ld, int H, int c_s, int mult, float rsq,
+                                                       int mask_per_copy) {
   constexpr int KS = D + 4, VS = 36, KQ = D / 4;
   __shared__ __attribute__((aligned(16))) float ks[2][32][KS];
   __shared__ __attribute__((aligned(16))) float vs[2][D][VS];
@@ -364,7 +367,7 @@ __global__ __launch_bounds__(256) void attn_f32_kernel(const float* __restrict__
   const float* brow = bias + (((size_t)b * H + hd) * N + qi) * ld;
   const float* kbase = k + (size_t)bm * N * c_s + hd * D;
   const float* vtb = vt + ((size_t)bm * c_s + hd * D) * ld;
-  const uint8_t* mrow = mask + (size_t)b * N;
+  const uint8_t* mrow = mask + (size_t)(mask_per_copy ? bm : b) * N;
   // staging: thread tid moves K float4 (key tid / KQ, chunk tid % KQ) and
   // V^T float4 (channel tid / 8, keys 4 (tid % 8) ..), thread tid < 32 a mask byte
   const int sk_key = tid / KQ, sk_chunk = tid % KQ;
@@ -742,10 +745,10 @@ extern "C" int bioemu_apb_fwd_f32(const float* s, const float* z, const uint8_t*
     const float rsq = 1.0f / std::sqrt((float)d);
     if (d == 24)
       hipLaunchKernelGGL(attn_f32_kernel<24>, grid, dim3(256), 0, stream, buf.q, buf.k, buf.v, buf.g, buf.bias, mask,
-                         buf.go, (int)N, ldb, (int)H, (int)c_s, (int)mult, rsq);
+                         buf.go, (int)N, ldb, (int)H, (int)c_s, (int)mult, rsq, 0);
     else
       hipLaunchKernelGGL(attn_f32_kernel<32>, grid, dim3(256), 0, stream, buf.q, buf.k, buf.v, buf.g, buf.bias, mask,
-                         buf.go, (int)N, ldb, (int)H, (int)c_s, (int)mult, rsq);
+                         buf.go, (int)N, ldb, (int)H, (int)c_s, (int)mult, rsq, 0);
   }
   rc = check_launch("f32_attention");
   if (rc) return rc;
@@ -1453,4 +1456,127 @@ extern "C" int bioemu_distogram_fwd_f32(const float* z, const float* w, const fl
   if (rc) return rc;
   return gemm_f32(kGemmEpiStore, sym, w, nullptr, b, nullptr, out, B * N * N, (int)c_z, (int)num_bins, stream,
                   "f32_distogram");
+}
+
+// ---------------------------------------------------------------------------
+// Triangle attention in fp32 (AlphaFold3 suppl. Alg. 14/15 with the masking
+// of the reference's attention: a masked key's logit is replaced by -1e6).
+// Starting node: sequence (b, i) is the pair row z[b, i, :]; its queries and
+// keys are j, k along that row, bias[b][h][j][k] = LN(z[b, j, k]) . w_b[h]
+// (shared by every row i of batch b), key mask mask[b, i, k].  The ending node
+// runs the same on z^T and mask^T and transposes the gated attention output
+// back before the output projection, so its residual rows are z's own.
+// ---------------------------------------------------------------------------
+namespace bioemu {
+namespace {
+
+// dst[b][i][j][:] = src[b][j][i][:] for C fp32 channels (C % 4 == 0): one
+// thread per 16-byte chunk, consecutive threads along a destination row.
+__global__ __launch_bounds__(256) void transpose_pairs_f32_kernel(const float* __restrict__ src,
+                                                                  float* __restrict__ dst, int N, int C,
+                                                                  long long total) {
+  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (t >= total) return;
+  const int cq = C / 4;
+  const long long pair = t / cq;
+  const int q = (int)(t - pair * cq);
+  const long long nn = (long long)N * N;
+  const long long b = pair / nn, r = pair - b * nn;
+  const long long i = r / N, j = r - i * N;
+  const f32x4 v = *reinterpret_cast<const f32x4*>(src + ((b * N + j) * N + i) * C + 4 * q);
+  *reinterpret_cast<f32x4*>(dst + pair * C + 4 * q) = v;
+}
+
+// dst[b][i][j] = src[b][j][i] over B x N x N bytes.
+__global__ __launch_bounds__(256) void transpose_mask_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+                                                             int N, long long total) {
+  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (t >= total) return;
+  const long long nn = (long long)N * N;
+  const long long b = t / nn, r = t - b * nn;
+  const long long i = r / N, j = r - i * N;
+  dst[t] = src[(b * N + j) * N + i];
+}
+
+int transpose_pairs_f32(const float* src, float* dst, long long B, int N, int C, hipStream_t stream,
+                        const char* name) {
+  const long long total = B * N * N * (C / 4);
+  KernelTimerScope timed(name, stream);
+  hipLaunchKernelGGL(transpose_pairs_f32_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, src, dst,
+                     N, C, total);
+  return check_launch(name);
+}
+
+}  // namespace
+}  // namespace bioemu
+
+extern "C" size_t bioemu_triatt_f32_workspace_bytes(int64_t B, int64_t N, int64_t D, int64_t H) {
+  if (B <= 0 || N <= 0 || D <= 0 || H <= 0) return 0;
+  const int64_t P = B * N * N, ld = round_up(N, 32);
+  return (size_t)round_up(P * D * 4, 256) + (size_t)round_up(P, 256) +
+         attn_f32_layout(P, (int)D, B * N * D * ld, B * H * N * ld, true, nullptr, nullptr);
+}
+
+extern "C" int bioemu_triatt_fwd_f32(const float* z, const uint8_t* mask, const float* norm_w, const float* norm_b,
+                                     const float* w_proj, const float* w_o, float* out, void* workspace,
+                                     size_t workspace_bytes, int64_t B, int64_t N, int64_t D, int64_t H, int starting,
+                                     int residual, hipStream_t stream) {
+  if (H <= 0 || D % H || D / H != 32 || (D != 32 && D != 128))
+    return set_error(BIOEMU_ERR_UNSUPPORTED,
+                     "triatt_f32: supported are c = 32 or 128 with heads of 32 channels (got c=%lld H=%lld)",
+                     (long long)D, (long long)H);
+  if (B <= 0 || N <= 0 || B * N > 65535)
+    return set_error(BIOEMU_ERR_INVALID_ARG, "triatt_f32: bad shape B=%lld N=%lld (B * N <= 65535)", (long long)B,
+                     (long long)N);
+  if (!z || !mask || !norm_w || !norm_b || !w_proj || !w_o || !out || !workspace)
+    return set_error(BIOEMU_ERR_INVALID_ARG, "triatt_f32: null pointer argument");
+  if (!aligned16(z) || !aligned16(out) || !aligned16(w_proj) || !aligned16(w_o) || !aligned16(workspace))
+    return set_error(BIOEMU_ERR_INVALID_ARG, "triatt_f32: tensors must be 16-byte aligned");
+  if (out == z && !residual)
+    return set_error(BIOEMU_ERR_INVALID_ARG, "triatt_f32: out may alias z only with residual=1");
+  if (workspace_bytes < bioemu_triatt_f32_workspace_bytes(B, N, D, H))
+    return set_error(BIOEMU_ERR_WORKSPACE, "triatt_f32: workspace too small");
+  const long long P = B * N * N;
+  const int ld = (int)round_up(N, 32), c = (int)D;
+  char* p = static_cast<char*>(workspace);
+  float* zt = reinterpret_cast<float*>(p);
+  p += round_up(P * D * 4, 256);
+  uint8_t* mt = reinterpret_cast<uint8_t*>(p);
+  p += round_up(P, 256);
+  AttnF32Buffers buf;
+  attn_f32_layout(P, c, B * N * D * ld, B * H * N * ld, true, &buf, p);
+  const float* src = z;
+  const uint8_t* msk = mask;
+  int rc = 0;
+  if (!starting) {
+    if ((rc = transpose_pairs_f32(z, zt, B, (int)N, c, stream, "f32_triatt_transpose_in"))) return rc;
+    {
+      KernelTimerScope timed("f32_triatt_transpose_mask", stream);
+      hipLaunchKernelGGL(transpose_mask_kernel, dim3((unsigned)((P + 255) / 256)), dim3(256), 0, stream, mask, mt,
+                         (int)N, P);
+    }
+    if ((rc = check_launch("f32_triatt_transpose_mask"))) return rc;
+    src = zt;
+    msk = mt;
+  }
+  // w_proj rows: [Wq; Wk; Wv] (3c), Wg (c), Wb (H)
+  rc = attn_f32_projections(src, norm_w, norm_b, w_proj, nullptr, w_proj + 3 * D * D, buf, P, c, (int)N, ld, stream);
+  if (rc) return rc;
+  rc = pair_proj_f32(src, norm_w, norm_b, w_proj + 4 * D * D, buf.bias, P, (int)N, (int)N, ld, (int)H, c, stream,
+                     "f32_triatt_bias");
+  if (rc) return rc;
+  {
+    KernelTimerScope timed("f32_triatt_attention", stream);
+    const dim3 grid((unsigned)((N + 127) / 128), (unsigned)H, (unsigned)(B * N));
+    hipLaunchKernelGGL(attn_f32_kernel<32>, grid, dim3(256), 0, stream, buf.q, buf.k, buf.v, buf.g, buf.bias, msk,
+                       buf.go, (int)N, ld, (int)H, c, (int)N, 1.0f / std::sqrt(32.0f), 1);
+  }
+  if ((rc = check_launch("f32_triatt_attention"))) return rc;
+  const float* go = buf.go;
+  if (!starting) {
+    if ((rc = transpose_pairs_f32(buf.go, zt, B, (int)N, c, stream, "f32_triatt_transpose_out"))) return rc;
+    go = zt;
+  }
+  return gemm_f32(residual ? kGemmEpiResidual : kGemmEpiStore, go, w_o, nullptr, nullptr, z, out, P, c, c, stream,
+                  "f32_triatt_proj_o");
 }

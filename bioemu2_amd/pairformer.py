@@ -116,10 +116,47 @@ class PairformerBlockHip(nn.Module):
                                      tail=s_tail)
         return s, z
 
+    def workspace_bytes_f32(self, B: int, N: int) -> int:
+        return max(
+            _ops.trimul_f32_workspace_bytes(B, N, self.c_z),
+            _ops.triatt_f32_workspace_bytes(B, N, self.c_z, self.tri_att_start.num_heads),
+            _ops.apb_f32_workspace_bytes(B, 1, N, self.c_s, self.apb_heads),
+            _ops.transition_f32_workspace_bytes(B * N, self.c_s, self.transition_s.hidden),
+            _ops.transition_f32_workspace_bytes(B * N * N, self.c_z, self.transition_z.hidden),
+        )
+
+    @torch.no_grad()
+    def forward_f32_(self, s: Tensor, z: Tensor, token_mask: Tensor, ws: Tensor | None = None
+                     ) -> tuple[Tensor, Tensor]:
+        """In place on fp32 ``s [B,N,c_s]`` and ``z [B,N,N,c_z]`` in fp32 arithmetic (fp32 inputs with autocast
+        off), in the order of ``forward_``; ``ws``: at least ``workspace_bytes_f32(B, N)`` bytes."""
+        _ops.require_gpu(z, type(self).__name__)
+        B, N = token_mask.shape
+        if ws is None:
+            need = self.workspace_bytes_f32(B, N)
+            if self._ws is None or self._ws.numel() < need or self._ws.device != z.device:
+                self._ws = _ops.workspace(need, z.device)
+            ws = self._ws
+        tok, pm = pair_masks(token_mask)
+        _ops.launch_trimul_f32(z, pm, *self.tri_mul_out.prepared_params_f32(), z, True, residual=True, ws=ws)
+        _ops.launch_trimul_f32(z, pm, *self.tri_mul_in.prepared_params_f32(), z, False, residual=True, ws=ws)
+        heads = self.tri_att_start.num_heads
+        _ops.launch_triatt_f32(z, pm, *self.tri_att_start.prepared_params_f32(), z, True, heads, residual=True, ws=ws)
+        _ops.launch_triatt_f32(z, pm, *self.tri_att_end.prepared_params_f32(), z, False, heads, residual=True, ws=ws)
+        _ops.launch_transition_f32(z, *self.transition_z.prepared_params_f32(), z, residual=True, ws=ws)
+        _ops.launch_apb_f32(s, z, tok, *self.attention_pair_bias.prepared_params_f32(), s, self.apb_heads,
+                            residual=True, ws=ws)
+        _ops.launch_transition_f32(s, *self.transition_s.prepared_params_f32(), s, residual=True, ws=ws)
+        return s, z
+
     def forward(self, s: Tensor, z: Tensor, token_mask: Tensor) -> tuple[Tensor, Tensor]:
-        """Out-of-place block: returns new ``(s, z)`` in the input dtypes (streams carried with tails).  fp32
-        inputs need bf16 autocast (the block has no fp32 arithmetic)."""
-        _ops.require_mixed_precision(z, type(self).__name__)
+        """Out-of-place block: returns new ``(s, z)`` in the input dtypes.  fp32 inputs with autocast off compute
+        in fp32 throughout (``forward_f32_`` on copies); otherwise the bf16 path with the streams carried with
+        tails."""
+        _ops.require_gpu(z, type(self).__name__)
+        if _ops.fp32_mode(z):
+            s32, z32 = s.to(torch.float32).contiguous().clone(), z.contiguous().clone()
+            return self.forward_f32_(s32, z32, token_mask)
         (s_hi, s_tail), (z_hi, z_tail) = split_stream(s), split_stream(z)
         self.forward_(s_hi, z_hi, token_mask, s_tail, z_tail)
         return join_stream(s_hi, s_tail, s.dtype), join_stream(z_hi, z_tail, z.dtype)

@@ -33,20 +33,12 @@ class TriAttVariant(str, Enum):
 
 
 class _PackedTriAttParams(PreparedParams):
-    """norm fp32; [Wq; Wk; Wv; Wg; Wb] packed bf16; Wo bf16."""
+    """norm fp32; [Wq; Wk; Wv; Wg; Wb] packed and Wo in ``dtype`` (bf16, or fp32 for the fp32 path)."""
 
-    def __init__(self):
+    def __init__(self, dtype: torch.dtype = torch.bfloat16):
         super().__init__(
-            [
-                ("norm.weight", torch.float32),
-                ("norm.bias", torch.float32),
-                ("proj_q.weight", torch.bfloat16),
-                ("proj_k.weight", torch.bfloat16),
-                ("proj_v.weight", torch.bfloat16),
-                ("proj_g.weight", torch.bfloat16),
-                ("proj_b.weight", torch.bfloat16),
-                ("proj_o.weight", torch.bfloat16),
-            ]
+            [("norm.weight", torch.float32), ("norm.bias", torch.float32)]
+            + [(f"proj_{n}.weight", dtype) for n in ("q", "k", "v", "g", "b", "o")]
         )
 
     def get(self, module: nn.Module) -> tuple[Tensor, ...]:
@@ -63,8 +55,10 @@ class TriangleAttentionHip(nn.Module):
 
     ``forward(z [B,N,N,c], mask [B,N,N]) -> [B,N,N,c]`` returns the update
     (callers add the residual, as ``PairMixerLayer.forward`` does for its ops,
-    pairmixer.py:446-456).  bf16 operands, fp32 accumulation and softmax.
-    Supported: c = 128, 4 heads of 32.  Inference only.
+    pairmixer.py:446-456).  bf16 operands, fp32 accumulation and softmax; fp32
+    inputs with autocast off (the reference's fp32 mode) compute in fp32
+    throughout.  Supported: c = 128 with 4 heads of 32 (fp32: also c = 32, one
+    head).  Inference only.
     """
 
     def __init__(
@@ -93,15 +87,23 @@ class TriangleAttentionHip(nn.Module):
         self.proj_b = nn.Linear(c_z, num_heads, bias=False)
         self.proj_o = nn.Linear(hd, c_z, bias=False)
         self._prepared = _PackedTriAttParams()
+        self._prepared32 = _PackedTriAttParams(torch.float32)
 
     def prepared_params(self) -> tuple[Tensor, ...]:
         return self._prepared.get(self)
 
+    def prepared_params_f32(self) -> tuple[Tensor, ...]:
+        """The same packed parameters, all fp32, for the fp32 arithmetic path."""
+        return self._prepared32.get(self)
+
     def forward(self, z: Tensor, mask: Tensor) -> Tensor:
         _ops.require_gpu(z, type(self).__name__)
-        _ops.require_mixed_precision(z, type(self).__name__)
         if self.inf != 1e6:
             raise ValueError("TriangleAttentionHip: only inf=1e6 (the reference masking value) is supported")
+        if _ops.fp32_mode(z):
+            return torch.ops.bioemu_mi355x.triangle_attention_f32(
+                z, _ops.mask_u8(mask), *self.prepared_params_f32(), self.starting, self.num_heads
+            )
         return torch.ops.bioemu_mi355x.triangle_attention(
             z, _ops.mask_u8(mask), *self.prepared_params(), self.starting, self.num_heads
         )

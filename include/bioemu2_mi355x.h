@@ -384,6 +384,10 @@ int bioemu_msa_embed_fwd(const float* msa, const float* has_deletion, const floa
  *                            z_norm(z_init)), :266-273); dim and hidden multiples of 32.
  *   bioemu_distogram_fwd_f32 DistogramModule.forward (embedders.py:191-206) on fp32 z:
  *                            (z + z^T) W^T + b; c_z a multiple of 8, num_bins of 32.
+ *   bioemu_triatt_fwd_f32    triangle attention (no counterpart in the reference, as
+ *                            bioemu_triatt_fwd) in fp32: the arguments of bioemu_triatt_fwd
+ *                            as fp32 without res_tail; D = 32 or 128 with heads of 32
+ *                            channels, B * N <= 65535.
  * Residual tails do not apply (the stream is fp32).
  */
 size_t bioemu_apb_f32_workspace_bytes(int64_t B, int64_t mult, int64_t N, int64_t c_s, int64_t H);
@@ -442,6 +446,10 @@ size_t bioemu_distogram_f32_workspace_bytes(int64_t B, int64_t N, int64_t c_z);
 int bioemu_distogram_fwd_f32(const float* z, const float* w, const float* b, float* out, void* workspace,
                              size_t workspace_bytes, int64_t B, int64_t N, int64_t c_z, int64_t num_bins,
                              hipStream_t stream);
+size_t bioemu_triatt_f32_workspace_bytes(int64_t B, int64_t N, int64_t D, int64_t H);
+int bioemu_triatt_fwd_f32(const float* z, const uint8_t* mask, const float* norm_w, const float* norm_b,
+                          const float* w_proj, const float* w_o, float* out, void* workspace, size_t workspace_bytes,
+                          int64_t B, int64_t N, int64_t D, int64_t H, int starting, int residual, hipStream_t stream);
 
 #ifdef __cplusplus
 }

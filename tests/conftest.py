@@ -29,9 +29,8 @@ def gpu_device() -> torch.device:
 
 @pytest.fixture
 def bf16_autocast():
-    """bf16 autocast on the GPU for the test: the trunk ops and their compositions have no fp32 arithmetic and
-    refuse fp32 inputs outside autocast; under it (the reference trunk's policy) fp32 inputs take their bf16
-    path with fp32 in and out."""
+    """bf16 autocast on the GPU for the test: under it (the reference trunk's policy) fp32 inputs take the ops'
+    bf16 path with fp32 in and out; outside it they take the fp32 arithmetic path."""
     with torch.autocast("cuda", dtype=torch.bfloat16):
         yield
 

@@ -198,11 +198,15 @@ def test_trunk_48_blocks_config5(gpu_device):
     assert torch.equal(za, zb) and torch.equal(sa, sb)
 
 
-def test_block_fp32_outside_autocast_is_refused(gpu_device):
-    """The block has no fp32 arithmetic: fp32 inputs with autocast off raise instead of computing in bf16."""
+def test_block_precision_follows_autocast(gpu_device):
+    """fp32 inputs with autocast off take the fp32 path (no bf16 rounding of the streams: the result differs
+    from the bf16 path's); bf16 inputs with autocast off select the bf16 path explicitly."""
     blk = _block(gpu_device)
     s, z, tok = _inputs(32, 0, gpu_device)
+    s_mixed, z_mixed = blk(s, z, tok)                       # bf16 autocast (module fixture)
     with torch.autocast("cuda", enabled=False):
-        with pytest.raises(ValueError, match="autocast"):
-            blk(s, z, tok)
-        blk(s.to(torch.bfloat16), z.to(torch.bfloat16), tok)   # bf16 inputs select the bf16 path explicitly
+        s32, z32 = blk(s, z, tok)
+        s16, z16 = blk(s.to(torch.bfloat16), z.to(torch.bfloat16), tok)
+    assert s32.dtype == torch.float32 and z16.dtype == torch.bfloat16
+    assert not torch.equal(z32, z_mixed)
+    assert torch.equal(z16, z_mixed.to(torch.bfloat16)) and torch.equal(s16, s_mixed.to(torch.bfloat16))

@@ -551,3 +551,82 @@ def test_distogram_f32_matches_oracle(gpu_device):
     mod = randomize_params(DistogramModule(128, 64), 5).to(gpu_device).eval()
     got = mod(z.to(gpu_device))
     _check(got.cpu(), oracle.distogram(z, state(mod)), "distogram_f32")
+
+
+# ----------------------------------------------------------------------------
+# Triangle attention and the Pairformer block
+# ----------------------------------------------------------------------------
+def _triatt(starting, device, c=128, H=4, seed=7):
+    from bioemu2_amd.triangle_attention import TriangleAttentionHip
+
+    torch.manual_seed(seed)
+    return randomize_params(TriangleAttentionHip(c, H, starting=starting), seed).to(device).eval()
+
+
+@pytest.mark.parametrize("starting", [True, False])
+@pytest.mark.parametrize("B,n,c,H", [(1, 16, 128, 4), (2, 37, 128, 4), (1, 100, 128, 4), (2, 45, 32, 1)])
+def test_triatt_f32_matches_oracle(gpu_device, starting, B, n, c, H):
+    """Random pair mask with one fully masked sequence (uniform weights over its keys, as the reference's
+    finite -1e6 fill gives)."""
+    m = _triatt(starting, gpu_device, c, H)
+    g = torch.Generator().manual_seed(n)
+    z = torch.randn(B, n, n, c, generator=g)
+    mask = torch.rand(B, n, n, generator=g) < 0.8
+    mask[0, 3, :] = False
+    mask[0, :, 5] = False
+    with torch.no_grad():
+        got = m(z.to(gpu_device), mask.to(gpu_device)).cpu()
+    want = oracle.triangle_attention(z, mask, state(m), H, starting)
+    _check(got, want, f"triatt_f32 starting={starting} B={B} n={n} c={c}")
+
+
+@pytest.mark.parametrize("starting", [True, False])
+def test_triatt_f32_padding_and_residual(gpu_device, starting):
+    """Token padding leaves the valid outputs bit-identical (padded keys weigh exactly 0), and the fused
+    residual is z + update with one fp32 add."""
+    d = gpu_device
+    m = _triatt(starting, d)
+    n, pad = 40, 9
+    g = torch.Generator().manual_seed(1)
+    z = torch.randn(1, n, n, 128, generator=g)
+    tok = torch.ones(1, n + pad, dtype=torch.bool)
+    tok[:, n:] = False
+    pm = oracle.pair_mask_from_token_mask(tok)
+    zp = torch.full((1, n + pad, n + pad, 128), 1000.0)
+    zp[:, :n, :n] = z
+    P = m.prepared_params_f32()
+    with torch.no_grad():
+        a = m(z.to(d), pm[:, :n, :n].to(d))
+        b = m(zp.to(d), pm.to(d))[:, :n, :n]
+        assert torch.equal(a, b)
+        zz = z.to(d).clone()
+        _ops.launch_triatt_f32(zz, _ops.mask_u8(pm[:, :n, :n].to(d)), *P, zz, starting, residual=True)
+    assert torch.equal(zz, z.to(d) + a)
+
+
+def test_triatt_f32_rejects_bad_heads(gpu_device):
+    m = _triatt(True, gpu_device, 128, 8)   # heads of 16 channels
+    with pytest.raises(ValueError):
+        m(torch.zeros(1, 8, 8, 128, device=gpu_device), torch.ones(1, 8, 8, dtype=torch.bool, device=gpu_device))
+
+
+@pytest.mark.parametrize("n,n_pad", [(24, 0), (50, 7)])
+def test_pairformer_block_f32_matches_oracle(gpu_device, n, n_pad):
+    """The whole block with autocast off: TriMul out/in, triangle attention start/end, both transitions and
+    attention with pair bias, each in fp32, against the oracle composition at the fp32 bound."""
+    from bioemu2_amd.pairformer import PairformerBlockHip
+
+    d = gpu_device
+    torch.manual_seed(0)
+    blk = randomize_params(PairformerBlockHip(), 3).to(d).eval()
+    g = torch.Generator().manual_seed(n)
+    z = torch.randn(1, n, n, 128, generator=g)
+    s = torch.randn(1, n, 384, generator=g)
+    tok = torch.ones(1, n, dtype=torch.bool)
+    if n_pad:
+        tok[:, n - n_pad:] = False
+    s_got, z_got = blk(s.to(d), z.to(d), tok.to(d))
+    s_want, z_want = oracle.pairformer_block(s, z, tok, state(blk))
+    pm = oracle.pair_mask_from_token_mask(tok)
+    _check(z_got.cpu()[pm], z_want[pm], f"pairformer_block_f32 n={n} z")
+    _check(s_got.cpu()[tok], s_want[tok], f"pairformer_block_f32 n={n} s")
