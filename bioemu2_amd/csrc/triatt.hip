@@ -578,93 +578,150 @@ void triatt_flash_kernel(
         const bf16x8 ka0 = load8(ks + t_off(krow, 2 * hh)), ka1 = load8(ks + kTile + t_off(krow, 2 * hh));
         const bf16x8 kb0 = load8(ks + t_off(krow, 2 * hh + 1)), kb1 = load8(ks + kTile + t_off(krow, 2 * hh + 1));
         // Logits minus the running max m, all on MFMA (no shift unless m is
-        // set; the rank-2 product only when there is a mask or a shift), for
-        // both query tiles before any softmax work so that one tile's
-        // exponentials overlap the other tile's matrix products.
+        // set; the rank-2 product only when there is a mask or a shift).
+        //
+        // Instruction order.  This chip overlaps a wave's VALU work with its
+        // own MFMAs in flight, not with another wave's, so the block is laid
+        // out as segments fenced by sched_barrier, each pairing MFMAs with
+        // independent VALU work of the same wave:
+        //   A: tile 0's logit MFMAs;
+        //   B: tile 1's logit MFMAs, each with a share of tile 0's weights
+        //      (exp2 of the logits as they are: the fast path, computed before
+        //      it is known to apply and recomputed by the slow path if not);
+        //   C: tile 0's P.V MFMAs with a share of tile 1's weights;
+        //   D: tile 1's P.V MFMAs.
+        static_assert(kFlashTiles == 2, "the segment layout pairs two query tiles");
         f32x16 s[kFlashTiles][2];
-#pragma unroll
-        for (int t = 0; t < kFlashTiles; ++t) {
-          if (compute) {
+        bf16x8 pa[kFlashTiles][2], pb[kFlashTiles][2];
+        // the j-th logit MFMA of tile t (0-3: q.k, 4-7: bias)
+        auto logit_mfma = [&](int t, int j) {
+          switch (j) {
+            case 0: s[t][0] = mfma32(ka0, qf[t][0], zero16()); break;
+            case 1: s[t][1] = mfma32(ka1, qf[t][0], zero16()); break;
+            case 2: s[t][0] = mfma32(kb0, qf[t][1], s[t][0]); break;
+            case 3: s[t][1] = mfma32(kb1, qf[t][1], s[t][1]); break;
+            case 4: s[t][0] = mfma32(ident[0], bias[t][0], s[t][0]); break;
+            case 5: s[t][1] = mfma32(ident[0], bias[t][2], s[t][1]); break;
+            case 6: s[t][0] = mfma32(ident[1], bias[t][1], s[t][0]); break;
+            default: s[t][1] = mfma32(ident[1], bias[t][3], s[t][1]); break;
+          }
+        };
+        auto mask_shift = [&](int t) {
+          if (m_set[t] || need_mask) {
             bf16x8 qs = qm[t];
             if (!m_set[t]) qs[1] = f2bf(0.f);
-            s[t][0] = mfma32(ka0, qf[t][0], zero16());
-            s[t][1] = mfma32(ka1, qf[t][0], zero16());
-            s[t][0] = mfma32(kb0, qf[t][1], s[t][0]);
-            s[t][1] = mfma32(kb1, qf[t][1], s[t][1]);
-            s[t][0] = mfma32(ident[0], bias[t][0], s[t][0]);
-            s[t][1] = mfma32(ident[0], bias[t][2], s[t][1]);
-            s[t][0] = mfma32(ident[1], bias[t][1], s[t][0]);
-            s[t][1] = mfma32(ident[1], bias[t][3], s[t][1]);
-            if (m_set[t] || need_mask) {
-              s[t][0] = mfma32(km0, qs, s[t][0]);
-              s[t][1] = mfma32(km1, qs, s[t][1]);
-            }
+            s[t][0] = mfma32(km0, qs, s[t][0]);
+            s[t][1] = mfma32(km1, qs, s[t][1]);
           }
-          bload(hn, kn, t, bias[t]);
+        };
+        // fast-path weights of tile t, part j of 8: four values of pa (j < 4) or
+        // pb.  The empty asm pins them to this segment (left alone, the
+        // optimizer sinks the pure exponentials to their first use).
+        auto exp_part = [&](int t, int j) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int u = 4 * (j & 3) + e;
+            if (j < 4)
+              pa[t][u >> 3][u & 7] = f2bf(fast_exp2(s[t][0][u]));
+            else
+              pb[t][u >> 3][u & 7] = f2bf(fast_exp2(s[t][1][u]));
+          }
+          bf16x8& done = j < 4 ? pa[t][(j & 3) >> 1] : pb[t][(j & 3) >> 1];
+          asm volatile("" : "+v"(done));
+        };
+        bf16x8 vf[4];   // V^T fragments of the block (shared by both tiles)
+        auto pv_mfma = [&](int t, int j) {
+          o[t] = mfma32(vf[j], j < 2 ? pa[t][j & 1] : pb[t][j & 1], o[t]);
+        };
+        // Weight sum of tile t; a block sum above 2^16 may hold a weight above
+        // 2^16 (then m moves: rare), and a fresh tile has no shift yet: both
+        // take the slow path, which recomputes the weights.
+        auto finish = [&](int t) {
+          f32x16& s0 = s[t][0];
+          f32x16& s1 = s[t][1];
+          float psum = sum8_bf16(pa[t][1], sum8_bf16(pa[t][0], 0.f)) + sum8_bf16(pb[t][1], sum8_bf16(pb[t][0], 0.f));
+          if (fresh[t] || __any(psum > kSlackSum)) {
+            // s0, s1 hold the logits minus `shift` (the MFMA subtracts m
+            // once m is set).  Everything here works on those shifted values,
+            // so the fast path never needs the unshifted logits.
+            const float shift = m_set[t] ? m[t] : 0.f;
+            float bmax = fmaxf(s0[0], s1[0]);
+#pragma unroll
+            for (int u = 1; u < 16; ++u) bmax = __builtin_fmaxf(bmax, __builtin_fmaxf(s0[u], s1[u]));
+            bmax = fmaxf(bmax, __shfl_xor(bmax, 32)) + shift;
+            float delta = 0.f;
+            if (fresh[t] && __all(bmax >= -64.f && bmax <= 16.f)) {
+              // unshifted from here on: every weight is at most 2^16 until a
+              // block sum says otherwise, and each row keeps a weight of at
+              // least 2^-64 (nothing is accumulated yet)
+              fresh[t] = false;
+            } else {
+              // The shift is kept bf16-representable: it enters the MFMA as -m.
+              // Leaving the unshifted mode, the running max is at least -64.
+              const float floor_m = m_set[t] ? m[t] : fresh[t] ? -INFINITY : -64.f;
+              const float m_new = bf2f(f2bf(fmaxf(floor_m, bmax)));
+              const float alpha = fresh[t] ? 0.f : fast_exp2(shift - m_new);
+              delta = m_new - shift;
+              m[t] = m_new;
+              l[t] *= alpha;
+#pragma unroll
+              for (int u = 0; u < 16; ++u) o[t][u] *= alpha;
+              // a block of masked keys only (logits ~ -1e30) does not set m
+              m_set[t] = m_set[t] || __all(m[t] > -1e29f);
+              fresh[t] = fresh[t] && !m_set[t];
+              if (hh == 0) qm[t][1] = f2bf(-m[t]);
+            }
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+              pa[t][u >> 3][u & 7] = f2bf(fast_exp2(s0[u] - delta));
+              pb[t][u >> 3][u & 7] = f2bf(fast_exp2(s1[u] - delta));
+            }
+            psum = sum8_bf16(pa[t][1], sum8_bf16(pa[t][0], 0.f)) + sum8_bf16(pb[t][1], sum8_bf16(pb[t][0], 0.f));
+          }
+          l[t] += psum;
+        };
+        if (compute) {
+          // A
+#pragma unroll
+          for (int j = 0; j < 8; ++j) logit_mfma(0, j);
+          mask_shift(0);
         }
+        bload(hn, kn, 0, bias[0]);
+        if (compute) {
+          // B
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            logit_mfma(1, j);
+            exp_part(0, j);
+            if (j == 7) {
+              vf[0] = load8(vs + t_off(krow, 2 * hh));
+              vf[1] = load8(vs + t_off(krow, 2 * hh + 1));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+          }
+          mask_shift(1);
+        }
+        bload(hn, kn, 1, bias[1]);
         if (ib + 1 == nact && hd + 1 < H) qload(hd + 1);
         if (compute) {
+          finish(0);
+          // C
+          __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-          for (int t = 0; t < kFlashTiles; ++t) {
-            f32x16& s0 = s[t][0];
-            f32x16& s1 = s[t][1];
-            bf16x8 pa[2], pb[2];
-            float psum;
-            bool slow = fresh[t];
-            if (!slow) {
-#pragma unroll
-              for (int u = 0; u < 16; ++u) {
-                pa[u >> 3][u & 7] = f2bf(fast_exp2(s0[u]));
-                pb[u >> 3][u & 7] = f2bf(fast_exp2(s1[u]));
-              }
-              psum = sum8_bf16(pa[1], sum8_bf16(pa[0], 0.f)) + sum8_bf16(pb[1], sum8_bf16(pb[0], 0.f));
-              // a sum above 2^16 may hold a weight above 2^16: move m (rare)
-              slow = __any(psum > kSlackSum);
+          for (int j = 0; j < 8; ++j) {
+            if (j == 0) {
+              vf[2] = load8(vs + kTile + t_off(krow, 2 * hh));
+              vf[3] = load8(vs + kTile + t_off(krow, 2 * hh + 1));
             }
-            if (slow) {
-              // s0, s1 hold the logits minus `shift` (the MFMA subtracts m
-              // once m is set).  Everything here works on those shifted values,
-              // so the fast path above never needs the unshifted logits.
-              const float shift = m_set[t] ? m[t] : 0.f;
-              float bmax = fmaxf(s0[0], s1[0]);
-#pragma unroll
-              for (int u = 1; u < 16; ++u) bmax = __builtin_fmaxf(bmax, __builtin_fmaxf(s0[u], s1[u]));
-              bmax = fmaxf(bmax, __shfl_xor(bmax, 32)) + shift;
-              float delta = 0.f;
-              if (fresh[t] && __all(bmax >= -64.f && bmax <= 16.f)) {
-                // unshifted from here on: every weight is at most 2^16 until a
-                // block sum says otherwise, and each row keeps a weight of at
-                // least 2^-64 (nothing is accumulated yet)
-                fresh[t] = false;
-              } else {
-                // The shift is kept bf16-representable: it enters the MFMA as -m.
-                // Leaving the unshifted mode, the running max is at least -64.
-                const float floor_m = m_set[t] ? m[t] : fresh[t] ? -INFINITY : -64.f;
-                const float m_new = bf2f(f2bf(fmaxf(floor_m, bmax)));
-                const float alpha = fresh[t] ? 0.f : fast_exp2(shift - m_new);
-                delta = m_new - shift;
-                m[t] = m_new;
-                l[t] *= alpha;
-#pragma unroll
-                for (int u = 0; u < 16; ++u) o[t][u] *= alpha;
-                // a block of masked keys only (logits ~ -1e30) does not set m
-                m_set[t] = m_set[t] || __all(m[t] > -1e29f);
-                fresh[t] = fresh[t] && !m_set[t];
-                if (hh == 0) qm[t][1] = f2bf(-m[t]);
-              }
-#pragma unroll
-              for (int u = 0; u < 16; ++u) {
-                pa[u >> 3][u & 7] = f2bf(fast_exp2(s0[u] - delta));
-                pb[u >> 3][u & 7] = f2bf(fast_exp2(s1[u] - delta));
-              }
-              psum = sum8_bf16(pa[1], sum8_bf16(pa[0], 0.f)) + sum8_bf16(pb[1], sum8_bf16(pb[0], 0.f));
-            }
-            l[t] += psum;
-            o[t] = mfma32(load8(vs + t_off(krow, 2 * hh)), pa[0], o[t]);
-            o[t] = mfma32(load8(vs + t_off(krow, 2 * hh + 1)), pa[1], o[t]);
-            o[t] = mfma32(load8(vs + kTile + t_off(krow, 2 * hh)), pb[0], o[t]);
-            o[t] = mfma32(load8(vs + kTile + t_off(krow, 2 * hh + 1)), pb[1], o[t]);
+            if ((j & 1) == 0) pv_mfma(0, j >> 1);
+            exp_part(1, j);
+            __builtin_amdgcn_sched_barrier(0);
           }
+          finish(1);
+          // D
+#pragma unroll
+          for (int j = 0; j < 4; ++j) pv_mfma(1, j);
         }
       }
       lstore(st ^ 1);
