@@ -165,6 +165,22 @@ __global__ __launch_bounds__(kProjThreads) void opm_proj_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// proj_o weight in MFMA A-operand fragment order: fragment (eb, ks) of 32
+// output rows x 16 inputs is 1 KB contiguous, lane (n, h) holding
+// W_o[eb * 32 + perm32(n)][16 ks + 8 h + 0..7], so that each fragment load of
+// the fused kernel's epilogue reads whole cache lines.
+// ---------------------------------------------------------------------------
+constexpr int kWoFrags = (COUT / 32) * (CH2 / 16) * 64;   // 16-byte slots
+
+__global__ __launch_bounds__(256) void opm_wo_tiles_kernel(const bf16* __restrict__ w_o, bf16* __restrict__ wt) {
+  const int f = blockIdx.x * 256 + threadIdx.x;
+  if (f >= kWoFrags) return;
+  const int lane = f & 63, ks = (f >> 6) % (CH2 / 16), eb = f / (64 * (CH2 / 16));
+  const int n = lane & 31, h = lane >> 5;
+  store8(wt + (size_t)f * 8, load8(w_o + (size_t)(eb * 32 + perm32(n)) * CH2 + 16 * ks + 8 * h));
+}
+
+// ---------------------------------------------------------------------------
 // Fused contraction + mean + output projection.
 // ---------------------------------------------------------------------------
 constexpr int kFusedThreads = 512;
@@ -175,7 +191,7 @@ constexpr int kFusedSmem = kNtSmem > kFusedSmemB ? kNtSmem : kFusedSmemB;
 
 __global__ __launch_bounds__(kFusedThreads) void opm_fused_kernel(
     const bf16* __restrict__ aT, const bf16* __restrict__ bT, const int* __restrict__ count, int mean_rows,
-    const bf16* __restrict__ w_o, const float* __restrict__ b_o, const bf16* zres, bf16* out, int8_t* tail, int N, int Nt, int Sp) {
+    const bf16* __restrict__ w_t, const float* __restrict__ b_o, const bf16* zres, bf16* out, int8_t* tail, int N, int Nt, int Sp) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   bf16* stage = reinterpret_cast<bf16*>(smem);
   bf16* xb = reinterpret_cast<bf16*>(smem);
@@ -219,15 +235,27 @@ __global__ __launch_bounds__(kFusedThreads) void opm_fused_kernel(
       for (int u = 0; u < 16; ++u) v[u] = acc[jb][ib][u] * inv;
       store16(xb + (ii * TJ + jj) * LDX + c * CH + 16 * h, v);
     }
-  __syncthreads();
 
-  // out^T[e][pair] = Wo[e][:] . xb[pair][:] ; wave -> (e block, pair block)
+  // out^T[e][pair] = Wo[e][:] . xb[pair][:] ; wave -> (e block, pair block).
+  // The weight fragments come from L2 (1 KB each, pre-tiled), kPf in flight;
+  // the first kPf are requested before the barrier that publishes xb.
   const int eb = wave & 3, pb = wave >> 2;
+  const bf16* wfr = w_t + ((size_t)eb * (CH2 / 16) * 64 + lane) * 8;   // fragment ks at wfr + 512 ks
+  constexpr int kPf = 32, kSteps = CH2 / 16;
+  bf16x8 wq[kPf];
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int q = 0; q < kPf; ++q) wq[q] = load8(wfr + 512 * q);
+  __syncthreads();
   f32x16 y = zero16();
-  const bf16* wrow = w_o + (size_t)(eb * 32 + perm32(n)) * CH2 + 8 * h;
   const bf16* xrow = xb + (pb * 32 + n) * LDX + 8 * h;
-#pragma unroll 8
-  for (int k = 0; k < CH2; k += 16) y = mfma32(load8(wrow + k), load8(xrow + k), y);
+#pragma unroll
+  for (int ks = 0; ks < kSteps; ++ks) {
+    const bf16x8 wc = wq[ks % kPf];
+    if (ks + kPf < kSteps) wq[ks % kPf] = load8(wfr + 512 * (ks + kPf));
+    y = mfma32(wc, load8(xrow + 16 * ks), y);
+    __builtin_amdgcn_sched_barrier(0);   // keeps each load kPf steps ahead of its use
+  }
   const int p = pb * 32 + n, ii = p / TJ, jj = p % TJ;
   const int i = i0 + ii, j = j0 + jj;
   if (i >= N || j >= N) return;
@@ -259,19 +287,22 @@ struct OpmLayout {
   int* count;
   bf16* aT;
   bf16* bT;
+  bf16* wt;   // proj_o weight in fragment order
 };
 
 size_t opm_layout(int64_t B, int64_t S, int64_t N, OpmLayout* L, char* base) {
   const size_t Nt = (size_t)round_up(N, 8), Sp = (size_t)round_up(S, 64);
   const size_t idx_b = round_up((size_t)B * S * 4, 256), cnt_b = round_up((size_t)B * 4, 256);
   const size_t ab_b = round_up((size_t)B * Nt * CH * Sp * 2, 256);
+  const size_t wt_b = (size_t)kWoFrags * 16;
   if (L) {
     L->idx = reinterpret_cast<int*>(base);
     L->count = reinterpret_cast<int*>(base + idx_b);
     L->aT = reinterpret_cast<bf16*>(base + idx_b + cnt_b);
     L->bT = reinterpret_cast<bf16*>(base + idx_b + cnt_b + ab_b);
+    L->wt = reinterpret_cast<bf16*>(base + idx_b + cnt_b + 2 * ab_b);
   }
-  return idx_b + cnt_b + 2 * ab_b;
+  return idx_b + cnt_b + 2 * ab_b + wt_b;
 }
 
 }  // namespace
@@ -331,6 +362,13 @@ extern "C" int bioemu_opm_fwd(const void* m, const uint8_t* mask, int mean_rows,
   rc = check_launch("opm_proj");
   if (rc) return rc;
 
+  {
+    KernelTimerScope timed("opm_wo_tiles", stream);
+    hipLaunchKernelGGL(opm_wo_tiles_kernel, dim3((kWoFrags + 255) / 256), dim3(256), 0, stream,
+                       static_cast<const bf16*>(w_o), L.wt);
+  }
+  rc = check_launch("opm_wo_tiles");
+  if (rc) return rc;
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(opm_fused_kernel),
                           hipFuncAttributeMaxDynamicSharedMemorySize, kFusedSmem) != hipSuccess)
     return set_error(BIOEMU_ERR_LAUNCH, "opm_fused: cannot set dynamic LDS size");
@@ -338,7 +376,7 @@ extern "C" int bioemu_opm_fwd(const void* m, const uint8_t* mask, int mean_rows,
   {
     KernelTimerScope timed("opm_fused", stream);
     hipLaunchKernelGGL(opm_fused_kernel, g3, dim3(kFusedThreads), kFusedSmem, stream, L.aT, L.bT, L.count, mean_rows,
-                       static_cast<const bf16*>(w_o), b_o, static_cast<const bf16*>(z_res), static_cast<bf16*>(out),
+                       L.wt, b_o, static_cast<const bf16*>(z_res), static_cast<bf16*>(out),
                        res_tail, (int)N, (int)Nt, (int)Sp);
   }
   return check_launch("opm_fused");
