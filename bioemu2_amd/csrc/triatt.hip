@@ -200,6 +200,37 @@ __global__ __launch_bounds__(kProjThreads) void triatt_proj_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Weights of the attention kernel's own projections in MFMA A-operand
+// fragment order: fragment f of 32 weight rows x 16 inputs is 1 KB contiguous
+// (lane l at bytes 16 l), so each fragment load reads whole cache lines.
+//   f = 0 .. 31   q rows, LayerNorm gamma folded in: block hd = f / 8, k-step
+//                 s = f % 8, lane (n, hh) holds W'q[hd*32 + perm32(n)][16 s + 8 hh + 0..7]
+//   f = 32 .. 63  g rows, folded: W'g[hd*32 + perm32(n)][32 (s >> 1) + 16 hh + 8 (s & 1) + 0..7]
+//   f = 64 .. 95  Wo: Wo[cb*32 + perm32(n)][32 (s >> 1) + 16 hh + 8 (s & 1) + 0..7]
+// The folded values are W * gamma rounded to bf16, bit for bit the fold of the
+// projection rows.
+// ---------------------------------------------------------------------------
+constexpr int kFragCount = 96;
+constexpr int kFragElems = kFragCount * 64 * 8;
+
+__global__ __launch_bounds__(256) void triatt_frag_kernel(const bf16* __restrict__ w_proj,
+                                                          const float* __restrict__ gamma,
+                                                          const bf16* __restrict__ w_o, bf16* __restrict__ wt) {
+  const int slot = blockIdx.x * 256 + threadIdx.x;   // 16-byte slot
+  if (slot >= kFragCount * 64) return;
+  const int f = slot >> 6, lane = slot & 63, n = lane & 31, hh = lane >> 5;
+  const int kind = f >> 5, blk = (f >> 3) & 3, s = f & 7;
+  const int row = blk * 32 + perm32(n);
+  const int c0 = kind == 0 ? 16 * s + 8 * hh : 32 * (s >> 1) + 16 * hh + 8 * (s & 1);
+  const bf16* src = kind == 2 ? w_o + (size_t)row * C : w_proj + (size_t)((kind == 0 ? kRowQ : kRowG) + row) * C;
+  const bf16x8 w = load8(src + c0);
+  bf16x8 o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = kind == 2 ? w[e] : f2bf(bf2f(w[e]) * gamma[c0 + e]);
+  store8(wt + (size_t)slot * 8, o);
+}
+
+// ---------------------------------------------------------------------------
 // Flash attention kernel.  Workgroup = (b, frame row i, 256 queries); wave w
 // owns the kFlashTiles = 2 32-query tiles q0 and q0 + 32, q0 = 256 qb + 64 w,
 // which share every K / V fragment the wave reads from LDS.
@@ -261,14 +292,14 @@ __device__ __forceinline__ int t_off(int r, int chunk) { return r * TLD + ((chun
 
 // With kTail the residual stream z carries an int8 tail plane (common.h),
 // read with z and rewritten with out (in place).
-// wf / cf: the packed projection with the LayerNorm folded in (rows
-// [q | k | v | g | bias], fold.hip), of which this kernel uses the q and g
-// rows; z is read for the query side, the gate and the residual (z = zres;
+// wt: the q and g rows of the packed projection (LayerNorm folded in) and Wo
+// in fragment order (triatt_frag_kernel); cf: the folded projection's bias
+// pairs (fold.hip), of which this kernel uses the q and g rows; z is read for the query side, the gate and the residual (z = zres;
 // out may alias it: every workgroup reads and writes only its own pairs).
 template <bool kStarting, bool kTail>
 __global__ __launch_bounds__(kFlashThreads) __attribute__((amdgpu_waves_per_eu(kFlashWavesPerEu, kFlashWavesPerEu)))
 void triatt_flash_kernel(
-    TriAttBuffers buf, const bf16* __restrict__ wf, const bf16* __restrict__ cf, const bf16* __restrict__ wo,
+    TriAttBuffers buf, const bf16* __restrict__ wt, const bf16* __restrict__ cf,
     const bf16* zres, bf16* out, int8_t* tail, int N, int Np, int residual, int nitems) {
   __shared__ __attribute__((aligned(16))) bf16 smem[2 * kStage];
   // H - 1 slots of [kFlashQueries][DH] bf16: slot s holds q of head s + 1 (times
@@ -456,15 +487,14 @@ void triatt_flash_kernel(
       normalize_half_row(v, q < N, xq[t]);
       xbq[t] = bias_step_x(q < N, hh);
     }
-    const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(wf, (unsigned)kProjRows * C * 2);
-    const unsigned wq_voff = (unsigned)(perm32(n) * C + 8 * hh) * 2;
+    const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(wt, (unsigned)kFragElems * 2);
 #pragma unroll 1
     for (int hd = 0; hd < H; ++hd) {
       const int r = kRowQ + hd * DH + perm32(n);
       bf16x8 wq[8], wb = zero8;
 #pragma unroll
       for (int s2 = 0; s2 < 8; ++s2)
-        wq[s2] = buffer_load8(wrs, wq_voff + 32 * s2, (unsigned)(kRowQ + hd * DH) * C * 2);
+        wq[s2] = buffer_load8(wrs, (unsigned)lane * 16, (unsigned)(hd * 8 + s2) * 1024);
       if (hh == 0) {
         wb[0] = cf[2 * r];
         wb[1] = cf[2 * r + 1];
@@ -757,26 +787,21 @@ void triatt_flash_kernel(
   // Epilogue, per 32-query tile.  Lane (n, hh) loads the z row of query
   // q0 + 32 t + n in the update's layout (channels 32 cb + 16 hh + 0..15,
   // cb = 0..3): the residual, and normalised (affine-free, gamma and beta
-  // folded into the g rows of wf / cf) the gate's input, whose k-step
-  // s2 = 2 cb + j carries channels 32 cb + 16 h + 8 j + e on both operands.
-  // g = sigmoid(LN(z) Wg^T) times o / l per head is the B operand of
-  // update^T = Wo (g o)^T; the residual is added and the result stored in z's
-  // frame.  Weight fragments are read per block (L2-resident) to keep the
-  // register budget; lanes of queries past N read pair 0 and store nothing.
-  // Weight fragments through buffer resources: lane (n, hh) reads row
-  // perm32(n) of a 32-row block at channel 16 hh + 32 (s2 >> 1) + 8 (s2 & 1);
-  // the block is a wave-uniform offset.
-  const unsigned we_voff = (unsigned)(perm32(n) * C + 16 * hh) * 2;
+  // folded into the g rows of the fragment copy / cf) the gate's input, whose
+  // k-step s2 = 2 cb + j carries channels 32 cb + 16 h + 8 j + e on both
+  // operands.  g = sigmoid(LN(z) Wg^T) times o / l per head is the B operand
+  // of update^T = Wo (g o)^T; the residual is added and the result stored in
+  // z's frame.  Weight fragments (1 KB each, in fragment order: wt) are read
+  // per block from L2 to keep the register budget; lanes of queries past N
+  // read pair 0 and store nothing.
 #pragma unroll
   for (int t = 0; t < kFlashTiles; ++t) {
     // Opaque copies of the weight pointers: the fragments are loop-invariant,
     // and hoisted out of this loop (64 of them) they would not fit the
     // register budget.
-    const bf16* wfe = wf;
-    const bf16* woe = wo;
-    asm volatile("" : "+s"(wfe), "+s"(woe));
-    const __amdgpu_buffer_rsrc_t wgrs = buffer_rsrc(wfe, (unsigned)kProjRows * C * 2);
-    const __amdgpu_buffer_rsrc_t wors = buffer_rsrc(woe, (unsigned)C * C * 2);
+    const bf16* wte = wt;
+    asm volatile("" : "+s"(wte));
+    const __amdgpu_buffer_rsrc_t wtrs = buffer_rsrc(wte, (unsigned)kFragElems * 2);
     const int q = q0 + 32 * t + n;
     const bool store = q < N;
     const size_t zpair = zpair_of(q);
@@ -822,8 +847,7 @@ void triatt_flash_kernel(
       f32x16 acc = zero16();
 #pragma unroll
       for (int s2 = 0; s2 < 8; ++s2)
-        acc = mfma32(buffer_load8(wgrs, we_voff + (32 * (s2 >> 1) + 8 * (s2 & 1)) * 2, (unsigned)(kRowG + hd * DH) * C * 2),
-                     xg[s2], acc);
+        acc = mfma32(buffer_load8(wtrs, (unsigned)lane * 16, (unsigned)(32 + hd * 8 + s2) * 1024), xg[s2], acc);
       bf16x8 wb = zero8;
       if (hh == 0) {
         wb[0] = cf[2 * r];
@@ -854,8 +878,7 @@ void triatt_flash_kernel(
       f32x16 acc = zero16();
 #pragma unroll
       for (int s2 = 0; s2 < 8; ++s2)
-        acc = mfma32(buffer_load8(wors, we_voff + (32 * (s2 >> 1) + 8 * (s2 & 1)) * 2, (unsigned)(cb * 32) * C * 2),
-                     gob[s2], acc);
+        acc = mfma32(buffer_load8(wtrs, (unsigned)lane * 16, (unsigned)(64 + cb * 8 + s2) * 1024), gob[s2], acc);
       if (store) {
         const size_t off = zpair * C + cb * 32 + 16 * hh;
         float v[16];
@@ -895,7 +918,7 @@ extern "C" size_t bioemu_triatt_workspace_bytes(int64_t B, int64_t N, int64_t Dc
   const size_t pairs = (size_t)B * Np * Np;
   // k, v^T (bf16 x C each) + bias (bf16 x H) + mask (u8), each 256-byte aligned
   return round_up(pairs * C * 2, 256) * 2 + round_up(pairs * H * 2, 256) + round_up(pairs, 256) +
-         fold_bytes(kProjRows);
+         fold_bytes(kProjRows) + (size_t)kFragElems * 2;
 }
 
 extern "C" int bioemu_triatt_fwd(const void* z, const uint8_t* mask, const float* norm_w,
@@ -934,9 +957,16 @@ extern "C" int bioemu_triatt_fwd(const void* z, const uint8_t* mask, const float
   p += round_up(pairs, 256);
   bf16* wf = reinterpret_cast<bf16*>(p);
   bf16* cf = reinterpret_cast<bf16*>(p + round_up((size_t)kProjRows * C * 2, 256));
+  bf16* wt = reinterpret_cast<bf16*>(p + fold_bytes(kProjRows));
   if (B * Np * (Np / 32) >= kMaxTiles) return set_error(BIOEMU_ERR_INVALID_ARG, "triatt: too many pair tiles");
   int rc = launch_fold_ln(w_proj, norm_w, norm_b, wf, cf, kProjRows, stream);
   if (rc) return rc;
+  {
+    KernelTimerScope timed("triatt_frag", stream);
+    hipLaunchKernelGGL(triatt_frag_kernel, dim3(kFragCount * 64 / 256), dim3(256), 0, stream,
+                       static_cast<const bf16*>(w_proj), norm_w, static_cast<const bf16*>(w_o), wt);
+  }
+  if ((rc = check_launch("triatt_frag"))) return rc;
 
   int dev = 0, cus = 0;
   (void)hipGetDevice(&dev);
@@ -971,8 +1001,8 @@ extern "C" int bioemu_triatt_fwd(const void* z, const uint8_t* mask, const float
   if (grid2 > 0x7fffffffLL) return set_error(BIOEMU_ERR_INVALID_ARG, "triatt: too many work items");
   {
     KernelTimerScope timed("triatt_flash", stream);
-    hipLaunchKernelGGL(kflash, dim3((unsigned)grid2), dim3(kFlashThreads), flash_smem, stream, buf, wf, cf,
-                       static_cast<const bf16*>(w_o), static_cast<const bf16*>(z), static_cast<bf16*>(out), res_tail,
+    hipLaunchKernelGGL(kflash, dim3((unsigned)grid2), dim3(kFlashThreads), flash_smem, stream, buf, wt, cf,
+                       static_cast<const bf16*>(z), static_cast<bf16*>(out), res_tail,
                        (int)N, (int)Np, residual, (int)nitems);
   }
   return check_launch("triatt_flash");

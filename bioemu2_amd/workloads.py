@@ -105,6 +105,9 @@ def triatt_kernel_work(name: str, B: int, N: int, c: int = 128, H: int = 4,
     if name == "triatt_proj":
         # LN + the key side, k, v (c -> 2c) + bias (c -> H): reads z, writes k, v, the bias and the frame mask
         return ("hbm", float(P * (c * 2 + 2 * c * 2 + H * 2 + 1)))
+    if name == "triatt_frag":
+        # the q and g rows of the projection and Wo ([c][c] each) read and written in fragment order
+        return ("hbm", float(2 * 3 * c * c * 2))
     if name == "triatt_flash":
         # q (c -> c) for the queries of rows with a valid key; QK^T and PV over the valid keys for every
         # (valid row, query, head); the gate g (c -> c) and the output projection for every pair
@@ -416,6 +419,8 @@ class OpmWorkload(Workload):
             return ("hbm", float(self.s_valid * n * 64 * 2 + 2 * S * n * 32 * 2))
         if kernel == "opm_rows":
             return ("hbm", float(S * n))
+        if kernel == "opm_wo_tiles":  # proj_o weight [128][1024] read and written in fragment order
+            return ("hbm", float(2 * 128 * 1024 * 2))
         raise KeyError(kernel)
 
 
