@@ -792,16 +792,27 @@ void triatt_flash_kernel(
   // operands.  g = sigmoid(LN(z) Wg^T) times o / l per head is the B operand
   // of update^T = Wo (g o)^T; the residual is added and the result stored in
   // z's frame.  Weight fragments (1 KB each, in fragment order: wt) are read
-  // per block from L2 to keep the register budget; lanes of queries past N
-  // read pair 0 and store nothing.
+  // from L2 in blocks of 8 (block k = 0..3: the g rows of head k, 4..7: Wo
+  // rows 32 (k - 4) ..), each block requested while the previous one is
+  // multiplied; lanes of queries past N read pair 0 and store nothing.
+  // One opaque copy of the weight pointer per tile: the tiles' fragments are
+  // the same, and shared between the tiles (64 of them) they would not fit
+  // the register budget.
+  const bf16* wte[kFlashTiles];
 #pragma unroll
   for (int t = 0; t < kFlashTiles; ++t) {
-    // Opaque copies of the weight pointers: the fragments are loop-invariant,
-    // and hoisted out of this loop (64 of them) they would not fit the
-    // register budget.
-    const bf16* wte = wt;
-    asm volatile("" : "+s"(wte));
-    const __amdgpu_buffer_rsrc_t wtrs = buffer_rsrc(wte, (unsigned)kFragElems * 2);
+    wte[t] = wt;
+    asm volatile("" : "+s"(wte[t]));
+  }
+  auto wblock = [&](int t, int k, bf16x8 (&f)[8]) {
+    const __amdgpu_buffer_rsrc_t r = buffer_rsrc(wte[t], (unsigned)kFragElems * 2);
+#pragma unroll
+    for (int s2 = 0; s2 < 8; ++s2) f[s2] = buffer_load8(r, (unsigned)lane * 16, (unsigned)(32 + 8 * k + s2) * 1024);
+  };
+  bf16x8 wnext[8];
+  wblock(0, 0, wnext);
+#pragma unroll
+  for (int t = 0; t < kFlashTiles; ++t) {
     const int q = q0 + 32 * t + n;
     const bool store = q < N;
     const size_t zpair = zpair_of(q);
@@ -843,11 +854,14 @@ void triatt_flash_kernel(
 #pragma unroll
     for (int hd = 0; hd < H; ++hd) {
       __builtin_amdgcn_sched_barrier(0);
+      bf16x8 wcur[8];
+#pragma unroll
+      for (int s2 = 0; s2 < 8; ++s2) wcur[s2] = wnext[s2];
+      wblock(t, hd + 1, wnext);
       const int r = kRowG + hd * DH + perm32(n);
       f32x16 acc = zero16();
 #pragma unroll
-      for (int s2 = 0; s2 < 8; ++s2)
-        acc = mfma32(buffer_load8(wtrs, (unsigned)lane * 16, (unsigned)(32 + hd * 8 + s2) * 1024), xg[s2], acc);
+      for (int s2 = 0; s2 < 8; ++s2) acc = mfma32(wcur[s2], xg[s2], acc);
       bf16x8 wb = zero8;
       if (hh == 0) {
         wb[0] = cf[2 * r];
@@ -875,10 +889,16 @@ void triatt_flash_kernel(
       // the residual's tail, requested ahead of this block's products
       u32x4 zt;
       if (kTail) zt = load_tail16(tail + zpair * C + cb * 32 + 16 * hh);
+      bf16x8 wcur[8];
+#pragma unroll
+      for (int s2 = 0; s2 < 8; ++s2) wcur[s2] = wnext[s2];
+      if (cb + 1 < 4)
+        wblock(t, 5 + cb, wnext);
+      else if (t + 1 < kFlashTiles)
+        wblock(t + 1, 0, wnext);   // the next tile's first block
       f32x16 acc = zero16();
 #pragma unroll
-      for (int s2 = 0; s2 < 8; ++s2)
-        acc = mfma32(buffer_load8(wtrs, (unsigned)lane * 16, (unsigned)(64 + cb * 8 + s2) * 1024), gob[s2], acc);
+      for (int s2 = 0; s2 < 8; ++s2) acc = mfma32(wcur[s2], gob[s2], acc);
       if (store) {
         const size_t off = zpair * C + cb * 32 + 16 * hh;
         float v[16];
