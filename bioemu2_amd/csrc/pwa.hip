@@ -236,22 +236,25 @@ __global__ __launch_bounds__(kPThreads) void pwa_proj_kernel(const bf16* __restr
 
 // ---------------------------------------------------------------------------
 // Contraction fused with the gate and the output projection.
-// Workgroup = (b, 4 MSA rows s0.., 128 query rows i0..); 8 waves, wave
-// (wi = wave & 1, ws = wave >> 1) owns rows i0 + 64 wi .. +63 of MSA row s0 + ws.
-// For each head h:
+// Workgroup = (b, 8 MSA rows s0.., 128 query rows i0..); 8 waves, wave
+// (wi = wave & 1, ws = wave >> 1) owns rows i0 + 64 wi .. +63 of MSA rows
+// s0 + 2 ws and s0 + 2 ws + 1.  For each head h:
 //   O_h[i][(s, d)] = sum_j W[b][h][i][j] V^T[b][h][(s, d)][j]    (MFMA, K = Np,
 //     64-deep k-tiles copied straight into LDS, double-buffered across heads)
 //   out^T[o][i] += sum_d Wo[o][h*32 + d] (g[b][s][i][h*32 + d] O_h[i][(s, d)])
 // with the gated O_h taken from the accumulator registers as the B operand of
 // the projection (Wo in LDS).  After the 8 heads the 64 output channels (+ m)
-// are written once: neither g * o nor o ever goes to HBM.
+// are written once: neither g * o nor o ever goes to HBM.  Per 16-deep k-step
+// a wave reads 4 operand fragments (W rows of its two i blocks, V^T rows of
+// its two MSA rows) for 4 MFMAs.
 // ---------------------------------------------------------------------------
 constexpr int kFuThreads = 512;
 constexpr int kFuI = 128;                       // query rows per workgroup
-constexpr int kFuS = 4;                         // MSA rows per workgroup
+constexpr int kFuS = 8;                         // MSA rows per workgroup (2 per wave)
 constexpr int kFuBK = 64;
-constexpr int kFuTile = kFuI * kFuBK;           // one operand tile: [128 rows][8 chunks of 8]
-constexpr int kFuStage = 2 * kFuTile;           // W tile | V^T tile
+constexpr int kFuWTile = kFuI * kFuBK;          // W tile: [128 rows][8 chunks of 8]
+constexpr int kFuVTile = kFuS * CH * kFuBK;     // V^T tile: [256 rows (s, d)][8 chunks of 8]
+constexpr int kFuStage = kFuWTile + kFuVTile;
 constexpr int kLdwO = HC + 8;                   // Wo row stride in LDS
 constexpr int kFuSmem = 2 * kFuStage * 2 + CM * kLdwO * 2;
 
@@ -283,41 +286,42 @@ __global__ __launch_bounds__(kFuThreads) void pwa_fused_kernel(const bf16* __res
     store8(wol + r * kLdwO + part * 8, load8(wo + (size_t)r * HC + part * 8));
   }
 
-  // Each operand tile (128 rows x 128 B) is 16 copies of 1 KB; wave w moves
-  // copies w and w + 8 of both.  Copy j writes LDS chunk 64 j + lane.
-  unsigned voff[2];
+  // The W tile (128 rows x 128 B) is 16 copies of 1 KB, the V^T tile (256
+  // rows) 32; wave w moves W copies w, w + 8 and V^T copies w, w + 8, w + 16,
+  // w + 24.  Copy j writes LDS chunk 64 j + lane of its tile.
+  unsigned voff[4];
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
+  for (int q = 0; q < 4; ++q) {
     const int p = (wave + 8 * q) * 64 + lane, r = p >> 3, c = (p & 7) ^ nt_swz(p >> 3);
     voff[q] = (unsigned)(r * Np + c * 8) * 2;
   }
-  const unsigned tile_bytes = (unsigned)kFuI * Np * 2;
   auto rsrcs = [&](int h, __amdgpu_buffer_rsrc_t& rw, __amdgpu_buffer_rsrc_t& rv) {
-    rw = buffer_rsrc(w + ((size_t)(b * NH + h) * Np + i0) * Np, tile_bytes);
-    rv = buffer_rsrc(vt + (((size_t)(b * NH + h) * S8 + s0) * CH) * Np, tile_bytes);
+    rw = buffer_rsrc(w + ((size_t)(b * NH + h) * Np + i0) * Np, (unsigned)kFuI * Np * 2);
+    rv = buffer_rsrc(vt + (((size_t)(b * NH + h) * S8 + s0) * CH) * Np, (unsigned)(kFuS * CH) * Np * 2);
   };
   auto stage = [&](__amdgpu_buffer_rsrc_t rw, __amdgpu_buffer_rsrc_t rv, int kt, int buf) {
     bf16* stg = smem + buf * kFuStage;
     const unsigned soff = (unsigned)(kt * kFuBK) * 2;
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      nt_copy16_to_lds(rw, stg + (wave + 8 * q) * 512, voff[q], soff);
-      nt_copy16_to_lds(rv, stg + kFuTile + (wave + 8 * q) * 512, voff[q], soff);
-    }
+    for (int q = 0; q < 2; ++q) nt_copy16_to_lds(rw, stg + (wave + 8 * q) * 512, voff[q], soff);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) nt_copy16_to_lds(rv, stg + kFuWTile + (wave + 8 * q) * 512, voff[q], soff);
   };
 
   const int nk = Np / kFuBK;
-  const int jrow = ws * 32 + perm32(ln);
-  int offi[2];
+  int jrow[2], offi[2];
+#pragma unroll
+  for (int si = 0; si < 2; ++si) jrow[si] = (2 * ws + si) * 32 + perm32(ln);
 #pragma unroll
   for (int ib = 0; ib < 2; ++ib) offi[ib] = wi * 64 + ib * 32 + ln;
-  const int s = s0 + ws;
 
-  f32x16 oacc[2][2];   // [ob][ib]: out^T rows ob*32.., columns i
+  f32x16 oacc[2][2][2];   // [si][ob][ib]: out^T rows ob*32.., columns i, MSA row s0 + 2 ws + si
 #pragma unroll
-  for (int ob = 0; ob < 2; ++ob)
+  for (int si = 0; si < 2; ++si)
 #pragma unroll
-    for (int ib = 0; ib < 2; ++ib) oacc[ob][ib] = zero16();
+    for (int ob = 0; ob < 2; ++ob)
+#pragma unroll
+      for (int ib = 0; ib < 2; ++ib) oacc[si][ob][ib] = zero16();
 
   __amdgpu_buffer_rsrc_t rw, rv;
   rsrcs(0, rw, rv);
@@ -325,7 +329,11 @@ __global__ __launch_bounds__(kFuThreads) void pwa_fused_kernel(const bf16* __res
   int gk = 0;   // running k-tile index: LDS buffer gk & 1
 #pragma unroll 1
   for (int h = 0; h < NH; ++h) {
-    f32x16 acc[2] = {zero16(), zero16()};
+    f32x16 acc[2][2];   // [si][ib]
+#pragma unroll
+    for (int si = 0; si < 2; ++si)
+#pragma unroll
+      for (int ib = 0; ib < 2; ++ib) acc[si][ib] = zero16();
 #pragma unroll 1
     for (int kt = 0; kt < nk; ++kt, ++gk) {
       __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's copies of the k-tile landed
@@ -337,70 +345,87 @@ __global__ __launch_bounds__(kFuThreads) void pwa_fused_kernel(const bf16* __res
         stage(rw, rv, 0, (gk + 1) & 1);
       }
       const bf16* sa = smem + (gk & 1) * kFuStage;
-      const bf16* sb = sa + kFuTile;
-      bf16x8 fj[4], fi[4][2];
+      const bf16* sb = sa + kFuWTile;
+      // fragments of k-step ks + 1 are read while k-step ks is multiplied
+      bf16x8 fj[2][2], fi[2][2];
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        fj[0][x] = load8(sb + nt_off(jrow[x], lh));
+        fi[0][x] = load8(sa + nt_off(offi[x], lh));
+      }
 #pragma unroll
       for (int ks = 0; ks < kFuBK / 16; ++ks) {
-        fj[ks] = load8(sb + nt_off(jrow, 2 * ks + lh));
+        const int c = ks & 1;
+        if (ks + 1 < kFuBK / 16) {
 #pragma unroll
-        for (int ib = 0; ib < 2; ++ib) fi[ks][ib] = load8(sa + nt_off(offi[ib], 2 * ks + lh));
+          for (int x = 0; x < 2; ++x) {
+            fj[c ^ 1][x] = load8(sb + nt_off(jrow[x], 2 * (ks + 1) + lh));
+            fi[c ^ 1][x] = load8(sa + nt_off(offi[x], 2 * (ks + 1) + lh));
+          }
+        }
+#pragma unroll
+        for (int si = 0; si < 2; ++si)
+#pragma unroll
+          for (int ib = 0; ib < 2; ++ib) acc[si][ib] = mfma32(fj[c][si], fi[c][ib], acc[si][ib]);
       }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int ks = 0; ks < kFuBK / 16; ++ks)
-#pragma unroll
-        for (int ib = 0; ib < 2; ++ib) acc[ib] = mfma32(fj[ks], fi[ks][ib], acc[ib]);
-      __builtin_amdgcn_sched_barrier(0);
     }
-    // acc[ib] lane (ln, lh) register u <-> O_h[i = i0 + wi*64 + ib*32 + ln][(s, d = 16 lh + u)]
+    // acc[si][ib] lane (ln, lh) register u <-> O_h[i = i0 + wi*64 + ib*32 + ln][(s0 + 2 ws + si, d = 16 lh + u)]
 #pragma unroll
-    for (int ib = 0; ib < 2; ++ib) {
-      const int i = i0 + offi[ib];
-      const bf16* gp = g + (((size_t)b * S8 + s) * Np + i) * HC + h * CH + 16 * lh;
-      const bf16x8 g0 = load8(gp), g1 = load8(gp + 8);
-      bf16x8 go0, go1;
+    for (int si = 0; si < 2; ++si) {
+      const int s = s0 + 2 * ws + si;
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        go0[u] = f2bf(acc[ib][u] * bf2f(g0[u]));
-        go1[u] = f2bf(acc[ib][8 + u] * bf2f(g1[u]));
-      }
+      for (int ib = 0; ib < 2; ++ib) {
+        const int i = i0 + offi[ib];
+        const bf16* gp = g + (((size_t)b * S8 + s) * Np + i) * HC + h * CH + 16 * lh;
+        const bf16x8 g0 = load8(gp), g1 = load8(gp + 8);
+        bf16x8 go0, go1;
 #pragma unroll
-      for (int ob = 0; ob < 2; ++ob) {
-        const bf16* wrow = wol + (ob * 32 + perm32(ln)) * kLdwO + h * CH + 16 * lh;
-        oacc[ob][ib] = mfma32(load8(wrow), go0, oacc[ob][ib]);
-        oacc[ob][ib] = mfma32(load8(wrow + 8), go1, oacc[ob][ib]);
+        for (int u = 0; u < 8; ++u) {
+          go0[u] = f2bf(acc[si][ib][u] * bf2f(g0[u]));
+          go1[u] = f2bf(acc[si][ib][8 + u] * bf2f(g1[u]));
+        }
+#pragma unroll
+        for (int ob = 0; ob < 2; ++ob) {
+          const bf16* wrow = wol + (ob * 32 + perm32(ln)) * kLdwO + h * CH + 16 * lh;
+          oacc[si][ob][ib] = mfma32(load8(wrow), go0, oacc[si][ob][ib]);
+          oacc[si][ob][ib] = mfma32(load8(wrow + 8), go1, oacc[si][ob][ib]);
+        }
       }
     }
   }
-  // oacc[ob][ib] lane (ln, lh) register u <-> out channel ob*32 + 16 lh + u of (s, i0 + offi[ib])
-  if (s >= S) return;
+  // oacc[si][ob][ib] lane (ln, lh) register u <-> out channel ob*32 + 16 lh + u of (s, i0 + offi[ib])
 #pragma unroll
-  for (int ib = 0; ib < 2; ++ib) {
-    const int i = i0 + offi[ib];
-    if (i >= N) continue;
+  for (int si = 0; si < 2; ++si) {
+    const int s = s0 + 2 * ws + si;
+    if (s >= S) continue;
 #pragma unroll
-    for (int ob = 0; ob < 2; ++ob) {
-      const size_t off = (((size_t)b * S + s) * N + i) * CM + ob * 32 + 16 * lh;
-      float v[16];
+    for (int ib = 0; ib < 2; ++ib) {
+      const int i = i0 + offi[ib];
+      if (i >= N) continue;
 #pragma unroll
-      for (int u = 0; u < 16; ++u) v[u] = oacc[ob][ib][u];
-      if (residual && tail) {   // residual stream with an int8 tail (common.h), in place
-        float mv[16];
-        tail_decode16(load8(mres + off), load8(mres + off + 8), load_tail16(tail + off), mv);
+      for (int ob = 0; ob < 2; ++ob) {
+        const size_t off = (((size_t)b * S + s) * N + i) * CM + ob * 32 + 16 * lh;
+        float v[16];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) v[u] += mv[u];
-        tail_store16(out + off, tail + off, v);
-        continue;
-      }
-      if (residual) {
-        const bf16x8 r0 = load8(mres + off), r1 = load8(mres + off + 8);
+        for (int u = 0; u < 16; ++u) v[u] = oacc[si][ob][ib][u];
+        if (residual && tail) {   // residual stream with an int8 tail (common.h), in place
+          float mv[16];
+          tail_decode16(load8(mres + off), load8(mres + off + 8), load_tail16(tail + off), mv);
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          v[u] += bf2f(r0[u]);
-          v[8 + u] += bf2f(r1[u]);
+          for (int u = 0; u < 16; ++u) v[u] += mv[u];
+          tail_store16(out + off, tail + off, v);
+          continue;
         }
+        if (residual) {
+          const bf16x8 r0 = load8(mres + off), r1 = load8(mres + off + 8);
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            v[u] += bf2f(r0[u]);
+            v[8 + u] += bf2f(r1[u]);
+          }
+        }
+        store16(out + off, v);
       }
-      store16(out + off, v);
     }
   }
 }
