@@ -625,6 +625,8 @@ class PairMixerMsaWorkload(Workload):
             return ("hbm", float(self.s_valid * n * 64 * 2 + 2 * S * n * 32 * 2))
         if kernel == "opm_rows":
             return ("hbm", float(S * n))
+        if kernel == "opm_wo_tiles":
+            return ("hbm", float(2 * 128 * 1024 * 2))
         if kernel in ("pwa_weights", "pwa_proj", "pwa_fused"):
             return PwaWorkload.kernel_work(self, kernel)
         if kernel == "transition_msa":
@@ -742,6 +744,8 @@ class PairMixerTrunkWorkload(Workload):
             return ("mfma", 2.0 * n * n * 128 * 12 * 128)
         if kernel == "opm_fused":
             return ("mfma", 2.0 * n * n * 1024 * self.s_valid + 2.0 * n * n * 1024 * 128)
+        if kernel == "opm_wo_tiles":
+            return ("hbm", float(2 * 128 * 1024 * 2))
         if kernel in ("pwa_weights", "pwa_proj", "pwa_fused"):
             return PwaWorkload.kernel_work(self, kernel)
         if kernel == "transition_msa":
