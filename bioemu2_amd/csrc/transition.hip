@@ -102,30 +102,37 @@ __global__ __launch_bounds__(kThreads) void transition_rows_kernel(
   const __amdgpu_buffer_rsrc_t r2 = buffer_rsrc(w2, HID * C * 2);
   const __amdgpu_buffer_rsrc_t r3 = buffer_rsrc(w3, C * HID * 2);
   const __amdgpu_buffer_rsrc_t rc = buffer_rsrc(cf, 2 * HID * 2 * 2);
-  // Copy k of a stage (k = wave, wave + 4, ...): fc1 rows, fc2 rows, fc3
-  // columns (1 KB each, LDS chunk 64 j + lane of the tile), last the bias
-  // pairs of both (4 bytes per lane).
+  // The copies of a stage, each 1 KB into LDS chunk j of its tile: this wave
+  // takes fc1 rows and fc2 rows j = wave + 4 q and fc3 columns j = wave + 4 q;
+  // wave 0 also the bias pairs of both (4 bytes per lane).  The assignment is
+  // fixed per wave, so a stage is straight-line code with a few offsets.
+  static_assert(G::W12Copies % 4 == 0 && G::W3Copies % 4 == 0, "copies split evenly over the 4 waves");
+  constexpr int Q12 = G::W12Copies / 4, Q3 = G::W3Copies / 4;
+  unsigned vo12[Q12], vo3[Q3];
+#pragma unroll
+  for (int q = 0; q < Q12; ++q) {
+    const int p = (wave + 4 * q) * 64 + lane, r = p / G::RowChunks, c = (p % G::RowChunks) ^ w12_swz<C>(r);
+    vo12[q] = (unsigned)(r * C + c * 8) * 2;
+  }
+#pragma unroll
+  for (int q = 0; q < Q3; ++q) {
+    // LDS row 32 cb + m <- fc3 row 32 cb + 16 ((m & 15) >> 3) + 8 (m >> 4) + (m & 7)
+    const int p = (wave + 4 * q) * 64 + lane, r = p >> 2, c = (p & 3) ^ swz4(r);
+    const int m = r & 31, rg = (r & ~31) + 16 * ((m & 15) >> 3) + 8 * (m >> 4) + (m & 7);
+    vo3[q] = (unsigned)(rg * HID + c * 8) * 2;
+  }
+  const unsigned vob = (unsigned)(((lane >> 5) * HID + (lane & 31)) * 2) * 2;
   auto stage_chunk = [&](int hc) {
     bf16* st = smem + (hc & 1) * G::Stage;
 #pragma unroll
-    for (int k = wave; k < G::Copies; k += 4) {
-      if (k < 2 * G::W12Copies) {
-        const bool second = k >= G::W12Copies;
-        const int j = second ? k - G::W12Copies : k;
-        const int p = j * 64 + lane, r = p / G::RowChunks, c = (p % G::RowChunks) ^ w12_swz<C>(r);
-        copy16_to_lds(second ? r2 : r1, st + (second ? G::W12Tile : 0) + j * 512, (unsigned)(r * C + c * 8) * 2,
-                      (unsigned)(hc * HC * C) * 2);
-      } else if (k < 2 * G::W12Copies + G::W3Copies) {
-        // LDS row 32 cb + m <- fc3 row 32 cb + 16 ((m & 15) >> 3) + 8 (m >> 4) + (m & 7)
-        const int j = k - 2 * G::W12Copies, p = j * 64 + lane, r = p >> 2, c = (p & 3) ^ swz4(r);
-        const int m = r & 31, rg = (r & ~31) + 16 * ((m & 15) >> 3) + 8 * (m >> 4) + (m & 7);
-        copy16_to_lds(r3, st + 2 * G::W12Tile + j * 512, (unsigned)(rg * HID + c * 8) * 2, (unsigned)(hc * HC) * 2);
-      } else if (use_norm) {
-        const int which = lane >> 5, row = lane & 31;
-        copy4_to_lds(rc, st + 2 * G::W12Tile + G::W3Tile, (unsigned)((which * HID + row) * 2) * 2,
-                     (unsigned)(hc * HC * 2) * 2);
-      }
+    for (int q = 0; q < Q12; ++q) {
+      copy16_to_lds(r1, st + (wave + 4 * q) * 512, vo12[q], (unsigned)(hc * HC * C) * 2);
+      copy16_to_lds(r2, st + G::W12Tile + (wave + 4 * q) * 512, vo12[q], (unsigned)(hc * HC * C) * 2);
     }
+#pragma unroll
+    for (int q = 0; q < Q3; ++q)
+      copy16_to_lds(r3, st + 2 * G::W12Tile + (wave + 4 * q) * 512, vo3[q], (unsigned)(hc * HC) * 2);
+    if (use_norm && wave == 0) copy4_to_lds(rc, st + 2 * G::W12Tile + G::W3Tile, vob, (unsigned)(hc * HC * 2) * 2);
   };
 
   stage_chunk(0);
