@@ -27,6 +27,13 @@ def split_stream(x: Tensor) -> tuple[Tensor, Tensor]:
 
 
 def join_stream(hi: Tensor, tail: Tensor, dtype: torch.dtype = torch.float32) -> Tensor:
-    """The stream's value in ``dtype``: fp32 exactly (hi + tail), other dtypes rounded once from it."""
+    """The stream's value in ``dtype``: fp32 exactly (hi + tail), other dtypes rounded once from it.
+
+    For bf16 that rounding is ``hi`` itself: hi is the nearest bf16 of the value and the tail is at most
+    127/256 of its ulp, less than half, so rounding hi + tail to bf16 gives hi back (bit for bit, except
+    that a -0 stays -0 where the fp32 sum -0 + 0 is +0), and ``hi`` is returned without another pass over
+    the stream."""
+    if dtype == torch.bfloat16:
+        return hi
     full = _ops.stream_join(hi, tail)
     return full if dtype == torch.float32 else full.to(dtype)

@@ -52,6 +52,17 @@ def test_split_join_bit_exact(gpu_device):
     assert np.array_equal(back.view(np.uint32), np_tail_decode(want_hi, want_t).view(np.uint32))
 
 
+def test_join_to_bf16_is_hi(gpu_device):
+    """A bf16 join returns hi, which equals the fp32 join rounded to bf16, on a stream an op has updated."""
+    x = _stream((2, 40, 40, 128), gpu_device, 11, scale=3.0)
+    hi, tail = split_stream(x)
+    m = init_module(Transition(128, 512), 0).to(gpu_device)
+    _ops.launch_transition_pair(hi, *m.prepared_params(), hi, residual=True, tail=tail)
+    want = _ops.stream_join(hi, tail).to(torch.bfloat16)
+    got = join_stream(hi, tail, torch.bfloat16)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
 def _run_with_tail(launch, x32):
     """launch(hi, tail) updates (hi, tail) in place; returns the joined fp32 result and hi as the op saw it."""
     hi, tail = split_stream(x32)

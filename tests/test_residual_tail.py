@@ -56,3 +56,24 @@ def test_negative_control_ulp_scale():
     wrong = np_bf16_to_f32(hi).astype(np.float64) + np.ldexp(t.astype(np.float64), e - 141)
     err = np.abs(wrong - x.astype(np.float64))
     assert np.any(err > np.abs(x.astype(np.float64)) * 2.0 ** -15 + 1e-38)
+
+
+def test_bf16_of_joined_value_is_hi():
+    """Rounding a stream's value hi + tail to bf16 gives hi back bit for bit (|tail| <= 127/256 ulp, and at a
+    binade edge the nearest-even tie keeps hi), so a bf16 join may return hi without a pass over the stream."""
+    x = _samples()
+    hi, t = np_tail_encode(x)
+    back = np_bf16_rne(np_tail_decode(hi, t))
+    # the one difference: -0 + 0 is +0 in the fp32 join, while hi keeps the zero's sign
+    assert np.array_equal(np.where(hi == 0x8000, 0, back), np.where(hi == 0x8000, 0, hi))
+    assert np.all(back[hi == 0x8000] == 0)
+    # values within one bf16 ulp of binade edges (where the spacing halves below the edge), every fp32
+    # step of the last 2^9 on either side
+    edges = np.ldexp(1.0, np.arange(-20, 21)).astype(np.float64)
+    steps = np.arange(-512, 513, dtype=np.float64)
+    near = np.concatenate([(e + steps * e * 2.0 ** -24) for e in edges]).astype(np.float32)
+    near = np.concatenate([near, -near])
+    hn, tn = np_tail_encode(near)
+    assert np.array_equal(np_bf16_rne(np_tail_decode(hn, tn)), hn)
+    assert np.array_equal(hn, np_bf16_rne(near))
+
